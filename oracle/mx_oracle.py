@@ -1,0 +1,551 @@
+"""CPU oracle for the mxtorch quantize / pack / block-scaled GEMM path.
+
+TEST INFRASTRUCTURE ONLY.  This module is the parity checker: only the test
+suite (tests/), ``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of
+``bench.py`` may import it.  The product package ``qtpytorch_amd`` never
+imports, links or calls anything under ``oracle/``; on a GPU it runs the HIP
+kernels in ``libmxk.so`` and fails loudly when that library is missing.
+
+What it is: a restatement of the reference's CPU path (mxtorch.py, one
+module, referenced below as ``mxtorch.py:LINE``) written with the same torch
+CPU operators in the same order, so that every intermediate is rounded the
+way the reference rounds it.  The arithmetic of the reference lives in torch
+CPU kernels (torch is the third-party dependency; the reference pins no
+version, this restatement runs on the torch in this image).  The facts it
+relies on are pinned by tests in tests/test_oracle_*.py:
+
+  * ``scalar / tensor`` is ``tensor.reciprocal() * scalar``
+    (torch/_tensor.py ``__rdiv__``), so the int quantizer rounds twice:
+    inv = fl(fl(1/a)*q), s = fl(1/inv)  (mxtorch.py:1458-1459);
+  * ``tensor / python_float`` on CPU is an IEEE division by fl32(value);
+  * ``round`` is round-half-to-even; ``bucketize`` (right=False) returns the
+    number of boundaries strictly below the value.
+
+Every function cites the reference lines it restates.  Pins (golden vectors
+written by importing the reference, the reference's own pack KATs, closed
+forms, brute force) are listed in the header of each test module.
+"""
+from __future__ import annotations
+
+import functools
+import math
+import re
+from typing import Optional, Tuple
+
+import torch
+import torch.nn.functional as F
+
+Tensor = torch.Tensor
+
+# ---------------------------------------------------------------------------
+# dtype names  (mxtorch.py:413-547, 567-581)
+# ---------------------------------------------------------------------------
+_NAME_RE = re.compile(r"^(int|float)(1|2|3|4|5|6|7|8|16|32|64|128)(d|u)(h|v|s|b|2)?$")
+
+
+def parse_dtype(name: str):
+    """Split an mxtorch dtype name into (kind, bits, mode, variant).
+
+    mxtorch.py:464-466 builds names as f"{kind}{bits}{mode}{variant}";
+    get_mx_dtype raises ValueError on anything else (mxtorch.py:577-581).
+    """
+    m = _NAME_RE.match(name)
+    if m is None:
+        raise ValueError(f"Unknown MX dtype {name!r}")
+    kind, bits, mode, variant = m.group(1), int(m.group(2)), m.group(3), m.group(4) or ""
+    return kind, bits, mode, variant
+
+
+def max_val(name: str) -> float:
+    """mx_dtype.max_val (mxtorch.py:509-523)."""
+    kind, bits, _, variant = parse_dtype(name)
+    if variant == "b":
+        return 1.0
+    if kind == "int":
+        return 1.0 if bits == 1 else float((1 << (bits - 1)) - 1)
+    fmax = {1: 1.0, 2: 1.5, 3: 3.5, 4: 6.0, 5: 14.0, 6: 28.0, 7: 56.0, 8: 448.0, 16: 65504.0}
+    return fmax.get(bits, float("inf"))
+
+
+# ---------------------------------------------------------------------------
+# bit packing  (mxtorch.py:870-985)
+# ---------------------------------------------------------------------------
+def pack(vals: Tensor, bits: int) -> Tensor:
+    """bit_packer.pack (mxtorch.py:882-910): LSB-first fields in int8 bytes."""
+    assert bits in (1, 2, 4, 8)
+    if bits == 8:
+        return vals.to(torch.int8)
+    ratio = 8 // bits
+    n = vals.numel()
+    pad = (-n) % ratio
+    if pad:
+        vals = torch.cat([vals.flatten(), vals.new_zeros(pad, dtype=vals.dtype)])
+    vals = vals.flatten().to(torch.int8)
+    mask = (1 << bits) - 1
+    packed = torch.zeros(vals.numel() // ratio, dtype=torch.int8)
+    for i in range(ratio):
+        slot = (vals[i::ratio] & mask).to(torch.int8)
+        packed = packed | (slot << (i * bits))
+    return packed
+
+
+def unpack(packed: Tensor, bits: int, n: int) -> Tensor:
+    """bit_packer.unpack (mxtorch.py:912-935): sign-extended codes as float32."""
+    assert bits in (1, 2, 4, 8)
+    if bits == 8:
+        return packed[:n].to(torch.float32)
+    ratio = 8 // bits
+    mask = (1 << bits) - 1
+    sign = 1 << (bits - 1)
+    out = torch.empty(len(packed) * ratio, dtype=torch.int8)
+    for i in range(ratio):
+        slot = ((packed >> (i * bits)) & mask).to(torch.int8)
+        signed = torch.where((slot.to(torch.int16) & sign) != 0,
+                             (slot.to(torch.int16) | (~mask & 0xFF)).to(torch.int8), slot)
+        out[i::ratio] = signed
+    return out[:n].to(torch.float32)
+
+
+def pack_arb(vals: Tensor, bits: int) -> Tensor:
+    """bit_packer.pack_arb (mxtorch.py:939-955): floor(32/bits) fields per int32 word."""
+    if bits in (1, 2, 4, 8):
+        return pack(vals.to(torch.int8), bits)
+    ratio = 32 // bits
+    n = vals.numel()
+    pad = (-n) % ratio
+    if pad:
+        vals = torch.cat([vals.flatten(), vals.new_zeros(pad, dtype=vals.dtype)])
+    v32 = vals.flatten().to(torch.int32)
+    mask = (1 << bits) - 1
+    packed = torch.zeros(len(v32) // ratio, dtype=torch.int32)
+    for i in range(ratio):
+        packed |= (v32[i::ratio] & mask) << (i * bits)
+    return packed
+
+
+def unpack_arb(packed: Tensor, bits: int, n: int) -> Tensor:
+    """bit_packer.unpack_arb (mxtorch.py:957-972)."""
+    if bits in (1, 2, 4, 8):
+        return unpack(packed.view(torch.int8) if packed.dtype != torch.int8 else packed, bits, n)
+    ratio = 32 // bits
+    mask = (1 << bits) - 1
+    sign = 1 << (bits - 1)
+    out = torch.empty(len(packed) * ratio, dtype=torch.int32)
+    for i in range(ratio):
+        slot = (packed >> (i * bits)) & mask
+        signed = torch.where((slot & sign) != 0, slot | ~mask, slot)
+        out[i::ratio] = signed
+    return out[:n].to(torch.float32)
+
+
+def pack_auto(vals: Tensor, bits: int) -> Tensor:
+    """bit_packer.pack_auto (mxtorch.py:976-980)."""
+    if bits in (1, 2, 4, 8):
+        return pack(vals.to(torch.int8), bits)
+    return pack_arb(vals, bits)
+
+
+def unpack_auto(packed: Tensor, bits: int, n: int) -> Tensor:
+    """bit_packer.unpack_auto (mxtorch.py:982-985)."""
+    if bits in (1, 2, 4, 8):
+        return unpack(packed.to(torch.int8), bits, n)
+    return unpack_arb(packed.to(torch.int32), bits, n)
+
+
+# ---------------------------------------------------------------------------
+# mini-float grids  (mxtorch.py:992-1054)
+# ---------------------------------------------------------------------------
+@functools.lru_cache(maxsize=8)
+def float_grid(bits: int) -> Tensor:
+    """_get_minifloat_grid for the FP4 E2M1 and FP8 E4M3 cases.
+
+    FP4: mxtorch.py:1023-1035.  FP8 (exponent 15 treated as a normal
+    binade, max 480): mxtorch.py:1038-1054.
+    """
+    if bits == 4:
+        pos = torch.tensor([0.0, 0.5, 1.0, 1.5, 2.0, 3.0, 4.0, 6.0], dtype=torch.float32)
+        scale = pos.abs().max().clamp(min=1e-9)
+        pos_n = pos / scale
+        neg_n = -pos_n.flip(0)
+        grid = torch.cat([neg_n, pos_n])
+        return grid.sort().values
+    if bits == 8:
+        vals = []
+        for code in range(256):
+            sign = -1.0 if (code >> 7) else 1.0
+            e = (code >> 3) & 0xF
+            m = code & 0x7
+            if e == 0:
+                v = sign * (m / 8.0) * (2.0 ** -6)
+            elif e == 0xF:
+                v = sign * (1.0 + m / 8.0) * (2.0 ** 8)
+            else:
+                v = sign * (1.0 + m / 8.0) * (2.0 ** (e - 7))
+            vals.append(v)
+        raw = torch.tensor(vals, dtype=torch.float32)
+        scale = raw.abs().max().clamp(min=1e-9)
+        return (raw / scale).sort().values
+    if bits == 16:
+        # every non-NaN/Inf half-precision value (NaN/Inf codes become 0.0),
+        # normalised by the largest magnitude (mxtorch.py:1117-1143); this
+        # is what float16d GEMM outputs (float8d @ float8d) dequantize with.
+        import numpy as np
+        h = np.arange(65536, dtype=np.uint32).astype(np.uint16).view(np.float16).astype(np.float32)
+        h[~np.isfinite(h)] = 0.0
+        raw = torch.from_numpy(h)
+        mx = raw.abs().max().clamp(min=1e-9)
+        return (raw / mx).sort().values
+    raise NotImplementedError(f"oracle grid for float{bits}")
+
+
+def float_mids(bits: int) -> Tensor:
+    """Bucket boundaries used by _quant_float (mxtorch.py:1523)."""
+    g = float_grid(bits)
+    return (g[:-1] + g[1:]) * 0.5
+
+
+# ---------------------------------------------------------------------------
+# quantizers  (mxtorch.py:1426-1528, 1684-1763)
+# ---------------------------------------------------------------------------
+def _blocks(x: Tensor, block: int):
+    flat = x.float().reshape(-1)
+    n = flat.numel()
+    nb = math.ceil(n / block)
+    pad = nb * block - n
+    if pad:
+        flat = torch.cat([flat, flat.new_zeros(pad)])
+    return flat.reshape(nb, block), n
+
+
+def quant_int(x: Tensor, bits: int, block: int) -> Tuple[Tensor, Tensor, int]:
+    """_quant_int (mxtorch.py:1426-1463)."""
+    blk, n = _blocks(x, block)
+    if bits == 1:  # mxtorch.py:1442-1454
+        scales = blk.abs().amax(dim=1).clamp(min=1e-12)
+        codes = torch.where(blk >= 0, torch.zeros_like(blk, dtype=torch.int32),
+                            torch.full_like(blk, -1, dtype=torch.int32))
+        return pack_auto(codes.reshape(-1), bits), scales, n
+    max_int = float((1 << (bits - 1)) - 1)
+    scale_inv = max_int / blk.abs().amax(dim=1).clamp(min=1e-12)   # reciprocal() * max_int
+    scales = scale_inv.reciprocal()
+    codes = (blk * scale_inv.unsqueeze(1)).clamp(-max_int, max_int).round_().to(torch.int32)
+    return pack_auto(codes.reshape(-1), bits), scales, n
+
+
+def quant_float(x: Tensor, bits: int, block: int) -> Tuple[Tensor, Tensor, int]:
+    """_quant_float for sub-16-bit grids (mxtorch.py:1465-1528)."""
+    blk, n = _blocks(x, block)
+    scales = blk.abs().amax(dim=1).clamp(min=1e-12)
+    normed = blk / scales.unsqueeze(1)
+    grid = float_grid(bits)
+    flat = normed.reshape(-1)
+    mids = (grid[:-1] + grid[1:]) * 0.5
+    idx = torch.bucketize(flat, mids)
+    codes = idx.to(torch.int32)
+    return pack_auto(codes, bits), scales, n
+
+
+def quant_vector(x: Tensor, name: str, block: int) -> Tuple[Tensor, Tensor, int]:
+    """The 'v' (per-row) branch of quantize (mxtorch.py:1739-1752)."""
+    _, bits, _, _ = parse_dtype(name)
+    blk, n = _blocks(x, block)
+    mx = max_val(name)
+    scales = blk.abs().amax(dim=1).clamp(min=1e-12) / mx
+    codes = (blk / scales.unsqueeze(1)).clamp(-mx, mx).round_().to(torch.int32)
+    return pack_auto(codes.reshape(-1), bits), scales, n
+
+
+# ---------------------------------------------------------------------------
+# Hadamard rotation  (mxtorch.py:2811-2904)
+# ---------------------------------------------------------------------------
+def hadamard_signs(n: int, seed: int) -> Tensor:
+    """hadamard_rotation.__init__ sign vector (mxtorch.py:2856-2864)."""
+    gen = torch.Generator()
+    gen.manual_seed(seed)
+    return torch.randint(0, 2, (n,), generator=gen).float() * 2 - 1
+
+
+def reference_hadamard_seed(name: str) -> int:
+    """The seed quantize() derives for 'h' dtypes (mxtorch.py:1723).
+
+    ``hash(str)`` is salted per process unless PYTHONHASHSEED is fixed, so
+    callers that need reproducible signs pass the seed explicitly.
+    """
+    return hash(name) % (2 ** 31)
+
+
+def fwht(x: Tensor) -> Tensor:
+    """_fast_hadamard_transform (mxtorch.py:2811-2832): butterflies with
+    half-width n/2, n/4, ..., 1 along the last dim, then an IEEE division by
+    fl32(sqrt(n))."""
+    n = x.shape[-1]
+    assert (n & (n - 1)) == 0
+    orig_shape = x.shape
+    h = x.reshape(-1, n).clone()
+    h2 = n
+    while h2 > 1:
+        h2 //= 2
+        h = h.reshape(h.shape[0], -1, 2 * h2)
+        even = h[..., :h2]
+        odd = h[..., h2:]
+        h = torch.cat([even + odd, even - odd], dim=-1)
+    return h.reshape(*orig_shape[:-1], n) / math.sqrt(n)
+
+
+def _pow2_ceil(d: int) -> int:
+    return 1 << math.ceil(math.log2(max(d, 1)))
+
+
+def rotate(x: Tensor, signs: Tensor) -> Tensor:
+    """hadamard_rotation.rotate (mxtorch.py:2866-2889); ``signs`` has the
+    rotation's power-of-two length."""
+    d = x.shape[-1]
+    n = _pow2_ceil(d)
+    x_f = x.float()
+    if n != d:
+        x_f = F.pad(x_f, (0, n - d))
+    s = signs if d == signs.numel() else signs[:d].sign()
+    sp = F.pad(s, (0, n - len(s)), value=1.0) if n > len(s) else s[:n]
+    return fwht(x_f * sp)[..., :d]
+
+
+def unrotate(x: Tensor, signs: Tensor) -> Tensor:
+    """hadamard_rotation.unrotate (mxtorch.py:2891-2904)."""
+    d = x.shape[-1]
+    n = _pow2_ceil(d)
+    x_f = x.float()
+    if n != d:
+        x_f = F.pad(x_f, (0, n - d))
+    x_rot = fwht(x_f)
+    s = signs if d == signs.numel() else signs[:d].sign()
+    sp = F.pad(s, (0, n - len(s)), value=1.0) if n > len(s) else s[:n]
+    return (x_rot * sp)[..., :d]
+
+
+def rotation_dim(shape) -> int:
+    """The rotated length quantize() picks (mxtorch.py:1721)."""
+    shape = tuple(shape)
+    if len(shape) >= 2:
+        return shape[-1]
+    return int(math.prod(shape))
+
+
+# ---------------------------------------------------------------------------
+# quantize / dequantize dispatch  (mxtorch.py:1530-1597, 1684-1763)
+# ---------------------------------------------------------------------------
+def quantize(x: Tensor, name: str, block: int = 128, seed: Optional[int] = None
+             ) -> Tuple[Tensor, Tensor, int]:
+    """quantize() CPU branch (mxtorch.py:1684-1763) for the base, 'h' and 'v'
+    variants.  For 'h' the seed defaults to the reference's hash-derived one."""
+    kind, bits, mode, variant = parse_dtype(name)
+    base = f"{kind}{bits}{mode}"
+    x_f = x.float()
+    if variant == "h":
+        d = x_f.shape[-1] if x_f.ndim >= 2 else x_f.numel()
+        if seed is None:
+            seed = reference_hadamard_seed(name)
+        signs = hadamard_signs(_pow2_ceil(d), seed)
+        x_rot = rotate(x_f, signs)
+        return quant_int(x_rot, bits, block) if kind == "int" else quant_float(x_rot, bits, block)
+    if variant == "v":
+        return quant_vector(x_f, name, block)
+    if variant != "":
+        raise NotImplementedError(f"oracle variant {variant!r}")
+    if kind == "int":
+        return quant_int(x_f, bits, block)
+    return quant_float(x_f, bits, block)
+
+
+def dequant(packed: Tensor, scales: Tensor, name: str, n: int, block: int,
+            seed: Optional[int] = None, orig_shape=None, hadamard_mode: str = "reference"
+            ) -> Tensor:
+    """_dequant (mxtorch.py:1530-1597).
+
+    hadamard_mode="reference" reproduces the reference's unrotation over the
+    whole flattened tensor (d = numel, mxtorch.py:1582-1595).  "rows"
+    unrotates each row of length rotation_dim(orig_shape), i.e. the inverse
+    of what quantize() rotated; both agree for 1-D tensors.
+    """
+    kind, bits, _, variant = parse_dtype(name)
+    codes = unpack_auto(packed, bits, n)
+    nb = scales.numel()
+    pad = nb * block - n
+    if pad > 0:
+        codes = torch.cat([codes, codes.new_zeros(pad)])
+    elif pad < 0:
+        codes = codes[:nb * block]
+    blk = codes.reshape(nb, block)
+    if kind == "int" and bits == 1 and variant != "b":
+        dq = torch.where(blk == 0, torch.ones_like(blk, dtype=torch.float32),
+                         torch.full_like(blk, -1.0, dtype=torch.float32))
+    elif kind == "float":
+        mask = (1 << bits) - 1
+        indices = (blk.to(torch.int64) & mask).long()
+        grid = float_grid(bits)
+        indices = indices.clamp(0, len(grid) - 1)
+        dq = grid[indices]
+    else:
+        dq = blk
+    flat = (dq * scales.unsqueeze(1)).reshape(-1)[:n]
+    if variant == "h":
+        if seed is None:
+            seed = reference_hadamard_seed(name)
+        if hadamard_mode == "reference" or orig_shape is None:
+            d = flat.numel()
+            n2 = _pow2_ceil(d)
+            signs = hadamard_signs(n2, seed)
+            flat = unrotate(flat.unsqueeze(0), signs).squeeze(0)[:d]
+        else:
+            d = rotation_dim(orig_shape)
+            signs = hadamard_signs(_pow2_ceil(d), seed)
+            flat = unrotate(flat.reshape(-1, d), signs).reshape(-1)
+    return flat
+
+
+# ---------------------------------------------------------------------------
+# GEMM  (mxtorch.py:1299-1423, 5497-5573)
+# ---------------------------------------------------------------------------
+_VALID_BITS = (1, 2, 3, 4, 5, 6, 7, 8, 16, 32, 64, 128)
+
+
+def matmul_out_bits(a_bits: int, b_bits: int) -> int:
+    """_optimal_output_dtype("matmul", ...) bit width (mxtorch.py:1393-1418)."""
+    ideal = min(32, a_bits + b_bits)
+    return min(_VALID_BITS, key=lambda x: (abs(x - ideal), -x))
+
+
+def qscale_matmul(a_codes: Tensor, a_scales: Tensor, b_codes: Tensor, b_scales: Tensor,
+                  M: int, K: int, N: int, bits: int, block: int, out_bits: int,
+                  return_c: bool = False):
+    """_qscale_matmul (mxtorch.py:1299-1385).
+
+    Returns (codes [M*N] int32, scales [ceil(M*N/block)]); with return_c the
+    fp32 accumulator C [M, N] before requantization is returned as well.
+    """
+    max_out = float((1 << (out_bits - 1)) - 1)
+    a_mat = a_codes.reshape(M, K).float()
+    b_mat = b_codes.reshape(K, N).float()
+    kba = math.ceil(K / block)
+    c_mat = torch.zeros(M, N, dtype=torch.float32)
+    a_s = a_scales.reshape(M, kba) if a_scales.numel() == M * kba else a_scales.new_ones(M, kba)
+    b_s = b_scales.reshape(kba, N) if b_scales.numel() == kba * N else b_scales.new_ones(kba, N)
+    for kb in range(kba):
+        k0, k1 = kb * block, min(kb * block + block, K)
+        prod = torch.mm(a_mat[:, k0:k1], b_mat[k0:k1, :])
+        c_mat += prod * a_s[:, kb].unsqueeze(1) * b_s[kb, :].unsqueeze(0)
+    nb_c = math.ceil(M * N / block)
+    c_flat = c_mat.reshape(-1)
+    pad = nb_c * block - c_flat.numel()
+    c_p = torch.cat([c_flat, c_flat.new_zeros(pad)]) if pad else c_flat
+    c_blk = c_p.reshape(nb_c, block)
+    c_scale = c_blk.abs().amax(dim=1).clamp(min=1e-12) / max_out
+    c_codes = (c_blk / c_scale.unsqueeze(1)).clamp(-max_out, max_out).round_()
+    c_codes = c_codes.to(torch.int32).reshape(-1)[:M * N]
+    if return_c:
+        return c_codes, c_scale, c_mat
+    return c_codes, c_scale
+
+
+def int_accumulators(a_codes: Tensor, b_codes: Tensor, M: int, K: int, N: int, block: int) -> Tensor:
+    """Per-K-block exact integer products P[kb] = A[:, kb] @ B[kb, :]
+    (the ``int_prod`` of mxtorch.py:1365), as int32 [KB, M, N]."""
+    a = a_codes.reshape(M, K).to(torch.int64)
+    b = b_codes.reshape(K, N).to(torch.int64)
+    kba = math.ceil(K / block)
+    out = torch.empty(kba, M, N, dtype=torch.int32)
+    for kb in range(kba):
+        k0, k1 = kb * block, min(kb * block + block, K)
+        out[kb] = (a[:, k0:k1] @ b[k0:k1, :]).to(torch.int32)
+    return out
+
+
+def dispatch_qgemm(a_packed: Tensor, a_scales: Tensor, a_name: str, a_shape, a_n: int,
+                   b_packed: Tensor, b_scales: Tensor, b_name: str, b_shape, b_n: int,
+                   block: int, return_c: bool = False):
+    """_dispatch_qgemm CPU branch (mxtorch.py:5497-5573): both operands are
+    unpacked with a's bit width (mxtorch.py:5564-5565).  Returns
+    (packed, scales, out_name[, C])."""
+    M, K = a_shape
+    K2, N = b_shape
+    assert K == K2
+    ak, abits, amode, _ = parse_dtype(a_name)
+    bk, bbits, bmode, _ = parse_dtype(b_name)
+    out_bits = matmul_out_bits(abits, bbits)
+    kind = "float" if (ak == "float" or bk == "float") else "int"
+    mode = "u" if (amode == "u" or bmode == "u") else "d"
+    out_name = f"{kind}{out_bits}{mode}"
+    a_codes = unpack_auto(a_packed, abits, a_n).to(torch.int32)
+    b_codes = unpack_auto(b_packed, abits, b_n).to(torch.int32)
+    res = qscale_matmul(a_codes, a_scales, b_codes, b_scales, M, K, N, abits, block,
+                        out_bits, return_c=return_c)
+    packed = pack_auto(res[0], out_bits)
+    if return_c:
+        return packed, res[1], out_name, res[2]
+    return packed, res[1], out_name
+
+
+def qgemm_ste_forward(a: Tensor, b: Tensor, name: str, block: int) -> Tensor:
+    """_QGemmSTE.forward (mxtorch.py:5295-5303): quantize both, packed GEMM,
+    dequantize the requantized output."""
+    pa, sa, na = quantize(a, name, block)
+    pb, sb, nb = quantize(b, name, block)
+    pc, sc, out_name = dispatch_qgemm(pa, sa, name, a.shape, na, pb, sb, name, b.shape, nb, block)
+    M, N = a.shape[0], b.shape[1]
+    return dequant(pc, sc, out_name, M * N, block).reshape(M, N)
+
+
+# ---------------------------------------------------------------------------
+# callers  (mxtorch.py:7439-7473, 3039-3086)
+# ---------------------------------------------------------------------------
+def linear_from_weight(weight: Tensor, name: str, block: int = 128):
+    """mx_linear.from_linear weight storage (mxtorch.py:7439-7452):
+    quantize(W.t()) -> [in, out] row-major, blocks along out."""
+    return quantize(weight.t(), name, block)
+
+
+def linear_forward(x: Tensor, w_packed: Tensor, w_scales: Tensor, name: str,
+                   in_features: int, out_features: int, block: int = 128,
+                   has_bias: bool = False) -> Tensor:
+    """mx_linear.forward (mxtorch.py:7454-7473).  A bias, when present, is
+    re-quantized from zeros on every call (mxtorch.py:7434-7436), so it adds
+    dequant(quantize(zeros))."""
+    x_f = x.float()
+    w_f = dequant(w_packed, w_scales, name, in_features * out_features, block
+                  ).reshape(in_features, out_features)
+    b_f = None
+    if has_bias:
+        pb, sb, nb = quantize(torch.zeros(out_features), name, block)
+        b_f = dequant(pb, sb, name, nb, block)
+    return F.linear(x_f, w_f.t(), b_f)
+
+
+def kv_append(k: Tensor, v: Tensor, name: str, head_dim: int, asymmetric_v: bool = True):
+    """kv_cache_quantizer.append_kv for one step (mxtorch.py:3039-3067).
+    Returns ((k_packed, k_scales, k_n), (v_packed, v_scales, v_n), v_zero_point)."""
+    k_f = k.float().reshape(-1, head_dim)
+    v_f = v.float().reshape(-1, head_dim)
+    kq = quantize(k_f, name, head_dim)
+    if asymmetric_v:
+        v_min = v_f.min(dim=1, keepdim=True).values
+        vq = quantize(v_f - v_min, name, head_dim)
+        return kq, vq, v_min.squeeze(1)
+    return kq, quantize(v_f, name, head_dim), None
+
+
+def kv_get(steps, name: str, head_dim: int, n_heads: int):
+    """kv_cache_quantizer.get (mxtorch.py:3069-3086); ``steps`` is a list of
+    kv_append results."""
+    ks, vs, zps = [], [], []
+    for kq, vq, zp in steps:
+        rows = kq[2] // head_dim
+        ks.append(dequant(kq[0], kq[1], name, kq[2], head_dim).reshape(rows, head_dim))
+        vs.append(dequant(vq[0], vq[1], name, vq[2], head_dim).reshape(rows, head_dim))
+        if zp is not None:
+            zps.append(zp)
+    T = len(steps)
+    k_all = torch.stack(ks, dim=1)
+    v_all = torch.stack(vs, dim=1)
+    if zps:
+        v_all = v_all + torch.stack(zps, dim=1).unsqueeze(-1)
+    BH, _, D = k_all.shape
+    return k_all.reshape(-1, n_heads, T, D), v_all.reshape(-1, n_heads, T, D)
