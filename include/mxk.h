@@ -1,0 +1,162 @@
+/*
+ * mxk.h — C ABI of libmxk.so, the MI355X (gfx950) kernels behind the
+ * mxtorch quantize / dequantize / packed-GEMM hot path.
+ *
+ * The reference (mxtorch.py, a single Python module) has no FFI: its swap
+ * points are Python functions.  Each entry point below names the reference
+ * function it replaces (mxtorch.py:LINE).  The Python package qtpytorch_amd
+ * binds these symbols with ctypes and keeps the reference's Python API
+ * (mx_tensor.quantize / dequantize / @, mx_linear, to_mx, _QGemmSTE,
+ * mx_matmul, kv_cache_quantizer) and its byte and scale layouts.
+ *
+ * Conventions
+ *  - All pointers except `signs`' host copy are device pointers; the caller
+ *    owns and allocates every buffer (outputs, optional workspaces).  The
+ *    library never allocates device memory.
+ *  - Every call is asynchronous on `stream` (a hipStream_t; NULL is the
+ *    default stream).  Entry points are reentrant; calls that share a
+ *    workspace must not overlap.
+ *  - Return 0 on success or a negative mxk_status; mxk_last_error() gives a
+ *    thread-local message.  No exceptions cross the ABI.
+ *  - Layouts (mxtorch.py:870-985, 6044-6049): values are blocked over the
+ *    row-major flattened tensor, zero-padded to nb = ceil(n/block) blocks.
+ *    For bits in {1,2,4,8} codes are packed LSB-first into bytes (element j
+ *    at byte j/(8/bits), bit (j%(8/bits))*bits); for bits in {3,5,6,7,16}
+ *    into little-endian int32 words holding floor(32/bits) fields.  Int
+ *    fields are two's complement; float fields are indices into the sorted
+ *    grid.  Scales are float32 [nb].
+ */
+#ifndef MXK_H
+#define MXK_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MXK_ABI_VERSION 1
+
+typedef enum {
+  MXK_OK = 0,
+  MXK_EINVAL = -22,       /* bad argument (shape, size, pointer, alignment) */
+  MXK_EUNSUPPORTED = -95, /* combination this build does not implement     */
+  MXK_ELAUNCH = -5        /* a HIP launch or runtime call failed            */
+} mxk_status;
+
+typedef enum { MXK_IN_F32 = 0, MXK_IN_F16 = 1, MXK_IN_BF16 = 2 } mxk_elem_type;
+typedef enum { MXK_KIND_INT = 0, MXK_KIND_FLOAT = 1 } mxk_kind;
+typedef enum {
+  MXK_VAR_BASE = 0,     /* ""  : block absmax                              */
+  MXK_VAR_HADAMARD = 1, /* "h" : randomized Walsh-Hadamard, then base      */
+  MXK_VAR_VECTOR = 2    /* "v" : per-row absmax, true division             */
+} mxk_variant;
+
+/* Library version; equals MXK_ABI_VERSION. */
+int mxk_abi_version(void);
+
+/* Thread-local message describing the last failed call on this thread. */
+const char* mxk_last_error(void);
+
+/* Bytes of packed storage for n_codes codes of `bits` width: the length of
+ * bit_packer.pack_auto's output (mxtorch.py:882-955) in bytes. */
+int64_t mxk_packed_nbytes(int bits, int64_t n_codes);
+
+/* Host-side copy of the sorted mini-float grid and its bucket midpoints for
+ * float4d (bits=4) and float8d (bits=8): _get_minifloat_grid
+ * (mxtorch.py:993-1054) and the mids of _quant_float (mxtorch.py:1523).
+ * grid has 2^bits entries, mids 2^bits - 1.  Pure host code (no GPU). */
+int mxk_float_grid(int bits, float* grid, float* mids);
+
+/* Workspace bytes mxk_quantize needs for this problem (0 if none). */
+size_t mxk_quantize_workspace(int64_t n, int kind, int bits, int variant, int block,
+                              int64_t rot_dim);
+
+/* quantize(x, dt, block) -> (packed, scales, n)  (mxtorch.py:1684-1763),
+ * CPU semantics of _quant_int (mxtorch.py:1426-1463), _quant_float
+ * (mxtorch.py:1465-1528), the 'v' branch (mxtorch.py:1739-1752) and the 'h'
+ * branch (mxtorch.py:1720-1736, rotation mxtorch.py:2834-2889).
+ *
+ *  x         device input, n elements of x_type (row-major flattened).
+ *  kind/bits int: bits in {1..8,16}; float: bits in {4,8}.
+ *  variant   mxk_variant.  For MXK_VAR_HADAMARD, rot_dim is the rotated
+ *            length d (the last dimension, or n for 1-D inputs), n must be a
+ *            multiple of d, and `signs` holds next_pow2(d) device floats
+ *            (+1/-1), the rotation's sign vector.  Otherwise signs=NULL,
+ *            rot_dim=0.
+ *  packed    output, packed_nbytes = mxk_packed_nbytes(bits, n_store).
+ *  scales    output, ceil(n/block) floats.
+ *  n_store   codes to store: ceil(n/block)*block for quantize (the
+ *            reference packs the padded blocks), n for GEMM requantization
+ *            (mxtorch.py:1384).
+ */
+int mxk_quantize(const void* x, int x_type, int64_t n, int kind, int bits, int variant,
+                 int block, const float* signs, int64_t rot_dim, void* packed,
+                 int64_t packed_nbytes, float* scales, int64_t n_store, void* workspace,
+                 size_t workspace_nbytes, void* stream);
+
+/* _dequant(packed, scales, dt, n, block) (mxtorch.py:1530-1597) -> out[n]
+ * float32.  Reads only the first packed_nbytes bytes (GEMM outputs store n
+ * codes, quantize stores the padded blocks).  For MXK_VAR_HADAMARD the
+ * unrotation runs over rows of rot_dim elements (rot_dim = n reproduces the
+ * reference's whole-tensor inverse, mxtorch.py:1582-1595); signs as for
+ * mxk_quantize; a workspace of mxk_dequantize_workspace() bytes is needed
+ * when next_pow2(rot_dim) > 8192. */
+int mxk_dequantize(const void* packed, int64_t packed_nbytes, const float* scales, int64_t nb,
+                   int64_t n, int kind, int bits, int variant, int block, const float* signs,
+                   int64_t rot_dim, float* out, void* workspace, size_t workspace_nbytes,
+                   void* stream);
+
+/* Workspace bytes mxk_dequantize needs (0 if none). */
+size_t mxk_dequantize_workspace(int64_t n, int variant, int64_t rot_dim);
+
+/* Workspace bytes mxk_qgemm needs; out_bits = 0 when no packed output is
+ * requested. */
+size_t mxk_qgemm_workspace(int64_t M, int64_t K, int64_t N, int bits, int block, int out_bits);
+
+/* Packed block-scaled GEMM: the CPU branch of _dispatch_qgemm
+ * (mxtorch.py:5563-5573) around _qscale_matmul (mxtorch.py:1299-1385).
+ *
+ *  A [M,K] and B [K,N] are bits-packed codes (bits in {1,2,4,8}; both
+ *  unpacked with this width and sign-extended, as the reference unpacks b
+ *  with a's width, mxtorch.py:5564-5565).  KB = ceil(K/block).
+ *  SA[m,kb] = a_scales[m*KB+kb] if a_nscales == M*KB, else 1.
+ *  SB[kb,n] = b_scales[kb*N+n]  if b_nscales == KB*N, else 1 (the
+ *  reference's reading of B's flat scales, mxtorch.py:1354).
+ *  For kb ascending: P = exact int32 sum over the block,
+ *  C = RN(C + RN(RN(P*SA)*SB)).
+ *
+ *  Optional outputs (NULL to skip, at least one required):
+ *   c_f32    float32 [M,N], C before requantization;
+ *   acc_i32  int32 [KB,M,N], the per-block integer products P;
+ *   c_packed/c_scales  out_bits > 0: C requantized per `block` flat
+ *            elements, s = RN(max(absmax,1e-12)/q), code = rne(clamp(RN(C/s)))
+ *            (mxtorch.py:1372-1385), M*N codes packed (mxtorch.py:5570),
+ *            scales [ceil(M*N/block)].
+ */
+int mxk_qgemm(const void* a_packed, const float* a_scales, int64_t a_nscales, const void* b_packed,
+              const float* b_scales, int64_t b_nscales, int64_t M, int64_t K, int64_t N, int bits,
+              int block, int out_bits, void* c_packed, int64_t c_packed_nbytes, float* c_scales,
+              float* c_f32, int32_t* acc_i32, void* workspace, size_t workspace_nbytes,
+              void* stream);
+
+/* Workspace bytes mxk_linear_wq needs (0 if none). */
+size_t mxk_linear_workspace(int64_t M, int64_t K, int64_t N, int bits, int block);
+
+/* Weight-only linear, mx_linear.forward (mxtorch.py:7454-7473):
+ * out[M,N] = x[M,K] (x_type, converted to float32) @ dequant(W) (+ bias[N]),
+ * W = the packed codes/scales of quantize(weight.t()): [K,N] row-major,
+ * blocks of `block` flat elements (mxtorch.py:7447).  The dequantized
+ * weight RN(code*s) (mxtorch.py:1573-1575) is formed in registers only.
+ * kind/bits as for mxk_quantize (base variant).  Float32 accumulation. */
+int mxk_linear_wq(const void* x, int x_type, int64_t M, int64_t K, const void* w_packed,
+                  const float* w_scales, int64_t N, int kind, int bits, int block,
+                  const float* bias, float* out, void* workspace, size_t workspace_nbytes,
+                  void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MXK_H */

@@ -1,0 +1,188 @@
+// Internal helpers shared by the libmxk HIP sources (gfx950 only).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+#include <hip/hip_bfloat16.h>
+#include <stdint.h>
+#include <string>
+
+#include "../../include/mxk.h"
+
+namespace mxk {
+
+// ---------------------------------------------------------------- errors
+void set_error(const std::string& msg);
+int fail(int code, const std::string& msg);
+int check_launch(const char* what);
+
+inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+inline bool is_pow2(int64_t v) { return v > 0 && (v & (v - 1)) == 0; }
+inline int64_t next_pow2(int64_t v) {
+  int64_t p = 1;
+  while (p < v) p <<= 1;
+  return p;
+}
+inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// Number of CUs of the current device (cached per device).
+int num_cus();
+
+// ---------------------------------------------------------------- device math
+// Quantizer modes.
+enum QMode : int { Q_INT = 0, Q_INT1 = 1, Q_VEC = 2, Q_FP = 3 };
+
+// fl32(1e-12): the clamp(min=1e-12) of every quantizer (mxtorch.py:1444,1458,1497,1748).
+#define MXK_AMIN 9.99999996e-13f
+
+// IEEE division a/b given y = RN(1/b), by Markstein's correction
+// (q0 = RN(a*y); r = a - b*q0 exactly by FMA; q1 = RN(q0 + r*y)).  The
+// residual is exact and the result correctly rounded when |a| >= 2^-96 and
+// b, a/b are normal; below that the hardware divide sequence is used.
+__device__ __forceinline__ float div_rn(float a, float b, float y) {
+  if (__builtin_expect(__builtin_fabsf(a) < 0x1p-96f, 0)) return a / b;
+  float q0 = a * y;
+  float r = __builtin_fmaf(-q0, b, a);
+  return __builtin_fmaf(r, y, q0);
+}
+
+__device__ __forceinline__ float rne(float v) { return __builtin_rintf(v); }
+
+// Lane-group max over `G` consecutive lanes (G a power of two <= 64); every
+// lane of the group ends with the group maximum.
+template <int G>
+__device__ __forceinline__ float group_max(float v) {
+  if constexpr (G >= 2)
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xF, 0xF, true)));
+  if constexpr (G >= 4)
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x4E, 0xF, 0xF, true)));
+  if constexpr (G >= 8)  // row_half_mirror: lane i <-> 7-i within 8
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x141, 0xF, 0xF, true)));
+  if constexpr (G >= 16)  // row_mirror: lane i <-> 15-i within 16
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x140, 0xF, 0xF, true)));
+  if constexpr (G >= 32)  // swap 16-lane halves of each 32
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x401F)));
+  if constexpr (G >= 64) v = fmaxf(v, __shfl_xor(v, 32));
+  return v;
+}
+
+// ---------------------------------------------------------------- element loads
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+template <typename T> struct ElemT;
+template <> struct ElemT<float> {
+  static __device__ __forceinline__ float cvt(float v) { return v; }
+};
+template <> struct ElemT<__half> {
+  static __device__ __forceinline__ float cvt(__half v) { return __half2float(v); }
+};
+template <> struct ElemT<hip_bfloat16> {
+  static __device__ __forceinline__ float cvt(hip_bfloat16 v) {
+    return __uint_as_float(static_cast<uint32_t>(reinterpret_cast<const uint16_t&>(v)) << 16);
+  }
+};
+
+// Load E consecutive elements starting at `idx` as float; elements at or
+// beyond n read as +0.0 (the reference zero-pads the last block).  A full
+// in-range group uses 16-byte loads (the caller guarantees alignment).
+template <typename T, int E>
+__device__ __forceinline__ void load_elems(const T* __restrict__ x, int64_t idx, int64_t n,
+                                           float (&v)[E]) {
+  constexpr int PER16 = 16 / sizeof(T);
+  static_assert(E % PER16 == 0, "E must cover whole 16-byte vectors");
+  if (idx + E <= n) {
+    const u32x4* p = reinterpret_cast<const u32x4*>(x + idx);
+#pragma unroll
+    for (int q = 0; q < E / PER16; ++q) {
+      u32x4 w = __builtin_nontemporal_load(p + q);
+      const T* t = reinterpret_cast<const T*>(&w);
+#pragma unroll
+      for (int i = 0; i < PER16; ++i) v[q * PER16 + i] = ElemT<T>::cvt(t[i]);
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < E; ++i) v[i] = (idx + i < n) ? ElemT<T>::cvt(x[idx + i]) : 0.0f;
+  }
+}
+
+// Store `NB` bytes from `w` at dst+off when they fit below `limit`; bytes at
+// or past `limit` are dropped (tail of a packed buffer).
+template <int NB>
+__device__ __forceinline__ void store_bytes(uint8_t* __restrict__ dst, int64_t off, int64_t limit,
+                                            const uint32_t* w) {
+  if (off + NB <= limit) {
+    if constexpr (NB == 1) dst[off] = static_cast<uint8_t>(w[0]);
+    else if constexpr (NB == 2) *reinterpret_cast<uint16_t*>(dst + off) = static_cast<uint16_t>(w[0]);
+    else if constexpr (NB == 4) *reinterpret_cast<uint32_t*>(dst + off) = w[0];
+    else if constexpr (NB == 8) *reinterpret_cast<u32x2*>(dst + off) = u32x2{w[0], w[1]};
+    else if constexpr (NB == 16)
+      *reinterpret_cast<u32x4*>(dst + off) = u32x4{w[0], w[1], w[2], w[3]};
+  } else {
+    for (int b = 0; b < NB; ++b)
+      if (off + b < limit) dst[off + b] = static_cast<uint8_t>(w[b >> 2] >> ((b & 3) * 8));
+  }
+}
+
+// ---------------------------------------------------------------- float grids
+// Positive grid magnitude of code c (c < 2^(bits-1)), in units of the
+// format's largest value, exactly as _get_minifloat_grid builds it
+// (mxtorch.py:1023-1054): FP4 E2M1 values /6, FP8 E4M3 values (exponent 15
+// is a normal binade, max 480) /480, each an IEEE float32 division.
+__host__ __device__ inline float fmt_value(int bits, int c) {
+  if (bits == 4) {
+    int e = c >> 1, m = c & 1;
+    return e == 0 ? 0.5f * (float)m : ldexpf((float)(2 + m), e - 2);
+  }
+  int e = c >> 3, m = c & 7;
+  return e == 0 ? ldexpf((float)m, -9) : ldexpf((float)(8 + m), e - 10);
+}
+__host__ __device__ inline float fmt_max(int bits) { return bits == 4 ? 6.0f : 480.0f; }
+
+// LDS tables for a float format with H = 2^(bits-1):
+//   P[0] = -inf, P[j] = RN(RN(g[j-1]+g[j])*0.5) for j in [1,H), P[H] = +inf
+//   G[0..2H): the sorted grid; G[H-1] = -0.0, G[H] = +0.0 (torch.sort's order).
+template <int BITS>
+__device__ void build_tables(float* P, float* G) {
+  constexpr int H = 1 << (BITS - 1);
+  __shared__ float g[H];
+  for (int c = threadIdx.x; c < H; c += blockDim.x) g[c] = fmt_value(BITS, c) / fmt_max(BITS);
+  __syncthreads();
+  for (int j = threadIdx.x; j <= H; j += blockDim.x) {
+    if (P) P[j] = j == 0 ? -INFINITY : (j == H ? INFINITY : (g[j - 1] + g[j]) * 0.5f);
+  }
+  if (G)
+    for (int c = threadIdx.x; c < H; c += blockDim.x) {
+      G[H + c] = g[c];
+      G[H - 1 - c] = -g[c];
+    }
+  __syncthreads();
+}
+
+// Index of y in the sorted grid: #{mids < y} (torch.bucketize, right=False).
+// By the grid's symmetry this is H + #{P_j < |y|} for y > 0 and
+// H-1 - #{P_j <= |y|} otherwise.  The count comes from rounding |y| to the
+// nearest format value (a candidate at most one off) and one comparison
+// with each neighbouring midpoint.
+template <int BITS>
+__device__ __forceinline__ int bucket(float y, const float* __restrict__ P) {
+  constexpr int H = 1 << (BITS - 1);
+  float a = __builtin_fabsf(y);
+  int c0;
+  if constexpr (BITS == 8) {
+    float t = a * 480.0f;
+    c0 = t < 0x1p-6f ? (int)__builtin_rintf(t * 512.0f) : (int)((__float_as_uint(t) + 0x80000u) >> 20) - 960;
+  } else {
+    float t = a * 6.0f;
+    c0 = t < 1.0f ? (int)__builtin_rintf(t * 2.0f) : (int)((__float_as_uint(t) + 0x200000u) >> 22) - 252;
+  }
+  c0 = min(max(c0, 0), H - 1);
+  float lo = P[c0], hi = P[c0 + 1];
+  if (y > 0.0f) return H + c0 + (hi < a ? 1 : 0) - (lo >= a ? 1 : 0);
+  return (H - 1) - (c0 + (hi <= a ? 1 : 0) - (lo > a ? 1 : 0));
+}
+
+// 'v'-rule requantization of a float32 buffer (GEMM outputs), mxtorch.py:1372-1385.
+int requant_vec_f32(const float* x, int64_t n, int bits, int block, void* packed, int64_t packed_nbytes,
+                    float* scales, int64_t n_store, void* ws, size_t ws_bytes, hipStream_t st);
+
+}  // namespace mxk

@@ -1,0 +1,783 @@
+// Block-absmax quantize / dequantize with bit packing, for gfx950.
+//
+// Semantics follow the reference's CPU path (mxtorch.py):
+//   int base   _quant_int    mxtorch.py:1426-1463  r=RN(1/a'), inv=RN(r*q), s=RN(1/inv),
+//                                                  code=rne(clamp(RN(x*inv),-q,q))
+//   int1       _quant_int    mxtorch.py:1442-1454  s=a', code = x>=0 ? 0 : -1
+//   'v'        quantize      mxtorch.py:1739-1752  s=RN(a'/q), code=rne(clamp(RN(x/s)))
+//   float4/8   _quant_float  mxtorch.py:1465-1528  s=a', y=RN(x/s), idx=#{mids < y}
+//   'h'        quantize      mxtorch.py:1720-1736  rotate (mxtorch.py:2866-2889) then base
+//   dequant    _dequant      mxtorch.py:1530-1597
+// where a' = max(absmax(block), fl32(1e-12)).
+//
+// Layout of work: a "group" of LPB consecutive lanes owns one block of
+// B = E*LPB elements; each lane holds E consecutive elements (16-byte
+// vector loads), the block absmax is a DPP / ds_swizzle reduction across
+// the group, and each lane packs its E codes into E*bits/8 bytes that it
+// stores directly.  A 256-thread workgroup walks blocks grid-stride.
+#include "mxk_internal.h"
+
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+#include <mutex>
+#include <vector>
+
+namespace mxk {
+
+// ---------------------------------------------------------------- errors
+static thread_local std::string g_err;
+void set_error(const std::string& msg) { g_err = msg; }
+int fail(int code, const std::string& msg) {
+  g_err = msg;
+  return code;
+}
+int check_launch(const char* what) {
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(MXK_ELAUNCH, std::string(what) + ": " + hipGetErrorString(e));
+  return MXK_OK;
+}
+
+int num_cus() {
+  static std::mutex mu;
+  static std::vector<int> cache;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 256;
+  std::lock_guard<std::mutex> lk(mu);
+  if ((int)cache.size() <= dev) cache.resize(dev + 1, 0);
+  if (cache[dev] == 0) {
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+      cus = 256;
+    cache[dev] = cus;
+  }
+  return cache[dev];
+}
+
+// ---------------------------------------------------------------- per-block params
+struct BlockParams {
+  float s;    // stored scale
+  float mul;  // Q_INT: inv ; Q_VEC/Q_FP: RN(1/s)
+};
+
+template <int MODE>
+__device__ __forceinline__ BlockParams block_params(float ap, float qf) {
+  BlockParams bp;
+  if constexpr (MODE == Q_INT) {
+    float r = 1.0f / ap;
+    bp.mul = r * qf;
+    bp.s = 1.0f / bp.mul;
+  } else if constexpr (MODE == Q_VEC) {
+    bp.s = ap / qf;
+    bp.mul = 1.0f / bp.s;
+  } else {  // Q_INT1, Q_FP
+    bp.s = ap;
+    bp.mul = 1.0f / ap;
+  }
+  return bp;
+}
+
+template <int MODE, int BITS>
+__device__ __forceinline__ int encode(float v, const BlockParams& bp, float qf, const float* P) {
+  if constexpr (MODE == Q_INT) {
+    return (int)rne(fminf(fmaxf(v * bp.mul, -qf), qf));
+  } else if constexpr (MODE == Q_INT1) {
+    return v >= 0.0f ? 0 : 1;
+  } else if constexpr (MODE == Q_VEC) {
+    return (int)rne(fminf(fmaxf(div_rn(v, bp.s, bp.mul), -qf), qf));
+  } else {
+    return bucket<BITS>(div_rn(v, bp.s, bp.mul), P);
+  }
+}
+
+// ---------------------------------------------------------------- fast quantize
+template <typename T, int E, int LPB, int MODE, int BITS>
+__global__ __launch_bounds__(256) void k_quant_fast(const T* __restrict__ x, int64_t n, int64_t nb,
+                                                    uint8_t* __restrict__ packed, int64_t packed_nbytes,
+                                                    int64_t n_store, float* __restrict__ scales, float qf) {
+  constexpr int B = E * LPB;
+  constexpr int GPW = 64 / LPB;
+  constexpr int GPB = 4 * GPW;
+  constexpr int NW = (E * BITS + 31) / 32;
+  constexpr int NB = E * BITS / 8;
+  constexpr uint32_t MASK = BITS == 32 ? 0xFFFFFFFFu : ((1u << BITS) - 1u);
+  constexpr int H = MODE == Q_FP ? (1 << (BITS - 1)) : 1;
+  __shared__ float sP[H + 1];
+  if constexpr (MODE == Q_FP) build_tables<BITS>(sP, nullptr);
+
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int g = lane / LPB, li = lane % LPB;
+  for (int64_t b0 = (int64_t)blockIdx.x * GPB; b0 < nb; b0 += (int64_t)gridDim.x * GPB) {
+    const int64_t blk = b0 + wave * GPW + g;
+    const int64_t idx = blk * B + (int64_t)li * E;
+    float v[E];
+    load_elems<T, E>(x, idx, n, v);
+    float m = 0.0f;
+#pragma unroll
+    for (int i = 0; i < E; ++i) m = fmaxf(m, __builtin_fabsf(v[i]));
+    const float ap = fmaxf(group_max<LPB>(m), MXK_AMIN);
+    const BlockParams bp = block_params<MODE>(ap, qf);
+    uint32_t w[NW];
+#pragma unroll
+    for (int k = 0; k < NW; ++k) w[k] = 0u;
+#pragma unroll
+    for (int i = 0; i < E; ++i) {
+      uint32_t f = (uint32_t)encode<MODE, BITS>(v[i], bp, qf, sP) & MASK;
+      if (idx + i >= n_store) f = 0u;
+      w[(i * BITS) >> 5] |= f << ((i * BITS) & 31);
+    }
+    if (blk < nb) {
+      store_bytes<NB>(packed, idx * BITS / 8, packed_nbytes, w);
+      if (li == 0) scales[blk] = bp.s;
+    }
+  }
+}
+
+// ---------------------------------------------------------------- generic quantize
+// Any block size and any supported width: pass 1 reduces one block per wave
+// and stores the scale and the multiplier, pass 2 writes one packed byte
+// (bits in {1,2,4,8}) or one int32 word (bits in {3,5,6,7,16}) per thread.
+template <typename T, int MODE>
+__global__ __launch_bounds__(256) void k_block_params(const T* __restrict__ x, int64_t n, int64_t nb,
+                                                      int block, float qf, float* __restrict__ scales,
+                                                      float2* __restrict__ params) {
+  const int lane = threadIdx.x & 63;
+  const int64_t wave0 = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
+  const int64_t nwaves = ((int64_t)gridDim.x * blockDim.x) >> 6;
+  for (int64_t blk = wave0; blk < nb; blk += nwaves) {
+    float m = 0.0f;
+    for (int i = lane; i < block; i += 64) {
+      int64_t j = blk * block + i;
+      if (j < n) m = fmaxf(m, __builtin_fabsf(ElemT<T>::cvt(x[j])));
+    }
+    const float ap = fmaxf(group_max<64>(m), MXK_AMIN);
+    const BlockParams bp = block_params<MODE>(ap, qf);
+    if (lane == 0) {
+      scales[blk] = bp.s;
+      params[blk] = make_float2(bp.s, bp.mul);
+    }
+  }
+}
+
+template <typename T, int MODE, int BITS>
+__global__ __launch_bounds__(256) void k_pack_generic(const T* __restrict__ x, int64_t n, int block,
+                                                      float qf, const float2* __restrict__ params,
+                                                      int bits, int64_t n_store, uint8_t* __restrict__ packed,
+                                                      int64_t packed_nbytes) {
+  constexpr int H = MODE == Q_FP ? (1 << (BITS - 1)) : 1;
+  __shared__ float sP[H + 1];
+  if constexpr (MODE == Q_FP) build_tables<BITS>(sP, nullptr);
+  const bool words = !(bits == 1 || bits == 2 || bits == 4 || bits == 8);
+  const int per = words ? 32 / bits : 8 / bits;
+  const int64_t units = words ? packed_nbytes / 4 : packed_nbytes;
+  const uint32_t mask = (bits >= 32) ? 0xFFFFFFFFu : ((1u << bits) - 1u);
+  for (int64_t u = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; u < units;
+       u += (int64_t)gridDim.x * blockDim.x) {
+    uint32_t word = 0u;
+    for (int f = 0; f < per; ++f) {
+      int64_t j = u * per + f;
+      if (j >= n_store) break;
+      float v = j < n ? ElemT<T>::cvt(x[j]) : 0.0f;
+      float2 p = params[j / block];
+      BlockParams bp{p.x, p.y};
+      uint32_t code = (uint32_t)encode<MODE, BITS>(v, bp, qf, sP) & mask;
+      word |= code << (f * bits);
+    }
+    if (words) reinterpret_cast<uint32_t*>(packed)[u] = word;
+    else packed[u] = (uint8_t)word;
+  }
+}
+
+// ---------------------------------------------------------------- Hadamard
+// Randomized Walsh-Hadamard over rows of d elements zero-padded to
+// n = next_pow2(d) (hadamard_rotation.rotate, mxtorch.py:2866-2889, and
+// _fast_hadamard_transform, mxtorch.py:2811-2832): forward multiplies by the
+// sign vector, runs butterflies (u,v)->(u+v,u-v) at half-widths n/2 ... 1,
+// then divides by fl32(sqrt(n)); inverse (unrotate, mxtorch.py:2891-2904)
+// runs the butterflies, divides, then multiplies by the signs.  Every
+// butterfly is an independent IEEE add/sub, so any schedule that keeps the
+// level order reproduces the reference bit for bit.
+//
+// Fused block-128 path: rows of 128 = one quantization block.  A group of 8
+// lanes owns a row, 16 elements per lane.  Levels 64..8 run in registers
+// after an LDS transpose (lane holds positions base+8j), levels 4..1 after
+// the transpose back (lane holds 16 consecutive positions).
+template <int STRIDE_LO, int COUNT>
+__device__ __forceinline__ void butterflies(float (&v)[16]) {
+  // pairs (j, j + STRIDE_LO) inside groups of 2*STRIDE_LO, over 16 registers
+#pragma unroll
+  for (int base = 0; base < 16; base += 2 * STRIDE_LO)
+#pragma unroll
+    for (int j = 0; j < STRIDE_LO; ++j) {
+      float u = v[base + j], w = v[base + j + STRIDE_LO];
+      v[base + j] = u + w;
+      v[base + j + STRIDE_LO] = u - w;
+    }
+}
+
+__device__ __forceinline__ void fwht128_group(float (&v)[16], float* __restrict__ row, int li) {
+  // v: natural layout, positions li*16 + i.  row: 128(+pad) floats of LDS for this group.
+#pragma unroll
+  for (int q = 0; q < 4; ++q)
+    *reinterpret_cast<float4*>(row + li * 16 + 4 * q) = make_float4(v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]);
+  __syncthreads();
+#pragma unroll
+  for (int j = 0; j < 16; ++j) v[j] = row[li + 8 * j];
+  // positions li + 8j: level 64 pairs j<->j+8, 32: j<->j+4, 16: j<->j+2, 8: j<->j+1
+  butterflies<8, 1>(v);
+  butterflies<4, 1>(v);
+  butterflies<2, 1>(v);
+  butterflies<1, 1>(v);
+  __syncthreads();
+#pragma unroll
+  for (int j = 0; j < 16; ++j) row[li + 8 * j] = v[j];
+  __syncthreads();
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    float4 t = *reinterpret_cast<const float4*>(row + li * 16 + 4 * q);
+    v[4 * q] = t.x; v[4 * q + 1] = t.y; v[4 * q + 2] = t.z; v[4 * q + 3] = t.w;
+  }
+  // natural positions li*16 + i: level 4 pairs i<->i+4 (groups of 8), 2, 1
+  butterflies<4, 1>(v);
+  butterflies<2, 1>(v);
+  butterflies<1, 1>(v);
+}
+
+#define MXK_ROWPAD 132  // 128 + 4 floats: keeps float4 alignment, skews banks per row
+
+template <typename T, int MODE, int BITS>
+__global__ __launch_bounds__(256) void k_quant_had128(const T* __restrict__ x, int64_t n, int64_t nb,
+                                                      const float* __restrict__ signs,
+                                                      uint8_t* __restrict__ packed, int64_t packed_nbytes,
+                                                      int64_t n_store, float* __restrict__ scales, float qf) {
+  constexpr int E = 16, LPB = 8, GPW = 8, GPB = 32;
+  constexpr int NW = (E * BITS + 31) / 32;
+  constexpr int NB = E * BITS / 8;
+  constexpr uint32_t MASK = (1u << BITS) - 1u;
+  constexpr int H = MODE == Q_FP ? (1 << (BITS - 1)) : 1;
+  __shared__ float sP[H + 1];
+  __shared__ __attribute__((aligned(16))) float srow[GPB * MXK_ROWPAD];
+  if constexpr (MODE == Q_FP) build_tables<BITS>(sP, nullptr);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int g = lane / LPB, li = lane % LPB;
+  float* row = srow + (wave * GPW + g) * MXK_ROWPAD;
+  float sg[E];
+#pragma unroll
+  for (int i = 0; i < E; ++i) sg[i] = signs[li * 16 + i];
+  const float rdiv = 11.3137083f;           // fl32(sqrt(128))
+  const float rinv = 1.0f / 11.3137083f;
+  for (int64_t b0 = (int64_t)blockIdx.x * GPB; b0 < nb; b0 += (int64_t)gridDim.x * GPB) {
+    const int64_t blk = b0 + wave * GPW + g;
+    const int64_t idx = blk * 128 + (int64_t)li * E;
+    float v[E];
+    load_elems<T, E>(x, idx, n, v);
+#pragma unroll
+    for (int i = 0; i < E; ++i) v[i] = v[i] * sg[i];
+    fwht128_group(v, row, li);
+    float m = 0.0f;
+#pragma unroll
+    for (int i = 0; i < E; ++i) {
+      v[i] = div_rn(v[i], rdiv, rinv);
+      m = fmaxf(m, __builtin_fabsf(v[i]));
+    }
+    const float ap = fmaxf(group_max<LPB>(m), MXK_AMIN);
+    const BlockParams bp = block_params<MODE>(ap, qf);
+    uint32_t w[NW];
+#pragma unroll
+    for (int k = 0; k < NW; ++k) w[k] = 0u;
+#pragma unroll
+    for (int i = 0; i < E; ++i) {
+      uint32_t f = (uint32_t)encode<MODE, BITS>(v[i], bp, qf, sP) & MASK;
+      if (idx + i >= n_store) f = 0u;
+      w[(i * BITS) >> 5] |= f << ((i * BITS) & 31);
+    }
+    if (blk < nb) {
+      store_bytes<NB>(packed, idx * BITS / 8, packed_nbytes, w);
+      if (li == 0) scales[blk] = bp.s;
+    }
+  }
+}
+
+// Generic rotation: one workgroup per row, n = next_pow2(d) <= 8192 in LDS.
+// FWD: out[r, :d] = (WHT(pad(x[r]) * signs) / sqrt(n))[:d]
+// INV: out[r, :d] = (WHT(pad(x[r])) / sqrt(n) * signs)[:d]
+template <typename T, bool FWD>
+__global__ __launch_bounds__(256) void k_fwht_rows(const T* in, float* out,
+                                                   int64_t rows, int64_t d, int n, int logn,
+                                                   const float* __restrict__ signs, float rdiv, float rinv) {
+  extern __shared__ float sh[];
+  for (int64_t r = blockIdx.x; r < rows; r += gridDim.x) {
+    for (int i = threadIdx.x; i < n; i += blockDim.x) {
+      float v = i < d ? ElemT<T>::cvt(in[r * d + i]) : 0.0f;
+      if (FWD) v = v * signs[i];
+      sh[i] = v;
+    }
+    __syncthreads();
+    for (int lvl = logn - 1; lvl >= 0; --lvl) {
+      const int h = 1 << lvl;
+      for (int p = threadIdx.x; p < n / 2; p += blockDim.x) {
+        int i = ((p >> lvl) << (lvl + 1)) | (p & (h - 1));
+        float u = sh[i], w = sh[i + h];
+        sh[i] = u + w;
+        sh[i + h] = u - w;
+      }
+      __syncthreads();
+    }
+    for (int i = threadIdx.x; i < d; i += blockDim.x) {
+      float v = div_rn(sh[i], rdiv, rinv);
+      if (!FWD) v = v * signs[i];
+      out[r * d + i] = v;
+    }
+    __syncthreads();
+  }
+}
+
+// Large rotations (n > 8192): the input is first staged into a padded
+// [rows, n] float buffer (with signs for FWD), the levels n/2 ... 8192 run
+// as global passes, and the last 13 levels plus the division run in LDS.
+template <typename T, bool FWD>
+__global__ void k_fwht_stage(const T* __restrict__ in, float* __restrict__ buf, int64_t rows, int64_t d,
+                             int64_t n, const float* __restrict__ signs) {
+  int64_t total = rows * n;
+  for (int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; t < total; t += (int64_t)gridDim.x * blockDim.x) {
+    int64_t r = t / n, i = t % n;
+    float v = i < d ? ElemT<T>::cvt(in[r * d + i]) : 0.0f;
+    if (FWD) v = v * signs[i];
+    buf[t] = v;
+  }
+}
+
+__global__ void k_fwht_level(float* __restrict__ buf, int64_t rows, int64_t n, int64_t h) {
+  int64_t pairs = rows * (n / 2);
+  for (int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; t < pairs; t += (int64_t)gridDim.x * blockDim.x) {
+    int64_t r = t / (n / 2), p = t % (n / 2);
+    int64_t i = (p / h) * (2 * h) + (p % h);
+    float* row = buf + r * n;
+    float u = row[i], w = row[i + h];
+    row[i] = u + w;
+    row[i + h] = u - w;
+  }
+}
+
+// last 13 levels of each 8192-element segment, then division, signs, crop
+template <bool FWD>
+__global__ __launch_bounds__(256) void k_fwht_tail(const float* __restrict__ buf, float* __restrict__ out,
+                                                   int64_t rows, int64_t d, int64_t n,
+                                                   const float* __restrict__ signs, float rdiv, float rinv) {
+  constexpr int S = 8192;
+  extern __shared__ float sh[];
+  const int64_t segs = rows * (n / S);
+  for (int64_t sgi = blockIdx.x; sgi < segs; sgi += gridDim.x) {
+    const int64_t r = sgi / (n / S), off = (sgi % (n / S)) * S;
+    const float* src = buf + r * n + off;
+    for (int i = threadIdx.x; i < S; i += blockDim.x) sh[i] = src[i];
+    __syncthreads();
+    for (int lvl = 12; lvl >= 0; --lvl) {
+      const int h = 1 << lvl;
+      for (int p = threadIdx.x; p < S / 2; p += blockDim.x) {
+        int i = ((p >> lvl) << (lvl + 1)) | (p & (h - 1));
+        float u = sh[i], w = sh[i + h];
+        sh[i] = u + w;
+        sh[i + h] = u - w;
+      }
+      __syncthreads();
+    }
+    for (int i = threadIdx.x; i < S; i += blockDim.x) {
+      int64_t col = off + i;
+      if (col < d) {
+        float v = div_rn(sh[i], rdiv, rinv);
+        if (!FWD) v = v * signs[col];
+        out[r * d + col] = v;
+      }
+    }
+    __syncthreads();
+  }
+}
+
+// ---------------------------------------------------------------- dequantize
+// One lane per 4 outputs.  Fields are read from the packed buffer (only
+// bytes below packed_nbytes), sign-extended, and decoded as
+//   int: RN(code * s)   int1: code==0 ? s : -s   float: RN(G[idx] * s).
+template <int MODE, int BITS>
+__global__ __launch_bounds__(256) void k_dequant(const uint8_t* __restrict__ packed, int64_t packed_nbytes,
+                                                 const float* __restrict__ scales, int64_t nb, int64_t n,
+                                                 int block, float* __restrict__ out) {
+  constexpr int H = MODE == Q_FP ? (1 << (BITS - 1)) : 1;
+  __shared__ float sG[2 * H];
+  if constexpr (MODE == Q_FP) build_tables<BITS>(nullptr, sG);
+  constexpr bool WORDS = !(BITS == 1 || BITS == 2 || BITS == 4 || BITS == 8);
+  constexpr int PER = WORDS ? 32 / BITS : 8 / BITS;
+  constexpr uint32_t MASK = BITS >= 32 ? 0xFFFFFFFFu : ((1u << BITS) - 1u);
+  const int64_t quads = (n + 3) / 4;
+  for (int64_t q = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; q < quads; q += (int64_t)gridDim.x * blockDim.x) {
+    float r[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int64_t j = q * 4 + i;
+      uint32_t f = 0u;
+      const int64_t unit = j / PER;
+      const int sh = (int)(j % PER) * BITS;
+      if (WORDS) {
+        if (unit * 4 + 3 < packed_nbytes) f = (reinterpret_cast<const uint32_t*>(packed)[unit] >> sh) & MASK;
+      } else {
+        if (unit < packed_nbytes) f = ((uint32_t)packed[unit] >> sh) & MASK;
+      }
+      const int64_t b = j / block;
+      const float s = (j < n && b < nb) ? scales[b] : 0.0f;
+      float val;
+      if constexpr (MODE == Q_INT1) {
+        val = f == 0u ? s : -s;
+      } else if constexpr (MODE == Q_FP) {
+        val = sG[f] * s;
+      } else {
+        int32_t c = BITS >= 32 ? (int32_t)f : ((int32_t)(f << (32 - BITS)) >> (32 - BITS));
+        val = (float)c * s;
+      }
+      r[i] = val;
+    }
+    const int64_t j0 = q * 4;
+    if (j0 + 4 <= n && ((reinterpret_cast<uintptr_t>(out) & 15u) == 0)) {
+      *reinterpret_cast<float4*>(out + j0) = make_float4(r[0], r[1], r[2], r[3]);
+    } else {
+      for (int i = 0; i < 4; ++i)
+        if (j0 + i < n) out[j0 + i] = r[i];
+    }
+  }
+}
+
+// ---------------------------------------------------------------- host dispatch
+static int grid_for(int64_t work_items, int per_block) {
+  int64_t blocks = ceil_div(work_items, per_block);
+  int64_t cap = (int64_t)num_cus() * 8;
+  return (int)std::max<int64_t>(1, std::min<int64_t>(blocks, cap));
+}
+
+static float qmax_for(int kind, int bits, int variant) {
+  (void)kind;
+  (void)variant;
+  if (bits == 1) return 1.0f;
+  return (float)((1u << (bits - 1)) - 1u);
+}
+
+static int mode_for(int kind, int bits, int variant) {
+  if (kind == MXK_KIND_FLOAT) return Q_FP;
+  if (variant == MXK_VAR_VECTOR) return Q_VEC;
+  if (bits == 1) return Q_INT1;
+  return Q_INT;
+}
+
+template <typename T, int MODE, int BITS, int E>
+static void launch_fast_b(const T* x, int64_t n, int64_t nb, int block, uint8_t* packed, int64_t pbytes,
+                          int64_t n_store, float* scales, float qf, hipStream_t st, bool* done) {
+  auto go = [&](auto lpb_tag) {
+    constexpr int LPB = decltype(lpb_tag)::value;
+    constexpr int GPB = 4 * (64 / LPB);
+    hipLaunchKernelGGL((k_quant_fast<T, E, LPB, MODE, BITS>), dim3(grid_for(nb, GPB)), dim3(256), 0, st, x, n, nb,
+                       packed, pbytes, n_store, scales, qf);
+    *done = true;
+  };
+  switch (block / E) {
+    case 2: go(std::integral_constant<int, 2>()); break;
+    case 4: go(std::integral_constant<int, 4>()); break;
+    case 8: go(std::integral_constant<int, 8>()); break;
+    case 16: go(std::integral_constant<int, 16>()); break;
+    case 32: go(std::integral_constant<int, 32>()); break;
+    case 64: go(std::integral_constant<int, 64>()); break;
+    default: break;
+  }
+}
+
+template <typename T, int MODE, int BITS>
+static bool try_fast(const T* x, int64_t n, int64_t nb, int block, uint8_t* packed, int64_t pbytes,
+                     int64_t n_store, float* scales, float qf, hipStream_t st) {
+  constexpr int PER16 = 16 / (int)sizeof(T);
+  constexpr int E = (8 / BITS) > PER16 ? (8 / BITS) : PER16;
+  if (block % E != 0 || !is_pow2(block / E) || block / E > 64 || block / E < 2) return false;
+  if (!aligned16(x) || (E * BITS) % 8 != 0) return false;
+  const int NB = E * BITS / 8;
+  if ((reinterpret_cast<uintptr_t>(packed) % (uintptr_t)(NB >= 16 ? 16 : NB)) != 0) return false;
+  bool done = false;
+  launch_fast_b<T, MODE, BITS, E>(x, n, nb, block, packed, pbytes, n_store, scales, qf, st, &done);
+  return done;
+}
+
+template <typename T, int MODE, int BITS>
+static int run_generic(const T* x, int64_t n, int64_t nb, int block, int bits, uint8_t* packed, int64_t pbytes,
+                       int64_t n_store, float* scales, float qf, void* ws, size_t ws_bytes, hipStream_t st) {
+  if (ws == nullptr || ws_bytes < (size_t)nb * sizeof(float2))
+    return fail(MXK_EINVAL, "quantize: workspace too small for the generic path");
+  float2* params = reinterpret_cast<float2*>(ws);
+  hipLaunchKernelGGL((k_block_params<T, MODE>), dim3(grid_for(nb, 4)), dim3(256), 0, st, x, n, nb, block, qf, scales,
+                     params);
+  const bool words = !(bits == 1 || bits == 2 || bits == 4 || bits == 8);
+  const int64_t units = words ? pbytes / 4 : pbytes;
+  hipLaunchKernelGGL((k_pack_generic<T, MODE, BITS>), dim3(grid_for(units, 256)), dim3(256), 0, st, x, n, block, qf,
+                     params, bits, n_store, packed, pbytes);
+  return check_launch("quantize(generic)");
+}
+
+template <typename T>
+static int quantize_t(const T* x, int64_t n, int kind, int bits, int variant, int block, uint8_t* packed,
+                      int64_t pbytes, float* scales, int64_t n_store, void* ws, size_t ws_bytes, hipStream_t st) {
+  const int64_t nb = ceil_div(n, block);
+  const int mode = mode_for(kind, bits, variant);
+  const float qf = qmax_for(kind, bits, variant);
+#define MXK_TRY(MODE, BITS)                                                                               \
+  if (mode == MODE && bits == BITS) {                                                                     \
+    if (try_fast<T, MODE, BITS>(x, n, nb, block, packed, pbytes, n_store, scales, qf, st))               \
+      return check_launch("quantize");                                                                    \
+    return run_generic<T, MODE, BITS>(x, n, nb, block, bits, packed, pbytes, n_store, scales, qf, ws, ws_bytes, st); \
+  }
+  MXK_TRY(Q_INT, 2)
+  MXK_TRY(Q_INT, 4)
+  MXK_TRY(Q_INT, 8)
+  MXK_TRY(Q_INT, 16)
+  MXK_TRY(Q_INT1, 1)
+  MXK_TRY(Q_VEC, 2)
+  MXK_TRY(Q_VEC, 4)
+  MXK_TRY(Q_VEC, 8)
+  MXK_TRY(Q_VEC, 16)
+  MXK_TRY(Q_FP, 4)
+  MXK_TRY(Q_FP, 8)
+#undef MXK_TRY
+#define MXK_GEN(MODE, BITS) \
+  if (mode == MODE && bits == BITS) return run_generic<T, MODE, BITS>(x, n, nb, block, bits, packed, pbytes, n_store, scales, qf, ws, ws_bytes, st);
+  MXK_GEN(Q_INT, 3)
+  MXK_GEN(Q_INT, 5)
+  MXK_GEN(Q_INT, 6)
+  MXK_GEN(Q_INT, 7)
+  MXK_GEN(Q_VEC, 1)
+  MXK_GEN(Q_VEC, 3)
+  MXK_GEN(Q_VEC, 5)
+  MXK_GEN(Q_VEC, 6)
+  MXK_GEN(Q_VEC, 7)
+#undef MXK_GEN
+  return fail(MXK_EUNSUPPORTED, "quantize: unsupported kind/bits/variant combination");
+}
+
+template <typename T>
+static bool try_had128(const T* x, int64_t n, int mode, int bits, const float* signs, uint8_t* packed,
+                       int64_t pbytes, int64_t n_store, float* scales, float qf, hipStream_t st) {
+  if (!aligned16(x)) return false;
+  const int64_t nb = ceil_div(n, 128);
+  const int grid = grid_for(nb, 32);
+#define MXK_H(MODE, BITS)                                                                                   \
+  if (mode == MODE && bits == BITS) {                                                                       \
+    hipLaunchKernelGGL((k_quant_had128<T, MODE, BITS>), dim3(grid), dim3(256), 0, st, x, n, nb, signs, packed, \
+                       pbytes, n_store, scales, qf);                                                        \
+    return true;                                                                                            \
+  }
+  MXK_H(Q_INT, 2)
+  MXK_H(Q_INT, 4)
+  MXK_H(Q_INT, 8)
+  MXK_H(Q_INT1, 1)
+  MXK_H(Q_FP, 4)
+  MXK_H(Q_FP, 8)
+#undef MXK_H
+  return false;
+}
+
+// Rotate rows of d (padded to n) into a float buffer `rot` [rows, d].
+template <typename T, bool FWD>
+static int rotate_rows(const T* in, float* rot, int64_t rows, int64_t d, const float* signs, void* ws,
+                       size_t ws_bytes, hipStream_t st) {
+  const int64_t n = next_pow2(d);
+  int logn = 0;
+  while ((int64_t(1) << logn) < n) ++logn;
+  const float rdiv = (float)std::sqrt((double)n);
+  const float rinv = 1.0f / rdiv;
+  if (n <= 8192) {
+    const int grid = (int)std::min<int64_t>(rows, (int64_t)num_cus() * 8);
+    hipLaunchKernelGGL((k_fwht_rows<T, FWD>), dim3(std::max(grid, 1)), dim3(256), n * sizeof(float), st, in, rot, rows,
+                       d, (int)n, logn, signs, rdiv, rinv);
+    return check_launch("rotate");
+  }
+  if (ws == nullptr || ws_bytes < (size_t)(rows * n) * sizeof(float))
+    return fail(MXK_EINVAL, "rotation: workspace too small");
+  float* buf = reinterpret_cast<float*>(ws);
+  const int g = grid_for(rows * n, 256);
+  hipLaunchKernelGGL((k_fwht_stage<T, FWD>), dim3(g), dim3(256), 0, st, in, buf, rows, d, n, signs);
+  for (int64_t h = n / 2; h >= 8192; h /= 2)
+    hipLaunchKernelGGL(k_fwht_level, dim3(grid_for(rows * n / 2, 256)), dim3(256), 0, st, buf, rows, n, h);
+  const int gt = (int)std::min<int64_t>(rows * (n / 8192), (int64_t)num_cus() * 4);
+  hipLaunchKernelGGL((k_fwht_tail<FWD>), dim3(gt), dim3(256), 8192 * sizeof(float), st, buf, rot, rows, d, n, signs,
+                     rdiv, rinv);
+  return check_launch("rotate(large)");
+}
+
+static size_t rot_ws_bytes(int64_t n, int64_t d) {
+  // rotated copy [n] floats + staging [rows, next_pow2(d)] when next_pow2(d) > 8192
+  const int64_t np = next_pow2(d);
+  size_t bytes = (size_t)n * sizeof(float);
+  if (np > 8192) bytes += (size_t)(n / d) * (size_t)np * sizeof(float);
+  return bytes;
+}
+
+template <int MODE, int BITS>
+static int launch_dequant(const void* packed, int64_t pbytes, const float* scales, int64_t nb, int64_t n, int block,
+                          float* out, hipStream_t st) {
+  hipLaunchKernelGGL((k_dequant<MODE, BITS>), dim3(grid_for(ceil_div(n, 4), 256)), dim3(256), 0, st,
+                     reinterpret_cast<const uint8_t*>(packed), pbytes, scales, nb, n, block, out);
+  return check_launch("dequantize");
+}
+
+int requant_vec_f32(const float* x, int64_t n, int bits, int block, void* packed, int64_t packed_nbytes,
+                    float* scales, int64_t n_store, void* ws, size_t ws_bytes, hipStream_t st) {
+  return quantize_t<float>(x, n, MXK_KIND_INT, bits, MXK_VAR_VECTOR, block, reinterpret_cast<uint8_t*>(packed),
+                           packed_nbytes, scales, n_store, ws, ws_bytes, st);
+}
+
+}  // namespace mxk
+
+using namespace mxk;
+
+extern "C" {
+
+int mxk_abi_version(void) { return MXK_ABI_VERSION; }
+
+const char* mxk_last_error(void) { return g_err.c_str(); }
+
+int64_t mxk_packed_nbytes(int bits, int64_t n_codes) {
+  if (n_codes < 0 || bits <= 0 || bits > 16) return -1;
+  if (bits == 1 || bits == 2 || bits == 4 || bits == 8) return ceil_div(n_codes, 8 / bits);
+  return 4 * ceil_div(n_codes, 32 / bits);
+}
+
+int mxk_float_grid(int bits, float* grid, float* mids) {
+  if (bits != 4 && bits != 8) return fail(MXK_EUNSUPPORTED, "float grid: bits must be 4 or 8");
+  const int H = 1 << (bits - 1);
+  std::vector<float> g(H);
+  for (int c = 0; c < H; ++c) g[c] = fmt_value(bits, c) / fmt_max(bits);
+  if (grid) {
+    for (int c = 0; c < H; ++c) {
+      grid[H + c] = g[c];
+      grid[H - 1 - c] = -g[c];
+    }
+  }
+  if (mids) {
+    for (int j = 1; j < H; ++j) {
+      float s = g[j - 1] + g[j];
+      mids[H - 1 + j] = s * 0.5f;
+      mids[H - 1 - j] = -(s * 0.5f);
+    }
+    mids[H - 1] = 0.0f;
+  }
+  return MXK_OK;
+}
+
+size_t mxk_quantize_workspace(int64_t n, int kind, int bits, int variant, int block, int64_t rot_dim) {
+  (void)kind;
+  (void)bits;
+  if (n <= 0 || block <= 0) return 0;
+  size_t bytes = (size_t)ceil_div(n, block) * sizeof(float2) + 256;
+  if (variant == MXK_VAR_HADAMARD && rot_dim > 0) bytes += rot_ws_bytes(n, rot_dim) + 256;
+  return bytes;
+}
+
+int mxk_quantize(const void* x, int x_type, int64_t n, int kind, int bits, int variant, int block,
+                 const float* signs, int64_t rot_dim, void* packed, int64_t packed_nbytes, float* scales,
+                 int64_t n_store, void* workspace, size_t workspace_nbytes, void* stream) {
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  if (n <= 0) return fail(MXK_EINVAL, "quantize: n must be positive");
+  if (block <= 0) return fail(MXK_EINVAL, "quantize: block must be positive");
+  if (!x || !packed || !scales) return fail(MXK_EINVAL, "quantize: null pointer");
+  if (kind == MXK_KIND_FLOAT && bits != 4 && bits != 8)
+    return fail(MXK_EUNSUPPORTED, "quantize: float kinds support bits 4 and 8");
+  if (kind == MXK_KIND_INT && !((bits >= 1 && bits <= 8) || bits == 16))
+    return fail(MXK_EUNSUPPORTED, "quantize: int kinds support bits 1..8 and 16");
+  const int64_t nb = ceil_div(n, block);
+  if (n_store < 0 || n_store > nb * block) return fail(MXK_EINVAL, "quantize: n_store out of range");
+  if (packed_nbytes < mxk_packed_nbytes(bits, n_store)) return fail(MXK_EINVAL, "quantize: packed buffer too small");
+  if (x_type != MXK_IN_F32 && x_type != MXK_IN_F16 && x_type != MXK_IN_BF16)
+    return fail(MXK_EINVAL, "quantize: bad input type");
+  uint8_t* pk = reinterpret_cast<uint8_t*>(packed);
+  const int mode = mode_for(kind, bits, variant);
+  const float qf = qmax_for(kind, bits, variant);
+
+  if (variant == MXK_VAR_HADAMARD) {
+    if (!signs || rot_dim <= 0 || n % rot_dim != 0)
+      return fail(MXK_EINVAL, "quantize: hadamard needs signs and a rot_dim dividing n");
+    if (rot_dim == 128 && block == 128) {
+      bool ok = false;
+      if (x_type == MXK_IN_F32) ok = try_had128<float>((const float*)x, n, mode, bits, signs, pk, packed_nbytes, n_store, scales, qf, st);
+      else if (x_type == MXK_IN_F16) ok = try_had128<__half>((const __half*)x, n, mode, bits, signs, pk, packed_nbytes, n_store, scales, qf, st);
+      else ok = try_had128<hip_bfloat16>((const hip_bfloat16*)x, n, mode, bits, signs, pk, packed_nbytes, n_store, scales, qf, st);
+      if (ok) return check_launch("quantize(hadamard128)");
+    }
+    // rotate into the workspace, then quantize the float32 rotated copy
+    const size_t need = mxk_quantize_workspace(n, kind, bits, variant, block, rot_dim);
+    if (!workspace || workspace_nbytes < need) return fail(MXK_EINVAL, "quantize: workspace too small");
+    uint8_t* wsb = reinterpret_cast<uint8_t*>(workspace);
+    const size_t pbytes_params = ((size_t)nb * sizeof(float2) + 255) & ~(size_t)255;
+    float* rot = reinterpret_cast<float*>(wsb + pbytes_params);
+    void* stage = wsb + pbytes_params + (((size_t)n * sizeof(float) + 255) & ~(size_t)255);
+    size_t stage_bytes = workspace_nbytes - (pbytes_params + (((size_t)n * sizeof(float) + 255) & ~(size_t)255));
+    const int64_t rows = n / rot_dim;
+    int rc;
+    if (x_type == MXK_IN_F32) rc = rotate_rows<float, true>((const float*)x, rot, rows, rot_dim, signs, stage, stage_bytes, st);
+    else if (x_type == MXK_IN_F16) rc = rotate_rows<__half, true>((const __half*)x, rot, rows, rot_dim, signs, stage, stage_bytes, st);
+    else rc = rotate_rows<hip_bfloat16, true>((const hip_bfloat16*)x, rot, rows, rot_dim, signs, stage, stage_bytes, st);
+    if (rc != MXK_OK) return rc;
+    return quantize_t<float>(rot, n, kind, bits, MXK_VAR_BASE, block, pk, packed_nbytes, scales, n_store, wsb,
+                             pbytes_params, st);
+  }
+  if (variant != MXK_VAR_BASE && variant != MXK_VAR_VECTOR) return fail(MXK_EUNSUPPORTED, "quantize: bad variant");
+  (void)mode;
+  (void)qf;
+  if (x_type == MXK_IN_F32)
+    return quantize_t<float>((const float*)x, n, kind, bits, variant, block, pk, packed_nbytes, scales, n_store,
+                             workspace, workspace_nbytes, st);
+  if (x_type == MXK_IN_F16)
+    return quantize_t<__half>((const __half*)x, n, kind, bits, variant, block, pk, packed_nbytes, scales, n_store,
+                              workspace, workspace_nbytes, st);
+  return quantize_t<hip_bfloat16>((const hip_bfloat16*)x, n, kind, bits, variant, block, pk, packed_nbytes, scales,
+                                  n_store, workspace, workspace_nbytes, st);
+}
+
+int mxk_dequantize(const void* packed, int64_t packed_nbytes, const float* scales, int64_t nb, int64_t n, int kind,
+                   int bits, int variant, int block, const float* signs, int64_t rot_dim, float* out,
+                   void* workspace, size_t workspace_nbytes, void* stream) {
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  if (n <= 0 || block <= 0 || nb <= 0) return fail(MXK_EINVAL, "dequantize: sizes must be positive");
+  if (!packed || !scales || !out) return fail(MXK_EINVAL, "dequantize: null pointer");
+  const int mode = mode_for(kind, bits, variant == MXK_VAR_VECTOR ? MXK_VAR_BASE : variant);
+  int rc = MXK_EUNSUPPORTED;
+#define MXK_D(MODE, BITS) \
+  else if (mode == MODE && bits == BITS) rc = launch_dequant<MODE, BITS>(packed, packed_nbytes, scales, nb, n, block, out, st);
+  if (false) {
+  }
+  MXK_D(Q_INT1, 1)
+  MXK_D(Q_INT, 2)
+  MXK_D(Q_INT, 3)
+  MXK_D(Q_INT, 4)
+  MXK_D(Q_INT, 5)
+  MXK_D(Q_INT, 6)
+  MXK_D(Q_INT, 7)
+  MXK_D(Q_INT, 8)
+  MXK_D(Q_INT, 16)
+  MXK_D(Q_FP, 4)
+  MXK_D(Q_FP, 8)
+  else return fail(MXK_EUNSUPPORTED, "dequantize: unsupported kind/bits");
+#undef MXK_D
+  if (rc != MXK_OK) return rc;
+  if (variant == MXK_VAR_HADAMARD) {
+    if (!signs || rot_dim <= 0 || n % rot_dim != 0)
+      return fail(MXK_EINVAL, "dequantize: hadamard needs signs and a rot_dim dividing n");
+    // in-place unrotation of out viewed as [n/rot_dim, rot_dim]
+    const int64_t np = next_pow2(rot_dim);
+    if (np <= 8192) return rotate_rows<float, false>(out, out, n / rot_dim, rot_dim, signs, nullptr, 0, st);
+    if (!workspace || workspace_nbytes < (size_t)(n / rot_dim) * (size_t)np * sizeof(float))
+      return fail(MXK_EINVAL, "dequantize: workspace too small for the large rotation");
+    return rotate_rows<float, false>(out, out, n / rot_dim, rot_dim, signs, workspace, workspace_nbytes, st);
+  }
+  return MXK_OK;
+}
+
+size_t mxk_dequantize_workspace(int64_t n, int variant, int64_t rot_dim) {
+  if (variant != MXK_VAR_HADAMARD || rot_dim <= 0) return 0;
+  const int64_t np = next_pow2(rot_dim);
+  if (np <= 8192) return 0;
+  return (size_t)(n / rot_dim) * (size_t)np * sizeof(float);
+}
+
+}  // extern "C"

@@ -1,0 +1,241 @@
+"""Functional entry points of the hot path, on GPU tensors, through libmxk.so.
+
+Each function keeps the signature and return convention of the reference
+function it replaces:
+
+  quantize(x, dt, block) -> (packed, scales, n)         mxtorch.py:1684-1763
+  _dequant(packed, scales, dt, n, block) -> float32[n]   mxtorch.py:1530-1597
+  _qscale_gemm(...) -> (packed, scales[, C])             mxtorch.py:1299-1385, 5497-5573
+  linear_wq(x, w_packed, w_scales, dt, K, N, block)      mxtorch.py:7454-7473
+
+Inputs must live on a GPU; every computation is a HIP kernel (no CPU path).
+"""
+from __future__ import annotations
+
+import math
+from typing import Optional, Tuple
+
+import torch
+
+from . import _lib as L
+from .dtypes import get_mx_dtype, matmul_output_dtype, mx_dtype
+
+Tensor = torch.Tensor
+
+# dequantize of Hadamard ('h') dtypes: "rows" inverts exactly the rotation
+# quantize() applied (rows of the last dimension); "reference" reproduces the
+# reference's whole-tensor unrotation (mxtorch.py:1582-1595), which is the
+# inverse only for 1-D tensors.  Both agree on 1-D tensors.
+HADAMARD_DEQUANT_MODE = "rows"
+
+_SIGNS_CACHE = {}
+
+
+def packed_nbytes(bits: int, n_codes: int) -> int:
+    return int(L.lib().mxk_packed_nbytes(bits, n_codes))
+
+
+def packed_storage(bits: int, n_codes: int, device) -> Tensor:
+    """Empty packed buffer with the reference's dtype and length: int8 of
+    ceil(n/(8/bits)) for bits in {1,2,4,8}, else int32 words (mxtorch.py:882-955)."""
+    nbytes = packed_nbytes(bits, n_codes)
+    if bits in (1, 2, 4, 8):
+        return torch.empty(nbytes, dtype=torch.int8, device=device)
+    return torch.empty(nbytes // 4, dtype=torch.int32, device=device)
+
+
+def reference_hadamard_seed(dt: mx_dtype) -> int:
+    """The seed quantize() uses for 'h' dtypes: hash(name) % 2**31
+    (mxtorch.py:1723).  Python salts str hashes per process unless
+    PYTHONHASHSEED is fixed, exactly as in the reference."""
+    return hash(dt.name) % (2 ** 31)
+
+
+def hadamard_signs(n: int, seed: int, device) -> Tensor:
+    """Sign vector of hadamard_rotation(n, seed) (mxtorch.py:2856-2864): the
+    CPU generator's randint(0, 2, (n,)) * 2 - 1, moved to the device.  This
+    builds the rotation's parameters (n values); no tensor data touches it."""
+    key = (n, seed, str(device))
+    s = _SIGNS_CACHE.get(key)
+    if s is None:
+        gen = torch.Generator()
+        gen.manual_seed(seed)
+        s = (torch.randint(0, 2, (n,), generator=gen).float() * 2 - 1).to(device)
+        _SIGNS_CACHE[key] = s
+    return s
+
+
+def _pow2(d: int) -> int:
+    return 1 << math.ceil(math.log2(max(d, 1)))
+
+
+def rotation_dim(shape) -> int:
+    """Length quantize() rotates for 'h' dtypes (mxtorch.py:1721)."""
+    shape = tuple(shape)
+    if len(shape) >= 2:
+        return int(shape[-1])
+    return int(math.prod(shape)) if shape else 1
+
+
+def _kind_variant(dt: mx_dtype):
+    kind = L.MXK_KIND_FLOAT if dt.is_float else L.MXK_KIND_INT
+    if dt.is_hadamard:
+        var = L.MXK_VAR_HADAMARD
+    elif dt.is_vector:
+        var = L.MXK_VAR_VECTOR
+    elif dt.variant == "":
+        var = L.MXK_VAR_BASE
+    else:
+        raise L.MXKError(f"variant {dt.variant!r} of {dt.name} is outside this build's hot path "
+                         f"(base, 'h' and 'v' variants are implemented)")
+    return kind, var
+
+
+def _workspace(nbytes: int, device) -> Optional[Tensor]:
+    if nbytes <= 0:
+        return None
+    return torch.empty(int(nbytes), dtype=torch.uint8, device=device)
+
+
+def quantize(x: Tensor, dt, block: int = 128, *, seed: Optional[int] = None,
+             signs: Optional[Tensor] = None, n_store: Optional[int] = None
+             ) -> Tuple[Tensor, Tensor, int]:
+    """quantize(x, dt, block) -> (packed, scales, n) on the GPU (mxtorch.py:1684-1763)."""
+    dt = get_mx_dtype(dt)
+    dev = L.require_gpu(x)
+    kind, var = _kind_variant(dt)
+    if x.dtype not in (torch.float32, torch.float16, torch.bfloat16):
+        x = x.float()
+    xc = x.contiguous()
+    n = xc.numel()
+    if n == 0:
+        raise L.MXKError("quantize: empty tensor")
+    nb = -(-n // block)
+    if n_store is None:
+        n_store = nb * block
+    packed = packed_storage(dt.bits, n_store, dev)
+    scales = torch.empty(nb, dtype=torch.float32, device=dev)
+    rot_dim = 0
+    sg = None
+    if var == L.MXK_VAR_HADAMARD:
+        rot_dim = rotation_dim(x.shape)
+        if signs is None:
+            signs = hadamard_signs(_pow2(rot_dim), reference_hadamard_seed(dt) if seed is None else seed, dev)
+        sg = signs.to(device=dev, dtype=torch.float32).contiguous()
+    lib = L.lib()
+    ws_bytes = lib.mxk_quantize_workspace(n, kind, dt.bits, var, block, rot_dim)
+    ws = _workspace(ws_bytes, dev)
+    with torch.cuda.device(dev):
+        rc = lib.mxk_quantize(xc.data_ptr(), L.elem_type(xc.dtype), n, kind, dt.bits, var, block,
+                              L.ptr(sg), rot_dim, packed.data_ptr(), packed.numel() * packed.element_size(),
+                              scales.data_ptr(), n_store, L.ptr(ws), ws_bytes, L.stream_of(xc))
+    L.check(rc, f"quantize({dt.name}, block={block})")
+    return packed, scales, n
+
+
+def _dequant(packed: Tensor, scales: Tensor, dt, n: int, block: int, *, orig_shape=None,
+             seed: Optional[int] = None, signs: Optional[Tensor] = None,
+             hadamard_mode: Optional[str] = None) -> Tensor:
+    """_dequant(packed, scales, dt, n, block) -> float32 [n] (mxtorch.py:1530-1597)."""
+    dt = get_mx_dtype(dt)
+    dev = L.require_gpu(packed, scales)
+    kind, var = _kind_variant(dt)
+    if dt.is_float and dt.bits not in (4, 8):
+        raise L.MXKError(f"dequantize: {dt.name} grids are outside this build (float4/float8 only)")
+    pk = packed.contiguous()
+    sc = scales.contiguous().float()
+    out = torch.empty(n, dtype=torch.float32, device=dev)
+    rot_dim = 0
+    sg = None
+    if var == L.MXK_VAR_HADAMARD:
+        mode = hadamard_mode or HADAMARD_DEQUANT_MODE
+        rot_dim = n if (mode == "reference" or orig_shape is None) else rotation_dim(orig_shape)
+        if signs is None:
+            signs = hadamard_signs(_pow2(rot_dim), reference_hadamard_seed(dt) if seed is None else seed, dev)
+        sg = signs.to(device=dev, dtype=torch.float32).contiguous()
+    lib = L.lib()
+    ws_bytes = lib.mxk_dequantize_workspace(n, var, rot_dim)
+    ws = _workspace(ws_bytes, dev)
+    with torch.cuda.device(dev):
+        rc = lib.mxk_dequantize(pk.data_ptr(), pk.numel() * pk.element_size(), sc.data_ptr(), sc.numel(), n,
+                                kind, dt.bits, var, block, L.ptr(sg), rot_dim, out.data_ptr(), L.ptr(ws),
+                                ws_bytes, L.stream_of(pk))
+    L.check(rc, f"dequantize({dt.name})")
+    return out
+
+
+def qscale_gemm(a_packed: Tensor, a_scales: Tensor, b_packed: Tensor, b_scales: Tensor,
+                M: int, K: int, N: int, bits: int, block: int, out_bits: int, *,
+                want_packed: bool = True, want_c: bool = False, want_acc: bool = False):
+    """The packed GEMM of _dispatch_qgemm's CPU branch (mxtorch.py:5563-5573,
+    _qscale_matmul mxtorch.py:1299-1385) on MFMA.
+
+    Returns a dict with any of: "packed" (out_bits codes of the requantized C,
+    M*N codes), "scales" ([ceil(M*N/block)]), "c" (float32 [M, N] before
+    requantization), "acc" (int32 [ceil(K/block), M, N], per-K-block integer
+    products)."""
+    dev = L.require_gpu(a_packed, a_scales, b_packed, b_scales)
+    out = {}
+    cp = cs = cf = acc = None
+    if want_packed:
+        cp = packed_storage(out_bits, M * N, dev)
+        cs = torch.empty(-(-(M * N) // block), dtype=torch.float32, device=dev)
+        out["packed"], out["scales"] = cp, cs
+    if want_c:
+        cf = torch.empty(M, N, dtype=torch.float32, device=dev)
+        out["c"] = cf
+    if want_acc:
+        acc = torch.empty(-(-K // block), M, N, dtype=torch.int32, device=dev)
+        out["acc"] = acc
+    ap, asc = a_packed.contiguous(), a_scales.contiguous().float()
+    bp, bsc = b_packed.contiguous(), b_scales.contiguous().float()
+    lib = L.lib()
+    ws_bytes = lib.mxk_qgemm_workspace(M, K, N, bits, block, out_bits if want_packed else 0)
+    ws = _workspace(ws_bytes, dev)
+    with torch.cuda.device(dev):
+        rc = lib.mxk_qgemm(ap.data_ptr(), asc.data_ptr(), asc.numel(), bp.data_ptr(), bsc.data_ptr(), bsc.numel(),
+                           M, K, N, bits, block, out_bits if want_packed else 0,
+                           L.ptr(cp), 0 if cp is None else cp.numel() * cp.element_size(), L.ptr(cs), L.ptr(cf),
+                           L.ptr(acc), L.ptr(ws), ws_bytes, L.stream_of(ap))
+    L.check(rc, f"qgemm(bits={bits}, {M}x{K}x{N})")
+    return out
+
+
+def linear_wq(x: Tensor, w_packed: Tensor, w_scales: Tensor, dt, in_features: int, out_features: int,
+              block: int = 128, bias: Optional[Tensor] = None) -> Tensor:
+    """y = x.float() @ dequant(W) (+ bias) for W stored as quantize(weight.t())
+    ([in, out] row-major, mxtorch.py:7447), fused: the weight is never
+    dequantized to memory (mx_linear.forward, mxtorch.py:7454-7473)."""
+    dt = get_mx_dtype(dt)
+    dev = L.require_gpu(x, w_packed, w_scales)
+    kind, var = _kind_variant(dt)
+    if var != L.MXK_VAR_BASE:
+        raise L.MXKError(f"linear_wq: {dt.name} weights need the base variant")
+    lead = x.shape[:-1]
+    K, N = in_features, out_features
+    if x.shape[-1] != K:
+        raise L.MXKError(f"linear_wq: x has {x.shape[-1]} features, weight expects {K}")
+    xc = x.reshape(-1, K)
+    if xc.dtype not in (torch.float32, torch.float16, torch.bfloat16):
+        xc = xc.float()
+    xc = xc.contiguous()
+    M = xc.shape[0]
+    out = torch.empty(M, N, dtype=torch.float32, device=dev)
+    b = None if bias is None else bias.to(device=dev, dtype=torch.float32).contiguous()
+    lib = L.lib()
+    ws_bytes = lib.mxk_linear_workspace(M, K, N, dt.bits, block)
+    ws = _workspace(ws_bytes, dev)
+    with torch.cuda.device(dev):
+        rc = lib.mxk_linear_wq(xc.data_ptr(), L.elem_type(xc.dtype), M, K, w_packed.contiguous().data_ptr(),
+                               w_scales.contiguous().data_ptr(), N, kind, dt.bits, block, L.ptr(b),
+                               out.data_ptr(), L.ptr(ws), ws_bytes, L.stream_of(xc))
+    L.check(rc, f"linear_wq({dt.name}, M={M}, K={K}, N={N})")
+    return out.reshape(*lead, N)
+
+
+def float_grid(bits: int) -> Tuple[Tensor, Tensor]:
+    """(grid, mids) as the library builds them (host copy, no GPU needed)."""
+    g = torch.empty(1 << bits, dtype=torch.float32)
+    m = torch.empty((1 << bits) - 1, dtype=torch.float32)
+    L.check(L.lib().mxk_float_grid(bits, g.data_ptr(), m.data_ptr()), "float_grid")
+    return g, m

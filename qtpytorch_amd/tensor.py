@@ -1,0 +1,352 @@
+"""mx_tensor: the packed quantized tensor, with the reference's API and layout.
+
+Mirrors mxtorch.mx_tensor (mxtorch.py:6028-6425): a torch.Tensor subclass
+over a 0-d placeholder that carries
+
+    _mx_packed      int8 bytes (bits 1/2/4/8) or int32 words (other widths)
+    _mx_scales      float32 [ceil(n / block)]
+    _mx_dtype       mx_dtype
+    _mx_orig_shape  torch.Size of the logical tensor
+    _mx_n           number of logical elements
+    _mx_block       block size
+
+``quantize``/``dequantize``/``@`` run the HIP kernels of libmxk.so.
+Attribute reads (.device, .requires_grad, .dtype, .is_cuda) are answered
+from the packed storage instead of dequantizing the whole tensor per read
+(the reference routes them through its dequantizing fallback,
+mxtorch.py:7315-7337); the answers equal what that fallback returns.
+"""
+from __future__ import annotations
+
+import math
+from typing import Optional
+
+import torch
+from torch.utils._pytree import tree_map
+
+from . import ops
+from .dtypes import get_mx_dtype, matmul_output_dtype, mx_dtype
+
+Tensor = torch.Tensor
+
+
+class mx_tensor(torch.Tensor):
+    """A quantized tensor that is a torch.Tensor (mxtorch.py:6028)."""
+
+    def __new__(cls, packed: Tensor, scales: Tensor, mx_dtype: mx_dtype, orig_shape, n: int,
+                block: int = 128, requires_grad: bool = False):
+        dummy = torch.empty((), dtype=torch.float32, device=packed.device)
+        inst = torch.Tensor._make_subclass(cls, dummy, requires_grad)
+        inst._mx_packed = packed
+        inst._mx_dtype = mx_dtype
+        inst._mx_scales = scales
+        inst._mx_orig_shape = torch.Size(orig_shape)
+        inst._mx_n = int(n)
+        inst._mx_block = int(block)
+        return inst
+
+    def __init__(self, packed, scales, mx_dtype, orig_shape, n, block=128, requires_grad=False):
+        pass
+
+    # ---- tensor-subclass protocol (mxtorch.py:6058-6085) ----
+    def __tensor_flatten__(self):
+        return ["_mx_packed", "_mx_scales"], {
+            "mx_dtype": self._mx_dtype, "orig_shape": self._mx_orig_shape,
+            "n": self._mx_n, "block": self._mx_block}
+
+    @staticmethod
+    def __tensor_unflatten__(inner_tensors, metadata, outer_size, outer_stride):
+        return mx_tensor(inner_tensors["_mx_packed"], inner_tensors["_mx_scales"], metadata["mx_dtype"],
+                         metadata["orig_shape"], metadata["n"], metadata["block"])
+
+    # ---- factory / inverse (mxtorch.py:6096-6115) ----
+    @classmethod
+    def quantize(cls, x: Tensor, dt, block: int = 128, requires_grad: Optional[bool] = None) -> "mx_tensor":
+        dt = get_mx_dtype(dt)
+        if isinstance(x, mx_tensor):
+            x = x.dequantize()
+        packed, scales, n = ops.quantize(x, dt, block)
+        return cls(packed, scales, dt, x.shape, n, block, True)
+
+    def dequantize(self) -> Tensor:
+        flat = ops._dequant(self._mx_packed, self._mx_scales, self._mx_dtype, self._mx_n, self._mx_block,
+                            orig_shape=self._mx_orig_shape)
+        return flat.reshape(self._mx_orig_shape)
+
+    # ---- shape and metadata ----
+    @property
+    def shape(self) -> torch.Size:
+        return self._mx_orig_shape
+
+    def size(self, dim: Optional[int] = None):
+        if dim is None:
+            return self._mx_orig_shape
+        return self._mx_orig_shape[dim]
+
+    def dim(self) -> int:
+        return len(self._mx_orig_shape)
+
+    def numel(self) -> int:
+        return self._mx_n
+
+    @property
+    def mx_dtype(self) -> mx_dtype:
+        return self._mx_dtype
+
+    @property
+    def mx_scales(self) -> Tensor:
+        return self._mx_scales
+
+    @property
+    def mx_block(self) -> int:
+        return self._mx_block
+
+    @property
+    def packed(self) -> Tensor:
+        return self._mx_packed
+
+    @property
+    def nbytes_packed(self) -> int:
+        return self._mx_packed.nbytes + self._mx_scales.nbytes
+
+    @property
+    def compression_ratio(self) -> float:
+        return (self._mx_n * 4) / max(self.nbytes_packed, 1)
+
+    # ---- torch function routing ----
+    @classmethod
+    def __torch_function__(cls, func, types, args=(), kwargs=None):
+        kwargs = kwargs or {}
+        if getattr(func, "__name__", "") == "__get__" and args and isinstance(args[0], mx_tensor):
+            attr = getattr(getattr(func, "__self__", None), "__name__", None)
+            getter = _GETTERS.get(attr)
+            if getter is not None:
+                return getter(args[0])
+        if func in _MM_FUNCS and len(args) >= 2 and isinstance(args[0], mx_tensor) and isinstance(args[1], mx_tensor):
+            return _mx_mm(args[0], args[1])
+        return _fallback(func, args, kwargs)
+
+    # ---- arithmetic sugar ----
+    def __matmul__(self, o):
+        return _mx_mm(self, o)
+
+    def __rmatmul__(self, o):
+        return _mx_mm(o, self)
+
+    def __neg__(self):
+        return mx_tensor.quantize(-self.dequantize(), self._mx_dtype, self._mx_block)
+
+    def __repr__(self):
+        return (f"mx_tensor({self._mx_dtype.name}, shape={tuple(self._mx_orig_shape)}, "
+                f"device={self._mx_packed.device}, {self.compression_ratio:.1f}x compression, "
+                f"{self.nbytes_packed / 1024:.2f} KB packed)")
+
+    def __len__(self):
+        return self._mx_orig_shape[0]
+
+    def float(self):
+        return self.dequantize()
+
+    def half(self):
+        return self.dequantize().half()
+
+    def bfloat16(self):
+        return self.dequantize().bfloat16()
+
+    # ---- moves and re-quantization (mxtorch.py:6215-6307) ----
+    def to(self, *args, **kwargs):
+        kw_device = kwargs.get("device", None)
+        kw_dtype = kwargs.get("dtype", None)
+        target = args[0] if args else None
+
+        def _is_device(v):
+            if isinstance(v, torch.device) or isinstance(v, int):
+                return True
+            if isinstance(v, str):
+                return v in ("cpu", "cuda") or v.startswith("cuda:") or v.startswith("cpu:")
+            return False
+
+        def _to_dev(v):
+            return torch.device("cuda", v) if isinstance(v, int) else torch.device(v)
+
+        if isinstance(target, mx_dtype) or (isinstance(target, str) and _is_mx_name(target)):
+            return mx_tensor.quantize(self.dequantize(), get_mx_dtype(target), self._mx_block)
+        if isinstance(kw_dtype, mx_dtype) or (isinstance(kw_dtype, str) and _is_mx_name(kw_dtype)):
+            base = self._move_device(_to_dev(kw_device)) if kw_device is not None else self
+            return mx_tensor.quantize(base.dequantize(), get_mx_dtype(kw_dtype), self._mx_block)
+        dev = kw_device if kw_device is not None else (target if _is_device(target) else None)
+        if dev is not None:
+            return self._move_device(_to_dev(dev))
+        return self.dequantize().to(*args, **kwargs)
+
+    def _move_device(self, device: torch.device) -> "mx_tensor":
+        return mx_tensor(self._mx_packed.to(device), self._mx_scales.to(device), self._mx_dtype,
+                         self._mx_orig_shape, self._mx_n, self._mx_block)
+
+    def cuda(self, device=None):
+        if device is None:
+            return self._move_device(torch.device("cuda"))
+        if isinstance(device, int):
+            return self._move_device(torch.device("cuda", device))
+        if isinstance(device, str) and ":" in device:
+            return self._move_device(torch.device(device))
+        return self._move_device(torch.device("cuda", int(device) if str(device).isdigit() else 0))
+
+    def cpu(self):
+        return self._move_device(torch.device("cpu"))
+
+    def clone(self):
+        return mx_tensor(self._mx_packed.clone(), self._mx_scales.clone(), self._mx_dtype, self._mx_orig_shape,
+                         self._mx_n, self._mx_block)
+
+    def detach(self):
+        return mx_tensor(self._mx_packed.detach(), self._mx_scales.detach(), self._mx_dtype,
+                         self._mx_orig_shape, self._mx_n, self._mx_block)
+
+    def reshape(self, *shape):
+        if len(shape) == 1 and isinstance(shape[0], (tuple, list, torch.Size)):
+            shape = tuple(shape[0])
+        known = math.prod(s for s in shape if s != -1)
+        shape = tuple(self._mx_n // known if s == -1 else s for s in shape)
+        t = self.clone()
+        t._mx_orig_shape = torch.Size(shape)
+        return t
+
+    def view(self, *shape):
+        return self.reshape(*shape)
+
+    def flatten(self, start=0, end=-1):
+        return self.reshape(-1)
+
+    def contiguous(self, *a, **k):
+        return self.clone()
+
+    def t(self):
+        return mx_tensor.quantize(self.dequantize().t(), self._mx_dtype, self._mx_block)
+
+    def __getitem__(self, idx):
+        return mx_tensor.quantize(self.dequantize()[idx], self._mx_dtype, self._mx_block)
+
+    def __reduce_ex__(self, protocol):
+        return (_rebuild_mxtensor, (self._mx_packed.cpu(), self._mx_scales.cpu(), self._mx_dtype.name,
+                                    tuple(self._mx_orig_shape), self._mx_n, self._mx_block))
+
+
+def _rebuild_mxtensor(packed, scales, dt, shape, n, block):
+    return mx_tensor(packed, scales, get_mx_dtype(dt), torch.Size(shape), n, block)
+
+
+def _is_mx_name(s: str) -> bool:
+    try:
+        get_mx_dtype(s)
+        return True
+    except ValueError:
+        return False
+
+
+_GETTERS = {
+    "device": lambda t: t._mx_packed.device,
+    "is_cuda": lambda t: t._mx_packed.is_cuda,
+    "requires_grad": lambda t: False,
+    "dtype": lambda t: torch.float32,
+    "ndim": lambda t: len(t._mx_orig_shape),
+    "grad": lambda t: None,
+    "is_leaf": lambda t: True,
+    "grad_fn": lambda t: None,
+    "layout": lambda t: torch.strided,
+}
+
+_MM_FUNCS = {torch.mm, torch.matmul, torch.Tensor.mm, torch.Tensor.matmul, torch.Tensor.__matmul__}
+
+
+def _unwrap(x):
+    return x.dequantize() if isinstance(x, mx_tensor) else x
+
+
+def _pick_ref(*args):
+    for a in args:
+        if isinstance(a, mx_tensor):
+            return a
+        if isinstance(a, (list, tuple)):
+            r = _pick_ref(*a)
+            if r is not None:
+                return r
+    return None
+
+
+def _fallback(func, args, kwargs):
+    """Any other torch op: dequantize, run it, requantize floating results
+    with the first mx_tensor's dtype (the reference's universal fallback,
+    mxtorch.py:7315-7337)."""
+    ref = _pick_ref(*args, *kwargs.values())
+    a2 = tree_map(_unwrap, args)
+    k2 = tree_map(_unwrap, kwargs)
+    with torch._C.DisableTorchFunctionSubclass():
+        out = func(*a2, **k2)
+    if ref is not None and isinstance(out, Tensor) and not isinstance(out, mx_tensor):
+        if out.ndim > 0 and out.dtype.is_floating_point:
+            return mx_tensor.quantize(out, ref._mx_dtype, ref._mx_block)
+    return out
+
+
+# ---------------------------------------------------------------- GEMM
+def _dispatch_qgemm(a: mx_tensor, b: mx_tensor) -> mx_tensor:
+    """True quantized GEMM (mxtorch.py:5497-5573): packed codes in, packed
+    codes out, with the CPU branch's semantics on the GPU."""
+    assert len(a._mx_orig_shape) == 2 and len(b._mx_orig_shape) == 2
+    M, K = a._mx_orig_shape
+    K2, N = b._mx_orig_shape
+    assert K == K2, f"GEMM shape mismatch: {a._mx_orig_shape} @ {b._mx_orig_shape}"
+    bits = a._mx_dtype.bits
+    block = a._mx_block
+    out_dt = matmul_output_dtype(a._mx_dtype, b._mx_dtype)
+    res = ops.qscale_gemm(a._mx_packed, a._mx_scales, b._mx_packed, b._mx_scales, M, K, N, bits, block,
+                          out_dt.bits)
+    return mx_tensor(res["packed"], res["scales"], out_dt, torch.Size([M, N]), M * N, block)
+
+
+def _mx_mm(a, b):
+    """Packed matmul routing (mxtorch.py:6508-6549).  The reference reads
+    ``requires_grad`` of both operands through its dequantizing fallback,
+    which is False for quantized tensors, so 2-D operands always reach
+    _dispatch_qgemm; other ranks take dequantize -> matmul -> requantize."""
+    if not isinstance(a, mx_tensor) or not isinstance(b, mx_tensor):
+        raise TypeError("_mx_mm expects two mx_tensor operands")
+    out_dt = matmul_output_dtype(a._mx_dtype, b._mx_dtype)
+    if len(a._mx_orig_shape) == 2 and len(b._mx_orig_shape) == 2:
+        return _dispatch_qgemm(a, b)
+    res = torch.matmul(a.dequantize(), b.dequantize())
+    return mx_tensor.quantize(res, out_dt, a._mx_block)
+
+
+class _QGemmSTE(torch.autograd.Function):
+    """Quantized GEMM with a straight-through gradient (mxtorch.py:5284-5311)."""
+
+    @staticmethod
+    def forward(ctx, a: Tensor, b: Tensor, mx_dt, block: int) -> Tensor:
+        ctx.save_for_backward(a, b)
+        with torch.no_grad():
+            qa = mx_tensor.quantize(a, mx_dt, block)
+            qb = mx_tensor.quantize(b, mx_dt, block)
+            result = _dispatch_qgemm(qa, qb).dequantize()
+        return result.detach()
+
+    @staticmethod
+    def backward(ctx, grad: Tensor):
+        a, b = ctx.saved_tensors
+        return grad @ b.t(), a.t() @ grad, None, None
+
+
+def mx_matmul(a: Tensor, b: Tensor, dtype="int4d", block: int = 128):
+    """Public packed matmul (mxtorch.py:10694-10723)."""
+    dt = get_mx_dtype(dtype)
+    if not isinstance(a, mx_tensor):
+        a = mx_tensor.quantize(a.float(), dt, block)
+    if not isinstance(b, mx_tensor):
+        b = mx_tensor.quantize(b.float(), dt, block)
+    return _mx_mm(a, b)
+
+
+def mx_quantize(x: Tensor, dtype="int4d", block: int = 128) -> mx_tensor:
+    """Alias of mx_tensor.quantize (mxtorch.py:7391-7396)."""
+    return mx_tensor.quantize(x, get_mx_dtype(dtype), block)

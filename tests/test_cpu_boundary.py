@@ -1,0 +1,89 @@
+"""CPU-only checks of the drop-in boundary (no GPU compute):
+
+  * libmxk.so loads and exports every entry point include/mxk.h declares;
+  * host-side helpers: packed sizes equal the reference packer's lengths,
+    the float grids/mids equal the oracle's (torch) tables bit for bit;
+  * the dtype registry mirrors the reference's names and properties;
+  * the product refuses CPU tensors loudly (no CPU compute path).
+"""
+import os
+import re
+
+import pytest
+import torch
+
+from oracle import mx_oracle as orc
+from tests import _golden as G
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def _declared_symbols():
+    src = open(os.path.join(ROOT, "include", "mxk.h")).read()
+    return sorted(set(re.findall(r"\b(mxk_[a-z0-9_]+)\s*\(", src)))
+
+
+def test_library_exports_every_declared_symbol():
+    from qtpytorch_amd import _lib as L
+    h = L.lib()
+    declared = _declared_symbols()
+    assert len(declared) >= 12
+    for name in declared:
+        assert hasattr(h, name), f"libmxk.so does not export {name}"
+        assert name in L.SIGNATURES, f"ctypes binding lacks {name}"
+    assert h.mxk_abi_version() == 1
+
+
+@pytest.mark.parametrize("bits", [1, 2, 3, 4, 5, 6, 7, 8, 16])
+@pytest.mark.parametrize("n", [1, 7, 8, 100, 128, 300, 1000])
+def test_packed_nbytes_matches_reference_packer(bits, n):
+    from qtpytorch_amd import _lib as L
+    codes = torch.zeros(n, dtype=torch.int32)
+    ref = orc.pack_auto(codes, bits)
+    assert L.lib().mxk_packed_nbytes(bits, n) == ref.numel() * ref.element_size()
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+def test_float_grid_tables_match_oracle(bits):
+    from qtpytorch_amd import ops
+    g, m = ops.float_grid(bits)
+    assert G.bits_equal(g, orc.float_grid(bits))
+    assert G.bits_equal(m, orc.float_mids(bits))
+    # and the reference's own grid from the golden file
+    assert G.bits_equal(g, G.get(f"grid/{bits}"))
+
+
+def test_dtype_registry_mirrors_reference():
+    import qtpytorch_amd as qa
+    from qtpytorch_amd.dtypes import _DTYPE_REGISTRY
+    assert len(_DTYPE_REGISTRY) == 2 * 12 * 2 * 6
+    d = qa.get_mx_dtype("int4d")
+    assert (d.kind, d.bits, d.mode, d.variant, d.max_val, d.pack_ratio) == ("int", 4, "d", "", 7.0, 2)
+    assert qa.get_mx_dtype("int1d").max_val == 1.0
+    assert qa.get_mx_dtype("float8d").max_val == 448.0
+    assert qa.get_mx_dtype("int4dh").base is qa.get_mx_dtype("int4d")
+    with pytest.raises(ValueError):
+        qa.get_mx_dtype("int8v")  # config 5's "int8v" has no mode letter
+    for a, b, out in (("int8d", "int8d", "int16d"), ("int4d", "int4d", "int8d"), ("int2d", "int2d", "int4d"),
+                      ("int1d", "int1d", "int2d"), ("float4d", "float4d", "float8d"), ("int4u", "int4d", "int8u")):
+        assert qa.matmul_output_dtype(qa.get_mx_dtype(a), qa.get_mx_dtype(b)).name == out
+        assert orc.matmul_out_bits(qa.get_mx_dtype(a).bits, qa.get_mx_dtype(b).bits) == qa.get_mx_dtype(out).bits
+
+
+def test_cpu_tensors_are_refused():
+    import qtpytorch_amd as qa
+    from qtpytorch_amd._lib import MXKError
+    with pytest.raises(MXKError):
+        qa.mx_tensor.quantize(torch.randn(256), qa.get_mx_dtype("int4d"), 128)
+
+
+def test_bad_arguments_return_errors_without_gpu():
+    """Argument validation happens on the host before any launch."""
+    from qtpytorch_amd import _lib as L
+    h = L.lib()
+    rc = h.mxk_quantize(None, 0, 256, 0, 4, 0, 128, None, 0, None, 0, None, 256, None, 0, None)
+    assert rc == -22 and b"null" in h.mxk_last_error()
+    rc = h.mxk_quantize(8, 0, 256, 1, 5, 0, 128, None, 0, 8, 1024, 8, 256, None, 0, None)
+    assert rc == -95
+    rc = h.mxk_qgemm(8, 8, 1, 8, 8, 1, 4, 4, 4, 16, 128, 0, None, 0, None, 8, None, None, 0, None)
+    assert rc == -95

@@ -1,0 +1,278 @@
+"""GPU parity: the HIP path (libmxk.so through qtpytorch_amd) against the
+reference's golden vectors and the CPU oracle on the same seeded inputs.
+
+Bar (from the north star):
+  * packed codes, scales, dequantized floats, int32 GEMM accumulators and
+    the fp32 GEMM accumulator C: bitwise equal;
+  * fp32 outputs of mx_linear (an fp32 sgemm in the reference, whose
+    summation order is library-defined): max|y - y_ref| <= 1e-3 * max|y_ref|.
+"""
+import math
+
+import pytest
+import torch
+
+from oracle import mx_oracle as orc
+from tests import _golden as G
+
+pytestmark = pytest.mark.gpu
+
+LINEAR_RTOL = 1e-3
+
+
+@pytest.fixture(scope="module")
+def qa():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    import qtpytorch_amd
+    return qtpytorch_amd
+
+
+def dev():
+    return torch.device("cuda:0")
+
+
+def _bits_eq(a, b):
+    return G.bits_equal(a.detach().cpu(), b.detach().cpu())
+
+
+# ---------------------------------------------------------------- golden vectors
+QCASES = G.cases("quantize")
+
+
+@pytest.mark.parametrize("case", QCASES, ids=[c["key"] for c in QCASES])
+def test_quantize_golden(qa, case):
+    x = G.input_tensor(case["input"]).to(dev())
+    dt = qa.get_mx_dtype(case["dtype"])
+    seed = G.index()["hash_seed"].get(case["dtype"]) if dt.is_hadamard else None
+    packed, scales, n = qa.ops.quantize(x, dt, case["block"], seed=seed)
+    assert n == case["n"]
+    assert _bits_eq(packed, G.get(case["key"] + "/packed")), "packed codes differ"
+    assert _bits_eq(scales, G.get(case["key"] + "/scales")), "scales differ"
+    dq = qa.ops._dequant(packed, scales, dt, n, case["block"], orig_shape=tuple(case["shape"]), seed=seed,
+                         hadamard_mode="reference")
+    assert _bits_eq(dq.reshape(case["shape"]), G.get(case["key"] + "/dequant")), "dequantized values differ"
+
+
+MCASES = G.cases("matmul")
+
+
+@pytest.mark.parametrize("case", MCASES, ids=[c["key"] for c in MCASES])
+def test_qgemm_golden(qa, case):
+    A = G.get(case["key"] + "/A").to(dev())
+    B = G.get(case["key"] + "/B").to(dev())
+    dt = qa.get_mx_dtype(case["dtype"])
+    qa_ = qa.mx_tensor.quantize(A, dt, 128)
+    qb_ = qa.mx_tensor.quantize(B, dt, 128)
+    qc = qa_ @ qb_
+    assert isinstance(qc, qa.mx_tensor)
+    assert qc._mx_dtype.name == case["out_dtype"]
+    assert _bits_eq(qc._mx_packed, G.get(case["key"] + "/packed"))
+    assert _bits_eq(qc._mx_scales, G.get(case["key"] + "/scales"))
+    if qc._mx_dtype.is_int:
+        assert _bits_eq(qc.dequantize(), G.get(case["key"] + "/dequant"))
+        ste = qa._QGemmSTE.apply(A, B, dt, 128)
+        assert _bits_eq(ste, G.get(case["key"] + "/ste"))
+
+
+LCASES = G.cases("linear")
+
+
+@pytest.mark.parametrize("case", LCASES, ids=[c["key"] for c in LCASES])
+def test_linear_golden(qa, case):
+    W = G.get(case["key"] + "/W")
+    lin = torch.nn.Linear(case["in"], case["out"], bias=case["bias"])
+    with torch.no_grad():
+        lin.weight.copy_(W)
+        if case["bias"]:
+            lin.bias.copy_(G.get(case["key"] + "/bias"))
+    lin = lin.to(dev())
+    m = qa.mx_linear.from_linear(lin, qa.get_mx_dtype(case["dtype"]), 128)
+    assert _bits_eq(m._mx_weight._mx_packed, G.get(case["key"] + "/w_packed"))
+    assert _bits_eq(m._mx_weight._mx_scales, G.get(case["key"] + "/w_scales"))
+    y = m(G.get(case["key"] + "/x").to(dev())).cpu()
+    y_ref = G.get(case["key"] + "/y")
+    assert (y - y_ref).abs().max().item() <= LINEAR_RTOL * y_ref.abs().max().item()
+
+
+KCASES = G.cases("kv")
+
+
+@pytest.mark.parametrize("case", KCASES, ids=[c["key"] for c in KCASES])
+def test_kv_cache_golden(qa, case):
+    key = case["key"]
+    cache = qa.kv_cache_quantizer(n_heads=case["H"], head_dim=case["D"], dtype=case["dtype"])
+    ks, vs = G.get(key + "/k"), G.get(key + "/v")
+    for t in range(case["T"]):
+        cache.append_kv(ks[t].to(dev()), vs[t].to(dev()))
+    kq, vq = cache.get_quantized()
+    for t in range(case["T"]):
+        assert _bits_eq(kq[t]._mx_packed, G.get(f"{key}/kq{t}/packed"))
+        assert _bits_eq(kq[t]._mx_scales, G.get(f"{key}/kq{t}/scales"))
+        assert _bits_eq(vq[t]._mx_packed, G.get(f"{key}/vq{t}/packed"))
+        assert _bits_eq(vq[t]._mx_scales, G.get(f"{key}/vq{t}/scales"))
+    K, V = cache.get()
+    assert _bits_eq(K, G.get(key + "/K"))
+    assert _bits_eq(V, G.get(key + "/V"))
+
+
+# ---------------------------------------------------------------- seeded vs oracle
+def _randn(shape, seed, outliers=0.0, scale=50.0):
+    g = torch.Generator()
+    g.manual_seed(seed)
+    x = torch.randn(*shape, generator=g)
+    if outliers:
+        m = torch.rand(*shape, generator=g) < outliers
+        x[m] *= scale
+    return x
+
+
+QDTYPES = ["int8d", "int4d", "int2d", "int1d", "int3d", "int5d", "int7d", "float4d", "float8d", "int8dv",
+           "int4dv", "int16d", "int4dh", "int8dh", "float8dh", "int1dh"]
+
+
+@pytest.mark.parametrize("dtype", QDTYPES)
+@pytest.mark.parametrize("block", [128, 64, 32, 256, 96])
+def test_quantize_seeded_vs_oracle(qa, dtype, block):
+    seed = 1000 + QDTYPES.index(dtype) * 7 + block
+    x = _randn((37, 1024 + 3 * 128), seed, outliers=1e-3)
+    if dtype.endswith("h"):
+        x = x[:, :512].contiguous()
+    dt = qa.get_mx_dtype(dtype)
+    hseed = 12345 if dt.is_hadamard else None
+    packed, scales, n = qa.ops.quantize(x.to(dev()), dt, block, seed=hseed)
+    rp, rs, rn = orc.quantize(x, dtype, block, seed=hseed)
+    assert n == rn
+    assert _bits_eq(packed, rp), f"{dtype}/{block}: packed codes differ"
+    assert _bits_eq(scales, rs), f"{dtype}/{block}: scales differ"
+    dq = qa.ops._dequant(packed, scales, dt, n, block, orig_shape=tuple(x.shape), seed=hseed,
+                         hadamard_mode="rows")
+    rdq = orc.dequant(rp, rs, dtype, rn, block, seed=hseed, orig_shape=tuple(x.shape), hadamard_mode="rows")
+    assert _bits_eq(dq, rdq), f"{dtype}/{block}: dequantized values differ"
+
+
+@pytest.mark.parametrize("src", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("dtype", ["int8d", "int4d", "int8dv", "float8d", "int4dh", "int1d"])
+def test_quantize_half_inputs(qa, src, dtype):
+    x = _randn((64, 256), 77, outliers=1e-2, scale=20.0).to(src)
+    dt = qa.get_mx_dtype(dtype)
+    hseed = 99 if dt.is_hadamard else None
+    packed, scales, n = qa.ops.quantize(x.to(dev()), dt, 128, seed=hseed)
+    rp, rs, _ = orc.quantize(x, dtype, 128, seed=hseed)
+    assert _bits_eq(packed, rp) and _bits_eq(scales, rs)
+
+
+@pytest.mark.parametrize("n", [1, 5, 127, 129, 1000, 4097])
+@pytest.mark.parametrize("dtype", ["int8d", "int4d", "int2d", "int1d", "float4d", "float8d", "int8dv"])
+def test_ragged_lengths(qa, n, dtype):
+    x = _randn((n,), 5 + n)
+    packed, scales, m = qa.ops.quantize(x.to(dev()), qa.get_mx_dtype(dtype), 128)
+    rp, rs, _ = orc.quantize(x, dtype, 128)
+    assert _bits_eq(packed, rp) and _bits_eq(scales, rs)
+    dq = qa.ops._dequant(packed, scales, qa.get_mx_dtype(dtype), m, 128)
+    assert _bits_eq(dq, orc.dequant(rp, rs, dtype, m, 128))
+
+
+def test_misaligned_input_takes_generic_path(qa):
+    base = _randn((1025,), 3).to(dev())
+    x = base[1:]  # 4-byte offset: not 16-byte aligned
+    for dtype in ("int4d", "float8d", "int8dv"):
+        packed, scales, _ = qa.ops.quantize(x, qa.get_mx_dtype(dtype), 128)
+        rp, rs, _ = orc.quantize(x.cpu(), dtype, 128)
+        assert _bits_eq(packed, rp) and _bits_eq(scales, rs)
+
+
+def test_hadamard_large_rotation(qa):
+    """1-D input: one whole-tensor rotation of next_pow2(n) = 16384 points
+    (global butterfly pass + LDS tail)."""
+    x = _randn((12000,), 8)
+    dt = qa.get_mx_dtype("int4dh")
+    packed, scales, n = qa.ops.quantize(x.to(dev()), dt, 128, seed=7)
+    rp, rs, _ = orc.quantize(x, "int4dh", 128, seed=7)
+    assert _bits_eq(packed, rp) and _bits_eq(scales, rs)
+    dq = qa.ops._dequant(packed, scales, dt, n, 128, seed=7, hadamard_mode="reference")
+    assert _bits_eq(dq, orc.dequant(rp, rs, "int4dh", n, 128, seed=7))
+
+
+GEMM_SHAPES = [(512, 512, 512), (256, 384, 200), (100, 256, 130), (33, 128, 17), (8, 640, 1024)]
+
+
+@pytest.mark.parametrize("dtype", ["int8d", "int4d", "int2d", "int1d"])
+@pytest.mark.parametrize("shape", GEMM_SHAPES, ids=lambda s: "x".join(map(str, s)))
+def test_qgemm_seeded_vs_oracle(qa, dtype, shape):
+    M, K, N = shape
+    A = _randn((M, K), 31 + M)
+    B = _randn((K, N), 37 + N)
+    dt = qa.get_mx_dtype(dtype)
+    pa, sa, na = qa.ops.quantize(A.to(dev()), dt, 128)
+    pb, sb, nb = qa.ops.quantize(B.to(dev()), dt, 128)
+    out_dt = qa.matmul_output_dtype(dt, dt)
+    res = qa.ops.qscale_gemm(pa, sa, pb, sb, M, K, N, dt.bits, 128, out_dt.bits, want_c=True, want_acc=True)
+    rpa, rsa, _ = orc.quantize(A, dtype, 128)
+    rpb, rsb, _ = orc.quantize(B, dtype, 128)
+    ac = orc.unpack_auto(rpa, dt.bits, M * K).to(torch.int32)
+    bc = orc.unpack_auto(rpb, dt.bits, K * N).to(torch.int32)
+    codes, scales, C = orc.qscale_matmul(ac, rsa, bc, rsb, M, K, N, dt.bits, 128, out_dt.bits, return_c=True)
+    acc = orc.int_accumulators(ac, bc, M, K, N, 128)
+    assert torch.equal(res["acc"].cpu(), acc), "int32 accumulators differ"
+    assert _bits_eq(res["c"], C), "fp32 accumulator C differs"
+    assert _bits_eq(res["packed"], orc.pack_auto(codes, out_dt.bits))
+    assert _bits_eq(res["scales"], scales)
+
+
+@pytest.mark.parametrize("dtype", ["int4d", "int8d", "int2d", "float4d", "float8d", "int1d"])
+@pytest.mark.parametrize("shape", [(16, 1024, 768), (3, 300, 200), (64, 512, 256), (1, 128, 128)])
+@pytest.mark.parametrize("xdt", [torch.float32, torch.bfloat16])
+def test_linear_vs_oracle(qa, dtype, shape, xdt):
+    M, K, N = shape
+    W = _randn((N, K), 11 + K, outliers=1e-3, scale=20.0) * 0.02
+    x = _randn((M, K), 13 + M).to(xdt)
+    lin = torch.nn.Linear(K, N, bias=False)
+    with torch.no_grad():
+        lin.weight.copy_(W)
+    m = qa.mx_linear.from_linear(lin.to(dev()), qa.get_mx_dtype(dtype), 128)
+    y = m(x.to(dev())).cpu()
+    wp, ws, _ = orc.linear_from_weight(W, dtype, 128)
+    assert _bits_eq(m._mx_weight._mx_packed, wp)
+    y_ref = orc.linear_forward(x, wp, ws, dtype, K, N, 128)
+    err = (y - y_ref).abs().max().item()
+    assert err <= LINEAR_RTOL * y_ref.abs().max().item(), f"max err {err}"
+
+
+def test_kv_bulk_roundtrip(qa):
+    """Config-5 layout at reduced size: fp16 K [B,H,S,D] -> int8dv / int4d per row of D."""
+    k = _randn((2, 4, 256, 128), 55).half()
+    for dtype in ("int8dv", "int4d"):
+        rows = k.reshape(-1, 128)
+        packed, scales, n = qa.ops.quantize(rows.to(dev()), qa.get_mx_dtype(dtype), 128)
+        rp, rs, _ = orc.quantize(rows, dtype, 128)
+        assert _bits_eq(packed, rp) and _bits_eq(scales, rs)
+        dq = qa.ops._dequant(packed, scales, qa.get_mx_dtype(dtype), n, 128)
+        assert _bits_eq(dq, orc.dequant(rp, rs, dtype, n, 128))
+
+
+def test_mx_tensor_api(qa):
+    x = _randn((64, 256), 1).to(dev())
+    q = qa.mx_tensor.quantize(x, qa.get_mx_dtype("int4d"), 128)
+    assert q.shape == torch.Size([64, 256]) and q.dim() == 2 and q.numel() == 64 * 256
+    assert q.device == x.device and q.requires_grad is False and q.dtype == torch.float32
+    assert q.compression_ratio > 7.0
+    assert "int4d" in repr(q)
+    q2 = q.to("int8d")
+    assert q2._mx_dtype.name == "int8d"
+    qc = q.cpu()
+    assert qc._mx_packed.device.type == "cpu"
+    assert _bits_eq(qc.cuda().dequantize(), q.dequantize())
+    assert torch.matmul(q, q.t()).shape == torch.Size([64, 64])
+    y = qa.mx_matmul(x, x.t().contiguous(), "int8d")
+    assert isinstance(y, qa.mx_tensor) and y._mx_dtype.name == "int16d"
+
+
+def test_to_mx_model(qa):
+    torch.manual_seed(0)
+    model = torch.nn.Sequential(torch.nn.Linear(256, 512), torch.nn.ReLU(), torch.nn.Linear(512, 128)).to(dev())
+    x = torch.randn(4, 256, device=dev())
+    model.to("int8d")
+    assert isinstance(model[0], qa.mx_linear) and isinstance(model[2], qa.mx_linear)
+    y = model(x)
+    assert y.shape == (4, 128) and torch.isfinite(y).all()
