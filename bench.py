@@ -1,0 +1,278 @@
+"""Benchmark of the MX quantize/pack + block-scaled GEMM path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-extras] [--no-cpu]
+
+Headline (the JSON line's `value`): BASELINE config 2, the int4d
+weight-only linear at decode shape — x fp32 [16, 8192] ~ N(0,1), W
+[8192 (out), 8192 (in)] ~ 0.02 N(0,1) with 0.1% outliers x20, stored as
+quantize(W.t()) int4d block 128 — one step = one mx_linear forward (one
+fused kernel).  `value` = algorithmic bytes per step (packed weights 32 MiB +
+scales 2 MiB + x + y = 36,700,160 B) / time per step, in GB/s.
+
+Timing: W warm-up steps, then K steps captured into one HIP graph and
+replayed between two HIP events recorded on the stream the kernels run on
+(torch's current stream), synchronize on both sides; inputs are resident
+in HBM.  ms_per_step = elapsed / K.
+
+`cpu_baseline`: the CPU oracle (oracle/mx_oracle.py, the reference's CPU
+path restated with the same torch ops) on the full config-2 workload, 2
+warm-ups then the median of 5, on this host's cores.
+
+`extras`: configs 1, 3, 4 and 5 measured the same way, each with its
+roofline fraction (HBM 8.0 TB/s, dense int8 MFMA 5.0 POP/s).
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+
+import torch
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+INT8_PEAK_TOPS = 5000.0
+PROFILES = os.path.join(ROOT, "profiles")
+
+
+def gen(seed: int, device="cpu") -> torch.Generator:
+    g = torch.Generator(device=device)
+    g.manual_seed(seed)
+    return g
+
+
+def graph_time(step, steps: int, warmup: int) -> float:
+    """Seconds per step: `steps` calls of step() captured in one graph,
+    replayed between events on the current stream."""
+    for _ in range(max(warmup, 1)):
+        step()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(g, stream=s):
+            for _ in range(steps):
+                step()
+    torch.cuda.current_stream().wait_stream(s)
+    g.replay()  # warm replay
+    torch.cuda.synchronize()
+    st = torch.cuda.current_stream()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record(st)
+    g.replay()
+    e1.record(st)
+    torch.cuda.synchronize()
+    dt = e0.elapsed_time(e1) / 1e3 / steps
+    del g
+    return dt
+
+
+def load_traffic(name: str):
+    """HBM bytes per launch from a committed rocprofv3 PMC summary, if any."""
+    p = os.path.join(PROFILES, f"{name}.traffic.json")
+    if not os.path.exists(p):
+        return None
+    with open(p) as f:
+        return json.load(f).get("traffic_bytes")
+
+
+# ---------------------------------------------------------------- config 2
+def config2_inputs():
+    K = N = 8192
+    x = torch.randn(16, K, generator=gen(2))
+    W = 0.02 * torch.randn(N, K, generator=gen(3))
+    W[torch.rand(N, K, generator=gen(4)) < 1e-3] *= 20
+    return x, W
+
+
+def bench_linear(args, qa):
+    dev = torch.device("cuda:0")
+    x_cpu, W_cpu = config2_inputs()
+    K = N = 8192
+    lin = torch.nn.Linear(K, N, bias=False)
+    with torch.no_grad():
+        lin.weight.copy_(W_cpu)
+    m = qa.mx_linear.from_linear(lin.to(dev), qa.get_mx_dtype("int4d"), 128)
+    x = x_cpu.to(dev)
+    y = m(x)
+    torch.cuda.synchronize()
+    sec = graph_time(lambda: m(x), args.steps, args.warmup)
+    algo_bytes = K * N // 2 + (K * N // 128) * 4 + 16 * K * 4 + 16 * N * 4
+    gbs = algo_bytes / sec / 1e9
+    res = {"sec": sec, "algo_bytes": algo_bytes, "gbs": gbs, "y": y.cpu(),
+           "w_packed": m._mx_weight._mx_packed.cpu(), "w_scales": m._mx_weight._mx_scales.cpu(),
+           "x": x_cpu}
+    return res
+
+
+def cpu_baseline_linear(res):
+    from oracle import mx_oracle as orc
+
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    x, wp, ws = res["x"], res["w_packed"], res["w_scales"]
+
+    def run():
+        return orc.linear_forward(x, wp, ws, "int4d", 8192, 8192, 128)
+
+    for _ in range(2):
+        y_ref = run()
+    ts = []
+    for _ in range(5):
+        t0 = time.perf_counter()
+        y_ref = run()
+        ts.append(time.perf_counter() - t0)
+    sec = statistics.median(ts)
+    err = (res["y"] - y_ref).abs().max().item() / y_ref.abs().max().item()
+    return {"value": round(res["algo_bytes"] / sec / 1e9, 3), "unit": "GB/s", "cores": cores, "kind": "port",
+            "sample": "full config-2 workload (x[16,8192] @ dequant(int4d W[8192,8192])), "
+                      "median of 5 after 2 warm-ups",
+            "sec_per_step": round(sec, 4)}, err
+
+
+# ---------------------------------------------------------------- extras
+def bench_quant_sweep(qa, reps):
+    dev = torch.device("cuda:0")
+    n = 1 << 28
+    g = gen(7, "cuda")
+    x = torch.randn(n, generator=g, device=dev)
+    mask = torch.rand(n, generator=gen(8, "cuda"), device=dev) < 1e-3
+    x[mask] *= 50
+    del mask
+    x = x.view(1 << 21, 128)
+    out = {}
+    for name in ("int8d", "int4d", "int2d", "int1d", "float4d", "float8d", "int4dh"):
+        dt = qa.get_mx_dtype(name)
+        bits = dt.bits
+        algo = n * 4 + n * bits // 8 + (n // 128) * 4
+        seed = 1534857261 if dt.is_hadamard else None
+        packed, scales, _ = qa.ops.quantize(x, dt, 128, seed=seed)
+        tq = graph_time(lambda: qa.ops.quantize(x, dt, 128, seed=seed), reps, 1)
+        td = graph_time(lambda: qa.ops._dequant(packed, scales, dt, n, 128, orig_shape=(1 << 21, 128),
+                                                seed=seed), reps, 1)
+        out[name] = {"quantize_us": round(tq * 1e6, 2), "quantize_GBs": round(algo / tq / 1e9, 1),
+                     "quantize_frac": round(algo / tq / 1e9 / HBM_PEAK_GBS, 4),
+                     "dequantize_us": round(td * 1e6, 2), "dequantize_GBs": round(algo / td / 1e9, 1),
+                     "dequantize_frac": round(algo / td / 1e9 / HBM_PEAK_GBS, 4)}
+        del packed, scales
+        torch.cuda.empty_cache()
+    return out
+
+
+def bench_gemm(qa, M, K, N, reps):
+    dev = torch.device("cuda:0")
+    A = torch.randn(M, K, generator=gen(5, "cuda"), device=dev)
+    B = torch.randn(K, N, generator=gen(6, "cuda"), device=dev)
+    d8 = qa.get_mx_dtype("int8d")
+    pa, sa, _ = qa.ops.quantize(A, d8, 128)
+    pb, sb, _ = qa.ops.quantize(B, d8, 128)
+    del A, B
+    t_c = graph_time(lambda: qa.ops.qscale_gemm(pa, sa, pb, sb, M, K, N, 8, 128, 16, want_packed=False,
+                                                  want_c=True), reps, 1)
+    t_p = graph_time(lambda: qa.ops.qscale_gemm(pa, sa, pb, sb, M, K, N, 8, 128, 16), reps, 1)
+    ops = 2.0 * M * K * N
+    return {"shape": [M, K, N], "fp32_out_us": round(t_c * 1e6, 2), "fp32_out_TOPS": round(ops / t_c / 1e12, 2),
+            "fp32_out_frac_int8_peak": round(ops / t_c / 1e12 / INT8_PEAK_TOPS, 4),
+            "packed_int16d_out_us": round(t_p * 1e6, 2), "packed_TOPS": round(ops / t_p / 1e12, 2)}
+
+
+def bench_kv(qa, reps):
+    dev = torch.device("cuda:0")
+    shape = (8, 32, 4096, 128)
+    out = {}
+    k = torch.randn(*shape, generator=gen(9, "cuda"), device=dev).half()
+    v = torch.randn(*shape, generator=gen(10, "cuda"), device=dev).half()
+    rows_k, rows_v = k.view(-1, 128), v.view(-1, 128)
+    n = rows_k.numel()
+    for name in ("int8dv", "int4d"):
+        dt = qa.get_mx_dtype(name)
+        q_algo = 2 * (n * 2 + n * dt.bits // 8 + (n // 128) * 4)
+        d_algo = 2 * (n * 4 + n * dt.bits // 8 + (n // 128) * 4)
+        pk, sk, _ = qa.ops.quantize(rows_k, dt, 128)
+        pv, sv, _ = qa.ops.quantize(rows_v, dt, 128)
+
+        def q():
+            qa.ops.quantize(rows_k, dt, 128)
+            qa.ops.quantize(rows_v, dt, 128)
+
+        def d():
+            qa.ops._dequant(pk, sk, dt, n, 128)
+            qa.ops._dequant(pv, sv, dt, n, 128)
+
+        tq = graph_time(q, reps, 1)
+        td = graph_time(d, reps, 1)
+        out[name] = {"quantize_us": round(tq * 1e6, 2), "quantize_GBs": round(q_algo / tq / 1e9, 1),
+                     "quantize_frac": round(q_algo / tq / 1e9 / HBM_PEAK_GBS, 4),
+                     "dequantize_us": round(td * 1e6, 2), "dequantize_GBs": round(d_algo / td / 1e9, 1),
+                     "dequantize_frac": round(d_algo / td / 1e9 / HBM_PEAK_GBS, 4)}
+    return out
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--no-extras", action="store_true")
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--only", default="", help="comma list of extras: quant,gemm,kv,small")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU: every box in this build has one MI355X, and the path shards "
+              "without collectives (see the design notes); run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+    assert torch.cuda.is_available(), "bench.py needs a GPU"
+    import qtpytorch_amd as qa
+
+    res = bench_linear(args, qa)
+    line = {
+        "metric": "packed GEMM TOPS (int8d/int4d) + quantize GB/s; % of MI355X roofline",
+        "value": round(res["gbs"], 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(res["sec"] * 1e3, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int4 codes, fp32 math",
+        "data": "synthetic (seeded randn; weights 0.02*randn with 0.1% outliers x20)",
+        "config": {"workload": "int4d weight-only linear, decode: x fp32 [16,8192] @ dequant(W int4d [8192,8192] "
+                               "block 128), one mx_linear forward per step",
+                   "M": 16, "K": 8192, "N": 8192, "block": 128, "weight_dtype": "int4d", "x_dtype": "float32"},
+        "roofline": {"bound": "hbm", "achieved": round(res["gbs"], 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(res["gbs"] / HBM_PEAK_GBS, 4),
+                     "traffic": load_traffic("linear_int4d_decode_16x8192x8192")},
+    }
+    if not args.no_cpu:
+        cb, err = cpu_baseline_linear(res)
+        line["cpu_baseline"] = cb
+        line["max_rel_err_vs_oracle"] = err
+    else:
+        line["cpu_baseline"] = None
+    if not args.no_extras:
+        only = set(filter(None, args.only.split(",")))
+        extras = {}
+        if not only or "small" in only:
+            extras["config1_int8d_gemm_512"] = bench_gemm(qa, 512, 512, 512, 50)
+        if not only or "gemm" in only:
+            extras["config3_int8d_gemm_8192"] = bench_gemm(qa, 8192, 8192, 8192, 3)
+        if not only or "quant" in only:
+            extras["config4_quant_sweep_2e28"] = bench_quant_sweep(qa, 5)
+        if not only or "kv" in only:
+            extras["config5_kv_8x32x4096x128_fp16"] = bench_kv(qa, 5)
+        line["extras"] = extras
+    print(json.dumps(line))
+
+
+if __name__ == "__main__":
+    main()

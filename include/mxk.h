@@ -141,7 +141,12 @@ int mxk_qgemm(const void* a_packed, const float* a_scales, int64_t a_nscales, co
               float* c_f32, int32_t* acc_i32, void* workspace, size_t workspace_nbytes,
               void* stream);
 
-/* Workspace bytes mxk_linear_wq needs (0 if none). */
+/* Workspace bytes mxk_linear_wq needs (0 if none).  The decode path
+ * (int4 weights, block 128, M <= 16, K % 32 == 0, N % 128 == 0) splits K
+ * across workgroups; its workspace (a 64 KiB counter prefix, then the
+ * partial sums) must be zero-filled before first use, and every call, of
+ * any shape, leaves it ready for the next one.  Calls sharing a workspace
+ * must not overlap. */
 size_t mxk_linear_workspace(int64_t M, int64_t K, int64_t N, int bits, int block);
 
 /* Weight-only linear, mx_linear.forward (mxtorch.py:7454-7473):

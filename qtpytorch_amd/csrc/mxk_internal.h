@@ -105,6 +105,18 @@ __device__ __forceinline__ void load_elems(const T* __restrict__ x, int64_t idx,
   }
 }
 
+// Raw buffer resource over [p, p + bytes): loads past the end return 0
+// (hardware range check), offsets are 32-bit (one per lane + one scalar).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* p, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, 0x00020000);
+}
+__device__ __forceinline__ uint32_t buf_load_b32(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+  return (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(r, (int)voff, (int)soff, 0);
+}
+__device__ __forceinline__ u32x4 buf_load_b128(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+  return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)voff, (int)soff, 0));
+}
+
 // Store `NB` bytes from `w` at dst+off when they fit below `limit`; bytes at
 // or past `limit` are dropped (tail of a packed buffer).
 template <int NB>

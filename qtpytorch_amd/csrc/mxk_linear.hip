@@ -102,6 +102,336 @@ __global__ __launch_bounds__(256) void k_linear_generic(const T* __restrict__ x,
   }
 }
 
+// ---------------------------------------------------------------- int4 decode (M <= 16)
+// y[m, n] = sum_k x[m,k] * RN(code[k,n] * s[k, n/128]), weights int4 [K][N]
+// packed along N (LSB nibble = even column), block 128 along N.
+//
+// Work split: a workgroup of 8 waves owns NBW scale blocks (NBW*128 output
+// columns) and 8/NBW*RPW rows of K.  Wave w takes block w % NBW and row
+// group w / NBW, so the waves that share rows share their x and scale
+// cache lines through L1.  Per 32-row step a wave runs
+// v_mfma_f32_16x16x32_f16 on
+//   A[m][k] = x[m,k] * s[k,nb]           split as f16 hi + f16 lo (22 bits)
+//   B[k][c] = f16 with bit pattern ((code+8) << 4), i.e. (code+8) * 2^-20
+// over 8 tiles of 16 columns.  Lane (j = lane&15, g = lane>>4) loads the u32
+// holding columns 8j..8j+7 of rows 8g..8g+7; tile t takes nibble t of each,
+// so tile t covers columns {8j + t}.  One v_perm_b32 builds the B operand
+// dword for two rows.  The +8 offset is removed with a correction tile
+// (B = 8 * 2^-20): y = 2^20 * (D - D_corr).
+// Reductions are deterministic: waves of a block combine through LDS in a
+// fixed tree; workgroups that split K write partials with agent-coherent
+// stores, count arrivals on an atomic counter, and the last one sums the
+// partials in split order and resets the counter.
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
+
+#define DEC_WAVES 8
+#define DEC_P 4
+#define DEC_COUNTER_BYTES 65536  // split-K counters: up to 16384 column groups
+
+__device__ __forceinline__ void split_hi_lo(const float (&a)[8], f16x8& hi, f16x8& lo) {
+  uint32_t h[4], l[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    auto hp = __builtin_amdgcn_cvt_pkrtz(a[2 * q], a[2 * q + 1]);
+    const float r0 = a[2 * q] - (float)hp[0];
+    const float r1 = a[2 * q + 1] - (float)hp[1];
+    auto lp = __builtin_amdgcn_cvt_pkrtz(r0, r1);
+    h[q] = __builtin_bit_cast(uint32_t, hp);
+    l[q] = __builtin_bit_cast(uint32_t, lp);
+  }
+  hi = __builtin_bit_cast(f16x8, u32x4v{h[0], h[1], h[2], h[3]});
+  lo = __builtin_bit_cast(f16x8, u32x4v{l[0], l[1], l[2], l[3]});
+}
+
+template <typename T, int STEPS, int NBW>
+__global__ __launch_bounds__(64 * DEC_WAVES, 1) void k_linear_w4_decode(
+    const T* __restrict__ x, int M, int64_t K, int64_t N, const uint32_t* __restrict__ w,
+    const float* __restrict__ scales, const float* __restrict__ bias, float* __restrict__ out,
+    float* __restrict__ partials, unsigned* __restrict__ counters, int S) {
+  constexpr int RPW = STEPS * 32;
+  constexpr int RG = DEC_WAVES / NBW;  // row groups per workgroup
+  __shared__ __attribute__((aligned(16))) f32x4 red[4 * 8 * 64];   // tree slots, lane-major
+  __shared__ __attribute__((aligned(16))) float sS[DEC_WAVES * RPW];  // each wave's scales
+  __shared__ int s_last;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int j = lane & 15, g = lane >> 4;
+  const int nbl = wave % NBW, rg = wave / NBW;
+  const int64_t NB = N / 128;
+  const int64_t cg = blockIdx.x / S;
+  const int ks = blockIdx.x % S;
+  const int64_t nb = cg * NBW + nbl;
+  const int64_t k_begin = ((int64_t)ks * RG + rg) * RPW;
+
+  f32x4 acc[8];
+#pragma unroll
+  for (int t = 0; t < 8; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+  f32x4 corr = f32x4{0.f, 0.f, 0.f, 0.f};
+  const f16x8 b8 = __builtin_bit_cast(f16x8, u32x4v{0x00800080u, 0x00800080u, 0x00800080u, 0x00800080u});
+
+  // P-deep software prefetch over a fully unrolled step sequence: step st
+  // computes from slot st % P, then the slot is refilled with step st + P.
+  // Straight-line code lets the compiler wait for exactly the loads each
+  // step needs.  Buffer loads carry one per-lane offset (lane's k-group and
+  // column word) and the step's row in the scalar offset.  The hardware range
+  // check does not cover the scalar offset, so every address is kept valid
+  // by construction: a step past K (only in the last split when K is not a
+  // multiple of the split) re-reads rows 0..31 with its x and scales forced
+  // to zero, and x rows past M read row 0 and are zeroed.
+  uint32_t wv[DEC_P][8];
+  float xv[DEC_P][8];
+  const __amdgpu_buffer_rsrc_t rw = make_rsrc(w, (uint32_t)(K * N / 2));
+  const __amdgpu_buffer_rsrc_t rs = make_rsrc(scales, (uint32_t)(K * NB * 4));
+  const __amdgpu_buffer_rsrc_t rx = make_rsrc(x, (uint32_t)((int64_t)M * K * sizeof(T)));
+  const uint32_t row_bytes = (uint32_t)(N / 2), srow_bytes = (uint32_t)(NB * 4);
+  const bool mrow = j < M;
+  const uint32_t vw = (uint32_t)(8 * g * row_bytes + (nb * 16 + j) * 4);
+  // this wave's RPW scales s[k, nb] go to LDS once (rows past K stage 0)
+  float* wS = sS + wave * RPW;
+#pragma unroll
+  for (int i = 0; i < RPW / 64; ++i) {
+    const int64_t row = k_begin + i * 64 + lane;
+    const bool ok = row < K;
+    const float sc = __uint_as_float(buf_load_b32(rs, (uint32_t)((ok ? row : 0) * srow_bytes + nb * 4), 0u));
+    wS[i * 64 + lane] = ok ? sc : 0.0f;
+  }
+  const uint32_t vx = (uint32_t)(((int64_t)(mrow ? j : 0) * K + 8 * g) * sizeof(T));
+  auto issue = [&](int slot, int st) {
+    const int64_t k0 = k_begin + (int64_t)st * 32;
+    const bool sin = k0 < K;  // wave-uniform; K % 32 == 0, so a step is wholly in or out
+    const uint32_t kr = sin ? (uint32_t)k0 : 0u;
+#pragma unroll
+    for (int r = 0; r < 8; ++r) wv[slot][r] = buf_load_b32(rw, vw, (kr + r) * row_bytes);
+    const bool xok = sin && mrow;
+    if constexpr (sizeof(T) == 4) {
+      const u32x4 a0 = buf_load_b128(rx, vx, kr * 4u);
+      const u32x4 a1 = buf_load_b128(rx, vx + 16u, kr * 4u);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        xv[slot][i] = xok ? __uint_as_float(a0[i]) : 0.0f;
+        xv[slot][4 + i] = xok ? __uint_as_float(a1[i]) : 0.0f;
+      }
+    } else {
+      const u32x4 a0 = buf_load_b128(rx, vx, kr * 2u);
+      const T* tt = reinterpret_cast<const T*>(&a0);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) xv[slot][i] = xok ? ElemT<T>::cvt(tt[i]) : 0.0f;
+    }
+  };
+#pragma unroll
+  for (int q = 0; q < DEC_P && q < STEPS; ++q) issue(q, q);
+  // keep the prefetch loads where they are written (the scheduler would
+  // otherwise sink them next to their first use)
+  __builtin_amdgcn_sched_barrier(0);
+  __syncthreads();  // staged scales visible to every lane
+#pragma unroll
+  for (int st = 0; st < STEPS; ++st) {
+    const int q = st % DEC_P;
+    const f32x4 s0 = *reinterpret_cast<const f32x4*>(wS + st * 32 + 8 * g);
+    const f32x4 s1 = *reinterpret_cast<const f32x4*>(wS + st * 32 + 8 * g + 4);
+    float a[8];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      a[r] = xv[q][r] * s0[r];
+      a[4 + r] = xv[q][4 + r] * s1[r];
+    }
+    f16x8 ahi, alo;
+    split_hi_lo(a, ahi, alo);
+    uint32_t lo4[8], hi4[8];
+#pragma unroll
+    for (int r = 0; r < 8; ++r) {
+      const uint32_t X = wv[q][r] ^ 0x88888888u;
+      hi4[r] = X & 0xF0F0F0F0u;
+      lo4[r] = (X << 4) & 0xF0F0F0F0u;
+    }
+    if (st + DEC_P < STEPS) issue(q, st + DEC_P);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+      const uint32_t p = (uint32_t)(t >> 1);
+      const uint32_t sel = 0x0C000C00u | ((4u + p) << 16) | p;
+      uint32_t bq[4];
+#pragma unroll
+      for (int h = 0; h < 4; ++h) {
+        const uint32_t s0 = (t & 1) ? hi4[2 * h] : lo4[2 * h];
+        const uint32_t s1 = (t & 1) ? hi4[2 * h + 1] : lo4[2 * h + 1];
+        bq[h] = __builtin_amdgcn_perm(s1, s0, sel);
+      }
+      const f16x8 bt = __builtin_bit_cast(f16x8, u32x4v{bq[0], bq[1], bq[2], bq[3]});
+      acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi, bt, acc[t], 0, 0, 0);
+      acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo, bt, acc[t], 0, 0, 0);
+    }
+    corr = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi, b8, corr, 0, 0, 0);
+    corr = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo, b8, corr, 0, 0, 0);
+  }
+  // this wave's partial: rows m = 4g+i, columns 8j+t of block nb
+  float v[8][4];
+#pragma unroll
+  for (int t = 0; t < 8; ++t)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[t][i] = (acc[t][i] - corr[i]) * 1048576.0f;
+
+  // fixed-order tree over the RG row groups of each block
+#pragma unroll
+  for (int half = RG / 2; half >= 1; half >>= 1) {
+    if (rg >= half && rg < 2 * half) {
+      f32x4* slot = red + ((rg - half) * NBW + nbl) * 512;
+#pragma unroll
+      for (int t = 0; t < 8; ++t) slot[t * 64 + lane] = f32x4{v[t][0], v[t][1], v[t][2], v[t][3]};
+    }
+    __syncthreads();
+    if (rg < half) {
+      const f32x4* slot = red + (rg * NBW + nbl) * 512;
+#pragma unroll
+      for (int t = 0; t < 8; ++t) {
+        const f32x4 o = slot[t * 64 + lane];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) v[t][i] = v[t][i] + o[i];
+      }
+    }
+    __syncthreads();
+  }
+  const int64_t col0 = nb * 128;
+  if (S == 1) {
+    if (rg == 0) {
+#pragma unroll
+      for (int t = 0; t < 8; ++t)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int m = 4 * g + i;
+          const int64_t col = col0 + 8 * j + t;
+          if (m < M) out[(int64_t)m * N + col] = bias ? v[t][i] + bias[col] : v[t][i];
+        }
+    }
+    return;
+  }
+  // partials: [S][column group][NBW][8 tiles][64 lanes] float4, written with
+  // agent-coherent (sc1) stores that complete before the workgroup is counted
+  const int64_t NCG = NB / NBW;
+  const uint32_t part_bytes = (uint32_t)((int64_t)S * NB * 8 * 64 * 16);
+  const __amdgpu_buffer_rsrc_t rp = make_rsrc(partials, part_bytes);
+  const uint32_t pbase = (uint32_t)((((int64_t)cg * NBW + nbl) * 512 + lane) * 16);
+  const uint32_t split_stride = (uint32_t)(NCG * NBW * 512 * 16);
+  if (rg == 0) {
+#pragma unroll
+    for (int t = 0; t < 8; ++t)
+      __builtin_amdgcn_raw_buffer_store_b128(f32x4{v[t][0], v[t][1], v[t][2], v[t][3]}, rp,
+                                             pbase + (uint32_t)t * 1024u, (uint32_t)ks * split_stride, 16);
+    __builtin_amdgcn_s_waitcnt(0);
+  }
+  __syncthreads();
+  if (threadIdx.x == 0)
+    s_last = __hip_atomic_fetch_add(&counters[cg], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+             (unsigned)(S - 1);
+  __syncthreads();
+  if (!s_last) return;
+  // last workgroup of this column group: the row-group-0 waves sum the S
+  // partials of their block in split order (agent-coherent loads)
+  if (rg == 0) {
+    f32x4 sum[8];
+#pragma unroll
+    for (int t = 0; t < 8; ++t)
+      sum[t] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rp, pbase + (uint32_t)t * 1024u, 0u, 16));
+    for (int s2 = 1; s2 < S; ++s2) {
+#pragma unroll
+      for (int t = 0; t < 8; ++t) {
+        const f32x4 o = __builtin_bit_cast(
+            f32x4, __builtin_amdgcn_raw_buffer_load_b128(rp, pbase + (uint32_t)t * 1024u, (uint32_t)s2 * split_stride, 16));
+        sum[t] = sum[t] + o;
+      }
+    }
+#pragma unroll
+    for (int t = 0; t < 8; ++t)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int m = 4 * g + i;
+        const int64_t col = col0 + 8 * j + t;
+        if (m < M) out[(int64_t)m * N + col] = bias ? sum[t][i] + bias[col] : sum[t][i];
+      }
+  }
+  if (threadIdx.x == 0) __hip_atomic_store(&counters[cg], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+struct DecodePlan {
+  int S, steps, nbw;
+  size_t partial_bytes, counter_bytes;
+};
+
+static DecodePlan plan_decode(int64_t K, int64_t N) {
+  DecodePlan p;
+  const int64_t NB = N / 128;
+  // widest column group (shared x / scale lines) that still gives every CU
+  // a workgroup with 8-step waves; fall back to narrower groups, then 4 steps
+  p.nbw = 1;
+  p.steps = 4;
+  const int64_t target = num_cus();
+  for (int nbw : {4, 2, 1}) {
+    if (NB % nbw) continue;
+    for (int steps : {8, 4}) {
+      const int64_t rows_per_wg = (int64_t)(DEC_WAVES / nbw) * 32 * steps;
+      const int64_t wgs = (NB / nbw) * ceil_div(K, rows_per_wg);
+      const int64_t S = ceil_div(K, rows_per_wg);
+      if (wgs >= target && S <= 8) {
+        p.nbw = nbw;
+        p.steps = steps;
+        goto done;
+      }
+    }
+  }
+done:
+  p.S = (int)ceil_div(K, (int64_t)(DEC_WAVES / p.nbw) * 32 * p.steps);
+  p.partial_bytes = p.S > 1 ? (((size_t)p.S * (size_t)(N / 128) * 8 * 64 * 16 + 255) & ~(size_t)255) : 0;
+  // the counters live in a fixed prefix so that their position never depends
+  // on the problem shape: a zero-filled workspace stays valid across calls of
+  // any shape (each call resets the counters it used)
+  p.counter_bytes = p.S > 1 ? DEC_COUNTER_BYTES : 0;
+  return p;
+}
+
+template <typename T, int STEPS, int NBW>
+static void launch_decode_t(const DecodePlan& p, hipStream_t st, const void* x, int64_t M, int64_t K, int64_t N,
+                            const uint32_t* w, const float* scales, const float* bias, float* out, float* partials,
+                            unsigned* counters) {
+  const dim3 grid((unsigned)((N / 128 / NBW) * p.S));
+  hipLaunchKernelGGL((k_linear_w4_decode<T, STEPS, NBW>), grid, dim3(64 * DEC_WAVES), 0, st, (const T*)x, (int)M, K,
+                     N, w, scales, bias, out, partials, counters, p.S);
+}
+
+template <typename T>
+static void launch_decode(const DecodePlan& p, hipStream_t st, const void* x, int64_t M, int64_t K, int64_t N,
+                          const uint32_t* w, const float* scales, const float* bias, float* out, float* partials,
+                          unsigned* counters) {
+#define MXK_DEC(STEPS, NBW)                                                                          \
+  if (p.steps == STEPS && p.nbw == NBW) {                                                           \
+    launch_decode_t<T, STEPS, NBW>(p, st, x, M, K, N, w, scales, bias, out, partials, counters);    \
+    return;                                                                                         \
+  }
+  MXK_DEC(8, 4)
+  MXK_DEC(8, 2)
+  MXK_DEC(8, 1)
+  MXK_DEC(4, 4)
+  MXK_DEC(4, 2)
+  MXK_DEC(4, 1)
+#undef MXK_DEC
+}
+
+static bool decode_eligible(int64_t M, int64_t K, int64_t N, int kind, int bits, int block, const void* x,
+                            int x_type, const void* w) {
+  if (kind != MXK_KIND_INT || bits != 4 || block != 128) return false;
+  if (M < 1 || M > 16 || K % 32 != 0 || N % 128 != 0) return false;
+  if (N / 128 > DEC_COUNTER_BYTES / 4) return false;
+  if (!aligned16(x) || (reinterpret_cast<uintptr_t>(w) & 3u) != 0) return false;
+  const int esz = x_type == MXK_IN_F32 ? 4 : 2;
+  if ((K * esz) % 16 != 0) return false;
+  // 32-bit buffer offsets with headroom
+  if (K * N / 2 >= (int64_t(1) << 31) || K * (N / 128) * 4 >= (int64_t(1) << 31) || 16 * K * esz >= (int64_t(1) << 31))
+    return false;
+  // partial buffer: S * (N/128) * 8 KiB, addressed with 32-bit offsets
+  if ((K / 32 + 1) * (N / 128) * 8192 >= (int64_t(1) << 31)) return false;
+  return true;
+}
+
 template <typename T, int MODE, int BITS>
 static int launch_linear(const T* x, int64_t M, int64_t K, int64_t N, const uint8_t* packed, int64_t pbytes,
                          const float* scales, int block, const float* bias, float* out, hipStream_t st) {
@@ -140,22 +470,29 @@ using namespace mxk;
 extern "C" {
 
 size_t mxk_linear_workspace(int64_t M, int64_t K, int64_t N, int bits, int block) {
-  (void)M;
-  (void)K;
-  (void)N;
-  (void)bits;
-  (void)block;
-  return 0;
+  if (M < 1 || M > 16 || bits != 4 || block != 128 || K <= 0 || N <= 0 || K % 32 != 0 || N % 128 != 0) return 0;
+  DecodePlan p = plan_decode(K, N);
+  return p.partial_bytes + p.counter_bytes;
 }
 
 int mxk_linear_wq(const void* x, int x_type, int64_t M, int64_t K, const void* w_packed, const float* w_scales,
                   int64_t N, int kind, int bits, int block, const float* bias, float* out, void* workspace,
                   size_t workspace_nbytes, void* stream) {
-  (void)workspace;
-  (void)workspace_nbytes;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   if (M <= 0 || K <= 0 || N <= 0 || block <= 0) return fail(MXK_EINVAL, "linear_wq: sizes must be positive");
   if (!x || !w_packed || !w_scales || !out) return fail(MXK_EINVAL, "linear_wq: null pointer");
+  if (decode_eligible(M, K, N, kind, bits, block, x, x_type, w_packed)) {
+    DecodePlan p = plan_decode(K, N);
+    if (p.S > 1 && (!workspace || workspace_nbytes < p.partial_bytes + p.counter_bytes))
+      return fail(MXK_EINVAL, "linear_wq: decode path needs a zero-initialised workspace of mxk_linear_workspace() bytes");
+    unsigned* counters = p.S > 1 ? reinterpret_cast<unsigned*>(workspace) : nullptr;
+    float* partials = p.S > 1 ? reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(workspace) + DEC_COUNTER_BYTES) : nullptr;
+    const uint32_t* wq = reinterpret_cast<const uint32_t*>(w_packed);
+    if (x_type == MXK_IN_F32) launch_decode<float>(p, st, x, M, K, N, wq, w_scales, bias, out, partials, counters);
+    else if (x_type == MXK_IN_F16) launch_decode<__half>(p, st, x, M, K, N, wq, w_scales, bias, out, partials, counters);
+    else launch_decode<hip_bfloat16>(p, st, x, M, K, N, wq, w_scales, bias, out, partials, counters);
+    return check_launch("linear_wq(decode)");
+  }
   const int64_t nb = ceil_div(K * N, block);
   const int64_t pbytes = mxk_packed_nbytes(bits, nb * block);
   const uint8_t* pk = reinterpret_cast<const uint8_t*>(w_packed);

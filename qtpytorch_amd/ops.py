@@ -97,6 +97,23 @@ def _workspace(nbytes: int, device) -> Optional[Tensor]:
     return torch.empty(int(nbytes), dtype=torch.uint8, device=device)
 
 
+_ZEROED_WS = {}
+
+
+def _zeroed_workspace(nbytes: int, device) -> Optional[Tensor]:
+    """A per-device workspace that starts zero-filled; the kernels that use
+    it (split-K counters) leave it zeroed after each call.  Calls on one
+    device must not overlap while sharing it (same stream, or synchronized)."""
+    if nbytes <= 0:
+        return None
+    key = str(device)
+    ws = _ZEROED_WS.get(key)
+    if ws is None or ws.numel() < nbytes:
+        ws = torch.zeros(int(nbytes), dtype=torch.uint8, device=device)
+        _ZEROED_WS[key] = ws
+    return ws
+
+
 def quantize(x: Tensor, dt, block: int = 128, *, seed: Optional[int] = None,
              signs: Optional[Tensor] = None, n_store: Optional[int] = None
              ) -> Tuple[Tensor, Tensor, int]:
@@ -224,7 +241,7 @@ def linear_wq(x: Tensor, w_packed: Tensor, w_scales: Tensor, dt, in_features: in
     b = None if bias is None else bias.to(device=dev, dtype=torch.float32).contiguous()
     lib = L.lib()
     ws_bytes = lib.mxk_linear_workspace(M, K, N, dt.bits, block)
-    ws = _workspace(ws_bytes, dev)
+    ws = _zeroed_workspace(ws_bytes, dev)
     with torch.cuda.device(dev):
         rc = lib.mxk_linear_wq(xc.data_ptr(), L.elem_type(xc.dtype), M, K, w_packed.contiguous().data_ptr(),
                                w_scales.contiguous().data_ptr(), N, kind, dt.bits, block, L.ptr(b),

@@ -239,6 +239,39 @@ def test_linear_vs_oracle(qa, dtype, shape, xdt):
     assert err <= LINEAR_RTOL * y_ref.abs().max().item(), f"max err {err}"
 
 
+@pytest.mark.parametrize("shape", [(16, 8192, 256), (5, 4096, 384), (16, 2048, 1024), (1, 8192, 128)])
+def test_linear_decode_split_k(qa, shape):
+    """Shapes whose K is split across workgroups (partials + last-workgroup
+    reduction) on the int4 decode path, against the oracle."""
+    M, K, N = shape
+    W = _randn((N, K), 21 + K, outliers=1e-3, scale=20.0) * 0.02
+    x = _randn((M, K), 23 + M)
+    lin = torch.nn.Linear(K, N, bias=False)
+    with torch.no_grad():
+        lin.weight.copy_(W)
+    m = qa.mx_linear.from_linear(lin.to(dev()), qa.get_mx_dtype("int4d"), 128)
+    wp, ws = m._mx_weight._mx_packed.cpu(), m._mx_weight._mx_scales.cpu()
+    y_ref = orc.linear_forward(x, wp, ws, "int4d", K, N, 128)
+    for _ in range(3):  # repeated calls reuse the self-resetting split-K counters
+        y = m(x.to(dev())).cpu()
+        err = (y - y_ref).abs().max().item()
+        assert err <= LINEAR_RTOL * y_ref.abs().max().item(), f"max err {err}"
+
+
+def test_linear_decode_config2_shape(qa):
+    """The benchmark shape: x [16, 8192] @ int4d W [8192, 8192]."""
+    x = _randn((16, 8192), 2)
+    W = _randn((8192, 8192), 3) * 0.02
+    lin = torch.nn.Linear(8192, 8192, bias=False)
+    with torch.no_grad():
+        lin.weight.copy_(W)
+    m = qa.mx_linear.from_linear(lin.to(dev()), qa.get_mx_dtype("int4d"), 128)
+    y = m(x.to(dev())).cpu()
+    y_ref = orc.linear_forward(x, m._mx_weight._mx_packed.cpu(), m._mx_weight._mx_scales.cpu(), "int4d",
+                               8192, 8192, 128)
+    assert (y - y_ref).abs().max().item() <= LINEAR_RTOL * y_ref.abs().max().item()
+
+
 def test_kv_bulk_roundtrip(qa):
     """Config-5 layout at reduced size: fp16 K [B,H,S,D] -> int8dv / int4d per row of D."""
     k = _randn((2, 4, 256, 128), 55).half()
