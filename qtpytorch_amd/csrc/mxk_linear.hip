@@ -155,7 +155,10 @@ __global__ __launch_bounds__(64 * DEC_WAVES, 1) void k_linear_w4_decode(
   __shared__ __attribute__((aligned(16))) f32x4 red[4 * 8 * 64];   // tree slots, lane-major
   __shared__ __attribute__((aligned(16))) float sS[DEC_WAVES * RPW];  // each wave's scales
   __shared__ int s_last;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  // the wave index goes through readfirstlane so that everything derived
+  // from it (row ranges, scalar buffer offsets) is known to be wave-uniform
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int j = lane & 15, g = lane >> 4;
   const int nbl = wave % NBW, rg = wave / NBW;
   const int64_t NB = N / 128;
@@ -187,18 +190,23 @@ __global__ __launch_bounds__(64 * DEC_WAVES, 1) void k_linear_w4_decode(
   const uint32_t row_bytes = (uint32_t)(N / 2), srow_bytes = (uint32_t)(NB * 4);
   const bool mrow = j < M;
   const uint32_t vw = (uint32_t)(8 * g * row_bytes + (nb * 16 + j) * 4);
-  // this wave's RPW scales s[k, nb] go to LDS once (rows past K stage 0)
+  // this wave's RPW scales s[k, nb] go to LDS once (rows past K stage 0);
+  // they are loaded before the weight prefetch and written to LDS after it,
+  // so the two load latencies overlap
   float* wS = sS + wave * RPW;
+  float sc_stage[RPW / 64];
 #pragma unroll
   for (int i = 0; i < RPW / 64; ++i) {
     const int64_t row = k_begin + i * 64 + lane;
-    const bool ok = row < K;
-    const float sc = __uint_as_float(buf_load_b32(rs, (uint32_t)((ok ? row : 0) * srow_bytes + nb * 4), 0u));
-    wS[i * 64 + lane] = ok ? sc : 0.0f;
+    sc_stage[i] = __uint_as_float(buf_load_b32(rs, (uint32_t)((row < K ? row : 0) * srow_bytes + nb * 4), 0u));
   }
   const uint32_t vx = (uint32_t)(((int64_t)(mrow ? j : 0) * K + 8 * g) * sizeof(T));
+  // column groups walk their rows in rotated order, so that the workgroups
+  // sharing an x slice do not all read the same lines at the same moment
+  const int rot = (int)(cg % STEPS);
   auto issue = [&](int slot, int st) {
-    const int64_t k0 = k_begin + (int64_t)st * 32;
+    const int sr = (st + rot) % STEPS;
+    const int64_t k0 = k_begin + (int64_t)sr * 32;
     const bool sin = k0 < K;  // wave-uniform; K % 32 == 0, so a step is wholly in or out
     const uint32_t kr = sin ? (uint32_t)k0 : 0u;
 #pragma unroll
@@ -224,12 +232,15 @@ __global__ __launch_bounds__(64 * DEC_WAVES, 1) void k_linear_w4_decode(
   // keep the prefetch loads where they are written (the scheduler would
   // otherwise sink them next to their first use)
   __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int i = 0; i < RPW / 64; ++i) wS[i * 64 + lane] = (k_begin + i * 64 + lane < K) ? sc_stage[i] : 0.0f;
   __syncthreads();  // staged scales visible to every lane
 #pragma unroll
   for (int st = 0; st < STEPS; ++st) {
     const int q = st % DEC_P;
-    const f32x4 s0 = *reinterpret_cast<const f32x4*>(wS + st * 32 + 8 * g);
-    const f32x4 s1 = *reinterpret_cast<const f32x4*>(wS + st * 32 + 8 * g + 4);
+    const int sr = (st + rot) % STEPS;
+    const f32x4 s0 = *reinterpret_cast<const f32x4*>(wS + sr * 32 + 8 * g);
+    const f32x4 s1 = *reinterpret_cast<const f32x4*>(wS + sr * 32 + 8 * g + 4);
     float a[8];
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
@@ -326,29 +337,32 @@ __global__ __launch_bounds__(64 * DEC_WAVES, 1) void k_linear_w4_decode(
              (unsigned)(S - 1);
   __syncthreads();
   if (!s_last) return;
-  // last workgroup of this column group: the row-group-0 waves sum the S
-  // partials of their block in split order (agent-coherent loads)
-  if (rg == 0) {
-    f32x4 sum[8];
+  // last workgroup of this column group: every thread sums NBW*2 float4 of
+  // the S partials in split order, with all of a chunk's loads in flight
+  const uint32_t cg_base = (uint32_t)((int64_t)cg * NBW * 512 * 16);
+  for (int e0 = 0; e0 < NBW * 512; e0 += 512) {
+    const int e = e0 + threadIdx.x;  // float4 index within this column group's block
+    const uint32_t off = cg_base + (uint32_t)e * 16u;
+    f32x4 sum = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int sb = 0; sb < S; sb += 8) {
+      f32x4 part[8];
 #pragma unroll
-    for (int t = 0; t < 8; ++t)
-      sum[t] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rp, pbase + (uint32_t)t * 1024u, 0u, 16));
-    for (int s2 = 1; s2 < S; ++s2) {
+      for (int u = 0; u < 8; ++u)
+        part[u] = (sb + u < S) ? __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                      rp, off, (uint32_t)(sb + u) * split_stride, 16))
+                               : f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int t = 0; t < 8; ++t) {
-        const f32x4 o = __builtin_bit_cast(
-            f32x4, __builtin_amdgcn_raw_buffer_load_b128(rp, pbase + (uint32_t)t * 1024u, (uint32_t)s2 * split_stride, 16));
-        sum[t] = sum[t] + o;
-      }
+      for (int u = 0; u < 8; ++u)
+        if (sb + u < S) sum = (sb + u == 0) ? part[u] : sum + part[u];
     }
+    const int enbl = e / 512, et = (e / 64) % 8, el = e % 64;
+    const int eg = el >> 4, ej = el & 15;
+    const int64_t col = (cg * NBW + enbl) * 128 + 8 * ej + et;
 #pragma unroll
-    for (int t = 0; t < 8; ++t)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int m = 4 * g + i;
-        const int64_t col = col0 + 8 * j + t;
-        if (m < M) out[(int64_t)m * N + col] = bias ? sum[t][i] + bias[col] : sum[t][i];
-      }
+    for (int i = 0; i < 4; ++i) {
+      const int m = 4 * eg + i;
+      if (m < M) out[(int64_t)m * N + col] = bias ? sum[i] + bias[col] : sum[i];
+    }
   }
   if (threadIdx.x == 0) __hip_atomic_store(&counters[cg], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
