@@ -36,7 +36,7 @@
 extern "C" {
 #endif
 
-#define MXK_ABI_VERSION 1
+#define MXK_ABI_VERSION 2
 
 typedef enum {
   MXK_OK = 0,
@@ -143,22 +143,34 @@ int mxk_qgemm(const void* a_packed, const float* a_scales, int64_t a_nscales, co
 
 /* Workspace bytes mxk_linear_wq needs (0 if none).  The decode path
  * (int4 weights, block 128, M <= 16, K % 32 == 0, N % 128 == 0) splits K
- * across workgroups; its workspace (a 64 KiB counter prefix, then the
- * partial sums) must be zero-filled before first use, and every call, of
- * any shape, leaves it ready for the next one.  Calls sharing a workspace
- * must not overlap. */
+ * across workgroups; its workspace (a 64 KiB counter prefix, the partial
+ * sums, then room for block-major scales when w_scales_t is NULL) must be
+ * zero-filled before first use, and every call, of any shape, leaves the
+ * counter prefix ready for the next one.  Calls sharing a workspace must
+ * not overlap. */
 size_t mxk_linear_workspace(int64_t M, int64_t K, int64_t N, int bits, int block);
+
+/* Block-major copy of a weight's scales for the decode path: w_scales_t[b][k]
+ * = w_scales[k * (N/128) + b], i.e. [N/128][K] from the [K][N/128] layout
+ * that quantize(weight.t()) stores (mxtorch.py:7447, 1684-1763).  block must
+ * be 128 and N a multiple of 128.  No reference counterpart: the reference
+ * dequantizes the whole weight instead (mxtorch.py:7454-7473).  Weights are
+ * static, so callers make this copy once per weight. */
+int mxk_linear_prepack_scales(const float* w_scales, int64_t K, int64_t N, int block, float* w_scales_t,
+                              void* stream);
 
 /* Weight-only linear, mx_linear.forward (mxtorch.py:7454-7473):
  * out[M,N] = x[M,K] (x_type, converted to float32) @ dequant(W) (+ bias[N]),
  * W = the packed codes/scales of quantize(weight.t()): [K,N] row-major,
  * blocks of `block` flat elements (mxtorch.py:7447).  The dequantized
  * weight RN(code*s) (mxtorch.py:1573-1575) is formed in registers only.
- * kind/bits as for mxk_quantize (base variant).  Float32 accumulation. */
+ * kind/bits as for mxk_quantize (base variant).  Float32 accumulation.
+ * w_scales_t: optional mxk_linear_prepack_scales() copy of w_scales, read
+ * by the int4 decode path (NULL: that path transposes into the workspace). */
 int mxk_linear_wq(const void* x, int x_type, int64_t M, int64_t K, const void* w_packed,
-                  const float* w_scales, int64_t N, int kind, int bits, int block,
-                  const float* bias, float* out, void* workspace, size_t workspace_nbytes,
-                  void* stream);
+                  const float* w_scales, const float* w_scales_t, int64_t N, int kind, int bits,
+                  int block, const float* bias, float* out, void* workspace,
+                  size_t workspace_nbytes, void* stream);
 
 #ifdef __cplusplus
 }

@@ -43,8 +43,9 @@ SIGNATURES = {
     "mxk_qgemm": (c_int, [c_vp, c_vp, c_i64, c_vp, c_vp, c_i64, c_i64, c_i64, c_i64, c_int, c_int, c_int,
                           c_vp, c_i64, c_vp, c_vp, c_vp, c_vp, c_sz, c_vp]),
     "mxk_linear_workspace": (c_sz, [c_i64, c_i64, c_i64, c_int, c_int]),
-    "mxk_linear_wq": (c_int, [c_vp, c_int, c_i64, c_i64, c_vp, c_vp, c_i64, c_int, c_int, c_int, c_vp,
+    "mxk_linear_wq": (c_int, [c_vp, c_int, c_i64, c_i64, c_vp, c_vp, c_vp, c_i64, c_int, c_int, c_int, c_vp,
                               c_vp, c_vp, c_sz, c_vp]),
+    "mxk_linear_prepack_scales": (c_int, [c_vp, c_i64, c_i64, c_int, c_vp, c_vp]),
 }
 
 
@@ -71,7 +72,7 @@ def lib():
                 raise MXKError(f"{LIB_PATH} does not export {name}")
             fn.restype = res
             fn.argtypes = args
-        if h.mxk_abi_version() != 1:
+        if h.mxk_abi_version() != 2:
             raise MXKError("libmxk.so ABI version mismatch")
         _lib = h
         return h

@@ -104,39 +104,55 @@ __global__ __launch_bounds__(256) void k_linear_generic(const T* __restrict__ x,
 
 // ---------------------------------------------------------------- int4 decode (M <= 16)
 // y[m, n] = sum_k x[m,k] * RN(code[k,n] * s[k, n/128]), weights int4 [K][N]
-// packed along N (LSB nibble = even column), block 128 along N.
+// packed along N (LSB nibble = even column), block 128 along N.  The kernel
+// reads the scales block-major, sT[n/128][k] (mxk_linear_prepack_scales), so
+// that a block's scales along K are contiguous.
 //
 // Work split: a workgroup of 8 waves owns NBW scale blocks (NBW*128 output
-// columns) and 8/NBW*RPW rows of K.  Wave w takes block w % NBW and row
-// group w / NBW, so the waves that share rows share their x and scale
-// cache lines through L1.  Per 32-row step a wave runs
-// v_mfma_f32_16x16x32_f16 on
-//   A[m][k] = x[m,k] * s[k,nb]           split as f16 hi + f16 lo (22 bits)
-//   B[k][c] = f16 with bit pattern ((code+8) << 4), i.e. (code+8) * 2^-20
+// columns) and R = 8/NBW * RPW rows of K.  Wave w takes block w % NBW and
+// row group w / NBW.  Before the main loop the workgroup stages its x rows in
+// LDS as float (rows m >= M and rows past K as zeros; coalesced 16-byte
+// loads, shared by the NBW waves of a row group) and every wave stages its
+// own RPW scales with one 16-byte load per lane; both are issued ahead of the
+// weight prefetch.
+//
+// Per 32-row step a wave runs v_mfma_f32_16x16x32_f16 on
+//   A[m][k] = x[m,k] * s[k,nb]          split as f16 hi + f16 lo (22 bits)
+//   B[k][c] = f16 denormal (code+8) * 2^-24 (even column: low nibble in bits
+//             0-3) or (code+8) * 2^-20 (odd column: high nibble in bits 4-7)
 // over 8 tiles of 16 columns.  Lane (j = lane&15, g = lane>>4) loads the u32
 // holding columns 8j..8j+7 of rows 8g..8g+7; tile t takes nibble t of each,
-// so tile t covers columns {8j + t}.  One v_perm_b32 builds the B operand
-// dword for two rows.  The +8 offset is removed with a correction tile
-// (B = 8 * 2^-20): y = 2^20 * (D - D_corr).
+// so tile t covers columns {8j + t}.  Per row one v_bitop3 isolates the low
+// nibbles (and flips the code's sign bit, giving code+8), one the high
+// nibbles; one v_perm_b32 then builds a B dword from two rows.  The +8 offset
+// is removed with a correction tile D_corr (B = 8 * 2^-20):
+//   odd tiles  y = 2^20 * (D - D_corr),  even tiles  y = 2^24 * (D - D_corr / 16).
 // Reductions are deterministic: waves of a block combine through LDS in a
 // fixed tree; workgroups that split K write partials with agent-coherent
 // stores, count arrivals on an atomic counter, and the last one sums the
-// partials in split order and resets the counter.
+// partials in split order and resets the counter.  When the column groups
+// divide evenly over the 8 XCDs (workgroup b runs on XCD b % 8), all splits of
+// a column group are placed on one XCD; the protocol does not depend on it.
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
 
 #define DEC_WAVES 8
-#define DEC_P 4
 #define DEC_COUNTER_BYTES 65536  // split-K counters: up to 16384 column groups
+#define DEC_XPAD 4               // LDS row padding of the staged x (floats)
+#define DEC_OOB 0x80000000u      // buffer offset past every range: the load returns zeros
 
-__device__ __forceinline__ void split_hi_lo(const float (&a)[8], f16x8& hi, f16x8& lo) {
+// A = x * s as f16 hi + f16 lo: hi = RZ(x*s), lo = RZ(fma(x, s, -hi))
+__device__ __forceinline__ void split_hi_lo(const f32x4& x0, const f32x4& x1, const f32x4& s0, const f32x4& s1,
+                                            f16x8& hi, f16x8& lo) {
+  const float xa[8] = {x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
+  const float sa[8] = {s0[0], s0[1], s0[2], s0[3], s1[0], s1[1], s1[2], s1[3]};
   uint32_t h[4], l[4];
 #pragma unroll
   for (int q = 0; q < 4; ++q) {
-    auto hp = __builtin_amdgcn_cvt_pkrtz(a[2 * q], a[2 * q + 1]);
-    const float r0 = a[2 * q] - (float)hp[0];
-    const float r1 = a[2 * q + 1] - (float)hp[1];
+    auto hp = __builtin_amdgcn_cvt_pkrtz(xa[2 * q] * sa[2 * q], xa[2 * q + 1] * sa[2 * q + 1]);
+    const float r0 = __builtin_fmaf(xa[2 * q], sa[2 * q], -(float)hp[0]);
+    const float r1 = __builtin_fmaf(xa[2 * q + 1], sa[2 * q + 1], -(float)hp[1]);
     auto lp = __builtin_amdgcn_cvt_pkrtz(r0, r1);
     h[q] = __builtin_bit_cast(uint32_t, hp);
     l[q] = __builtin_bit_cast(uint32_t, lp);
@@ -145,15 +161,29 @@ __device__ __forceinline__ void split_hi_lo(const float (&a)[8], f16x8& hi, f16x
   lo = __builtin_bit_cast(f16x8, u32x4v{l[0], l[1], l[2], l[3]});
 }
 
-template <typename T, int STEPS, int NBW>
+template <int STEPS, int NBW>
+struct DecGeom {
+  static constexpr int RPW = STEPS * 32;        // rows per wave
+  static constexpr int RG = DEC_WAVES / NBW;    // row groups per workgroup
+  static constexpr int R = RG * RPW;            // rows per workgroup
+  static constexpr int XS = R + DEC_XPAD;       // LDS row stride of the staged x
+  static constexpr int TREE = RG / 2 > 0 ? RG / 2 : 1;
+};
+
+template <typename T, int STEPS, int NBW, int P>
 __global__ __launch_bounds__(64 * DEC_WAVES, 1) void k_linear_w4_decode(
     const T* __restrict__ x, int M, int64_t K, int64_t N, const uint32_t* __restrict__ w,
-    const float* __restrict__ scales, const float* __restrict__ bias, float* __restrict__ out,
-    float* __restrict__ partials, unsigned* __restrict__ counters, int S) {
-  constexpr int RPW = STEPS * 32;
-  constexpr int RG = DEC_WAVES / NBW;  // row groups per workgroup
-  __shared__ __attribute__((aligned(16))) f32x4 red[4 * 8 * 64];   // tree slots, lane-major
-  __shared__ __attribute__((aligned(16))) float sS[DEC_WAVES * RPW];  // each wave's scales
+    const float* __restrict__ scales_t, const float* __restrict__ bias, float* __restrict__ out,
+    float* __restrict__ partials, unsigned* __restrict__ counters, int S, int xcd_map) {
+  using G = DecGeom<STEPS, NBW>;
+  constexpr int RPW = G::RPW, RG = G::RG, R = G::R, XS = G::XS;
+  constexpr int EPL = 16 / (int)sizeof(T);  // x elements per 16-byte load
+  constexpr int XL = 16 * R / EPL / 512;    // x loads per thread
+  static_assert(XL * 512 * EPL == 16 * R, "x staging must divide evenly");
+  static_assert(RPW / 4 <= 64, "one 16-byte scale load per lane");
+  __shared__ __attribute__((aligned(16))) float sX[16 * XS];
+  __shared__ __attribute__((aligned(16))) float sS[DEC_WAVES * RPW];
+  __shared__ __attribute__((aligned(16))) f32x4 red[G::TREE * NBW * 512];  // tree slots, lane-major
   __shared__ int s_last;
   // the wave index goes through readfirstlane so that everything derived
   // from it (row ranges, scalar buffer offsets) is known to be wave-uniform
@@ -162,101 +192,103 @@ __global__ __launch_bounds__(64 * DEC_WAVES, 1) void k_linear_w4_decode(
   const int j = lane & 15, g = lane >> 4;
   const int nbl = wave % NBW, rg = wave / NBW;
   const int64_t NB = N / 128;
-  const int64_t cg = blockIdx.x / S;
-  const int ks = blockIdx.x % S;
+  int64_t cg;
+  int ks;
+  if (xcd_map) {
+    const int i = (int)(blockIdx.x >> 3);
+    cg = (int64_t)(i / S) * 8 + (blockIdx.x & 7);
+    ks = i % S;
+  } else {
+    cg = blockIdx.x / S;
+    ks = blockIdx.x % S;
+  }
   const int64_t nb = cg * NBW + nbl;
-  const int64_t k_begin = ((int64_t)ks * RG + rg) * RPW;
+  const int64_t k0w = (int64_t)ks * R;                 // first row of the workgroup
+  const int kv = (int)(K - k0w < R ? K - k0w : R);     // its rows inside K (a multiple of 32)
+  const int64_t kw = k0w + (int64_t)rg * RPW;          // this wave's first row
+
+  // ---- staging loads: x rows (workgroup) and this wave's scales, zeros out of range
+  const __amdgpu_buffer_rsrc_t rx = make_rsrc(x, (uint32_t)((int64_t)M * K * sizeof(T)));
+  const __amdgpu_buffer_rsrc_t rs = make_rsrc(scales_t, (uint32_t)(K * NB * 4));
+  u32x4 xst[XL];
+#pragma unroll
+  for (int i = 0; i < XL; ++i) {
+    const int e = threadIdx.x + 512 * i;
+    const int m = e / (R / EPL), c = e % (R / EPL);
+    const bool ok = m < M && c * EPL < kv;
+    xst[i] = buf_load_b128(rx, ok ? (uint32_t)(((int64_t)m * K + k0w + (int64_t)c * EPL) * sizeof(T)) : DEC_OOB, 0u);
+  }
+  const int64_t r4 = kw + 4 * lane;  // K % 4 == 0: a 16-byte group is wholly in or out
+  const u32x4 sst = buf_load_b128(rs, (lane < RPW / 4 && r4 < K) ? (uint32_t)((nb * K + r4) * 4) : DEC_OOB, 0u);
+
+  // ---- weight prefetch, P steps deep over a fully unrolled step sequence:
+  // step st computes from slot st % P, then the slot is refilled with step
+  // st + P.  Straight-line code lets the compiler wait for exactly the loads
+  // each step needs.  Buffer loads carry one per-lane offset (lane's k-group
+  // and column word) and the step's row in the scalar offset.  The hardware
+  // range check does not cover the scalar offset, so every address is kept
+  // valid by construction: a step past K (only in the last split when K is
+  // not a multiple of R) re-reads rows 0..31, and its x rows and scales are
+  // zeros.
+  const __amdgpu_buffer_rsrc_t rw = make_rsrc(w, (uint32_t)(K * N / 2));
+  const uint32_t row_bytes = (uint32_t)(N / 2);
+  const uint32_t vw = (uint32_t)(8 * g * row_bytes + (nb * 16 + j) * 4);
+  uint32_t wv[P][8];
+  auto issue = [&](int slot, int st) {
+    const int64_t k0 = kw + (int64_t)st * 32;
+    const uint32_t kr = k0 < K ? (uint32_t)k0 : 0u;  // wave-uniform
+#pragma unroll
+    for (int r = 0; r < 8; ++r) wv[slot][r] = buf_load_b32(rw, vw, (kr + r) * row_bytes);
+  };
+#pragma unroll
+  for (int q = 0; q < P && q < STEPS; ++q) issue(q, q);
+  // keep the prefetch loads where they are written (the scheduler would
+  // otherwise sink them next to their first use)
+  __builtin_amdgcn_sched_barrier(0);
+
+  // ---- staged data to LDS: float x, row m at sX[m * XS]; scales per wave
+#pragma unroll
+  for (int i = 0; i < XL; ++i) {
+    const int e = threadIdx.x + 512 * i;
+    const int m = e / (R / EPL), c = e % (R / EPL);
+    float* dst = sX + m * XS + c * EPL;
+    if constexpr (EPL == 4) {
+      *reinterpret_cast<f32x4*>(dst) = __builtin_bit_cast(f32x4, xst[i]);
+    } else {
+      const T* tt = reinterpret_cast<const T*>(&xst[i]);
+      *reinterpret_cast<f32x4*>(dst) =
+          f32x4{ElemT<T>::cvt(tt[0]), ElemT<T>::cvt(tt[1]), ElemT<T>::cvt(tt[2]), ElemT<T>::cvt(tt[3])};
+      *reinterpret_cast<f32x4*>(dst + 4) =
+          f32x4{ElemT<T>::cvt(tt[4]), ElemT<T>::cvt(tt[5]), ElemT<T>::cvt(tt[6]), ElemT<T>::cvt(tt[7])};
+    }
+  }
+  float* wS = sS + wave * RPW;
+  if (lane < RPW / 4) *reinterpret_cast<f32x4*>(wS + 4 * lane) = __builtin_bit_cast(f32x4, sst);
+  __syncthreads();
 
   f32x4 acc[8];
 #pragma unroll
   for (int t = 0; t < 8; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
   f32x4 corr = f32x4{0.f, 0.f, 0.f, 0.f};
   const f16x8 b8 = __builtin_bit_cast(f16x8, u32x4v{0x00800080u, 0x00800080u, 0x00800080u, 0x00800080u});
-
-  // P-deep software prefetch over a fully unrolled step sequence: step st
-  // computes from slot st % P, then the slot is refilled with step st + P.
-  // Straight-line code lets the compiler wait for exactly the loads each
-  // step needs.  Buffer loads carry one per-lane offset (lane's k-group and
-  // column word) and the step's row in the scalar offset.  The hardware range
-  // check does not cover the scalar offset, so every address is kept valid
-  // by construction: a step past K (only in the last split when K is not a
-  // multiple of the split) re-reads rows 0..31 with its x and scales forced
-  // to zero, and x rows past M read row 0 and are zeroed.
-  uint32_t wv[DEC_P][8];
-  float xv[DEC_P][8];
-  const __amdgpu_buffer_rsrc_t rw = make_rsrc(w, (uint32_t)(K * N / 2));
-  const __amdgpu_buffer_rsrc_t rs = make_rsrc(scales, (uint32_t)(K * NB * 4));
-  const __amdgpu_buffer_rsrc_t rx = make_rsrc(x, (uint32_t)((int64_t)M * K * sizeof(T)));
-  const uint32_t row_bytes = (uint32_t)(N / 2), srow_bytes = (uint32_t)(NB * 4);
-  const bool mrow = j < M;
-  const uint32_t vw = (uint32_t)(8 * g * row_bytes + (nb * 16 + j) * 4);
-  // this wave's RPW scales s[k, nb] go to LDS once (rows past K stage 0);
-  // they are loaded before the weight prefetch and written to LDS after it,
-  // so the two load latencies overlap
-  float* wS = sS + wave * RPW;
-  float sc_stage[RPW / 64];
-#pragma unroll
-  for (int i = 0; i < RPW / 64; ++i) {
-    const int64_t row = k_begin + i * 64 + lane;
-    sc_stage[i] = __uint_as_float(buf_load_b32(rs, (uint32_t)((row < K ? row : 0) * srow_bytes + nb * 4), 0u));
-  }
-  const uint32_t vx = (uint32_t)(((int64_t)(mrow ? j : 0) * K + 8 * g) * sizeof(T));
-  // column groups walk their rows in rotated order, so that the workgroups
-  // sharing an x slice do not all read the same lines at the same moment
-  const int rot = (int)(cg % STEPS);
-  auto issue = [&](int slot, int st) {
-    const int sr = (st + rot) % STEPS;
-    const int64_t k0 = k_begin + (int64_t)sr * 32;
-    const bool sin = k0 < K;  // wave-uniform; K % 32 == 0, so a step is wholly in or out
-    const uint32_t kr = sin ? (uint32_t)k0 : 0u;
-#pragma unroll
-    for (int r = 0; r < 8; ++r) wv[slot][r] = buf_load_b32(rw, vw, (kr + r) * row_bytes);
-    const bool xok = sin && mrow;
-    if constexpr (sizeof(T) == 4) {
-      const u32x4 a0 = buf_load_b128(rx, vx, kr * 4u);
-      const u32x4 a1 = buf_load_b128(rx, vx + 16u, kr * 4u);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        xv[slot][i] = xok ? __uint_as_float(a0[i]) : 0.0f;
-        xv[slot][4 + i] = xok ? __uint_as_float(a1[i]) : 0.0f;
-      }
-    } else {
-      const u32x4 a0 = buf_load_b128(rx, vx, kr * 2u);
-      const T* tt = reinterpret_cast<const T*>(&a0);
-#pragma unroll
-      for (int i = 0; i < 8; ++i) xv[slot][i] = xok ? ElemT<T>::cvt(tt[i]) : 0.0f;
-    }
-  };
-#pragma unroll
-  for (int q = 0; q < DEC_P && q < STEPS; ++q) issue(q, q);
-  // keep the prefetch loads where they are written (the scheduler would
-  // otherwise sink them next to their first use)
-  __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-  for (int i = 0; i < RPW / 64; ++i) wS[i * 64 + lane] = (k_begin + i * 64 + lane < K) ? sc_stage[i] : 0.0f;
-  __syncthreads();  // staged scales visible to every lane
+  const float* xrow = sX + j * XS + rg * RPW + 8 * g;
+  const float* srow = wS + 8 * g;
 #pragma unroll
   for (int st = 0; st < STEPS; ++st) {
-    const int q = st % DEC_P;
-    const int sr = (st + rot) % STEPS;
-    const f32x4 s0 = *reinterpret_cast<const f32x4*>(wS + sr * 32 + 8 * g);
-    const f32x4 s1 = *reinterpret_cast<const f32x4*>(wS + sr * 32 + 8 * g + 4);
-    float a[8];
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      a[r] = xv[q][r] * s0[r];
-      a[4 + r] = xv[q][4 + r] * s1[r];
-    }
+    const int q = st % P;
+    const f32x4 x0 = *reinterpret_cast<const f32x4*>(xrow + st * 32);
+    const f32x4 x1 = *reinterpret_cast<const f32x4*>(xrow + st * 32 + 4);
+    const f32x4 s0 = *reinterpret_cast<const f32x4*>(srow + st * 32);
+    const f32x4 s1 = *reinterpret_cast<const f32x4*>(srow + st * 32 + 4);
     f16x8 ahi, alo;
-    split_hi_lo(a, ahi, alo);
+    split_hi_lo(x0, x1, s0, s1, ahi, alo);
     uint32_t lo4[8], hi4[8];
 #pragma unroll
     for (int r = 0; r < 8; ++r) {
-      const uint32_t X = wv[q][r] ^ 0x88888888u;
-      hi4[r] = X & 0xF0F0F0F0u;
-      lo4[r] = (X << 4) & 0xF0F0F0F0u;
+      lo4[r] = (wv[q][r] & 0x0F0F0F0Fu) ^ 0x08080808u;
+      hi4[r] = (wv[q][r] & 0xF0F0F0F0u) ^ 0x80808080u;
     }
-    if (st + DEC_P < STEPS) issue(q, st + DEC_P);
+    if (st + P < STEPS) issue(q, st + P);
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int t = 0; t < 8; ++t) {
@@ -265,9 +297,9 @@ __global__ __launch_bounds__(64 * DEC_WAVES, 1) void k_linear_w4_decode(
       uint32_t bq[4];
 #pragma unroll
       for (int h = 0; h < 4; ++h) {
-        const uint32_t s0 = (t & 1) ? hi4[2 * h] : lo4[2 * h];
-        const uint32_t s1 = (t & 1) ? hi4[2 * h + 1] : lo4[2 * h + 1];
-        bq[h] = __builtin_amdgcn_perm(s1, s0, sel);
+        const uint32_t a0 = (t & 1) ? hi4[2 * h] : lo4[2 * h];
+        const uint32_t a1 = (t & 1) ? hi4[2 * h + 1] : lo4[2 * h + 1];
+        bq[h] = __builtin_amdgcn_perm(a1, a0, sel);
       }
       const f16x8 bt = __builtin_bit_cast(f16x8, u32x4v{bq[0], bq[1], bq[2], bq[3]});
       acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi, bt, acc[t], 0, 0, 0);
@@ -281,7 +313,8 @@ __global__ __launch_bounds__(64 * DEC_WAVES, 1) void k_linear_w4_decode(
 #pragma unroll
   for (int t = 0; t < 8; ++t)
 #pragma unroll
-    for (int i = 0; i < 4; ++i) v[t][i] = (acc[t][i] - corr[i]) * 1048576.0f;
+    for (int i = 0; i < 4; ++i)
+      v[t][i] = (t & 1) ? (acc[t][i] - corr[i]) * 1048576.0f : (acc[t][i] - corr[i] * 0.0625f) * 16777216.0f;
 
   // fixed-order tree over the RG row groups of each block
 #pragma unroll
@@ -337,69 +370,102 @@ __global__ __launch_bounds__(64 * DEC_WAVES, 1) void k_linear_w4_decode(
              (unsigned)(S - 1);
   __syncthreads();
   if (!s_last) return;
-  // last workgroup of this column group: every thread sums NBW*2 float4 of
-  // the S partials in split order, with all of a chunk's loads in flight
+  // last workgroup of this column group: every thread sums NBW float4 of the
+  // S partials in split order, with up to 16 loads in flight per round
+  constexpr int CH = 16 / NBW;  // splits per round
   const uint32_t cg_base = (uint32_t)((int64_t)cg * NBW * 512 * 16);
-  for (int e0 = 0; e0 < NBW * 512; e0 += 512) {
-    const int e = e0 + threadIdx.x;  // float4 index within this column group's block
-    const uint32_t off = cg_base + (uint32_t)e * 16u;
-    f32x4 sum = f32x4{0.f, 0.f, 0.f, 0.f};
-    for (int sb = 0; sb < S; sb += 8) {
-      f32x4 part[8];
+  f32x4 sum[NBW];
+  for (int sb = 0; sb < S; sb += CH) {
+    f32x4 part[CH][NBW];
 #pragma unroll
-      for (int u = 0; u < 8; ++u)
-        part[u] = (sb + u < S) ? __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                                      rp, off, (uint32_t)(sb + u) * split_stride, 16))
-                               : f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int u = 0; u < CH; ++u)
 #pragma unroll
-      for (int u = 0; u < 8; ++u)
-        if (sb + u < S) sum = (sb + u == 0) ? part[u] : sum + part[u];
-    }
+      for (int b = 0; b < NBW; ++b)
+        part[u][b] = __builtin_bit_cast(
+            f32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                       rp, sb + u < S ? cg_base + (uint32_t)(threadIdx.x + 512 * b) * 16u : DEC_OOB,
+                       sb + u < S ? (uint32_t)(sb + u) * split_stride : 0u, 16));
+#pragma unroll
+    for (int u = 0; u < CH; ++u)
+      if (sb + u < S) {
+#pragma unroll
+        for (int b = 0; b < NBW; ++b) sum[b] = (sb + u == 0) ? part[u][b] : sum[b] + part[u][b];
+      }
+  }
+#pragma unroll
+  for (int b = 0; b < NBW; ++b) {
+    const int e = threadIdx.x + 512 * b;  // float4 index within this column group's blocks
     const int enbl = e / 512, et = (e / 64) % 8, el = e % 64;
     const int eg = el >> 4, ej = el & 15;
     const int64_t col = (cg * NBW + enbl) * 128 + 8 * ej + et;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int m = 4 * eg + i;
-      if (m < M) out[(int64_t)m * N + col] = bias ? sum[i] + bias[col] : sum[i];
+      if (m < M) out[(int64_t)m * N + col] = bias ? sum[b][i] + bias[col] : sum[b][i];
     }
   }
   if (threadIdx.x == 0) __hip_atomic_store(&counters[cg], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// sT[b][k] = s[k][b]: the reference's scales of a [K, N] weight with blocks
+// of 128 along N ([K][NB] row-major) to the block-major order the decode
+// kernel reads ([NB][K]).  32x32 tiles through LDS, both sides coalesced.
+__global__ __launch_bounds__(256) void k_transpose_scales(const float* __restrict__ s, int64_t K, int64_t NB,
+                                                          float* __restrict__ sT) {
+  __shared__ float tile[32][33];
+  const int64_t b0 = (int64_t)blockIdx.x * 32, k0 = (int64_t)blockIdx.y * 32;
+  const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;
+  for (int i = ty; i < 32; i += 8) {
+    const int64_t k = k0 + i, b = b0 + tx;
+    tile[i][tx] = (k < K && b < NB) ? s[k * NB + b] : 0.0f;
+  }
+  __syncthreads();
+  for (int i = ty; i < 32; i += 8) {
+    const int64_t b = b0 + i, k = k0 + tx;
+    if (b < NB && k < K) sT[b * K + k] = tile[tx][i];
+  }
+}
+
+static void launch_transpose_scales(const float* s, int64_t K, int64_t NB, float* sT, hipStream_t st) {
+  const dim3 grid((unsigned)ceil_div(NB, 32), (unsigned)ceil_div(K, 32));
+  hipLaunchKernelGGL(k_transpose_scales, grid, dim3(256), 0, st, s, K, NB, sT);
+}
+
 struct DecodePlan {
-  int S, steps, nbw;
-  size_t partial_bytes, counter_bytes;
+  int S, steps, nbw, xcd_map;
+  size_t partial_bytes, counter_bytes, scales_t_bytes;
 };
+
+static int64_t dec_rows(int nbw, int steps) { return (int64_t)(DEC_WAVES / nbw) * 32 * steps; }
 
 static DecodePlan plan_decode(int64_t K, int64_t N) {
   DecodePlan p;
   const int64_t NB = N / 128;
-  // widest column group (shared x / scale lines) that still gives every CU
-  // a workgroup with 8-step waves; fall back to narrower groups, then 4 steps
+  // widest column group (shared x / scale staging) that still gives every CU
+  // a workgroup; fall back to narrower groups, then shorter waves
+  static const int cand[][2] = {{2, 8}, {4, 8}, {2, 4}, {4, 4}, {1, 4}};
   p.nbw = 1;
   p.steps = 4;
   const int64_t target = num_cus();
-  for (int nbw : {4, 2, 1}) {
+  for (const auto& c : cand) {
+    const int nbw = c[0], steps = c[1];
     if (NB % nbw) continue;
-    for (int steps : {8, 4}) {
-      const int64_t rows_per_wg = (int64_t)(DEC_WAVES / nbw) * 32 * steps;
-      const int64_t wgs = (NB / nbw) * ceil_div(K, rows_per_wg);
-      const int64_t S = ceil_div(K, rows_per_wg);
-      if (wgs >= target && S <= 8) {
-        p.nbw = nbw;
-        p.steps = steps;
-        goto done;
-      }
+    const int64_t S = ceil_div(K, dec_rows(nbw, steps));
+    if ((NB / nbw) * S >= target && S <= 32) {
+      p.nbw = nbw;
+      p.steps = steps;
+      break;
     }
   }
-done:
-  p.S = (int)ceil_div(K, (int64_t)(DEC_WAVES / p.nbw) * 32 * p.steps);
+  p.S = (int)ceil_div(K, dec_rows(p.nbw, p.steps));
+  p.xcd_map = (NB / p.nbw) % 8 == 0 ? 1 : 0;
   p.partial_bytes = p.S > 1 ? (((size_t)p.S * (size_t)(N / 128) * 8 * 64 * 16 + 255) & ~(size_t)255) : 0;
-  // the counters live in a fixed prefix so that their position never depends
-  // on the problem shape: a zero-filled workspace stays valid across calls of
-  // any shape (each call resets the counters it used)
-  p.counter_bytes = p.S > 1 ? DEC_COUNTER_BYTES : 0;
+  // the counters live in a fixed prefix that nothing else overwrites, so a
+  // zero-filled workspace stays valid across calls of any shape (each call
+  // resets the counters it used)
+  p.counter_bytes = DEC_COUNTER_BYTES;
+  // room for block-major scales when the caller has no prepacked copy
+  p.scales_t_bytes = ((size_t)K * (size_t)NB * 4 + 255) & ~(size_t)255;
   return p;
 }
 
@@ -408,8 +474,8 @@ static void launch_decode_t(const DecodePlan& p, hipStream_t st, const void* x, 
                             const uint32_t* w, const float* scales, const float* bias, float* out, float* partials,
                             unsigned* counters) {
   const dim3 grid((unsigned)((N / 128 / NBW) * p.S));
-  hipLaunchKernelGGL((k_linear_w4_decode<T, STEPS, NBW>), grid, dim3(64 * DEC_WAVES), 0, st, (const T*)x, (int)M, K,
-                     N, w, scales, bias, out, partials, counters, p.S);
+  hipLaunchKernelGGL((k_linear_w4_decode<T, STEPS, NBW, 4>), grid, dim3(64 * DEC_WAVES), 0, st, (const T*)x, (int)M,
+                     K, N, w, scales, bias, out, partials, counters, p.S, p.xcd_map);
 }
 
 template <typename T>
@@ -421,11 +487,10 @@ static void launch_decode(const DecodePlan& p, hipStream_t st, const void* x, in
     launch_decode_t<T, STEPS, NBW>(p, st, x, M, K, N, w, scales, bias, out, partials, counters);    \
     return;                                                                                         \
   }
-  MXK_DEC(8, 4)
   MXK_DEC(8, 2)
-  MXK_DEC(8, 1)
-  MXK_DEC(4, 4)
+  MXK_DEC(8, 4)
   MXK_DEC(4, 2)
+  MXK_DEC(4, 4)
   MXK_DEC(4, 1)
 #undef MXK_DEC
 }
@@ -434,7 +499,7 @@ static bool decode_eligible(int64_t M, int64_t K, int64_t N, int kind, int bits,
                             int x_type, const void* w) {
   if (kind != MXK_KIND_INT || bits != 4 || block != 128) return false;
   if (M < 1 || M > 16 || K % 32 != 0 || N % 128 != 0) return false;
-  if (N / 128 > DEC_COUNTER_BYTES / 4) return false;
+  if (N / 128 > DEC_COUNTER_BYTES / 4 || K / 32 >= 65536) return false;
   if (!aligned16(x) || (reinterpret_cast<uintptr_t>(w) & 3u) != 0) return false;
   const int esz = x_type == MXK_IN_F32 ? 4 : 2;
   if ((K * esz) % 16 != 0) return false;
@@ -486,25 +551,43 @@ extern "C" {
 size_t mxk_linear_workspace(int64_t M, int64_t K, int64_t N, int bits, int block) {
   if (M < 1 || M > 16 || bits != 4 || block != 128 || K <= 0 || N <= 0 || K % 32 != 0 || N % 128 != 0) return 0;
   DecodePlan p = plan_decode(K, N);
-  return p.partial_bytes + p.counter_bytes;
+  return p.counter_bytes + p.partial_bytes + p.scales_t_bytes;
+}
+
+int mxk_linear_prepack_scales(const float* w_scales, int64_t K, int64_t N, int block, float* w_scales_t,
+                              void* stream) {
+  if (!w_scales || !w_scales_t) return fail(MXK_EINVAL, "linear_prepack_scales: null pointer");
+  if (block != 128 || K <= 0 || N <= 0 || N % 128 != 0)
+    return fail(MXK_EINVAL, "linear_prepack_scales: needs block 128, K > 0 and N a multiple of 128");
+  if (ceil_div(K, 32) >= 65536) return fail(MXK_EUNSUPPORTED, "linear_prepack_scales: K too large");
+  launch_transpose_scales(w_scales, K, N / 128, w_scales_t, reinterpret_cast<hipStream_t>(stream));
+  return check_launch("linear_prepack_scales");
 }
 
 int mxk_linear_wq(const void* x, int x_type, int64_t M, int64_t K, const void* w_packed, const float* w_scales,
-                  int64_t N, int kind, int bits, int block, const float* bias, float* out, void* workspace,
-                  size_t workspace_nbytes, void* stream) {
+                  const float* w_scales_t, int64_t N, int kind, int bits, int block, const float* bias, float* out,
+                  void* workspace, size_t workspace_nbytes, void* stream) {
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   if (M <= 0 || K <= 0 || N <= 0 || block <= 0) return fail(MXK_EINVAL, "linear_wq: sizes must be positive");
   if (!x || !w_packed || !w_scales || !out) return fail(MXK_EINVAL, "linear_wq: null pointer");
   if (decode_eligible(M, K, N, kind, bits, block, x, x_type, w_packed)) {
     DecodePlan p = plan_decode(K, N);
-    if (p.S > 1 && (!workspace || workspace_nbytes < p.partial_bytes + p.counter_bytes))
+    const size_t need = p.counter_bytes + p.partial_bytes + (w_scales_t ? 0 : p.scales_t_bytes);
+    if (need > 0 && (!workspace || workspace_nbytes < need))
       return fail(MXK_EINVAL, "linear_wq: decode path needs a zero-initialised workspace of mxk_linear_workspace() bytes");
-    unsigned* counters = p.S > 1 ? reinterpret_cast<unsigned*>(workspace) : nullptr;
-    float* partials = p.S > 1 ? reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(workspace) + DEC_COUNTER_BYTES) : nullptr;
+    uint8_t* ws = reinterpret_cast<uint8_t*>(workspace);
+    unsigned* counters = p.S > 1 ? reinterpret_cast<unsigned*>(ws) : nullptr;
+    float* partials = p.S > 1 ? reinterpret_cast<float*>(ws + p.counter_bytes) : nullptr;
+    const float* sT = w_scales_t;
+    if (!sT) {
+      float* tmp = reinterpret_cast<float*>(ws + p.counter_bytes + p.partial_bytes);
+      launch_transpose_scales(w_scales, K, N / 128, tmp, st);
+      sT = tmp;
+    }
     const uint32_t* wq = reinterpret_cast<const uint32_t*>(w_packed);
-    if (x_type == MXK_IN_F32) launch_decode<float>(p, st, x, M, K, N, wq, w_scales, bias, out, partials, counters);
-    else if (x_type == MXK_IN_F16) launch_decode<__half>(p, st, x, M, K, N, wq, w_scales, bias, out, partials, counters);
-    else launch_decode<hip_bfloat16>(p, st, x, M, K, N, wq, w_scales, bias, out, partials, counters);
+    if (x_type == MXK_IN_F32) launch_decode<float>(p, st, x, M, K, N, wq, sT, bias, out, partials, counters);
+    else if (x_type == MXK_IN_F16) launch_decode<__half>(p, st, x, M, K, N, wq, sT, bias, out, partials, counters);
+    else launch_decode<hip_bfloat16>(p, st, x, M, K, N, wq, sT, bias, out, partials, counters);
     return check_launch("linear_wq(decode)");
   }
   const int64_t nb = ceil_div(K * N, block);

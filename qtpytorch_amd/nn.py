@@ -79,7 +79,21 @@ class mx_linear(nn.Module):
         if self.apply_bias and self._mx_bias is not None:
             bias = self._mx_bias.dequantize()
         return ops.linear_wq(x, w._mx_packed, w._mx_scales, w._mx_dtype, self.in_features, self.out_features,
-                             w._mx_block, bias=bias)
+                             w._mx_block, bias=bias, w_scales_t=self._decode_scales(w))
+
+    def _decode_scales(self, w) -> Optional[Tensor]:
+        """Block-major copy of the weight's scales for the int4 decode kernel,
+        made once per weight tensor and rebuilt when the weight's scales are
+        replaced or modified in place."""
+        if not ops.decode_prepack_eligible(w._mx_dtype, w._mx_block, self.in_features, self.out_features):
+            return None
+        sc = w._mx_scales
+        key = (sc.data_ptr(), str(sc.device), sc._version)
+        cached = self.__dict__.get("_scales_t_cache")
+        if cached is None or cached[0] != key:
+            cached = (key, ops.prepack_scales(sc, self.in_features, self.out_features, w._mx_block))
+            self.__dict__["_scales_t_cache"] = cached
+        return cached[1]
 
     @property
     def weight(self):

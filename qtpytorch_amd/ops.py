@@ -218,11 +218,36 @@ def qscale_gemm(a_packed: Tensor, a_scales: Tensor, b_packed: Tensor, b_scales: 
     return out
 
 
+def decode_prepack_eligible(dt, block: int, in_features: int, out_features: int) -> bool:
+    """Whether the int4 decode kernel can use block-major scales for this
+    weight (int4 base codes, block 128, whole 128-column blocks)."""
+    dt = get_mx_dtype(dt)
+    return (not dt.is_float and dt.bits == 4 and not dt.is_hadamard and not dt.is_vector and block == 128
+            and out_features % 128 == 0 and in_features % 32 == 0)
+
+
+def prepack_scales(w_scales: Tensor, in_features: int, out_features: int, block: int = 128) -> Tensor:
+    """Block-major copy [out/128, in] of a quantized [in, out] weight's
+    scales (stored [in, out/128]), the layout the decode kernel reads."""
+    dev = L.require_gpu(w_scales)
+    K, N = in_features, out_features
+    sc = w_scales.contiguous().float()
+    if sc.numel() != K * (N // block):
+        raise L.MXKError(f"prepack_scales: {sc.numel()} scales for a {K}x{N} weight with block {block}")
+    out = torch.empty(N // block, K, dtype=torch.float32, device=dev)
+    with torch.cuda.device(dev):
+        rc = L.lib().mxk_linear_prepack_scales(sc.data_ptr(), K, N, block, out.data_ptr(), L.stream_of(sc))
+    L.check(rc, f"prepack_scales({K}x{N})")
+    return out
+
+
 def linear_wq(x: Tensor, w_packed: Tensor, w_scales: Tensor, dt, in_features: int, out_features: int,
-              block: int = 128, bias: Optional[Tensor] = None) -> Tensor:
+              block: int = 128, bias: Optional[Tensor] = None, w_scales_t: Optional[Tensor] = None) -> Tensor:
     """y = x.float() @ dequant(W) (+ bias) for W stored as quantize(weight.t())
     ([in, out] row-major, mxtorch.py:7447), fused: the weight is never
-    dequantized to memory (mx_linear.forward, mxtorch.py:7454-7473)."""
+    dequantized to memory (mx_linear.forward, mxtorch.py:7454-7473).
+    `w_scales_t` is an optional prepack_scales() copy; without it the int4
+    decode path transposes the scales into its workspace on every call."""
     dt = get_mx_dtype(dt)
     dev = L.require_gpu(x, w_packed, w_scales)
     kind, var = _kind_variant(dt)
@@ -237,6 +262,11 @@ def linear_wq(x: Tensor, w_packed: Tensor, w_scales: Tensor, dt, in_features: in
         xc = xc.float()
     xc = xc.contiguous()
     M = xc.shape[0]
+    if w_scales_t is not None:
+        if (w_scales_t.device != dev or w_scales_t.dtype != torch.float32 or not w_scales_t.is_contiguous()
+                or w_scales_t.numel() != K * (N // block)):
+            raise L.MXKError("linear_wq: w_scales_t must be prepack_scales() of this weight (float32, contiguous, "
+                             "same device)")
     out = torch.empty(M, N, dtype=torch.float32, device=dev)
     b = None if bias is None else bias.to(device=dev, dtype=torch.float32).contiguous()
     lib = L.lib()
@@ -244,8 +274,8 @@ def linear_wq(x: Tensor, w_packed: Tensor, w_scales: Tensor, dt, in_features: in
     ws = _zeroed_workspace(ws_bytes, dev)
     with torch.cuda.device(dev):
         rc = lib.mxk_linear_wq(xc.data_ptr(), L.elem_type(xc.dtype), M, K, w_packed.contiguous().data_ptr(),
-                               w_scales.contiguous().data_ptr(), N, kind, dt.bits, block, L.ptr(b),
-                               out.data_ptr(), L.ptr(ws), ws_bytes, L.stream_of(xc))
+                               w_scales.contiguous().data_ptr(), L.ptr(w_scales_t), N, kind, dt.bits, block,
+                               L.ptr(b), out.data_ptr(), L.ptr(ws), ws_bytes, L.stream_of(xc))
     L.check(rc, f"linear_wq({dt.name}, M={M}, K={K}, N={N})")
     return out.reshape(*lead, N)
 

@@ -31,7 +31,7 @@ def test_library_exports_every_declared_symbol():
     for name in declared:
         assert hasattr(h, name), f"libmxk.so does not export {name}"
         assert name in L.SIGNATURES, f"ctypes binding lacks {name}"
-    assert h.mxk_abi_version() == 1
+    assert h.mxk_abi_version() == 2
 
 
 @pytest.mark.parametrize("bits", [1, 2, 3, 4, 5, 6, 7, 8, 16])
@@ -87,3 +87,9 @@ def test_bad_arguments_return_errors_without_gpu():
     assert rc == -95
     rc = h.mxk_qgemm(8, 8, 1, 8, 8, 1, 4, 4, 4, 16, 128, 0, None, 0, None, 8, None, None, 0, None)
     assert rc == -95
+    rc = h.mxk_linear_prepack_scales(None, 256, 256, 128, 8, None)
+    assert rc == -22 and b"null" in h.mxk_last_error()
+    rc = h.mxk_linear_prepack_scales(8, 256, 200, 128, 8, None)
+    assert rc == -22
+    rc = h.mxk_linear_prepack_scales(8, 256, 256, 64, 8, None)
+    assert rc == -22

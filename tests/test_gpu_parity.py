@@ -272,6 +272,43 @@ def test_linear_decode_config2_shape(qa):
     assert (y - y_ref).abs().max().item() <= LINEAR_RTOL * y_ref.abs().max().item()
 
 
+@pytest.mark.parametrize("shape", [(16, 4096, 1024), (7, 2048, 384)])
+@pytest.mark.parametrize("xdt", [torch.float32, torch.float16, torch.bfloat16])
+def test_linear_decode_scale_layouts(qa, shape, xdt):
+    """The decode kernel with block-major scales from prepack_scales and with
+    the reference-layout scales transposed on the fly: same result, within
+    tolerance of the oracle; the prepacked copy is the exact transpose."""
+    M, K, N = shape
+    W = _randn((N, K), 31 + K, outliers=1e-3, scale=20.0) * 0.02
+    x = _randn((M, K), 33 + M).to(xdt)
+    wp, ws, _ = orc.linear_from_weight(W, "int4d", 128)
+    dt = qa.get_mx_dtype("int4d")
+    wpg, wsg, xg = wp.to(dev()), ws.to(dev()), x.to(dev())
+    st = qa.ops.prepack_scales(wsg, K, N, 128)
+    assert torch.equal(st.cpu(), ws.reshape(K, N // 128).t().contiguous())
+    y_pre = qa.ops.linear_wq(xg, wpg, wsg, dt, K, N, 128, w_scales_t=st).cpu()
+    y_fly = qa.ops.linear_wq(xg, wpg, wsg, dt, K, N, 128).cpu()
+    assert _bits_eq(y_pre, y_fly)
+    y_ref = orc.linear_forward(x, wp, ws, "int4d", K, N, 128)
+    assert (y_pre - y_ref).abs().max().item() <= LINEAR_RTOL * y_ref.abs().max().item()
+
+
+def test_linear_prepacked_scales_follow_weight_updates(qa):
+    """mx_linear rebuilds its block-major scale copy when the weight's scales
+    change in place."""
+    K, N = 1024, 256
+    W = _randn((N, K), 41) * 0.02
+    lin = torch.nn.Linear(K, N, bias=False)
+    with torch.no_grad():
+        lin.weight.copy_(W)
+    m = qa.mx_linear.from_linear(lin.to(dev()), qa.get_mx_dtype("int4d"), 128)
+    x = _randn((4, K), 43).to(dev())
+    y1 = m(x).cpu()
+    m._mx_weight._mx_scales.mul_(2.0)
+    y2 = m(x).cpu()
+    assert (y2 - 2.0 * y1).abs().max().item() <= 1e-5 * y1.abs().max().item()
+
+
 def test_kv_bulk_roundtrip(qa):
     """Config-5 layout at reduced size: fp16 K [B,H,S,D] -> int8dv / int4d per row of D."""
     k = _randn((2, 4, 256, 128), 55).half()
