@@ -69,6 +69,7 @@ __device__ __forceinline__ float group_max(float v) {
 // ---------------------------------------------------------------- element loads
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x4v __attribute__((ext_vector_type(4)));
 template <typename T> struct ElemT;
 template <> struct ElemT<float> {
   static __device__ __forceinline__ float cvt(float v) { return v; }

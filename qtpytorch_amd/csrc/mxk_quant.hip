@@ -107,28 +107,40 @@ __global__ __launch_bounds__(256) void k_quant_fast(const T* __restrict__ x, int
 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int g = lane / LPB, li = lane % LPB;
-  for (int64_t b0 = (int64_t)blockIdx.x * GPB; b0 < nb; b0 += (int64_t)gridDim.x * GPB) {
-    const int64_t blk = b0 + wave * GPW + g;
-    const int64_t idx = blk * B + (int64_t)li * E;
-    float v[E];
-    load_elems<T, E>(x, idx, n, v);
-    float m = 0.0f;
+  // U rounds of GPB blocks per iteration, a grid-stride apart, with all
+  // their loads issued before the first reduction (U = 2 and 4 measured
+  // slower on 2^28 elements than one round)
+  constexpr int U = 1;
+  const int64_t rstride = (int64_t)gridDim.x * GPB;
+  for (int64_t b0 = (int64_t)blockIdx.x * GPB; b0 < nb; b0 += U * rstride) {
+    float v[U][E];
 #pragma unroll
-    for (int i = 0; i < E; ++i) m = fmaxf(m, __builtin_fabsf(v[i]));
-    const float ap = fmaxf(group_max<LPB>(m), MXK_AMIN);
-    const BlockParams bp = block_params<MODE>(ap, qf);
-    uint32_t w[NW];
-#pragma unroll
-    for (int k = 0; k < NW; ++k) w[k] = 0u;
-#pragma unroll
-    for (int i = 0; i < E; ++i) {
-      uint32_t f = (uint32_t)encode<MODE, BITS>(v[i], bp, qf, sP) & MASK;
-      if (idx + i >= n_store) f = 0u;
-      w[(i * BITS) >> 5] |= f << ((i * BITS) & 31);
+    for (int u = 0; u < U; ++u) {
+      const int64_t blk = b0 + u * rstride + wave * GPW + g;
+      load_elems<T, E>(x, blk * B + (int64_t)li * E, n, v[u]);
     }
-    if (blk < nb) {
-      store_bytes<NB>(packed, idx * BITS / 8, packed_nbytes, w);
-      if (li == 0) scales[blk] = bp.s;
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t blk = b0 + u * rstride + wave * GPW + g;
+      const int64_t idx = blk * B + (int64_t)li * E;
+      float m = 0.0f;
+#pragma unroll
+      for (int i = 0; i < E; ++i) m = fmaxf(m, __builtin_fabsf(v[u][i]));
+      const float ap = fmaxf(group_max<LPB>(m), MXK_AMIN);
+      const BlockParams bp = block_params<MODE>(ap, qf);
+      uint32_t w[NW];
+#pragma unroll
+      for (int k = 0; k < NW; ++k) w[k] = 0u;
+#pragma unroll
+      for (int i = 0; i < E; ++i) {
+        uint32_t f = (uint32_t)encode<MODE, BITS>(v[u][i], bp, qf, sP) & MASK;
+        if (idx + i >= n_store) f = 0u;
+        w[(i * BITS) >> 5] |= f << ((i * BITS) & 31);
+      }
+      if (blk < nb) {
+        store_bytes<NB>(packed, idx * BITS / 8, packed_nbytes, w);
+        if (li == 0) scales[blk] = bp.s;
+      }
     }
   }
 }
@@ -445,6 +457,152 @@ __global__ __launch_bounds__(256) void k_dequant(const uint8_t* __restrict__ pac
   }
 }
 
+// Fast dequantize for bits 1/2/4/8 with blocks that are a multiple of 4: a
+// lane decodes slots of 4 consecutive outputs (one 1-4 byte load of its
+// codes, one scale) and writes each slot with one 16-byte store, so each
+// store instruction of a wave covers 1 KiB of contiguous output.  A thread
+// takes U slots a grid-stride apart per iteration, loads first.  Slots that
+// cross the end of the data or of the packed buffer take the element path.
+template <int MODE, int BITS>
+__device__ __forceinline__ float decode_field(uint32_t word, int sh, float s, const float* sG) {
+  if constexpr (MODE == Q_INT1) {
+    return ((word >> sh) & 1u) == 0u ? s : -s;
+  } else if constexpr (MODE == Q_FP) {
+    return sG[(word >> sh) & ((1u << BITS) - 1u)] * s;
+  } else {
+    const int32_t c = (int32_t)(word << (32 - BITS - sh)) >> (32 - BITS);
+    return (float)c * s;
+  }
+}
+
+template <int MODE, int BITS>
+__global__ __launch_bounds__(256) void k_dequant_fast(const uint8_t* __restrict__ packed, int64_t packed_nbytes,
+                                                      const float* __restrict__ scales, int64_t nb, int64_t n,
+                                                      int block, float* __restrict__ out) {
+  constexpr int U = 4;
+  constexpr int H = MODE == Q_FP ? (1 << (BITS - 1)) : 1;
+  __shared__ float sG[2 * H];
+  if constexpr (MODE == Q_FP) build_tables<BITS>(nullptr, sG);
+  const int64_t slots = (n + 3) / 4;
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t s0 = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; s0 < slots; s0 += U * stride) {
+    uint32_t w[U];
+    float sc[U];
+    bool full[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t sl = s0 + u * stride;
+      const int64_t j0 = sl * 4;
+      const int64_t last_byte = (j0 + 3) * BITS / 8;  // last byte holding this slot's codes
+      full[u] = sl < slots && j0 + 4 <= n && last_byte < packed_nbytes;
+      w[u] = 0u;
+      if (full[u]) {
+        if constexpr (BITS == 8) w[u] = *reinterpret_cast<const uint32_t*>(packed + j0);
+        else if constexpr (BITS == 4) w[u] = *reinterpret_cast<const uint16_t*>(packed + j0 / 2);
+        else if constexpr (BITS == 2) w[u] = packed[j0 / 4];
+        else w[u] = (uint32_t)packed[j0 / 8] >> (j0 & 4);
+      }
+      const int64_t b = j0 / block;
+      sc[u] = (sl < slots && b < nb) ? scales[b] : 0.0f;
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t sl = s0 + u * stride;
+      if (sl >= slots) break;
+      const int64_t j0 = sl * 4;
+      if (full[u]) {
+        f32x4v v;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) v[i] = decode_field<MODE, BITS>(w[u], i * BITS, sc[u], sG);
+        __builtin_nontemporal_store(v, reinterpret_cast<f32x4v*>(out + j0));
+      } else {
+        for (int i = 0; i < 4; ++i) {
+          const int64_t j = j0 + i;
+          if (j >= n) break;
+          const int64_t unit = j / (8 / BITS);
+          const uint32_t f = unit < packed_nbytes ? (uint32_t)packed[unit] : 0u;
+          const float sj = (j / block) < nb ? scales[j / block] : 0.0f;
+          out[j] = decode_field<MODE, BITS>(f, (int)(j % (8 / BITS)) * BITS, sj, sG);
+        }
+      }
+    }
+  }
+}
+
+// Fused dequantize + inverse rotation for 'h' dtypes with rows of 128 =
+// blocks of 128 (unrotate, mxtorch.py:2891-2904, over the rows quantize
+// rotated): out = (WHT(RN(code*s)) / fl32(sqrt 128)) * signs.  Same lane
+// layout and butterfly schedule as k_quant_had128.
+template <int MODE, int BITS>
+__global__ __launch_bounds__(256) void k_dequant_had128(const uint8_t* __restrict__ packed, int64_t packed_nbytes,
+                                                        const float* __restrict__ scales, int64_t nb,
+                                                        const float* __restrict__ signs, float* __restrict__ out) {
+  constexpr int E = 16, LPB = 8, GPW = 8, GPB = 32;
+  constexpr int LB = E * BITS / 8;
+  constexpr int NWD = (LB + 3) / 4;
+  constexpr int H = MODE == Q_FP ? (1 << (BITS - 1)) : 1;
+  __shared__ float sG[2 * H];
+  __shared__ __attribute__((aligned(16))) float srow[GPB * MXK_ROWPAD];
+  if constexpr (MODE == Q_FP) build_tables<BITS>(nullptr, sG);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int g = lane / LPB, li = lane % LPB;
+  float* row = srow + (wave * GPW + g) * MXK_ROWPAD;
+  float sg[E];
+#pragma unroll
+  for (int i = 0; i < E; ++i) sg[i] = signs[li * 16 + i];
+  const float rdiv = 11.3137083f;  // fl32(sqrt(128))
+  const float rinv = 1.0f / 11.3137083f;
+  // every workgroup runs the same number of iterations (the FWHT uses
+  // workgroup barriers); groups past the last row compute on zeros
+  const int64_t iters = (nb + (int64_t)gridDim.x * GPB - 1) / ((int64_t)gridDim.x * GPB);
+  for (int64_t it = 0; it < iters; ++it) {
+    const int64_t blk = (it * gridDim.x + blockIdx.x) * GPB + wave * GPW + g;
+    const int64_t u0 = blk * (128 * BITS / 8) + (int64_t)li * LB;
+    const bool live = blk < nb;
+    uint32_t w[NWD];
+#pragma unroll
+    for (int k = 0; k < NWD; ++k) w[k] = 0u;
+    if (live && u0 + LB <= packed_nbytes) {
+      if constexpr (LB == 16) {
+        const u32x4 t = *reinterpret_cast<const u32x4*>(packed + u0);
+        w[0] = t[0]; w[1] = t[1]; w[2] = t[2]; w[3] = t[3];
+      } else if constexpr (LB == 8) {
+        const u32x2 t = *reinterpret_cast<const u32x2*>(packed + u0);
+        w[0] = t[0]; w[1] = t[1];
+      } else if constexpr (LB == 4) {
+        w[0] = *reinterpret_cast<const uint32_t*>(packed + u0);
+      } else {
+        w[0] = *reinterpret_cast<const uint16_t*>(packed + u0);
+      }
+    } else if (live) {
+      for (int k = 0; k < LB; ++k)
+        if (u0 + k < packed_nbytes) w[k >> 2] |= (uint32_t)packed[u0 + k] << ((k & 3) * 8);
+    }
+    const float s = live ? scales[blk] : 0.0f;
+    float v[E];
+#pragma unroll
+    for (int i = 0; i < E; ++i) v[i] = decode_field<MODE, BITS>(w[(i * BITS) >> 5], (i * BITS) & 31, s, sG);
+    fwht128_group(v, row, li);
+#pragma unroll
+    for (int i = 0; i < E; ++i) v[i] = div_rn(v[i], rdiv, rinv) * sg[i];
+    // through the row's LDS once more, so that store q of the 8 lanes covers
+    // positions 32q .. 32q+31: one whole 128-byte line per store
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      *reinterpret_cast<f32x4v*>(row + li * 16 + 4 * q) = f32x4v{v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]};
+    __syncthreads();
+    f32x4v o[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) o[q] = *reinterpret_cast<const f32x4v*>(row + 32 * q + 4 * li);
+    __syncthreads();
+    if (live) {
+      float* dst = out + blk * 128 + 4 * li;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) __builtin_nontemporal_store(o[q], reinterpret_cast<f32x4v*>(dst + 32 * q));
+    }
+  }
+}
+
 // ---------------------------------------------------------------- host dispatch
 static int grid_for(int64_t work_items, int per_block) {
   int64_t blocks = ceil_div(work_items, per_block);
@@ -616,9 +774,28 @@ static size_t rot_ws_bytes(int64_t n, int64_t d) {
 template <int MODE, int BITS>
 static int launch_dequant(const void* packed, int64_t pbytes, const float* scales, int64_t nb, int64_t n, int block,
                           float* out, hipStream_t st) {
+  if constexpr (BITS == 1 || BITS == 2 || BITS == 4 || BITS == 8) {
+    if (block % 4 == 0 && (reinterpret_cast<uintptr_t>(packed) & 3u) == 0 &&
+        (reinterpret_cast<uintptr_t>(out) & 15u) == 0) {
+      const int64_t slots = ceil_div(n, 4);
+      const int grid = (int)std::max<int64_t>(1, std::min<int64_t>(ceil_div(slots, 256 * 4), (int64_t)num_cus() * 8));
+      hipLaunchKernelGGL((k_dequant_fast<MODE, BITS>), dim3(grid), dim3(256), 0, st,
+                         reinterpret_cast<const uint8_t*>(packed), pbytes, scales, nb, n, block, out);
+      return check_launch("dequantize");
+    }
+  }
   hipLaunchKernelGGL((k_dequant<MODE, BITS>), dim3(grid_for(ceil_div(n, 4), 256)), dim3(256), 0, st,
                      reinterpret_cast<const uint8_t*>(packed), pbytes, scales, nb, n, block, out);
   return check_launch("dequantize");
+}
+
+template <int MODE, int BITS>
+static int launch_dequant_had128(const void* packed, int64_t pbytes, const float* scales, int64_t nb,
+                                 const float* signs, float* out, hipStream_t st) {
+  const int grid = (int)std::max<int64_t>(1, std::min<int64_t>(ceil_div(nb, 32), (int64_t)num_cus() * 8));
+  hipLaunchKernelGGL((k_dequant_had128<MODE, BITS>), dim3(grid), dim3(256), 0, st,
+                     reinterpret_cast<const uint8_t*>(packed), pbytes, scales, nb, signs, out);
+  return check_launch("dequantize(hadamard128)");
 }
 
 int requant_vec_f32(const float* x, int64_t n, int bits, int block, void* packed, int64_t packed_nbytes,
@@ -741,6 +918,18 @@ int mxk_dequantize(const void* packed, int64_t packed_nbytes, const float* scale
   if (n <= 0 || block <= 0 || nb <= 0) return fail(MXK_EINVAL, "dequantize: sizes must be positive");
   if (!packed || !scales || !out) return fail(MXK_EINVAL, "dequantize: null pointer");
   const int mode = mode_for(kind, bits, variant == MXK_VAR_VECTOR ? MXK_VAR_BASE : variant);
+  if (variant == MXK_VAR_HADAMARD && rot_dim == 128 && block == 128 && n % 128 == 0 && nb == n / 128 && signs &&
+      (reinterpret_cast<uintptr_t>(out) & 15u) == 0 && (reinterpret_cast<uintptr_t>(packed) & 15u) == 0) {
+#define MXK_DH(MODE, BITS) \
+    if (mode == MODE && bits == BITS) return launch_dequant_had128<MODE, BITS>(packed, packed_nbytes, scales, nb, signs, out, st);
+    MXK_DH(Q_INT1, 1)
+    MXK_DH(Q_INT, 2)
+    MXK_DH(Q_INT, 4)
+    MXK_DH(Q_INT, 8)
+    MXK_DH(Q_FP, 4)
+    MXK_DH(Q_FP, 8)
+#undef MXK_DH
+  }
   int rc = MXK_EUNSUPPORTED;
 #define MXK_D(MODE, BITS) \
   else if (mode == MODE && bits == BITS) rc = launch_dequant<MODE, BITS>(packed, packed_nbytes, scales, nb, n, block, out, st);

@@ -194,6 +194,21 @@ def test_hadamard_large_rotation(qa):
     assert _bits_eq(dq, orc.dequant(rp, rs, "int4dh", n, 128, seed=7))
 
 
+@pytest.mark.parametrize("dtype", ["int4dh", "int8dh", "int2dh", "int1dh", "float4dh", "float8dh"])
+def test_hadamard_rows128_dequant(qa, dtype):
+    """Rows of 128 = blocks of 128: the fused dequantize + inverse rotation
+    kernel, bit-exact against the oracle's row-wise unrotation, with a row
+    count that leaves the last workgroup partly idle."""
+    x = _randn((1000, 128), 61, outliers=1e-3)
+    dt = qa.get_mx_dtype(dtype)
+    packed, scales, n = qa.ops.quantize(x.to(dev()), dt, 128, seed=4242)
+    rp, rs, rn = orc.quantize(x, dtype, 128, seed=4242)
+    assert _bits_eq(packed, rp) and _bits_eq(scales, rs)
+    dq = qa.ops._dequant(packed, scales, dt, n, 128, orig_shape=(1000, 128), seed=4242, hadamard_mode="rows")
+    rdq = orc.dequant(rp, rs, dtype, rn, 128, seed=4242, orig_shape=(1000, 128), hadamard_mode="rows")
+    assert _bits_eq(dq, rdq)
+
+
 GEMM_SHAPES = [(512, 512, 512), (256, 384, 200), (100, 256, 130), (33, 128, 17), (8, 640, 1024)]
 
 
