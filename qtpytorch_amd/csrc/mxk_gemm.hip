@@ -59,6 +59,37 @@ __global__ __launch_bounds__(256) void k_unpack_rows(const uint8_t* __restrict__
   }
 }
 
+// int8 B [K][N] (row-major, N % 16 == 0) to k-contiguous rows
+// B8[n][k] (n < Npad, k < KBP) when the padded block equals the block
+// (block % 64 == 0): a 64x64 byte tile per workgroup through LDS, 16-byte
+// loads along n and 16-byte stores along k; zeros past K and past N.
+__global__ __launch_bounds__(256) void k_transpose_b8(const int8_t* __restrict__ B, int64_t K, int64_t N,
+                                                      int64_t Npad, int64_t KBP, int8_t* __restrict__ B8) {
+  __shared__ uint8_t tile[64][64 + 4];
+  const int t = threadIdx.x;
+  const int64_t n0 = (int64_t)blockIdx.x * 64, k0 = (int64_t)blockIdx.y * 64;
+  {
+    const int kr = t >> 2, nc = (t & 3) * 16;
+    const int64_t k = k0 + kr, n = n0 + nc;
+    u32x4 v = u32x4{0u, 0u, 0u, 0u};
+    if (k < K && n < N) v = *reinterpret_cast<const u32x4*>(B + k * N + n);
+    const uint8_t* vb = reinterpret_cast<const uint8_t*>(&v);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) tile[kr][nc + i] = vb[i];
+  }
+  __syncthreads();
+  {
+    const int nr = t >> 2, kc = (t & 3) * 16;
+    const int64_t n = n0 + nr, k = k0 + kc;
+    if (n < Npad && k < KBP) {
+      uint32_t w[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+      for (int i = 0; i < 16; ++i) w[i >> 2] |= (uint32_t)tile[kc + i][nr] << ((i & 3) * 8);
+      *reinterpret_cast<u32x4*>(B8 + n * KBP + k) = u32x4{w[0], w[1], w[2], w[3]};
+    }
+  }
+}
+
 #define QG_BM 128
 #define QG_BN 128
 #define QG_LDS_STRIDE 80  // 64 bytes of K + 16 bytes of skew per row
@@ -151,11 +182,439 @@ __global__ __launch_bounds__(256) void k_qgemm_i8(const int8_t* __restrict__ A8,
   }
 }
 
+// v2 for blocks of 65..128 (one 128-byte padded K block, BP = 128): the
+// same 128x128 tile and MFMA layout, one K block per pipeline stage, two
+// LDS buffers.  The next stage's A/B tiles go straight from global memory to
+// LDS (global_load_lds_dwordx4: lane L of a wave instruction fills bytes
+// 16L..16L+15 of a 1 KiB window) while the MFMAs and the fp32 epilogue of
+// the current stage run; one barrier per K block.  Rows are 128 bytes with
+// no padding; the 16-byte chunk c of row r sits in slot c ^ ((r >> 1) & 7),
+// which makes the 16-row fragment reads of a wave bank-conflict free.  SA
+// comes pre-transposed ([KB][M]), SB is a row of b_scales; both go through
+// registers into LDS.
+__device__ __forceinline__ int qg2_slot(int r, int c) { return c ^ ((r >> 1) & 7); }
+
+template <bool WRITE_ACC, bool WRITE_C>
+__global__ __launch_bounds__(256, 2) void k_qgemm_i8_v2(const int8_t* __restrict__ A8, int64_t lda, int64_t Arows,
+                                                        const int8_t* __restrict__ B8, int64_t ldb, int64_t Brows,
+                                                        const float* __restrict__ sa_t, int a_ok,
+                                                        const float* __restrict__ b_scales, int b_ok, int64_t M,
+                                                        int64_t N, int KB, float* __restrict__ C,
+                                                        int32_t* __restrict__ acc_out, int grouped) {
+  __shared__ __attribute__((aligned(1024))) int8_t sA[2][QG_BM * 128];
+  __shared__ __attribute__((aligned(1024))) int8_t sB[2][QG_BN * 128];
+  __shared__ __attribute__((aligned(16))) float sSA[2][QG_BM];
+  __shared__ __attribute__((aligned(16))) float sSB[2][QG_BN];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave >> 1, wn = wave & 1;
+  // tile order: with `grouped`, the workgroups on one XCD (b % 8) take 8x8
+  // blocks of tiles in turn, so that the 64 tiles an XCD runs at once share
+  // 8 A row panels and 8 B column panels in its L2; otherwise row-major
+  // (the host enables it only when the tile counts are multiples of 8 and
+  // the tile total a multiple of 512, so that every XCD owns whole blocks)
+  int tm, tn;
+  {
+    const int b = (int)blockIdx.x;
+    const int tiles_n = (int)((N + QG_BN - 1) / QG_BN);
+    if (grouped) {
+      const int xcd = b & 7, local = b >> 3;
+      const int gidx = (local >> 6) * 8 + xcd, within = local & 63;
+      const int groups_n = tiles_n >> 3;
+      tm = (gidx / groups_n) * 8 + (within >> 3);
+      tn = (gidx % groups_n) * 8 + (within & 7);
+    } else {
+      tm = b / tiles_n;
+      tn = b % tiles_n;
+    }
+  }
+  const int64_t m0 = (int64_t)tm * QG_BM, n0 = (int64_t)tn * QG_BN;
+  const int lr = lane & 15, lg = lane >> 4;
+
+  // wave w fills rows 32w .. 32w+31 of each tile, 8 rows per instruction:
+  // lane L -> row 32w + 8q + (L >> 3), slot L & 7, holding chunk slot ^ ((row >> 1) & 7)
+  const int8_t* ga[4];
+  const int8_t* gb[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int r = 32 * wave + 8 * q + (lane >> 3);
+    const int cch = qg2_slot(r, lane & 7);
+    ga[q] = A8 + std::min<int64_t>(m0 + r, Arows - 1) * lda + cch * 16;
+    gb[q] = B8 + std::min<int64_t>(n0 + r, Brows - 1) * ldb + cch * 16;
+  }
+  auto load_tiles = [&](int kb, int buf) {
+    const int64_t k0 = (int64_t)kb * 128;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)(ga[q] + k0),
+                                       (__attribute__((address_space(3))) void*)(&sA[buf][(32 * wave + 8 * q) * 128]),
+                                       16, 0, 0);
+      __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)(gb[q] + k0),
+                                       (__attribute__((address_space(3))) void*)(&sB[buf][(32 * wave + 8 * q) * 128]),
+                                       16, 0, 0);
+    }
+  };
+  auto load_scale = [&](int kb) -> float {
+    if (tid < 128) {
+      const int64_t row = m0 + tid;
+      return (a_ok && row < M) ? sa_t[(int64_t)kb * M + row] : 1.0f;
+    }
+    const int64_t col = n0 + tid - 128;
+    return (b_ok && col < N) ? b_scales[(int64_t)kb * N + col] : 1.0f;
+  };
+  auto store_scale = [&](int buf, float v) {
+    if (tid < 128) sSA[buf][tid] = v;
+    else sSB[buf][tid - 128] = v;
+  };
+
+  float c[4][4][4];
+#pragma unroll
+  for (int a = 0; a < 4; ++a)
+#pragma unroll
+    for (int b = 0; b < 4; ++b)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) c[a][b][i] = 0.0f;
+
+  load_tiles(0, 0);
+  store_scale(0, load_scale(0));
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  for (int kb = 0; kb < KB; ++kb) {
+    const int cur = kb & 1;
+    float rs = 1.0f;
+    if (kb + 1 < KB) {
+      load_tiles(kb + 1, cur ^ 1);
+      rs = load_scale(kb + 1);
+    }
+    i32x4 p[4][4];
+#pragma unroll
+    for (int a = 0; a < 4; ++a)
+#pragma unroll
+      for (int b = 0; b < 4; ++b) p[a][b] = i32x4{0, 0, 0, 0};
+#pragma unroll
+    for (int sub = 0; sub < 2; ++sub) {
+      i32x4 bf[4];
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const int r = wn * 64 + t * 16 + lr;
+        bf[t] = *reinterpret_cast<const i32x4*>(&sB[cur][r * 128 + qg2_slot(r, sub * 4 + lg) * 16]);
+      }
+#pragma unroll
+      for (int a = 0; a < 4; ++a) {
+        const int r = wm * 64 + a * 16 + lr;
+        const i32x4 af = *reinterpret_cast<const i32x4*>(&sA[cur][r * 128 + qg2_slot(r, sub * 4 + lg) * 16]);
+#pragma unroll
+        for (int b = 0; b < 4; ++b) p[a][b] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af, bf[b], p[a][b], 0, 0, 0);
+      }
+    }
+    // epilogue of this K block: C = RN(C + RN(RN(P*SA)*SB))
+    float sb[4];
+#pragma unroll
+    for (int b = 0; b < 4; ++b) sb[b] = sSB[cur][wn * 64 + b * 16 + lr];
+#pragma unroll
+    for (int a = 0; a < 4; ++a) {
+      const f32x4v sa4 = *reinterpret_cast<const f32x4v*>(&sSA[cur][wm * 64 + a * 16 + lg * 4]);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+          const float t = ((float)p[a][b][i] * sa4[i]) * sb[b];
+          c[a][b][i] = c[a][b][i] + t;
+          if (WRITE_ACC) {
+            const int64_t row = m0 + wm * 64 + a * 16 + lg * 4 + i;
+            const int64_t col = n0 + wn * 64 + b * 16 + lr;
+            if (row < M && col < N) acc_out[((int64_t)kb * M + row) * N + col] = p[a][b][i];
+          }
+        }
+      }
+    }
+    if (kb + 1 < KB) store_scale(cur ^ 1, rs);
+    __builtin_amdgcn_s_waitcnt(0);  // this thread's tile loads have landed in LDS
+    __syncthreads();
+  }
+  if (WRITE_C) {
+#pragma unroll
+    for (int a = 0; a < 4; ++a)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int64_t row = m0 + wm * 64 + a * 16 + lg * 4 + i;
+        if (row >= M) continue;
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+          const int64_t col = n0 + wn * 64 + b * 16 + lr;
+          if (col < N) C[row * N + col] = c[a][b][i];
+        }
+      }
+  }
+}
+
+// v3 for large problems, blocks of 65..128: 512 threads (8 waves, 2 per
+// SIMD) on a 256x128 tile, each wave 64x64 as in v2; three LDS stages of one
+// K block each (A 32 KiB + B 16 KiB + scales), filled two stages ahead with
+// global_load_lds (tiles, 16 B per lane; scales, 4 B per lane).  Every
+// thread issues the same 7 loads per stage, so one vmcnt value waits for a
+// stage; one barrier per K block, placed before the loads that refill the
+// stage every wave has just finished.  sa_t is [KB][M] and sb_src [KB][N]
+// (both all ones when the reference would use ones).
+#define QG3_BM 256
+#define QG3_BN 128
+#define QG3_NS 3
+
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 0xF) | 0x0F70 | ((N >> 4) << 14));
+}
+
+// Barrier without a memory fence: the LDS data a stage reads arrives by
+// global_load_lds, whose completion each thread waits for with vmcnt
+// before the barrier; a fence here would make the compiler wait for every
+// load in flight, including the stages still being prefetched.
+__device__ __forceinline__ void qg3_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+// Fragment reads of the current stage as inline-asm ds_read_b128, each
+// followed (before first use) by an lgkmcnt wait tied to its result.  The
+// compiler does not see these as LDS reads, so it does not add vmcnt waits
+// for the global_load_lds traffic still filling the other stages (it cannot
+// prove that a runtime-indexed stage differs from those); every LDS op
+// completes in order, so its own lgkmcnt bookkeeping stays valid.
+__device__ __forceinline__ i32x4 qg3_ds_read(uint32_t lds_byte_addr) {
+  i32x4 v;
+  asm volatile("ds_read_b128 %0, %1" : "=v"(v) : "v"(lds_byte_addr) : "memory");
+  return v;
+}
+template <int N>
+__device__ __forceinline__ void qg3_lgkm_wait(i32x4& v) {
+  asm volatile("s_waitcnt lgkmcnt(%1)" : "+v"(v) : "n"(N));
+}
+__device__ __forceinline__ float qg3_ds_read_f32(uint32_t lds_byte_addr) {
+  float v;
+  asm volatile("ds_read_b32 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(v) : "v"(lds_byte_addr) : "memory");
+  return v;
+}
+
+template <bool WRITE_ACC, bool WRITE_C>
+__global__ __launch_bounds__(512, 1) void k_qgemm_i8_v3(const int8_t* __restrict__ A8, int64_t lda, int64_t Arows,
+                                                        const int8_t* __restrict__ B8, int64_t ldb, int64_t Brows,
+                                                        const float* __restrict__ sa_t,
+                                                        const float* __restrict__ sb_src, int64_t M, int64_t N,
+                                                        int KB, float* __restrict__ C, int32_t* __restrict__ acc_out,
+                                                        int grouped) {
+  __shared__ __attribute__((aligned(1024))) int8_t sA[QG3_NS][QG3_BM * 128];
+  __shared__ __attribute__((aligned(1024))) int8_t sB[QG3_NS][QG3_BN * 128];
+  __shared__ __attribute__((aligned(1024))) float sS[QG3_NS][512];  // SA 0..255, SB 256..383
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave >> 1, wn = wave & 1;
+  int tm, tn;
+  {
+    const int b = (int)blockIdx.x;
+    const int tiles_n = (int)((N + QG3_BN - 1) / QG3_BN);
+    if (grouped) {
+      const int xcd = b & 7, local = b >> 3;
+      const int gidx = (local >> 6) * 8 + xcd, within = local & 63;
+      const int groups_n = tiles_n >> 3;
+      tm = (gidx / groups_n) * 8 + (within >> 3);
+      tn = (gidx % groups_n) * 8 + (within & 7);
+    } else {
+      tm = b / tiles_n;
+      tn = b % tiles_n;
+    }
+  }
+  const int64_t m0 = (int64_t)tm * QG3_BM, n0 = (int64_t)tn * QG3_BN;
+  const int lr = lane & 15, lg = lane >> 4;
+
+  // 32-bit per-lane byte offsets (the host keeps A8, B8 and the scale
+  // arrays below 2^31 bytes); the K block goes into the uniform base.
+  // A rows 32w + 8q + (L >> 3), B rows 16w + 8q + (L >> 3), chunk =
+  // slot ^ ((row >> 1) & 7) as in v2; scale float 64w + L.
+  uint32_t oa[4], ob[2];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int r = 32 * wave + 8 * q + (lane >> 3);
+    oa[q] = (uint32_t)(std::min<int64_t>(m0 + r, Arows - 1) * lda + qg2_slot(r, lane & 7) * 16);
+  }
+#pragma unroll
+  for (int q = 0; q < 2; ++q) {
+    const int r = 16 * wave + 8 * q + (lane >> 3);
+    ob[q] = (uint32_t)(std::min<int64_t>(n0 + r, Brows - 1) * ldb + qg2_slot(r, lane & 7) * 16);
+  }
+  const int f = 64 * wave + lane;
+  // waves 0-3: SA rows, 4-5: SB columns, 6-7: a harmless load of SA row 0
+  const bool is_b = wave == 4 || wave == 5;
+  const char* gsb = reinterpret_cast<const char*>(is_b ? sb_src : sa_t);
+  const int64_t gstride = is_b ? N : M;
+  const uint32_t os = (uint32_t)(4 * (f < 256 ? std::min<int64_t>(m0 + f, M - 1)
+                                              : (f < 384 ? std::min<int64_t>(n0 + f - 256, N - 1) : 0)));
+  auto load_stage = [&](int kb, int buf) {
+    const char* a0 = reinterpret_cast<const char*>(A8) + (int64_t)kb * 128;
+    const char* b0 = reinterpret_cast<const char*>(B8) + (int64_t)kb * 128;
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)(a0 + oa[q]),
+                                       (__attribute__((address_space(3))) void*)(&sA[buf][(32 * wave + 8 * q) * 128]),
+                                       16, 0, 0);
+#pragma unroll
+    for (int q = 0; q < 2; ++q)
+      __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)(b0 + ob[q]),
+                                       (__attribute__((address_space(3))) void*)(&sB[buf][(16 * wave + 8 * q) * 128]),
+                                       16, 0, 0);
+    const char* s0 = gsb + (int64_t)kb * gstride * 4;
+    __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)(s0 + os),
+                                     (__attribute__((address_space(3))) void*)(&sS[buf][64 * wave]), 4, 0, 0);
+  };
+
+  // LDS byte addresses of this lane's fragments in stage 0: row r = base +
+  // 16a + lr keeps (r >> 1) & 7 = (lr >> 1) & 7 for every slice a, so slice
+  // a adds a * 2048; stage s adds s * the stage size
+  const int sw = (lr >> 1) & 7;
+  const uint32_t ldsA = (uint32_t)(uintptr_t)(&sA[0][0]), ldsB = (uint32_t)(uintptr_t)(&sB[0][0]);
+  const uint32_t offA0 = ldsA + (wm * 64 + lr) * 128 + ((lg ^ sw) * 16);
+  const uint32_t offA1 = ldsA + (wm * 64 + lr) * 128 + (((4 + lg) ^ sw) * 16);
+  const uint32_t offB0 = ldsB + (wn * 64 + lr) * 128 + ((lg ^ sw) * 16);
+  const uint32_t offB1 = ldsB + (wn * 64 + lr) * 128 + (((4 + lg) ^ sw) * 16);
+
+  float c[4][4][4];
+#pragma unroll
+  for (int a = 0; a < 4; ++a)
+#pragma unroll
+    for (int b = 0; b < 4; ++b)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) c[a][b][i] = 0.0f;
+
+  load_stage(0, 0);
+  if (KB > 1) load_stage(1, 1);
+  int cur = 0;
+  for (int kb = 0; kb < KB; ++kb) {
+    // stage kb has landed once at most the next stage's 7 loads are pending
+    if (kb + 1 < KB) wait_vmcnt<7>();
+    else wait_vmcnt<0>();
+    qg3_barrier();  // stage kb visible; every wave is done with stage kb-1
+    if (kb + 2 < KB) load_stage(kb + 2, cur == 0 ? 2 : cur - 1);
+    const uint32_t sa_off = (uint32_t)cur * (QG3_BM * 128), sb_off = (uint32_t)cur * (QG3_BN * 128);
+    const uint32_t cS = (uint32_t)(uintptr_t)(&sS[0][0]) + (uint32_t)cur * 2048u;
+    // LDS reads are issued ahead and waited for with partial lgkmcnt counts
+    // (LDS ops complete in order): A slice 0, all B fragments, A slice 1,
+    // then each slice's MFMAs prefetch the slice after next.  The four
+    // 16-row slices are software-pipelined: the MFMAs of slice a+1 are issued
+    // before the fp32 epilogue of slice a, C = RN(C + RN(RN(P*SA)*SB)).
+    i32x4 af[4][2], bf[2][4];
+    af[0][0] = qg3_ds_read(offA0 + sa_off);
+    af[0][1] = qg3_ds_read(offA1 + sa_off);
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      bf[0][t] = qg3_ds_read(offB0 + sb_off + t * 2048);
+      bf[1][t] = qg3_ds_read(offB1 + sb_off + t * 2048);
+    }
+    af[1][0] = qg3_ds_read(offA0 + sa_off + 2048);
+    af[1][1] = qg3_ds_read(offA1 + sa_off + 2048);
+    // A slice 0 and B are the first 10 of 12 reads in flight
+    qg3_lgkm_wait<2>(af[0][0]);
+    qg3_lgkm_wait<2>(af[0][1]);
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      qg3_lgkm_wait<2>(bf[0][t]);
+      qg3_lgkm_wait<2>(bf[1][t]);
+    }
+    float sb[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) sb[t] = qg3_ds_read_f32(cS + 4u * (256 + wn * 64 + t * 16 + lr));
+    // (each scale read waits for lgkmcnt(0), which also lands A slice 1)
+    auto slice_mfma = [&](int a, i32x4 (&p)[4]) {
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        p[t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af[a][0], bf[0][t], i32x4{0, 0, 0, 0}, 0, 0, 0);
+        p[t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af[a][1], bf[1][t], p[t], 0, 0, 0);
+      }
+    };
+    auto load_slice = [&](int a) {
+      af[a][0] = qg3_ds_read(offA0 + sa_off + a * 2048);
+      af[a][1] = qg3_ds_read(offA1 + sa_off + a * 2048);
+    };
+    auto slice_epilogue = [&](int a, const i32x4 (&p)[4]) {
+      i32x4 sa4 = qg3_ds_read(cS + 4u * (wm * 64 + a * 16 + lg * 4));
+      qg3_lgkm_wait<0>(sa4);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          const float v = ((float)p[t][i] * __int_as_float(sa4[i])) * sb[t];
+          c[a][t][i] = c[a][t][i] + v;
+          if (WRITE_ACC) {
+            const int64_t row = m0 + wm * 64 + a * 16 + lg * 4 + i;
+            const int64_t col = n0 + wn * 64 + t * 16 + lr;
+            if (row < M && col < N) acc_out[((int64_t)kb * M + row) * N + col] = p[t][i];
+          }
+        }
+      }
+    };
+    i32x4 p0[4], p1[4];
+    slice_mfma(0, p0);
+    load_slice(2);
+    __builtin_amdgcn_sched_barrier(0);
+    slice_mfma(1, p1);
+    __builtin_amdgcn_sched_barrier(0);
+    slice_epilogue(0, p0);  // its lgkmcnt(0) also lands A slice 2
+    __builtin_amdgcn_sched_barrier(0);
+    slice_mfma(2, p0);
+    load_slice(3);
+    __builtin_amdgcn_sched_barrier(0);
+    slice_epilogue(1, p1);  // lands A slice 3
+    __builtin_amdgcn_sched_barrier(0);
+    slice_mfma(3, p1);
+    __builtin_amdgcn_sched_barrier(0);
+    slice_epilogue(2, p0);
+    __builtin_amdgcn_sched_barrier(0);
+    slice_epilogue(3, p1);
+    cur = cur == 2 ? 0 : cur + 1;
+  }
+  if (WRITE_C) {
+#pragma unroll
+    for (int a = 0; a < 4; ++a)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int64_t row = m0 + wm * 64 + a * 16 + lg * 4 + i;
+        if (row >= M) continue;
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+          const int64_t col = n0 + wn * 64 + b * 16 + lr;
+          if (col < N) C[row * N + col] = c[a][b][i];
+        }
+      }
+  }
+}
+
+__global__ __launch_bounds__(256) void k_fill_ones(float* __restrict__ p, int64_t n) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
+    p[i] = 1.0f;
+}
+
+// sa_t[kb][m] = a_scales[m * KB + kb]: A's scales in K-block-major order
+__global__ __launch_bounds__(256) void k_transpose_sa(const float* __restrict__ s, int64_t M, int64_t KB,
+                                                      float* __restrict__ t) {
+  __shared__ float tile[32][33];
+  const int64_t k0 = (int64_t)blockIdx.x * 32, m0 = (int64_t)blockIdx.y * 32;
+  const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;
+  for (int i = ty; i < 32; i += 8) {
+    const int64_t m = m0 + i, k = k0 + tx;
+    tile[i][tx] = (m < M && k < KB) ? s[m * KB + k] : 0.0f;
+  }
+  __syncthreads();
+  for (int i = ty; i < 32; i += 8) {
+    const int64_t k = k0 + i, m = m0 + tx;
+    if (k < KB && m < M) t[k * M + m] = tile[tx][i];
+  }
+}
+
 struct GemmPlan {
   int KB, BP;
   int64_t KBP, Mpad, Npad;
-  bool direct_a;
-  size_t a_bytes, b_bytes, c_bytes, q_bytes;
+  bool direct_a, v2, v3;
+  size_t a_bytes, b_bytes, c_bytes, q_bytes, sa_bytes, sb_bytes;
 };
 
 static GemmPlan plan_gemm(int64_t M, int64_t K, int64_t N, int bits, int block, int out_bits) {
@@ -171,6 +630,10 @@ static GemmPlan plan_gemm(int64_t M, int64_t K, int64_t N, int bits, int block, 
   p.b_bytes = up((size_t)p.Npad * (size_t)p.KBP);
   p.c_bytes = out_bits > 0 ? up((size_t)M * (size_t)N * sizeof(float)) : 0;
   p.q_bytes = out_bits > 0 ? up((size_t)ceil_div(M * N, block) * sizeof(float2)) : 0;
+  p.v2 = p.BP == 128 && p.KB < 65536;
+  p.v3 = p.v2 && ceil_div(M, QG3_BM) * ceil_div(N, QG3_BN) >= num_cus();
+  p.sa_bytes = p.v2 ? up((size_t)p.KB * (size_t)M * sizeof(float)) : 0;
+  p.sb_bytes = p.v3 ? up((size_t)p.KB * (size_t)N * sizeof(float)) : 0;  // ones, when B's scales do not fit
   return p;
 }
 
@@ -183,7 +646,7 @@ extern "C" {
 size_t mxk_qgemm_workspace(int64_t M, int64_t K, int64_t N, int bits, int block, int out_bits) {
   if (M <= 0 || K <= 0 || N <= 0 || block <= 0) return 0;
   GemmPlan p = plan_gemm(M, K, N, bits, block, out_bits);
-  return p.a_bytes + p.b_bytes + p.c_bytes + p.q_bytes + 1024;
+  return p.a_bytes + p.b_bytes + p.c_bytes + p.q_bytes + p.sa_bytes + p.sb_bytes + 1024;
 }
 
 int mxk_qgemm(const void* a_packed, const float* a_scales, int64_t a_nscales, const void* b_packed,
@@ -201,13 +664,16 @@ int mxk_qgemm(const void* a_packed, const float* a_scales, int64_t a_nscales, co
   if (out_bits > 0 && c_packed_nbytes < mxk_packed_nbytes(out_bits, M * N))
     return fail(MXK_EINVAL, "qgemm: packed output too small");
   GemmPlan p = plan_gemm(M, K, N, bits, block, out_bits);
-  const size_t need = p.a_bytes + p.b_bytes + p.c_bytes + p.q_bytes;
+  const size_t need = p.a_bytes + p.b_bytes + p.c_bytes + p.q_bytes + p.sa_bytes + p.sb_bytes;
   if (!workspace || workspace_nbytes < need) return fail(MXK_EINVAL, "qgemm: workspace too small");
   uint8_t* ws = reinterpret_cast<uint8_t*>(workspace);
   int8_t* A8 = p.direct_a ? (int8_t*)a_packed : reinterpret_cast<int8_t*>(ws);
   int8_t* B8 = reinterpret_cast<int8_t*>(ws + p.a_bytes);
   float* Cbuf = c_f32 ? c_f32 : (p.c_bytes ? reinterpret_cast<float*>(ws + p.a_bytes + p.b_bytes) : nullptr);
   void* qws = ws + p.a_bytes + p.b_bytes + p.c_bytes;
+  float* sa_t = p.v2 ? reinterpret_cast<float*>(ws + p.a_bytes + p.b_bytes + p.c_bytes + p.q_bytes) : nullptr;
+  float* sb_one = p.v3 ? reinterpret_cast<float*>(ws + p.a_bytes + p.b_bytes + p.c_bytes + p.q_bytes + p.sa_bytes)
+                       : nullptr;
   const int64_t a_bytes_src = mxk_packed_nbytes(bits, M * K);
   const int64_t b_bytes_src = mxk_packed_nbytes(bits, K * N);
   const int cap = num_cus() * 8;
@@ -216,7 +682,11 @@ int mxk_qgemm(const void* a_packed, const float* a_scales, int64_t a_nscales, co
     hipLaunchKernelGGL(k_unpack_rows, dim3((int)std::min<int64_t>(ceil_div(total, 256), cap)), dim3(256), 0, st,
                        (const uint8_t*)a_packed, a_bytes_src, bits, M, p.Mpad, K, K, 1, block, p.BP, p.KB, A8);
   }
-  {
+  if (bits == 8 && p.BP == block && N % 16 == 0 && (reinterpret_cast<uintptr_t>(b_packed) & 15u) == 0 &&
+      ceil_div(p.KBP, 64) < 65536) {
+    const dim3 tg((unsigned)ceil_div(p.Npad, 64), (unsigned)ceil_div(p.KBP, 64));
+    hipLaunchKernelGGL(k_transpose_b8, tg, dim3(256), 0, st, (const int8_t*)b_packed, K, N, p.Npad, p.KBP, B8);
+  } else {
     const int64_t total = p.Npad * (p.KBP / 16);
     hipLaunchKernelGGL(k_unpack_rows, dim3((int)std::min<int64_t>(ceil_div(total, 256), cap)), dim3(256), 0, st,
                        (const uint8_t*)b_packed, b_bytes_src, bits, N, p.Npad, K, 1, N, block, p.BP, p.KB, B8);
@@ -227,17 +697,59 @@ int mxk_qgemm(const void* a_packed, const float* a_scales, int64_t a_nscales, co
   const int64_t lda = p.direct_a ? K : p.KBP;
   const int64_t arows = p.direct_a ? M : p.Mpad;
   const bool wc = Cbuf != nullptr;
-  if (acc_i32 && wc)
+  if (!wc && !acc_i32) return fail(MXK_EINVAL, "qgemm: no output requested");
+  if (p.v3) {
+    const int64_t tiles_m = ceil_div(M, QG3_BM), tiles_n = ceil_div(N, QG3_BN);
+    const int grouped = (tiles_m % 8 == 0 && tiles_n % 8 == 0 && (tiles_m * tiles_n) % 512 == 0) ? 1 : 0;
+    const dim3 g1((unsigned)(tiles_m * tiles_n));
+    if (a_ok) {
+      const dim3 tg((unsigned)ceil_div(p.KB, 32), (unsigned)ceil_div(M, 32));
+      hipLaunchKernelGGL(k_transpose_sa, tg, dim3(256), 0, st, a_scales, M, (int64_t)p.KB, sa_t);
+    } else {
+      hipLaunchKernelGGL(k_fill_ones, dim3((unsigned)std::min<int64_t>(ceil_div((int64_t)p.KB * M, 256), cap)),
+                         dim3(256), 0, st, sa_t, (int64_t)p.KB * M);
+    }
+    const float* sbs = b_scales;
+    if (!b_ok) {
+      hipLaunchKernelGGL(k_fill_ones, dim3((unsigned)std::min<int64_t>(ceil_div((int64_t)p.KB * N, 256), cap)),
+                         dim3(256), 0, st, sb_one, (int64_t)p.KB * N);
+      sbs = sb_one;
+    }
+    if (acc_i32 && wc)
+      hipLaunchKernelGGL((k_qgemm_i8_v3<true, true>), g1, dim3(512), 0, st, A8, lda, arows, B8, p.KBP, p.Npad, sa_t,
+                         sbs, M, N, p.KB, Cbuf, acc_i32, grouped);
+    else if (acc_i32)
+      hipLaunchKernelGGL((k_qgemm_i8_v3<true, false>), g1, dim3(512), 0, st, A8, lda, arows, B8, p.KBP, p.Npad,
+                         sa_t, sbs, M, N, p.KB, Cbuf, acc_i32, grouped);
+    else
+      hipLaunchKernelGGL((k_qgemm_i8_v3<false, true>), g1, dim3(512), 0, st, A8, lda, arows, B8, p.KBP, p.Npad,
+                         sa_t, sbs, M, N, p.KB, Cbuf, acc_i32, grouped);
+  } else if (p.v2) {
+    const int64_t tiles_m = ceil_div(M, QG_BM), tiles_n = ceil_div(N, QG_BN);
+    const int grouped = (tiles_m % 8 == 0 && tiles_n % 8 == 0 && (tiles_m * tiles_n) % 512 == 0) ? 1 : 0;
+    const dim3 g1((unsigned)(tiles_m * tiles_n));
+    if (a_ok) {
+      const dim3 tg((unsigned)ceil_div(p.KB, 32), (unsigned)ceil_div(M, 32));
+      hipLaunchKernelGGL(k_transpose_sa, tg, dim3(256), 0, st, a_scales, M, (int64_t)p.KB, sa_t);
+    }
+    if (acc_i32 && wc)
+      hipLaunchKernelGGL((k_qgemm_i8_v2<true, true>), g1, dim3(256), 0, st, A8, lda, arows, B8, p.KBP, p.Npad, sa_t,
+                         a_ok, b_scales, b_ok, M, N, p.KB, Cbuf, acc_i32, grouped);
+    else if (acc_i32)
+      hipLaunchKernelGGL((k_qgemm_i8_v2<true, false>), g1, dim3(256), 0, st, A8, lda, arows, B8, p.KBP, p.Npad,
+                         sa_t, a_ok, b_scales, b_ok, M, N, p.KB, Cbuf, acc_i32, grouped);
+    else
+      hipLaunchKernelGGL((k_qgemm_i8_v2<false, true>), g1, dim3(256), 0, st, A8, lda, arows, B8, p.KBP, p.Npad,
+                         sa_t, a_ok, b_scales, b_ok, M, N, p.KB, Cbuf, acc_i32, grouped);
+  } else if (acc_i32 && wc)
     hipLaunchKernelGGL((k_qgemm_i8<true, true>), grid, dim3(256), 0, st, A8, lda, arows, B8, p.KBP, p.Npad, a_scales,
                        a_ok, b_scales, b_ok, M, N, p.KB, p.BP, Cbuf, acc_i32);
   else if (acc_i32)
     hipLaunchKernelGGL((k_qgemm_i8<true, false>), grid, dim3(256), 0, st, A8, lda, arows, B8, p.KBP, p.Npad,
                        a_scales, a_ok, b_scales, b_ok, M, N, p.KB, p.BP, Cbuf, acc_i32);
-  else if (wc)
+  else
     hipLaunchKernelGGL((k_qgemm_i8<false, true>), grid, dim3(256), 0, st, A8, lda, arows, B8, p.KBP, p.Npad,
                        a_scales, a_ok, b_scales, b_ok, M, N, p.KB, p.BP, Cbuf, acc_i32);
-  else
-    return fail(MXK_EINVAL, "qgemm: no output requested");
   int rc = check_launch("qgemm");
   if (rc != MXK_OK) return rc;
   if (out_bits > 0)

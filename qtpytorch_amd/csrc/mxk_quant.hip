@@ -108,8 +108,8 @@ __global__ __launch_bounds__(256) void k_quant_fast(const T* __restrict__ x, int
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int g = lane / LPB, li = lane % LPB;
   // U rounds of GPB blocks per iteration, a grid-stride apart, with all
-  // their loads issued before the first reduction (U = 2 and 4 measured
-  // slower on 2^28 elements than one round)
+  // their loads issued before the first reduction (U = 4 measured slower
+  // on 2^28 elements than one round)
   constexpr int U = 1;
   const int64_t rstride = (int64_t)gridDim.x * GPB;
   for (int64_t b0 = (int64_t)blockIdx.x * GPB; b0 < nb; b0 += U * rstride) {

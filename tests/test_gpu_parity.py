@@ -235,6 +235,33 @@ def test_qgemm_seeded_vs_oracle(qa, dtype, shape):
     assert _bits_eq(res["scales"], scales)
 
 
+@pytest.mark.parametrize("shape", [(4096, 384, 2048), (4100, 640, 2050), (4096, 256, 4096)],
+                         ids=lambda s: "x".join(map(str, s)))
+def test_qgemm_large_tiles_sampled_rows(qa, shape):
+    """Shapes large enough for the 256x128-tile pipelined kernel (grouped and
+    row-major tile orders, K blocks past the 3-stage ring, ragged M/N).
+    Output rows are independent, so the oracle runs on a sample of A's rows
+    and must match those rows of C and of the int32 accumulators bitwise."""
+    M, K, N = shape
+    dt = qa.get_mx_dtype("int8d")
+    A = _randn((M, K), 101 + K)
+    B = _randn((K, N), 103 + N)
+    pa, sa, _ = qa.ops.quantize(A.to(dev()), dt, 128)
+    pb, sb, _ = qa.ops.quantize(B.to(dev()), dt, 128)
+    res = qa.ops.qscale_gemm(pa, sa, pb, sb, M, K, N, 8, 128, 16, want_packed=False, want_c=True, want_acc=True)
+    c_only = qa.ops.qscale_gemm(pa, sa, pb, sb, M, K, N, 8, 128, 16, want_packed=False, want_c=True)
+    assert _bits_eq(res["c"], c_only["c"])
+    KB = -(-K // 128)
+    rows = sorted({0, 1, 15, 16, 17, 127, 128, 255, 256, 1000, M // 2, M - 2, M - 1})
+    ac = orc.unpack_auto(pa.cpu(), 8, M * K).to(torch.int32).reshape(M, K)[rows].reshape(-1)
+    bc = orc.unpack_auto(pb.cpu(), 8, K * N).to(torch.int32)
+    sa_rows = sa.cpu().reshape(M, KB)[rows].reshape(-1)
+    _, _, C = orc.qscale_matmul(ac, sa_rows, bc, sb.cpu(), len(rows), K, N, 8, 128, 16, return_c=True)
+    assert _bits_eq(res["c"].cpu()[rows], C.reshape(len(rows), N))
+    acc = orc.int_accumulators(ac, bc, len(rows), K, N, 128)
+    assert torch.equal(res["acc"].cpu()[:, rows], acc)
+
+
 @pytest.mark.parametrize("dtype", ["int4d", "int8d", "int2d", "float4d", "float8d", "int1d"])
 @pytest.mark.parametrize("shape", [(16, 1024, 768), (3, 300, 200), (64, 512, 256), (1, 128, 128)])
 @pytest.mark.parametrize("xdt", [torch.float32, torch.bfloat16])
