@@ -125,8 +125,8 @@ def quantize(x: Tensor, dt, block: int = 128, *, seed: Optional[int] = None,
         x = x.float()
     xc = x.contiguous()
     n = xc.numel()
-    if n == 0:
-        raise L.MXKError("quantize: empty tensor")
+    if n == 0:  # the reference returns empty codes and scales (nb = 0)
+        return packed_storage(dt.bits, 0, dev), torch.empty(0, dtype=torch.float32, device=dev), 0
     nb = -(-n // block)
     if n_store is None:
         n_store = nb * block
@@ -162,6 +162,8 @@ def _dequant(packed: Tensor, scales: Tensor, dt, n: int, block: int, *, orig_sha
     pk = packed.contiguous()
     sc = scales.contiguous().float()
     out = torch.empty(n, dtype=torch.float32, device=dev)
+    if n == 0:
+        return out
     rot_dim = 0
     sg = None
     if var == L.MXK_VAR_HADAMARD:
@@ -194,6 +196,19 @@ def qscale_gemm(a_packed: Tensor, a_scales: Tensor, b_packed: Tensor, b_scales: 
     dev = L.require_gpu(a_packed, a_scales, b_packed, b_scales)
     out = {}
     cp = cs = cf = acc = None
+    if M == 0 or N == 0 or K == 0:
+        # empty operands: C is all zeros (an empty K sum) and has no blocks to requantize
+        if want_packed:
+            out["packed"] = packed_storage(out_bits, M * N, dev)
+            out["packed"].zero_()
+            # an all-zero block: s = fl32(1e-12) / q in float32, as the 'v' requantizer computes it
+            out["scales"] = (torch.full((-(-(M * N) // block),), 1e-12, dtype=torch.float32, device=dev)
+                             / float((1 << (out_bits - 1)) - 1))
+        if want_c:
+            out["c"] = torch.zeros(M, N, dtype=torch.float32, device=dev)
+        if want_acc:
+            out["acc"] = torch.zeros(0, M, N, dtype=torch.int32, device=dev)
+        return out
     if want_packed:
         cp = packed_storage(out_bits, M * N, dev)
         cs = torch.empty(-(-(M * N) // block), dtype=torch.float32, device=dev)
@@ -262,6 +277,8 @@ def linear_wq(x: Tensor, w_packed: Tensor, w_scales: Tensor, dt, in_features: in
         xc = xc.float()
     xc = xc.contiguous()
     M = xc.shape[0]
+    if M == 0:
+        return torch.empty(*lead, N, dtype=torch.float32, device=dev)
     if w_scales_t is not None:
         if (w_scales_t.device != dev or w_scales_t.dtype != torch.float32 or not w_scales_t.is_contiguous()
                 or w_scales_t.numel() != K * (N // block)):
