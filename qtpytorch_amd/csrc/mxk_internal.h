@@ -46,6 +46,37 @@ __device__ __forceinline__ float div_rn(float a, float b, float y) {
   return __builtin_fmaf(r, y, q0);
 }
 
+// The same quotient without the per-element check, for callers that have
+// already established that no lane of the wave holds a nonzero |a| < 2^-96
+// (div_rn_all): a per-element branch costs more than the division itself.
+// For b > 0 the quotient has the sign of a, zeros included, and the final
+// copysign restores it where the last FMA would turn -0 into +0.
+__device__ __forceinline__ float div_rn_nochk(float a, float b, float y) {
+  float q0 = a * y;
+  float r = __builtin_fmaf(-q0, b, a);
+  return __builtin_copysignf(__builtin_fmaf(r, y, q0), a);
+}
+
+// v[i] = RN(v[i] / b) for E values and b > 0: one wave-wide vote on the
+// smallest nonzero magnitude picks the Markstein path for the whole wave, or
+// the hardware divide when any lane holds a nonzero value below 2^-96.
+template <int E>
+__device__ __forceinline__ void div_rn_all(float (&v)[E], float b, float y) {
+  float mn = __builtin_inff();
+#pragma unroll
+  for (int i = 0; i < E; ++i) {
+    const float t = __builtin_fabsf(v[i]);
+    mn = fminf(mn, t == 0.0f ? __builtin_inff() : t);
+  }
+  if (__builtin_expect(__ballot(mn < 0x1p-96f) != 0ull, 0)) {
+#pragma unroll
+    for (int i = 0; i < E; ++i) v[i] = v[i] / b;
+  } else {
+#pragma unroll
+    for (int i = 0; i < E; ++i) v[i] = div_rn_nochk(v[i], b, y);
+  }
+}
+
 __device__ __forceinline__ float rne(float v) { return __builtin_rintf(v); }
 
 // Lane-group max over `G` consecutive lanes (G a power of two <= 64); every

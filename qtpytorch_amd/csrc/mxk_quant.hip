@@ -286,12 +286,10 @@ __global__ __launch_bounds__(256) void k_quant_had128(const T* __restrict__ x, i
 #pragma unroll
     for (int i = 0; i < E; ++i) v[i] = v[i] * sg[i];
     fwht128_group(v, row, li);
+    div_rn_all<E>(v, rdiv, rinv);
     float m = 0.0f;
 #pragma unroll
-    for (int i = 0; i < E; ++i) {
-      v[i] = div_rn(v[i], rdiv, rinv);
-      m = fmaxf(m, __builtin_fabsf(v[i]));
-    }
+    for (int i = 0; i < E; ++i) m = fmaxf(m, __builtin_fabsf(v[i]));
     const float ap = fmaxf(group_max<LPB>(m), MXK_AMIN);
     const BlockParams bp = block_params<MODE>(ap, qf);
     uint32_t w[NW];
@@ -583,8 +581,9 @@ __global__ __launch_bounds__(256) void k_dequant_had128(const uint8_t* __restric
 #pragma unroll
     for (int i = 0; i < E; ++i) v[i] = decode_field<MODE, BITS>(w[(i * BITS) >> 5], (i * BITS) & 31, s, sG);
     fwht128_group(v, row, li);
+    div_rn_all<E>(v, rdiv, rinv);
 #pragma unroll
-    for (int i = 0; i < E; ++i) v[i] = div_rn(v[i], rdiv, rinv) * sg[i];
+    for (int i = 0; i < E; ++i) v[i] = v[i] * sg[i];
     // through the row's LDS once more, so that store q of the 8 lanes covers
     // positions 32q .. 32q+31: one whole 128-byte line per store
 #pragma unroll
@@ -719,19 +718,19 @@ static bool try_had128(const T* x, int64_t n, int mode, int bits, const float* s
   if (!aligned16(x)) return false;
   const int64_t nb = ceil_div(n, 128);
   const int grid = grid_for(nb, 32);
-#define MXK_H(MODE, BITS)                                                                                   \
-  if (mode == MODE && bits == BITS) {                                                                       \
+#define MXK_HAD_CASE(MODE, BITS)                                                                               \
+  if (mode == MODE && bits == BITS) {                                                                          \
     hipLaunchKernelGGL((k_quant_had128<T, MODE, BITS>), dim3(grid), dim3(256), 0, st, x, n, nb, signs, packed, \
-                       pbytes, n_store, scales, qf);                                                        \
-    return true;                                                                                            \
+                       pbytes, n_store, scales, qf);                                                           \
+    return true;                                                                                               \
   }
-  MXK_H(Q_INT, 2)
-  MXK_H(Q_INT, 4)
-  MXK_H(Q_INT, 8)
-  MXK_H(Q_INT1, 1)
-  MXK_H(Q_FP, 4)
-  MXK_H(Q_FP, 8)
-#undef MXK_H
+  MXK_HAD_CASE(Q_INT, 2)
+  MXK_HAD_CASE(Q_INT, 4)
+  MXK_HAD_CASE(Q_INT, 8)
+  MXK_HAD_CASE(Q_INT1, 1)
+  MXK_HAD_CASE(Q_FP, 4)
+  MXK_HAD_CASE(Q_FP, 8)
+#undef MXK_HAD_CASE
   return false;
 }
 

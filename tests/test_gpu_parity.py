@@ -209,6 +209,32 @@ def test_hadamard_rows128_dequant(qa, dtype):
     assert _bits_eq(dq, rdq)
 
 
+@pytest.mark.parametrize("dtype", ["int4dh", "float8dh"])
+def test_hadamard_rows128_tiny_values(qa, dtype):
+    """Rotated values below 2^-96 take the exactly rounded division path of
+    the fused kernels (one wave-wide vote per row group): rows scaled by
+    1e-33, all-zero rows and rows mixing both, bit-exact against the oracle."""
+    x = _randn((384, 128), 62)
+    x[::3] *= 1e-33
+    x[1::7] = 0.0
+    x[2::5, :64] *= 1e-36
+    dt = qa.get_mx_dtype(dtype)
+    packed, scales, n = qa.ops.quantize(x.to(dev()), dt, 128, seed=99)
+    rp, rs, rn = orc.quantize(x, dtype, 128, seed=99)
+    assert _bits_eq(packed, rp) and _bits_eq(scales, rs)
+    dq = qa.ops._dequant(packed, scales, dt, n, 128, orig_shape=(384, 128), seed=99, hadamard_mode="rows")
+    rdq = orc.dequant(rp, rs, dtype, rn, 128, seed=99, orig_shape=(384, 128), hadamard_mode="rows")
+    assert _bits_eq(dq, rdq)
+    # quantized scales never go below 1e-12, so caller-supplied tiny scales
+    # drive the dequantize side below 2^-96 (every third row of normal codes)
+    ts = rs.clone()
+    ts[1::3] *= 1e-30
+    dq = qa.ops._dequant(packed, ts.to(dev()), dt, n, 128, orig_shape=(384, 128), seed=99, hadamard_mode="rows")
+    rdq = orc.dequant(rp, ts, dtype, rn, 128, seed=99, orig_shape=(384, 128), hadamard_mode="rows")
+    assert _bits_eq(dq, rdq)
+    assert 0 < rdq[rdq != 0].abs().min() < 2.0 ** -96
+
+
 GEMM_SHAPES = [(512, 512, 512), (256, 384, 200), (100, 256, 130), (33, 128, 17), (8, 640, 1024)]
 
 
