@@ -202,6 +202,24 @@ __device__ void build_tables(float* P, float* G) {
   __syncthreads();
 }
 
+// Value of sorted-grid index f of the 8-bit float format without a table
+// (G[f] of build_tables<8>): codes 0..127 are the negative half, in
+// decreasing magnitude, so the magnitude index is c = f ^ 0x7F there and
+// f - 128 above.  With e = c >> 3 and mantissa m = c & 7 (plus 8 when e > 0),
+// fmt_value(c) / 480 = (m / 15) * 2^(max(e,1) - 15); the power of two scales
+// exactly (the smallest nonzero value, 2^-14 / 15, is normal), so the value
+// is RN(m / 15) scaled, and RN(m / 15) is the exactly rounded quotient of two
+// small integers.  Index 127 gives -0.0, as in the table.
+__device__ __forceinline__ float fp8_grid_value(uint32_t f) {
+  const uint32_t neg = ((f >> 7) & 1u) ^ 1u;
+  const uint32_t c = (f ^ (neg * 0x7Fu)) & 0x7Fu;
+  const uint32_t e = c >> 3;
+  const float m = (float)((c & 7u) | (e != 0u ? 8u : 0u));
+  const float q = div_rn_nochk(m, 15.0f, 0x1.111112p-4f);  // RN(1/15)
+  const float g = __builtin_ldexpf(q, (int)(e != 0u ? e : 1u) - 15);
+  return neg ? -g : g;
+}
+
 // Index of y in the sorted grid: #{mids < y} (torch.bucketize, right=False).
 // By the grid's symmetry this is H + #{P_j < |y|} for y > 0 and
 // H-1 - #{P_j <= |y|} otherwise.  The count comes from rounding |y| to the

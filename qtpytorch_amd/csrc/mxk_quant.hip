@@ -465,6 +465,8 @@ template <int MODE, int BITS>
 __device__ __forceinline__ float decode_field(uint32_t word, int sh, float s, const float* sG) {
   if constexpr (MODE == Q_INT1) {
     return ((word >> sh) & 1u) == 0u ? s : -s;
+  } else if constexpr (MODE == Q_FP && BITS == 8) {
+    return fp8_grid_value((word >> sh) & 0xFFu) * s;
   } else if constexpr (MODE == Q_FP) {
     return sG[(word >> sh) & ((1u << BITS) - 1u)] * s;
   } else {
@@ -480,7 +482,7 @@ __global__ __launch_bounds__(256) void k_dequant_fast(const uint8_t* __restrict_
   constexpr int U = 4;
   constexpr int H = MODE == Q_FP ? (1 << (BITS - 1)) : 1;
   __shared__ float sG[2 * H];
-  if constexpr (MODE == Q_FP) build_tables<BITS>(nullptr, sG);
+  if constexpr (MODE == Q_FP && BITS != 8) build_tables<BITS>(nullptr, sG);
   const int64_t slots = (n + 3) / 4;
   const int64_t stride = (int64_t)gridDim.x * blockDim.x;
   for (int64_t s0 = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; s0 < slots; s0 += U * stride) {
@@ -541,7 +543,7 @@ __global__ __launch_bounds__(256) void k_dequant_had128(const uint8_t* __restric
   constexpr int H = MODE == Q_FP ? (1 << (BITS - 1)) : 1;
   __shared__ float sG[2 * H];
   __shared__ __attribute__((aligned(16))) float srow[GPB * MXK_ROWPAD];
-  if constexpr (MODE == Q_FP) build_tables<BITS>(nullptr, sG);
+  if constexpr (MODE == Q_FP && BITS != 8) build_tables<BITS>(nullptr, sG);
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int g = lane / LPB, li = lane % LPB;
   float* row = srow + (wave * GPW + g) * MXK_ROWPAD;

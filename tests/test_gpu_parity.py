@@ -209,6 +209,27 @@ def test_hadamard_rows128_dequant(qa, dtype):
     assert _bits_eq(dq, rdq)
 
 
+@pytest.mark.parametrize("dtype", ["float8d", "float4d", "int8d", "int4d", "int2d", "int1d", "float8dh"])
+def test_dequant_every_code(qa, dtype):
+    """Every byte value 0..255 (so every code of every width, and every pair
+    of 4-bit codes) in every position of a slot, against the oracle's grid
+    lookup; scales from 1e-30 to 1e30 and both signs of zero in the output."""
+    g = torch.Generator()
+    g.manual_seed(17)
+    perm = torch.cat([torch.randperm(256, generator=g) for _ in range(16)])
+    packed = perm.to(torch.uint8).view(torch.int8)
+    dt = qa.get_mx_dtype(dtype)
+    n = packed.numel() * 8 // dt.bits
+    nb = n // 128
+    scales = torch.logspace(-30, 30, nb, dtype=torch.float32)
+    hseed = 5 if dt.is_hadamard else None
+    shape = (n // 128, 128)
+    dq = qa.ops._dequant(packed.to(dev()), scales.to(dev()), dt, n, 128, orig_shape=shape, seed=hseed,
+                         hadamard_mode="rows")
+    rdq = orc.dequant(packed, scales, dtype, n, 128, seed=hseed, orig_shape=shape, hadamard_mode="rows")
+    assert _bits_eq(dq, rdq)
+
+
 @pytest.mark.parametrize("dtype", ["int4dh", "float8dh"])
 def test_hadamard_rows128_tiny_values(qa, dtype):
     """Rotated values below 2^-96 take the exactly rounded division path of
