@@ -108,13 +108,18 @@ __global__ __launch_bounds__(256) void k_linear_generic(const T* __restrict__ x,
 // reads the scales block-major, sT[n/128][k] (mxk_linear_prepack_scales), so
 // that a block's scales along K are contiguous.
 //
-// Work split: a workgroup of 8 waves owns NBW scale blocks (NBW*128 output
-// columns) and R = 8/NBW * RPW rows of K.  Wave w takes block w % NBW and
-// row group w / NBW.  Before the main loop the workgroup stages its x rows in
-// LDS as float (rows m >= M and rows past K as zeros; coalesced 16-byte
-// loads, shared by the NBW waves of a row group) and every wave stages its
-// own RPW scales with one 16-byte load per lane; both are issued ahead of the
-// weight prefetch.
+// Work split: a workgroup of 16 waves (4 per SIMD) owns NBW scale blocks
+// (NBW*128 output columns) and R = 16/NBW * RPW rows of K.  Wave w takes
+// block w % NBW and row group w / NBW.
+//
+// Start-up order.  Each CU returns memory data in request order, and at
+// launch every workgroup asks for its weights at once, so whatever is queued
+// first arrives first.  A workgroup therefore requests, in this order: its x
+// rows (staged once in LDS as float, rows m >= M and rows past K as zeros),
+// each wave's RPW scales (one 16-byte load per lane), and only the first
+// 32-row step of weights; it waits for x, writes x and the scales to LDS,
+// passes one barrier, and only then fills the rest of the P-deep weight
+// prefetch.  Compute starts as soon as x and the first step are in.
 //
 // Per 32-row step a wave runs v_mfma_f32_16x16x32_f16 on
 //   A[m][k] = x[m,k] * s[k,nb]          split as f16 hi + f16 lo (22 bits)
@@ -127,19 +132,27 @@ __global__ __launch_bounds__(256) void k_linear_generic(const T* __restrict__ x,
 // nibbles; one v_perm_b32 then builds a B dword from two rows.  The +8 offset
 // is removed with a correction tile D_corr (B = 8 * 2^-20):
 //   odd tiles  y = 2^20 * (D - D_corr),  even tiles  y = 2^24 * (D - D_corr / 16).
-// Reductions are deterministic: waves of a block combine through LDS in a
-// fixed tree; workgroups that split K write partials with agent-coherent
-// stores, count arrivals on an atomic counter, and the last one sums the
-// partials in split order and resets the counter.  When the column groups
-// divide evenly over the 8 XCDs (workgroup b runs on XCD b % 8), all splits of
-// a column group are placed on one XCD; the protocol does not depend on it.
+//
+// Reductions are deterministic.  The waves' 16 x 128 partials meet in LDS
+// (reusing the x rows once every wave has left the loop) and every thread
+// sums its float4s over the row groups in order.  Workgroups that split K
+// write their partials with write-through (sc1) stores, then count arrivals
+// on a 64-bit counter per column group holding one 8-bit count per XCC (the
+// XCC_ID hardware register).  The last arrival sums the partials in split
+// order and resets the counter.  When every split ran on its own XCC, which
+// shares one L2, it reads the partials through L2 (sc0); otherwise past it
+// (sc1).  When the column groups divide evenly over the 8 XCDs (workgroup b
+// runs on XCD b % 8), all splits of a column group are placed on one XCD;
+// the protocol does not depend on it.
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
 
-#define DEC_WAVES 8
-#define DEC_COUNTER_BYTES 65536  // split-K counters: up to 16384 column groups
+#define DEC_WAVES 16
+#define DEC_THREADS (64 * DEC_WAVES)
+#define DEC_COUNTER_BYTES 65536  // split-K counters: 8192 column groups of 8 bytes
 #define DEC_XPAD 4               // LDS row padding of the staged x (floats)
+#define DEC_RS 132               // LDS row stride of a wave partial (floats)
 #define DEC_OOB 0x80000000u      // buffer offset past every range: the load returns zeros
 
 // A = x * s as f16 hi + f16 lo: hi = RZ(x*s), lo = RZ(fma(x, s, -hi))
@@ -161,30 +174,43 @@ __device__ __forceinline__ void split_hi_lo(const f32x4& x0, const f32x4& x1, co
   lo = __builtin_bit_cast(f16x8, u32x4v{l[0], l[1], l[2], l[3]});
 }
 
+// s_barrier without the memory fence of __syncthreads: the fence would make
+// every wave wait for all of its weight loads still in flight.
+__device__ __forceinline__ void dec_barrier_nofence() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
 template <int STEPS, int NBW>
 struct DecGeom {
   static constexpr int RPW = STEPS * 32;        // rows per wave
   static constexpr int RG = DEC_WAVES / NBW;    // row groups per workgroup
   static constexpr int R = RG * RPW;            // rows per workgroup
   static constexpr int XS = R + DEC_XPAD;       // LDS row stride of the staged x
-  static constexpr int TREE = RG / 2 > 0 ? RG / 2 : 1;
+  static constexpr int LX = 16 * XS > DEC_WAVES * 16 * DEC_RS ? 16 * XS : DEC_WAVES * 16 * DEC_RS;
+  // reduction: TPB threads per block, CPT (a multiple of 4) outputs each
+  static constexpr int TPB = DEC_THREADS / NBW > 512 ? 512 : DEC_THREADS / NBW;
+  static constexpr int RT = TPB * NBW;          // threads taking part in the reduction
+  static constexpr int CPT = 2048 / TPB;
 };
 
 template <typename T, int STEPS, int NBW, int P>
-__global__ __launch_bounds__(64 * DEC_WAVES, 1) void k_linear_w4_decode(
+__global__ __launch_bounds__(DEC_THREADS, 1) void k_linear_w4_decode(
     const T* __restrict__ x, int M, int64_t K, int64_t N, const uint32_t* __restrict__ w,
     const float* __restrict__ scales_t, const float* __restrict__ bias, float* __restrict__ out,
-    float* __restrict__ partials, unsigned* __restrict__ counters, int S, int xcd_map) {
+    float* __restrict__ partials, unsigned long long* __restrict__ counters, int S, int xcd_map) {
   using G = DecGeom<STEPS, NBW>;
-  constexpr int RPW = G::RPW, RG = G::RG, R = G::R, XS = G::XS;
-  constexpr int EPL = 16 / (int)sizeof(T);  // x elements per 16-byte load
-  constexpr int XL = 16 * R / EPL / 512;    // x loads per thread
-  static_assert(XL * 512 * EPL == 16 * R, "x staging must divide evenly");
+  constexpr int RPW = G::RPW, RG = G::RG, R = G::R, XS = G::XS, TPB = G::TPB, RT = G::RT, CPT = G::CPT;
+  constexpr int EPL = 16 / (int)sizeof(T);        // x elements per 16-byte load
+  constexpr int XL = 16 * R / EPL / DEC_THREADS;  // x loads per thread
+  static_assert(XL * DEC_THREADS * EPL == 16 * R, "x staging must divide evenly");
   static_assert(RPW / 4 <= 64, "one 16-byte scale load per lane");
-  __shared__ __attribute__((aligned(16))) float sX[16 * XS];
+  static_assert(CPT % 4 == 0 && TPB * CPT == 2048, "reduction split");
+  // x rows during the loop, then the waves' partials
+  __shared__ __attribute__((aligned(16))) float sX[G::LX];
   __shared__ __attribute__((aligned(16))) float sS[DEC_WAVES * RPW];
-  __shared__ __attribute__((aligned(16))) f32x4 red[G::TREE * NBW * 512];  // tree slots, lane-major
-  __shared__ int s_last;
+  __shared__ int s_flags;
   // the wave index goes through readfirstlane so that everything derived
   // from it (row ranges, scalar buffer offsets) is known to be wave-uniform
   const int lane = threadIdx.x & 63;
@@ -207,13 +233,13 @@ __global__ __launch_bounds__(64 * DEC_WAVES, 1) void k_linear_w4_decode(
   const int kv = (int)(K - k0w < R ? K - k0w : R);     // its rows inside K (a multiple of 32)
   const int64_t kw = k0w + (int64_t)rg * RPW;          // this wave's first row
 
-  // ---- staging loads: x rows (workgroup) and this wave's scales, zeros out of range
+  // ---- requests in arrival order: x rows, scales, the first weight step
   const __amdgpu_buffer_rsrc_t rx = make_rsrc(x, (uint32_t)((int64_t)M * K * sizeof(T)));
   const __amdgpu_buffer_rsrc_t rs = make_rsrc(scales_t, (uint32_t)(K * NB * 4));
   u32x4 xst[XL];
 #pragma unroll
   for (int i = 0; i < XL; ++i) {
-    const int e = threadIdx.x + 512 * i;
+    const int e = threadIdx.x + DEC_THREADS * i;
     const int m = e / (R / EPL), c = e % (R / EPL);
     const bool ok = m < M && c * EPL < kv;
     xst[i] = buf_load_b128(rx, ok ? (uint32_t)(((int64_t)m * K + k0w + (int64_t)c * EPL) * sizeof(T)) : DEC_OOB, 0u);
@@ -223,9 +249,8 @@ __global__ __launch_bounds__(64 * DEC_WAVES, 1) void k_linear_w4_decode(
 
   // ---- weight prefetch, P steps deep over a fully unrolled step sequence:
   // step st computes from slot st % P, then the slot is refilled with step
-  // st + P.  Straight-line code lets the compiler wait for exactly the loads
-  // each step needs.  Buffer loads carry one per-lane offset (lane's k-group
-  // and column word) and the step's row in the scalar offset.  The hardware
+  // st + P.  Buffer loads carry one per-lane offset (lane's k-group and
+  // column word) and the step's row in the scalar offset.  The hardware
   // range check does not cover the scalar offset, so every address is kept
   // valid by construction: a step past K (only in the last split when K is
   // not a multiple of R) re-reads rows 0..31, and its x rows and scales are
@@ -240,16 +265,15 @@ __global__ __launch_bounds__(64 * DEC_WAVES, 1) void k_linear_w4_decode(
 #pragma unroll
     for (int r = 0; r < 8; ++r) wv[slot][r] = buf_load_b32(rw, vw, (kr + r) * row_bytes);
   };
-#pragma unroll
-  for (int q = 0; q < P && q < STEPS; ++q) issue(q, q);
-  // keep the prefetch loads where they are written (the scheduler would
-  // otherwise sink them next to their first use)
+  issue(0, 0);
+  // keep the loads where they are written (the scheduler would otherwise
+  // sink them next to their first use)
   __builtin_amdgcn_sched_barrier(0);
 
   // ---- staged data to LDS: float x, row m at sX[m * XS]; scales per wave
 #pragma unroll
   for (int i = 0; i < XL; ++i) {
-    const int e = threadIdx.x + 512 * i;
+    const int e = threadIdx.x + DEC_THREADS * i;
     const int m = e / (R / EPL), c = e % (R / EPL);
     float* dst = sX + m * XS + c * EPL;
     if constexpr (EPL == 4) {
@@ -265,6 +289,9 @@ __global__ __launch_bounds__(64 * DEC_WAVES, 1) void k_linear_w4_decode(
   float* wS = sS + wave * RPW;
   if (lane < RPW / 4) *reinterpret_cast<f32x4*>(wS + 4 * lane) = __builtin_bit_cast(f32x4, sst);
   __syncthreads();
+#pragma unroll
+  for (int q = 1; q < P && q < STEPS; ++q) issue(q, q);
+  __builtin_amdgcn_sched_barrier(0);
 
   f32x4 acc[8];
 #pragma unroll
@@ -308,103 +335,109 @@ __global__ __launch_bounds__(64 * DEC_WAVES, 1) void k_linear_w4_decode(
     corr = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi, b8, corr, 0, 0, 0);
     corr = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo, b8, corr, 0, 0, 0);
   }
-  // this wave's partial: rows m = 4g+i, columns 8j+t of block nb
-  float v[8][4];
-#pragma unroll
-  for (int t = 0; t < 8; ++t)
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-      v[t][i] = (t & 1) ? (acc[t][i] - corr[i]) * 1048576.0f : (acc[t][i] - corr[i] * 0.0625f) * 16777216.0f;
 
-  // fixed-order tree over the RG row groups of each block
+  // ---- wave partial (rows 4g+i, columns 8j+t of block nb) to LDS, after
+  // every wave has finished reading the x rows it overwrites
+  __syncthreads();
+  float* red = sX;
+  float* rwv = red + wave * 16 * DEC_RS;
 #pragma unroll
-  for (int half = RG / 2; half >= 1; half >>= 1) {
-    if (rg >= half && rg < 2 * half) {
-      f32x4* slot = red + ((rg - half) * NBW + nbl) * 512;
+  for (int i = 0; i < 4; ++i) {
+    float v[8];
 #pragma unroll
-      for (int t = 0; t < 8; ++t) slot[t * 64 + lane] = f32x4{v[t][0], v[t][1], v[t][2], v[t][3]};
-    }
-    __syncthreads();
-    if (rg < half) {
-      const f32x4* slot = red + (rg * NBW + nbl) * 512;
-#pragma unroll
-      for (int t = 0; t < 8; ++t) {
-        const f32x4 o = slot[t * 64 + lane];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) v[t][i] = v[t][i] + o[i];
-      }
-    }
-    __syncthreads();
+    for (int t = 0; t < 8; ++t)
+      v[t] = (t & 1) ? (acc[t][i] - corr[i]) * 1048576.0f : (acc[t][i] - corr[i] * 0.0625f) * 16777216.0f;
+    float* dst = rwv + (4 * g + i) * DEC_RS + 8 * j;
+    *reinterpret_cast<f32x4*>(dst) = f32x4{v[0], v[1], v[2], v[3]};
+    *reinterpret_cast<f32x4*>(dst + 4) = f32x4{v[4], v[5], v[6], v[7]};
   }
-  const int64_t col0 = nb * 128;
+  __syncthreads();
+  // thread (< RT): block b of the group, row m, columns c .. c+CPT-1,
+  // summed over the row groups in order
+  const bool rt = threadIdx.x < RT;
+  const int b = rt ? threadIdx.x / TPB : 0, r = threadIdx.x % TPB;
+  const int m = r / (128 / CPT), c = CPT * (r % (128 / CPT));
+  f32x4 sum[CPT / 4];
+#pragma unroll
+  for (int h = 0; h < CPT / 4; ++h) {
+    sum[h] = *reinterpret_cast<const f32x4*>(red + (b * 16 + m) * DEC_RS + c + 4 * h);
+#pragma unroll
+    for (int q = 1; q < RG; ++q)
+      sum[h] += *reinterpret_cast<const f32x4*>(red + ((q * NBW + b) * 16 + m) * DEC_RS + c + 4 * h);
+  }
+  const int64_t nbb = cg * NBW + b;
+  const int64_t col = nbb * 128 + c;
   if (S == 1) {
-    if (rg == 0) {
+    if (rt && m < M) {
 #pragma unroll
-      for (int t = 0; t < 8; ++t)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int m = 4 * g + i;
-          const int64_t col = col0 + 8 * j + t;
-          if (m < M) out[(int64_t)m * N + col] = bias ? v[t][i] + bias[col] : v[t][i];
-        }
+      for (int h = 0; h < CPT / 4; ++h) {
+        f32x4 o = sum[h];
+        if (bias) o += *reinterpret_cast<const f32x4*>(bias + col + 4 * h);
+        *reinterpret_cast<f32x4*>(out + (int64_t)m * N + col + 4 * h) = o;
+      }
     }
     return;
   }
-  // partials: [S][column group][NBW][8 tiles][64 lanes] float4, written with
-  // agent-coherent (sc1) stores that complete before the workgroup is counted
-  const int64_t NCG = NB / NBW;
-  const uint32_t part_bytes = (uint32_t)((int64_t)S * NB * 8 * 64 * 16);
-  const __amdgpu_buffer_rsrc_t rp = make_rsrc(partials, part_bytes);
-  const uint32_t pbase = (uint32_t)((((int64_t)cg * NBW + nbl) * 512 + lane) * 16);
-  const uint32_t split_stride = (uint32_t)(NCG * NBW * 512 * 16);
-  if (rg == 0) {
+  // partials: [S][N/128][16 rows][128 columns] floats, written through to
+  // memory before the workgroup is counted
+  const __amdgpu_buffer_rsrc_t rp = make_rsrc(partials, (uint32_t)((int64_t)S * NB * 16 * 128 * 4));
+  const uint32_t poff = (uint32_t)(((nbb * 16 + m) * 128 + c) * 4);
+  const uint32_t split_stride = (uint32_t)(NB * 16 * 128 * 4);
+  if (rt) {
 #pragma unroll
-    for (int t = 0; t < 8; ++t)
-      __builtin_amdgcn_raw_buffer_store_b128(f32x4{v[t][0], v[t][1], v[t][2], v[t][3]}, rp,
-                                             pbase + (uint32_t)t * 1024u, (uint32_t)ks * split_stride, 16);
-    __builtin_amdgcn_s_waitcnt(0);
+    for (int h = 0; h < CPT / 4; ++h)
+      __builtin_amdgcn_raw_buffer_store_b128(sum[h], rp, poff + 16u * h, (uint32_t)ks * split_stride, 16);
+  }
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    unsigned xcc;
+    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
+    xcc &= 7u;
+    const unsigned long long inc = 1ull << (8 * xcc);
+    const unsigned long long now =
+        __hip_atomic_fetch_add(&counters[cg], inc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + inc;
+    unsigned total = 0;
+#pragma unroll
+    for (int q = 0; q < 8; ++q) total += (unsigned)((now >> (8 * q)) & 0xFFull);
+    const bool same = ((now >> (8 * xcc)) & 0xFFull) == (unsigned long long)S;
+    s_flags = (total == (unsigned)S ? 1 : 0) | (same ? 2 : 0);
   }
   __syncthreads();
-  if (threadIdx.x == 0)
-    s_last = __hip_atomic_fetch_add(&counters[cg], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
-             (unsigned)(S - 1);
-  __syncthreads();
-  if (!s_last) return;
-  // last workgroup of this column group: every thread sums NBW float4 of the
-  // S partials in split order, with up to 16 loads in flight per round
-  constexpr int CH = 16 / NBW;  // splits per round
-  const uint32_t cg_base = (uint32_t)((int64_t)cg * NBW * 512 * 16);
-  f32x4 sum[NBW];
-  for (int sb = 0; sb < S; sb += CH) {
-    f32x4 part[CH][NBW];
+  const int fl = s_flags;
+  if (!(fl & 1) || !rt) return;  // thread 0 is a reduction thread: it resets the counter below
+  // last arrival: sum the S partials in split order (its own from registers)
+  f32x4 tot[CPT / 4];
+  for (int sb = 0; sb < S; sb += 8) {
+    f32x4 part[8][CPT / 4];
 #pragma unroll
-    for (int u = 0; u < CH; ++u)
+    for (int u = 0; u < 8; ++u)
 #pragma unroll
-      for (int b = 0; b < NBW; ++b)
-        part[u][b] = __builtin_bit_cast(
-            f32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                       rp, sb + u < S ? cg_base + (uint32_t)(threadIdx.x + 512 * b) * 16u : DEC_OOB,
-                       sb + u < S ? (uint32_t)(sb + u) * split_stride : 0u, 16));
-#pragma unroll
-    for (int u = 0; u < CH; ++u)
-      if (sb + u < S) {
-#pragma unroll
-        for (int b = 0; b < NBW; ++b) sum[b] = (sb + u == 0) ? part[u][b] : sum[b] + part[u][b];
+      for (int h = 0; h < CPT / 4; ++h) {
+        const bool ld = sb + u < S && sb + u != ks;
+        const uint32_t soff = ld ? (uint32_t)(sb + u) * split_stride : 0u;
+        if (!ld)
+          part[u][h] = sum[h];
+        else if (fl & 2)
+          part[u][h] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rp, poff + 16u * h, soff, 1));
+        else
+          part[u][h] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rp, poff + 16u * h, soff, 16));
       }
+#pragma unroll
+    for (int u = 0; u < 8; ++u)
+      if (sb + u < S)
+#pragma unroll
+        for (int h = 0; h < CPT / 4; ++h) tot[h] = (sb + u == 0) ? part[u][h] : tot[h] + part[u][h];
   }
+  if (m < M) {
 #pragma unroll
-  for (int b = 0; b < NBW; ++b) {
-    const int e = threadIdx.x + 512 * b;  // float4 index within this column group's blocks
-    const int enbl = e / 512, et = (e / 64) % 8, el = e % 64;
-    const int eg = el >> 4, ej = el & 15;
-    const int64_t col = (cg * NBW + enbl) * 128 + 8 * ej + et;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int m = 4 * eg + i;
-      if (m < M) out[(int64_t)m * N + col] = bias ? sum[b][i] + bias[col] : sum[b][i];
+    for (int h = 0; h < CPT / 4; ++h) {
+      f32x4 o = tot[h];
+      if (bias) o += *reinterpret_cast<const f32x4*>(bias + col + 4 * h);
+      *reinterpret_cast<f32x4*>(out + (int64_t)m * N + col + 4 * h) = o;
     }
   }
-  if (threadIdx.x == 0) __hip_atomic_store(&counters[cg], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (threadIdx.x == 0) __hip_atomic_store(&counters[cg], 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // sT[b][k] = s[k][b]: the reference's scales of a [K, N] weight with blocks
@@ -441,17 +474,26 @@ static int64_t dec_rows(int nbw, int steps) { return (int64_t)(DEC_WAVES / nbw) 
 static DecodePlan plan_decode(int64_t K, int64_t N) {
   DecodePlan p;
   const int64_t NB = N / 128;
-  // widest column group (shared x / scale staging) that still gives every CU
-  // a workgroup; fall back to narrower groups, then shorter waves
-  static const int cand[][2] = {{2, 8}, {4, 8}, {2, 4}, {4, 4}, {1, 4}};
-  p.nbw = 1;
-  p.steps = 4;
+  // two-block column groups (x staged once for two blocks, 128-byte weight
+  // rows) with the longest waves that still give every CU a workgroup; then
+  // single blocks; else the shape with the most workgroups
+  static const int cand[][2] = {{2, 4}, {2, 2}, {1, 4}, {1, 2}, {1, 1}};
   const int64_t target = num_cus();
+  p.nbw = 1;
+  p.steps = 1;
+  int64_t best = -1;
   for (const auto& c : cand) {
     const int nbw = c[0], steps = c[1];
     if (NB % nbw) continue;
     const int64_t S = ceil_div(K, dec_rows(nbw, steps));
-    if ((NB / nbw) * S >= target && S <= 32) {
+    if (S > 255) continue;  // 8-bit arrival counts per XCC
+    const int64_t grid = (NB / nbw) * S;
+    if (grid > best) {
+      best = grid;
+      p.nbw = nbw;
+      p.steps = steps;
+    }
+    if (grid >= target) {
       p.nbw = nbw;
       p.steps = steps;
       break;
@@ -459,7 +501,7 @@ static DecodePlan plan_decode(int64_t K, int64_t N) {
   }
   p.S = (int)ceil_div(K, dec_rows(p.nbw, p.steps));
   p.xcd_map = (NB / p.nbw) % 8 == 0 ? 1 : 0;
-  p.partial_bytes = p.S > 1 ? (((size_t)p.S * (size_t)(N / 128) * 8 * 64 * 16 + 255) & ~(size_t)255) : 0;
+  p.partial_bytes = p.S > 1 ? (((size_t)p.S * (size_t)NB * 8192 + 255) & ~(size_t)255) : 0;
   // the counters live in a fixed prefix that nothing else overwrites, so a
   // zero-filled workspace stays valid across calls of any shape (each call
   // resets the counters it used)
@@ -472,26 +514,26 @@ static DecodePlan plan_decode(int64_t K, int64_t N) {
 template <typename T, int STEPS, int NBW>
 static void launch_decode_t(const DecodePlan& p, hipStream_t st, const void* x, int64_t M, int64_t K, int64_t N,
                             const uint32_t* w, const float* scales, const float* bias, float* out, float* partials,
-                            unsigned* counters) {
+                            unsigned long long* counters) {
   const dim3 grid((unsigned)((N / 128 / NBW) * p.S));
-  hipLaunchKernelGGL((k_linear_w4_decode<T, STEPS, NBW, 4>), grid, dim3(64 * DEC_WAVES), 0, st, (const T*)x, (int)M,
-                     K, N, w, scales, bias, out, partials, counters, p.S, p.xcd_map);
+  hipLaunchKernelGGL((k_linear_w4_decode<T, STEPS, NBW, 4>), grid, dim3(DEC_THREADS), 0, st, (const T*)x, (int)M, K,
+                     N, w, scales, bias, out, partials, counters, p.S, p.xcd_map);
 }
 
 template <typename T>
 static void launch_decode(const DecodePlan& p, hipStream_t st, const void* x, int64_t M, int64_t K, int64_t N,
                           const uint32_t* w, const float* scales, const float* bias, float* out, float* partials,
-                          unsigned* counters) {
+                          unsigned long long* counters) {
 #define MXK_DEC(STEPS, NBW)                                                                          \
   if (p.steps == STEPS && p.nbw == NBW) {                                                           \
     launch_decode_t<T, STEPS, NBW>(p, st, x, M, K, N, w, scales, bias, out, partials, counters);    \
     return;                                                                                         \
   }
-  MXK_DEC(8, 2)
-  MXK_DEC(8, 4)
   MXK_DEC(4, 2)
-  MXK_DEC(4, 4)
+  MXK_DEC(2, 2)
   MXK_DEC(4, 1)
+  MXK_DEC(2, 1)
+  MXK_DEC(1, 1)
 #undef MXK_DEC
 }
 
@@ -499,7 +541,7 @@ static bool decode_eligible(int64_t M, int64_t K, int64_t N, int kind, int bits,
                             int x_type, const void* w) {
   if (kind != MXK_KIND_INT || bits != 4 || block != 128) return false;
   if (M < 1 || M > 16 || K % 32 != 0 || N % 128 != 0) return false;
-  if (N / 128 > DEC_COUNTER_BYTES / 4 || K / 32 >= 65536) return false;
+  if (N / 128 > DEC_COUNTER_BYTES / 8 || K / 32 >= 65536) return false;
   if (!aligned16(x) || (reinterpret_cast<uintptr_t>(w) & 3u) != 0) return false;
   const int esz = x_type == MXK_IN_F32 ? 4 : 2;
   if ((K * esz) % 16 != 0) return false;
@@ -576,7 +618,7 @@ int mxk_linear_wq(const void* x, int x_type, int64_t M, int64_t K, const void* w
     if (need > 0 && (!workspace || workspace_nbytes < need))
       return fail(MXK_EINVAL, "linear_wq: decode path needs a zero-initialised workspace of mxk_linear_workspace() bytes");
     uint8_t* ws = reinterpret_cast<uint8_t*>(workspace);
-    unsigned* counters = p.S > 1 ? reinterpret_cast<unsigned*>(ws) : nullptr;
+    unsigned long long* counters = p.S > 1 ? reinterpret_cast<unsigned long long*>(ws) : nullptr;
     float* partials = p.S > 1 ? reinterpret_cast<float*>(ws + p.counter_bytes) : nullptr;
     const float* sT = w_scales_t;
     if (!sT) {
