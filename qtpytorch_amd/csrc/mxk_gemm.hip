@@ -391,11 +391,6 @@ template <int N>
 __device__ __forceinline__ void qg3_lgkm_wait(i32x4& v) {
   asm volatile("s_waitcnt lgkmcnt(%1)" : "+v"(v) : "n"(N));
 }
-__device__ __forceinline__ float qg3_ds_read_f32(uint32_t lds_byte_addr) {
-  float v;
-  asm volatile("ds_read_b32 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(v) : "v"(lds_byte_addr) : "memory");
-  return v;
-}
 
 template <bool WRITE_ACC, bool WRITE_C>
 __global__ __launch_bounds__(512, 1) void k_qgemm_i8_v3(const int8_t* __restrict__ A8, int64_t lda, int64_t Arows,
@@ -448,8 +443,12 @@ __global__ __launch_bounds__(512, 1) void k_qgemm_i8_v3(const int8_t* __restrict
   const bool is_b = wave == 4 || wave == 5;
   const char* gsb = reinterpret_cast<const char*>(is_b ? sb_src : sa_t);
   const int64_t gstride = is_b ? N : M;
+  // SB is stored lane-major: float 256 + 64*wn + 4*lr + t holds column
+  // n0 + 64*wn + 16t + lr, so a lane's four SB values are one 16-byte read
+  const int fb = f - 256;  // 0..127 on waves 4-5
   const uint32_t os = (uint32_t)(4 * (f < 256 ? std::min<int64_t>(m0 + f, M - 1)
-                                              : (f < 384 ? std::min<int64_t>(n0 + f - 256, N - 1) : 0)));
+                                              : (f < 384 ? std::min<int64_t>(n0 + (fb & ~63) + (fb & 3) * 16 + ((fb & 63) >> 2), N - 1)
+                                                         : 0)));
   auto load_stage = [&](int kb, int buf) {
     const char* a0 = reinterpret_cast<const char*>(A8) + (int64_t)kb * 128;
     const char* b0 = reinterpret_cast<const char*>(B8) + (int64_t)kb * 128;
@@ -497,12 +496,11 @@ __global__ __launch_bounds__(512, 1) void k_qgemm_i8_v3(const int8_t* __restrict
     if (kb + 2 < KB) load_stage(kb + 2, cur == 0 ? 2 : cur - 1);
     const uint32_t sa_off = (uint32_t)cur * (QG3_BM * 128), sb_off = (uint32_t)cur * (QG3_BN * 128);
     const uint32_t cS = (uint32_t)(uintptr_t)(&sS[0][0]) + (uint32_t)cur * 2048u;
-    // LDS reads are issued ahead and waited for with partial lgkmcnt counts
-    // (LDS ops complete in order): A slice 0, all B fragments, A slice 1,
-    // then each slice's MFMAs prefetch the slice after next.  The four
-    // 16-row slices are software-pipelined: the MFMAs of slice a+1 are issued
-    // before the fp32 epilogue of slice a, C = RN(C + RN(RN(P*SA)*SB)).
-    i32x4 af[4][2], bf[2][4];
+    // LDS reads in need order, at most 15 in flight (the lgkmcnt limit),
+    // waited for with partial counts (LDS ops complete in order): A slice 0,
+    // the B fragments, A slice 1, SB, SA of slices 0-1; then A slices 2-3
+    // and SA 2-3 while slice 1 computes.
+    i32x4 af[4][2], bf[2][4], sa[4], sbv;
     af[0][0] = qg3_ds_read(offA0 + sa_off);
     af[0][1] = qg3_ds_read(offA1 + sa_off);
 #pragma unroll
@@ -512,18 +510,16 @@ __global__ __launch_bounds__(512, 1) void k_qgemm_i8_v3(const int8_t* __restrict
     }
     af[1][0] = qg3_ds_read(offA0 + sa_off + 2048);
     af[1][1] = qg3_ds_read(offA1 + sa_off + 2048);
-    // A slice 0 and B are the first 10 of 12 reads in flight
-    qg3_lgkm_wait<2>(af[0][0]);
-    qg3_lgkm_wait<2>(af[0][1]);
+    sbv = qg3_ds_read(cS + 4u * (256 + wn * 64 + 4 * lr));
+    sa[0] = qg3_ds_read(cS + 4u * (wm * 64 + lg * 4));
+    sa[1] = qg3_ds_read(cS + 4u * (wm * 64 + 16 + lg * 4));
+    qg3_lgkm_wait<5>(af[0][0]);
+    qg3_lgkm_wait<5>(af[0][1]);
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
-      qg3_lgkm_wait<2>(bf[0][t]);
-      qg3_lgkm_wait<2>(bf[1][t]);
+      qg3_lgkm_wait<5>(bf[0][t]);
+      qg3_lgkm_wait<5>(bf[1][t]);
     }
-    float sb[4];
-#pragma unroll
-    for (int t = 0; t < 4; ++t) sb[t] = qg3_ds_read_f32(cS + 4u * (256 + wn * 64 + t * 16 + lr));
-    // (each scale read waits for lgkmcnt(0), which also lands A slice 1)
     auto slice_mfma = [&](int a, i32x4 (&p)[4]) {
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
@@ -531,18 +527,13 @@ __global__ __launch_bounds__(512, 1) void k_qgemm_i8_v3(const int8_t* __restrict
         p[t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af[a][1], bf[1][t], p[t], 0, 0, 0);
       }
     };
-    auto load_slice = [&](int a) {
-      af[a][0] = qg3_ds_read(offA0 + sa_off + a * 2048);
-      af[a][1] = qg3_ds_read(offA1 + sa_off + a * 2048);
-    };
+    // C = RN(C + RN(RN(P*SA)*SB)) for the 16 outputs of slice a
     auto slice_epilogue = [&](int a, const i32x4 (&p)[4]) {
-      i32x4 sa4 = qg3_ds_read(cS + 4u * (wm * 64 + a * 16 + lg * 4));
-      qg3_lgkm_wait<0>(sa4);
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
-          const float v = ((float)p[t][i] * __int_as_float(sa4[i])) * sb[t];
+          const float v = ((float)p[t][i] * __int_as_float(sa[a][i])) * __int_as_float(sbv[t]);
           c[a][t][i] = c[a][t][i] + v;
           if (WRITE_ACC) {
             const int64_t row = m0 + wm * 64 + a * 16 + lg * 4 + i;
@@ -552,24 +543,51 @@ __global__ __launch_bounds__(512, 1) void k_qgemm_i8_v3(const int8_t* __restrict
         }
       }
     };
+    // The MFMAs of slice a+1 go one by one between the epilogue VALU ops of
+    // slice a (8 MFMAs, 64 VALU ops), so the matrix core runs while the same
+    // wave issues the epilogue.
+#define QG3_INTERLEAVE()                                 \
+    for (int ii = 0; ii < 8; ++ii) {                     \
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0); \
+      __builtin_amdgcn_sched_group_barrier(0x002, 8, 0); \
+    }
     i32x4 p0[4], p1[4];
     slice_mfma(0, p0);
-    load_slice(2);
+    __builtin_amdgcn_sched_barrier(0);
+    qg3_lgkm_wait<0>(af[1][0]);
+    qg3_lgkm_wait<0>(af[1][1]);
+    qg3_lgkm_wait<0>(sbv);
+    qg3_lgkm_wait<0>(sa[0]);
+    qg3_lgkm_wait<0>(sa[1]);
+    af[2][0] = qg3_ds_read(offA0 + sa_off + 2 * 2048);
+    af[2][1] = qg3_ds_read(offA1 + sa_off + 2 * 2048);
+    sa[2] = qg3_ds_read(cS + 4u * (wm * 64 + 32 + lg * 4));
+    af[3][0] = qg3_ds_read(offA0 + sa_off + 3 * 2048);
+    af[3][1] = qg3_ds_read(offA1 + sa_off + 3 * 2048);
+    sa[3] = qg3_ds_read(cS + 4u * (wm * 64 + 48 + lg * 4));
     __builtin_amdgcn_sched_barrier(0);
     slice_mfma(1, p1);
+    slice_epilogue(0, p0);
+    QG3_INTERLEAVE();
     __builtin_amdgcn_sched_barrier(0);
-    slice_epilogue(0, p0);  // its lgkmcnt(0) also lands A slice 2
+    qg3_lgkm_wait<3>(af[2][0]);
+    qg3_lgkm_wait<3>(af[2][1]);
+    qg3_lgkm_wait<3>(sa[2]);
     __builtin_amdgcn_sched_barrier(0);
     slice_mfma(2, p0);
-    load_slice(3);
+    slice_epilogue(1, p1);
+    QG3_INTERLEAVE();
     __builtin_amdgcn_sched_barrier(0);
-    slice_epilogue(1, p1);  // lands A slice 3
+    qg3_lgkm_wait<0>(af[3][0]);
+    qg3_lgkm_wait<0>(af[3][1]);
+    qg3_lgkm_wait<0>(sa[3]);
     __builtin_amdgcn_sched_barrier(0);
     slice_mfma(3, p1);
-    __builtin_amdgcn_sched_barrier(0);
     slice_epilogue(2, p0);
+    QG3_INTERLEAVE();
     __builtin_amdgcn_sched_barrier(0);
     slice_epilogue(3, p1);
+#undef QG3_INTERLEAVE
     cur = cur == 2 ? 0 : cur + 1;
   }
   if (WRITE_C) {
