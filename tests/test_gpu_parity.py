@@ -347,6 +347,31 @@ def test_linear_decode_split_k(qa, shape):
         assert err <= LINEAR_RTOL * y_ref.abs().max().item(), f"max err {err}"
 
 
+@pytest.mark.parametrize("shape,xdt", [
+    ((16, 4096, 8192), torch.float32),   # two-block groups, 64-row waves, 8 splits
+    ((9, 8192, 8064), torch.float16),    # odd block count: single-block groups, 64-row waves
+    ((16, 8160, 8192), torch.float32),   # K not a multiple of the split: a partial last split
+    ((4, 1024, 2176), torch.bfloat16),   # 17 blocks, 32-row waves
+])
+def test_linear_decode_plans(qa, shape, xdt):
+    """Each work split of the decode kernel (column-group width, rows per
+    wave, split count, partial last split) against the oracle; the fused
+    bias equals the bias added afterwards, bit for bit."""
+    M, K, N = shape
+    W = _randn((N, K), 51 + N, outliers=1e-3, scale=20.0) * 0.02
+    x = _randn((M, K), 53 + M).to(xdt)
+    wp, ws, _ = orc.linear_from_weight(W, "int4d", 128)
+    dt = qa.get_mx_dtype("int4d")
+    wpg, wsg, xg = wp.to(dev()), ws.to(dev()), x.to(dev())
+    st = qa.ops.prepack_scales(wsg, K, N, 128)
+    y = qa.ops.linear_wq(xg, wpg, wsg, dt, K, N, 128, w_scales_t=st).cpu()
+    y_ref = orc.linear_forward(x, wp, ws, "int4d", K, N, 128)
+    assert (y - y_ref).abs().max().item() <= LINEAR_RTOL * y_ref.abs().max().item()
+    b = _randn((N,), 57)
+    yb = qa.ops.linear_wq(xg, wpg, wsg, dt, K, N, 128, bias=b.to(dev()), w_scales_t=st).cpu()
+    assert _bits_eq(yb, y + b)
+
+
 def test_linear_decode_config2_shape(qa):
     """The benchmark shape: x [16, 8192] @ int4d W [8192, 8192]."""
     x = _randn((16, 8192), 2)
