@@ -53,9 +53,10 @@ def gen(seed: int, device="cpu") -> torch.Generator:
 EAGER = False  # --eager: launch the steps directly (no graph), for counter collection
 
 
-def graph_time(step, steps: int, warmup: int) -> float:
+def graph_time(step, steps: int, warmup: int, repeats: int = 1) -> float:
     """Seconds per step: `steps` calls of step() captured in one graph,
-    replayed between events on the current stream."""
+    replayed between events on the current stream (the median over
+    `repeats` timed replays)."""
     for _ in range(max(warmup, 1)):
         step()
     torch.cuda.synchronize()
@@ -80,15 +81,18 @@ def graph_time(step, steps: int, warmup: int) -> float:
     g.replay()  # warm replay
     torch.cuda.synchronize()
     st = torch.cuda.current_stream()
-    e0 = torch.cuda.Event(enable_timing=True)
-    e1 = torch.cuda.Event(enable_timing=True)
-    e0.record(st)
-    g.replay()
-    e1.record(st)
-    torch.cuda.synchronize()
-    dt = e0.elapsed_time(e1) / 1e3 / steps
+    times = []
+    for _ in range(max(repeats, 1)):
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record(st)
+        g.replay()
+        e1.record(st)
+        torch.cuda.synchronize()
+        times.append(e0.elapsed_time(e1) / 1e3 / steps)
     del g
-    return dt
+    times.sort()
+    return times[len(times) // 2]
 
 
 def load_traffic(name: str):
@@ -204,9 +208,10 @@ def bench_gemm(qa, M, K, N, reps):
     pa, sa, _ = qa.ops.quantize(A, d8, 128)
     pb, sb, _ = qa.ops.quantize(B, d8, 128)
     del A, B
+    # the median of 5 replays: back-to-back 8192^3 GEMMs move the clock by +-10% from launch to launch
     t_c = graph_time(lambda: qa.ops.qscale_gemm(pa, sa, pb, sb, M, K, N, 8, 128, 16, want_packed=False,
-                                                  want_c=True), reps, 1)
-    t_p = graph_time(lambda: qa.ops.qscale_gemm(pa, sa, pb, sb, M, K, N, 8, 128, 16), reps, 1)
+                                                  want_c=True), reps, 1, repeats=5)
+    t_p = graph_time(lambda: qa.ops.qscale_gemm(pa, sa, pb, sb, M, K, N, 8, 128, 16), reps, 1, repeats=5)
     ops = 2.0 * M * K * N
     return {"shape": [M, K, N], "fp32_out_us": round(t_c * 1e6, 2), "fp32_out_TOPS": round(ops / t_c / 1e12, 2),
             "fp32_out_frac_int8_peak": round(ops / t_c / 1e12 / INT8_PEAK_TOPS, 4),

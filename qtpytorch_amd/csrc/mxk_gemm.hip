@@ -349,13 +349,17 @@ __global__ __launch_bounds__(256, 2) void k_qgemm_i8_v2(const int8_t* __restrict
 }
 
 // v3 for large problems, blocks of 65..128: 512 threads (8 waves, 2 per
-// SIMD) on a 256x128 tile, each wave 64x64 as in v2; three LDS stages of one
-// K block each (A 32 KiB + B 16 KiB + scales), filled two stages ahead with
-// global_load_lds (tiles, 16 B per lane; scales, 4 B per lane).  Every
-// thread issues the same 7 loads per stage, so one vmcnt value waits for a
-// stage; one barrier per K block, placed before the loads that refill the
-// stage every wave has just finished.  sa_t is [KB][M] and sb_src [KB][N]
-// (both all ones when the reference would use ones).
+// SIMD) on a 256x128 tile, each wave 64x64 as in v2 (4 slices of 16 rows x
+// 4 column fragments); three LDS stages of one K block each (A 32 KiB, B
+// 16 KiB, scales 2 KiB), filled two stages ahead by buffer loads straight to
+// LDS (tiles 16 B per lane, scales 4 B per lane).  Every thread issues the
+// same 7 loads per stage, spread over the slices of the K block two stages
+// earlier, so that one vmcnt value waits for a stage and the LDS writes do
+// not pile onto the fragment reads that follow each barrier.  One barrier
+// per K block, before the loads that refill the stage every wave has just
+// finished.  sa_t is [KB][M] and sb_src [KB][N] (both all ones when the
+// reference would use ones).  The host takes this path only when A8, B8
+// and both scale arrays stay below 2^31 bytes (32-bit buffer offsets).
 #define QG3_BM 256
 #define QG3_BN 128
 #define QG3_NS 3
@@ -367,7 +371,7 @@ __device__ __forceinline__ void wait_vmcnt() {
 }
 
 // Barrier without a memory fence: the LDS data a stage reads arrives by
-// global_load_lds, whose completion each thread waits for with vmcnt
+// buffer loads to LDS, whose completion each thread waits for with vmcnt
 // before the barrier; a fence here would make the compiler wait for every
 // load in flight, including the stages still being prefetched.
 __device__ __forceinline__ void qg3_barrier() {
@@ -376,15 +380,19 @@ __device__ __forceinline__ void qg3_barrier() {
   asm volatile("" ::: "memory");
 }
 
-// Fragment reads of the current stage as inline-asm ds_read_b128, each
-// followed (before first use) by an lgkmcnt wait tied to its result.  The
-// compiler does not see these as LDS reads, so it does not add vmcnt waits
-// for the global_load_lds traffic still filling the other stages (it cannot
-// prove that a runtime-indexed stage differs from those); every LDS op
-// completes in order, so its own lgkmcnt bookkeeping stays valid.
-__device__ __forceinline__ i32x4 qg3_ds_read(uint32_t lds_byte_addr) {
+// Fragment reads as inline-asm ds_read_b128 (base VGPR + immediate offset),
+// each followed (before first use) by an lgkmcnt wait tied to its result.
+// The compiler does not see these as LDS reads, so it does not add vmcnt
+// waits for the buffer-load traffic still filling the other stages; every
+// LDS op completes in order, so the explicit lgkmcnt counts stay valid.
+// Every read must be waited for while its result is still live: the data
+// lands in the register asynchronously, and a register the compiler
+// considers free could already hold another value.
+template <uint32_t OFF>
+__device__ __forceinline__ i32x4 qg3_ds_read(uint32_t base) {
+  static_assert(OFF < 65536, "ds_read offset field");
   i32x4 v;
-  asm volatile("ds_read_b128 %0, %1" : "=v"(v) : "v"(lds_byte_addr) : "memory");
+  asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(v) : "v"(base), "n"(OFF) : "memory");
   return v;
 }
 template <int N>
@@ -399,9 +407,10 @@ __global__ __launch_bounds__(512, 1) void k_qgemm_i8_v3(const int8_t* __restrict
                                                         const float* __restrict__ sb_src, int64_t M, int64_t N,
                                                         int KB, float* __restrict__ C, int32_t* __restrict__ acc_out,
                                                         int grouped) {
-  __shared__ __attribute__((aligned(1024))) int8_t sA[QG3_NS][QG3_BM * 128];
-  __shared__ __attribute__((aligned(1024))) int8_t sB[QG3_NS][QG3_BN * 128];
-  __shared__ __attribute__((aligned(1024))) float sS[QG3_NS][512];  // SA 0..255, SB 256..383
+  // [A stages 0..2, 32 KiB each][B stages 0..2, 16 KiB each][scale stages 0..2, 2 KiB each]:
+  // a stage's scales hold SA rows at floats 0..255 and SB columns at 256..383
+  __shared__ __attribute__((aligned(1024))) int8_t lds[QG3_NS * (32768 + 16384 + 2048)];
+  constexpr uint32_t LA = 0, LB = QG3_NS * 32768, LS = QG3_NS * (32768 + 16384);
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave >> 1, wn = wave & 1;
@@ -423,10 +432,9 @@ __global__ __launch_bounds__(512, 1) void k_qgemm_i8_v3(const int8_t* __restrict
   const int64_t m0 = (int64_t)tm * QG3_BM, n0 = (int64_t)tn * QG3_BN;
   const int lr = lane & 15, lg = lane >> 4;
 
-  // 32-bit per-lane byte offsets (the host keeps A8, B8 and the scale
-  // arrays below 2^31 bytes); the K block goes into the uniform base.
-  // A rows 32w + 8q + (L >> 3), B rows 16w + 8q + (L >> 3), chunk =
-  // slot ^ ((row >> 1) & 7) as in v2; scale float 64w + L.
+  // Per-lane byte offsets of the stage loads; the K block goes into the
+  // scalar offset.  A rows 32w + 8q + (L >> 3), B rows 16w + 8q + (L >> 3),
+  // chunk = slot ^ ((row >> 1) & 7) as in v2; scale float 64w + L.
   uint32_t oa[4], ob[2];
 #pragma unroll
   for (int q = 0; q < 4; ++q) {
@@ -441,7 +449,7 @@ __global__ __launch_bounds__(512, 1) void k_qgemm_i8_v3(const int8_t* __restrict
   const int f = 64 * wave + lane;
   // waves 0-3: SA rows, 4-5: SB columns, 6-7: a harmless load of SA row 0
   const bool is_b = wave == 4 || wave == 5;
-  const char* gsb = reinterpret_cast<const char*>(is_b ? sb_src : sa_t);
+  const float* gsb = is_b ? sb_src : sa_t;
   const int64_t gstride = is_b ? N : M;
   // SB is stored lane-major: float 256 + 64*wn + 4*lr + t holds column
   // n0 + 64*wn + 16t + lr, so a lane's four SB values are one 16-byte read
@@ -449,33 +457,39 @@ __global__ __launch_bounds__(512, 1) void k_qgemm_i8_v3(const int8_t* __restrict
   const uint32_t os = (uint32_t)(4 * (f < 256 ? std::min<int64_t>(m0 + f, M - 1)
                                               : (f < 384 ? std::min<int64_t>(n0 + (fb & ~63) + (fb & 3) * 16 + ((fb & 63) >> 2), N - 1)
                                                          : 0)));
-  auto load_stage = [&](int kb, int buf) {
-    const char* a0 = reinterpret_cast<const char*>(A8) + (int64_t)kb * 128;
-    const char* b0 = reinterpret_cast<const char*>(B8) + (int64_t)kb * 128;
+  const __amdgpu_buffer_rsrc_t rA = make_rsrc(A8, (uint32_t)(Arows * lda));
+  const __amdgpu_buffer_rsrc_t rB = make_rsrc(B8, (uint32_t)(Brows * ldb));
+  const __amdgpu_buffer_rsrc_t rS = make_rsrc(gsb, (uint32_t)((int64_t)KB * gstride * 4));
+  typedef __attribute__((address_space(3))) void* lds_ptr;
+  // the 7 loads of a stage in 4 parts: A rows of q 0-1, A rows of q 2-3, B, scales
+  auto load_part = [&](int kb, int buf, int part) {
+    if (part < 2) {
 #pragma unroll
-    for (int q = 0; q < 4; ++q)
-      __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)(a0 + oa[q]),
-                                       (__attribute__((address_space(3))) void*)(&sA[buf][(32 * wave + 8 * q) * 128]),
-                                       16, 0, 0);
+      for (int q = 2 * part; q < 2 * part + 2; ++q)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rA, (lds_ptr)(&lds[LA + buf * 32768 + (32 * wave + 8 * q) * 128]), 16,
+                                                 (int)oa[q], kb * 128, 0, 0);
+    } else if (part == 2) {
 #pragma unroll
-    for (int q = 0; q < 2; ++q)
-      __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)(b0 + ob[q]),
-                                       (__attribute__((address_space(3))) void*)(&sB[buf][(16 * wave + 8 * q) * 128]),
-                                       16, 0, 0);
-    const char* s0 = gsb + (int64_t)kb * gstride * 4;
-    __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)(s0 + os),
-                                     (__attribute__((address_space(3))) void*)(&sS[buf][64 * wave]), 4, 0, 0);
+      for (int q = 0; q < 2; ++q)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rB, (lds_ptr)(&lds[LB + buf * 16384 + (16 * wave + 8 * q) * 128]), 16,
+                                                 (int)ob[q], kb * 128, 0, 0);
+    } else {
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rS, (lds_ptr)(&lds[LS + buf * 2048 + 256 * wave]), 4, (int)os,
+                                               (int)((int64_t)kb * gstride * 4), 0, 0);
+    }
   };
 
   // LDS byte addresses of this lane's fragments in stage 0: row r = base +
   // 16a + lr keeps (r >> 1) & 7 = (lr >> 1) & 7 for every slice a, so slice
-  // a adds a * 2048; stage s adds s * the stage size
+  // a adds a * 2048 (an immediate); a stage adds its size to the bases.
   const int sw = (lr >> 1) & 7;
-  const uint32_t ldsA = (uint32_t)(uintptr_t)(&sA[0][0]), ldsB = (uint32_t)(uintptr_t)(&sB[0][0]);
-  const uint32_t offA0 = ldsA + (wm * 64 + lr) * 128 + ((lg ^ sw) * 16);
-  const uint32_t offA1 = ldsA + (wm * 64 + lr) * 128 + (((4 + lg) ^ sw) * 16);
-  const uint32_t offB0 = ldsB + (wn * 64 + lr) * 128 + ((lg ^ sw) * 16);
-  const uint32_t offB1 = ldsB + (wn * 64 + lr) * 128 + (((4 + lg) ^ sw) * 16);
+  const uint32_t l0 = (uint32_t)(uintptr_t)(&lds[0]);
+  const uint32_t bA0 = l0 + LA + (wm * 64 + lr) * 128 + ((lg ^ sw) * 16);
+  const uint32_t bA1 = l0 + LA + (wm * 64 + lr) * 128 + (((4 + lg) ^ sw) * 16);
+  const uint32_t bB0 = l0 + LB + (wn * 64 + lr) * 128 + ((lg ^ sw) * 16);
+  const uint32_t bB1 = l0 + LB + (wn * 64 + lr) * 128 + (((4 + lg) ^ sw) * 16);
+  const uint32_t bSB = l0 + LS + 4u * (256 + wn * 64 + 4 * lr);
+  const uint32_t bSA = l0 + LS + 4u * (wm * 64 + lg * 4);
 
   float c[4][4][4];
 #pragma unroll
@@ -484,42 +498,52 @@ __global__ __launch_bounds__(512, 1) void k_qgemm_i8_v3(const int8_t* __restrict
     for (int b = 0; b < 4; ++b)
 #pragma unroll
       for (int i = 0; i < 4; ++i) c[a][b][i] = 0.0f;
+  // slice 3 of the previous K block, applied during slice 0 of the next one
+  // (zeros before the first block: C + RN(RN(0*0)*0) = C for C = +0)
+  i32x4 p3[4] = {{0, 0, 0, 0}, {0, 0, 0, 0}, {0, 0, 0, 0}, {0, 0, 0, 0}};
+  i32x4 sa3 = {0, 0, 0, 0}, sb3 = {0, 0, 0, 0};
 
-  load_stage(0, 0);
-  if (KB > 1) load_stage(1, 1);
-  int cur = 0;
-  for (int kb = 0; kb < KB; ++kb) {
+  // C = RN(C + RN(RN(P*SA)*SB)) for output (slice a, row i, fragment t) of K block kbw
+  auto epi_elem = [&](int a, int i, int t, const i32x4 (&p)[4], const i32x4& sav, const i32x4& sbvv, int kbw) {
+    const float v = ((float)p[t][i] * __int_as_float(sav[i])) * __int_as_float(sbvv[t]);
+    c[a][t][i] = c[a][t][i] + v;
+    if (WRITE_ACC) {
+      const int64_t row = m0 + wm * 64 + a * 16 + lg * 4 + i;
+      const int64_t col = n0 + wn * 64 + t * 16 + lr;
+      if (kbw >= 0 && row < M && col < N) acc_out[((int64_t)kbw * M + row) * N + col] = p[t][i];
+    }
+  };
+
+  auto body = [&](int kb, int cur) {
+    // stage bases for this K block; fragment offsets are immediates
+    const uint32_t b0 = bA0 + (uint32_t)cur * 32768u, b1 = bA1 + (uint32_t)cur * 32768u;
+    const uint32_t bb0 = bB0 + (uint32_t)cur * 16384u, bb1 = bB1 + (uint32_t)cur * 16384u;
+    const uint32_t bsa = bSA + (uint32_t)cur * 2048u, bsb = bSB + (uint32_t)cur * 2048u;
     // stage kb has landed once at most the next stage's 7 loads are pending
     if (kb + 1 < KB) wait_vmcnt<7>();
     else wait_vmcnt<0>();
     qg3_barrier();  // stage kb visible; every wave is done with stage kb-1
-    if (kb + 2 < KB) load_stage(kb + 2, cur == 0 ? 2 : cur - 1);
-    const uint32_t sa_off = (uint32_t)cur * (QG3_BM * 128), sb_off = (uint32_t)cur * (QG3_BN * 128);
-    const uint32_t cS = (uint32_t)(uintptr_t)(&sS[0][0]) + (uint32_t)cur * 2048u;
-    // LDS reads in need order, at most 15 in flight (the lgkmcnt limit),
-    // waited for with partial counts (LDS ops complete in order): A slice 0,
-    // the B fragments, A slice 1, SB, SA of slices 0-1; then A slices 2-3
-    // and SA 2-3 while slice 1 computes.
+    const bool ld = kb + 2 < KB;
+    const int lbuf = cur == 0 ? 2 : cur - 1;
+    // reads in need order, at most 15 in flight (the lgkmcnt limit): A
+    // slice 0, B column fragments 0..3, SB, SA0, A slice 1, SA1
     i32x4 af[4][2], bf[2][4], sa[4], sbv;
-    af[0][0] = qg3_ds_read(offA0 + sa_off);
-    af[0][1] = qg3_ds_read(offA1 + sa_off);
-#pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      bf[0][t] = qg3_ds_read(offB0 + sb_off + t * 2048);
-      bf[1][t] = qg3_ds_read(offB1 + sb_off + t * 2048);
-    }
-    af[1][0] = qg3_ds_read(offA0 + sa_off + 2048);
-    af[1][1] = qg3_ds_read(offA1 + sa_off + 2048);
-    sbv = qg3_ds_read(cS + 4u * (256 + wn * 64 + 4 * lr));
-    sa[0] = qg3_ds_read(cS + 4u * (wm * 64 + lg * 4));
-    sa[1] = qg3_ds_read(cS + 4u * (wm * 64 + 16 + lg * 4));
-    qg3_lgkm_wait<5>(af[0][0]);
-    qg3_lgkm_wait<5>(af[0][1]);
-#pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      qg3_lgkm_wait<5>(bf[0][t]);
-      qg3_lgkm_wait<5>(bf[1][t]);
-    }
+    af[0][0] = qg3_ds_read<0>(b0);
+    af[0][1] = qg3_ds_read<0>(b1);
+    bf[0][0] = qg3_ds_read<0 * 2048>(bb0);
+    bf[1][0] = qg3_ds_read<0 * 2048>(bb1);
+    bf[0][1] = qg3_ds_read<1 * 2048>(bb0);
+    bf[1][1] = qg3_ds_read<1 * 2048>(bb1);
+    bf[0][2] = qg3_ds_read<2 * 2048>(bb0);
+    bf[1][2] = qg3_ds_read<2 * 2048>(bb1);
+    bf[0][3] = qg3_ds_read<3 * 2048>(bb0);
+    bf[1][3] = qg3_ds_read<3 * 2048>(bb1);
+    sbv = qg3_ds_read<0>(bsb);
+    sa[0] = qg3_ds_read<0>(bsa);
+    af[1][0] = qg3_ds_read<2048>(b0);
+    af[1][1] = qg3_ds_read<2048>(b1);
+    sa[1] = qg3_ds_read<64>(bsa);
+    __builtin_amdgcn_sched_barrier(0);
     auto slice_mfma = [&](int a, i32x4 (&p)[4]) {
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
@@ -527,21 +551,11 @@ __global__ __launch_bounds__(512, 1) void k_qgemm_i8_v3(const int8_t* __restrict
         p[t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af[a][1], bf[1][t], p[t], 0, 0, 0);
       }
     };
-    // C = RN(C + RN(RN(P*SA)*SB)) for the 16 outputs of slice a
-    auto slice_epilogue = [&](int a, const i32x4 (&p)[4]) {
+    auto slice_epilogue = [&](int a, const i32x4 (&p)[4], const i32x4& sav) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
+      for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int t = 0; t < 4; ++t) {
-          const float v = ((float)p[t][i] * __int_as_float(sa[a][i])) * __int_as_float(sbv[t]);
-          c[a][t][i] = c[a][t][i] + v;
-          if (WRITE_ACC) {
-            const int64_t row = m0 + wm * 64 + a * 16 + lg * 4 + i;
-            const int64_t col = n0 + wn * 64 + t * 16 + lr;
-            if (row < M && col < N) acc_out[((int64_t)kb * M + row) * N + col] = p[t][i];
-          }
-        }
-      }
+        for (int t = 0; t < 4; ++t) epi_elem(a, i, t, p, sav, sbv, kb);
     };
     // The MFMAs of slice a+1 go one by one between the epilogue VALU ops of
     // slice a (8 MFMAs, 64 VALU ops), so the matrix core runs while the same
@@ -552,44 +566,95 @@ __global__ __launch_bounds__(512, 1) void k_qgemm_i8_v3(const int8_t* __restrict
       __builtin_amdgcn_sched_group_barrier(0x002, 8, 0); \
     }
     i32x4 p0[4], p1[4];
-    slice_mfma(0, p0);
+    // Slice 0: MFMA pair t waits only for its own fragments (A0 and B
+    // column fragment t: the first 4 + 2t reads); the carried slice-3
+    // epilogue of the previous K block fills the gaps, 2 outputs (8 VALU
+    // ops) per chunk.
+    auto chunk = [&](int j) {
+      epi_elem(3, (2 * j) >> 2, (2 * j) & 3, p3, sa3, sb3, kb - 1);
+      epi_elem(3, (2 * j + 1) >> 2, (2 * j + 1) & 3, p3, sa3, sb3, kb - 1);
+    };
+#define QG3_SLICE0_PAIR(T, WAITN)                                                                   \
+    chunk(2 * T);                                                                                   \
+    __builtin_amdgcn_sched_barrier(0);                                                              \
+    qg3_lgkm_wait<WAITN>(af[0][0]);                                                                 \
+    qg3_lgkm_wait<WAITN>(af[0][1]);                                                                 \
+    qg3_lgkm_wait<WAITN>(bf[0][T]);                                                                 \
+    qg3_lgkm_wait<WAITN>(bf[1][T]);                                                                 \
+    __builtin_amdgcn_sched_barrier(0);                                                              \
+    p0[T] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af[0][0], bf[0][T], i32x4{0, 0, 0, 0}, 0, 0, 0); \
+    __builtin_amdgcn_sched_barrier(0);                                                              \
+    chunk(2 * T + 1);                                                                               \
+    __builtin_amdgcn_sched_barrier(0);                                                              \
+    p0[T] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af[0][1], bf[1][T], p0[T], 0, 0, 0);             \
     __builtin_amdgcn_sched_barrier(0);
-    qg3_lgkm_wait<0>(af[1][0]);
-    qg3_lgkm_wait<0>(af[1][1]);
+    QG3_SLICE0_PAIR(0, 11)
+    QG3_SLICE0_PAIR(1, 9)
+    QG3_SLICE0_PAIR(2, 7)
+    QG3_SLICE0_PAIR(3, 5)
+#undef QG3_SLICE0_PAIR
     qg3_lgkm_wait<0>(sbv);
     qg3_lgkm_wait<0>(sa[0]);
+    qg3_lgkm_wait<0>(af[1][0]);
+    qg3_lgkm_wait<0>(af[1][1]);
     qg3_lgkm_wait<0>(sa[1]);
-    af[2][0] = qg3_ds_read(offA0 + sa_off + 2 * 2048);
-    af[2][1] = qg3_ds_read(offA1 + sa_off + 2 * 2048);
-    sa[2] = qg3_ds_read(cS + 4u * (wm * 64 + 32 + lg * 4));
-    af[3][0] = qg3_ds_read(offA0 + sa_off + 3 * 2048);
-    af[3][1] = qg3_ds_read(offA1 + sa_off + 3 * 2048);
-    sa[3] = qg3_ds_read(cS + 4u * (wm * 64 + 48 + lg * 4));
+    af[2][0] = qg3_ds_read<2 * 2048>(b0);
+    af[2][1] = qg3_ds_read<2 * 2048>(b1);
+    sa[2] = qg3_ds_read<128>(bsa);
+    af[3][0] = qg3_ds_read<3 * 2048>(b0);
+    af[3][1] = qg3_ds_read<3 * 2048>(b1);
+    sa[3] = qg3_ds_read<192>(bsa);
+    if (ld) load_part(kb + 2, lbuf, 0);
     __builtin_amdgcn_sched_barrier(0);
     slice_mfma(1, p1);
-    slice_epilogue(0, p0);
+    slice_epilogue(0, p0, sa[0]);
     QG3_INTERLEAVE();
     __builtin_amdgcn_sched_barrier(0);
     qg3_lgkm_wait<3>(af[2][0]);
     qg3_lgkm_wait<3>(af[2][1]);
     qg3_lgkm_wait<3>(sa[2]);
+    if (ld) load_part(kb + 2, lbuf, 1);
     __builtin_amdgcn_sched_barrier(0);
     slice_mfma(2, p0);
-    slice_epilogue(1, p1);
+    slice_epilogue(1, p1, sa[1]);
     QG3_INTERLEAVE();
     __builtin_amdgcn_sched_barrier(0);
     qg3_lgkm_wait<0>(af[3][0]);
     qg3_lgkm_wait<0>(af[3][1]);
     qg3_lgkm_wait<0>(sa[3]);
+    if (ld) {
+      load_part(kb + 2, lbuf, 2);
+      load_part(kb + 2, lbuf, 3);
+    }
     __builtin_amdgcn_sched_barrier(0);
-    slice_mfma(3, p1);
-    slice_epilogue(2, p0);
+    slice_mfma(3, p3);
+    slice_epilogue(2, p0, sa[2]);
     QG3_INTERLEAVE();
     __builtin_amdgcn_sched_barrier(0);
-    slice_epilogue(3, p1);
 #undef QG3_INTERLEAVE
+    sa3 = sa[3];
+    sb3 = sbv;
+  };
+
+  load_part(0, 0, 0);
+  load_part(0, 0, 1);
+  load_part(0, 0, 2);
+  load_part(0, 0, 3);
+  if (KB > 1) {
+    load_part(1, 1, 0);
+    load_part(1, 1, 1);
+    load_part(1, 1, 2);
+    load_part(1, 1, 3);
+  }
+  int cur = 0;
+  for (int kb = 0; kb < KB; ++kb) {
+    body(kb, cur);
     cur = cur == 2 ? 0 : cur + 1;
   }
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int t = 0; t < 4; ++t) epi_elem(3, i, t, p3, sa3, sb3, KB - 1);
   if (WRITE_C) {
 #pragma unroll
     for (int a = 0; a < 4; ++a)
@@ -649,7 +714,11 @@ static GemmPlan plan_gemm(int64_t M, int64_t K, int64_t N, int bits, int block, 
   p.c_bytes = out_bits > 0 ? up((size_t)M * (size_t)N * sizeof(float)) : 0;
   p.q_bytes = out_bits > 0 ? up((size_t)ceil_div(M * N, block) * sizeof(float2)) : 0;
   p.v2 = p.BP == 128 && p.KB < 65536;
-  p.v3 = p.v2 && ceil_div(M, QG3_BM) * ceil_div(N, QG3_BN) >= num_cus();
+  // v3 addresses A8, B8 and the scale arrays with 32-bit buffer offsets
+  const int64_t lim = (int64_t)1 << 31;
+  const int64_t a_span = p.direct_a ? M * K : p.Mpad * p.KBP;
+  const bool fits32 = a_span < lim && p.Npad * p.KBP < lim && (int64_t)p.KB * M * 4 < lim && (int64_t)p.KB * N * 4 < lim;
+  p.v3 = p.v2 && fits32 && ceil_div(M, QG3_BM) * ceil_div(N, QG3_BN) >= num_cus();
   p.sa_bytes = p.v2 ? up((size_t)p.KB * (size_t)M * sizeof(float)) : 0;
   p.sb_bytes = p.v3 ? up((size_t)p.KB * (size_t)N * sizeof(float)) : 0;  // ones, when B's scales do not fit
   return p;

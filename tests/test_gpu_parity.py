@@ -282,13 +282,16 @@ def test_qgemm_seeded_vs_oracle(qa, dtype, shape):
     assert _bits_eq(res["scales"], scales)
 
 
-@pytest.mark.parametrize("shape", [(4096, 384, 2048), (4100, 640, 2050), (4096, 256, 4096)],
+@pytest.mark.parametrize("shape", [(4096, 384, 2048), (4100, 640, 2050), (4096, 256, 4096), (4096, 128, 2048),
+                                   (4096, 1152, 2048)],
                          ids=lambda s: "x".join(map(str, s)))
 def test_qgemm_large_tiles_sampled_rows(qa, shape):
     """Shapes large enough for the 256x128-tile pipelined kernel (grouped and
-    row-major tile orders, K blocks past the 3-stage ring, ragged M/N).
-    Output rows are independent, so the oracle runs on a sample of A's rows
-    and must match those rows of C and of the int32 accumulators bitwise."""
+    row-major tile orders, one and two K blocks, K blocks past the 3-stage
+    ring, ragged M/N).  Output rows are independent, so the oracle runs on a
+    sample of A's rows and must match those rows of C and of the int32
+    accumulators bitwise.  The three kernel variants (C and accumulators, C
+    only, accumulators only) must agree."""
     M, K, N = shape
     dt = qa.get_mx_dtype("int8d")
     A = _randn((M, K), 101 + K)
@@ -297,7 +300,9 @@ def test_qgemm_large_tiles_sampled_rows(qa, shape):
     pb, sb, _ = qa.ops.quantize(B.to(dev()), dt, 128)
     res = qa.ops.qscale_gemm(pa, sa, pb, sb, M, K, N, 8, 128, 16, want_packed=False, want_c=True, want_acc=True)
     c_only = qa.ops.qscale_gemm(pa, sa, pb, sb, M, K, N, 8, 128, 16, want_packed=False, want_c=True)
+    acc_only = qa.ops.qscale_gemm(pa, sa, pb, sb, M, K, N, 8, 128, 16, want_packed=False, want_acc=True)
     assert _bits_eq(res["c"], c_only["c"])
+    assert torch.equal(res["acc"], acc_only["acc"])
     KB = -(-K // 128)
     rows = sorted({0, 1, 15, 16, 17, 127, 128, 255, 256, 1000, M // 2, M - 2, M - 1})
     ac = orc.unpack_auto(pa.cpu(), 8, M * K).to(torch.int32).reshape(M, K)[rows].reshape(-1)
