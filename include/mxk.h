@@ -36,7 +36,7 @@
 extern "C" {
 #endif
 
-#define MXK_ABI_VERSION 2
+#define MXK_ABI_VERSION 3
 
 typedef enum {
   MXK_OK = 0,
@@ -171,6 +171,32 @@ int mxk_linear_wq(const void* x, int x_type, int64_t M, int64_t K, const void* w
                   const float* w_scales, const float* w_scales_t, int64_t N, int kind, int bits,
                   int block, const float* bias, float* out, void* workspace,
                   size_t workspace_nbytes, void* stream);
+
+/* One step of kv_cache_quantizer.append_kv (mxtorch.py:3039-3067) written
+ * into a caller-owned ring slot (the reference appends a new mx_tensor to a
+ * Python list instead, mxtorch.py:3058-3065).
+ *  k, v      device [rows, head_dim] of x_type (rows = B*H of the step), 16-byte aligned.
+ *  K rows:   quantize(k_f, dt, head_dim): one block per row.
+ *  V rows:   with asymmetric_v, zp = row min, quantize(v_f - zp, dt, head_dim)
+ *            and v_zero_point[r] = zp (mxtorch.py:3060-3065); else as K.
+ *  Outputs:  k_codes / v_codes   packed codes of the slot, rows*head_dim*bits/8 bytes;
+ *            k_scales / v_scales float32 [rows]; v_zero_point float32 [rows]
+ *            (unused when asymmetric_v = 0).
+ *  Covers head_dim in {64, 128, 256}; int widths 1, 2, 4, 8 and float 4, 8,
+ *  base or 'v' variant (MXK_EUNSUPPORTED otherwise: use mxk_quantize). */
+int mxk_kv_append(const void* k, const void* v, int x_type, int64_t rows, int head_dim, int kind, int bits,
+                  int variant, int asymmetric_v, void* k_codes, float* k_scales, void* v_codes, float* v_scales,
+                  float* v_zero_point, void* stream);
+
+/* kv_cache_quantizer.get for one tensor (mxtorch.py:3069-3086): out float32
+ * [rows, count, head_dim] = the dequantized slots start, start+1, ... (mod
+ * capacity) of a ring whose slot s holds codes at codes + s*rows*head_dim*bits/8,
+ * scales at scales + s*rows and (V, asymmetric) zero points at
+ * zero_point + s*rows, added after the dequantization (RN(dq + zp));
+ * zero_point = NULL adds nothing.  Same dtype coverage as mxk_kv_append. */
+int mxk_kv_gather(const void* codes, const float* scales, const float* zero_point, int64_t rows, int head_dim,
+                  int kind, int bits, int variant, int64_t capacity, int64_t start, int64_t count, float* out,
+                  void* stream);
 
 #ifdef __cplusplus
 }

@@ -46,6 +46,10 @@ SIGNATURES = {
     "mxk_linear_wq": (c_int, [c_vp, c_int, c_i64, c_i64, c_vp, c_vp, c_vp, c_i64, c_int, c_int, c_int, c_vp,
                               c_vp, c_vp, c_sz, c_vp]),
     "mxk_linear_prepack_scales": (c_int, [c_vp, c_i64, c_i64, c_int, c_vp, c_vp]),
+    "mxk_kv_append": (c_int, [c_vp, c_vp, c_int, c_i64, c_int, c_int, c_int, c_int, c_int, c_vp, c_vp, c_vp, c_vp,
+                              c_vp, c_vp]),
+    "mxk_kv_gather": (c_int, [c_vp, c_vp, c_vp, c_i64, c_int, c_int, c_int, c_int, c_i64, c_i64, c_i64, c_vp,
+                              c_vp]),
 }
 
 
@@ -72,7 +76,7 @@ def lib():
                 raise MXKError(f"{LIB_PATH} does not export {name}")
             fn.restype = res
             fn.argtypes = args
-        if h.mxk_abi_version() != 2:
+        if h.mxk_abi_version() != 3:
             raise MXKError("libmxk.so ABI version mismatch")
         _lib = h
         return h

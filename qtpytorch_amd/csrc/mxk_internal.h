@@ -243,6 +243,59 @@ __device__ __forceinline__ int bucket(float y, const float* __restrict__ P) {
   return (H - 1) - (c0 + (hi <= a ? 1 : 0) - (lo > a ? 1 : 0));
 }
 
+// ---------------------------------------------------------------- per-block params
+struct BlockParams {
+  float s;    // stored scale
+  float mul;  // Q_INT: inv ; Q_VEC/Q_FP: RN(1/s)
+};
+
+template <int MODE>
+__device__ __forceinline__ BlockParams block_params(float ap, float qf) {
+  BlockParams bp;
+  if constexpr (MODE == Q_INT) {
+    float r = 1.0f / ap;
+    bp.mul = r * qf;
+    bp.s = 1.0f / bp.mul;
+  } else if constexpr (MODE == Q_VEC) {
+    bp.s = ap / qf;
+    bp.mul = 1.0f / bp.s;
+  } else {  // Q_INT1, Q_FP
+    bp.s = ap;
+    bp.mul = 1.0f / ap;
+  }
+  return bp;
+}
+
+template <int MODE, int BITS>
+__device__ __forceinline__ int encode(float v, const BlockParams& bp, float qf, const float* P) {
+  if constexpr (MODE == Q_INT) {
+    return (int)rne(fminf(fmaxf(v * bp.mul, -qf), qf));
+  } else if constexpr (MODE == Q_INT1) {
+    return v >= 0.0f ? 0 : 1;
+  } else if constexpr (MODE == Q_VEC) {
+    return (int)rne(fminf(fmaxf(div_rn(v, bp.s, bp.mul), -qf), qf));
+  } else {
+    return bucket<BITS>(div_rn(v, bp.s, bp.mul), P);
+  }
+}
+
+// ---------------------------------------------------------------- decode
+// Value of the field at bit `sh` of `word` for scale s (sG: the sorted grid
+// of a 4-bit float format; the 8-bit format decodes arithmetically).
+template <int MODE, int BITS>
+__device__ __forceinline__ float decode_field(uint32_t word, int sh, float s, const float* sG) {
+  if constexpr (MODE == Q_INT1) {
+    return ((word >> sh) & 1u) == 0u ? s : -s;
+  } else if constexpr (MODE == Q_FP && BITS == 8) {
+    return fp8_grid_value((word >> sh) & 0xFFu) * s;
+  } else if constexpr (MODE == Q_FP) {
+    return sG[(word >> sh) & ((1u << BITS) - 1u)] * s;
+  } else {
+    const int32_t c = (int32_t)(word << (32 - BITS - sh)) >> (32 - BITS);
+    return (float)c * s;
+  }
+}
+
 // 'v'-rule requantization of a float32 buffer (GEMM outputs), mxtorch.py:1372-1385.
 int requant_vec_f32(const float* x, int64_t n, int bits, int block, void* packed, int64_t packed_nbytes,
                     float* scales, int64_t n_store, void* ws, size_t ws_bytes, hipStream_t st);

@@ -1,0 +1,236 @@
+// KV-cache ring buffer for gfx950: the streaming form of kv_cache_quantizer
+// (mxtorch.py:2998-3090).
+//
+// The reference keeps a Python list of per-step mx_tensors and, per step,
+// runs k.float(), a reshape to [B*H, D], quantize(k_f, dt, D); for V (when
+// asymmetric) v_min = row min, v_f - v_min, quantize(..., D), and keeps
+// v_min as the zero point (mxtorch.py:3039-3067).  get() dequantizes every
+// step, stacks them along time and adds the zero points back to V
+// (mxtorch.py:3069-3086).
+//
+// Here the caller owns a ring of slots (codes, scales, zero points of one
+// step each).  k_kv_append quantizes one step's K and V rows straight into
+// their slot in one launch; k_kv_gather dequantizes a window of slots back
+// to float32 [rows, T, D] in time order in one launch per tensor.  Both use
+// the arithmetic of the block quantizer with block = D (one block per row).
+#include "mxk_internal.h"
+
+namespace mxk {
+
+// One row of D = 8 * LPB elements per group of LPB lanes; rows [0, rows)
+// are K's, rows [rows, 2 * rows) V's.  Every lane runs the reductions (the
+// DPP lane exchanges read the whole group); tasks past the end recompute the
+// last row and store nothing.
+template <typename T, int LPB, int MODE, int BITS>
+__global__ __launch_bounds__(256) void k_kv_append(const T* __restrict__ k, const T* __restrict__ v, int64_t rows,
+                                                   int asym, uint8_t* __restrict__ kc, float* __restrict__ ks,
+                                                   uint8_t* __restrict__ vc, float* __restrict__ vs,
+                                                   float* __restrict__ zp, float qf) {
+  constexpr int E = 8, D = E * LPB, GPW = 64 / LPB;
+  constexpr int NB = E * BITS / 8;
+  constexpr uint32_t MASK = (1u << BITS) - 1u;
+  constexpr int H = MODE == Q_FP ? (1 << (BITS - 1)) : 1;
+  __shared__ float sP[H + 1];
+  if constexpr (MODE == Q_FP) build_tables<BITS>(sP, nullptr);
+
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int g = lane / LPB, li = lane % LPB;
+  const int64_t task = ((int64_t)blockIdx.x * 4 + wave) * GPW + g;
+  const bool live = task < 2 * rows;
+  const int64_t tk = live ? task : 2 * rows - 1;
+  const bool is_v = tk >= rows;
+  const int64_t r = is_v ? tk - rows : tk;
+  float x[E];
+  load_elems<T, E>(is_v ? v : k, r * D + (int64_t)li * E, rows * D, x);
+  // V's row minimum (an exact comparison), subtracted in float32 as
+  // v_f - v_min (mxtorch.py:3062-3063)
+  float mn = x[0];
+#pragma unroll
+  for (int i = 1; i < E; ++i) mn = fminf(mn, x[i]);
+  mn = -group_max<LPB>(-mn);
+  const bool shift = is_v && asym;
+  if (shift) {
+#pragma unroll
+    for (int i = 0; i < E; ++i) x[i] = x[i] - mn;
+  }
+  float m = 0.0f;
+#pragma unroll
+  for (int i = 0; i < E; ++i) m = fmaxf(m, __builtin_fabsf(x[i]));
+  const float ap = fmaxf(group_max<LPB>(m), MXK_AMIN);
+  const BlockParams bp = block_params<MODE>(ap, qf);
+  uint32_t w[(NB + 3) / 4];
+#pragma unroll
+  for (int q = 0; q < (NB + 3) / 4; ++q) w[q] = 0u;
+#pragma unroll
+  for (int i = 0; i < E; ++i) {
+    const uint32_t f = (uint32_t)encode<MODE, BITS>(x[i], bp, qf, sP) & MASK;
+    w[(i * BITS) >> 5] |= f << ((i * BITS) & 31);
+  }
+  if (live) {
+    uint8_t* dst = is_v ? vc : kc;
+    store_bytes<NB>(dst, (r * D + (int64_t)li * E) * BITS / 8, rows * D * BITS / 8, w);
+    if (li == 0) {
+      (is_v ? vs : ks)[r] = bp.s;
+      if (shift) zp[r] = mn;
+    }
+  }
+}
+
+// out[r][j][d] for r < rows, j < T, d < D: slot (start + j) mod cap, decoded
+// as the dequantizer does (int: RN(c*s); int1: +-s; float: RN(G[c]*s)),
+// plus the slot's zero point when zp is given (RN(dq + zp), mxtorch.py:3083).
+// One thread per 32-bit word of codes.
+template <int MODE, int BITS>
+__global__ __launch_bounds__(256) void k_kv_gather(const uint8_t* __restrict__ codes, const float* __restrict__ scales,
+                                                   const float* __restrict__ zp, int64_t rows, int D, int64_t cap,
+                                                   int64_t start, int64_t T, float* __restrict__ out) {
+  constexpr int EPW = 32 / BITS;
+  constexpr int H = (MODE == Q_FP && BITS == 4) ? 16 : 1;
+  __shared__ float sG[H];
+  if constexpr (MODE == Q_FP && BITS == 4) build_tables<4>(nullptr, sG);
+  const int64_t wpr = (int64_t)D * BITS / 32;
+  const int64_t slot_bytes = rows * D * BITS / 8;
+  const int64_t total = rows * T * wpr;
+  for (int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; t < total; t += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t wd = t % wpr, rj = t / wpr;
+    const int64_t j = rj % T, r = rj / T;
+    int64_t slot = start + j;
+    if (slot >= cap) slot -= cap;
+    const uint32_t word = *reinterpret_cast<const uint32_t*>(codes + slot * slot_bytes + (r * wpr + wd) * 4);
+    const float s = scales[slot * rows + r];
+    float o[EPW];
+#pragma unroll
+    for (int e = 0; e < EPW; ++e) o[e] = decode_field<MODE, BITS>(word, e * BITS, s, sG);
+    if (zp) {
+      const float z = zp[slot * rows + r];
+#pragma unroll
+      for (int e = 0; e < EPW; ++e) o[e] = o[e] + z;
+    }
+    f32x4v* dst = reinterpret_cast<f32x4v*>(out + (r * T + j) * D + wd * EPW);
+#pragma unroll
+    for (int q = 0; q < EPW / 4; ++q) dst[q] = f32x4v{o[4 * q], o[4 * q + 1], o[4 * q + 2], o[4 * q + 3]};
+  }
+}
+
+// Quantizer rule, decode rule and max_val for the dtypes the kernels cover
+// (the rules of mxk_quantize / mxk_dequantize): 'v' rounds to integers for
+// every kind and decodes like the base dtype (mxtorch.py:1739-1752,
+// 1573-1575); Hadamard dtypes and the int32-word widths are not covered.
+static bool kv_mode(int kind, int bits, int variant, int& qmode, int& dmode, float& qf) {
+  if (variant == MXK_VAR_HADAMARD) return false;
+  const bool fl = kind == MXK_KIND_FLOAT;
+  if (fl ? !(bits == 4 || bits == 8) : !(bits == 1 || bits == 2 || bits == 4 || bits == 8)) return false;
+  if (variant == MXK_VAR_VECTOR && bits == 1) return false;
+  qf = fl ? (bits == 4 ? 6.0f : 448.0f) : (bits == 1 ? 1.0f : (float)((1u << (bits - 1)) - 1u));
+  dmode = fl ? Q_FP : (bits == 1 ? Q_INT1 : Q_INT);
+  qmode = variant == MXK_VAR_VECTOR ? Q_VEC : dmode;
+  return true;
+}
+
+template <typename T, int LPB>
+static void launch_append_t(int mode, int bits, const void* k, const void* v, int64_t rows, int asym, void* kc,
+                            float* ks, void* vc, float* vs, float* zp, float qf, hipStream_t st) {
+  const int64_t per_block = 4 * (64 / LPB);
+  const dim3 grid((unsigned)ceil_div(2 * rows, per_block));
+  const T* kt = reinterpret_cast<const T*>(k);
+  const T* vt = reinterpret_cast<const T*>(v);
+  uint8_t* kb = reinterpret_cast<uint8_t*>(kc);
+  uint8_t* vb = reinterpret_cast<uint8_t*>(vc);
+#define MXK_KVA(MODE, BITS)                                                                                    \
+  hipLaunchKernelGGL((k_kv_append<T, LPB, MODE, BITS>), grid, dim3(256), 0, st, kt, vt, rows, asym, kb, ks, vb, vs, \
+                     zp, qf)
+  if (mode == Q_FP) {
+    if (bits == 4) MXK_KVA(Q_FP, 4);
+    else MXK_KVA(Q_FP, 8);
+  } else if (mode == Q_INT1) {
+    MXK_KVA(Q_INT1, 1);
+  } else if (mode == Q_VEC) {
+    if (bits == 2) MXK_KVA(Q_VEC, 2);
+    else if (bits == 4) MXK_KVA(Q_VEC, 4);
+    else MXK_KVA(Q_VEC, 8);
+  } else {
+    if (bits == 2) MXK_KVA(Q_INT, 2);
+    else if (bits == 4) MXK_KVA(Q_INT, 4);
+    else MXK_KVA(Q_INT, 8);
+  }
+#undef MXK_KVA
+}
+
+template <typename T>
+static int launch_append(int head_dim, int mode, int bits, const void* k, const void* v, int64_t rows, int asym,
+                         void* kc, float* ks, void* vc, float* vs, float* zp, float qf, hipStream_t st) {
+  if (head_dim == 64) launch_append_t<T, 8>(mode, bits, k, v, rows, asym, kc, ks, vc, vs, zp, qf, st);
+  else if (head_dim == 128) launch_append_t<T, 16>(mode, bits, k, v, rows, asym, kc, ks, vc, vs, zp, qf, st);
+  else launch_append_t<T, 32>(mode, bits, k, v, rows, asym, kc, ks, vc, vs, zp, qf, st);
+  return check_launch("kv_append");
+}
+
+}  // namespace mxk
+
+using namespace mxk;
+
+extern "C" {
+
+int mxk_kv_append(const void* k, const void* v, int x_type, int64_t rows, int head_dim, int kind, int bits,
+                  int variant, int asymmetric_v, void* k_codes, float* k_scales, void* v_codes, float* v_scales,
+                  float* v_zero_point, void* stream) {
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  int mode = 0, dmode = 0;
+  float qf = 0.0f;
+  if (rows <= 0) return fail(MXK_EINVAL, "kv_append: rows must be positive");
+  if (!(head_dim == 64 || head_dim == 128 || head_dim == 256))
+    return fail(MXK_EUNSUPPORTED, "kv_append: head_dim must be 64, 128 or 256");
+  if (!kv_mode(kind, bits, variant, mode, dmode, qf))
+    return fail(MXK_EUNSUPPORTED, "kv_append: int widths 1, 2, 4, 8 and float 4, 8 (base or 'v') only");
+  if (!k || !v || !k_codes || !k_scales || !v_codes || !v_scales || (asymmetric_v && !v_zero_point))
+    return fail(MXK_EINVAL, "kv_append: null pointer");
+  if (!aligned16(k) || !aligned16(v)) return fail(MXK_EINVAL, "kv_append: k and v must be 16-byte aligned");
+  if (rows * head_dim * bits / 8 >= ((int64_t)1 << 40)) return fail(MXK_EINVAL, "kv_append: slot too large");
+  if (x_type == MXK_IN_F32)
+    return launch_append<float>(head_dim, mode, bits, k, v, rows, asymmetric_v, k_codes, k_scales, v_codes,
+                                v_scales, v_zero_point, qf, st);
+  if (x_type == MXK_IN_F16)
+    return launch_append<__half>(head_dim, mode, bits, k, v, rows, asymmetric_v, k_codes, k_scales, v_codes,
+                                 v_scales, v_zero_point, qf, st);
+  if (x_type == MXK_IN_BF16)
+    return launch_append<hip_bfloat16>(head_dim, mode, bits, k, v, rows, asymmetric_v, k_codes, k_scales,
+                                       v_codes, v_scales, v_zero_point, qf, st);
+  return fail(MXK_EINVAL, "kv_append: unknown x_type");
+}
+
+int mxk_kv_gather(const void* codes, const float* scales, const float* zero_point, int64_t rows, int head_dim,
+                  int kind, int bits, int variant, int64_t capacity, int64_t start, int64_t count, float* out,
+                  void* stream) {
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  int qmode = 0, mode = 0;
+  float qf = 0.0f;
+  if (rows <= 0 || capacity <= 0 || count <= 0 || count > capacity || start < 0 || start >= capacity)
+    return fail(MXK_EINVAL, "kv_gather: need rows > 0 and 0 <= start < capacity, 0 < count <= capacity");
+  if (!(head_dim == 64 || head_dim == 128 || head_dim == 256))
+    return fail(MXK_EUNSUPPORTED, "kv_gather: head_dim must be 64, 128 or 256");
+  if (!kv_mode(kind, bits, variant, qmode, mode, qf))
+    return fail(MXK_EUNSUPPORTED, "kv_gather: int widths 1, 2, 4, 8 and float 4, 8 (base or 'v') only");
+  if (!codes || !scales || !out) return fail(MXK_EINVAL, "kv_gather: null pointer");
+  if ((reinterpret_cast<uintptr_t>(codes) & 3u) != 0 || !aligned16(out))
+    return fail(MXK_EINVAL, "kv_gather: codes must be 4-byte and out 16-byte aligned");
+  const uint8_t* c = reinterpret_cast<const uint8_t*>(codes);
+  const int64_t total = rows * count * ((int64_t)head_dim * bits / 32);
+  const dim3 grid((unsigned)std::min<int64_t>(ceil_div(total, 256), (int64_t)num_cus() * 16));
+#define MXK_KVG(MODE, BITS)                                                                                       \
+  hipLaunchKernelGGL((k_kv_gather<MODE, BITS>), grid, dim3(256), 0, st, c, scales, zero_point, rows, head_dim, \
+                     capacity, start, count, out)
+  if (mode == Q_FP) {
+    if (bits == 4) MXK_KVG(Q_FP, 4);
+    else MXK_KVG(Q_FP, 8);
+  } else if (mode == Q_INT1) {
+    MXK_KVG(Q_INT1, 1);
+  } else {
+    if (bits == 2) MXK_KVG(Q_INT, 2);
+    else if (bits == 4) MXK_KVG(Q_INT, 4);
+    else MXK_KVG(Q_INT, 8);
+  }
+#undef MXK_KVG
+  return check_launch("kv_gather");
+}
+
+}  // extern "C"

@@ -54,42 +54,6 @@ int num_cus() {
   return cache[dev];
 }
 
-// ---------------------------------------------------------------- per-block params
-struct BlockParams {
-  float s;    // stored scale
-  float mul;  // Q_INT: inv ; Q_VEC/Q_FP: RN(1/s)
-};
-
-template <int MODE>
-__device__ __forceinline__ BlockParams block_params(float ap, float qf) {
-  BlockParams bp;
-  if constexpr (MODE == Q_INT) {
-    float r = 1.0f / ap;
-    bp.mul = r * qf;
-    bp.s = 1.0f / bp.mul;
-  } else if constexpr (MODE == Q_VEC) {
-    bp.s = ap / qf;
-    bp.mul = 1.0f / bp.s;
-  } else {  // Q_INT1, Q_FP
-    bp.s = ap;
-    bp.mul = 1.0f / ap;
-  }
-  return bp;
-}
-
-template <int MODE, int BITS>
-__device__ __forceinline__ int encode(float v, const BlockParams& bp, float qf, const float* P) {
-  if constexpr (MODE == Q_INT) {
-    return (int)rne(fminf(fmaxf(v * bp.mul, -qf), qf));
-  } else if constexpr (MODE == Q_INT1) {
-    return v >= 0.0f ? 0 : 1;
-  } else if constexpr (MODE == Q_VEC) {
-    return (int)rne(fminf(fmaxf(div_rn(v, bp.s, bp.mul), -qf), qf));
-  } else {
-    return bucket<BITS>(div_rn(v, bp.s, bp.mul), P);
-  }
-}
-
 // ---------------------------------------------------------------- fast quantize
 template <typename T, int E, int LPB, int MODE, int BITS>
 __global__ __launch_bounds__(256) void k_quant_fast(const T* __restrict__ x, int64_t n, int64_t nb,
@@ -462,20 +426,6 @@ __global__ __launch_bounds__(256) void k_dequant(const uint8_t* __restrict__ pac
 // takes U slots a grid-stride apart per iteration, loads first.  Slots that
 // cross the end of the data or of the packed buffer take the element path.
 template <int MODE, int BITS>
-__device__ __forceinline__ float decode_field(uint32_t word, int sh, float s, const float* sG) {
-  if constexpr (MODE == Q_INT1) {
-    return ((word >> sh) & 1u) == 0u ? s : -s;
-  } else if constexpr (MODE == Q_FP && BITS == 8) {
-    return fp8_grid_value((word >> sh) & 0xFFu) * s;
-  } else if constexpr (MODE == Q_FP) {
-    return sG[(word >> sh) & ((1u << BITS) - 1u)] * s;
-  } else {
-    const int32_t c = (int32_t)(word << (32 - BITS - sh)) >> (32 - BITS);
-    return (float)c * s;
-  }
-}
-
-template <int MODE, int BITS>
 __global__ __launch_bounds__(256) void k_dequant_fast(const uint8_t* __restrict__ packed, int64_t packed_nbytes,
                                                       const float* __restrict__ scales, int64_t nb, int64_t n,
                                                       int block, float* __restrict__ out) {
@@ -611,16 +561,22 @@ static int grid_for(int64_t work_items, int per_block) {
   return (int)std::max<int64_t>(1, std::min<int64_t>(blocks, cap));
 }
 
+// mx_dtype.max_val (mxtorch.py:509-523): q for int widths (1 for int1),
+// the format maximum for float widths.  Only the 'v' rule uses it for
+// float dtypes.
 static float qmax_for(int kind, int bits, int variant) {
-  (void)kind;
   (void)variant;
+  if (kind == MXK_KIND_FLOAT) return bits == 4 ? 6.0f : 448.0f;
   if (bits == 1) return 1.0f;
   return (float)((1u << (bits - 1)) - 1u);
 }
-
+// The quantizer rule: 'v' rounds to integers clamped at max_val for every
+// kind, float dtypes included (mxtorch.py:1739-1752, codes packed as ints);
+// otherwise float dtypes bucketize into the grid and int dtypes use
+// _quant_int (int1: sign codes).
 static int mode_for(int kind, int bits, int variant) {
-  if (kind == MXK_KIND_FLOAT) return Q_FP;
   if (variant == MXK_VAR_VECTOR) return Q_VEC;
+  if (kind == MXK_KIND_FLOAT) return Q_FP;
   if (bits == 1) return Q_INT1;
   return Q_INT;
 }
