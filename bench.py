@@ -250,6 +250,40 @@ def bench_kv(qa, reps):
     return out
 
 
+def bench_kv_stream(qa, steps):
+    """kv_cache_quantizer streaming at config 5's shape: per-step append of
+    K, V [8, 32, 1, 128] fp16 (one fused launch into the ring), then get()
+    over 4096 steps (one gather launch per tensor)."""
+    dev = torch.device("cuda:0")
+    B, H, D, T = 8, 32, 128, 4096
+    rows = B * H
+    out = {}
+    ks = torch.randn(steps, B, H, 1, D, generator=gen(11, "cuda"), device=dev).half()
+    vs = torch.randn(steps, B, H, 1, D, generator=gen(12, "cuda"), device=dev).half()
+    for name in ("int8dv", "int4d"):
+        dt = qa.get_mx_dtype(name)
+        cache = qa.kv_cache_quantizer(n_heads=H, head_dim=D, dtype=name, max_seq_len=T)
+        # fill the ring to T steps (eager), so that appends below evict and get() sees T steps
+        for t in range(T):
+            cache.append_kv(ks[t % steps], vs[t % steps])
+        i = [0]
+
+        def step():
+            cache.append_kv(ks[i[0] % steps], vs[i[0] % steps])
+            i[0] += 1
+
+        t_app = graph_time(step, steps, 2)
+        t_get = graph_time(lambda: cache.get(), 3, 1, repeats=3)
+        n = rows * T * D
+        code_b = n * dt.bits // 8
+        get_algo = 2 * (code_b + rows * T * 4 + n * 4) + rows * T * 4  # codes, scales, out (K and V) + V zero points
+        app_algo = 2 * (rows * D * 2 + rows * D * dt.bits // 8 + rows * 4) + rows * 4
+        out[name] = {"append_us_per_step": round(t_app * 1e6, 3), "append_bytes": app_algo,
+                     "get_us": round(t_get * 1e6, 2), "get_GBs": round(get_algo / t_get / 1e9, 1),
+                     "get_frac": round(get_algo / t_get / 1e9 / HBM_PEAK_GBS, 4)}
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -257,7 +291,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-extras", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--only", default="", help="comma list of extras: quant,gemm,kv,small")
+    ap.add_argument("--only", default="", help="comma list of extras: quant,gemm,kv,kvstream,small")
     ap.add_argument("--eager", action="store_true", help="no graph capture (for rocprofv3 --pmc runs)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a plain 512 MiB device copy (the reference kernel for HBM counter scaling)")
@@ -317,6 +351,8 @@ def main():
             extras["config4_quant_sweep_2e28"] = bench_quant_sweep(qa, 5)
         if not only or "kv" in only:
             extras["config5_kv_8x32x4096x128_fp16"] = bench_kv(qa, 5)
+        if not only or "kvstream" in only:
+            extras["kv_ring_stream_8x32x128_T4096"] = bench_kv_stream(qa, 64)
         line["extras"] = extras
     print(json.dumps(line))
 

@@ -79,36 +79,49 @@ __global__ __launch_bounds__(256) void k_kv_append(const T* __restrict__ k, cons
 // out[r][j][d] for r < rows, j < T, d < D: slot (start + j) mod cap, decoded
 // as the dequantizer does (int: RN(c*s); int1: +-s; float: RN(G[c]*s)),
 // plus the slot's zero point when zp is given (RN(dq + zp), mxtorch.py:3083).
-// One thread per 32-bit word of codes.
+// Tiles of KV_RT rows x KV_JT steps per block (row tiles on grid-x, step
+// tiles on grid-y, both looped): each thread writes float4s (4 codes, read
+// from the 32-bit word holding them); a tile reads KV_RT consecutive rows of
+// each of its slots and writes KV_RT runs of KV_JT * D contiguous floats.
+// rows * D * BITS < 2^35 and T < 2^31 (host-checked).
+#define KV_RT 4
+#define KV_JT 8
 template <int MODE, int BITS>
 __global__ __launch_bounds__(256) void k_kv_gather(const uint8_t* __restrict__ codes, const float* __restrict__ scales,
                                                    const float* __restrict__ zp, int64_t rows, int D, int64_t cap,
                                                    int64_t start, int64_t T, float* __restrict__ out) {
-  constexpr int EPW = 32 / BITS;
   constexpr int H = (MODE == Q_FP && BITS == 4) ? 16 : 1;
   __shared__ float sG[H];
   if constexpr (MODE == Q_FP && BITS == 4) build_tables<4>(nullptr, sG);
-  const int64_t wpr = (int64_t)D * BITS / 32;
-  const int64_t slot_bytes = rows * D * BITS / 8;
-  const int64_t total = rows * T * wpr;
-  for (int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; t < total; t += (int64_t)gridDim.x * blockDim.x) {
-    const int64_t wd = t % wpr, rj = t / wpr;
-    const int64_t j = rj % T, r = rj / T;
-    int64_t slot = start + j;
-    if (slot >= cap) slot -= cap;
-    const uint32_t word = *reinterpret_cast<const uint32_t*>(codes + slot * slot_bytes + (r * wpr + wd) * 4);
-    const float s = scales[slot * rows + r];
-    float o[EPW];
+  const uint32_t qpr = (uint32_t)D / 4;  // float4s per (row, step): 16, 32 or 64
+  const int lq = 31 - __builtin_clz(qpr);
+  const int ljq = lq + 3;                // log2(KV_JT * qpr)
+  const uint32_t tile = KV_RT * KV_JT * qpr;
+  const int64_t row_bytes = (int64_t)D * BITS / 8, slot_bytes = rows * row_bytes;
+  const int64_t ntr = (rows + KV_RT - 1) / KV_RT, ntj = (T + KV_JT - 1) / KV_JT;
+  for (int64_t tj = blockIdx.y; tj < ntj; tj += gridDim.y) {
+    for (int64_t tr = blockIdx.x; tr < ntr; tr += gridDim.x) {
+      for (uint32_t t = threadIdx.x; t < tile; t += blockDim.x) {
+        const uint32_t rr = t >> ljq, jj = (t >> lq) & (KV_JT - 1), q = t & (qpr - 1);
+        const int64_t r = tr * KV_RT + rr, j = tj * KV_JT + jj;
+        if (r >= rows || j >= T) continue;
+        int64_t slot = start + j;
+        if (slot >= cap) slot -= cap;
+        const int64_t bit0 = ((int64_t)r * D + 4 * q) * BITS;
+        const uint32_t word = *reinterpret_cast<const uint32_t*>(codes + slot * slot_bytes + (bit0 >> 5) * 4);
+        const int sh0 = (int)(bit0 & 31);
+        const float s = scales[slot * rows + r];
+        float o[4];
 #pragma unroll
-    for (int e = 0; e < EPW; ++e) o[e] = decode_field<MODE, BITS>(word, e * BITS, s, sG);
-    if (zp) {
-      const float z = zp[slot * rows + r];
+        for (int e = 0; e < 4; ++e) o[e] = decode_field<MODE, BITS>(word, sh0 + e * BITS, s, sG);
+        if (zp) {
+          const float z = zp[slot * rows + r];
 #pragma unroll
-      for (int e = 0; e < EPW; ++e) o[e] = o[e] + z;
+          for (int e = 0; e < 4; ++e) o[e] = o[e] + z;
+        }
+        *reinterpret_cast<f32x4v*>(out + ((r * T + j) << (lq + 2)) + q * 4) = f32x4v{o[0], o[1], o[2], o[3]};
+      }
     }
-    f32x4v* dst = reinterpret_cast<f32x4v*>(out + (r * T + j) * D + wd * EPW);
-#pragma unroll
-    for (int q = 0; q < EPW / 4; ++q) dst[q] = f32x4v{o[4 * q], o[4 * q + 1], o[4 * q + 2], o[4 * q + 3]};
   }
 }
 
@@ -213,9 +226,11 @@ int mxk_kv_gather(const void* codes, const float* scales, const float* zero_poin
   if (!codes || !scales || !out) return fail(MXK_EINVAL, "kv_gather: null pointer");
   if ((reinterpret_cast<uintptr_t>(codes) & 3u) != 0 || !aligned16(out))
     return fail(MXK_EINVAL, "kv_gather: codes must be 4-byte and out 16-byte aligned");
+  if (rows * head_dim * bits >= ((int64_t)1 << 35) || capacity >= ((int64_t)1 << 31))
+    return fail(MXK_EINVAL, "kv_gather: ring too large");
   const uint8_t* c = reinterpret_cast<const uint8_t*>(codes);
-  const int64_t total = rows * count * ((int64_t)head_dim * bits / 32);
-  const dim3 grid((unsigned)std::min<int64_t>(ceil_div(total, 256), (int64_t)num_cus() * 16));
+  const dim3 grid((unsigned)std::min<int64_t>(ceil_div(rows, KV_RT), 65535),
+                  (unsigned)std::min<int64_t>(ceil_div(count, KV_JT), 65535));
 #define MXK_KVG(MODE, BITS)                                                                                       \
   hipLaunchKernelGGL((k_kv_gather<MODE, BITS>), grid, dim3(256), 0, st, c, scales, zero_point, rows, head_dim, \
                      capacity, start, count, out)
