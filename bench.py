@@ -250,6 +250,31 @@ def bench_kv(qa, reps):
     return out
 
 
+def bench_elementwise(qa, reps):
+    """Quantized element-wise add / mul (mxtorch.py:5321-5497) on 2^28
+    elements, block 128: packed codes and scales in, packed codes and scales
+    out (one launch)."""
+    dev = torch.device("cuda:0")
+    n = 1 << 28
+    out = {}
+    x = torch.randn(n, generator=gen(13, "cuda"), device=dev)
+    y = torch.randn(n, generator=gen(14, "cuda"), device=dev) * 0.3
+    for name in ("int8d", "int4d"):
+        dt = qa.get_mx_dtype(name)
+        A = qa.mx_tensor.quantize(x, dt, 128)
+        B = qa.mx_tensor.quantize(y, dt, 128)
+        nb = n // 128
+        for op in ("add", "mul"):
+            ob = dt.bits if op == "add" else qa.dtypes.qmul_output_dtype(dt).bits
+            algo = n * (2 * dt.bits + ob) // 8 + 3 * nb * 4
+            f = (lambda: A + B) if op == "add" else (lambda: A * B)
+            t = graph_time(f, reps, 1, repeats=3)
+            out[f"{name}_{op}"] = {"us": round(t * 1e6, 2), "GBs": round(algo / t / 1e9, 1),
+                                   "frac": round(algo / t / 1e9 / HBM_PEAK_GBS, 4), "bytes": algo}
+        del A, B
+    return out
+
+
 def bench_kv_stream(qa, steps):
     """kv_cache_quantizer streaming at config 5's shape: per-step append of
     K, V [8, 32, 1, 128] fp16 (one fused launch into the ring), then get()
@@ -291,7 +316,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-extras", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--only", default="", help="comma list of extras: quant,gemm,kv,kvstream,small")
+    ap.add_argument("--only", default="", help="comma list of extras: quant,gemm,kv,kvstream,elementwise,small")
     ap.add_argument("--eager", action="store_true", help="no graph capture (for rocprofv3 --pmc runs)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a plain 512 MiB device copy (the reference kernel for HBM counter scaling)")
@@ -351,6 +376,8 @@ def main():
             extras["config4_quant_sweep_2e28"] = bench_quant_sweep(qa, 5)
         if not only or "kv" in only:
             extras["config5_kv_8x32x4096x128_fp16"] = bench_kv(qa, 5)
+        if not only or "elementwise" in only:
+            extras["elementwise_2e28_block128"] = bench_elementwise(qa, 5)
         if not only or "kvstream" in only:
             extras["kv_ring_stream_8x32x128_T4096"] = bench_kv_stream(qa, 64)
         line["extras"] = extras

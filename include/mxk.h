@@ -198,6 +198,31 @@ int mxk_kv_gather(const void* codes, const float* scales, const float* zero_poin
                   int kind, int bits, int variant, int64_t capacity, int64_t start, int64_t count, float* out,
                   void* stream);
 
+/* Workspace bytes mxk_qelementwise needs (0 when the output is packed in
+ * the same pass: block <= 256, out_bits in {1, 2, 4, 8, 16}, block*out_bits
+ * a multiple of 32). */
+size_t mxk_qelementwise_workspace(int op, int64_t n, int64_t nb, int block, int bits, int out_bits);
+
+/* Quantized element-wise arithmetic on packed operands (no float element
+ * values are formed beyond the reference's own):
+ *  op 0 add, 1 sub: the CPU branches of _dispatch_qadd / _dispatch_qsub
+ *       (mxtorch.py:5397-5401, 5425-5431) around _qscale_add
+ *       (mxtorch.py:1186-1256);
+ *  op 2 mul: _dispatch_qmul's CPU branch (mxtorch.py:5489-5497) around
+ *       _qscale_mul (mxtorch.py:1259-1296);
+ *  op 3 neg: mx_tensor.__neg__ (mxtorch.py:6177-6193), b and the scales
+ *       unused (the caller copies a's scales).
+ *  Both operands' first n codes are unpacked with `bits` (a's width,
+ *  bits in {2..8, 16}; neg also 1) and sign-extended; codes past n are 0.
+ *  Outputs: c_packed = the nb*block result codes packed with out_bits
+ *  (mxk_packed_nbytes(out_bits, nb*block) bytes; neg: the n codes, or all
+ *  a_nbytes codes for 8-bit operands, with the same width), c_scales [nb].
+ *  block <= 256.  Packed buffers 4-byte aligned. */
+int mxk_qelementwise(int op, const void* a_packed, int64_t a_nbytes, const float* a_scales, const void* b_packed,
+                     int64_t b_nbytes, const float* b_scales, int64_t n, int64_t nb, int block, int bits,
+                     int out_bits, void* c_packed, int64_t c_nbytes, float* c_scales, void* workspace,
+                     size_t workspace_nbytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -549,3 +549,121 @@ def kv_get(steps, name: str, head_dim: int, n_heads: int):
         v_all = v_all + torch.stack(zps, dim=1).unsqueeze(-1)
     BH, _, D = k_all.shape
     return k_all.reshape(-1, n_heads, T, D), v_all.reshape(-1, n_heads, T, D)
+
+
+# ---------------------------------------------------------------------------
+# Quantized element-wise arithmetic  (mxtorch.py:1186-1296, 5321-5497, 6177-6193)
+# ---------------------------------------------------------------------------
+def resolve_mixed(a_name: str, b_name: str) -> str:
+    """_resolve_mixed (mxtorch.py:584-598): mode u if either is u, the
+    narrower width, float if either is float, the higher-priority variant
+    (h > v > s > b > '')."""
+    ak, ab, am, av = parse_dtype(a_name)
+    bk, bb, bm, bv = parse_dtype(b_name)
+    prio = {"h": 4, "v": 3, "s": 2, "b": 1, "": 0}
+    mode = "u" if (am == "u" or bm == "u") else "d"
+    bits = min(ab, bb)
+    kind = "float" if (ak == "float" or bk == "float") else "int"
+    variant = av if prio.get(av, 0) >= prio.get(bv, 0) else bv
+    bits = min(_VALID_BITS, key=lambda x: abs(x - bits))
+    return f"{kind}{bits}{mode}{variant}"
+
+
+def qmul_out_name(name: str) -> str:
+    """Output dtype of _dispatch_qmul (mxtorch.py:5442-5445): {kind}{w}d with
+    w the valid width nearest min(2*bits, 16), ties to the wider."""
+    kind, bits, _, _ = parse_dtype(name)
+    ideal = min(bits * 2, 16)
+    w = min(_VALID_BITS, key=lambda x: (abs(x - ideal), -x))
+    return f"{kind}{w}d"
+
+
+def _pad_blocks(codes: Tensor, nb: int, block: int) -> Tensor:
+    n = codes.numel()
+    if n < nb * block:
+        codes = torch.cat([codes, torch.zeros(nb * block - n, dtype=codes.dtype)])
+    return codes
+
+
+def qscale_add(a_codes: Tensor, a_scales: Tensor, b_codes: Tensor, b_scales: Tensor,
+               bits: int, block: int) -> Tuple[Tensor, Tensor]:
+    """_qscale_add (mxtorch.py:1186-1256): per block, integer-domain add when
+    the scales are within 2:1 (rescaled to the larger scale, doubled once on
+    overflow), else dequantize, add and requantize with the 'v' rule."""
+    max_int = float((1 << (bits - 1)) - 1)
+    nb = a_scales.numel()
+    ac = _pad_blocks(a_codes, nb, block).reshape(nb, block).float()
+    bc = _pad_blocks(b_codes, nb, block).reshape(nb, block).float()
+    sa = a_scales.unsqueeze(1)
+    sb = b_scales.unsqueeze(1)
+    ratio = torch.max(sa, sb) / torch.min(sa, sb).clamp(min=1e-30)
+    use_int = (ratio <= 2.0).squeeze(1)
+    out_codes = torch.zeros(nb * block, dtype=torch.int32)
+    out_scales = torch.zeros(nb, dtype=torch.float32)
+    if use_int.any():
+        idx = use_int.nonzero(as_tuple=True)[0]
+        sc_i = torch.maximum(sa[idx], sb[idx])
+        ac_r = (ac[idx] * (sa[idx] / sc_i)).round_()
+        bc_r = (bc[idx] * (sb[idx] / sc_i)).round_()
+        c_w = ac_r + bc_r
+        overflow = c_w.abs().amax(dim=1) > max_int
+        if overflow.any():
+            sc_i = sc_i.clone()
+            sc_i[overflow] *= 2.0
+            ac_r = (ac[idx] * (sa[idx] / sc_i)).round_()
+            bc_r = (bc[idx] * (sb[idx] / sc_i)).round_()
+            c_w = ac_r + bc_r
+        out_codes.view(nb, block)[idx] = c_w.clamp(-max_int, max_int).to(torch.int32)
+        out_scales[idx] = sc_i.squeeze(1)
+    if (~use_int).any():
+        idx2 = (~use_int).nonzero(as_tuple=True)[0]
+        sum_f = ac[idx2] * sa[idx2] + bc[idx2] * sb[idx2]
+        sc_f = sum_f.abs().amax(dim=1).clamp(min=1e-12) / max_int
+        c_f = (sum_f / sc_f.unsqueeze(1)).clamp(-max_int, max_int).round_()
+        out_codes.view(nb, block)[idx2] = c_f.to(torch.int32)
+        out_scales[idx2] = sc_f
+    return out_codes, out_scales
+
+
+def qscale_mul(a_codes: Tensor, a_scales: Tensor, b_codes: Tensor, b_scales: Tensor,
+               bits: int, block: int) -> Tuple[Tensor, Tensor]:
+    """_qscale_mul (mxtorch.py:1259-1296): codes rne(clamp(RN(RN(a*b)/max_int))),
+    scales RN(RN(sa*sb)*max_int)."""
+    max_int = float((1 << (bits - 1)) - 1)
+    nb = a_scales.numel()
+    ac = _pad_blocks(a_codes, nb, block).reshape(nb, block).float()
+    bc = _pad_blocks(b_codes, nb, block).reshape(nb, block).float()
+    prod = ac * bc
+    prod_scales = a_scales * b_scales * max_int
+    c_codes = (prod / max_int).clamp(-max_int, max_int).round().to(torch.int32)
+    return c_codes.reshape(-1), prod_scales
+
+
+def dispatch_qelementwise(op: str, a_packed: Tensor, a_scales: Tensor, a_name: str, b_packed: Tensor,
+                          b_scales: Tensor, b_name: str, n: int, block: int):
+    """CPU branches of _dispatch_qadd / _dispatch_qsub / _dispatch_qmul
+    (mxtorch.py:5397-5401, 5425-5431, 5489-5497): both operands unpacked with
+    a's width, the codes packed with the output dtype's width.  Returns
+    (packed, scales, out_name)."""
+    _, bits, _, _ = parse_dtype(a_name)
+    ac = unpack_auto(a_packed, bits, n).to(torch.int32)
+    bc = unpack_auto(b_packed, bits, n).to(torch.int32)
+    if op == "mul":
+        out = qmul_out_name(a_name)
+        c, s = qscale_mul(ac, a_scales, bc, b_scales, bits, block)
+    else:
+        out = resolve_mixed(a_name, b_name)
+        c, s = qscale_add(ac, a_scales, (-bc).to(torch.int32) if op == "sub" else bc, b_scales, bits, block)
+    return pack_auto(c, parse_dtype(out)[1]), s, out
+
+
+def negate(packed: Tensor, scales: Tensor, name: str, n: int) -> Tuple[Tensor, Tensor]:
+    """mx_tensor.__neg__ (mxtorch.py:6177-6193): 8-bit codes negate every
+    stored byte (clamped to +-127); other widths unpack n codes, negate,
+    clamp and repack.  Scales are copied."""
+    _, bits, _, _ = parse_dtype(name)
+    max_i = (1 << (bits - 1)) - 1
+    if bits == 8:
+        return (-packed.to(torch.int16)).clamp(-max_i, max_i).to(torch.int8), scales.clone()
+    codes = unpack_auto(packed, bits, n).to(torch.int32)
+    return pack_auto((-codes).clamp(-max_i, max_i).to(torch.int32), bits), scales.clone()

@@ -50,6 +50,9 @@ SIGNATURES = {
                               c_vp, c_vp]),
     "mxk_kv_gather": (c_int, [c_vp, c_vp, c_vp, c_i64, c_int, c_int, c_int, c_int, c_i64, c_i64, c_i64, c_vp,
                               c_vp]),
+    "mxk_qelementwise_workspace": (c_sz, [c_int, c_i64, c_i64, c_int, c_int, c_int]),
+    "mxk_qelementwise": (c_int, [c_int, c_vp, c_i64, c_vp, c_vp, c_i64, c_vp, c_i64, c_i64, c_int, c_int, c_int,
+                                 c_vp, c_i64, c_vp, c_vp, c_sz, c_vp]),
 }
 
 

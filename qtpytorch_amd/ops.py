@@ -303,3 +303,44 @@ def float_grid(bits: int) -> Tuple[Tensor, Tensor]:
     m = torch.empty((1 << bits) - 1, dtype=torch.float32)
     L.check(L.lib().mxk_float_grid(bits, g.data_ptr(), m.data_ptr()), "float_grid")
     return g, m
+
+
+_ELEM_OPS = {"add": 0, "sub": 1, "mul": 2, "neg": 3}
+
+
+def qelementwise(op: str, a_packed: Tensor, a_scales: Tensor, b_packed: Optional[Tensor],
+                 b_scales: Optional[Tensor], n: int, block: int, bits: int, out_bits: int):
+    """Packed element-wise arithmetic: the CPU branches of _dispatch_qadd /
+    _dispatch_qsub / _dispatch_qmul (mxtorch.py:5397-5401, 5425-5431,
+    5489-5497; _qscale_add / _qscale_mul, mxtorch.py:1186-1296) and the code
+    negation of mx_tensor.__neg__ (mxtorch.py:6177-6193) on the GPU.
+
+    Both operands' first n codes are read with `bits` (a's width).  Returns
+    (packed, scales): for add/sub/mul the nb*block result codes packed with
+    out_bits and [nb] scales; for neg the negated codes with a's width (every
+    stored byte for 8-bit codes) and a copy of a's scales."""
+    code = _ELEM_OPS[op]
+    ts = [a_packed, a_scales] + ([] if op == "neg" else [b_packed, b_scales])
+    dev = L.require_gpu(*ts)
+    nb = a_scales.numel()
+    ap = a_packed.contiguous()
+    if op == "neg":
+        count = ap.numel() * ap.element_size() if bits == 8 else n
+        out = packed_storage(bits, count, dev)
+        scales = a_scales.clone()
+        bp = bsc = None
+    else:
+        out = packed_storage(out_bits, nb * block, dev)
+        scales = torch.empty(nb, dtype=torch.float32, device=dev)
+        bp, bsc = b_packed.contiguous(), b_scales.contiguous().float()
+    asc = a_scales.contiguous().float()
+    lib = L.lib()
+    ws_bytes = lib.mxk_qelementwise_workspace(code, n, nb, block, bits, out_bits)
+    ws = _workspace(ws_bytes, dev)
+    with torch.cuda.device(dev):
+        rc = lib.mxk_qelementwise(code, ap.data_ptr(), ap.numel() * ap.element_size(), asc.data_ptr(),
+                                  L.ptr(bp), 0 if bp is None else bp.numel() * bp.element_size(), L.ptr(bsc),
+                                  n, nb, block, bits, out_bits, out.data_ptr(), out.numel() * out.element_size(),
+                                  scales.data_ptr() if op != "neg" else 0, L.ptr(ws), ws_bytes, L.stream_of(ap))
+    L.check(rc, f"qelementwise({op}, bits={bits}, n={n}, block={block})")
+    return out, scales

@@ -25,7 +25,7 @@ import torch
 from torch.utils._pytree import tree_map
 
 from . import ops
-from .dtypes import get_mx_dtype, matmul_output_dtype, mx_dtype
+from .dtypes import get_mx_dtype, matmul_output_dtype, mx_dtype, qmul_output_dtype, resolve_mixed
 
 Tensor = torch.Tensor
 
@@ -124,6 +124,17 @@ class mx_tensor(torch.Tensor):
                 return getter(args[0])
         if func in _MM_FUNCS and len(args) >= 2 and isinstance(args[0], mx_tensor) and isinstance(args[1], mx_tensor):
             return _mx_mm(args[0], args[1])
+        if func in _POINTWISE and len(args) >= 1 and not kwargs.get("out"):
+            a = args[0]
+            b = args[1] if len(args) > 1 else kwargs.get("other", 1)
+            if isinstance(a, mx_tensor) or isinstance(b, mx_tensor):
+                # the reference hands _binary_op a wrapper whose name is not
+                # add/sub/mul, so two same-shape operands take its
+                # dequantize -> op -> requantize branch (mxtorch.py:6807-6819)
+                def _pw(x, y, _f=func):
+                    with torch._C.DisableTorchFunctionSubclass():
+                        return _f(_unwrap(x), _unwrap(y))
+                return _binary_op(a, b, _pw)
         return _fallback(func, args, kwargs)
 
     # ---- arithmetic sugar ----
@@ -133,8 +144,33 @@ class mx_tensor(torch.Tensor):
     def __rmatmul__(self, o):
         return _mx_mm(o, self)
 
+    def __add__(self, o):
+        return _binary_op(self, o, torch.add)
+
+    def __radd__(self, o):
+        return _binary_op(o, self, torch.add)
+
+    def __sub__(self, o):
+        return _binary_op(self, o, torch.sub)
+
+    def __rsub__(self, o):
+        return _binary_op(o, self, torch.sub)
+
+    def __mul__(self, o):
+        return _binary_op(self, o, torch.mul)
+
+    def __rmul__(self, o):
+        return _binary_op(o, self, torch.mul)
+
+    def __truediv__(self, o):
+        return _binary_op(self, o, torch.div)
+
     def __neg__(self):
-        return mx_tensor.quantize(-self.dequantize(), self._mx_dtype, self._mx_block)
+        """Code negation, scales unchanged (mxtorch.py:6177-6193)."""
+        bits = self._mx_dtype.bits
+        packed, scales = ops.qelementwise("neg", self._mx_packed, self._mx_scales, None, None, self._mx_n,
+                                          self._mx_block, bits, bits)
+        return mx_tensor(packed, scales, self._mx_dtype, self._mx_orig_shape, self._mx_n, self._mx_block)
 
     def __repr__(self):
         return (f"mx_tensor({self._mx_dtype.name}, shape={tuple(self._mx_orig_shape)}, "
@@ -272,6 +308,45 @@ def _pick_ref(*args):
             if r is not None:
                 return r
     return None
+
+
+_POINTWISE = {torch.add, torch.sub, torch.mul, torch.div, torch.pow}
+
+
+def _dispatch_qelementwise(op: str, a: "mx_tensor", b: "mx_tensor") -> "mx_tensor":
+    """_dispatch_qadd / _dispatch_qsub / _dispatch_qmul (mxtorch.py:5321-5497):
+    codes of both operands read with a's width, output dtype _resolve_mixed
+    (add, sub) or the widened {kind}{2*bits}d (mul)."""
+    bits = a._mx_dtype.bits
+    out_dt = qmul_output_dtype(a._mx_dtype) if op == "mul" else resolve_mixed(a._mx_dtype, b._mx_dtype)
+    packed, scales = ops.qelementwise(op, a._mx_packed, a._mx_scales, b._mx_packed, b._mx_scales, a._mx_n,
+                                      a._mx_block, bits, out_dt.bits)
+    return mx_tensor(packed, scales, out_dt, a._mx_orig_shape, a._mx_n, a._mx_block)
+
+
+def _binary_op(a, b, fn):
+    """_binary_op (mxtorch.py:6450-6506).  Two mx_tensors of one shape and
+    block: add / sub / mul stay in the code domain (the reference reads
+    requires_grad of quantized tensors as False, so its STE branch is not
+    taken); otherwise dequantize, apply fn, requantize (two mx_tensors: with
+    _resolve_mixed of their dtypes; one: with its dtype)."""
+    if isinstance(a, mx_tensor) and isinstance(b, mx_tensor):
+        if a._mx_orig_shape == b._mx_orig_shape and a._mx_block == b._mx_block:
+            name = getattr(fn, "__name__", "") or str(fn)
+            if "add" in name or fn is torch.add:
+                return _dispatch_qelementwise("add", a, b)
+            if "sub" in name or fn is torch.sub:
+                return _dispatch_qelementwise("sub", a, b)
+            if "mul" in name or fn is torch.mul:
+                return _dispatch_qelementwise("mul", a, b)
+        out_dt = resolve_mixed(a._mx_dtype, b._mx_dtype)
+        res = fn(_unwrap(a), _unwrap(b))
+        return mx_tensor.quantize(res, out_dt, a._mx_block)
+    ref = a if isinstance(a, mx_tensor) else b
+    res = fn(_unwrap(a), _unwrap(b))
+    if isinstance(res, Tensor) and not isinstance(res, mx_tensor):
+        return mx_tensor.quantize(res, ref._mx_dtype, ref._mx_block)
+    return res
 
 
 def _fallback(func, args, kwargs):

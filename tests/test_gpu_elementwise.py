@@ -1,0 +1,141 @@
+"""GPU parity of quantized element-wise arithmetic (qa + qb, qa - qb, qa * qb,
+-qa; mxtorch.py:5321-5497, 1186-1296, 6177-6193) against the oracle
+(oracle.dispatch_qelementwise / negate, pinned in
+tests/test_oracle_elementwise.py): packed codes, scales and dtypes bitwise
+equal."""
+import pytest
+import torch
+
+from oracle import mx_oracle as orc
+from tests import _golden as G
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def qa():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    import qtpytorch_amd
+    return qtpytorch_amd
+
+
+def dev():
+    return torch.device("cuda:0")
+
+
+def _bits_eq(a, b):
+    return G.bits_equal(a.detach().cpu(), b.detach().cpu())
+
+
+def _operands(shape, seed, block, a_name, b_name, mode):
+    g = torch.Generator()
+    g.manual_seed(seed)
+    x = torch.randn(*shape, generator=g)
+    if mode == "near":     # same block scales up to a few ulps: the integer path, with overflow
+        y = x * 1.0000001 + 1e-3 * torch.randn(*shape, generator=g)
+    elif mode == "far":    # scales 3-50x apart: the float path
+        y = torch.randn(*shape, generator=g) * 40.0
+    else:                  # mixed: both paths across blocks
+        y = torch.randn(*shape, generator=g) * torch.rand(*shape, generator=g).pow(4) * 8.0
+    pa, sa, n = orc.quantize(x, a_name, block)
+    pb, sb, _ = orc.quantize(y, b_name, block)
+    return (pa, sa), (pb, sb), n
+
+
+def _mx(qa, p, s, name, shape, n, block):
+    return qa.mx_tensor(p.to(dev()), s.to(dev()), qa.get_mx_dtype(name), torch.Size(shape), n, block)
+
+
+CASES = [
+    ("int8d", "int8d", 128, (16, 300), "near"),
+    ("int8d", "int8d", 128, (16, 300), "far"),
+    ("int8d", "int8d", 128, (16, 300), "mixed"),
+    ("int4d", "int4d", 64, (7, 129), "mixed"),
+    ("int4d", "int4d", 128, (3, 1000), "near"),
+    ("int2d", "int2d", 32, (5, 77), "mixed"),
+    ("int3d", "int3d", 128, (4, 333), "mixed"),
+    ("int16d", "int16d", 256, (2, 700), "mixed"),
+    ("float4d", "float4d", 128, (9, 200), "mixed"),
+    ("float8d", "float8d", 96, (9, 200), "mixed"),
+    ("int8dv", "int8dv", 128, (4, 512), "mixed"),
+    ("int8d", "int4d", 128, (8, 256), "mixed"),       # b read with a's width
+    ("int4d", "int8d", 128, (8, 256), "near"),
+    ("int8d", "float4u", 128, (8, 256), "mixed"),     # output dtype float4u
+    ("int5d", "int5d", 192, (3, 400), "far"),
+    ("int7d", "int6d", 200, (3, 401), "mixed"),       # block not a multiple of 64: two-pass packing
+]
+
+
+@pytest.mark.parametrize("op", ["add", "sub", "mul"])
+@pytest.mark.parametrize("a_name,b_name,block,shape,mode", CASES,
+                         ids=[f"{c[0]}-{c[1]}-b{c[2]}-{c[4]}" for c in CASES])
+def test_qelementwise_vs_oracle(qa, op, a_name, b_name, block, shape, mode):
+    (pa, sa), (pb, sb), n = _operands(shape, 17 + block, block, a_name, b_name, mode)
+    A = _mx(qa, pa, sa, a_name, shape, n, block)
+    B = _mx(qa, pb, sb, b_name, shape, n, block)
+    C = {"add": A + B, "sub": A - B, "mul": A * B}[op]
+    rp, rs, rname = orc.dispatch_qelementwise(op, pa, sa, a_name, pb, sb, b_name, n, block)
+    assert C._mx_dtype.name == rname
+    assert C._mx_n == n and tuple(C._mx_orig_shape) == shape and C._mx_block == block
+    assert _bits_eq(C._mx_scales, rs), "scales differ"
+    assert _bits_eq(C._mx_packed, rp), "packed codes differ"
+
+
+@pytest.mark.parametrize("name", ["int1d", "int2d", "int3d", "int4d", "int5d", "int8d", "int16d", "float4d",
+                                  "float8d", "int4dh"])
+def test_neg_vs_oracle(qa, name):
+    shape, block = (5, 301), 128   # a padded last block
+    x = torch.randn(*shape)
+    p, s, n = orc.quantize(x, name, block)
+    N = -_mx(qa, p, s, name, shape, n, block)
+    rp, rs = orc.negate(p, s, name, n)
+    assert N._mx_dtype.name == name
+    assert _bits_eq(N._mx_packed, rp) and _bits_eq(N._mx_scales, rs)
+
+
+def test_operator_routes(qa):
+    """Routes of _binary_op (mxtorch.py:6450-6506, 6807-6819): a scalar
+    operand requantizes the float result with the mx_tensor's dtype; torch.add
+    on two mx_tensors takes the dequantize -> add -> requantize branch with
+    _resolve_mixed's dtype; a shape mismatch fails as torch broadcasting does."""
+    shape, block = (6, 256), 128
+    (pa, sa), (pb, sb), n = _operands(shape, 5, block, "int8d", "int4d", "mixed")
+    A = _mx(qa, pa, sa, "int8d", shape, n, block)
+    B = _mx(qa, pb, sb, "int4d", shape, n, block)
+    da = orc.dequant(pa, sa, "int8d", n, block).reshape(shape)
+    db = orc.dequant(pb, sb, "int4d", n, block).reshape(shape)
+
+    def same(mx, x, name):
+        rp, rs, _ = orc.quantize(x, name, block)
+        return mx._mx_dtype.name == name and _bits_eq(mx._mx_packed, rp) and _bits_eq(mx._mx_scales, rs)
+
+    assert same(A + 2.5, da + 2.5, "int8d")
+    assert same(A * 3.0, da * 3.0, "int8d")
+    assert same(torch.add(A, B), da + db, "int4d")   # _resolve_mixed(int8d, int4d)
+    assert same(A / 4.0, da / 4.0, "int8d")
+    C = _mx(qa, pa[: 3 * 256].clone(), sa[:6].clone(), "int8d", (3, 256), 3 * 256, block)
+    with pytest.raises(RuntimeError):
+        _ = A + C                                      # broadcasting [6,256] + [3,256] fails, as in torch
+
+
+def test_large_elementwise_roundtrip(qa):
+    """A 2^24-element add on the GPU path against the oracle on a sampled
+    set of blocks (blocks are independent)."""
+    n, block = 1 << 24, 128
+    g = torch.Generator()
+    g.manual_seed(9)
+    x = torch.randn(n, generator=g)
+    y = torch.randn(n, generator=g) * torch.rand(n, generator=g).pow(3) * 4
+    dt = qa.get_mx_dtype("int8d")
+    A = qa.mx_tensor.quantize(x.to(dev()), dt, block)
+    B = qa.mx_tensor.quantize(y.to(dev()), dt, block)
+    C = A + B
+    nb = n // block
+    pick = torch.tensor(sorted({0, 1, 2, 777, nb // 2, nb - 2, nb - 1} | set(range(1000, nb, 9973))))
+    idx = (pick[:, None] * block + torch.arange(block)[None, :]).reshape(-1)
+    pa, sa, _ = orc.quantize(x[idx], "int8d", block)
+    pb, sb, _ = orc.quantize(y[idx], "int8d", block)
+    rp, rs, _ = orc.dispatch_qelementwise("add", pa, sa, "int8d", pb, sb, "int8d", idx.numel(), block)
+    assert _bits_eq(C._mx_scales.cpu()[pick], rs)
+    assert _bits_eq(C._mx_packed.cpu()[idx], rp)
