@@ -12,6 +12,7 @@ tensors must be on a GPU.
 """
 from . import dtypes as _dtypes
 from .dtypes import get_mx_dtype, matmul_output_dtype, mx_dtype
+from .io import load_quantized, save_quantized
 from .kv import kv_cache_quantizer
 from .nn import install_module_to, mx_linear, to_mx, uninstall_module_to
 from .ops import HADAMARD_DEQUANT_MODE, _dequant, quantize
@@ -24,4 +25,4 @@ install_module_to()
 
 __all__ = ["mx_dtype", "get_mx_dtype", "matmul_output_dtype", "mx_tensor", "quantize", "_dequant",
            "_dispatch_qgemm", "_mx_mm", "_QGemmSTE", "mx_matmul", "mx_quantize", "mx_linear", "to_mx",
-           "kv_cache_quantizer", "install_module_to", "uninstall_module_to"]
+           "kv_cache_quantizer", "install_module_to", "uninstall_module_to", "save_quantized", "load_quantized"]

@@ -162,3 +162,4 @@ def test_quantize_float_vector_dtypes(qa, dtype):
     assert _bits_eq(p, rp) and _bits_eq(s, rs)
     dq = qa.ops._dequant(p, s, dt, n, 128)
     assert _bits_eq(dq, orc.dequant(rp, rs, dtype, n, 128))
+
