@@ -36,7 +36,7 @@
 extern "C" {
 #endif
 
-#define MXK_ABI_VERSION 3
+#define MXK_ABI_VERSION 4
 
 typedef enum {
   MXK_OK = 0,
@@ -52,6 +52,11 @@ typedef enum {
   MXK_VAR_HADAMARD = 1, /* "h" : randomized Walsh-Hadamard, then base      */
   MXK_VAR_VECTOR = 2    /* "v" : per-row absmax, true division             */
 } mxk_variant;
+typedef enum {
+  MXK_DYN_PER_TOKEN = 0,   /* one scale per row of the last dimension        */
+  MXK_DYN_PER_CHANNEL = 1, /* one scale per column of x.reshape(shape[0], -1) */
+  MXK_DYN_PER_TENSOR = 2   /* one scale for the whole tensor                 */
+} mxk_dyn_granularity;
 
 /* Library version; equals MXK_ABI_VERSION. */
 int mxk_abi_version(void);
@@ -222,6 +227,55 @@ int mxk_qelementwise(int op, const void* a_packed, int64_t a_nbytes, const float
                      int64_t b_nbytes, const float* b_scales, int64_t n, int64_t nb, int block, int bits,
                      int out_bits, void* c_packed, int64_t c_nbytes, float* c_scales, void* workspace,
                      size_t workspace_nbytes, void* stream);
+
+/* Weight-only linear with the weight stored [N][K] (row n = output n):
+ * out[M,N] = x[M,K] (x_type, as float32) @ dequant(W)^T (+ bias[N]), the
+ * computation of mx_dynamic_linear.forward (mxtorch.py:8949-8962: the
+ * dequantized quantize(weight) applied as tokens @ w_dq.t() + bias) and of
+ * _MXLinearAutograd.backward (mxtorch.py:6729-6740: grad @ w_dq.t()).
+ * W: packed codes of any width/kind of mxk_quantize (base variant), flat
+ * blocks of `block` elements of the row-major [N][K] weight, w_nscales >=
+ * ceil(N*K/block).  Float32 accumulation. */
+int mxk_linear_wq_nt(const void* x, int x_type, int64_t M, int64_t K, const void* w_packed, int64_t w_nbytes,
+                     const float* w_scales, int64_t w_nscales, int64_t N, int kind, int bits, int block,
+                     const float* bias, float* out, void* stream);
+
+/* Workspace bytes mxk_linear_i8 needs (0 when the shapes are not covered). */
+size_t mxk_linear_i8_workspace(int64_t M, int64_t K, int64_t N, int x_bits, int w_bits, int64_t x_block,
+                               int64_t w_block);
+
+/* fused_int8_linear (mxtorch.py:3910-3960) on int codes: the reference's
+ * result is F.linear(x.dequantize(), weight.dequantize(), bias)
+ * (mxtorch.py:3957-3960), i.e.
+ *   out[m,n] = sum_k RN(xc[m,k]*sx) * RN(wc[n,k]*sw) + bias[n]
+ * with x [M][K] and W [N][K] packed int codes (widths 2, 4 or 8, base
+ * variant), sx = x_scales[(m*K+k)/x_block], sw = w_scales[(n*K+k)/w_block]
+ * (per-token activations from dynamic_quantize have x_block = K).  Here the
+ * exact integer product of each K chunk runs on int8 MFMA and the chunk is
+ * scaled once: out = sum_chunks RN(RN(P*sx)*sw) (+ bias), float32,
+ * within 1e-3 relative of the reference.  Needs 64 to divide K, x_block
+ * and w_block (MXK_EUNSUPPORTED otherwise: dequantize x and use
+ * mxk_linear_wq_nt).  8-bit operands are read in place (16-byte aligned). */
+int mxk_linear_i8(const void* x_packed, int64_t x_nbytes, const float* x_scales, int64_t x_nscales, int64_t x_block,
+                  int x_bits, const void* w_packed, int64_t w_nbytes, const float* w_scales, int64_t w_nscales,
+                  int64_t w_block, int w_bits, int64_t M, int64_t K, int64_t N, const float* bias, float* out,
+                  void* workspace, size_t workspace_nbytes, void* stream);
+
+/* Workspace bytes mxk_dynamic_quantize needs. */
+size_t mxk_dynamic_quantize_workspace(int64_t rows, int64_t cols, int granularity, int bits);
+
+/* dynamic_quantize(x, dt, granularity) (mxtorch.py:2665-2731) on x viewed
+ * as [rows][cols]: rows x cols = x.reshape(-1, shape[-1]) for per_token,
+ * x.reshape(shape[0], -1) for per_channel, any split for per_tensor.
+ *   s = RN(max(absmax, 1e-12) / max_int), max_int = 2^(bits-1)-1,
+ *   code = rne(clamp(RN(x / s), -max_int, max_int)),
+ * over a row (per_token: scales[rows]), a column (per_channel:
+ * scales[cols]) or the tensor (per_tensor: scales[1]); codes packed with
+ * pack_auto (mxtorch.py:976-985), packed_nbytes = mxk_packed_nbytes(bits,
+ * rows*cols).  Widths 2..8 and 16 per token, 2, 4 and 8 otherwise. */
+int mxk_dynamic_quantize(const void* x, int x_type, int64_t rows, int64_t cols, int granularity, int bits,
+                         void* packed, int64_t packed_nbytes, float* scales, void* workspace,
+                         size_t workspace_nbytes, void* stream);
 
 #ifdef __cplusplus
 }

@@ -667,3 +667,99 @@ def negate(packed: Tensor, scales: Tensor, name: str, n: int) -> Tuple[Tensor, T
         return (-packed.to(torch.int16)).clamp(-max_i, max_i).to(torch.int8), scales.clone()
     codes = unpack_auto(packed, bits, n).to(torch.int32)
     return pack_auto((-codes).clamp(-max_i, max_i).to(torch.int32), bits), scales.clone()
+
+
+# ---------------------------------------------------------------------------
+# dynamic activations and the int8 x int8 linear
+# (mxtorch.py:2665-2731, 3910-3960, 8870-8968, 6693-6752)
+# ---------------------------------------------------------------------------
+def dynamic_quantize(x: Tensor, name: str, granularity: str = "per_token", block: int = 64):
+    """dynamic_quantize (mxtorch.py:2665-2731) -> (packed, scales, orig_shape,
+    n, block) of the mx_tensor it returns; the trailing ``.reshape(*shape)``
+    of the per_token / per_channel branches only relabels the shape
+    (mx_tensor.reshape, mxtorch.py:6319-6326)."""
+    _, bits, _, _ = parse_dtype(name)
+    max_int = float((1 << (bits - 1)) - 1)
+    x_f = x.float()
+    shape = tuple(x_f.shape)
+    if granularity == "per_token":            # mxtorch.py:2708-2714
+        x2 = x_f.reshape(-1, shape[-1])
+        scales = x2.abs().amax(dim=1).clamp(min=1e-12) / max_int
+        codes = (x2 / scales.unsqueeze(1)).round().clamp(-max_int, max_int).to(torch.int32)
+        return pack_auto(codes.reshape(-1), bits), scales, shape, x2.numel(), x2.shape[-1]
+    if granularity == "per_channel":          # mxtorch.py:2716-2722
+        x2 = x_f.reshape(shape[0], -1)
+        scales = x2.abs().amax(dim=0).clamp(min=1e-12) / max_int
+        codes = (x2 / scales.unsqueeze(0)).round().clamp(-max_int, max_int).to(torch.int32)
+        return pack_auto(codes.reshape(-1), bits), scales, shape, x2.numel(), x2.shape[0]
+    if granularity == "per_tensor":           # mxtorch.py:2724-2729
+        scale = x_f.abs().max().clamp(min=1e-12) / max_int
+        codes = (x_f / scale).round().clamp(-max_int, max_int).to(torch.int32)
+        return pack_auto(codes.reshape(-1), bits), scale.unsqueeze(0), shape, x_f.numel(), x_f.numel()
+    p, s, n = quantize(x_f, name, block)      # mxtorch.py:2731
+    return p, s, shape, n, block
+
+
+def fused_int8_linear(x_packed: Tensor, x_scales: Tensor, x_name: str, x_shape, x_n: int, x_block: int,
+                      w_packed: Tensor, w_scales: Tensor, w_name: str, w_shape, w_n: int, w_block: int,
+                      bias: Optional[Tensor] = None) -> Tensor:
+    """fused_int8_linear's CPU branch (mxtorch.py:3957-3960):
+    F.linear(x.dequantize(), weight.dequantize(), bias)."""
+    x_f = dequant(x_packed, x_scales, x_name, x_n, x_block).reshape(x_shape)
+    w_f = dequant(w_packed, w_scales, w_name, w_n, w_block).reshape(w_shape)
+    return F.linear(x_f, w_f, bias)
+
+
+def dynamic_linear_from_weight(weight: Tensor, name: str, block: int = 128):
+    """mx_dynamic_linear.from_linear weight storage (mxtorch.py:8916-8917):
+    quantize(weight) in nn.Linear's [out, in] layout, not transposed."""
+    return quantize(weight, name, block)
+
+
+def dynamic_linear_forward(x: Tensor, w_packed: Tensor, w_scales: Tensor, name: str, in_features: int,
+                           out_features: int, block: int = 128, bias: Optional[Tensor] = None) -> Tensor:
+    """mx_dynamic_linear.forward (mxtorch.py:8945-8962).  The per-token
+    quantization it computes first (mxtorch.py:8947) does not reach the
+    output: the product takes the unquantized tokens (mxtorch.py:8955-8957)."""
+    x_f = x.float()
+    tokens = x_f.reshape(-1, in_features)
+    w_dq = dequant(w_packed, w_scales, name, in_features * out_features, block).reshape(out_features, in_features)
+    out = tokens.float() @ w_dq.t()
+    out = out.reshape(*x_f.shape[:-1], out_features)
+    if bias is not None:
+        out = out + bias
+    return out
+
+
+def mx_linear_autograd_forward(x: Tensor, w_packed: Tensor, w_scales: Tensor, w_name: str, x_name: str,
+                               in_features: int, out_features: int, block: int,
+                               b_packed: Optional[Tensor] = None, b_scales: Optional[Tensor] = None) -> Tensor:
+    """_MXLinearAutograd.forward (mxtorch.py:6696-6726) for an [in, out]
+    weight: quantize the 2-D input with x_name, _mx_mm -> _dispatch_qgemm
+    (packed output of the matmul dtype), dequantize, add the dequantized bias."""
+    orig_shape = x.shape
+    x2 = x.reshape(-1, in_features) if x.dim() > 2 else x
+    xp, xs, xn = quantize(x2, x_name, block)
+    pc, sc, out_name = dispatch_qgemm(xp, xs, x_name, tuple(x2.shape), xn, w_packed, w_scales, w_name,
+                                      (in_features, out_features), in_features * out_features, block)
+    M = x2.shape[0]
+    out = dequant(pc, sc, out_name, M * out_features, block).reshape(M, out_features)
+    if len(orig_shape) > 2:
+        out = out.reshape(*orig_shape[:-1], out_features)
+    if b_packed is not None:
+        b_f = dequant(b_packed, b_scales, w_name, out_features, block)
+        if len(orig_shape) > 2:
+            b_f = b_f.unsqueeze(0)
+        out = out + b_f
+    return out
+
+
+def mx_linear_autograd_backward(grad: Tensor, w_packed: Tensor, w_scales: Tensor, w_name: str, in_features: int,
+                                out_features: int, block: int, orig_shape) -> Tensor:
+    """_MXLinearAutograd.backward (mxtorch.py:6729-6746): grad @ w_dq.t()."""
+    w_dq = dequant(w_packed, w_scales, w_name, in_features * out_features, block).reshape(in_features, out_features)
+    grad_2d = grad.reshape(-1, w_dq.shape[1]) if grad.dim() > 2 else grad
+    gi = grad_2d @ w_dq.t()
+    if len(orig_shape) > 2:
+        gi = gi.reshape(*orig_shape[:-1], in_features)
+    return gi

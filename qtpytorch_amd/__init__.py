@@ -14,9 +14,10 @@ from . import dtypes as _dtypes
 from .dtypes import get_mx_dtype, matmul_output_dtype, mx_dtype
 from .io import load_quantized, save_quantized
 from .kv import kv_cache_quantizer
-from .nn import install_module_to, mx_linear, to_mx, uninstall_module_to
+from .nn import install_module_to, mx_dynamic_linear, mx_linear, to_mx, uninstall_module_to
 from .ops import HADAMARD_DEQUANT_MODE, _dequant, quantize
-from .tensor import _dispatch_qgemm, _mx_mm, _QGemmSTE, mx_matmul, mx_quantize, mx_tensor
+from .tensor import (_dispatch_qgemm, _mx_linear_forward, _mx_mm, _MXLinearAutograd, _QGemmSTE,
+                     dynamic_quantize, fused_int8_linear, mx_fused_ops, mx_matmul, mx_quantize, mx_tensor)
 
 for _n in _dtypes._DTYPE_REGISTRY:
     globals()[_n] = _dtypes._DTYPE_REGISTRY[_n]
@@ -25,4 +26,6 @@ install_module_to()
 
 __all__ = ["mx_dtype", "get_mx_dtype", "matmul_output_dtype", "mx_tensor", "quantize", "_dequant",
            "_dispatch_qgemm", "_mx_mm", "_QGemmSTE", "mx_matmul", "mx_quantize", "mx_linear", "to_mx",
-           "kv_cache_quantizer", "install_module_to", "uninstall_module_to", "save_quantized", "load_quantized"]
+           "kv_cache_quantizer", "install_module_to", "uninstall_module_to", "save_quantized", "load_quantized",
+           "dynamic_quantize", "fused_int8_linear", "mx_fused_ops", "mx_dynamic_linear", "_MXLinearAutograd",
+           "_mx_linear_forward"]

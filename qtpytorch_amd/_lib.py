@@ -18,6 +18,8 @@ MXK_OK = 0
 MXK_IN_F32, MXK_IN_F16, MXK_IN_BF16 = 0, 1, 2
 MXK_KIND_INT, MXK_KIND_FLOAT = 0, 1
 MXK_VAR_BASE, MXK_VAR_HADAMARD, MXK_VAR_VECTOR = 0, 1, 2
+MXK_DYN_PER_TOKEN, MXK_DYN_PER_CHANNEL, MXK_DYN_PER_TENSOR = 0, 1, 2
+ABI_VERSION = 4
 
 _lock = threading.Lock()
 _lib = None
@@ -53,6 +55,13 @@ SIGNATURES = {
     "mxk_qelementwise_workspace": (c_sz, [c_int, c_i64, c_i64, c_int, c_int, c_int]),
     "mxk_qelementwise": (c_int, [c_int, c_vp, c_i64, c_vp, c_vp, c_i64, c_vp, c_i64, c_i64, c_int, c_int, c_int,
                                  c_vp, c_i64, c_vp, c_vp, c_sz, c_vp]),
+    "mxk_linear_wq_nt": (c_int, [c_vp, c_int, c_i64, c_i64, c_vp, c_i64, c_vp, c_i64, c_i64, c_int, c_int, c_int,
+                                 c_vp, c_vp, c_vp]),
+    "mxk_linear_i8_workspace": (c_sz, [c_i64, c_i64, c_i64, c_int, c_int, c_i64, c_i64]),
+    "mxk_linear_i8": (c_int, [c_vp, c_i64, c_vp, c_i64, c_i64, c_int, c_vp, c_i64, c_vp, c_i64, c_i64, c_int,
+                              c_i64, c_i64, c_i64, c_vp, c_vp, c_vp, c_sz, c_vp]),
+    "mxk_dynamic_quantize_workspace": (c_sz, [c_i64, c_i64, c_int, c_int]),
+    "mxk_dynamic_quantize": (c_int, [c_vp, c_int, c_i64, c_i64, c_int, c_int, c_vp, c_i64, c_vp, c_vp, c_sz, c_vp]),
 }
 
 
@@ -79,7 +88,7 @@ def lib():
                 raise MXKError(f"{LIB_PATH} does not export {name}")
             fn.restype = res
             fn.argtypes = args
-        if h.mxk_abi_version() != 3:
+        if h.mxk_abi_version() != ABI_VERSION:
             raise MXKError("libmxk.so ABI version mismatch")
         _lib = h
         return h

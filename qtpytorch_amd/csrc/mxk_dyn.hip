@@ -1,0 +1,165 @@
+// Dynamic (runtime) activation quantization, dynamic_quantize
+// (mxtorch.py:2665-2731), for gfx950.
+//
+// Every granularity uses the same per-element rule with max_int =
+// 2^(bits-1)-1 of the dtype's width (for float dtypes too, mxtorch.py:2705):
+//   s = RN(max(absmax, 1e-12) / max_int),  code = rne(clamp(RN(x / s), +-max_int))
+// and packs the codes with pack_auto (mxtorch.py:976-985).  They differ in
+// what one scale covers:
+//   per_token    one scale per row of the last dimension: the 'v' rule with
+//                block = row length, run by mxk_quantize (mxtorch.py:2708-2714);
+//   per_channel  one scale per column of x.reshape(shape[0], -1)
+//                (mxtorch.py:2716-2722);
+//   per_tensor   one scale for the whole tensor (mxtorch.py:2724-2729).
+// The absmax of a column or of the tensor is reduced with atomicMax on the
+// bit patterns of non-negative floats, which order like the floats: the
+// result is exact and independent of the order of arrival.
+#include "mxk_internal.h"
+
+#include <algorithm>
+
+namespace mxk {
+
+__global__ __launch_bounds__(256) void k_fill_u32(uint32_t* __restrict__ p, int64_t n, uint32_t v) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
+    p[i] = v;
+}
+
+// amax[c] = max over rows of |x[r][c]|; blockIdx.y takes `rows_per` rows.
+template <typename T>
+__global__ __launch_bounds__(256) void k_absmax_cols(const T* __restrict__ x, int64_t R, int64_t C, int64_t rows_per,
+                                                     uint32_t* __restrict__ amax) {
+  const int64_t c = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (c >= C) return;
+  const int64_t r0 = (int64_t)blockIdx.y * rows_per;
+  const int64_t r1 = std::min<int64_t>(R, r0 + rows_per);
+  float m = 0.0f;
+  for (int64_t r = r0; r < r1; ++r) m = fmaxf(m, __builtin_fabsf(ElemT<T>::cvt(x[r * C + c])));
+  atomicMax(amax + c, __float_as_uint(m));
+}
+
+// amax[0] = max over all n of |x|: grid-stride, wave maximum, one atomic per wave.
+template <typename T>
+__global__ __launch_bounds__(256) void k_absmax_all(const T* __restrict__ x, int64_t n, uint32_t* __restrict__ amax) {
+  float m = 0.0f;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
+    m = fmaxf(m, __builtin_fabsf(ElemT<T>::cvt(x[i])));
+  m = group_max<64>(m);
+  if ((threadIdx.x & 63) == 0) atomicMax(amax, __float_as_uint(m));
+}
+
+// scales[i] = RN(max(amax[i], fl32(1e-12)) / max_int)
+__global__ __launch_bounds__(256) void k_dyn_scales(const uint32_t* __restrict__ amax, int64_t cnt, float q,
+                                                    float* __restrict__ scales) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < cnt; i += (int64_t)gridDim.x * blockDim.x)
+    scales[i] = fmaxf(__uint_as_float(amax[i]), MXK_AMIN) / q;
+}
+
+// One packed byte per thread: the 8/BITS codes of elements u*per .. u*per+per-1,
+// each divided by its scale (scales[j % C], or scales[0] when C == 0).
+template <typename T, int BITS>
+__global__ __launch_bounds__(256) void k_dyn_encode(const T* __restrict__ x, int64_t n, int64_t C,
+                                                    const float* __restrict__ scales, float q,
+                                                    uint8_t* __restrict__ packed, int64_t nbytes) {
+  constexpr int PER = 8 / BITS;
+  constexpr uint32_t MASK = (1u << BITS) - 1u;
+  for (int64_t u = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; u < nbytes; u += (int64_t)gridDim.x * blockDim.x) {
+    uint32_t w = 0u;
+#pragma unroll
+    for (int f = 0; f < PER; ++f) {
+      const int64_t j = u * PER + f;
+      if (j >= n) break;
+      const float s = scales[C ? j % C : 0];
+      const float y = ElemT<T>::cvt(x[j]) / s;
+      const int code = (int)rne(fminf(fmaxf(y, -q), q));
+      w |= ((uint32_t)code & MASK) << (f * BITS);
+    }
+    packed[u] = (uint8_t)w;
+  }
+}
+
+template <typename T>
+static int dyn_run(const T* x, int64_t rows, int64_t cols, int granularity, int bits, uint8_t* packed,
+                   int64_t pbytes, float* scales, uint32_t* amax, hipStream_t st) {
+  const int64_t n = rows * cols;
+  const float q = (float)((1u << (bits - 1)) - 1u);
+  const int cap = num_cus() * 8;
+  const int64_t cnt = granularity == MXK_DYN_PER_CHANNEL ? cols : 1;
+  hipLaunchKernelGGL(k_fill_u32, dim3((unsigned)std::min<int64_t>(ceil_div(cnt, 256), cap)), dim3(256), 0, st, amax,
+                     cnt, 0u);
+  if (granularity == MXK_DYN_PER_CHANNEL) {
+    // enough row chunks that the grid fills the chip; each chunk reads whole rows
+    const int64_t col_blocks = ceil_div(cols, 256);
+    const int64_t chunks = std::max<int64_t>(1, std::min<int64_t>(rows, ceil_div((int64_t)num_cus() * 4, col_blocks)));
+    const int64_t rows_per = ceil_div(rows, chunks);
+    hipLaunchKernelGGL((k_absmax_cols<T>), dim3((unsigned)col_blocks, (unsigned)ceil_div(rows, rows_per)), dim3(256),
+                       0, st, x, rows, cols, rows_per, amax);
+  } else {
+    hipLaunchKernelGGL((k_absmax_all<T>), dim3((unsigned)std::min<int64_t>(ceil_div(n, 256), cap)), dim3(256), 0, st,
+                       x, n, amax);
+  }
+  hipLaunchKernelGGL(k_dyn_scales, dim3((unsigned)std::min<int64_t>(ceil_div(cnt, 256), cap)), dim3(256), 0, st, amax,
+                     cnt, q, scales);
+  const int64_t C = granularity == MXK_DYN_PER_CHANNEL ? cols : 0;
+  const dim3 g((unsigned)std::min<int64_t>(ceil_div(pbytes, 256), cap));
+  switch (bits) {
+    case 2: hipLaunchKernelGGL((k_dyn_encode<T, 2>), g, dim3(256), 0, st, x, n, C, scales, q, packed, pbytes); break;
+    case 4: hipLaunchKernelGGL((k_dyn_encode<T, 4>), g, dim3(256), 0, st, x, n, C, scales, q, packed, pbytes); break;
+    default: hipLaunchKernelGGL((k_dyn_encode<T, 8>), g, dim3(256), 0, st, x, n, C, scales, q, packed, pbytes); break;
+  }
+  return check_launch("dynamic_quantize");
+}
+
+}  // namespace mxk
+
+using namespace mxk;
+
+extern "C" {
+
+size_t mxk_dynamic_quantize_workspace(int64_t rows, int64_t cols, int granularity, int bits) {
+  if (rows <= 0 || cols <= 0) return 0;
+  if (granularity == MXK_DYN_PER_TOKEN)
+    return mxk_quantize_workspace(rows * cols, MXK_KIND_INT, bits, MXK_VAR_VECTOR, (int)cols, 0);
+  const int64_t cnt = granularity == MXK_DYN_PER_CHANNEL ? cols : 1;
+  return (size_t)((cnt * 4 + 255) & ~(int64_t)255);
+}
+
+int mxk_dynamic_quantize(const void* x, int x_type, int64_t rows, int64_t cols, int granularity, int bits,
+                         void* packed, int64_t packed_nbytes, float* scales, void* workspace,
+                         size_t workspace_nbytes, void* stream) {
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  if (rows <= 0 || cols <= 0) return fail(MXK_EINVAL, "dynamic_quantize: rows and cols must be positive");
+  if (!x || !packed || !scales) return fail(MXK_EINVAL, "dynamic_quantize: null buffer");
+  if (x_type != MXK_IN_F32 && x_type != MXK_IN_F16 && x_type != MXK_IN_BF16)
+    return fail(MXK_EINVAL, "dynamic_quantize: x_type must be f32, f16 or bf16");
+  if (granularity < MXK_DYN_PER_TOKEN || granularity > MXK_DYN_PER_TENSOR)
+    return fail(MXK_EINVAL, "dynamic_quantize: unknown granularity");
+  const int64_t n = rows * cols;
+  if (granularity == MXK_DYN_PER_TOKEN) {
+    // the 'v' rule with one block per row and max_int of the width
+    if (!(bits == 2 || bits == 3 || bits == 4 || bits == 5 || bits == 6 || bits == 7 || bits == 8 || bits == 16))
+      return fail(MXK_EUNSUPPORTED, "dynamic_quantize(per_token): widths 2..8 and 16 are implemented");
+    if (cols > INT32_MAX) return fail(MXK_EINVAL, "dynamic_quantize(per_token): row too long");
+    return mxk_quantize(x, x_type, n, MXK_KIND_INT, bits, MXK_VAR_VECTOR, (int)cols, nullptr, 0, packed,
+                        packed_nbytes, scales, n, workspace, workspace_nbytes, stream);
+  }
+  if (!(bits == 2 || bits == 4 || bits == 8))
+    return fail(MXK_EUNSUPPORTED, "dynamic_quantize(per_channel/per_tensor): widths 2, 4 and 8 are implemented");
+  if (packed_nbytes != mxk_packed_nbytes(bits, n))
+    return fail(MXK_EINVAL, "dynamic_quantize: packed buffer must hold exactly pack_auto's bytes");
+  if (!workspace || workspace_nbytes < mxk_dynamic_quantize_workspace(rows, cols, granularity, bits))
+    return fail(MXK_EINVAL, "dynamic_quantize: workspace too small");
+  uint32_t* amax = reinterpret_cast<uint32_t*>(workspace);
+  uint8_t* pk = reinterpret_cast<uint8_t*>(packed);
+  switch (x_type) {
+    case MXK_IN_F32:
+      return dyn_run(reinterpret_cast<const float*>(x), rows, cols, granularity, bits, pk, packed_nbytes, scales, amax, st);
+    case MXK_IN_F16:
+      return dyn_run(reinterpret_cast<const __half*>(x), rows, cols, granularity, bits, pk, packed_nbytes, scales, amax, st);
+    default:
+      return dyn_run(reinterpret_cast<const hip_bfloat16*>(x), rows, cols, granularity, bits, pk, packed_nbytes, scales,
+                     amax, st);
+  }
+}
+
+}  // extern "C"

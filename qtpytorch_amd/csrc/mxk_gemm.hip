@@ -99,7 +99,8 @@ __global__ __launch_bounds__(256) void k_qgemm_i8(const int8_t* __restrict__ A8,
                                                   const int8_t* __restrict__ B8, int64_t ldb, int64_t Brows,
                                                   const float* __restrict__ a_scales, int a_ok,
                                                   const float* __restrict__ b_scales, int b_ok, int64_t M, int64_t N,
-                                                  int KB, int BP, float* __restrict__ C, int32_t* __restrict__ acc_out) {
+                                                  int KB, int BP, float* __restrict__ C, int32_t* __restrict__ acc_out,
+                                                  const float* __restrict__ bias) {
   __shared__ __attribute__((aligned(16))) int8_t sA[QG_BM * QG_LDS_STRIDE];
   __shared__ __attribute__((aligned(16))) int8_t sB[QG_BN * QG_LDS_STRIDE];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -176,7 +177,7 @@ __global__ __launch_bounds__(256) void k_qgemm_i8(const int8_t* __restrict__ A8,
 #pragma unroll
         for (int b = 0; b < 4; ++b) {
           const int64_t col = n0 + wn * 64 + b * 16 + lr;
-          if (col < N) C[row * N + col] = c[a][b][i];
+          if (col < N) C[row * N + col] = bias ? c[a][b][i] + bias[col] : c[a][b][i];
         }
       }
   }
@@ -200,7 +201,8 @@ __global__ __launch_bounds__(256, 2) void k_qgemm_i8_v2(const int8_t* __restrict
                                                         const float* __restrict__ sa_t, int a_ok,
                                                         const float* __restrict__ b_scales, int b_ok, int64_t M,
                                                         int64_t N, int KB, float* __restrict__ C,
-                                                        int32_t* __restrict__ acc_out, int grouped) {
+                                                        int32_t* __restrict__ acc_out, int grouped,
+                                                        const float* __restrict__ bias) {
   __shared__ __attribute__((aligned(1024))) int8_t sA[2][QG_BM * 128];
   __shared__ __attribute__((aligned(1024))) int8_t sB[2][QG_BN * 128];
   __shared__ __attribute__((aligned(16))) float sSA[2][QG_BM];
@@ -342,7 +344,7 @@ __global__ __launch_bounds__(256, 2) void k_qgemm_i8_v2(const int8_t* __restrict
 #pragma unroll
         for (int b = 0; b < 4; ++b) {
           const int64_t col = n0 + wn * 64 + b * 16 + lr;
-          if (col < N) C[row * N + col] = c[a][b][i];
+          if (col < N) C[row * N + col] = bias ? c[a][b][i] + bias[col] : c[a][b][i];
         }
       }
   }
@@ -406,7 +408,7 @@ __global__ __launch_bounds__(512, 1) void k_qgemm_i8_v3(const int8_t* __restrict
                                                         const float* __restrict__ sa_t,
                                                         const float* __restrict__ sb_src, int64_t M, int64_t N,
                                                         int KB, float* __restrict__ C, int32_t* __restrict__ acc_out,
-                                                        int grouped) {
+                                                        int grouped, const float* __restrict__ bias) {
   // [A stages 0..2, 32 KiB each][B stages 0..2, 16 KiB each][scale stages 0..2, 2 KiB each]:
   // a stage's scales hold SA rows at floats 0..255 and SB columns at 256..383
   __shared__ __attribute__((aligned(1024))) int8_t lds[QG3_NS * (32768 + 16384 + 2048)];
@@ -665,7 +667,7 @@ __global__ __launch_bounds__(512, 1) void k_qgemm_i8_v3(const int8_t* __restrict
 #pragma unroll
         for (int b = 0; b < 4; ++b) {
           const int64_t col = n0 + wn * 64 + b * 16 + lr;
-          if (col < N) C[row * N + col] = c[a][b][i];
+          if (col < N) C[row * N + col] = bias ? c[a][b][i] + bias[col] : c[a][b][i];
         }
       }
   }
@@ -690,6 +692,21 @@ __global__ __launch_bounds__(256) void k_transpose_sa(const float* __restrict__ 
   for (int i = ty; i < 32; i += 8) {
     const int64_t k = k0 + i, m = m0 + tx;
     if (k < KB && m < M) t[k * M + m] = tile[tx][i];
+  }
+}
+
+// t[kb][r] (kb_major) or t[r][kb] = s[(r*K + kb*kblk) / B]: the scale of
+// the kblk-wide K chunk kb of row r of a [R][K] operand whose flat blocks
+// of B elements each carry one scale (0 past the ns scales given).
+__global__ __launch_bounds__(256) void k_gather_scales(const float* __restrict__ s, int64_t ns, int64_t R, int64_t K,
+                                                       int64_t B, int kblk, int KB, int kb_major,
+                                                       float* __restrict__ t) {
+  const int64_t total = R * (int64_t)KB;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t r = kb_major ? i % R : i / KB;
+    const int64_t kb = kb_major ? i / R : i % KB;
+    const int64_t j = (r * K + kb * kblk) / B;
+    t[i] = j < ns ? s[j] : 0.0f;
   }
 }
 
@@ -721,6 +738,41 @@ static GemmPlan plan_gemm(int64_t M, int64_t K, int64_t N, int bits, int block, 
   p.v3 = p.v2 && fits32 && ceil_div(M, QG3_BM) * ceil_div(N, QG3_BN) >= num_cus();
   p.sa_bytes = p.v2 ? up((size_t)p.KB * (size_t)M * sizeof(float)) : 0;
   p.sb_bytes = p.v3 ? up((size_t)p.KB * (size_t)N * sizeof(float)) : 0;  // ones, when B's scales do not fit
+  return p;
+}
+
+// ---------------------------------------------------------------- int8 x int8 linear
+// fused_int8_linear's operands: x [M][K] and W [N][K] codes, both with K
+// contiguous, each with one scale per flat block (Bx, Bw elements).  The
+// MFMA kernels need one scale per row per K chunk of kblk (128: v2/v3, 64:
+// the one-stage kernel), which holds when kblk divides K, Bx and Bw.
+struct I8LinPlan {
+  int kblk, KB;
+  bool direct_x, direct_w, v2, v3;
+  int64_t Mpad, Npad;
+  size_t x_bytes, w_bytes, sa_bytes, sb_bytes;
+};
+
+static I8LinPlan plan_i8lin(int64_t M, int64_t K, int64_t N, int xbits, int wbits, int64_t xb, int64_t wb) {
+  I8LinPlan p{};
+  p.kblk = (K % 128 == 0 && xb % 128 == 0 && wb % 128 == 0) ? 128
+           : ((K % 64 == 0 && xb % 64 == 0 && wb % 64 == 0) ? 64 : 0);
+  if (p.kblk == 0) return p;
+  p.KB = (int)(K / p.kblk);
+  p.Mpad = ceil_div(M, QG_BM) * QG_BM;
+  p.Npad = ceil_div(N, QG_BN) * QG_BN;
+  p.direct_x = xbits == 8;
+  p.direct_w = wbits == 8;
+  auto up = [](size_t v) { return (v + 255) & ~(size_t)255; };
+  p.x_bytes = p.direct_x ? 0 : up((size_t)p.Mpad * (size_t)K);
+  p.w_bytes = p.direct_w ? 0 : up((size_t)p.Npad * (size_t)K);
+  p.sa_bytes = up((size_t)p.KB * (size_t)M * sizeof(float));
+  p.sb_bytes = up((size_t)p.KB * (size_t)N * sizeof(float));
+  p.v2 = p.kblk == 128 && p.KB < 65536;
+  const int64_t lim = (int64_t)1 << 31;
+  const bool fits32 = (p.direct_x ? M : p.Mpad) * K < lim && (p.direct_w ? N : p.Npad) * K < lim &&
+                      (int64_t)p.KB * M * 4 < lim && (int64_t)p.KB * N * 4 < lim;
+  p.v3 = p.v2 && fits32 && ceil_div(M, QG3_BM) * ceil_div(N, QG3_BN) >= num_cus();
   return p;
 }
 
@@ -804,13 +856,13 @@ int mxk_qgemm(const void* a_packed, const float* a_scales, int64_t a_nscales, co
     }
     if (acc_i32 && wc)
       hipLaunchKernelGGL((k_qgemm_i8_v3<true, true>), g1, dim3(512), 0, st, A8, lda, arows, B8, p.KBP, p.Npad, sa_t,
-                         sbs, M, N, p.KB, Cbuf, acc_i32, grouped);
+                         sbs, M, N, p.KB, Cbuf, acc_i32, grouped, nullptr);
     else if (acc_i32)
       hipLaunchKernelGGL((k_qgemm_i8_v3<true, false>), g1, dim3(512), 0, st, A8, lda, arows, B8, p.KBP, p.Npad,
-                         sa_t, sbs, M, N, p.KB, Cbuf, acc_i32, grouped);
+                         sa_t, sbs, M, N, p.KB, Cbuf, acc_i32, grouped, nullptr);
     else
       hipLaunchKernelGGL((k_qgemm_i8_v3<false, true>), g1, dim3(512), 0, st, A8, lda, arows, B8, p.KBP, p.Npad,
-                         sa_t, sbs, M, N, p.KB, Cbuf, acc_i32, grouped);
+                         sa_t, sbs, M, N, p.KB, Cbuf, acc_i32, grouped, nullptr);
   } else if (p.v2) {
     const int64_t tiles_m = ceil_div(M, QG_BM), tiles_n = ceil_div(N, QG_BN);
     const int grouped = (tiles_m % 8 == 0 && tiles_n % 8 == 0 && (tiles_m * tiles_n) % 512 == 0) ? 1 : 0;
@@ -821,28 +873,100 @@ int mxk_qgemm(const void* a_packed, const float* a_scales, int64_t a_nscales, co
     }
     if (acc_i32 && wc)
       hipLaunchKernelGGL((k_qgemm_i8_v2<true, true>), g1, dim3(256), 0, st, A8, lda, arows, B8, p.KBP, p.Npad, sa_t,
-                         a_ok, b_scales, b_ok, M, N, p.KB, Cbuf, acc_i32, grouped);
+                         a_ok, b_scales, b_ok, M, N, p.KB, Cbuf, acc_i32, grouped, nullptr);
     else if (acc_i32)
       hipLaunchKernelGGL((k_qgemm_i8_v2<true, false>), g1, dim3(256), 0, st, A8, lda, arows, B8, p.KBP, p.Npad,
-                         sa_t, a_ok, b_scales, b_ok, M, N, p.KB, Cbuf, acc_i32, grouped);
+                         sa_t, a_ok, b_scales, b_ok, M, N, p.KB, Cbuf, acc_i32, grouped, nullptr);
     else
       hipLaunchKernelGGL((k_qgemm_i8_v2<false, true>), g1, dim3(256), 0, st, A8, lda, arows, B8, p.KBP, p.Npad,
-                         sa_t, a_ok, b_scales, b_ok, M, N, p.KB, Cbuf, acc_i32, grouped);
+                         sa_t, a_ok, b_scales, b_ok, M, N, p.KB, Cbuf, acc_i32, grouped, nullptr);
   } else if (acc_i32 && wc)
     hipLaunchKernelGGL((k_qgemm_i8<true, true>), grid, dim3(256), 0, st, A8, lda, arows, B8, p.KBP, p.Npad, a_scales,
-                       a_ok, b_scales, b_ok, M, N, p.KB, p.BP, Cbuf, acc_i32);
+                       a_ok, b_scales, b_ok, M, N, p.KB, p.BP, Cbuf, acc_i32, nullptr);
   else if (acc_i32)
     hipLaunchKernelGGL((k_qgemm_i8<true, false>), grid, dim3(256), 0, st, A8, lda, arows, B8, p.KBP, p.Npad,
-                       a_scales, a_ok, b_scales, b_ok, M, N, p.KB, p.BP, Cbuf, acc_i32);
+                       a_scales, a_ok, b_scales, b_ok, M, N, p.KB, p.BP, Cbuf, acc_i32, nullptr);
   else
     hipLaunchKernelGGL((k_qgemm_i8<false, true>), grid, dim3(256), 0, st, A8, lda, arows, B8, p.KBP, p.Npad,
-                       a_scales, a_ok, b_scales, b_ok, M, N, p.KB, p.BP, Cbuf, acc_i32);
+                       a_scales, a_ok, b_scales, b_ok, M, N, p.KB, p.BP, Cbuf, acc_i32, nullptr);
   int rc = check_launch("qgemm");
   if (rc != MXK_OK) return rc;
   if (out_bits > 0)
     return requant_vec_f32(Cbuf, M * N, out_bits, block, c_packed, c_packed_nbytes, c_scales, M * N, qws,
                                      p.q_bytes, st);
   return MXK_OK;
+}
+
+size_t mxk_linear_i8_workspace(int64_t M, int64_t K, int64_t N, int x_bits, int w_bits, int64_t x_block,
+                               int64_t w_block) {
+  if (M <= 0 || K <= 0 || N <= 0 || x_block <= 0 || w_block <= 0) return 0;
+  I8LinPlan p = plan_i8lin(M, K, N, x_bits, w_bits, x_block, w_block);
+  if (p.kblk == 0) return 0;
+  return p.x_bytes + p.w_bytes + p.sa_bytes + p.sb_bytes;
+}
+
+int mxk_linear_i8(const void* x_packed, int64_t x_nbytes, const float* x_scales, int64_t x_nscales, int64_t x_block,
+                  int x_bits, const void* w_packed, int64_t w_nbytes, const float* w_scales, int64_t w_nscales,
+                  int64_t w_block, int w_bits, int64_t M, int64_t K, int64_t N, const float* bias, float* out,
+                  void* workspace, size_t workspace_nbytes, void* stream) {
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  if (M <= 0 || K <= 0 || N <= 0 || x_block <= 0 || w_block <= 0)
+    return fail(MXK_EINVAL, "linear_i8: sizes must be positive");
+  if (!x_packed || !w_packed || !x_scales || !w_scales || !out) return fail(MXK_EINVAL, "linear_i8: null pointer");
+  auto width_ok = [](int b) { return b == 2 || b == 4 || b == 8; };
+  if (!width_ok(x_bits) || !width_ok(w_bits))
+    return fail(MXK_EUNSUPPORTED, "linear_i8: int code widths 2, 4 and 8 are implemented");
+  I8LinPlan p = plan_i8lin(M, K, N, x_bits, w_bits, x_block, w_block);
+  if (p.kblk == 0)
+    return fail(MXK_EUNSUPPORTED, "linear_i8: needs 64 (or 128) dividing K and both block sizes");
+  if (x_nbytes < mxk_packed_nbytes(x_bits, M * K) || w_nbytes < mxk_packed_nbytes(w_bits, N * K))
+    return fail(MXK_EINVAL, "linear_i8: packed operand shorter than its codes");
+  if (x_nscales < ceil_div(M * K, x_block) || w_nscales < ceil_div(N * K, w_block))
+    return fail(MXK_EINVAL, "linear_i8: fewer scales than blocks");
+  if ((p.direct_x && !aligned16(x_packed)) || (p.direct_w && !aligned16(w_packed)))
+    return fail(MXK_EINVAL, "linear_i8: 8-bit codes must be 16-byte aligned");
+  const size_t need = p.x_bytes + p.w_bytes + p.sa_bytes + p.sb_bytes;
+  if (!workspace || workspace_nbytes < need) return fail(MXK_EINVAL, "linear_i8: workspace too small");
+  uint8_t* ws = reinterpret_cast<uint8_t*>(workspace);
+  const int8_t* A8 = p.direct_x ? (const int8_t*)x_packed : reinterpret_cast<int8_t*>(ws);
+  const int8_t* B8 = p.direct_w ? (const int8_t*)w_packed : reinterpret_cast<int8_t*>(ws + p.x_bytes);
+  float* sa = reinterpret_cast<float*>(ws + p.x_bytes + p.w_bytes);
+  float* sb = reinterpret_cast<float*>(ws + p.x_bytes + p.w_bytes + p.sa_bytes);
+  const int cap = num_cus() * 8;
+  if (!p.direct_x) {
+    const int64_t total = p.Mpad * (K / 16);
+    hipLaunchKernelGGL(k_unpack_rows, dim3((unsigned)std::min<int64_t>(ceil_div(total, 256), cap)), dim3(256), 0, st,
+                       (const uint8_t*)x_packed, x_nbytes, x_bits, M, p.Mpad, K, K, 1, p.kblk, p.kblk, p.KB,
+                       (int8_t*)A8);
+  }
+  if (!p.direct_w) {
+    const int64_t total = p.Npad * (K / 16);
+    hipLaunchKernelGGL(k_unpack_rows, dim3((unsigned)std::min<int64_t>(ceil_div(total, 256), cap)), dim3(256), 0, st,
+                       (const uint8_t*)w_packed, w_nbytes, w_bits, N, p.Npad, K, K, 1, p.kblk, p.kblk, p.KB,
+                       (int8_t*)B8);
+  }
+  // SA: [KB][M] for v2/v3, [M][KB] for the one-stage kernel; SB: [KB][N]
+  hipLaunchKernelGGL(k_gather_scales, dim3((unsigned)std::min<int64_t>(ceil_div(M * p.KB, 256), cap)), dim3(256), 0,
+                     st, x_scales, x_nscales, M, K, x_block, p.kblk, p.KB, p.v2 ? 1 : 0, sa);
+  hipLaunchKernelGGL(k_gather_scales, dim3((unsigned)std::min<int64_t>(ceil_div(N * p.KB, 256), cap)), dim3(256), 0,
+                     st, w_scales, w_nscales, N, K, w_block, p.kblk, p.KB, 1, sb);
+  const int64_t arows = p.direct_x ? M : p.Mpad, brows = p.direct_w ? N : p.Npad;
+  if (p.v3) {
+    const int64_t tiles_m = ceil_div(M, QG3_BM), tiles_n = ceil_div(N, QG3_BN);
+    const int grouped = (tiles_m % 8 == 0 && tiles_n % 8 == 0 && (tiles_m * tiles_n) % 512 == 0) ? 1 : 0;
+    hipLaunchKernelGGL((k_qgemm_i8_v3<false, true>), dim3((unsigned)(tiles_m * tiles_n)), dim3(512), 0, st, A8, K,
+                       arows, B8, K, brows, sa, sb, M, N, p.KB, out, nullptr, grouped, bias);
+  } else if (p.v2) {
+    const int64_t tiles_m = ceil_div(M, QG_BM), tiles_n = ceil_div(N, QG_BN);
+    const int grouped = (tiles_m % 8 == 0 && tiles_n % 8 == 0 && (tiles_m * tiles_n) % 512 == 0) ? 1 : 0;
+    hipLaunchKernelGGL((k_qgemm_i8_v2<false, true>), dim3((unsigned)(tiles_m * tiles_n)), dim3(256), 0, st, A8, K,
+                       arows, B8, K, brows, sa, 1, sb, 1, M, N, p.KB, out, nullptr, grouped, bias);
+  } else {
+    const dim3 grid((unsigned)ceil_div(N, QG_BN), (unsigned)ceil_div(M, QG_BM));
+    hipLaunchKernelGGL((k_qgemm_i8<false, true>), grid, dim3(256), 0, st, A8, K, arows, B8, K, brows, sa, 1, sb, 1,
+                       M, N, p.KB, p.kblk, out, nullptr, bias);
+  }
+  return check_launch("linear_i8");
 }
 
 }  // extern "C"

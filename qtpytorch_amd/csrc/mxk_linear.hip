@@ -5,7 +5,10 @@
 // RN(code * s) (mxtorch.py:1573-1575) and never touches memory.
 //
 // Generic kernel: 64x64 output tiles, K steps of 16, weights decoded into
-// LDS, fp32 FMA accumulation.  Any M, K, N, width and block size.
+// LDS, fp32 FMA accumulation.  Any M, K, N, width and block size.  With WT
+// the weight is stored [N][K] instead (y = x @ dequant(W)^T, the layout of
+// mx_dynamic_linear's weight, mxtorch.py:8916-8917, and of the input
+// gradient of _MXLinearAutograd, mxtorch.py:6729-6740).
 #include "mxk_internal.h"
 
 #include <algorithm>
@@ -39,7 +42,7 @@ __device__ __forceinline__ float decode_weight(const uint8_t* __restrict__ packe
   }
 }
 
-template <typename T, int MODE, int BITS>
+template <typename T, int MODE, int BITS, bool WT>
 __global__ __launch_bounds__(256) void k_linear_generic(const T* __restrict__ x, int64_t M, int64_t K, int64_t N,
                                                         const uint8_t* __restrict__ packed, int64_t pbytes,
                                                         const float* __restrict__ scales, int block,
@@ -68,11 +71,12 @@ __global__ __launch_bounds__(256) void k_linear_generic(const T* __restrict__ x,
         const int64_t gm = m0 + mm, gk = k0 + kk;
         sx[kk][mm] = (gm < M && gk < K) ? ElemT<T>::cvt(x[gm * K + gk]) : 0.0f;
       }
-      // w tile: [BK][BN]
+      // w tile: [BK][BN]; consecutive threads walk the weight's contiguous dimension
       {
-        const int kk = e / BN, nn = e % BN;
+        const int kk = WT ? e % BK : e / BN, nn = WT ? e / BK : e % BN;
         const int64_t gk = k0 + kk, gn = n0 + nn;
-        sw[kk][nn] = (gk < K && gn < N) ? decode_weight<MODE, BITS>(packed, pbytes, scales, gk * N + gn, block, sG) : 0.0f;
+        const int64_t flat = WT ? gn * K + gk : gk * N + gn;
+        sw[kk][nn] = (gk < K && gn < N) ? decode_weight<MODE, BITS>(packed, pbytes, scales, flat, block, sG) : 0.0f;
       }
     }
     __syncthreads();
@@ -553,21 +557,21 @@ static bool decode_eligible(int64_t M, int64_t K, int64_t N, int kind, int bits,
   return true;
 }
 
-template <typename T, int MODE, int BITS>
+template <bool WT, typename T, int MODE, int BITS>
 static int launch_linear(const T* x, int64_t M, int64_t K, int64_t N, const uint8_t* packed, int64_t pbytes,
                          const float* scales, int block, const float* bias, float* out, hipStream_t st) {
   dim3 grid((unsigned)ceil_div(N, 64), (unsigned)ceil_div(M, 64));
-  hipLaunchKernelGGL((k_linear_generic<T, MODE, BITS>), grid, dim3(256), 0, st, x, M, K, N, packed, pbytes, scales,
-                     block, bias, out);
-  return check_launch("linear_wq");
+  hipLaunchKernelGGL((k_linear_generic<T, MODE, BITS, WT>), grid, dim3(256), 0, st, x, M, K, N, packed, pbytes,
+                     scales, block, bias, out);
+  return check_launch(WT ? "linear_wq_nt" : "linear_wq");
 }
 
-template <typename T>
+template <bool WT, typename T>
 static int linear_t(const T* x, int64_t M, int64_t K, int64_t N, const uint8_t* packed, int64_t pbytes,
                     const float* scales, int kind, int bits, int block, const float* bias, float* out,
                     hipStream_t st) {
 #define MXK_L(MODE, BITS) \
-  if (mode == MODE && bits == BITS) return launch_linear<T, MODE, BITS>(x, M, K, N, packed, pbytes, scales, block, bias, out, st);
+  if (mode == MODE && bits == BITS) return launch_linear<WT, T, MODE, BITS>(x, M, K, N, packed, pbytes, scales, block, bias, out, st);
   const int mode = kind == MXK_KIND_FLOAT ? Q_FP : (bits == 1 ? Q_INT1 : Q_INT);
   MXK_L(Q_INT1, 1)
   MXK_L(Q_INT, 2)
@@ -636,13 +640,33 @@ int mxk_linear_wq(const void* x, int x_type, int64_t M, int64_t K, const void* w
   const int64_t pbytes = mxk_packed_nbytes(bits, nb * block);
   const uint8_t* pk = reinterpret_cast<const uint8_t*>(w_packed);
   if (x_type == MXK_IN_F32)
-    return linear_t<float>((const float*)x, M, K, N, pk, pbytes, w_scales, kind, bits, block, bias, out, st);
+    return linear_t<false, float>((const float*)x, M, K, N, pk, pbytes, w_scales, kind, bits, block, bias, out, st);
   if (x_type == MXK_IN_F16)
-    return linear_t<__half>((const __half*)x, M, K, N, pk, pbytes, w_scales, kind, bits, block, bias, out, st);
+    return linear_t<false, __half>((const __half*)x, M, K, N, pk, pbytes, w_scales, kind, bits, block, bias, out, st);
   if (x_type == MXK_IN_BF16)
-    return linear_t<hip_bfloat16>((const hip_bfloat16*)x, M, K, N, pk, pbytes, w_scales, kind, bits, block, bias,
-                                  out, st);
+    return linear_t<false, hip_bfloat16>((const hip_bfloat16*)x, M, K, N, pk, pbytes, w_scales, kind, bits, block,
+                                         bias, out, st);
   return fail(MXK_EINVAL, "linear_wq: bad input type");
+}
+
+int mxk_linear_wq_nt(const void* x, int x_type, int64_t M, int64_t K, const void* w_packed, int64_t w_nbytes,
+                     const float* w_scales, int64_t w_nscales, int64_t N, int kind, int bits, int block,
+                     const float* bias, float* out, void* stream) {
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  if (M <= 0 || K <= 0 || N <= 0 || block <= 0) return fail(MXK_EINVAL, "linear_wq_nt: sizes must be positive");
+  if (!x || !w_packed || !w_scales || !out) return fail(MXK_EINVAL, "linear_wq_nt: null pointer");
+  if (w_nscales < ceil_div(N * K, block)) return fail(MXK_EINVAL, "linear_wq_nt: fewer scales than blocks");
+  if (w_nbytes < mxk_packed_nbytes(bits, N * K)) return fail(MXK_EINVAL, "linear_wq_nt: packed weight too short");
+  const uint8_t* pk = reinterpret_cast<const uint8_t*>(w_packed);
+  if (x_type == MXK_IN_F32)
+    return linear_t<true, float>((const float*)x, M, K, N, pk, w_nbytes, w_scales, kind, bits, block, bias, out, st);
+  if (x_type == MXK_IN_F16)
+    return linear_t<true, __half>((const __half*)x, M, K, N, pk, w_nbytes, w_scales, kind, bits, block, bias, out,
+                                  st);
+  if (x_type == MXK_IN_BF16)
+    return linear_t<true, hip_bfloat16>((const hip_bfloat16*)x, M, K, N, pk, w_nbytes, w_scales, kind, bits, block,
+                                        bias, out, st);
+  return fail(MXK_EINVAL, "linear_wq_nt: bad input type");
 }
 
 }  // extern "C"

@@ -78,6 +78,9 @@ class mx_linear(nn.Module):
         bias = None
         if self.apply_bias and self._mx_bias is not None:
             bias = self._mx_bias.dequantize()
+        if torch.is_grad_enabled() and x.requires_grad:
+            # the reference's F.linear(x, W_dq) carries the input gradient grad @ W_dq^T
+            return _LinearWQ.apply(x, w, bias, self.in_features, self.out_features, self._decode_scales(w))
         return ops.linear_wq(x, w._mx_packed, w._mx_scales, w._mx_dtype, self.in_features, self.out_features,
                              w._mx_block, bias=bias, w_scales_t=self._decode_scales(w))
 
@@ -106,6 +109,113 @@ class mx_linear(nn.Module):
     def extra_repr(self):
         return (f"in={self.in_features}, out={self.out_features}, dtype={self.mx_dtype.name}, "
                 f"bias={self._mx_bias is not None}")
+
+
+class _LinearWQ(torch.autograd.Function):
+    """x @ dequant(W) with W stored [in, out] (mx_linear), and its input
+    gradient grad @ dequant(W)^T (mxtorch.py:7473: F.linear(x, W_dq.t())
+    differentiates to that); the packed weight gets no gradient."""
+
+    @staticmethod
+    def forward(ctx, x, w, bias, in_features, out_features, w_scales_t):
+        ctx.w = w
+        ctx.in_features, ctx.out_features = in_features, out_features
+        return ops.linear_wq(x.detach(), w._mx_packed, w._mx_scales, w._mx_dtype, in_features, out_features,
+                             w._mx_block, bias=bias, w_scales_t=w_scales_t)
+
+    @staticmethod
+    def backward(ctx, grad):
+        w = ctx.w
+        gi = ops.linear_wq_nt(grad.contiguous(), w._mx_packed, w._mx_scales, w._mx_dtype, ctx.in_features,
+                              ctx.out_features, w._mx_block)
+        return gi, None, None, None, None, None
+
+
+class _LinearWQNT(torch.autograd.Function):
+    """x @ dequant(W)^T with W stored [out, in] (mx_dynamic_linear), and its
+    input gradient grad @ dequant(W), which is the [in, out]-layout product
+    of ops.linear_wq with the roles of the two dimensions exchanged."""
+
+    @staticmethod
+    def forward(ctx, x, w, bias, in_features, out_features):
+        ctx.w = w
+        ctx.in_features, ctx.out_features = in_features, out_features
+        return ops.linear_wq_nt(x.detach(), w._mx_packed, w._mx_scales, w._mx_dtype, out_features, in_features,
+                                w._mx_block, bias=bias)
+
+    @staticmethod
+    def backward(ctx, grad):
+        w = ctx.w
+        gi = ops.linear_wq(grad.contiguous(), w._mx_packed, w._mx_scales, w._mx_dtype, ctx.out_features,
+                           ctx.in_features, w._mx_block)
+        return gi, None, None, None, None
+
+
+class mx_dynamic_linear(nn.Module):
+    """Statically quantized weight with per-token activation quantization
+    (mxtorch.py:8870-8968).
+
+    The weight is ``mx_tensor.quantize(linear.weight)`` in nn.Linear's
+    [out, in] layout (not transposed, mxtorch.py:8916-8917), the bias is kept
+    in float.  The reference's forward quantizes the activations per token
+    (mxtorch.py:8947) but multiplies the unquantized tokens by the
+    dequantized weight (mxtorch.py:8955-8957), so its output is
+    ``x.float() @ dequant(W).t() + bias``; that is what forward computes here,
+    in one kernel that decodes the weight in registers (ops.linear_wq_nt),
+    without the unused activation quantization.
+    ``quantize_activation`` gives the per-token mx_tensor the reference builds."""
+
+    def __init__(self, in_features: int, out_features: int, weight_dtype: mx_dtype = None, act_dtype: mx_dtype = None,
+                 bias: bool = True, weight_block: int = 128):
+        super().__init__()
+        self.in_features = in_features
+        self.out_features = out_features
+        self.weight_dtype = get_mx_dtype(weight_dtype) if weight_dtype is not None else get_mx_dtype("int4d")
+        self.act_dtype = get_mx_dtype(act_dtype) if act_dtype is not None else get_mx_dtype("int8d")
+        self.weight_block = weight_block
+        self.register_buffer("weight", None)
+        self.register_buffer("bias", None)
+
+    @classmethod
+    def from_linear(cls, linear: nn.Linear, weight_dtype: Union[str, mx_dtype] = "int4d",
+                    act_dtype: Union[str, mx_dtype] = "int8d", weight_block: int = 128) -> "mx_dynamic_linear":
+        m = cls(linear.in_features, linear.out_features, get_mx_dtype(weight_dtype), get_mx_dtype(act_dtype),
+                linear.bias is not None, weight_block)
+        m.weight = mx_tensor.quantize(linear.weight.data, m.weight_dtype, weight_block)
+        m.bias = linear.bias.data.clone() if linear.bias is not None else None
+        return m
+
+    def quantize_activation(self, x: Tensor) -> mx_tensor:
+        """_dynamic_quantize_activation (mxtorch.py:8927-8943): per-token codes
+        of the activation dtype's width, block = feature count."""
+        from .tensor import dynamic_quantize
+        return dynamic_quantize(x, self.act_dtype, "per_token")
+
+    _dynamic_quantize_activation = quantize_activation
+
+    def forward(self, x: Tensor) -> Tensor:
+        x_f = x.dequantize() if isinstance(x, mx_tensor) else x
+        w = self.weight
+        if not isinstance(w, mx_tensor):
+            w = mx_tensor.quantize(w, self.weight_dtype, self.weight_block)
+        if w._mx_packed.device != x_f.device:
+            w = w._move_device(x_f.device)
+            self.weight = w
+        b = self.bias
+        if b is not None and b.device != x_f.device:
+            b = b.to(x_f.device)
+        if not ops.linear_nt_eligible(w._mx_dtype):
+            out = x_f.float().reshape(-1, self.in_features) @ w.dequantize().t()
+            out = out.reshape(*x_f.shape[:-1], self.out_features)
+            return out + b if b is not None else out
+        if torch.is_grad_enabled() and x_f.requires_grad:
+            return _LinearWQNT.apply(x_f, w, b, self.in_features, self.out_features)
+        return ops.linear_wq_nt(x_f, w._mx_packed, w._mx_scales, w._mx_dtype, self.out_features, self.in_features,
+                                w._mx_block, bias=b)
+
+    def extra_repr(self):
+        return (f"in={self.in_features}, out={self.out_features}, "
+                f"w={self.weight_dtype.name}, act={self.act_dtype.name}")
 
 
 def _replace_module(parent: nn.Module, name: str, module: nn.Module, dt: mx_dtype, block: int) -> bool:

@@ -7,6 +7,9 @@ function it replaces:
   _dequant(packed, scales, dt, n, block) -> float32[n]   mxtorch.py:1530-1597
   _qscale_gemm(...) -> (packed, scales[, C])             mxtorch.py:1299-1385, 5497-5573
   linear_wq(x, w_packed, w_scales, dt, K, N, block)      mxtorch.py:7454-7473
+  linear_wq_nt(x, w_packed, w_scales, dt, N, K, block)   mxtorch.py:8949-8962, 6729-6740
+  linear_i8(x codes, w codes, ...)                       mxtorch.py:3910-3960
+  dynamic_quantize(x, dt, granularity)                   mxtorch.py:2665-2731
 
 Inputs must live on a GPU; every computation is a HIP kernel (no CPU path).
 """
@@ -344,3 +347,125 @@ def qelementwise(op: str, a_packed: Tensor, a_scales: Tensor, b_packed: Optional
                                   scales.data_ptr() if op != "neg" else 0, L.ptr(ws), ws_bytes, L.stream_of(ap))
     L.check(rc, f"qelementwise({op}, bits={bits}, n={n}, block={block})")
     return out, scales
+
+
+_GRANULARITY = {"per_token": 0, "per_channel": 1, "per_tensor": 2}
+
+
+def dynamic_quantize(x: Tensor, dt, granularity: str = "per_token") -> Tuple[Tensor, Tensor, Tuple[int, int]]:
+    """dynamic_quantize's per_token / per_channel / per_tensor branches
+    (mxtorch.py:2706-2729) on the GPU.  Returns (packed, scales, (rows, cols))
+    where [rows, cols] is the 2-D view the reference quantizes: x.reshape(-1,
+    shape[-1]) per token, x.reshape(shape[0], -1) per channel, the flat
+    tensor per tensor (rows = 1)."""
+    dt = get_mx_dtype(dt)
+    g = _GRANULARITY[granularity]
+    dev = L.require_gpu(x)
+    if dt.bits < 2:
+        raise L.MXKError(f"dynamic_quantize: {dt.name} has max_int = 0 in the reference (scales of 1/0); "
+                         f"widths of 2 bits and more are supported")
+    xs = x if x.dtype in (torch.float32, torch.float16, torch.bfloat16) else x.float()
+    xs = xs.contiguous()
+    shape = tuple(xs.shape)
+    n = xs.numel()
+    if g == 0:
+        cols = shape[-1] if len(shape) >= 1 else 1
+    elif g == 1:
+        cols = n // shape[0] if len(shape) >= 1 and shape[0] else 1
+    else:
+        cols = n
+    rows = n // cols if cols else 0
+    nscales = rows if g == 0 else (cols if g == 1 else 1)
+    packed = packed_storage(dt.bits, n, dev)
+    scales = torch.empty(nscales, dtype=torch.float32, device=dev)
+    if n == 0:
+        return packed, scales, (rows, cols)
+    lib = L.lib()
+    ws_bytes = lib.mxk_dynamic_quantize_workspace(rows, cols, g, dt.bits)
+    ws = _workspace(ws_bytes, dev)
+    with torch.cuda.device(dev):
+        rc = lib.mxk_dynamic_quantize(xs.data_ptr(), L.elem_type(xs.dtype), rows, cols, g, dt.bits, packed.data_ptr(),
+                                      packed.numel() * packed.element_size(), scales.data_ptr(), L.ptr(ws), ws_bytes,
+                                      L.stream_of(xs))
+    L.check(rc, f"dynamic_quantize({dt.name}, {granularity}, {rows}x{cols})")
+    return packed, scales, (rows, cols)
+
+
+def linear_wq_nt(x: Tensor, w_packed: Tensor, w_scales: Tensor, dt, out_features: int, in_features: int,
+                 block: int = 128, bias: Optional[Tensor] = None) -> Tensor:
+    """y = x.float() @ dequant(W).t() (+ bias) for a weight stored [out, in]
+    (mx_dynamic_linear.forward, mxtorch.py:8949-8962, and the input gradient
+    of _MXLinearAutograd, mxtorch.py:6729-6740); the weight is decoded in
+    registers, never dequantized to memory."""
+    dt = get_mx_dtype(dt)
+    dev = L.require_gpu(x, w_packed, w_scales)
+    kind, var = _kind_variant(dt)
+    if var != L.MXK_VAR_BASE:
+        raise L.MXKError(f"linear_wq_nt: {dt.name} weights need the base variant")
+    N, K = out_features, in_features
+    if x.shape[-1] != K:
+        raise L.MXKError(f"linear_wq_nt: x has {x.shape[-1]} features, weight expects {K}")
+    lead = x.shape[:-1]
+    xc = x.reshape(-1, K)
+    if xc.dtype not in (torch.float32, torch.float16, torch.bfloat16):
+        xc = xc.float()
+    xc = xc.contiguous()
+    M = xc.shape[0]
+    out = torch.empty(M, N, dtype=torch.float32, device=dev)
+    if M == 0 or N == 0:
+        return out.reshape(*lead, N)
+    if K == 0:
+        out.zero_()
+        if bias is not None:
+            out += bias.to(device=dev, dtype=torch.float32)
+        return out.reshape(*lead, N)
+    b = None if bias is None else bias.to(device=dev, dtype=torch.float32).contiguous()
+    wp, ws = w_packed.contiguous(), w_scales.contiguous().float()
+    with torch.cuda.device(dev):
+        rc = L.lib().mxk_linear_wq_nt(xc.data_ptr(), L.elem_type(xc.dtype), M, K, wp.data_ptr(),
+                                      wp.numel() * wp.element_size(), ws.data_ptr(), ws.numel(), N, kind, dt.bits,
+                                      block, L.ptr(b), out.data_ptr(), L.stream_of(xc))
+    L.check(rc, f"linear_wq_nt({dt.name}, M={M}, K={K}, N={N})")
+    return out.reshape(*lead, N)
+
+
+def linear_nt_eligible(dt) -> bool:
+    """Weight dtypes linear_wq / linear_wq_nt decode in registers: base
+    variant, int widths 1-8 and 16, float widths 4 and 8."""
+    dt = get_mx_dtype(dt)
+    if not dt.is_base:
+        return False
+    return dt.bits in (4, 8) if dt.is_float else dt.bits in (1, 2, 3, 4, 5, 6, 7, 8, 16)
+
+
+def linear_i8_eligible(x_dt, w_dt, K: int, x_block: int, w_block: int) -> bool:
+    """Whether mxk_linear_i8 covers these operands: int codes of 2, 4 or 8
+    bits (base variant) and 64 dividing K and both block sizes."""
+    def ok(d):
+        return d.is_int and d.is_base and d.bits in (2, 4, 8)
+    return ok(x_dt) and ok(w_dt) and K > 0 and K % 64 == 0 and x_block % 64 == 0 and w_block % 64 == 0
+
+
+def linear_i8(x_packed: Tensor, x_scales: Tensor, x_dt, x_block: int, w_packed: Tensor, w_scales: Tensor, w_dt,
+              w_block: int, M: int, K: int, N: int, bias: Optional[Tensor] = None) -> Tensor:
+    """fused_int8_linear on packed int codes (mxtorch.py:3910-3960): out[M, N]
+    = dequant(x)[M, K] @ dequant(W)[N, K].t() (+ bias), the integer products on
+    int8 MFMA.  The caller checks linear_i8_eligible first."""
+    x_dt, w_dt = get_mx_dtype(x_dt), get_mx_dtype(w_dt)
+    dev = L.require_gpu(x_packed, x_scales, w_packed, w_scales)
+    out = torch.empty(M, N, dtype=torch.float32, device=dev)
+    if M == 0 or N == 0:
+        return out
+    xp, xs = x_packed.contiguous(), x_scales.contiguous().float()
+    wp, wsc = w_packed.contiguous(), w_scales.contiguous().float()
+    b = None if bias is None else bias.to(device=dev, dtype=torch.float32).contiguous()
+    lib = L.lib()
+    ws_bytes = lib.mxk_linear_i8_workspace(M, K, N, x_dt.bits, w_dt.bits, x_block, w_block)
+    ws = _workspace(ws_bytes, dev)
+    with torch.cuda.device(dev):
+        rc = lib.mxk_linear_i8(xp.data_ptr(), xp.numel() * xp.element_size(), xs.data_ptr(), xs.numel(), x_block,
+                               x_dt.bits, wp.data_ptr(), wp.numel() * wp.element_size(), wsc.data_ptr(), wsc.numel(),
+                               w_block, w_dt.bits, M, K, N, L.ptr(b), out.data_ptr(), L.ptr(ws), ws_bytes,
+                               L.stream_of(xp))
+    L.check(rc, f"linear_i8({x_dt.name} x {w_dt.name}, {M}x{K}x{N})")
+    return out

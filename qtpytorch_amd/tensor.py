@@ -263,6 +263,10 @@ class mx_tensor(torch.Tensor):
     def __getitem__(self, idx):
         return mx_tensor.quantize(self.dequantize()[idx], self._mx_dtype, self._mx_block)
 
+    def fused_int8_linear(self, weight, bias=None):
+        """Tensor-method binding of fused_int8_linear (mxtorch.py:11980-11982)."""
+        return fused_int8_linear(self, weight, bias)
+
     def __reduce_ex__(self, protocol):
         return (_rebuild_mxtensor, (self._mx_packed.cpu(), self._mx_scales.cpu(), self._mx_dtype.name,
                                     tuple(self._mx_orig_shape), self._mx_n, self._mx_block))
@@ -425,3 +429,117 @@ def mx_matmul(a: Tensor, b: Tensor, dtype="int4d", block: int = 128):
 def mx_quantize(x: Tensor, dtype="int4d", block: int = 128) -> mx_tensor:
     """Alias of mx_tensor.quantize (mxtorch.py:7391-7396)."""
     return mx_tensor.quantize(x, get_mx_dtype(dtype), block)
+
+
+# ---------------------------------------------------------------- dynamic activations, int8 x int8 linear
+def dynamic_quantize(x: Tensor, dtype="int8d", granularity: str = "per_token", block: int = 64) -> mx_tensor:
+    """dynamic_quantize (mxtorch.py:2665-2731): scales computed from the
+    input at run time with max_int = 2^(bits-1)-1 of the dtype's width.
+
+    per_token    one scale per row of x.reshape(-1, shape[-1]), block = row length;
+    per_channel  one scale per column of x.reshape(shape[0], -1), block =
+                 shape[0] (as the reference stores it: the scales are per
+                 column, the block records the row count);
+    per_tensor   one scale, block = numel;
+    otherwise    mx_tensor.quantize(x, dtype, block) (per_block).
+    Codes are packed as ints of the dtype's width whatever its kind, as in
+    the reference."""
+    dt = get_mx_dtype(dtype) if isinstance(dtype, str) else dtype
+    if isinstance(x, mx_tensor):
+        x = x.dequantize()
+    if granularity not in ("per_token", "per_channel", "per_tensor"):
+        return mx_tensor.quantize(x.float(), dt, block)
+    shape = x.shape
+    packed, scales, (rows, cols) = ops.dynamic_quantize(x, dt, granularity)
+    n = rows * cols
+    if granularity == "per_token":
+        return mx_tensor(packed, scales, dt, torch.Size([rows, cols]), n, cols).reshape(*shape)
+    if granularity == "per_channel":
+        return mx_tensor(packed, scales, dt, torch.Size([rows, cols]), n, rows).reshape(*shape)
+    return mx_tensor(packed, scales, dt, torch.Size(shape), n, n)
+
+
+def fused_int8_linear(x, weight, bias: Optional[Tensor] = None, block: int = 128) -> Tensor:
+    """fused_int8_linear (mxtorch.py:3910-3960): the reference's result is
+    F.linear(x.dequantize(), weight.dequantize(), bias) (mxtorch.py:3957-3960)
+    for x [..., K] and weight [N, K].
+
+    Packed int operands (widths 2-8, 64 dividing K and both block sizes;
+    per-token activations from dynamic_quantize qualify) run on int8 MFMA
+    (ops.linear_i8).  Other packed weights are decoded in registers
+    (ops.linear_wq_nt) after dequantizing x; plain float tensors take
+    F.linear."""
+    import torch.nn.functional as F
+
+    if isinstance(x, mx_tensor) and isinstance(weight, mx_tensor):
+        xs, ws = x._mx_orig_shape, weight._mx_orig_shape
+        if len(ws) == 2 and len(xs) >= 1 and xs[-1] == ws[1]:
+            N, K = int(ws[0]), int(ws[1])
+            M = x._mx_n // K if K else 0
+            if ops.linear_i8_eligible(x._mx_dtype, weight._mx_dtype, K, x._mx_block, weight._mx_block):
+                out = ops.linear_i8(x._mx_packed, x._mx_scales, x._mx_dtype, x._mx_block, weight._mx_packed,
+                                    weight._mx_scales, weight._mx_dtype, weight._mx_block, M, K, N, bias)
+                return out.reshape(*xs[:-1], N)
+    x_f = x.dequantize() if isinstance(x, mx_tensor) else x
+    if isinstance(weight, mx_tensor):
+        ws = weight._mx_orig_shape
+        if len(ws) == 2 and ops.linear_nt_eligible(weight._mx_dtype):
+            return ops.linear_wq_nt(x_f, weight._mx_packed, weight._mx_scales, weight._mx_dtype, int(ws[0]),
+                                    int(ws[1]), weight._mx_block, bias=bias)
+        weight = weight.dequantize()
+    return F.linear(x_f, weight, bias)
+
+
+class mx_fused_ops:
+    """Namespace of the reference's fused ops that lie on this path
+    (mxtorch.py:11395-11405)."""
+
+    @staticmethod
+    def fused_int8_linear(x, weight, bias: Optional[Tensor] = None, block: int = 128) -> Tensor:
+        return fused_int8_linear(x, weight, bias, block)
+
+
+class _MXLinearAutograd(torch.autograd.Function):
+    """mx_linear's quantized-activation forward with a float input gradient
+    (mxtorch.py:6693-6746).
+
+    forward: quantize x (2-D view) with mx_dtype, packed GEMM with the
+    [in, out] weight (_mx_mm -> _dispatch_qgemm, packed output), dequantize,
+    add the dequantized bias.  backward: grad @ dequant(W).t(), with W decoded
+    in registers (ops.linear_wq_nt); no gradient for the packed weight."""
+
+    @staticmethod
+    def forward(ctx, x: Tensor, w_mx: "mx_tensor", b_mx, mx_dtype, block, in_features, out_features) -> Tensor:
+        orig_shape = x.shape
+        x_2d = x.reshape(-1, in_features) if x.dim() > 2 else x
+        with torch.no_grad():
+            x_mx = mx_tensor.quantize(x_2d.detach(), mx_dtype, block)
+            out = _mx_mm(x_mx, w_mx).dequantize().detach()
+        if len(orig_shape) > 2:
+            out = out.reshape(*orig_shape[:-1], out_features)
+        if b_mx is not None:
+            with torch.no_grad():
+                b_f = b_mx.dequantize().detach()
+            if len(orig_shape) > 2:
+                b_f = b_f.unsqueeze(0)
+            out = out + b_f
+        ctx.w_mx = w_mx
+        ctx.orig_shape = orig_shape
+        ctx.in_features = in_features
+        return out
+
+    @staticmethod
+    def backward(ctx, grad_output: Tensor):
+        w = ctx.w_mx
+        ws = w._mx_orig_shape   # [in, out] for mx_linear's weight
+        grad_2d = grad_output.reshape(-1, ws[1]) if grad_output.dim() > 2 else grad_output
+        gi = ops.linear_wq_nt(grad_2d.contiguous(), w._mx_packed, w._mx_scales, w._mx_dtype, int(ws[0]), int(ws[1]),
+                              w._mx_block)
+        if len(ctx.orig_shape) > 2:
+            gi = gi.reshape(*ctx.orig_shape[:-1], ctx.in_features)
+        return gi, None, None, None, None, None, None
+
+
+def _mx_linear_forward(x: Tensor, w_mx: "mx_tensor", b_mx, mx_dtype, block, in_features, out_features) -> Tensor:
+    """mxtorch.py:6749-6752."""
+    return _MXLinearAutograd.apply(x, w_mx, b_mx, mx_dtype, block, in_features, out_features)

@@ -31,7 +31,7 @@ def test_library_exports_every_declared_symbol():
     for name in declared:
         assert hasattr(h, name), f"libmxk.so does not export {name}"
         assert name in L.SIGNATURES, f"ctypes binding lacks {name}"
-    assert h.mxk_abi_version() == 3
+    assert h.mxk_abi_version() == L.ABI_VERSION
 
 
 @pytest.mark.parametrize("bits", [1, 2, 3, 4, 5, 6, 7, 8, 16])
