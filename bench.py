@@ -309,6 +309,61 @@ def bench_kv_stream(qa, steps):
     return out
 
 
+def bench_dynamic(qa, steps, reps):
+    """The int8 x int8 / dynamic-activation row (mxtorch.py:2665-2731,
+    3910-3960, 8870-8968):
+      * mx_dynamic_linear forward at config 2's decode shape: x fp32 [16, 8192]
+        @ dequant(W int4d stored [8192 out][8192 in], block 128 along in).T,
+        12 rotated layers as for the headline; HBM-bound, same algorithmic
+        bytes as config 2;
+      * fused_int8_linear with per-token int8 activations [8192, 8192] and int8d
+        weights [8192, 8192] block 128: 2*8192^3 int8 ops on MFMA;
+      * dynamic_quantize per token of fp32 [8192, 8192] to int8: 4 B read +
+        1 B written per element + 4 B per row."""
+    dev = torch.device("cuda:0")
+    out = {}
+    x_cpu, W_cpu = config2_inputs()
+    K = N = 8192
+    lin = torch.nn.Linear(K, N, bias=False)
+    with torch.no_grad():
+        lin.weight.copy_(W_cpu)
+    lin = lin.to(dev)
+    layers = [qa.mx_dynamic_linear.from_linear(lin, "int4d", "int8d") for _ in range(N_LAYERS)]
+    del lin
+    x = x_cpu.to(dev)
+    it = [0]
+
+    def step():
+        layers[it[0] % N_LAYERS](x)
+        it[0] += 1
+
+    t = graph_time(step, steps, 5)
+    algo = K * N // 2 + (K * N // 128) * 4 + 16 * K * 4 + 16 * N * 4
+    out["dynamic_linear_int4d_decode_16x8192x8192"] = {
+        "us": round(t * 1e6, 2), "GBs": round(algo / t / 1e9, 1), "frac": round(algo / t / 1e9 / HBM_PEAK_GBS, 4),
+        "bytes": algo}
+    del layers
+    torch.cuda.empty_cache()
+
+    M = 8192
+    xa = torch.randn(M, K, generator=gen(15, "cuda"), device=dev)
+    wa = torch.randn(N, K, generator=gen(16, "cuda"), device=dev) * 0.02
+    xq = qa.dynamic_quantize(xa, "int8d", "per_token")
+    wq = qa.mx_tensor.quantize(wa, qa.get_mx_dtype("int8d"), 128)
+    t = graph_time(lambda: qa.fused_int8_linear(xq, wq), reps, 1, repeats=5)
+    ops = 2.0 * M * K * N
+    out["fused_int8_linear_per_token_8192"] = {"us": round(t * 1e6, 2), "TOPS": round(ops / t / 1e12, 2),
+                                               "frac_int8_peak": round(ops / t / 1e12 / INT8_PEAK_TOPS, 4)}
+    del wa, wq, xq
+    torch.cuda.empty_cache()
+    t = graph_time(lambda: qa.dynamic_quantize(xa, "int8d", "per_token"), reps, 1, repeats=3)
+    algo = M * K * 5 + M * 4
+    out["dynamic_quantize_per_token_8192x8192"] = {
+        "us": round(t * 1e6, 2), "GBs": round(algo / t / 1e9, 1), "frac": round(algo / t / 1e9 / HBM_PEAK_GBS, 4),
+        "bytes": algo}
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -316,7 +371,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-extras", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--only", default="", help="comma list of extras: quant,gemm,kv,kvstream,elementwise,small")
+    ap.add_argument("--only", default="",
+                    help="comma list of extras: quant,gemm,kv,kvstream,elementwise,small,dynamic")
     ap.add_argument("--eager", action="store_true", help="no graph capture (for rocprofv3 --pmc runs)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a plain 512 MiB device copy (the reference kernel for HBM counter scaling)")
@@ -380,6 +436,8 @@ def main():
             extras["elementwise_2e28_block128"] = bench_elementwise(qa, 5)
         if not only or "kvstream" in only:
             extras["kv_ring_stream_8x32x128_T4096"] = bench_kv_stream(qa, 64)
+        if not only or "dynamic" in only:
+            extras["dynamic_int8"] = bench_dynamic(qa, 120, 5)
         line["extras"] = extras
     print(json.dumps(line))
 

@@ -235,10 +235,16 @@ int mxk_qelementwise(int op, const void* a_packed, int64_t a_nbytes, const float
  * _MXLinearAutograd.backward (mxtorch.py:6729-6740: grad @ w_dq.t()).
  * W: packed codes of any width/kind of mxk_quantize (base variant), flat
  * blocks of `block` elements of the row-major [N][K] weight, w_nscales >=
- * ceil(N*K/block).  Float32 accumulation. */
+ * ceil(N*K/block).  Float32 accumulation.  With int4 codes, block 128 and
+ * M <= 16 the K sum is split over workgroups (workspace below). */
 int mxk_linear_wq_nt(const void* x, int x_type, int64_t M, int64_t K, const void* w_packed, int64_t w_nbytes,
                      const float* w_scales, int64_t w_nscales, int64_t N, int kind, int bits, int block,
-                     const float* bias, float* out, void* stream);
+                     const float* bias, float* out, void* workspace, size_t workspace_nbytes, void* stream);
+
+/* Workspace bytes mxk_linear_wq_nt needs (0 if none): the decode path (int4
+ * base codes, block 128, M <= 16, K % 128 == 0, N % 16 == 0) splits K over
+ * workgroups of 1024 rows of K and sums their partials in a second launch. */
+size_t mxk_linear_nt_workspace(int64_t M, int64_t K, int64_t N, int bits, int block);
 
 /* Workspace bytes mxk_linear_i8 needs (0 when the shapes are not covered). */
 size_t mxk_linear_i8_workspace(int64_t M, int64_t K, int64_t N, int x_bits, int w_bits, int64_t x_block,

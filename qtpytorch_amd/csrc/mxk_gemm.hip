@@ -402,7 +402,7 @@ __device__ __forceinline__ void qg3_lgkm_wait(i32x4& v) {
   asm volatile("s_waitcnt lgkmcnt(%1)" : "+v"(v) : "n"(N));
 }
 
-template <bool WRITE_ACC, bool WRITE_C>
+template <bool WRITE_ACC, bool WRITE_C, bool ROWSCALE = false>
 __global__ __launch_bounds__(512, 1) void k_qgemm_i8_v3(const int8_t* __restrict__ A8, int64_t lda, int64_t Arows,
                                                         const int8_t* __restrict__ B8, int64_t ldb, int64_t Brows,
                                                         const float* __restrict__ sa_t,
@@ -505,10 +505,15 @@ __global__ __launch_bounds__(512, 1) void k_qgemm_i8_v3(const int8_t* __restrict
   i32x4 p3[4] = {{0, 0, 0, 0}, {0, 0, 0, 0}, {0, 0, 0, 0}, {0, 0, 0, 0}};
   i32x4 sa3 = {0, 0, 0, 0}, sb3 = {0, 0, 0, 0};
 
-  // C = RN(C + RN(RN(P*SA)*SB)) for output (slice a, row i, fragment t) of K block kbw
+  // C = RN(C + RN(RN(P*SA)*SB)) for output (slice a, row i, fragment t) of K block kbw;
+  // ROWSCALE (SA the same in every K block of a row): C = fma(P, SB, C), times SA at the end
   auto epi_elem = [&](int a, int i, int t, const i32x4 (&p)[4], const i32x4& sav, const i32x4& sbvv, int kbw) {
-    const float v = ((float)p[t][i] * __int_as_float(sav[i])) * __int_as_float(sbvv[t]);
-    c[a][t][i] = c[a][t][i] + v;
+    if constexpr (ROWSCALE) {
+      c[a][t][i] = __builtin_fmaf((float)p[t][i], __int_as_float(sbvv[t]), c[a][t][i]);
+    } else {
+      const float v = ((float)p[t][i] * __int_as_float(sav[i])) * __int_as_float(sbvv[t]);
+      c[a][t][i] = c[a][t][i] + v;
+    }
     if (WRITE_ACC) {
       const int64_t row = m0 + wm * 64 + a * 16 + lg * 4 + i;
       const int64_t col = n0 + wn * 64 + t * 16 + lr;
@@ -664,10 +669,12 @@ __global__ __launch_bounds__(512, 1) void k_qgemm_i8_v3(const int8_t* __restrict
       for (int i = 0; i < 4; ++i) {
         const int64_t row = m0 + wm * 64 + a * 16 + lg * 4 + i;
         if (row >= M) continue;
+        const float rs = ROWSCALE ? sa_t[row] : 1.0f;
 #pragma unroll
         for (int b = 0; b < 4; ++b) {
           const int64_t col = n0 + wn * 64 + b * 16 + lr;
-          if (col < N) C[row * N + col] = bias ? c[a][b][i] + bias[col] : c[a][b][i];
+          const float v = ROWSCALE ? c[a][b][i] * rs : c[a][b][i];
+          if (col < N) C[row * N + col] = bias ? v + bias[col] : v;
         }
       }
   }
@@ -954,8 +961,13 @@ int mxk_linear_i8(const void* x_packed, int64_t x_nbytes, const float* x_scales,
   if (p.v3) {
     const int64_t tiles_m = ceil_div(M, QG3_BM), tiles_n = ceil_div(N, QG3_BN);
     const int grouped = (tiles_m % 8 == 0 && tiles_n % 8 == 0 && (tiles_m * tiles_n) % 512 == 0) ? 1 : 0;
-    hipLaunchKernelGGL((k_qgemm_i8_v3<false, true>), dim3((unsigned)(tiles_m * tiles_n)), dim3(512), 0, st, A8, K,
-                       arows, B8, K, brows, sa, sb, M, N, p.KB, out, nullptr, grouped, bias);
+    // per-token activations (one x scale per row): the row scale leaves the K loop
+    if (x_block % K == 0)
+      hipLaunchKernelGGL((k_qgemm_i8_v3<false, true, true>), dim3((unsigned)(tiles_m * tiles_n)), dim3(512), 0, st,
+                         A8, K, arows, B8, K, brows, sa, sb, M, N, p.KB, out, nullptr, grouped, bias);
+    else
+      hipLaunchKernelGGL((k_qgemm_i8_v3<false, true>), dim3((unsigned)(tiles_m * tiles_n)), dim3(512), 0, st, A8, K,
+                         arows, B8, K, brows, sa, sb, M, N, p.KB, out, nullptr, grouped, bias);
   } else if (p.v2) {
     const int64_t tiles_m = ceil_div(M, QG_BM), tiles_n = ceil_div(N, QG_BN);
     const int grouped = (tiles_m % 8 == 0 && tiles_n % 8 == 0 && (tiles_m * tiles_n) % 512 == 0) ? 1 : 0;

@@ -468,6 +468,246 @@ static void launch_transpose_scales(const float* s, int64_t K, int64_t NB, float
   hipLaunchKernelGGL(k_transpose_scales, grid, dim3(256), 0, st, s, K, NB, sT);
 }
 
+// ---------------------------------------------------------------- int4 decode, weight [N][K]
+// y[m, n] = sum_k x[m,k] * RN(code[n,k] * s[n, k/128]) for a weight stored
+// [N][K] with blocks of 128 along K (mx_dynamic_linear's quantize(weight),
+// mxtorch.py:8916-8917; the input gradient of mx_linear / _MXLinearAutograd,
+// mxtorch.py:6729-6740), M <= 16.
+//
+// A workgroup of 16 waves owns 256 columns (rows of W) and 8 blocks of K.
+// Wave (q, h) takes block q and the 8 tiles of 16 columns of half h.  The
+// scale of a block is one per column, so x needs no scaling: the workgroup
+// stages x[16][1024] once in LDS as f16 hi + lo (22 significant bits), in
+// the v_mfma_f32_16x16x32_f16 A layout, and every wave reads it.
+//
+// Lane (j = lane&15, g = lane>>4) loads the 16 bytes at byte 16g of column
+// n's 64-byte block segment: codes k = 32g .. 32g+31 of the block.  MFMA
+// step s takes codes 32g+8s .. 32g+8s+7 of every lane group, so the A lane
+// (i, g) of step s holds x[i][32g+8s .. 32g+8s+7]: the sum over k is the
+// same, taken in another order.  B holds code+8 as the f16 denormal
+// (code+8)*2^-24 (nibble isolated, sign bit flipped, placed by v_perm_b32);
+// a correction tile with B = 8*2^-24 removes the offset:
+//   y += s * 2^24 * (D - D_corr).
+// x is staged as x * 2^-e, the power of two that puts the workgroup's
+// largest |x| in [2^14, 2^15); 2^e returns after the scale.
+//
+// The 8 waves of a column half meet in LDS and sum their partials in block
+// order.  With more than one K split the workgroup writes its partial to
+// partials[split][16][N] and k_sum_splits adds them in split order (+ bias).
+#define NT_WAVES 16
+#define NT_THREADS 1024
+#define NT_COLS 256
+#define NT_BLKS 8
+#define NT_RED_STRIDE 260  // LDS row stride of the partial sums (floats)
+
+template <typename T>
+__global__ __launch_bounds__(NT_THREADS, 1) void k_linear_w4t_decode(
+    const T* __restrict__ x, int M, int64_t K, int64_t N, const uint8_t* __restrict__ w,
+    const float* __restrict__ scales, const float* __restrict__ bias, float* __restrict__ out,
+    float* __restrict__ partials, int S) {
+  // A staging (8 blocks x 4 steps x hi/lo x 1 KiB = 64 KiB), then the
+  // partial sums [8 blocks][16 rows][256 (+4) columns]
+  __shared__ __attribute__((aligned(16))) float lds[NT_BLKS * 16 * NT_RED_STRIDE];
+  __shared__ float s_wmax[NT_WAVES];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int j = lane & 15, g = lane >> 4;
+  const int cg = (int)(blockIdx.x / S), ks = (int)(blockIdx.x % S);
+  const int64_t KB = K / 128;
+  const int64_t kb0 = (int64_t)ks * NT_BLKS;
+  const int q = wave & 7, h = wave >> 3;
+  const int64_t kb = kb0 + q;
+  const bool live = kb < KB;  // wave-uniform
+  const int64_t n0 = (int64_t)cg * NT_COLS + h * 128;
+
+  // ---- requests in arrival order: x chunks, then weights and scales
+  constexpr int EPL = 16 / (int)sizeof(T);   // elements per 16-byte load
+  constexpr int LPC = 8 / EPL;               // loads per 8-element chunk
+  const __amdgpu_buffer_rsrc_t rx = make_rsrc(x, (uint32_t)((int64_t)M * K * sizeof(T)));
+  u32x4 xr[2][LPC];
+#pragma unroll
+  for (int r = 0; r < 2; ++r) {
+    const int c = threadIdx.x + NT_THREADS * r;   // chunk: row c >> 7, 8 elements at 8 * (c & 127)
+    const int m = c >> 7, kk = c & 127;
+    const int64_t k = kb0 * 128 + 8 * kk;
+    const bool ok = m < M && k < K;
+#pragma unroll
+    for (int l = 0; l < LPC; ++l)
+      xr[r][l] = buf_load_b128(rx, ok ? (uint32_t)(((int64_t)m * K + k + l * EPL) * sizeof(T)) : DEC_OOB, 0u);
+  }
+  const __amdgpu_buffer_rsrc_t rw = make_rsrc(w, (uint32_t)(N * K / 2));
+  const __amdgpu_buffer_rsrc_t rs = make_rsrc(scales, (uint32_t)(N * KB * 4));
+  u32x4 wv[8];
+  float sc[8];
+  if (live) {
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+      const int64_t n = std::min<int64_t>(n0 + 16 * t + j, N - 1);
+      wv[t] = buf_load_b128(rw, (uint32_t)(n * (K / 2) + kb * 64 + 16 * g), 0u);
+    }
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+      const int64_t n = std::min<int64_t>(n0 + 16 * t + j, N - 1);
+      sc[t] = __uint_as_float(buf_load_b32(rs, (uint32_t)((n * KB + kb) * 4), 0u));
+    }
+  }
+  __builtin_amdgcn_sched_barrier(0);
+
+  // ---- x to float, the workgroup's largest |x|
+  float xv[2][8];
+  float mx = 0.0f;
+#pragma unroll
+  for (int r = 0; r < 2; ++r) {
+    if constexpr (EPL == 4) {
+#pragma unroll
+      for (int l = 0; l < 2; ++l)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) xv[r][4 * l + e] = __uint_as_float(xr[r][l][e]);
+    } else {
+      const T* tt = reinterpret_cast<const T*>(&xr[r][0]);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) xv[r][e] = ElemT<T>::cvt(tt[e]);
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) mx = fmaxf(mx, __builtin_fabsf(xv[r][e]));
+  }
+  mx = group_max<64>(mx);
+  if (lane == 0) s_wmax[wave] = mx;
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the LDS write above (vmcnt untouched)
+  dec_barrier_nofence();
+  float wmax = 0.0f;
+#pragma unroll
+  for (int i = 0; i < NT_WAVES; ++i) wmax = fmaxf(wmax, s_wmax[i]);
+  // 2^-shift brings the largest |x| into [2^14, 2^15): within the f16 range,
+  // and the rest of x as far above the f16 denormals as it can be
+  const int bexp = (int)((__float_as_uint(wmax) >> 23) & 0xFFu);
+  const int shift = (bexp == 0 || bexp == 0xFF) ? 0 : bexp - 127 - 14;
+  const float xs = __builtin_ldexpf(1.0f, -shift);
+
+  // ---- stage hi / lo: chunk (m, kk) -> block kk >> 4, lane group (kk >> 2) & 3, step kk & 3
+#pragma unroll
+  for (int r = 0; r < 2; ++r) {
+    const int c = threadIdx.x + NT_THREADS * r;
+    const int m = c >> 7, kk = c & 127;
+    const int blk = kk >> 4, gg = (kk >> 2) & 3, st = kk & 3;
+    uint32_t hw[4], lw[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float a = xv[r][2 * e] * xs, b = xv[r][2 * e + 1] * xs;
+      auto hp = __builtin_amdgcn_cvt_pkrtz(a, b);
+      auto lp = __builtin_amdgcn_cvt_pkrtz(a - (float)hp[0], b - (float)hp[1]);
+      hw[e] = __builtin_bit_cast(uint32_t, hp);
+      lw[e] = __builtin_bit_cast(uint32_t, lp);
+    }
+    float* base = lds + ((blk * 4 + st) * 2) * 256 + (m + 16 * gg) * 4;
+    *reinterpret_cast<u32x4*>(base) = u32x4{hw[0], hw[1], hw[2], hw[3]};
+    *reinterpret_cast<u32x4*>(base + 256) = u32x4{lw[0], lw[1], lw[2], lw[3]};
+  }
+  __builtin_amdgcn_s_waitcnt(0xC07F);
+  dec_barrier_nofence();
+
+  // ---- MFMA: 4 steps x (8 tiles + the correction tile) x hi/lo
+  f32x4 acc[8];
+#pragma unroll
+  for (int t = 0; t < 8; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+  f32x4 corr = f32x4{0.f, 0.f, 0.f, 0.f};
+  if (live) {
+    const f16x8 b8 = __builtin_bit_cast(f16x8, u32x4v{0x00080008u, 0x00080008u, 0x00080008u, 0x00080008u});
+#pragma unroll
+    for (int st = 0; st < 4; ++st) {
+      const float* ab = lds + ((q * 4 + st) * 2) * 256 + lane * 4;
+      const f16x8 ahi = __builtin_bit_cast(f16x8, *reinterpret_cast<const u32x4*>(ab));
+      const f16x8 alo = __builtin_bit_cast(f16x8, *reinterpret_cast<const u32x4*>(ab + 256));
+      corr = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi, b8, corr, 0, 0, 0);
+      corr = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo, b8, corr, 0, 0, 0);
+#pragma unroll
+      for (int t = 0; t < 8; ++t) {
+        const uint32_t wd = wv[t][st];
+        const uint32_t lo = (wd & 0x0F0F0F0Fu) ^ 0x08080808u;
+        const uint32_t hi = ((wd >> 4) & 0x0F0F0F0Fu) ^ 0x08080808u;
+        const uint32_t d0 = __builtin_amdgcn_perm(hi, lo, 0x0C040C00u);
+        const uint32_t d1 = __builtin_amdgcn_perm(hi, lo, 0x0C050C01u);
+        const uint32_t d2 = __builtin_amdgcn_perm(hi, lo, 0x0C060C02u);
+        const uint32_t d3 = __builtin_amdgcn_perm(hi, lo, 0x0C070C03u);
+        const f16x8 bt = __builtin_bit_cast(f16x8, u32x4v{d0, d1, d2, d3});
+        acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi, bt, acc[t], 0, 0, 0);
+        acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo, bt, acc[t], 0, 0, 0);
+      }
+    }
+  }
+  // every wave is done reading the staged x before the partials overwrite it
+  __syncthreads();
+  {
+    float* red = lds + (q * 16) * NT_RED_STRIDE + h * 128;
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+      const float sf = live ? sc[t] * 16777216.0f : 0.0f;
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        red[(4 * g + i) * NT_RED_STRIDE + 16 * t + j] = __builtin_ldexpf(sf * (acc[t][i] - corr[i]), shift);
+    }
+  }
+  __syncthreads();
+  // thread: row m, columns c .. c+3, summed over the 8 blocks in order
+  const int m = threadIdx.x >> 6, c = 4 * (threadIdx.x & 63);
+  f32x4 sum = *reinterpret_cast<const f32x4*>(lds + m * NT_RED_STRIDE + c);
+#pragma unroll
+  for (int b = 1; b < NT_BLKS; ++b) sum += *reinterpret_cast<const f32x4*>(lds + (b * 16 + m) * NT_RED_STRIDE + c);
+  const int64_t n = (int64_t)cg * NT_COLS + c;
+  if (m >= M || n >= N) return;
+  if (S == 1) {
+    if (bias) sum += *reinterpret_cast<const f32x4*>(bias + n);
+    *reinterpret_cast<f32x4*>(out + (int64_t)m * N + n) = sum;
+  } else {
+    *reinterpret_cast<f32x4*>(partials + ((int64_t)ks * 16 + m) * N + n) = sum;
+  }
+}
+
+// out[m][n] = sum over splits in order of partials[s][m][n] (+ bias[n]), 4 columns per thread
+__global__ __launch_bounds__(256) void k_sum_splits(const float* __restrict__ partials, int S, int M, int64_t N,
+                                                    const float* __restrict__ bias, float* __restrict__ out) {
+  const int64_t per_row = N / 4;
+  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= (int64_t)M * per_row) return;
+  const int64_t m = t / per_row, n = 4 * (t % per_row);
+  f32x4 sum = *reinterpret_cast<const f32x4*>(partials + m * N + n);
+  for (int s = 1; s < S; ++s) sum += *reinterpret_cast<const f32x4*>(partials + ((int64_t)s * 16 + m) * N + n);
+  if (bias) sum += *reinterpret_cast<const f32x4*>(bias + n);
+  *reinterpret_cast<f32x4*>(out + m * N + n) = sum;
+}
+
+static bool nt_decode_eligible(int64_t M, int64_t K, int64_t N, int kind, int bits, int block, const void* x,
+                               int x_type, int64_t w_nbytes, int64_t w_nscales) {
+  if (kind != MXK_KIND_INT || bits != 4 || block != 128) return false;
+  if (M < 1 || M > 16 || K % 128 != 0 || N % 16 != 0) return false;
+  if (!aligned16(x) || w_nbytes < N * K / 2 || w_nscales < N * (K / 128)) return false;
+  const int esz = x_type == MXK_IN_F32 ? 4 : 2;
+  const int64_t lim = int64_t(1) << 31;
+  return N * K / 2 < lim && N * (K / 128) * 4 < lim && 16 * K * esz < lim;
+}
+
+static int nt_splits(int64_t K) { return (int)ceil_div(K / 128, NT_BLKS); }
+
+static size_t nt_partial_bytes(int64_t K, int64_t N) {
+  const int S = nt_splits(K);
+  return S > 1 ? (size_t)S * 16 * (size_t)N * 4 : 0;
+}
+
+template <typename T>
+static int launch_nt_decode(const T* x, int64_t M, int64_t K, int64_t N, const uint8_t* w, const float* scales,
+                            const float* bias, float* out, float* partials, hipStream_t st) {
+  const int S = nt_splits(K);
+  const int64_t groups = ceil_div(N, NT_COLS);
+  hipLaunchKernelGGL((k_linear_w4t_decode<T>), dim3((unsigned)(groups * S)), dim3(NT_THREADS), 0, st, x, (int)M, K,
+                     N, w, scales, bias, out, partials, S);
+  if (S > 1) {
+    const int64_t threads = M * (N / 4);
+    hipLaunchKernelGGL(k_sum_splits, dim3((unsigned)ceil_div(threads, 256)), dim3(256), 0, st, partials, S, (int)M,
+                       N, bias, out);
+  }
+  return check_launch("linear_wq_nt(decode)");
+}
+
 struct DecodePlan {
   int S, steps, nbw, xcd_map;
   size_t partial_bytes, counter_bytes, scales_t_bytes;
@@ -649,15 +889,30 @@ int mxk_linear_wq(const void* x, int x_type, int64_t M, int64_t K, const void* w
   return fail(MXK_EINVAL, "linear_wq: bad input type");
 }
 
+size_t mxk_linear_nt_workspace(int64_t M, int64_t K, int64_t N, int bits, int block) {
+  if (M < 1 || M > 16 || bits != 4 || block != 128 || K <= 0 || N <= 0 || K % 128 != 0 || N % 16 != 0) return 0;
+  return nt_partial_bytes(K, N);
+}
+
 int mxk_linear_wq_nt(const void* x, int x_type, int64_t M, int64_t K, const void* w_packed, int64_t w_nbytes,
                      const float* w_scales, int64_t w_nscales, int64_t N, int kind, int bits, int block,
-                     const float* bias, float* out, void* stream) {
+                     const float* bias, float* out, void* workspace, size_t workspace_nbytes, void* stream) {
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   if (M <= 0 || K <= 0 || N <= 0 || block <= 0) return fail(MXK_EINVAL, "linear_wq_nt: sizes must be positive");
   if (!x || !w_packed || !w_scales || !out) return fail(MXK_EINVAL, "linear_wq_nt: null pointer");
   if (w_nscales < ceil_div(N * K, block)) return fail(MXK_EINVAL, "linear_wq_nt: fewer scales than blocks");
   if (w_nbytes < mxk_packed_nbytes(bits, N * K)) return fail(MXK_EINVAL, "linear_wq_nt: packed weight too short");
   const uint8_t* pk = reinterpret_cast<const uint8_t*>(w_packed);
+  if (nt_decode_eligible(M, K, N, kind, bits, block, x, x_type, w_nbytes, w_nscales)) {
+    const size_t need = nt_partial_bytes(K, N);
+    if (need > 0 && (!workspace || workspace_nbytes < need))
+      return fail(MXK_EINVAL, "linear_wq_nt: decode path needs a workspace of mxk_linear_nt_workspace() bytes");
+    float* part = reinterpret_cast<float*>(workspace);
+    if (x_type == MXK_IN_F32) return launch_nt_decode((const float*)x, M, K, N, pk, w_scales, bias, out, part, st);
+    if (x_type == MXK_IN_F16) return launch_nt_decode((const __half*)x, M, K, N, pk, w_scales, bias, out, part, st);
+    if (x_type == MXK_IN_BF16)
+      return launch_nt_decode((const hip_bfloat16*)x, M, K, N, pk, w_scales, bias, out, part, st);
+  }
   if (x_type == MXK_IN_F32)
     return linear_t<true, float>((const float*)x, M, K, N, pk, w_nbytes, w_scales, kind, bits, block, bias, out, st);
   if (x_type == MXK_IN_F16)

@@ -109,6 +109,65 @@ __global__ __launch_bounds__(256) void k_quant_fast(const T* __restrict__ x, int
   }
 }
 
+// ---------------------------------------------------------------- long blocks
+// Blocks of 264..8192 elements (a multiple of 8): one 256-thread workgroup
+// per block, grid-stride.  Thread t holds chunks t, t+256, ... of 8
+// consecutive elements in registers (x is read once), the block absmax is
+// a wave maximum then a 4-way LDS maximum, and each chunk packs into BITS
+// bytes stored directly (consecutive threads, consecutive bytes).
+template <typename T, int MODE, int BITS, int R>
+__global__ __launch_bounds__(256) void k_quant_rows(const T* __restrict__ x, int64_t n, int64_t nb, int block,
+                                                    uint8_t* __restrict__ packed, int64_t packed_nbytes,
+                                                    int64_t n_store, float* __restrict__ scales, float qf) {
+  constexpr int NW = (8 * BITS + 31) / 32;
+  constexpr uint32_t MASK = BITS == 32 ? 0xFFFFFFFFu : ((1u << BITS) - 1u);
+  constexpr int H = MODE == Q_FP ? (1 << (BITS - 1)) : 1;
+  __shared__ float sP[H + 1];
+  __shared__ float s_max[4];
+  if constexpr (MODE == Q_FP) build_tables<BITS>(sP, nullptr);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int chunks = block / 8;
+  for (int64_t blk = blockIdx.x; blk < nb; blk += gridDim.x) {
+    float v[R][8];
+    float m = 0.0f;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int c = threadIdx.x + 256 * r;
+      if (c < chunks) {
+        load_elems<T, 8>(x, blk * block + 8 * (int64_t)c, n, v[r]);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[r][e] = 0.0f;
+      }
+#pragma unroll
+      for (int e = 0; e < 8; ++e) m = fmaxf(m, __builtin_fabsf(v[r][e]));
+    }
+    m = group_max<64>(m);
+    if (lane == 0) s_max[wave] = m;
+    __syncthreads();
+    const float ap = fmaxf(fmaxf(fmaxf(s_max[0], s_max[1]), fmaxf(s_max[2], s_max[3])), MXK_AMIN);
+    const BlockParams bp = block_params<MODE>(ap, qf);
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int c = threadIdx.x + 256 * r;
+      if (c >= chunks) continue;
+      const int64_t idx = blk * block + 8 * (int64_t)c;
+      uint32_t w[NW];
+#pragma unroll
+      for (int k = 0; k < NW; ++k) w[k] = 0u;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        uint32_t f = (uint32_t)encode<MODE, BITS>(v[r][e], bp, qf, sP) & MASK;
+        if (idx + e >= n_store) f = 0u;
+        w[(e * BITS) >> 5] |= f << ((e * BITS) & 31);
+      }
+      store_bytes<BITS>(packed, idx * BITS / 8, packed_nbytes, w);
+    }
+    if (threadIdx.x == 0) scales[blk] = bp.s;
+    __syncthreads();  // s_max is rewritten by the next block
+  }
+}
+
 // ---------------------------------------------------------------- generic quantize
 // Any block size and any supported width: pass 1 reduces one block per wave
 // and stores the scale and the multiplier, pass 2 writes one packed byte
@@ -617,6 +676,25 @@ static bool try_fast(const T* x, int64_t n, int64_t nb, int block, uint8_t* pack
 }
 
 template <typename T, int MODE, int BITS>
+static bool try_rows(const T* x, int64_t n, int64_t nb, int block, uint8_t* packed, int64_t pbytes,
+                     int64_t n_store, float* scales, float qf, hipStream_t st) {
+  if (block % 8 != 0 || block <= 256 || block > 8192 || !aligned16(x)) return false;
+  if ((reinterpret_cast<uintptr_t>(packed) % (uintptr_t)(BITS >= 16 ? 16 : BITS)) != 0) return false;
+  const int chunks = block / 8;
+  const dim3 grid((unsigned)std::max<int64_t>(1, std::min<int64_t>(nb, (int64_t)num_cus() * 8)));
+  if (chunks <= 256)
+    hipLaunchKernelGGL((k_quant_rows<T, MODE, BITS, 1>), grid, dim3(256), 0, st, x, n, nb, block, packed, pbytes,
+                       n_store, scales, qf);
+  else if (chunks <= 512)
+    hipLaunchKernelGGL((k_quant_rows<T, MODE, BITS, 2>), grid, dim3(256), 0, st, x, n, nb, block, packed, pbytes,
+                       n_store, scales, qf);
+  else
+    hipLaunchKernelGGL((k_quant_rows<T, MODE, BITS, 4>), grid, dim3(256), 0, st, x, n, nb, block, packed, pbytes,
+                       n_store, scales, qf);
+  return true;
+}
+
+template <typename T, int MODE, int BITS>
 static int run_generic(const T* x, int64_t n, int64_t nb, int block, int bits, uint8_t* packed, int64_t pbytes,
                        int64_t n_store, float* scales, float qf, void* ws, size_t ws_bytes, hipStream_t st) {
   if (ws == nullptr || ws_bytes < (size_t)nb * sizeof(float2))
@@ -641,6 +719,8 @@ static int quantize_t(const T* x, int64_t n, int kind, int bits, int variant, in
   if (mode == MODE && bits == BITS) {                                                                     \
     if (try_fast<T, MODE, BITS>(x, n, nb, block, packed, pbytes, n_store, scales, qf, st))               \
       return check_launch("quantize");                                                                    \
+    if (try_rows<T, MODE, BITS>(x, n, nb, block, packed, pbytes, n_store, scales, qf, st))               \
+      return check_launch("quantize(rows)");                                                              \
     return run_generic<T, MODE, BITS>(x, n, nb, block, bits, packed, pbytes, n_store, scales, qf, ws, ws_bytes, st); \
   }
   MXK_TRY(Q_INT, 2)

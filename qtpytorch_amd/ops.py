@@ -421,10 +421,13 @@ def linear_wq_nt(x: Tensor, w_packed: Tensor, w_scales: Tensor, dt, out_features
         return out.reshape(*lead, N)
     b = None if bias is None else bias.to(device=dev, dtype=torch.float32).contiguous()
     wp, ws = w_packed.contiguous(), w_scales.contiguous().float()
+    lib = L.lib()
+    ws_bytes = lib.mxk_linear_nt_workspace(M, K, N, dt.bits, block)
+    wk = _workspace(ws_bytes, dev)
     with torch.cuda.device(dev):
-        rc = L.lib().mxk_linear_wq_nt(xc.data_ptr(), L.elem_type(xc.dtype), M, K, wp.data_ptr(),
-                                      wp.numel() * wp.element_size(), ws.data_ptr(), ws.numel(), N, kind, dt.bits,
-                                      block, L.ptr(b), out.data_ptr(), L.stream_of(xc))
+        rc = lib.mxk_linear_wq_nt(xc.data_ptr(), L.elem_type(xc.dtype), M, K, wp.data_ptr(),
+                                  wp.numel() * wp.element_size(), ws.data_ptr(), ws.numel(), N, kind, dt.bits,
+                                  block, L.ptr(b), out.data_ptr(), L.ptr(wk), ws_bytes, L.stream_of(xc))
     L.check(rc, f"linear_wq_nt({dt.name}, M={M}, K={K}, N={N})")
     return out.reshape(*lead, N)
 

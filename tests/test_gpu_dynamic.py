@@ -242,3 +242,29 @@ def test_mx_linear_autograd_function(qa, xname, wname, shape, has_bias):
     g = _x(tuple(y.shape), 32)
     y.backward(g.to(dev()))
     _close(xg.grad, orc.mx_linear_autograd_backward(g, wp, ws, wname, K, N, 128, x.shape))
+
+
+# ---------------------------------------------------------------- int4 decode with [N][K] weights
+@pytest.mark.parametrize("M", [1, 5, 16])
+@pytest.mark.parametrize("K,N", [(128, 16), (1024, 272), (1152, 1024), (8192, 4096)])
+@pytest.mark.parametrize("src", ["f32", "f16", "bf16"])
+def test_linear_wq_nt_decode_path(qa, M, K, N, src):
+    w = _x((N, K), 33, 0.02)
+    w[torch.rand(N, K, generator=torch.Generator().manual_seed(34)) < 1e-3] *= 20
+    wp, ws, _ = orc.dynamic_linear_from_weight(w, "int4d", 128)
+    x = _x((M, K), 35)
+    x = {"f32": x, "f16": x.half(), "bf16": x.bfloat16()}[src]
+    b = _x((N,), 36)
+    y = qa.ops.linear_wq_nt(x.to(dev()), wp.to(dev()), ws.to(dev()), "int4d", N, K, 128, bias=b.to(dev()))
+    _close(y, orc.dynamic_linear_forward(x, wp, ws, "int4d", K, N, 128, b))
+
+
+@pytest.mark.parametrize("mag", [1e6, 1e-6])
+def test_linear_wq_nt_decode_extreme_activations(qa, mag):
+    """Activations past the f16 range (staged with a power-of-two rescale) and tiny ones."""
+    K, N = 2048, 512
+    w = _x((N, K), 37, 0.02)
+    wp, ws, _ = orc.dynamic_linear_from_weight(w, "int4d", 128)
+    x = _x((16, K), 38) * mag
+    y = qa.ops.linear_wq_nt(x.to(dev()), wp.to(dev()), ws.to(dev()), "int4d", N, K, 128)
+    _close(y, orc.dynamic_linear_forward(x, wp, ws, "int4d", K, N, 128))

@@ -465,3 +465,24 @@ def test_to_mx_model(qa):
     assert isinstance(model[0], qa.mx_linear) and isinstance(model[2], qa.mx_linear)
     y = model(x)
     assert y.shape == (4, 128) and torch.isfinite(y).all()
+
+
+# ---------------------------------------------------------------- long blocks (one workgroup per block)
+@pytest.mark.parametrize("name", ["int8d", "int4d", "int2d", "int1d", "float4d", "float8d", "int8dv", "int4dv",
+                                  "int16d"])
+@pytest.mark.parametrize("block", [264, 512, 1000, 2048, 8192])
+@pytest.mark.parametrize("n", [8192 * 3, 8192 * 3 - 100])
+@pytest.mark.parametrize("src", ["f32", "bf16"])
+def test_quantize_long_blocks(qa, name, block, n, src):
+    g = torch.Generator()
+    g.manual_seed(block + n)
+    x = torch.randn(n, generator=g)
+    x[::997] *= 40.0
+    if src == "bf16":
+        x = x.bfloat16()
+    dt = qa.get_mx_dtype(name)
+    packed, scales, nn = qa.ops.quantize(x.to(dev()), dt, block)
+    rp, rs, rn = orc.quantize(x, name, block)
+    assert nn == rn
+    assert _bits_eq(packed, rp), "packed codes differ"
+    assert _bits_eq(scales, rs), "scales differ"
