@@ -243,7 +243,10 @@ int mxk_linear_wq_nt(const void* x, int x_type, int64_t M, int64_t K, const void
 
 /* Workspace bytes mxk_linear_wq_nt needs (0 if none): the decode path (int4
  * base codes, block 128, M <= 16, K % 128 == 0, N % 16 == 0) splits K over
- * workgroups of 1024 rows of K and sums their partials in a second launch. */
+ * workgroups of 1024 rows of K; its workspace (a 64 KiB prefix of arrival
+ * counters, then the partial sums) must be zero-filled before first use,
+ * and every call leaves the counters zero again.  Calls sharing a workspace
+ * must not overlap. */
 size_t mxk_linear_nt_workspace(int64_t M, int64_t K, int64_t N, int bits, int block);
 
 /* Workspace bytes mxk_linear_i8 needs (0 when the shapes are not covered). */

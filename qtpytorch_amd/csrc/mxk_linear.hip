@@ -491,9 +491,13 @@ static void launch_transpose_scales(const float* s, int64_t K, int64_t NB, float
 // x is staged as x * 2^-e, the power of two that puts the workgroup's
 // largest |x| in [2^14, 2^15); 2^e returns after the scale.
 //
-// The 8 waves of a column half meet in LDS and sum their partials in block
-// order.  With more than one K split the workgroup writes its partial to
-// partials[split][16][N] and k_sum_splits adds them in split order (+ bias).
+// Each wave runs its tiles in load order, so the MFMAs of the first tiles
+// overlap the arrival of the last.  The 8 waves of a column half meet in LDS
+// and sum their partials in block order.  With more than one K split the
+// workgroup publishes its partial (partials[split][16][N], write-through
+// stores) and counts its arrival; the last workgroup of the column group
+// reads the others past the L2s, adds the S partials in split order
+// (+ bias) and resets the counter.
 #define NT_WAVES 16
 #define NT_THREADS 1024
 #define NT_COLS 256
@@ -504,11 +508,12 @@ template <typename T>
 __global__ __launch_bounds__(NT_THREADS, 1) void k_linear_w4t_decode(
     const T* __restrict__ x, int M, int64_t K, int64_t N, const uint8_t* __restrict__ w,
     const float* __restrict__ scales, const float* __restrict__ bias, float* __restrict__ out,
-    float* __restrict__ partials, int S) {
+    float* __restrict__ partials, unsigned int* __restrict__ counters, int S) {
   // A staging (8 blocks x 4 steps x hi/lo x 1 KiB = 64 KiB), then the
   // partial sums [8 blocks][16 rows][256 (+4) columns]
   __shared__ __attribute__((aligned(16))) float lds[NT_BLKS * 16 * NT_RED_STRIDE];
   __shared__ float s_wmax[NT_WAVES];
+  __shared__ int s_last;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int j = lane & 15, g = lane >> 4;
@@ -520,7 +525,8 @@ __global__ __launch_bounds__(NT_THREADS, 1) void k_linear_w4t_decode(
   const bool live = kb < KB;  // wave-uniform
   const int64_t n0 = (int64_t)cg * NT_COLS + h * 128;
 
-  // ---- requests in arrival order: x chunks, then weights and scales
+  // ---- requests in arrival order: x chunks, the first weight tile; the
+  // scales and the other tiles once x is staged
   constexpr int EPL = 16 / (int)sizeof(T);   // elements per 16-byte load
   constexpr int LPC = 8 / EPL;               // loads per 8-element chunk
   const __amdgpu_buffer_rsrc_t rx = make_rsrc(x, (uint32_t)((int64_t)M * K * sizeof(T)));
@@ -539,18 +545,12 @@ __global__ __launch_bounds__(NT_THREADS, 1) void k_linear_w4t_decode(
   const __amdgpu_buffer_rsrc_t rs = make_rsrc(scales, (uint32_t)(N * KB * 4));
   u32x4 wv[8];
   float sc[8];
-  if (live) {
-#pragma unroll
-    for (int t = 0; t < 8; ++t) {
-      const int64_t n = std::min<int64_t>(n0 + 16 * t + j, N - 1);
-      wv[t] = buf_load_b128(rw, (uint32_t)(n * (K / 2) + kb * 64 + 16 * g), 0u);
-    }
-#pragma unroll
-    for (int t = 0; t < 8; ++t) {
-      const int64_t n = std::min<int64_t>(n0 + 16 * t + j, N - 1);
-      sc[t] = __uint_as_float(buf_load_b32(rs, (uint32_t)((n * KB + kb) * 4), 0u));
-    }
-  }
+  auto load_tile = [&](int t) {
+    const int64_t n = std::min<int64_t>(n0 + 16 * t + j, N - 1);
+    wv[t] = buf_load_b128(rw, (uint32_t)(n * (K / 2) + kb * 64 + 16 * g), 0u);
+  };
+  // only the first tile before x is staged: requests queued ahead of x delay it
+  if (live) load_tile(0);
   __builtin_amdgcn_sched_barrier(0);
 
   // ---- x to float, the workgroup's largest |x|
@@ -605,23 +605,40 @@ __global__ __launch_bounds__(NT_THREADS, 1) void k_linear_w4t_decode(
   }
   __builtin_amdgcn_s_waitcnt(0xC07F);
   dec_barrier_nofence();
-
-  // ---- MFMA: 4 steps x (8 tiles + the correction tile) x hi/lo
-  f32x4 acc[8];
-#pragma unroll
-  for (int t = 0; t < 8; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
-  f32x4 corr = f32x4{0.f, 0.f, 0.f, 0.f};
   if (live) {
-    const f16x8 b8 = __builtin_bit_cast(f16x8, u32x4v{0x00080008u, 0x00080008u, 0x00080008u, 0x00080008u});
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+      const int64_t n = std::min<int64_t>(n0 + 16 * t + j, N - 1);
+      sc[t] = __uint_as_float(buf_load_b32(rs, (uint32_t)((n * KB + kb) * 4), 0u));
+    }
+#pragma unroll
+    for (int t = 1; t < 8; ++t) load_tile(t);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+
+  // ---- MFMA, tile by tile as the weights arrive: the x fragments of the
+  // wave's block stay in registers; 4 steps x hi/lo per tile
+  f32x4 res[8];
+  if (live) {
+    f16x8 ahi[4], alo[4];
 #pragma unroll
     for (int st = 0; st < 4; ++st) {
       const float* ab = lds + ((q * 4 + st) * 2) * 256 + lane * 4;
-      const f16x8 ahi = __builtin_bit_cast(f16x8, *reinterpret_cast<const u32x4*>(ab));
-      const f16x8 alo = __builtin_bit_cast(f16x8, *reinterpret_cast<const u32x4*>(ab + 256));
-      corr = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi, b8, corr, 0, 0, 0);
-      corr = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo, b8, corr, 0, 0, 0);
+      ahi[st] = __builtin_bit_cast(f16x8, *reinterpret_cast<const u32x4*>(ab));
+      alo[st] = __builtin_bit_cast(f16x8, *reinterpret_cast<const u32x4*>(ab + 256));
+    }
+    const f16x8 b8 = __builtin_bit_cast(f16x8, u32x4v{0x00080008u, 0x00080008u, 0x00080008u, 0x00080008u});
+    f32x4 corr = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int t = 0; t < 8; ++t) {
+    for (int st = 0; st < 4; ++st) {
+      corr = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi[st], b8, corr, 0, 0, 0);
+      corr = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo[st], b8, corr, 0, 0, 0);
+    }
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+      f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int st = 0; st < 4; ++st) {
         const uint32_t wd = wv[t][st];
         const uint32_t lo = (wd & 0x0F0F0F0Fu) ^ 0x08080808u;
         const uint32_t hi = ((wd >> 4) & 0x0F0F0F0Fu) ^ 0x08080808u;
@@ -630,22 +647,25 @@ __global__ __launch_bounds__(NT_THREADS, 1) void k_linear_w4t_decode(
         const uint32_t d2 = __builtin_amdgcn_perm(hi, lo, 0x0C060C02u);
         const uint32_t d3 = __builtin_amdgcn_perm(hi, lo, 0x0C070C03u);
         const f16x8 bt = __builtin_bit_cast(f16x8, u32x4v{d0, d1, d2, d3});
-        acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi, bt, acc[t], 0, 0, 0);
-        acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo, bt, acc[t], 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi[st], bt, acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo[st], bt, acc, 0, 0, 0);
       }
+      const float sf = sc[t] * 16777216.0f;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) res[t][i] = __builtin_ldexpf(sf * (acc[i] - corr[i]), shift);
     }
+  } else {
+#pragma unroll
+    for (int t = 0; t < 8; ++t) res[t] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
   // every wave is done reading the staged x before the partials overwrite it
   __syncthreads();
   {
     float* red = lds + (q * 16) * NT_RED_STRIDE + h * 128;
 #pragma unroll
-    for (int t = 0; t < 8; ++t) {
-      const float sf = live ? sc[t] * 16777216.0f : 0.0f;
+    for (int t = 0; t < 8; ++t)
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
-        red[(4 * g + i) * NT_RED_STRIDE + 16 * t + j] = __builtin_ldexpf(sf * (acc[t][i] - corr[i]), shift);
-    }
+      for (int i = 0; i < 4; ++i) red[(4 * g + i) * NT_RED_STRIDE + 16 * t + j] = res[t][i];
   }
   __syncthreads();
   // thread: row m, columns c .. c+3, summed over the 8 blocks in order
@@ -654,57 +674,74 @@ __global__ __launch_bounds__(NT_THREADS, 1) void k_linear_w4t_decode(
 #pragma unroll
   for (int b = 1; b < NT_BLKS; ++b) sum += *reinterpret_cast<const f32x4*>(lds + (b * 16 + m) * NT_RED_STRIDE + c);
   const int64_t n = (int64_t)cg * NT_COLS + c;
-  if (m >= M || n >= N) return;
+  const bool mine = m < M && n < N;
   if (S == 1) {
+    if (!mine) return;
     if (bias) sum += *reinterpret_cast<const f32x4*>(bias + n);
     *reinterpret_cast<f32x4*>(out + (int64_t)m * N + n) = sum;
-  } else {
-    *reinterpret_cast<f32x4*>(partials + ((int64_t)ks * 16 + m) * N + n) = sum;
+    return;
   }
+  // split K: publish the partial with write-through (sc1) stores, wait for
+  // them, count the arrival; the last workgroup of the column group reads
+  // the other partials past the L2s (sc1), adds the S partials in split
+  // order and resets the counter
+  const __amdgpu_buffer_rsrc_t rp = make_rsrc(partials, (uint32_t)((int64_t)S * 16 * N * 4));
+  const uint32_t poff = (uint32_t)(((int64_t)m * N + n) * 4);
+  const uint32_t split_stride = (uint32_t)(16 * N * 4);
+  if (mine) __builtin_amdgcn_raw_buffer_store_b128(sum, rp, poff, (uint32_t)ks * split_stride, 16);
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const unsigned prev = __hip_atomic_fetch_add(counters + cg, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    s_last = prev == (unsigned)(S - 1) ? 1 : 0;
+  }
+  __syncthreads();
+  if (!s_last) return;
+  if (mine) {
+    f32x4 tot = sum;
+    for (int sp = 0; sp < S; ++sp) {
+      const f32x4 pv = sp == ks ? sum
+                                : __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                                rp, poff, (uint32_t)sp * split_stride, 16));
+      tot = sp == 0 ? pv : tot + pv;
+    }
+    if (bias) tot += *reinterpret_cast<const f32x4*>(bias + n);
+    *reinterpret_cast<f32x4*>(out + (int64_t)m * N + n) = tot;
+  }
+  if (threadIdx.x == 0) __hip_atomic_store(counters + cg, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// out[m][n] = sum over splits in order of partials[s][m][n] (+ bias[n]), 4 columns per thread
-__global__ __launch_bounds__(256) void k_sum_splits(const float* __restrict__ partials, int S, int M, int64_t N,
-                                                    const float* __restrict__ bias, float* __restrict__ out) {
-  const int64_t per_row = N / 4;
-  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (t >= (int64_t)M * per_row) return;
-  const int64_t m = t / per_row, n = 4 * (t % per_row);
-  f32x4 sum = *reinterpret_cast<const f32x4*>(partials + m * N + n);
-  for (int s = 1; s < S; ++s) sum += *reinterpret_cast<const f32x4*>(partials + ((int64_t)s * 16 + m) * N + n);
-  if (bias) sum += *reinterpret_cast<const f32x4*>(bias + n);
-  *reinterpret_cast<f32x4*>(out + m * N + n) = sum;
-}
+static int nt_splits(int64_t K) { return (int)ceil_div(K / 128, NT_BLKS); }
 
 static bool nt_decode_eligible(int64_t M, int64_t K, int64_t N, int kind, int bits, int block, const void* x,
                                int x_type, int64_t w_nbytes, int64_t w_nscales) {
   if (kind != MXK_KIND_INT || bits != 4 || block != 128) return false;
   if (M < 1 || M > 16 || K % 128 != 0 || N % 16 != 0) return false;
+  if (ceil_div(N, NT_COLS) * 4 > DEC_COUNTER_BYTES) return false;
   if (!aligned16(x) || w_nbytes < N * K / 2 || w_nscales < N * (K / 128)) return false;
   const int esz = x_type == MXK_IN_F32 ? 4 : 2;
   const int64_t lim = int64_t(1) << 31;
-  return N * K / 2 < lim && N * (K / 128) * 4 < lim && 16 * K * esz < lim;
+  return N * K / 2 < lim && N * (K / 128) * 4 < lim && 16 * K * esz < lim &&
+         (int64_t)nt_splits(K) * 16 * N * 4 < lim;
 }
 
-static int nt_splits(int64_t K) { return (int)ceil_div(K / 128, NT_BLKS); }
 
-static size_t nt_partial_bytes(int64_t K, int64_t N) {
+// workspace: arrival counters (one per 256-column group, DEC_COUNTER_BYTES,
+// zero between calls), then the partials [S][16][N]
+static size_t nt_workspace_bytes(int64_t K, int64_t N) {
   const int S = nt_splits(K);
-  return S > 1 ? (size_t)S * 16 * (size_t)N * 4 : 0;
+  return S > 1 ? DEC_COUNTER_BYTES + (size_t)S * 16 * (size_t)N * 4 : 0;
 }
 
 template <typename T>
 static int launch_nt_decode(const T* x, int64_t M, int64_t K, int64_t N, const uint8_t* w, const float* scales,
-                            const float* bias, float* out, float* partials, hipStream_t st) {
+                            const float* bias, float* out, uint8_t* ws, hipStream_t st) {
   const int S = nt_splits(K);
   const int64_t groups = ceil_div(N, NT_COLS);
+  unsigned int* counters = S > 1 ? reinterpret_cast<unsigned int*>(ws) : nullptr;
+  float* partials = S > 1 ? reinterpret_cast<float*>(ws + DEC_COUNTER_BYTES) : nullptr;
   hipLaunchKernelGGL((k_linear_w4t_decode<T>), dim3((unsigned)(groups * S)), dim3(NT_THREADS), 0, st, x, (int)M, K,
-                     N, w, scales, bias, out, partials, S);
-  if (S > 1) {
-    const int64_t threads = M * (N / 4);
-    hipLaunchKernelGGL(k_sum_splits, dim3((unsigned)ceil_div(threads, 256)), dim3(256), 0, st, partials, S, (int)M,
-                       N, bias, out);
-  }
+                     N, w, scales, bias, out, partials, counters, S);
   return check_launch("linear_wq_nt(decode)");
 }
 
@@ -891,7 +928,7 @@ int mxk_linear_wq(const void* x, int x_type, int64_t M, int64_t K, const void* w
 
 size_t mxk_linear_nt_workspace(int64_t M, int64_t K, int64_t N, int bits, int block) {
   if (M < 1 || M > 16 || bits != 4 || block != 128 || K <= 0 || N <= 0 || K % 128 != 0 || N % 16 != 0) return 0;
-  return nt_partial_bytes(K, N);
+  return nt_workspace_bytes(K, N);
 }
 
 int mxk_linear_wq_nt(const void* x, int x_type, int64_t M, int64_t K, const void* w_packed, int64_t w_nbytes,
@@ -904,10 +941,11 @@ int mxk_linear_wq_nt(const void* x, int x_type, int64_t M, int64_t K, const void
   if (w_nbytes < mxk_packed_nbytes(bits, N * K)) return fail(MXK_EINVAL, "linear_wq_nt: packed weight too short");
   const uint8_t* pk = reinterpret_cast<const uint8_t*>(w_packed);
   if (nt_decode_eligible(M, K, N, kind, bits, block, x, x_type, w_nbytes, w_nscales)) {
-    const size_t need = nt_partial_bytes(K, N);
+    const size_t need = nt_workspace_bytes(K, N);
     if (need > 0 && (!workspace || workspace_nbytes < need))
-      return fail(MXK_EINVAL, "linear_wq_nt: decode path needs a workspace of mxk_linear_nt_workspace() bytes");
-    float* part = reinterpret_cast<float*>(workspace);
+      return fail(MXK_EINVAL, "linear_wq_nt: decode path needs a zero-initialised workspace of "
+                              "mxk_linear_nt_workspace() bytes");
+    uint8_t* part = reinterpret_cast<uint8_t*>(workspace);
     if (x_type == MXK_IN_F32) return launch_nt_decode((const float*)x, M, K, N, pk, w_scales, bias, out, part, st);
     if (x_type == MXK_IN_F16) return launch_nt_decode((const __half*)x, M, K, N, pk, w_scales, bias, out, part, st);
     if (x_type == MXK_IN_BF16)

@@ -423,7 +423,7 @@ def linear_wq_nt(x: Tensor, w_packed: Tensor, w_scales: Tensor, dt, out_features
     wp, ws = w_packed.contiguous(), w_scales.contiguous().float()
     lib = L.lib()
     ws_bytes = lib.mxk_linear_nt_workspace(M, K, N, dt.bits, block)
-    wk = _workspace(ws_bytes, dev)
+    wk = _zeroed_workspace(ws_bytes, dev)
     with torch.cuda.device(dev):
         rc = lib.mxk_linear_wq_nt(xc.data_ptr(), L.elem_type(xc.dtype), M, K, wp.data_ptr(),
                                   wp.numel() * wp.element_size(), ws.data_ptr(), ws.numel(), N, kind, dt.bits,
