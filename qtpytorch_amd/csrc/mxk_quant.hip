@@ -664,8 +664,14 @@ static void launch_fast_b(const T* x, int64_t n, int64_t nb, int block, uint8_t*
 template <typename T, int MODE, int BITS>
 static bool try_fast(const T* x, int64_t n, int64_t nb, int block, uint8_t* packed, int64_t pbytes,
                      int64_t n_store, float* scales, float qf, hipStream_t st) {
+  // elements per lane: two 16-byte loads where per-element work dominates
+  // (division and bucket search of the 'v' and float rules) or the input is
+  // 16-bit; one for the fp32 int rule, which measured faster that way
   constexpr int PER16 = 16 / (int)sizeof(T);
-  constexpr int E = (8 / BITS) > PER16 ? (8 / BITS) : PER16;
+  // (at most 16 packed bytes per lane: 128 / BITS elements)
+  constexpr int EW0 = (MODE == Q_FP || MODE == Q_VEC || sizeof(T) == 2) ? 2 * PER16 : PER16;
+  constexpr int EW = EW0 * BITS > 128 ? PER16 : EW0;
+  constexpr int E = (8 / BITS) > EW ? (8 / BITS) : EW;
   if (block % E != 0 || !is_pow2(block / E) || block / E > 64 || block / E < 2) return false;
   if (!aligned16(x) || (E * BITS) % 8 != 0) return false;
   const int NB = E * BITS / 8;
