@@ -62,8 +62,17 @@ __global__ __launch_bounds__(256) void k_quant_fast(const T* __restrict__ x, int
   constexpr int B = E * LPB;
   constexpr int GPW = 64 / LPB;
   constexpr int GPB = 4 * GPW;
-  constexpr int NW = (E * BITS + 31) / 32;
-  constexpr int NB = E * BITS / 8;
+  // fp32: a lane's E elements are Q chunks of CH consecutive elements (one
+  // 16-byte load each), chunk q at offset q * B / Q in the block, so that
+  // every load instruction of a wave covers whole lines; chunks whose codes
+  // would not fill whole bytes (1-bit codes of 4 fp32) stay one consecutive
+  // run.  16-bit inputs keep one consecutive run (measured faster).
+  constexpr int PER16 = 16 / (int)sizeof(T);
+  constexpr bool SPLIT = sizeof(T) == 4 && E / PER16 > 1 && (PER16 * BITS) % 8 == 0;
+  constexpr int Q = SPLIT ? E / PER16 : 1;
+  constexpr int CH = E / Q;
+  constexpr int NW = (CH * BITS + 31) / 32;
+  constexpr int NB = CH * BITS / 8;
   constexpr uint32_t MASK = BITS == 32 ? 0xFFFFFFFFu : ((1u << BITS) - 1u);
   constexpr int H = MODE == Q_FP ? (1 << (BITS - 1)) : 1;
   __shared__ float sP[H + 1];
@@ -71,41 +80,34 @@ __global__ __launch_bounds__(256) void k_quant_fast(const T* __restrict__ x, int
 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int g = lane / LPB, li = lane % LPB;
-  // U rounds of GPB blocks per iteration, a grid-stride apart, with all
-  // their loads issued before the first reduction (U = 4 measured slower
-  // on 2^28 elements than one round)
-  constexpr int U = 1;
   const int64_t rstride = (int64_t)gridDim.x * GPB;
-  for (int64_t b0 = (int64_t)blockIdx.x * GPB; b0 < nb; b0 += U * rstride) {
-    float v[U][E];
+  for (int64_t b0 = (int64_t)blockIdx.x * GPB; b0 < nb; b0 += rstride) {
+    const int64_t blk = b0 + wave * GPW + g;
+    float v[Q][CH];
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int64_t blk = b0 + u * rstride + wave * GPW + g;
-      load_elems<T, E>(x, blk * B + (int64_t)li * E, n, v[u]);
-    }
+    for (int q = 0; q < Q; ++q) load_elems<T, CH>(x, blk * B + q * (B / Q) + (int64_t)li * CH, n, v[q]);
+    float m = 0.0f;
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int64_t blk = b0 + u * rstride + wave * GPW + g;
-      const int64_t idx = blk * B + (int64_t)li * E;
-      float m = 0.0f;
+    for (int q = 0; q < Q; ++q)
 #pragma unroll
-      for (int i = 0; i < E; ++i) m = fmaxf(m, __builtin_fabsf(v[u][i]));
-      const float ap = fmaxf(group_max<LPB>(m), MXK_AMIN);
-      const BlockParams bp = block_params<MODE>(ap, qf);
+      for (int i = 0; i < CH; ++i) m = fmaxf(m, __builtin_fabsf(v[q][i]));
+    const float ap = fmaxf(group_max<LPB>(m), MXK_AMIN);
+    const BlockParams bp = block_params<MODE>(ap, qf);
+#pragma unroll
+    for (int q = 0; q < Q; ++q) {
+      const int64_t idx = blk * B + q * (B / Q) + (int64_t)li * CH;
       uint32_t w[NW];
 #pragma unroll
       for (int k = 0; k < NW; ++k) w[k] = 0u;
 #pragma unroll
-      for (int i = 0; i < E; ++i) {
-        uint32_t f = (uint32_t)encode<MODE, BITS>(v[u][i], bp, qf, sP) & MASK;
+      for (int i = 0; i < CH; ++i) {
+        uint32_t f = (uint32_t)encode<MODE, BITS>(v[q][i], bp, qf, sP) & MASK;
         if (idx + i >= n_store) f = 0u;
         w[(i * BITS) >> 5] |= f << ((i * BITS) & 31);
       }
-      if (blk < nb) {
-        store_bytes<NB>(packed, idx * BITS / 8, packed_nbytes, w);
-        if (li == 0) scales[blk] = bp.s;
-      }
+      if (blk < nb) store_bytes<NB>(packed, idx * BITS / 8, packed_nbytes, w);
     }
+    if (blk < nb && li == 0) scales[blk] = bp.s;
   }
 }
 
@@ -661,24 +663,35 @@ static void launch_fast_b(const T* x, int64_t n, int64_t nb, int block, uint8_t*
   }
 }
 
-template <typename T, int MODE, int BITS>
-static bool try_fast(const T* x, int64_t n, int64_t nb, int block, uint8_t* packed, int64_t pbytes,
-                     int64_t n_store, float* scales, float qf, hipStream_t st) {
-  // elements per lane: two 16-byte loads where per-element work dominates
-  // (division and bucket search of the 'v' and float rules) or the input is
-  // 16-bit; one for the fp32 int rule, which measured faster that way
+template <typename T, int MODE, int BITS, int E>
+static bool try_fast_e(const T* x, int64_t n, int64_t nb, int block, uint8_t* packed, int64_t pbytes,
+                       int64_t n_store, float* scales, float qf, hipStream_t st) {
   constexpr int PER16 = 16 / (int)sizeof(T);
-  // (at most 16 packed bytes per lane: 128 / BITS elements)
-  constexpr int EW0 = (MODE == Q_FP || MODE == Q_VEC || sizeof(T) == 2) ? 2 * PER16 : PER16;
-  constexpr int EW = EW0 * BITS > 128 ? PER16 : EW0;
-  constexpr int E = (8 / BITS) > EW ? (8 / BITS) : EW;
+  constexpr bool SPLIT = sizeof(T) == 4 && E / PER16 > 1 && (PER16 * BITS) % 8 == 0;
+  constexpr int CH = SPLIT ? PER16 : E;
+  constexpr int NB = CH * BITS / 8;
   if (block % E != 0 || !is_pow2(block / E) || block / E > 64 || block / E < 2) return false;
-  if (!aligned16(x) || (E * BITS) % 8 != 0) return false;
-  const int NB = E * BITS / 8;
-  if ((reinterpret_cast<uintptr_t>(packed) % (uintptr_t)(NB >= 16 ? 16 : NB)) != 0) return false;
+  if (!aligned16(x) || (CH * BITS) % 8 != 0 || NB > 16) return false;
+  if ((reinterpret_cast<uintptr_t>(packed) % (uintptr_t)NB) != 0) return false;
   bool done = false;
   launch_fast_b<T, MODE, BITS, E>(x, n, nb, block, packed, pbytes, n_store, scales, qf, st, &done);
   return done;
+}
+
+// Elements per lane: two 16-byte loads (for fp32 half a block apart), which
+// halves the per-element share of the block reduction and scale arithmetic;
+// one load when the block is too small for two; 8 consecutive fp32 for 1-bit
+// codes (one packed byte per lane); at most 16 packed bytes per lane.
+template <typename T, int MODE, int BITS>
+static bool try_fast(const T* x, int64_t n, int64_t nb, int block, uint8_t* packed, int64_t pbytes,
+                     int64_t n_store, float* scales, float qf, hipStream_t st) {
+  constexpr int PER16 = 16 / (int)sizeof(T);
+  constexpr int E2x = (8 / BITS) > 2 * PER16 ? (8 / BITS) : 2 * PER16;
+  constexpr int E2 = (sizeof(T) == 2 && E2x * BITS > 128) ? PER16 : E2x;
+  constexpr int E1 = (8 / BITS) > PER16 ? (8 / BITS) : PER16;
+  if (try_fast_e<T, MODE, BITS, E2>(x, n, nb, block, packed, pbytes, n_store, scales, qf, st)) return true;
+  if constexpr (E1 != E2) return try_fast_e<T, MODE, BITS, E1>(x, n, nb, block, packed, pbytes, n_store, scales, qf, st);
+  return false;
 }
 
 template <typename T, int MODE, int BITS>
