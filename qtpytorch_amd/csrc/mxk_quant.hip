@@ -252,12 +252,22 @@ __device__ __forceinline__ void butterflies(float (&v)[16]) {
     }
 }
 
+// LDS exchange among lanes of one wave (each 8-lane group owns its row of
+// LDS): a wave's LDS operations execute in issue order, so ordering the
+// compiler is enough; no s_barrier and no wait for the wave's global memory
+// operations still in flight.
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
 __device__ __forceinline__ void fwht128_group(float (&v)[16], float* __restrict__ row, int li) {
   // v: natural layout, positions li*16 + i.  row: 128(+pad) floats of LDS for this group.
 #pragma unroll
   for (int q = 0; q < 4; ++q)
     *reinterpret_cast<float4*>(row + li * 16 + 4 * q) = make_float4(v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]);
-  __syncthreads();
+  wave_lds_sync();
 #pragma unroll
   for (int j = 0; j < 16; ++j) v[j] = row[li + 8 * j];
   // positions li + 8j: level 64 pairs j<->j+8, 32: j<->j+4, 16: j<->j+2, 8: j<->j+1
@@ -265,10 +275,10 @@ __device__ __forceinline__ void fwht128_group(float (&v)[16], float* __restrict_
   butterflies<4, 1>(v);
   butterflies<2, 1>(v);
   butterflies<1, 1>(v);
-  __syncthreads();
+  wave_lds_sync();
 #pragma unroll
   for (int j = 0; j < 16; ++j) row[li + 8 * j] = v[j];
-  __syncthreads();
+  wave_lds_sync();
 #pragma unroll
   for (int q = 0; q < 4; ++q) {
     float4 t = *reinterpret_cast<const float4*>(row + li * 16 + 4 * q);
@@ -602,11 +612,11 @@ __global__ __launch_bounds__(256) void k_dequant_had128(const uint8_t* __restric
 #pragma unroll
     for (int q = 0; q < 4; ++q)
       *reinterpret_cast<f32x4v*>(row + li * 16 + 4 * q) = f32x4v{v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]};
-    __syncthreads();
+    wave_lds_sync();
     f32x4v o[4];
 #pragma unroll
     for (int q = 0; q < 4; ++q) o[q] = *reinterpret_cast<const f32x4v*>(row + 32 * q + 4 * li);
-    __syncthreads();
+    wave_lds_sync();
     if (live) {
       float* dst = out + blk * 128 + 4 * li;
 #pragma unroll
