@@ -236,10 +236,14 @@ int mxk_qelementwise(int op, const void* a_packed, int64_t a_nbytes, const float
  * W: packed codes of any width/kind of mxk_quantize (base variant), flat
  * blocks of `block` elements of the row-major [N][K] weight, w_nscales >=
  * ceil(N*K/block).  Float32 accumulation.  With int4 codes, block 128 and
- * M <= 16 the K sum is split over workgroups (workspace below). */
+ * M <= 16 the K sum is split over workgroups (workspace below), and that
+ * path reads w_scales_t when given: the K-block-major copy [K/128][N] of the
+ * scales (mxk_linear_prepack_scales(w_scales, N, K, 128, w_scales_t) of the
+ * [N][K/128] layout), made once per weight.  NULL reads w_scales. */
 int mxk_linear_wq_nt(const void* x, int x_type, int64_t M, int64_t K, const void* w_packed, int64_t w_nbytes,
-                     const float* w_scales, int64_t w_nscales, int64_t N, int kind, int bits, int block,
-                     const float* bias, float* out, void* workspace, size_t workspace_nbytes, void* stream);
+                     const float* w_scales, int64_t w_nscales, const float* w_scales_t, int64_t N, int kind,
+                     int bits, int block, const float* bias, float* out, void* workspace, size_t workspace_nbytes,
+                     void* stream);
 
 /* Workspace bytes mxk_linear_wq_nt needs (0 if none): the decode path (int4
  * base codes, block 128, M <= 16, K % 128 == 0, N % 16 == 0) splits K over

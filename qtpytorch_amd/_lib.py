@@ -55,8 +55,8 @@ SIGNATURES = {
     "mxk_qelementwise_workspace": (c_sz, [c_int, c_i64, c_i64, c_int, c_int, c_int]),
     "mxk_qelementwise": (c_int, [c_int, c_vp, c_i64, c_vp, c_vp, c_i64, c_vp, c_i64, c_i64, c_int, c_int, c_int,
                                  c_vp, c_i64, c_vp, c_vp, c_sz, c_vp]),
-    "mxk_linear_wq_nt": (c_int, [c_vp, c_int, c_i64, c_i64, c_vp, c_i64, c_vp, c_i64, c_i64, c_int, c_int, c_int,
-                                 c_vp, c_vp, c_vp, c_sz, c_vp]),
+    "mxk_linear_wq_nt": (c_int, [c_vp, c_int, c_i64, c_i64, c_vp, c_i64, c_vp, c_i64, c_vp, c_i64, c_int, c_int,
+                                 c_int, c_vp, c_vp, c_vp, c_sz, c_vp]),
     "mxk_linear_nt_workspace": (c_sz, [c_i64, c_i64, c_i64, c_int, c_int]),
     "mxk_linear_i8_workspace": (c_sz, [c_i64, c_i64, c_i64, c_int, c_int, c_i64, c_i64]),
     "mxk_linear_i8": (c_int, [c_vp, c_i64, c_vp, c_i64, c_i64, c_int, c_vp, c_i64, c_vp, c_i64, c_i64, c_int,

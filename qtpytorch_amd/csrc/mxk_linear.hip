@@ -507,7 +507,7 @@ static void launch_transpose_scales(const float* s, int64_t K, int64_t NB, float
 template <typename T>
 __global__ __launch_bounds__(NT_THREADS, 1) void k_linear_w4t_decode(
     const T* __restrict__ x, int M, int64_t K, int64_t N, const uint8_t* __restrict__ w,
-    const float* __restrict__ scales, const float* __restrict__ bias, float* __restrict__ out,
+    const float* __restrict__ scales, int scales_kb_major, const float* __restrict__ bias, float* __restrict__ out,
     float* __restrict__ partials, unsigned int* __restrict__ counters, int S) {
   // A staging (8 blocks x 4 steps x hi/lo x 1 KiB = 64 KiB), then the
   // partial sums [8 blocks][16 rows][256 (+4) columns]
@@ -609,7 +609,8 @@ __global__ __launch_bounds__(NT_THREADS, 1) void k_linear_w4t_decode(
 #pragma unroll
     for (int t = 0; t < 8; ++t) {
       const int64_t n = std::min<int64_t>(n0 + 16 * t + j, N - 1);
-      sc[t] = __uint_as_float(buf_load_b32(rs, (uint32_t)((n * KB + kb) * 4), 0u));
+      const int64_t si = scales_kb_major ? kb * N + n : n * KB + kb;
+      sc[t] = __uint_as_float(buf_load_b32(rs, (uint32_t)(si * 4), 0u));
     }
 #pragma unroll
     for (int t = 1; t < 8; ++t) load_tile(t);
@@ -735,13 +736,13 @@ static size_t nt_workspace_bytes(int64_t K, int64_t N) {
 
 template <typename T>
 static int launch_nt_decode(const T* x, int64_t M, int64_t K, int64_t N, const uint8_t* w, const float* scales,
-                            const float* bias, float* out, uint8_t* ws, hipStream_t st) {
+                            int scales_kb_major, const float* bias, float* out, uint8_t* ws, hipStream_t st) {
   const int S = nt_splits(K);
   const int64_t groups = ceil_div(N, NT_COLS);
   unsigned int* counters = S > 1 ? reinterpret_cast<unsigned int*>(ws) : nullptr;
   float* partials = S > 1 ? reinterpret_cast<float*>(ws + DEC_COUNTER_BYTES) : nullptr;
   hipLaunchKernelGGL((k_linear_w4t_decode<T>), dim3((unsigned)(groups * S)), dim3(NT_THREADS), 0, st, x, (int)M, K,
-                     N, w, scales, bias, out, partials, counters, S);
+                     N, w, scales, scales_kb_major, bias, out, partials, counters, S);
   return check_launch("linear_wq_nt(decode)");
 }
 
@@ -932,8 +933,9 @@ size_t mxk_linear_nt_workspace(int64_t M, int64_t K, int64_t N, int bits, int bl
 }
 
 int mxk_linear_wq_nt(const void* x, int x_type, int64_t M, int64_t K, const void* w_packed, int64_t w_nbytes,
-                     const float* w_scales, int64_t w_nscales, int64_t N, int kind, int bits, int block,
-                     const float* bias, float* out, void* workspace, size_t workspace_nbytes, void* stream) {
+                     const float* w_scales, int64_t w_nscales, const float* w_scales_t, int64_t N, int kind,
+                     int bits, int block, const float* bias, float* out, void* workspace, size_t workspace_nbytes,
+                     void* stream) {
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   if (M <= 0 || K <= 0 || N <= 0 || block <= 0) return fail(MXK_EINVAL, "linear_wq_nt: sizes must be positive");
   if (!x || !w_packed || !w_scales || !out) return fail(MXK_EINVAL, "linear_wq_nt: null pointer");
@@ -946,10 +948,14 @@ int mxk_linear_wq_nt(const void* x, int x_type, int64_t M, int64_t K, const void
       return fail(MXK_EINVAL, "linear_wq_nt: decode path needs a zero-initialised workspace of "
                               "mxk_linear_nt_workspace() bytes");
     uint8_t* part = reinterpret_cast<uint8_t*>(workspace);
-    if (x_type == MXK_IN_F32) return launch_nt_decode((const float*)x, M, K, N, pk, w_scales, bias, out, part, st);
-    if (x_type == MXK_IN_F16) return launch_nt_decode((const __half*)x, M, K, N, pk, w_scales, bias, out, part, st);
+    const float* sc = w_scales_t ? w_scales_t : w_scales;
+    const int kbm = w_scales_t ? 1 : 0;
+    if (x_type == MXK_IN_F32)
+      return launch_nt_decode((const float*)x, M, K, N, pk, sc, kbm, bias, out, part, st);
+    if (x_type == MXK_IN_F16)
+      return launch_nt_decode((const __half*)x, M, K, N, pk, sc, kbm, bias, out, part, st);
     if (x_type == MXK_IN_BF16)
-      return launch_nt_decode((const hip_bfloat16*)x, M, K, N, pk, w_scales, bias, out, part, st);
+      return launch_nt_decode((const hip_bfloat16*)x, M, K, N, pk, sc, kbm, bias, out, part, st);
   }
   if (x_type == MXK_IN_F32)
     return linear_t<true, float>((const float*)x, M, K, N, pk, w_nbytes, w_scales, kind, bits, block, bias, out, st);

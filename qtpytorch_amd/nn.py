@@ -118,7 +118,7 @@ class _LinearWQ(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, x, w, bias, in_features, out_features, w_scales_t):
-        ctx.w = w
+        ctx.w, ctx.w_scales_t = w, w_scales_t
         ctx.in_features, ctx.out_features = in_features, out_features
         return ops.linear_wq(x.detach(), w._mx_packed, w._mx_scales, w._mx_dtype, in_features, out_features,
                              w._mx_block, bias=bias, w_scales_t=w_scales_t)
@@ -126,8 +126,10 @@ class _LinearWQ(torch.autograd.Function):
     @staticmethod
     def backward(ctx, grad):
         w = ctx.w
+        # the block-major scales [out/128, in] of the forward are the K-block-major
+        # scales of the transposed product
         gi = ops.linear_wq_nt(grad.contiguous(), w._mx_packed, w._mx_scales, w._mx_dtype, ctx.in_features,
-                              ctx.out_features, w._mx_block)
+                              ctx.out_features, w._mx_block, w_scales_t=ctx.w_scales_t)
         return gi, None, None, None, None, None
 
 
@@ -137,18 +139,18 @@ class _LinearWQNT(torch.autograd.Function):
     of ops.linear_wq with the roles of the two dimensions exchanged."""
 
     @staticmethod
-    def forward(ctx, x, w, bias, in_features, out_features):
-        ctx.w = w
+    def forward(ctx, x, w, bias, in_features, out_features, w_scales_t):
+        ctx.w, ctx.w_scales_t = w, w_scales_t
         ctx.in_features, ctx.out_features = in_features, out_features
         return ops.linear_wq_nt(x.detach(), w._mx_packed, w._mx_scales, w._mx_dtype, out_features, in_features,
-                                w._mx_block, bias=bias)
+                                w._mx_block, bias=bias, w_scales_t=w_scales_t)
 
     @staticmethod
     def backward(ctx, grad):
         w = ctx.w
         gi = ops.linear_wq(grad.contiguous(), w._mx_packed, w._mx_scales, w._mx_dtype, ctx.out_features,
-                           ctx.in_features, w._mx_block)
-        return gi, None, None, None, None
+                           ctx.in_features, w._mx_block, w_scales_t=ctx.w_scales_t)
+        return gi, None, None, None, None, None
 
 
 class mx_dynamic_linear(nn.Module):
@@ -208,10 +210,25 @@ class mx_dynamic_linear(nn.Module):
             out = x_f.float().reshape(-1, self.in_features) @ w.dequantize().t()
             out = out.reshape(*x_f.shape[:-1], self.out_features)
             return out + b if b is not None else out
+        st = self._block_major_scales(w)
         if torch.is_grad_enabled() and x_f.requires_grad:
-            return _LinearWQNT.apply(x_f, w, b, self.in_features, self.out_features)
+            return _LinearWQNT.apply(x_f, w, b, self.in_features, self.out_features, st)
         return ops.linear_wq_nt(x_f, w._mx_packed, w._mx_scales, w._mx_dtype, self.out_features, self.in_features,
-                                w._mx_block, bias=b)
+                                w._mx_block, bias=b, w_scales_t=st)
+
+    def _block_major_scales(self, w) -> Optional[Tensor]:
+        """K-block-major copy [in/128, out] of the [out, in] weight's scales,
+        read by both int4 decode kernels (this forward and its input
+        gradient); made once per weight and rebuilt when the scales change."""
+        if not ops.decode_prepack_eligible(w._mx_dtype, w._mx_block, self.out_features, self.in_features):
+            return None
+        sc = w._mx_scales
+        key = (sc.data_ptr(), str(sc.device), sc._version)
+        cached = self.__dict__.get("_scales_t_cache")
+        if cached is None or cached[0] != key:
+            cached = (key, ops.prepack_scales(sc, self.out_features, self.in_features, w._mx_block))
+            self.__dict__["_scales_t_cache"] = cached
+        return cached[1]
 
     def extra_repr(self):
         return (f"in={self.in_features}, out={self.out_features}, "

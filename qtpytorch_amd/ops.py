@@ -392,11 +392,13 @@ def dynamic_quantize(x: Tensor, dt, granularity: str = "per_token") -> Tuple[Ten
 
 
 def linear_wq_nt(x: Tensor, w_packed: Tensor, w_scales: Tensor, dt, out_features: int, in_features: int,
-                 block: int = 128, bias: Optional[Tensor] = None) -> Tensor:
+                 block: int = 128, bias: Optional[Tensor] = None, w_scales_t: Optional[Tensor] = None) -> Tensor:
     """y = x.float() @ dequant(W).t() (+ bias) for a weight stored [out, in]
     (mx_dynamic_linear.forward, mxtorch.py:8949-8962, and the input gradient
     of _MXLinearAutograd, mxtorch.py:6729-6740); the weight is decoded in
-    registers, never dequantized to memory."""
+    registers, never dequantized to memory.  `w_scales_t` is an optional
+    K-block-major copy [in/128, out] of the scales (prepack_scales(w_scales,
+    out, in)), read by the int4 decode path."""
     dt = get_mx_dtype(dt)
     dev = L.require_gpu(x, w_packed, w_scales)
     kind, var = _kind_variant(dt)
@@ -421,13 +423,18 @@ def linear_wq_nt(x: Tensor, w_packed: Tensor, w_scales: Tensor, dt, out_features
         return out.reshape(*lead, N)
     b = None if bias is None else bias.to(device=dev, dtype=torch.float32).contiguous()
     wp, ws = w_packed.contiguous(), w_scales.contiguous().float()
+    if w_scales_t is not None:
+        if (w_scales_t.device != dev or w_scales_t.dtype != torch.float32 or not w_scales_t.is_contiguous()
+                or w_scales_t.numel() != ws.numel()):
+            raise L.MXKError("linear_wq_nt: w_scales_t must be prepack_scales() of this weight's scales")
     lib = L.lib()
     ws_bytes = lib.mxk_linear_nt_workspace(M, K, N, dt.bits, block)
     wk = _zeroed_workspace(ws_bytes, dev)
     with torch.cuda.device(dev):
         rc = lib.mxk_linear_wq_nt(xc.data_ptr(), L.elem_type(xc.dtype), M, K, wp.data_ptr(),
-                                  wp.numel() * wp.element_size(), ws.data_ptr(), ws.numel(), N, kind, dt.bits,
-                                  block, L.ptr(b), out.data_ptr(), L.ptr(wk), ws_bytes, L.stream_of(xc))
+                                  wp.numel() * wp.element_size(), ws.data_ptr(), ws.numel(), L.ptr(w_scales_t), N,
+                                  kind, dt.bits, block, L.ptr(b), out.data_ptr(), L.ptr(wk), ws_bytes,
+                                  L.stream_of(xc))
     L.check(rc, f"linear_wq_nt({dt.name}, M={M}, K={K}, N={N})")
     return out.reshape(*lead, N)
 
