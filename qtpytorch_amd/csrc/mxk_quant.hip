@@ -64,15 +64,17 @@ __global__ __launch_bounds__(256) void k_quant_fast(const T* __restrict__ x, int
   constexpr int GPB = 4 * GPW;
   // fp32: a lane's E elements are Q chunks of CH consecutive elements (one
   // 16-byte load each), chunk q at offset q * B / Q in the block, so that
-  // every load instruction of a wave covers whole lines; chunks whose codes
-  // would not fill whole bytes (1-bit codes of 4 fp32) stay one consecutive
-  // run.  16-bit inputs keep one consecutive run (measured faster).
+  // every load instruction of a wave covers whole lines.  1-bit codes of a
+  // chunk fill half a byte: lanes 2i and 2i+1 swap nibbles (DPP) and the
+  // even lane stores the byte.  16-bit inputs keep one consecutive run
+  // (measured faster).
   constexpr int PER16 = 16 / (int)sizeof(T);
-  constexpr bool SPLIT = sizeof(T) == 4 && E / PER16 > 1 && (PER16 * BITS) % 8 == 0;
+  constexpr bool NIB = sizeof(T) == 4 && BITS == 1 && E / PER16 > 1;
+  constexpr bool SPLIT = sizeof(T) == 4 && E / PER16 > 1 && ((PER16 * BITS) % 8 == 0 || NIB);
   constexpr int Q = SPLIT ? E / PER16 : 1;
   constexpr int CH = E / Q;
   constexpr int NW = (CH * BITS + 31) / 32;
-  constexpr int NB = CH * BITS / 8;
+  constexpr int NB = NIB ? 1 : CH * BITS / 8;
   constexpr uint32_t MASK = BITS == 32 ? 0xFFFFFFFFu : ((1u << BITS) - 1u);
   constexpr int H = MODE == Q_FP ? (1 << (BITS - 1)) : 1;
   __shared__ float sP[H + 1];
@@ -105,7 +107,13 @@ __global__ __launch_bounds__(256) void k_quant_fast(const T* __restrict__ x, int
         if (idx + i >= n_store) f = 0u;
         w[(i * BITS) >> 5] |= f << ((i * BITS) & 31);
       }
-      if (blk < nb) store_bytes<NB>(packed, idx * BITS / 8, packed_nbytes, w);
+      if constexpr (NIB) {
+        const uint32_t other = (uint32_t)__builtin_amdgcn_mov_dpp((int)w[0], 0xB1, 0xF, 0xF, true);
+        w[0] = (w[0] & 0xFu) | ((other & 0xFu) << 4);
+        if (blk < nb && (li & 1) == 0) store_bytes<1>(packed, idx / 8, packed_nbytes, w);
+      } else {
+        if (blk < nb) store_bytes<NB>(packed, idx * BITS / 8, packed_nbytes, w);
+      }
     }
     if (blk < nb && li == 0) scales[blk] = bp.s;
   }
@@ -677,11 +685,12 @@ template <typename T, int MODE, int BITS, int E>
 static bool try_fast_e(const T* x, int64_t n, int64_t nb, int block, uint8_t* packed, int64_t pbytes,
                        int64_t n_store, float* scales, float qf, hipStream_t st) {
   constexpr int PER16 = 16 / (int)sizeof(T);
-  constexpr bool SPLIT = sizeof(T) == 4 && E / PER16 > 1 && (PER16 * BITS) % 8 == 0;
+  constexpr bool NIB = sizeof(T) == 4 && BITS == 1 && E / PER16 > 1;
+  constexpr bool SPLIT = sizeof(T) == 4 && E / PER16 > 1 && ((PER16 * BITS) % 8 == 0 || NIB);
   constexpr int CH = SPLIT ? PER16 : E;
-  constexpr int NB = CH * BITS / 8;
+  constexpr int NB = NIB ? 1 : CH * BITS / 8;
   if (block % E != 0 || !is_pow2(block / E) || block / E > 64 || block / E < 2) return false;
-  if (!aligned16(x) || (CH * BITS) % 8 != 0 || NB > 16) return false;
+  if (!aligned16(x) || ((CH * BITS) % 8 != 0 && !NIB) || NB > 16) return false;
   if ((reinterpret_cast<uintptr_t>(packed) % (uintptr_t)NB) != 0) return false;
   bool done = false;
   launch_fast_b<T, MODE, BITS, E>(x, n, nb, block, packed, pbytes, n_store, scales, qf, st, &done);
