@@ -119,7 +119,8 @@ __global__ __launch_bounds__(256) void k_kv_gather(const uint8_t* __restrict__ c
 #pragma unroll
           for (int e = 0; e < 4; ++e) o[e] = o[e] + z;
         }
-        *reinterpret_cast<f32x4v*>(out + ((r * T + j) << (lq + 2)) + q * 4) = f32x4v{o[0], o[1], o[2], o[3]};
+        __builtin_nontemporal_store(f32x4v{o[0], o[1], o[2], o[3]},
+                                    reinterpret_cast<f32x4v*>(out + ((r * T + j) << (lq + 2)) + q * 4));
       }
     }
   }
