@@ -513,12 +513,15 @@ __global__ __launch_bounds__(256) void k_dequant_fast(const uint8_t* __restrict_
   // int codes of up to 4 bits decode through a table of their values as
   // floats (the same float(code) * s): measured faster than the bit-field
   // extract and conversion; a 256-entry table for 8-bit codes was slower
-  constexpr bool ITAB = MODE == Q_INT && BITS <= 4;
+  constexpr bool ITAB = (MODE == Q_INT && BITS <= 4) || MODE == Q_INT1;
   constexpr int TS = ITAB ? (1 << BITS) : 2 * H;
   __shared__ float sG[TS];
   if constexpr (MODE == Q_FP && BITS != 8) build_tables<BITS>(nullptr, sG);
   if constexpr (ITAB) {
-    for (int c = threadIdx.x; c < TS; c += blockDim.x) sG[c] = (float)((int32_t)((uint32_t)c << (32 - BITS)) >> (32 - BITS));
+    // int1: code 0 -> +s, 1 -> -s (mxtorch.py:1553-1557), i.e. (+-1) * s exactly
+    for (int c = threadIdx.x; c < TS; c += blockDim.x)
+      sG[c] = MODE == Q_INT1 ? (c == 0 ? 1.0f : -1.0f)
+                             : (float)((int32_t)((uint32_t)c << (32 - BITS)) >> (32 - BITS));
     __syncthreads();
   }
   const int64_t slots = (n + 3) / 4;
