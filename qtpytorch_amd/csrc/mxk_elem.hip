@@ -159,13 +159,14 @@ __device__ __forceinline__ uint64_t load_packed(__amdgpu_buffer_rsrc_t r, uint32
   }
 }
 
-template <int OP, int BITS, int OB, int LPB>
+template <int OP, int BITS, int OB, int LPB, int E>
 __global__ __launch_bounds__(256) void k_qelem_fast(const uint8_t* __restrict__ a, int64_t a_nbytes,
                                                     const float* __restrict__ sa_, const uint8_t* __restrict__ b,
                                                     int64_t b_nbytes, const float* __restrict__ sb_, int64_t n,
                                                     int64_t nb, uint8_t* __restrict__ out, int64_t out_nbytes,
                                                     float* __restrict__ out_scales) {
-  constexpr int E = 8, B = E * LPB, GPW = 64 / LPB, GPB = 4 * GPW;
+  constexpr int B = E * LPB, GPW = 64 / LPB, GPB = 4 * GPW;
+  static_assert(E * BITS <= 64, "codes of a lane in one 64-bit load");
   constexpr int INB = E * BITS / 8, ONB = E * OB / 8;
   constexpr uint32_t OMASK = (1u << OB) - 1u;
   const float qf = (float)((1 << (BITS - 1)) - 1);
@@ -354,21 +355,24 @@ static bool fused_ok(int block, int out_bits) {
   return block <= 256 && (byte_bits(out_bits) || out_bits == 16) && (block * out_bits) % 32 == 0;
 }
 
-template <int OP, int BITS, int OB, int LPB>
+template <int OP, int BITS, int OB, int LPB, int E>
 static void launch_fast_t(const void* a, int64_t an, const float* sa, const void* b, int64_t bn, const float* sb,
                           int64_t n, int64_t nb, void* out, int64_t onb, float* cs, hipStream_t st) {
   constexpr int GPB = 4 * (64 / LPB);
   const dim3 g((unsigned)std::min<int64_t>(ceil_div(nb, GPB), (int64_t)num_cus() * 16));
-  hipLaunchKernelGGL((k_qelem_fast<OP, BITS, OB, LPB>), g, dim3(256), 0, st, (const uint8_t*)a, an, sa,
+  hipLaunchKernelGGL((k_qelem_fast<OP, BITS, OB, LPB, E>), g, dim3(256), 0, st, (const uint8_t*)a, an, sa,
                      (const uint8_t*)b, bn, sb, n, nb, (uint8_t*)out, onb, cs);
 }
 
+// Codes per lane: 16 for operands of up to 4 bits whose packed result fits
+// 16 bytes (more bytes in flight per lane), else 8.
 template <int OP, int BITS, int OB>
 static void launch_fast_b(int block, const void* a, int64_t an, const float* sa, const void* b, int64_t bn,
                           const float* sb, int64_t n, int64_t nb, void* out, int64_t onb, float* cs, hipStream_t st) {
-  if (block == 64) launch_fast_t<OP, BITS, OB, 8>(a, an, sa, b, bn, sb, n, nb, out, onb, cs, st);
-  else if (block == 128) launch_fast_t<OP, BITS, OB, 16>(a, an, sa, b, bn, sb, n, nb, out, onb, cs, st);
-  else launch_fast_t<OP, BITS, OB, 32>(a, an, sa, b, bn, sb, n, nb, out, onb, cs, st);
+  constexpr int E = (BITS <= 4 && 16 * OB <= 128) ? 16 : 8;
+  if (block == 64) launch_fast_t<OP, BITS, OB, 64 / E, E>(a, an, sa, b, bn, sb, n, nb, out, onb, cs, st);
+  else if (block == 128) launch_fast_t<OP, BITS, OB, 128 / E, E>(a, an, sa, b, bn, sb, n, nb, out, onb, cs, st);
+  else launch_fast_t<OP, BITS, OB, 256 / E, E>(a, an, sa, b, bn, sb, n, nb, out, onb, cs, st);
 }
 
 template <int OP, int BITS>
