@@ -734,7 +734,7 @@ static bool try_rows(const T* x, int64_t n, int64_t nb, int block, uint8_t* pack
   if (block % 8 != 0 || block <= 256 || block > 8192 || !aligned16(x)) return false;
   if ((reinterpret_cast<uintptr_t>(packed) % (uintptr_t)(BITS >= 16 ? 16 : BITS)) != 0) return false;
   const int chunks = block / 8;
-  const dim3 grid((unsigned)std::max<int64_t>(1, std::min<int64_t>(nb, (int64_t)num_cus() * 8)));
+  const dim3 grid((unsigned)std::max<int64_t>(1, std::min<int64_t>(nb, (int64_t)num_cus() * 64)));
   if (chunks <= 256)
     hipLaunchKernelGGL((k_quant_rows<T, MODE, BITS, 1>), grid, dim3(256), 0, st, x, n, nb, block, packed, pbytes,
                        n_store, scales, qf);
