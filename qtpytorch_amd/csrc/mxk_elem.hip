@@ -178,17 +178,24 @@ __global__ __launch_bounds__(256) void k_qelem_fast(const uint8_t* __restrict__ 
     const int64_t blk = b0 + wave * GPW + g;
     const bool live = blk < nb;
     const int64_t e0 = blk * B + (int64_t)li * E;
-    const uint64_t wa = load_packed<INB>(ra, (uint32_t)(live ? e0 * BITS / 8 : 0));
-    const uint64_t wb = load_packed<INB>(rb, (uint32_t)(live ? e0 * BITS / 8 : 0));
+    uint64_t wa = load_packed<INB>(ra, (uint32_t)(live ? e0 * BITS / 8 : 0));
+    uint64_t wb = load_packed<INB>(rb, (uint32_t)(live ? e0 * BITS / 8 : 0));
     const float sa = live ? sa_[blk] : 1.0f, sb = live ? sb_[blk] : 1.0f;
+    // codes at or past n (and every code of a dead lane) read as 0: one mask
+    // per lane instead of a bounds select per element
+    const int64_t rem = live ? n - e0 : 0;
+    if (rem < E) {
+      const uint64_t keep = rem <= 0 ? 0ull : ((1ull << (rem * BITS)) - 1ull);
+      wa &= keep;
+      wb &= keep;
+    }
     float ac[E], bc[E], cv[E];
 #pragma unroll
     for (int i = 0; i < E; ++i) {
-      const bool in = live && e0 + i < n;
       const int32_t ca = (int32_t)((uint32_t)(wa >> (i * BITS)) << (32 - BITS)) >> (32 - BITS);
       const int32_t cb = (int32_t)((uint32_t)(wb >> (i * BITS)) << (32 - BITS)) >> (32 - BITS);
-      ac[i] = in ? (float)ca : 0.0f;
-      bc[i] = in ? (float)(OP == E_SUB ? -cb : cb) : 0.0f;
+      ac[i] = (float)ca;
+      bc[i] = (float)(OP == E_SUB ? -cb : cb);
     }
     float scale;
     if constexpr (OP == E_MUL) {
@@ -203,9 +210,11 @@ __global__ __launch_bounds__(256) void k_qelem_fast(const uint8_t* __restrict__ 
       const float ratio = hi / fmaxf(fminf(sa, sb), 1e-30f);
       const bool use_int = ratio <= 2.0f;  // uniform over the LPB lanes of the block
       float sc = hi;
-      float ra_ = sa / sc, rb_ = sb / sc, m = 0.0f;
+      float ra_ = 1.0f, rb_ = 1.0f, m = 0.0f;
       // one form per block (the lanes of a block agree on use_int)
       if (use_int) {
+        ra_ = sa / sc;
+        rb_ = sb / sc;
 #pragma unroll
         for (int i = 0; i < E; ++i) cv[i] = rne(ac[i] * ra_) + rne(bc[i] * rb_);
       } else {
@@ -227,7 +236,13 @@ __global__ __launch_bounds__(256) void k_qelem_fast(const uint8_t* __restrict__ 
         for (int i = 0; i < E; ++i) cv[i] = fminf(fmaxf(cv[i], -qf), qf);
       } else {
         sc = fmaxf(m, MXK_AMIN) / qf;
-        div_rn_all<E>(cv, sc, 1.0f / sc);  // RN(sum / sc)
+        // RN(sum / sc) by Markstein's correction for every element, without
+        // div_rn_all's small-dividend vote: sc >= 1e-12 / 127 > 2^-47, so a
+        // dividend below 2^-96 has |quotient| < 2^-49 on either path and
+        // rounds to code 0 below
+        const float y = 1.0f / sc;
+#pragma unroll
+        for (int i = 0; i < E; ++i) cv[i] = div_rn_nochk(cv[i], sc, y);
 #pragma unroll
         for (int i = 0; i < E; ++i) cv[i] = rne(fminf(fmaxf(cv[i], -qf), qf));
       }
