@@ -145,10 +145,10 @@ __global__ __launch_bounds__(256) void k_qelem(const uint8_t* __restrict__ a, in
 }
 
 // Fast path for byte-packed operands (BITS in {2, 4, 8}) and outputs
-// OB in {2, 4, 8, 16} with block = 8 * LPB (64, 128, 256): each lane owns 8
-// consecutive codes of one block (one 2/4/8-byte buffer load per operand,
-// loads past the buffer return 0), LPB lanes share a block, and the lane
-// packs its 8 result codes into one 2..16-byte store.  Buffers < 4 GiB.
+// OB in {2, 4, 8, 16} with block = E * LPB (64, 128, 256): each lane owns E
+// (8 or 16) consecutive codes of one block (one 2..16-byte buffer load per
+// operand, loads past the buffer return 0), LPB lanes share a block, and the
+// lane packs its E result codes into one 2..16-byte store.  Buffers < 4 GiB.
 template <int NBYTES>
 __device__ __forceinline__ uint64_t load_packed(__amdgpu_buffer_rsrc_t r, uint32_t off) {
   if constexpr (NBYTES == 2) return (uint64_t)__builtin_amdgcn_raw_buffer_load_b16(r, (int)off, 0, 0);
@@ -159,6 +159,26 @@ __device__ __forceinline__ uint64_t load_packed(__amdgpu_buffer_rsrc_t r, uint32
   }
 }
 
+// A lane's packed codes (NBYTES <= 16) as 64-bit words, low codes first.
+// A 16-byte load that would cross the buffer's end (nbytes) is made as two
+// 8-byte loads, so that the bytes below the end are read as for 8 codes per lane.
+template <int NBYTES>
+__device__ __forceinline__ void load_codes(__amdgpu_buffer_rsrc_t r, uint32_t off, int64_t nbytes,
+                                           uint64_t (&w)[(NBYTES + 7) / 8]) {
+  if constexpr (NBYTES == 16) {
+    if ((int64_t)off + 16 <= nbytes) {
+      const u32x4 v = buf_load_b128(r, off, 0u);
+      w[0] = (uint64_t)v[0] | ((uint64_t)v[1] << 32);
+      w[1] = (uint64_t)v[2] | ((uint64_t)v[3] << 32);
+    } else {
+      w[0] = load_packed<8>(r, off);
+      w[1] = load_packed<8>(r, off + 8u);
+    }
+  } else {
+    w[0] = load_packed<NBYTES>(r, off);
+  }
+}
+
 template <int OP, int BITS, int OB, int LPB, int E>
 __global__ __launch_bounds__(256) void k_qelem_fast(const uint8_t* __restrict__ a, int64_t a_nbytes,
                                                     const float* __restrict__ sa_, const uint8_t* __restrict__ b,
@@ -166,7 +186,8 @@ __global__ __launch_bounds__(256) void k_qelem_fast(const uint8_t* __restrict__ 
                                                     int64_t nb, uint8_t* __restrict__ out, int64_t out_nbytes,
                                                     float* __restrict__ out_scales) {
   constexpr int B = E * LPB, GPW = 64 / LPB, GPB = 4 * GPW;
-  static_assert(E * BITS <= 64, "codes of a lane in one 64-bit load");
+  static_assert(E * BITS <= 128, "codes of a lane in one load of up to 16 bytes");
+  constexpr int NW = (E * BITS + 63) / 64;  // 64-bit words of a lane's codes
   constexpr int INB = E * BITS / 8, ONB = E * OB / 8;
   constexpr uint32_t OMASK = (1u << OB) - 1u;
   const float qf = (float)((1 << (BITS - 1)) - 1);
@@ -178,22 +199,28 @@ __global__ __launch_bounds__(256) void k_qelem_fast(const uint8_t* __restrict__ 
     const int64_t blk = b0 + wave * GPW + g;
     const bool live = blk < nb;
     const int64_t e0 = blk * B + (int64_t)li * E;
-    uint64_t wa = load_packed<INB>(ra, (uint32_t)(live ? e0 * BITS / 8 : 0));
-    uint64_t wb = load_packed<INB>(rb, (uint32_t)(live ? e0 * BITS / 8 : 0));
+    uint64_t wa[NW], wb[NW];
+    load_codes<INB>(ra, (uint32_t)(live ? e0 * BITS / 8 : 0), a_nbytes, wa);
+    load_codes<INB>(rb, (uint32_t)(live ? e0 * BITS / 8 : 0), b_nbytes, wb);
     const float sa = live ? sa_[blk] : 1.0f, sb = live ? sb_[blk] : 1.0f;
     // codes at or past n (and every code of a dead lane) read as 0: one mask
     // per lane instead of a bounds select per element
     const int64_t rem = live ? n - e0 : 0;
     if (rem < E) {
-      const uint64_t keep = rem <= 0 ? 0ull : ((1ull << (rem * BITS)) - 1ull);
-      wa &= keep;
-      wb &= keep;
+      const int kb = rem <= 0 ? 0 : (int)rem * BITS;  // bits kept, < E * BITS
+#pragma unroll
+      for (int k = 0; k < NW; ++k) {
+        const int kk = kb - 64 * k;
+        const uint64_t keep = kk <= 0 ? 0ull : (kk >= 64 ? ~0ull : ((1ull << kk) - 1ull));
+        wa[k] &= keep;
+        wb[k] &= keep;
+      }
     }
     float ac[E], bc[E], cv[E];
 #pragma unroll
     for (int i = 0; i < E; ++i) {
-      const int32_t ca = (int32_t)((uint32_t)(wa >> (i * BITS)) << (32 - BITS)) >> (32 - BITS);
-      const int32_t cb = (int32_t)((uint32_t)(wb >> (i * BITS)) << (32 - BITS)) >> (32 - BITS);
+      const int32_t ca = (int32_t)((uint32_t)(wa[(i * BITS) >> 6] >> ((i * BITS) & 63)) << (32 - BITS)) >> (32 - BITS);
+      const int32_t cb = (int32_t)((uint32_t)(wb[(i * BITS) >> 6] >> ((i * BITS) & 63)) << (32 - BITS)) >> (32 - BITS);
       ac[i] = (float)ca;
       bc[i] = (float)(OP == E_SUB ? -cb : cb);
     }
@@ -379,12 +406,13 @@ static void launch_fast_t(const void* a, int64_t an, const float* sa, const void
                      (const uint8_t*)b, bn, sb, n, nb, (uint8_t*)out, onb, cs);
 }
 
-// Codes per lane: 16 for operands of up to 4 bits whose packed result fits
-// 16 bytes (more bytes in flight per lane), else 8.
+// Codes per lane: 16 when a lane's codes of each operand and its packed
+// result each fit 16 bytes (more bytes in flight and the per-block work over
+// more codes), else 8.
 template <int OP, int BITS, int OB>
 static void launch_fast_b(int block, const void* a, int64_t an, const float* sa, const void* b, int64_t bn,
                           const float* sb, int64_t n, int64_t nb, void* out, int64_t onb, float* cs, hipStream_t st) {
-  constexpr int E = (BITS <= 4 && 16 * OB <= 128) ? 16 : 8;
+  constexpr int E = (16 * BITS <= 128 && 16 * OB <= 128) ? 16 : 8;
   if (block == 64) launch_fast_t<OP, BITS, OB, 64 / E, E>(a, an, sa, b, bn, sb, n, nb, out, onb, cs, st);
   else if (block == 128) launch_fast_t<OP, BITS, OB, 128 / E, E>(a, an, sa, b, bn, sb, n, nb, out, onb, cs, st);
   else launch_fast_t<OP, BITS, OB, 256 / E, E>(a, an, sa, b, bn, sb, n, nb, out, onb, cs, st);
