@@ -265,13 +265,19 @@ def hadamard_signs(n: int, seed: int) -> Tensor:
     return torch.randint(0, 2, (n,), generator=gen).float() * 2 - 1
 
 
+@functools.lru_cache(maxsize=None)
 def reference_hadamard_seed(name: str) -> int:
-    """The seed quantize() derives for 'h' dtypes (mxtorch.py:1723).
-
-    ``hash(str)`` is salted per process unless PYTHONHASHSEED is fixed, so
-    callers that need reproducible signs pass the seed explicitly.
-    """
-    return hash(name) % (2 ** 31)
+    """The seed quantize() derives for 'h' dtypes, ``hash(name) % 2**31``
+    (mxtorch.py:1723), as it evaluates in a Python process started with
+    PYTHONHASHSEED=0: the expression is run in such a subprocess of this
+    interpreter.  (``hash(str)`` is salted per process otherwise, so the
+    reference's own seed changes from run to run.)"""
+    import subprocess
+    import sys
+    out = subprocess.run([sys.executable, "-c", f"print(hash({name!r}) % (2 ** 31))"],
+                         env={"PYTHONHASHSEED": "0", "PATH": "/usr/bin:/bin"}, capture_output=True, text=True,
+                         check=True)
+    return int(out.stdout.strip())
 
 
 def fwht(x: Tensor) -> Tensor:
@@ -336,7 +342,8 @@ def rotation_dim(shape) -> int:
 def quantize(x: Tensor, name: str, block: int = 128, seed: Optional[int] = None
              ) -> Tuple[Tensor, Tensor, int]:
     """quantize() CPU branch (mxtorch.py:1684-1763) for the base, 'h' and 'v'
-    variants.  For 'h' the seed defaults to the reference's hash-derived one."""
+    variants.  For 'h' the seed defaults to the reference's hash-derived one as it
+    evaluates under PYTHONHASHSEED=0."""
     kind, bits, mode, variant = parse_dtype(name)
     base = f"{kind}{bits}{mode}"
     x_f = x.float()

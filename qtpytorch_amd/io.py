@@ -10,6 +10,12 @@ The file is the reference's MX-native checkpoint, a torch.save'd dict:
 with the packed codes and scales byte for byte as in memory (mxtorch.py:
 9886-9893).  Differences from the reference, on purpose:
 
+  * entries of Hadamard ('h') tensors also hold "seed", the seed of the
+    rotation their codes were made with, so that a checkpoint dequantizes
+    with the same signs in any process (the reference re-derives the seed
+    from the per-process salted hash(name), mxtorch.py:1584, 1723); an entry
+    without it gets the default seed (ops.hadamard_seed);
+
   * mx_linear layers are saved under "<path>._mx_weight" / "<path>._mx_bias".
     The reference looks only for "weight"/"bias" attributes holding
     mx_tensors, so its save_quantized skips mx_linear's packed buffers
@@ -41,9 +47,12 @@ _FLOAT_NAMES = ("float32", "fp32", "float", "float16", "bfloat16")
 
 
 def _entry(t: mx_tensor) -> dict:
-    return {"dtype": t._mx_dtype.name, "packed": t._mx_packed.detach().cpu(),
-            "scales": t._mx_scales.detach().cpu(), "shape": list(t._mx_orig_shape),
-            "n": int(t._mx_n), "block": int(t._mx_block)}
+    e = {"dtype": t._mx_dtype.name, "packed": t._mx_packed.detach().cpu(),
+         "scales": t._mx_scales.detach().cpu(), "shape": list(t._mx_orig_shape),
+         "n": int(t._mx_n), "block": int(t._mx_block)}
+    if t._mx_seed is not None:
+        e["seed"] = int(t._mx_seed)
+    return e
 
 
 def _payload(p) -> Optional[mx_tensor]:
@@ -99,7 +108,7 @@ def load_quantized(checkpoint_path: str, model_class, dtype: Union[str, Dict[str
             if mod_name not in mods:
                 continue
             t = mx_tensor(entry["packed"].to(dev), entry["scales"].to(dev), get_mx_dtype(entry["dtype"]),
-                          torch.Size(entry["shape"]), int(entry["n"]), int(entry["block"]))
+                          torch.Size(entry["shape"]), int(entry["n"]), int(entry["block"]), seed=entry.get("seed"))
             if attr in ("_mx_weight", "_mx_bias"):
                 linear_parts.setdefault(mod_name, {})[attr] = t
                 continue
@@ -118,7 +127,8 @@ def load_quantized(checkpoint_path: str, model_class, dtype: Union[str, Dict[str
                 nn.Module.__init__(target)
                 target.in_features, target.out_features = in_f, out_f
                 target.mx_dtype, target.block, target.apply_bias = w._mx_dtype, w._mx_block, False
-                target._mx_weight = target._mx_bias = None
+                target.register_buffer("_mx_weight", None)
+                target.register_buffer("_mx_bias", None)
                 if mod_name:
                     _set_submodule(model, mod_name, target)
                 else:

@@ -42,8 +42,10 @@ class mx_linear(nn.Module):
         self.mx_dtype = get_mx_dtype(mx_dtype) if mx_dtype is not None else get_mx_dtype("int4d")
         self.block = block
         self.apply_bias = False
-        self._mx_weight = None
-        self._mx_bias = None
+        # buffers, as in the reference (mxtorch.py:7420-7425, 7447-7451), so
+        # that Module.to / cuda / state_dict / named_buffers see the packed data
+        self.register_buffer("_mx_weight", None)
+        self.register_buffer("_mx_bias", None)
         if device is not None:
             w = torch.randn(in_features, out_features, device=device) * 0.01
             self._mx_weight = mx_tensor.quantize(w, self.mx_dtype, block)
@@ -59,15 +61,20 @@ class mx_linear(nn.Module):
         m.mx_dtype = get_mx_dtype(mx_dtype)
         m.block = block
         m.apply_bias = False
-        m._mx_weight = mx_tensor.quantize(linear.weight.data.t(), m.mx_dtype, block)
-        m._mx_bias = (mx_tensor.quantize(linear.bias.data, m.mx_dtype, block)
-                      if linear.bias is not None else None)
+        m.register_buffer("_mx_weight", mx_tensor.quantize(linear.weight.data.t(), m.mx_dtype, block))
+        m.register_buffer("_mx_bias", mx_tensor.quantize(linear.bias.data, m.mx_dtype, block)
+                          if linear.bias is not None else None)
         return m
 
     def forward(self, x: Tensor) -> Tensor:
         w = self._mx_weight
         if w is None:
             raise RuntimeError("mx_linear has no weight (build it with from_linear or device=...)")
+        if not isinstance(w, mx_tensor):
+            # a float [in, out] weight put in place of the packed one (e.g. by
+            # Module.half(), which dequantizes floating buffers): quantize it again
+            w = mx_tensor.quantize(w.float(), self.mx_dtype, self.block)
+            self._mx_weight = w
         if w._mx_packed.device != x.device:
             w = w._move_device(x.device)
             self._mx_weight = w

@@ -34,7 +34,7 @@ class mx_tensor(torch.Tensor):
     """A quantized tensor that is a torch.Tensor (mxtorch.py:6028)."""
 
     def __new__(cls, packed: Tensor, scales: Tensor, mx_dtype: mx_dtype, orig_shape, n: int,
-                block: int = 128, requires_grad: bool = False):
+                block: int = 128, requires_grad: bool = False, seed: Optional[int] = None):
         dummy = torch.empty((), dtype=torch.float32, device=packed.device)
         inst = torch.Tensor._make_subclass(cls, dummy, requires_grad)
         inst._mx_packed = packed
@@ -43,34 +43,47 @@ class mx_tensor(torch.Tensor):
         inst._mx_orig_shape = torch.Size(orig_shape)
         inst._mx_n = int(n)
         inst._mx_block = int(block)
+        # seed of the 'h' rotation the codes were made with (None otherwise);
+        # it travels with the codes so that dequantize undoes that rotation
+        # in any process
+        inst._mx_seed = None
+        if mx_dtype.is_hadamard:
+            inst._mx_seed = int(seed) if seed is not None else ops.hadamard_seed(mx_dtype)
         return inst
 
-    def __init__(self, packed, scales, mx_dtype, orig_shape, n, block=128, requires_grad=False):
+    def __init__(self, packed, scales, mx_dtype, orig_shape, n, block=128, requires_grad=False, seed=None):
         pass
 
     # ---- tensor-subclass protocol (mxtorch.py:6058-6085) ----
     def __tensor_flatten__(self):
-        return ["_mx_packed", "_mx_scales"], {
-            "mx_dtype": self._mx_dtype, "orig_shape": self._mx_orig_shape,
-            "n": self._mx_n, "block": self._mx_block}
+        meta = {"mx_dtype": self._mx_dtype, "orig_shape": self._mx_orig_shape,
+                "n": self._mx_n, "block": self._mx_block}
+        if self._mx_seed is not None:
+            meta["seed"] = self._mx_seed
+        return ["_mx_packed", "_mx_scales"], meta
 
     @staticmethod
     def __tensor_unflatten__(inner_tensors, metadata, outer_size, outer_stride):
         return mx_tensor(inner_tensors["_mx_packed"], inner_tensors["_mx_scales"], metadata["mx_dtype"],
-                         metadata["orig_shape"], metadata["n"], metadata["block"])
+                         metadata["orig_shape"], metadata["n"], metadata["block"], seed=metadata.get("seed"))
 
     # ---- factory / inverse (mxtorch.py:6096-6115) ----
     @classmethod
-    def quantize(cls, x: Tensor, dt, block: int = 128, requires_grad: Optional[bool] = None) -> "mx_tensor":
+    def quantize(cls, x: Tensor, dt, block: int = 128, requires_grad: Optional[bool] = None, *,
+                 seed: Optional[int] = None) -> "mx_tensor":
+        """`seed` (keyword, 'h' dtypes only) overrides the rotation's default
+        seed, ops.hadamard_seed(dt)."""
         dt = get_mx_dtype(dt)
         if isinstance(x, mx_tensor):
             x = x.dequantize()
-        packed, scales, n = ops.quantize(x, dt, block)
-        return cls(packed, scales, dt, x.shape, n, block, True)
+        if dt.is_hadamard and seed is None:
+            seed = ops.hadamard_seed(dt)
+        packed, scales, n = ops.quantize(x, dt, block, seed=seed)
+        return cls(packed, scales, dt, x.shape, n, block, True, seed=seed)
 
     def dequantize(self) -> Tensor:
         flat = ops._dequant(self._mx_packed, self._mx_scales, self._mx_dtype, self._mx_n, self._mx_block,
-                            orig_shape=self._mx_orig_shape)
+                            orig_shape=self._mx_orig_shape, seed=self._mx_seed)
         return flat.reshape(self._mx_orig_shape)
 
     # ---- shape and metadata ----
@@ -170,7 +183,8 @@ class mx_tensor(torch.Tensor):
         bits = self._mx_dtype.bits
         packed, scales = ops.qelementwise("neg", self._mx_packed, self._mx_scales, None, None, self._mx_n,
                                           self._mx_block, bits, bits)
-        return mx_tensor(packed, scales, self._mx_dtype, self._mx_orig_shape, self._mx_n, self._mx_block)
+        return mx_tensor(packed, scales, self._mx_dtype, self._mx_orig_shape, self._mx_n, self._mx_block,
+                         seed=self._mx_seed)
 
     def __repr__(self):
         return (f"mx_tensor({self._mx_dtype.name}, shape={tuple(self._mx_orig_shape)}, "
@@ -217,7 +231,7 @@ class mx_tensor(torch.Tensor):
 
     def _move_device(self, device: torch.device) -> "mx_tensor":
         return mx_tensor(self._mx_packed.to(device), self._mx_scales.to(device), self._mx_dtype,
-                         self._mx_orig_shape, self._mx_n, self._mx_block)
+                         self._mx_orig_shape, self._mx_n, self._mx_block, seed=self._mx_seed)
 
     def cuda(self, device=None):
         if device is None:
@@ -233,11 +247,11 @@ class mx_tensor(torch.Tensor):
 
     def clone(self):
         return mx_tensor(self._mx_packed.clone(), self._mx_scales.clone(), self._mx_dtype, self._mx_orig_shape,
-                         self._mx_n, self._mx_block)
+                         self._mx_n, self._mx_block, seed=self._mx_seed)
 
     def detach(self):
         return mx_tensor(self._mx_packed.detach(), self._mx_scales.detach(), self._mx_dtype,
-                         self._mx_orig_shape, self._mx_n, self._mx_block)
+                         self._mx_orig_shape, self._mx_n, self._mx_block, seed=self._mx_seed)
 
     def reshape(self, *shape):
         if len(shape) == 1 and isinstance(shape[0], (tuple, list, torch.Size)):
@@ -263,17 +277,39 @@ class mx_tensor(torch.Tensor):
     def __getitem__(self, idx):
         return mx_tensor.quantize(self.dequantize()[idx], self._mx_dtype, self._mx_block)
 
+    # Module._apply (to / cuda / half) asks these of every floating buffer;
+    # answering them directly avoids a dequantize per question
+    def is_floating_point(self) -> bool:
+        return True
+
+    def is_complex(self) -> bool:
+        return False
+
+    def copy_(self, src, non_blocking: bool = False):
+        """In-place copy of another mx_tensor's packed data (Module.load_state_dict
+        copies saved buffers into the module's own this way)."""
+        if not isinstance(src, mx_tensor):
+            src = mx_tensor.quantize(src.float().to(self._mx_packed.device), self._mx_dtype, self._mx_block)
+        if (src._mx_dtype != self._mx_dtype or src._mx_n != self._mx_n or src._mx_block != self._mx_block
+                or src._mx_packed.shape != self._mx_packed.shape):
+            raise ValueError(f"copy_: {src!r} does not match the layout of {self!r}")
+        self._mx_packed.copy_(src._mx_packed, non_blocking=non_blocking)
+        self._mx_scales.copy_(src._mx_scales, non_blocking=non_blocking)
+        self._mx_orig_shape = src._mx_orig_shape
+        self._mx_seed = src._mx_seed
+        return self
+
     def fused_int8_linear(self, weight, bias=None):
         """Tensor-method binding of fused_int8_linear (mxtorch.py:11980-11982)."""
         return fused_int8_linear(self, weight, bias)
 
     def __reduce_ex__(self, protocol):
         return (_rebuild_mxtensor, (self._mx_packed.cpu(), self._mx_scales.cpu(), self._mx_dtype.name,
-                                    tuple(self._mx_orig_shape), self._mx_n, self._mx_block))
+                                    tuple(self._mx_orig_shape), self._mx_n, self._mx_block, self._mx_seed))
 
 
-def _rebuild_mxtensor(packed, scales, dt, shape, n, block):
-    return mx_tensor(packed, scales, get_mx_dtype(dt), torch.Size(shape), n, block)
+def _rebuild_mxtensor(packed, scales, dt, shape, n, block, seed=None):
+    return mx_tensor(packed, scales, get_mx_dtype(dt), torch.Size(shape), n, block, seed=seed)
 
 
 def _is_mx_name(s: str) -> bool:
