@@ -57,8 +57,13 @@ def graph_time(step, steps: int, warmup: int, repeats: int = 1) -> float:
     """Seconds per step: `steps` calls of step() captured in one graph,
     replayed between events on the current stream (the median over
     `repeats` timed replays)."""
-    for _ in range(max(warmup, 1)):
-        step()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    # warm-up on the stream the graph is captured on, so that per-stream
+    # workspaces exist before the capture
+    with torch.cuda.stream(s):
+        for _ in range(max(warmup, 1)):
+            step()
     torch.cuda.synchronize()
     if EAGER:
         st = torch.cuda.current_stream()
@@ -71,8 +76,6 @@ def graph_time(step, steps: int, warmup: int, repeats: int = 1) -> float:
         torch.cuda.synchronize()
         return e0.elapsed_time(e1) / 1e3 / steps
     g = torch.cuda.CUDAGraph()
-    s = torch.cuda.Stream()
-    s.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(s):
         with torch.cuda.graph(g, stream=s):
             for _ in range(steps):

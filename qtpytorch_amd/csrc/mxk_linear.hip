@@ -118,12 +118,19 @@ __global__ __launch_bounds__(256) void k_linear_generic(const T* __restrict__ x,
 //
 // Start-up order.  Each CU returns memory data in request order, and at
 // launch every workgroup asks for its weights at once, so whatever is queued
-// first arrives first.  A workgroup therefore requests, in this order: its x
-// rows (staged once in LDS as float, rows m >= M and rows past K as zeros),
-// each wave's RPW scales (one 16-byte load per lane), and only the first
-// 32-row step of weights; it waits for x, writes x and the scales to LDS,
-// passes one barrier, and only then fills the rest of the P-deep weight
-// prefetch.  Compute starts as soon as x and the first step are in.
+// first arrives first.  Every wave therefore requests its share of the x rows
+// (staged once in LDS as float, rows m >= M and rows past K as zeros) and its
+// RPW scales (one 16-byte load per lane); one barrier (no memory wait) puts
+// all of these ahead of any weight request; then each wave requests its
+// whole P-deep weight prefetch.  It waits for x and the scales only, stages
+// them, passes a second barrier that leaves the weight loads in flight, and
+// computes step by step as the weights arrive.
+//
+// Range.  x is staged as x * 2^ex with ex chosen per (row m, row group) so
+// that the group's largest |x| lies in [1, 2), and each wave's scales as
+// s * 2^es with its largest scale in [2^13, 2^14).  Every product x*s then
+// lies below 2^15, inside the f16 range, for inputs of any magnitude; the
+// epilogue multiplies by 2^-(ex + es).
 //
 // Per 32-row step a wave runs v_mfma_f32_16x16x32_f16 on
 //   A[m][k] = x[m,k] * s[k,nb]          split as f16 hi + f16 lo (22 bits)
@@ -211,9 +218,13 @@ __global__ __launch_bounds__(DEC_THREADS, 1) void k_linear_w4_decode(
   static_assert(XL * DEC_THREADS * EPL == 16 * R, "x staging must divide evenly");
   static_assert(RPW / 4 <= 64, "one 16-byte scale load per lane");
   static_assert(CPT % 4 == 0 && TPB * CPT == 2048, "reduction split");
+  constexpr int XG = RPW / EPL;  // consecutive lanes whose x loads make up one (row, row group)
+  static_assert(XG >= 1 && XG <= 64 && (XG & (XG - 1)) == 0 && (R / EPL) % XG == 0, "x row-group lanes");
   // x rows during the loop, then the waves' partials
   __shared__ __attribute__((aligned(16))) float sX[G::LX];
   __shared__ __attribute__((aligned(16))) float sS[DEC_WAVES * RPW];
+  // power-of-two exponent each (row m, row group) of x was staged with
+  __shared__ int sXe[16 * RG];
   __shared__ int s_flags;
   // the wave index goes through readfirstlane so that everything derived
   // from it (row ranges, scalar buffer offsets) is known to be wave-uniform
@@ -237,7 +248,8 @@ __global__ __launch_bounds__(DEC_THREADS, 1) void k_linear_w4_decode(
   const int kv = (int)(K - k0w < R ? K - k0w : R);     // its rows inside K (a multiple of 32)
   const int64_t kw = k0w + (int64_t)rg * RPW;          // this wave's first row
 
-  // ---- requests in arrival order: x rows, scales, the first weight step
+  // ---- requests in arrival order: x rows and scales of every wave, then
+  // the whole weight prefetch
   const __amdgpu_buffer_rsrc_t rx = make_rsrc(x, (uint32_t)((int64_t)M * K * sizeof(T)));
   const __amdgpu_buffer_rsrc_t rs = make_rsrc(scales_t, (uint32_t)(K * NB * 4));
   u32x4 xst[XL];
@@ -250,6 +262,10 @@ __global__ __launch_bounds__(DEC_THREADS, 1) void k_linear_w4_decode(
   }
   const int64_t r4 = kw + 4 * lane;  // K % 4 == 0: a 16-byte group is wholly in or out
   const u32x4 sst = buf_load_b128(rs, (lane < RPW / 4 && r4 < K) ? (uint32_t)((nb * K + r4) * 4) : DEC_OOB, 0u);
+  // every wave's x and scale requests are issued before any wave's weight
+  // requests: the CU returns data in request order, so x arrives first while
+  // the weight stream is already queued behind it
+  __builtin_amdgcn_sched_barrier(0);
 
   // ---- weight prefetch, P steps deep over a fully unrolled step sequence:
   // step st computes from slot st % P, then the slot is refilled with step
@@ -274,25 +290,57 @@ __global__ __launch_bounds__(DEC_THREADS, 1) void k_linear_w4_decode(
   // sink them next to their first use)
   __builtin_amdgcn_sched_barrier(0);
 
-  // ---- staged data to LDS: float x, row m at sX[m * XS]; scales per wave
+  // ---- range: the MFMA operand A = x*s is an f16 pair (hi + lo), so x and
+  // the scales are brought to fixed binades by powers of two first (exact),
+  // and the powers return in the epilogue.  x: each (row m, row group) is
+  // scaled so that its largest |x| lies in [1, 2); its XG loads sit in XG
+  // consecutive lanes.  Scales: each wave's largest scale goes to
+  // [2^13, 2^14).  Every product then lies below 2^15, within the f16 range,
+  // and a product 2^k below its row group's largest one keeps full
+  // precision down to k = 28 (f16 normals for hi, then lo).
 #pragma unroll
   for (int i = 0; i < XL; ++i) {
     const int e = threadIdx.x + DEC_THREADS * i;
     const int m = e / (R / EPL), c = e % (R / EPL);
-    float* dst = sX + m * XS + c * EPL;
+    float v[EPL];
     if constexpr (EPL == 4) {
-      *reinterpret_cast<f32x4*>(dst) = __builtin_bit_cast(f32x4, xst[i]);
+#pragma unroll
+      for (int u = 0; u < 4; ++u) v[u] = __uint_as_float(xst[i][u]);
     } else {
       const T* tt = reinterpret_cast<const T*>(&xst[i]);
-      *reinterpret_cast<f32x4*>(dst) =
-          f32x4{ElemT<T>::cvt(tt[0]), ElemT<T>::cvt(tt[1]), ElemT<T>::cvt(tt[2]), ElemT<T>::cvt(tt[3])};
-      *reinterpret_cast<f32x4*>(dst + 4) =
-          f32x4{ElemT<T>::cvt(tt[4]), ElemT<T>::cvt(tt[5]), ElemT<T>::cvt(tt[6]), ElemT<T>::cvt(tt[7])};
+#pragma unroll
+      for (int u = 0; u < EPL; ++u) v[u] = ElemT<T>::cvt(tt[u]);
     }
+    float mx = 0.0f;
+#pragma unroll
+    for (int u = 0; u < EPL; ++u) mx = fmaxf(mx, __builtin_fabsf(v[u]));
+    mx = group_max<XG>(mx);
+    const int be = (int)((__float_as_uint(mx) >> 23) & 0xFFu);
+    const int xe = be == 0xFF ? 0 : 127 - (be == 0 ? 1 : be);  // zero rows: any shift
+#pragma unroll
+    for (int u = 0; u < EPL; ++u) v[u] = __builtin_ldexpf(v[u], xe);
+    float* dst = sX + m * XS + c * EPL;
+#pragma unroll
+    for (int u = 0; u < EPL; u += 4) *reinterpret_cast<f32x4*>(dst + u) = f32x4{v[u], v[u + 1], v[u + 2], v[u + 3]};
+    if ((lane & (XG - 1)) == 0) sXe[m * RG + (c * EPL) / RPW] = xe;
   }
+  float sv[4];
+  float smx = 0.0f;
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    sv[u] = __uint_as_float(sst[u]);
+    smx = fmaxf(smx, __builtin_fabsf(sv[u]));
+  }
+  smx = group_max<64>(smx);
+  const int sbe = (int)((__float_as_uint(smx) >> 23) & 0xFFu);
+  const int se = sbe == 0xFF ? 0 : 140 - (sbe == 0 ? 1 : sbe);  // largest scale to [2^13, 2^14)
   float* wS = sS + wave * RPW;
-  if (lane < RPW / 4) *reinterpret_cast<f32x4*>(wS + 4 * lane) = __builtin_bit_cast(f32x4, sst);
-  __syncthreads();
+  if (lane < RPW / 4)
+    *reinterpret_cast<f32x4*>(wS + 4 * lane) = f32x4{__builtin_ldexpf(sv[0], se), __builtin_ldexpf(sv[1], se),
+                                                     __builtin_ldexpf(sv[2], se), __builtin_ldexpf(sv[3], se)};
+  // LDS writes done, then a barrier that leaves the weight loads in flight
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0), vmcnt untouched
+  dec_barrier_nofence();
 #pragma unroll
   for (int q = 1; q < P && q < STEPS; ++q) issue(q, q);
   __builtin_amdgcn_sched_barrier(0);
@@ -347,10 +395,14 @@ __global__ __launch_bounds__(DEC_THREADS, 1) void k_linear_w4_decode(
   float* rwv = red + wave * 16 * DEC_RS;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
+    // undo the code placement (2^24 even, 2^20 odd) and the range scaling of
+    // x row 4g+i and of this wave's scales
+    const int sh = -sXe[(4 * g + i) * RG + rg] - se;
     float v[8];
 #pragma unroll
     for (int t = 0; t < 8; ++t)
-      v[t] = (t & 1) ? (acc[t][i] - corr[i]) * 1048576.0f : (acc[t][i] - corr[i] * 0.0625f) * 16777216.0f;
+      v[t] = (t & 1) ? __builtin_ldexpf(acc[t][i] - corr[i], 20 + sh)
+                     : __builtin_ldexpf(acc[t][i] - corr[i] * 0.0625f, 24 + sh);
     float* dst = rwv + (4 * g + i) * DEC_RS + 8 * j;
     *reinterpret_cast<f32x4*>(dst) = f32x4{v[0], v[1], v[2], v[3]};
     *reinterpret_cast<f32x4*>(dst + 4) = f32x4{v[4], v[5], v[6], v[7]};
@@ -405,11 +457,15 @@ __global__ __launch_bounds__(DEC_THREADS, 1) void k_linear_w4_decode(
 #pragma unroll
     for (int q = 0; q < 8; ++q) total += (unsigned)((now >> (8 * q)) & 0xFFull);
     const bool same = ((now >> (8 * xcc)) & 0xFFull) == (unsigned long long)S;
-    s_flags = (total == (unsigned)S ? 1 : 0) | (same ? 2 : 0);
+    const bool last = total == (unsigned)S;
+    // no split of this call touches the counter again: reset it now, so
+    // that the reset's round trip overlaps the reads below
+    if (last) __hip_atomic_store(&counters[cg], 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    s_flags = (last ? 1 : 0) | (same ? 2 : 0);
   }
   __syncthreads();
   const int fl = s_flags;
-  if (!(fl & 1) || !rt) return;  // thread 0 is a reduction thread: it resets the counter below
+  if (!(fl & 1) || !rt) return;
   // last arrival: sum the S partials in split order (its own from registers)
   f32x4 tot[CPT / 4];
   for (int sb = 0; sb < S; sb += 8) {
@@ -441,7 +497,6 @@ __global__ __launch_bounds__(DEC_THREADS, 1) void k_linear_w4_decode(
       *reinterpret_cast<f32x4*>(out + (int64_t)m * N + col + 4 * h) = o;
     }
   }
-  if (threadIdx.x == 0) __hip_atomic_store(&counters[cg], 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // sT[b][k] = s[k][b]: the reference's scales of a [K, N] weight with blocks
@@ -832,7 +887,8 @@ static bool decode_eligible(int64_t M, int64_t K, int64_t N, int kind, int bits,
     return false;
   // partial buffer: S * (N/128) * 8 KiB, addressed with 32-bit offsets
   if ((K / 32 + 1) * (N / 128) * 8192 >= (int64_t(1) << 31)) return false;
-  return true;
+  // each XCC's arrival count is 8 bits of a 64-bit counter: at most 255 splits
+  return plan_decode(K, N).S <= 255;
 }
 
 template <bool WT, typename T, int MODE, int BITS>
@@ -875,6 +931,7 @@ extern "C" {
 size_t mxk_linear_workspace(int64_t M, int64_t K, int64_t N, int bits, int block) {
   if (M < 1 || M > 16 || bits != 4 || block != 128 || K <= 0 || N <= 0 || K % 32 != 0 || N % 128 != 0) return 0;
   DecodePlan p = plan_decode(K, N);
+  if (p.S > 255) return 0;  // the generic kernel takes these shapes
   return p.counter_bytes + p.partial_bytes + p.scales_t_bytes;
 }
 

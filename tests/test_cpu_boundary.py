@@ -93,3 +93,17 @@ def test_bad_arguments_return_errors_without_gpu():
     assert rc == -22
     rc = h.mxk_linear_prepack_scales(8, 256, 256, 64, 8, None)
     assert rc == -22
+
+
+def test_decode_workspace_limits():
+    """The int4 decode path counts split arrivals in 8 bits per XCC, so it
+    takes no shape that would need more than 255 splits: for those the
+    workspace query returns 0 (the generic kernel runs instead).  Covered
+    shapes get a workspace with the 64 KiB counter prefix."""
+    from qtpytorch_amd import _lib as L
+    h = L.lib()
+    assert h.mxk_linear_workspace(16, 8192, 8192, 4, 128) >= 65536
+    # one 128-column block: at most 2048 rows of K per split -> K = 600000 needs 293 splits
+    assert h.mxk_linear_workspace(1, 600000, 128, 4, 128) == 0
+    assert h.mxk_linear_workspace(1, 2048 * 255, 128, 4, 128) > 0
+    assert h.mxk_linear_workspace(17, 8192, 8192, 4, 128) == 0     # M > 16: generic kernel
