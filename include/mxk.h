@@ -177,6 +177,21 @@ int mxk_linear_wq(const void* x, int x_type, int64_t M, int64_t K, const void* w
                   int block, const float* bias, float* out, void* workspace,
                   size_t workspace_nbytes, void* stream);
 
+/* mxk_linear_wq without a workspace argument, for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  No counterpart in the reference.
+ * Same arguments and result as mxk_linear_wq; the decode path's split-K
+ * workspace is a static 8 MiB device array of the library (one per GPU,
+ * held until the process ends), so shapes that need more (for example
+ * N = 16384, K = 8192) return MXK_EINVAL: pass w_scales_t or use
+ * mxk_linear_wq.  The call allocates nothing; the first call on a device
+ * clears the array's counters with a fill kernel on `stream`.  All calls on
+ * one GPU share the array: calls that overlap on one GPU (other streams,
+ * concurrent graph replays) race and must not be issued. */
+int mxk_linear_wq_noalloc(const void* x, int x_type, int64_t M, int64_t K, const void* w_packed,
+                          const float* w_scales, const float* w_scales_t, int64_t N, int kind, int bits, int block,
+                          const float* bias, float* out, void* stream);
+
 /* One step of kv_cache_quantizer.append_kv (mxtorch.py:3039-3067) written
  * into a caller-owned ring slot (the reference appends a new mx_tensor to a
  * Python list instead, mxtorch.py:3058-3065).

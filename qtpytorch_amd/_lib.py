@@ -48,6 +48,8 @@ SIGNATURES = {
     "mxk_linear_wq": (c_int, [c_vp, c_int, c_i64, c_i64, c_vp, c_vp, c_vp, c_i64, c_int, c_int, c_int, c_vp,
                               c_vp, c_vp, c_sz, c_vp]),
     "mxk_linear_prepack_scales": (c_int, [c_vp, c_i64, c_i64, c_int, c_vp, c_vp]),
+    "mxk_linear_wq_noalloc": (c_int, [c_vp, c_int, c_i64, c_i64, c_vp, c_vp, c_vp, c_i64, c_int, c_int, c_int, c_vp,
+                                      c_vp, c_vp]),
     "mxk_kv_append": (c_int, [c_vp, c_vp, c_int, c_i64, c_int, c_int, c_int, c_int, c_int, c_vp, c_vp, c_vp, c_vp,
                               c_vp, c_vp]),
     "mxk_kv_gather": (c_int, [c_vp, c_vp, c_vp, c_i64, c_int, c_int, c_int, c_int, c_i64, c_i64, c_i64, c_vp,

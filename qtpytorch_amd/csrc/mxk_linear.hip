@@ -12,6 +12,8 @@
 #include "mxk_internal.h"
 
 #include <algorithm>
+#include <mutex>
+#include <vector>
 
 namespace mxk {
 
@@ -922,6 +924,51 @@ static int linear_t(const T* x, int64_t M, int64_t K, int64_t N, const uint8_t* 
   return fail(MXK_EUNSUPPORTED, "linear_wq: unsupported weight kind/bits");
 }
 
+// ---------------------------------------------------------------- allocation-free entry
+// mxk_linear_wq_noalloc runs the decode linear with its split-K workspace in
+// this file-scope array instead of a caller-provided buffer.  Each GPU holds
+// its own copy until the process ends.  Host code never passes the array's
+// name to a kernel (on the host it is only a stand-in): it uses the device
+// address that hipGetSymbolAddress returns for the current device, kept per
+// device.  The first NOALLOC_COUNTER_BYTES are the arrival counters, which
+// must start at zero and which every call leaves zero.
+#define NOALLOC_SCRATCH_BYTES (8u << 20)
+static __device__ __align__(256) unsigned char scratch[NOALLOC_SCRATCH_BYTES];
+
+__global__ void k_zero_words(uint32_t* __restrict__ p, uint32_t words) {
+  for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < words; i += gridDim.x * blockDim.x) p[i] = 0u;
+}
+
+// The current device's copy of `scratch`; on the first call for a device
+// (with that device current) its address is looked up and its counter
+// prefix is cleared by a fill kernel on `st` (no memset, so the call may
+// also be captured into a graph).  Returns nullptr on failure (message set).
+static void* noalloc_scratch(hipStream_t st) {
+  static std::mutex mu;
+  static std::vector<void*> ptrs;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) {
+    fail(MXK_ELAUNCH, "linear_wq_noalloc: hipGetDevice failed");
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lk(mu);
+  if ((int)ptrs.size() <= dev) ptrs.resize(dev + 1, nullptr);
+  if (!ptrs[dev]) {
+    void* ptr = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !ptr) {
+      fail(MXK_ELAUNCH, std::string("linear_wq_noalloc: hipGetSymbolAddress(scratch) failed: ") +
+                            hipGetErrorString(e));
+      return nullptr;
+    }
+    hipLaunchKernelGGL(k_zero_words, dim3(16), dim3(256), 0, st, reinterpret_cast<uint32_t*>(ptr),
+                       (uint32_t)(DEC_COUNTER_BYTES / 4));
+    if (check_launch("linear_wq_noalloc(clear counters)") != MXK_OK) return nullptr;
+    ptrs[dev] = ptr;
+  }
+  return ptrs[dev];
+}
+
 }  // namespace mxk
 
 using namespace mxk;
@@ -982,6 +1029,28 @@ int mxk_linear_wq(const void* x, int x_type, int64_t M, int64_t K, const void* w
     return linear_t<false, hip_bfloat16>((const hip_bfloat16*)x, M, K, N, pk, pbytes, w_scales, kind, bits, block,
                                          bias, out, st);
   return fail(MXK_EINVAL, "linear_wq: bad input type");
+}
+
+int mxk_linear_wq_noalloc(const void* x, int x_type, int64_t M, int64_t K, const void* w_packed,
+                          const float* w_scales, const float* w_scales_t, int64_t N, int kind, int bits, int block,
+                          const float* bias, float* out, void* stream) {
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  if (M <= 0 || K <= 0 || N <= 0 || block <= 0) return fail(MXK_EINVAL, "linear_wq_noalloc: sizes must be positive");
+  if (!x || !w_packed || !w_scales || !out) return fail(MXK_EINVAL, "linear_wq_noalloc: null pointer");
+  size_t need = 0;
+  if (decode_eligible(M, K, N, kind, bits, block, x, x_type, w_packed)) {
+    const DecodePlan p = plan_decode(K, N);
+    need = p.counter_bytes + p.partial_bytes + (w_scales_t ? 0 : p.scales_t_bytes);
+  }
+  if (need > NOALLOC_SCRATCH_BYTES)
+    return fail(MXK_EINVAL, "linear_wq_noalloc: this shape needs " + std::to_string(need) +
+                                " bytes of split-K workspace, more than the " +
+                                std::to_string(NOALLOC_SCRATCH_BYTES) +
+                                "-byte static scratch (pass w_scales_t, or use mxk_linear_wq with a workspace)");
+  void* ws = nullptr;
+  if (need > 0 && !(ws = noalloc_scratch(st))) return MXK_ELAUNCH;
+  return mxk_linear_wq(x, x_type, M, K, w_packed, w_scales, w_scales_t, N, kind, bits, block, bias, out, ws,
+                       need > 0 ? NOALLOC_SCRATCH_BYTES : 0, stream);
 }
 
 size_t mxk_linear_nt_workspace(int64_t M, int64_t K, int64_t N, int bits, int block) {
