@@ -770,3 +770,101 @@ def mx_linear_autograd_backward(grad: Tensor, w_packed: Tensor, w_scales: Tensor
     if len(orig_shape) > 2:
         gi = gi.reshape(*orig_shape[:-1], in_features)
     return gi
+
+
+# ---------------------------------------------------------------------------
+# model-level modules built around mx_linear (mxtorch.py:7612-7660,
+# 7800-7877, 9161-9260)
+# ---------------------------------------------------------------------------
+def _dq_entry(e, name: str, block: int) -> Tensor:
+    """Dequantize (packed, scales, shape) produced by quantize()."""
+    packed, scales, shape = e
+    n = int(math.prod(shape))
+    return dequant(packed, scales, name, n, block, orig_shape=shape, hadamard_mode="rows").reshape(shape)
+
+
+def layer_norm_from(weight: Tensor, bias: Optional[Tensor], name: str, block: int = 128):
+    """mx_layer_norm.from_layer_norm (mxtorch.py:7640-7649): weight and bias
+    quantized with the module's dtype.  Returns ((packed, scales, shape) or None) x 2."""
+    w = quantize(weight, name, block)[:2] + (tuple(weight.shape),)
+    b = quantize(bias, name, block)[:2] + (tuple(bias.shape),) if bias is not None else None
+    return w, b
+
+
+def layer_norm_forward(x: Tensor, w, b, normalized_shape, eps: float, name: str, block: int = 128):
+    """mx_layer_norm.forward (mxtorch.py:7651-7657): F.layer_norm of x.float()
+    with the dequantized weight and bias, requantized with the module's dtype.
+    Returns (packed, scales, shape)."""
+    w_f = _dq_entry(w, name, block) if w is not None else None
+    b_f = _dq_entry(b, name, block) if b is not None else None
+    out = F.layer_norm(x.float(), tuple(normalized_shape), w_f, b_f, eps)
+    p, s, _ = quantize(out, name, block)
+    return p, s, tuple(out.shape)
+
+
+def mha_from(in_proj_weight: Tensor, out_proj_weight: Tensor, out_proj_bias: Optional[Tensor], name: str,
+             block: int = 128):
+    """mx_multihead_attention.from_mha (mxtorch.py:7808-7842) for the packed
+    in_proj case: in_proj_weight quantized as stored ([3E, E]); out_proj an
+    mx_linear (quantize(W.t()), and its bias quantized)."""
+    inp = quantize(in_proj_weight, name, block)[:2] + (tuple(in_proj_weight.shape),)
+    outw = quantize(out_proj_weight.t(), name, block)[:2] + (tuple(out_proj_weight.t().shape),)
+    outb = (quantize(out_proj_bias, name, block)[:2] + (tuple(out_proj_bias.shape),)
+            if out_proj_bias is not None else None)
+    return inp, outw, outb
+
+
+def mha_forward(query: Tensor, key: Tensor, value: Tensor, embed_dim: int, num_heads: int, in_proj, in_proj_bias,
+                out_w, out_b, name: str, block: int = 128, need_weights: bool = True):
+    """mx_multihead_attention.forward (mxtorch.py:7848-7873), eval mode, no
+    masks: F.multi_head_attention_forward on float inputs with the
+    dequantized in_proj weight.  The output projection weight is
+    mx_linear.weight, the dequantized [in, out] storage, passed where
+    F.multi_head_attention_forward expects [out, in]; its bias is the
+    dequantized stored bias.  The output is requantized with the module's
+    dtype.  Returns ((packed, scales, shape), attn_weights, float output).
+    Inputs are passed as given: F.multi_head_attention_forward reads
+    dimension 0 as the sequence even for batch_first modules."""
+    w_in = _dq_entry(in_proj, name, block)
+    w_out = _dq_entry(out_w, name, block)
+    b_out = _dq_entry(out_b, name, block) if out_b is not None else None
+    # the inputs go to F.multi_head_attention_forward as given, dimension 0
+    # read as the sequence, whatever batch_first says (the reference does not
+    # transpose)
+    q, k, v = query.float(), key.float(), value.float()
+    out, attn = F.multi_head_attention_forward(q, k, v, embed_dim, num_heads, w_in, in_proj_bias, None, None, False,
+                                               0.0, w_out, b_out, training=False, need_weights=need_weights)
+    p, s, _ = quantize(out, name, block)
+    return (p, s, tuple(out.shape)), attn, out
+
+
+def encoder_layer_forward(src: Tensor, params: dict, name: str, block: int = 128, nhead: int = 4,
+                          eps: float = 1e-5, activation=F.relu) -> Tensor:
+    """mx_transformer_encoder_layer.forward (mxtorch.py:9260-9278), eval mode,
+    norm_first=False, from from_encoder_layer (mxtorch.py:9214-9234).
+    `params` holds the nn.TransformerEncoderLayer's float parameters by name.
+      x  = src.float() + dequant(self_attn(src))          (_sa_block)
+      x  = dequant(norm1(x))
+      x  = x + linear2(act(linear1(x)))                    (_ff_block; the
+           mx_linear biases are re-quantized zeros, mxtorch.py:7434-7436)
+      out = dequant(norm2(x))"""
+    E = src.shape[-1]
+    inp, outw, outb = mha_from(params["self_attn.in_proj_weight"], params["self_attn.out_proj.weight"],
+                               params["self_attn.out_proj.bias"], name, block)
+    (sp, ss, sshape), _, _ = mha_forward(src, src, src, E, nhead, inp, params["self_attn.in_proj_bias"], outw, outb,
+                                         name, block)
+    x = src.float() + _dq_entry((sp, ss, sshape), name, block)
+    n1w, n1b = layer_norm_from(params["norm1.weight"], params["norm1.bias"], name, block)
+    x = _dq_entry(layer_norm_forward(x, n1w, n1b, (E,), eps, name, block), name, block)
+    ffs = []
+    for lin in ("linear1", "linear2"):
+        W = params[f"{lin}.weight"]
+        wp, ws, _ = linear_from_weight(W, name, block)
+        ffs.append((wp, ws, W.shape[1], W.shape[0]))
+    wp, ws, K1, N1 = ffs[0]
+    h = linear_forward(x, wp, ws, name, K1, N1, block, has_bias=True)
+    wp, ws, K2, N2 = ffs[1]
+    ff = linear_forward(activation(h), wp, ws, name, K2, N2, block, has_bias=True)
+    x = x + ff
+    n2w, n2b = layer_norm_from(params["norm2.weight"], params["norm2.bias"], name, block)
+    return _dq_entry(layer_norm_forward(x, n2w, n2b, (E,), eps, name, block), name, block)

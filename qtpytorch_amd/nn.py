@@ -242,11 +242,174 @@ class mx_dynamic_linear(nn.Module):
                 f"w={self.weight_dtype.name}, act={self.act_dtype.name}")
 
 
+def _dq(t) -> Optional[Tensor]:
+    """Float value of an optional weight: dequantized mx_tensor, else float."""
+    if t is None:
+        return None
+    if isinstance(t, nn.Parameter) and isinstance(t.data, mx_tensor):
+        t = t.data
+    return t.dequantize() if isinstance(t, mx_tensor) else t.float()
+
+
+class mx_layer_norm(nn.Module):
+    """nn.LayerNorm with packed weight and bias (mxtorch.py:7612-7660): the
+    normalisation runs in float32 on the dequantized parameters and the
+    output is quantized with the module's dtype (an mx_tensor)."""
+
+    def __init__(self, normalized_shape, eps: float = 1e-5, mx_dtype: mx_dtype = None, block: int = 128):
+        super().__init__()
+        self.mx_dtype = get_mx_dtype(mx_dtype) if mx_dtype is not None else get_mx_dtype("int8d")
+        self.normalized_shape = torch.Size((normalized_shape,) if isinstance(normalized_shape, int)
+                                           else normalized_shape)
+        self.eps = eps
+        self.elementwise_affine = True
+        self.block = block
+        # packed parameters as buffers, so that Module.to / state_dict /
+        # save_quantized see them (the reference wraps them in Parameters);
+        # a module built without from_layer_norm has no affine parameters
+        # (the reference quantizes ones and zeros, mxtorch.py:7627-7636)
+        self.register_buffer("weight", None)
+        self.register_buffer("bias", None)
+
+    @classmethod
+    def from_layer_norm(cls, ln: nn.LayerNorm, mx_dtype, block: int = 128) -> "mx_layer_norm":
+        m = cls(ln.normalized_shape, ln.eps, mx_dtype, block)
+        m.elementwise_affine = ln.elementwise_affine
+        m.weight = (mx_tensor.quantize(ln.weight.data, m.mx_dtype, block) if ln.weight is not None else None)
+        m.bias = (mx_tensor.quantize(ln.bias.data, m.mx_dtype, block) if ln.bias is not None else None)
+        return m
+
+    def forward(self, x: Tensor) -> mx_tensor:
+        x_f = x.dequantize() if isinstance(x, mx_tensor) else x.float()
+        out = torch.nn.functional.layer_norm(x_f, self.normalized_shape, _dq(self.weight), _dq(self.bias), self.eps)
+        return mx_tensor.quantize(out, self.mx_dtype, self.block)
+
+    def extra_repr(self):
+        return f"shape={tuple(self.normalized_shape)}, dtype={self.mx_dtype.name}"
+
+
+class mx_multihead_attention(nn.Module):
+    """nn.MultiheadAttention with packed projections (mxtorch.py:7800-7877):
+    in_proj_weight (or q/k/v_proj_weight) quantized as stored, out_proj an
+    mx_linear; in_proj_bias, bias_k and bias_v stay float.
+
+    forward keeps the reference's arithmetic, which differs from
+    nn.MultiheadAttention in two ways: the output projection weight is
+    out_proj.weight, the dequantized [in, out] storage of the mx_linear,
+    placed where F.multi_head_attention_forward expects [out, in]; and the
+    inputs are passed as given, dimension 0 read as the sequence even for
+    batch_first modules.  The attention output is quantized with the
+    module's dtype (an mx_tensor); the attention weights are returned float."""
+
+    @classmethod
+    def from_mha(cls, mha: nn.MultiheadAttention, mx_dtype, block: int = 128) -> "mx_multihead_attention":
+        m = cls.__new__(cls)
+        nn.Module.__init__(m)
+        dt = get_mx_dtype(mx_dtype)
+        m.embed_dim, m.num_heads, m.dropout = mha.embed_dim, mha.num_heads, mha.dropout
+        m.batch_first, m.kdim, m.vdim = mha.batch_first, mha.kdim, mha.vdim
+        m._qkv_same_embed_dim = mha._qkv_same_embed_dim
+        m.mx_dtype, m.block = dt, block
+        if mha.in_proj_weight is not None:
+            m.register_buffer("in_proj_weight", mx_tensor.quantize(mha.in_proj_weight.data, dt, block))
+        else:
+            m.register_buffer("in_proj_weight", None)
+        for attr in ("q_proj_weight", "k_proj_weight", "v_proj_weight"):
+            w = getattr(mha, attr, None) if mha.in_proj_weight is None else None
+            m.register_buffer(attr, mx_tensor.quantize(w.data, dt, block) if w is not None else None)
+        m.in_proj_bias = mha.in_proj_bias
+        m.out_proj = mx_linear.from_linear(mha.out_proj, dt, block)
+        m.bias_k, m.bias_v, m.add_zero_attn = mha.bias_k, mha.bias_v, mha.add_zero_attn
+        return m
+
+    def forward(self, query, key, value, key_padding_mask=None, need_weights=True, attn_mask=None,
+                average_attn_weights=True, **kwargs):
+        F = torch.nn.functional
+        q_f, k_f, v_f = _dq(query), _dq(key), _dq(value)
+        separate = self.in_proj_weight is None
+        out, attn = F.multi_head_attention_forward(
+            q_f, k_f, v_f, self.embed_dim, self.num_heads, _dq(self.in_proj_weight), self.in_proj_bias,
+            self.bias_k, self.bias_v, self.add_zero_attn, self.dropout if self.training else 0.0,
+            self.out_proj.weight, self.out_proj.bias, training=self.training, key_padding_mask=key_padding_mask,
+            need_weights=need_weights, attn_mask=attn_mask, average_attn_weights=average_attn_weights,
+            use_separate_proj_weight=separate, q_proj_weight=_dq(self.q_proj_weight) if separate else None,
+            k_proj_weight=_dq(self.k_proj_weight) if separate else None,
+            v_proj_weight=_dq(self.v_proj_weight) if separate else None)
+        return mx_tensor.quantize(out, self.mx_dtype, self.block), attn
+
+    def extra_repr(self):
+        return f"embed_dim={self.embed_dim}, num_heads={self.num_heads}, dtype={self.mx_dtype.name}"
+
+
+class mx_transformer_encoder_layer(nn.Module):
+    """nn.TransformerEncoderLayer with packed weights (mxtorch.py:9161-9278):
+    self-attention an mx_multihead_attention, the feed-forward pair
+    mx_linear (whose biases the forward replaces with quantized zeros, as in
+    the reference, mxtorch.py:7434-7436), the norms mx_layer_norm.  With
+    norm_first the reference's forward returns nothing (its branch ends
+    without a return); here it returns the layer output."""
+
+    @classmethod
+    def from_encoder_layer(cls, enc: nn.TransformerEncoderLayer, mx_dtype,
+                           block: int = 128) -> "mx_transformer_encoder_layer":
+        m = cls.__new__(cls)
+        nn.Module.__init__(m)
+        dt = get_mx_dtype(mx_dtype)
+        m.mx_dtype, m.block = dt, block
+        m.d_model, m.nhead = enc.self_attn.embed_dim, enc.self_attn.num_heads
+        m.dropout_p = enc.dropout.p if hasattr(enc.dropout, "p") else 0.0
+        m.norm_first = getattr(enc, "norm_first", False)
+        m.batch_first = enc.self_attn.batch_first
+        m.self_attn = mx_multihead_attention.from_mha(enc.self_attn, dt, block)
+        m.linear1 = mx_linear.from_linear(enc.linear1, dt, block)
+        m.linear2 = mx_linear.from_linear(enc.linear2, dt, block)
+        m.norm1 = mx_layer_norm.from_layer_norm(enc.norm1, dt, block)
+        m.norm2 = mx_layer_norm.from_layer_norm(enc.norm2, dt, block)
+        m.activation = enc.activation if callable(enc.activation) else torch.nn.functional.relu
+        return m
+
+    def _ff_block(self, x: Tensor) -> Tensor:
+        h = self.linear1(_dq(x))
+        out = self.linear2(self.activation(_dq(h)))
+        return torch.nn.functional.dropout(_dq(out), p=self.dropout_p, training=self.training)
+
+    def _sa_block(self, x: Tensor, attn_mask=None, key_padding_mask=None) -> Tensor:
+        x_f = _dq(x)
+        out, _ = self.self_attn(x_f, x_f, x_f, attn_mask=attn_mask, key_padding_mask=key_padding_mask)
+        return torch.nn.functional.dropout(_dq(out), p=self.dropout_p, training=self.training)
+
+    def forward(self, src: Tensor, src_mask=None, src_key_padding_mask=None) -> Tensor:
+        if self.norm_first:
+            src = _dq(src) + self._sa_block(_dq(self.norm1(src)), src_mask, src_key_padding_mask)
+            return src + self._ff_block(_dq(self.norm2(src)))
+        src = _dq(src) + self._sa_block(src, src_mask, src_key_padding_mask)
+        src = _dq(self.norm1(src))
+        src = src + self._ff_block(src)
+        return _dq(self.norm2(src))
+
+    def extra_repr(self):
+        return f"d={self.d_model}, heads={self.nhead}, dtype={self.mx_dtype.name}, norm_first={self.norm_first}"
+
+
 def _replace_module(parent: nn.Module, name: str, module: nn.Module, dt: mx_dtype, block: int) -> bool:
-    """The nn.Linear branch of _replace_module (mxtorch.py:7977-7989); other
-    module kinds are outside this build's path and are left unchanged."""
+    """The branches of _replace_module (mxtorch.py:7977-8030) for the module
+    kinds built around the packed path: Linear -> mx_linear,
+    MultiheadAttention -> mx_multihead_attention, TransformerEncoderLayer ->
+    mx_transformer_encoder_layer, LayerNorm -> mx_layer_norm, in the
+    reference's order.  Other module kinds (convolutions, embeddings, other
+    norms, the generic parameter quantization) are outside this build and
+    are left unchanged."""
     if isinstance(module, nn.Linear):
         setattr(parent, name, mx_linear.from_linear(module, dt, block))
+        return True
+    if isinstance(module, nn.MultiheadAttention):
+        setattr(parent, name, mx_multihead_attention.from_mha(module, dt, block))
+        return True
+    if isinstance(module, nn.TransformerEncoderLayer):
+        setattr(parent, name, mx_transformer_encoder_layer.from_encoder_layer(module, dt, block))
+        return True
+    if isinstance(module, nn.LayerNorm):
+        setattr(parent, name, mx_layer_norm.from_layer_norm(module, dt, block))
         return True
     return False
 

@@ -216,6 +216,114 @@ def _child(ref_dir: str) -> None:
         index["cases"].append({"kind": "kv", "key": key, "dtype": dname, "seed": seed,
                                "B": 2, "H": 4, "D": 128, "T": 3})
 
+    # ---------------- quantized element-wise ops (mxtorch.py:5321-5497, 6177-6193) ----------------
+    for dname, seed in (("int8d", 150), ("int4d", 151), ("int2d", 152)):
+        g = gen(seed)
+        A = torch.randn(4, 256, generator=g)
+        B = torch.randn(4, 256, generator=g)
+        dt = mx.get_mx_dtype(dname)
+        qa_ = mx.mx_tensor.quantize(A, dt, 128)
+        qb_ = mx.mx_tensor.quantize(B, dt, 128)
+        qw_ = mx.mx_tensor.quantize(B * 37.0, dt, 128)  # block scales more than 2:1 apart
+        key = f"ew/{dname}"
+        put(key + "/A", A)
+        put(key + "/B", B)
+        ops = {"add": qa_ + qb_, "sub": qa_ - qb_, "mul": qa_ * qb_, "neg": -qa_,
+               "addw": qa_ + qw_, "subw": qa_ - qw_, "mulw": qa_ * qw_}
+        out_names = {}
+        for opname, res in ops.items():
+            put(f"{key}/{opname}/packed", res._mx_packed)
+            put(f"{key}/{opname}/scales", res._mx_scales)
+            put(f"{key}/{opname}/dequant", res.dequantize())
+            out_names[opname] = res._mx_dtype.name
+        index["cases"].append({"kind": "elementwise", "key": key, "dtype": dname, "seed": seed,
+                               "shape": [4, 256], "wide_factor": 37.0, "out_dtype": out_names})
+
+    # ---------------- to_mx on a small model, and save_quantized (mxtorch.py:9744-9898) ----------------
+    class _MLP(torch.nn.Module):
+        def __init__(self):
+            super().__init__()
+            self.fc1 = torch.nn.Linear(64, 128)
+            self.act = torch.nn.ReLU()
+            self.norm = torch.nn.LayerNorm(128)
+            self.fc2 = torch.nn.Linear(128, 32)
+
+        def forward(self, x):
+            return self.fc2(self.norm(self.act(self.fc1(x))))
+
+    g = gen(160)
+    model = _MLP()
+    with torch.no_grad():
+        for p in model.parameters():
+            p.copy_(torch.randn(p.shape, generator=g) * 0.1 + (1.0 if p.ndim == 1 and p.numel() == 128 else 0.0))
+    x = torch.randn(6, 64, generator=g)
+    for name, p in model.named_parameters():
+        put(f"tomx/param/{name}", p.data)
+    put("tomx/x", x)
+    mx.to_mx(model, "int4d")
+    y = model(x)
+    put("tomx/y", y.dequantize() if isinstance(y, mx.mx_tensor) else y)
+    for attr in ("fc1", "fc2"):
+        lin = getattr(model, attr)
+        put(f"tomx/{attr}/w_packed", lin._mx_weight._mx_packed)
+        put(f"tomx/{attr}/w_scales", lin._mx_weight._mx_scales)
+    norm_w = model.norm.weight.data
+    norm_b = model.norm.bias.data
+    put("tomx/norm/w_packed", norm_w._mx_packed)
+    put("tomx/norm/w_scales", norm_w._mx_scales)
+    put("tomx/norm/b_packed", norm_b._mx_packed)
+    put("tomx/norm/b_scales", norm_b._mx_scales)
+    ckpt_path = os.path.join(HERE, "ref_checkpoint.pt")
+    mx.save_quantized(model, ckpt_path)
+    index["cases"].append({"kind": "to_mx", "key": "tomx", "dtype": "int4d", "seed": 160,
+                           "modules": {n: type(mm).__name__ for n, mm in model.named_children()},
+                           "checkpoint": os.path.basename(ckpt_path)})
+
+    # ---------------- mx_multihead_attention (mxtorch.py:7800-7877) ----------------
+    g = gen(170)
+    mha = torch.nn.MultiheadAttention(128, 4, batch_first=True)
+    with torch.no_grad():
+        for p in mha.parameters():
+            p.copy_(torch.randn(p.shape, generator=g) * 0.05)
+    q = torch.randn(2, 8, 128, generator=g)
+    for name, p in mha.named_parameters():
+        put(f"mha/param/{name}", p.data)
+    m = mx.mx_multihead_attention.from_mha(mha, mx.get_mx_dtype("int8d"), 128)
+    out, attn = m(q, q, q)
+    put("mha/q", q)
+    put("mha/in_proj/packed", m.in_proj_weight._mx_packed)
+    put("mha/in_proj/scales", m.in_proj_weight._mx_scales)
+    put("mha/out_proj/packed", m.out_proj._mx_weight._mx_packed)
+    put("mha/out_proj/scales", m.out_proj._mx_weight._mx_scales)
+    put("mha/out/packed", out._mx_packed)
+    put("mha/out/scales", out._mx_scales)
+    put("mha/out/dequant", out.dequantize())
+    put("mha/attn", attn)
+    index["cases"].append({"kind": "mha", "key": "mha", "dtype": "int8d", "seed": 170, "embed": 128,
+                           "heads": 4, "shape": [2, 8, 128], "out_dtype": out._mx_dtype.name})
+
+    # ---------------- mx_transformer_encoder_layer (mxtorch.py:9161-9260) ----------------
+    g = gen(180)
+    enc = torch.nn.TransformerEncoderLayer(d_model=128, nhead=4, dim_feedforward=256, dropout=0.0,
+                                           batch_first=True)
+    with torch.no_grad():
+        for name, p in enc.named_parameters():
+            base = 1.0 if ("norm" in name and name.endswith("weight")) else 0.0
+            p.copy_(torch.randn(p.shape, generator=g) * 0.05 + base)
+    enc.eval()
+    src = torch.randn(2, 8, 128, generator=g)
+    for name, p in enc.named_parameters():
+        put(f"enc/param/{name}", p.data)
+    m = mx.mx_transformer_encoder_layer.from_encoder_layer(enc, mx.get_mx_dtype("int8d"), 128)
+    m.eval()
+    y = m(src)
+    put("enc/src", src)
+    put("enc/y", y.dequantize() if isinstance(y, mx.mx_tensor) else y)
+    put("enc/linear1/w_packed", m.linear1._mx_weight._mx_packed)
+    put("enc/linear2/w_packed", m.linear2._mx_weight._mx_packed)
+    index["cases"].append({"kind": "encoder_layer", "key": "enc", "dtype": "int8d", "seed": 180, "d_model": 128,
+                           "nhead": 4, "ff": 256, "shape": [2, 8, 128]})
+
     # ---------------- pack KATs (mxtorch_test.py:86-112) ----------------
     vals = torch.tensor([3, -2, 7, -8, 0, 1, -1, 4], dtype=torch.int8)
     put("kat/pack4", mx.bit_packer.pack(vals, 4))
