@@ -305,6 +305,21 @@ int mxk_dynamic_quantize(const void* x, int x_type, int64_t rows, int64_t cols, 
                          void* packed, int64_t packed_nbytes, float* scales, void* workspace,
                          size_t workspace_nbytes, void* stream);
 
+/* vector_quantize(x, dtype, axis) (mxtorch.py:2946-2987) on x [rows][cols]:
+ * one scale per row (axis = 1) or per column (axis = 0),
+ *   s = RN(max(absmax, 1e-12) / max_int),  max_int = 2^(bits-1)-1,
+ *   codes = rne(clamp(RN(x / s), -max_int, max_int))  as int32 [rows][cols]
+ * (the reference rounds before clamping; with an integer max_int the two
+ * orders agree), scales float32 [rows] or [cols].  Widths 2..16.  No
+ * workspace: the absmax accumulates in `scales`. */
+int mxk_vector_quantize(const void* x, int x_type, int64_t rows, int64_t cols, int axis, int bits, int32_t* codes,
+                        float* scales, void* stream);
+
+/* vector_dequantize(codes, scales, axis) (mxtorch.py:2989-2994):
+ * out[r][c] = RN(codes[r][c] * s), s = scales[r] (axis = 1) or scales[c]. */
+int mxk_vector_dequantize(const int32_t* codes, const float* scales, int64_t rows, int64_t cols, int axis, float* out,
+                          void* stream);
+
 #ifdef __cplusplus
 }
 #endif

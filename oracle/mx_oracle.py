@@ -868,3 +868,28 @@ def encoder_layer_forward(src: Tensor, params: dict, name: str, block: int = 128
     x = x + ff
     n2w, n2b = layer_norm_from(params["norm2.weight"], params["norm2.bias"], name, block)
     return _dq_entry(layer_norm_forward(x, n2w, n2b, (E,), eps, name, block), name, block)
+
+
+# ---------------------------------------------------------------------------
+# vector-wise quantization  (mxtorch.py:2946-2994)
+# ---------------------------------------------------------------------------
+def vector_quantize(x: Tensor, name: str = "int8d", axis: int = 1) -> Tuple[Tensor, Tensor]:
+    """vector_quantize (mxtorch.py:2946-2987): s = max(absmax, 1e-12) / max_int
+    per row (axis=1) or column (axis=0), codes = round(x / s) clamped, int32."""
+    _, bits, _, _ = parse_dtype(name)
+    max_int = float((1 << (bits - 1)) - 1)
+    x_f = x.float()
+    if axis == 1:
+        scales = x_f.abs().amax(dim=1).clamp(min=1e-12) / max_int
+        codes = (x_f / scales.unsqueeze(1)).round().clamp(-max_int, max_int).to(torch.int32)
+    elif axis == 0:
+        scales = x_f.abs().amax(dim=0).clamp(min=1e-12) / max_int
+        codes = (x_f / scales.unsqueeze(0)).round().clamp(-max_int, max_int).to(torch.int32)
+    else:
+        raise ValueError(axis)
+    return codes, scales
+
+
+def vector_dequantize(codes: Tensor, scales: Tensor, axis: int = 1) -> Tensor:
+    """vector_dequantize (mxtorch.py:2989-2994)."""
+    return codes.float() * (scales.unsqueeze(1) if axis == 1 else scales.unsqueeze(0))

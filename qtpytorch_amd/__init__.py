@@ -16,7 +16,7 @@ from .io import load_quantized, save_quantized
 from .kv import kv_cache_quantizer
 from .nn import (install_module_to, mx_dynamic_linear, mx_layer_norm, mx_linear, mx_multihead_attention,
                  mx_transformer_encoder_layer, to_mx, uninstall_module_to)
-from .ops import HADAMARD_DEQUANT_MODE, _dequant, quantize
+from .ops import HADAMARD_DEQUANT_MODE, _dequant, quantize, vector_dequantize, vector_quantize
 from .tensor import (_dispatch_qgemm, _mx_linear_forward, _mx_mm, _MXLinearAutograd, _QGemmSTE,
                      dynamic_quantize, fused_int8_linear, mx_fused_ops, mx_matmul, mx_quantize, mx_tensor)
 
@@ -29,4 +29,5 @@ __all__ = ["mx_dtype", "get_mx_dtype", "matmul_output_dtype", "mx_tensor", "quan
            "_dispatch_qgemm", "_mx_mm", "_QGemmSTE", "mx_matmul", "mx_quantize", "mx_linear", "to_mx",
            "kv_cache_quantizer", "install_module_to", "uninstall_module_to", "save_quantized", "load_quantized",
            "dynamic_quantize", "fused_int8_linear", "mx_fused_ops", "mx_dynamic_linear", "_MXLinearAutograd",
-           "_mx_linear_forward", "mx_layer_norm", "mx_multihead_attention", "mx_transformer_encoder_layer"]
+           "_mx_linear_forward", "mx_layer_norm", "mx_multihead_attention", "mx_transformer_encoder_layer",
+           "vector_quantize", "vector_dequantize"]

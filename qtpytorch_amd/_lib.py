@@ -65,6 +65,8 @@ SIGNATURES = {
                               c_i64, c_i64, c_i64, c_vp, c_vp, c_vp, c_sz, c_vp]),
     "mxk_dynamic_quantize_workspace": (c_sz, [c_i64, c_i64, c_int, c_int]),
     "mxk_dynamic_quantize": (c_int, [c_vp, c_int, c_i64, c_i64, c_int, c_int, c_vp, c_i64, c_vp, c_vp, c_sz, c_vp]),
+    "mxk_vector_quantize": (c_int, [c_vp, c_int, c_i64, c_i64, c_int, c_int, c_vp, c_vp, c_vp]),
+    "mxk_vector_dequantize": (c_int, [c_vp, c_vp, c_i64, c_i64, c_int, c_vp, c_vp]),
 }
 
 

@@ -78,6 +78,75 @@ __global__ __launch_bounds__(256) void k_dyn_encode(const T* __restrict__ x, int
   }
 }
 
+// amax[r] = max over row r of |x[r][:]|, as float bits: one workgroup per
+// row (grid-stride over the rows), a wave maximum, then across the 4 waves.
+template <typename T>
+__global__ __launch_bounds__(256) void k_absmax_rows(const T* __restrict__ x, int64_t R, int64_t C,
+                                                     uint32_t* __restrict__ amax) {
+  __shared__ float sm[4];
+  for (int64_t r = blockIdx.x; r < R; r += gridDim.x) {
+    float m = 0.0f;
+    for (int64_t c = threadIdx.x; c < C; c += 256) m = fmaxf(m, __builtin_fabsf(ElemT<T>::cvt(x[r * C + c])));
+    m = group_max<64>(m);
+    if ((threadIdx.x & 63) == 0) sm[threadIdx.x >> 6] = m;
+    __syncthreads();
+    if (threadIdx.x == 0) amax[r] = __float_as_uint(fmaxf(fmaxf(sm[0], sm[1]), fmaxf(sm[2], sm[3])));
+    __syncthreads();
+  }
+}
+
+// int32 codes of vector_quantize: rne(clamp(RN(x / s), +-max_int)) with s the
+// element's row scale (PER_ROW) or column scale.
+template <typename T, bool PER_ROW>
+__global__ __launch_bounds__(256) void k_vec_encode(const T* __restrict__ x, int64_t n, int64_t C,
+                                                    const float* __restrict__ scales, float q,
+                                                    int32_t* __restrict__ codes) {
+  for (int64_t j = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; j < n; j += (int64_t)gridDim.x * blockDim.x) {
+    const float s = scales[PER_ROW ? j / C : j % C];
+    codes[j] = (int32_t)rne(fminf(fmaxf(ElemT<T>::cvt(x[j]) / s, -q), q));
+  }
+}
+
+// vector_dequantize: out = RN(code * s), s per row or per column.
+template <bool PER_ROW>
+__global__ __launch_bounds__(256) void k_vec_decode(const int32_t* __restrict__ codes, int64_t n, int64_t C,
+                                                    const float* __restrict__ scales, float* __restrict__ out) {
+  for (int64_t j = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; j < n; j += (int64_t)gridDim.x * blockDim.x)
+    out[j] = (float)codes[j] * scales[PER_ROW ? j / C : j % C];
+}
+
+template <typename T>
+static int vec_run(const T* x, int64_t rows, int64_t cols, int axis, int bits, int32_t* codes, float* scales,
+                   hipStream_t st) {
+  const int64_t n = rows * cols;
+  const float q = (float)((1u << (bits - 1)) - 1u);
+  const int cap = num_cus() * 8;
+  // the absmax bits accumulate in the scales buffer, which k_dyn_scales then
+  // turns into the scales in place
+  uint32_t* amax = reinterpret_cast<uint32_t*>(scales);
+  const int64_t cnt = axis == 1 ? rows : cols;
+  if (axis == 1) {
+    hipLaunchKernelGGL((k_absmax_rows<T>), dim3((unsigned)std::min<int64_t>(rows, (int64_t)cap * 2)), dim3(256), 0, st,
+                       x, rows, cols, amax);
+  } else {
+    hipLaunchKernelGGL(k_fill_u32, dim3((unsigned)std::min<int64_t>(ceil_div(cnt, 256), cap)), dim3(256), 0, st, amax,
+                       cnt, 0u);
+    const int64_t col_blocks = ceil_div(cols, 256);
+    const int64_t chunks = std::max<int64_t>(1, std::min<int64_t>(rows, ceil_div((int64_t)num_cus() * 4, col_blocks)));
+    const int64_t rows_per = ceil_div(rows, chunks);
+    hipLaunchKernelGGL((k_absmax_cols<T>), dim3((unsigned)col_blocks, (unsigned)ceil_div(rows, rows_per)), dim3(256),
+                       0, st, x, rows, cols, rows_per, amax);
+  }
+  hipLaunchKernelGGL(k_dyn_scales, dim3((unsigned)std::min<int64_t>(ceil_div(cnt, 256), cap)), dim3(256), 0, st, amax,
+                     cnt, q, scales);
+  const dim3 g((unsigned)std::min<int64_t>(ceil_div(n, 256), (int64_t)cap * 4));
+  if (axis == 1)
+    hipLaunchKernelGGL((k_vec_encode<T, true>), g, dim3(256), 0, st, x, n, cols, scales, q, codes);
+  else
+    hipLaunchKernelGGL((k_vec_encode<T, false>), g, dim3(256), 0, st, x, n, cols, scales, q, codes);
+  return check_launch("vector_quantize");
+}
+
 template <typename T>
 static int dyn_run(const T* x, int64_t rows, int64_t cols, int granularity, int bits, uint8_t* packed,
                    int64_t pbytes, float* scales, uint32_t* amax, hipStream_t st) {
@@ -160,6 +229,35 @@ int mxk_dynamic_quantize(const void* x, int x_type, int64_t rows, int64_t cols, 
       return dyn_run(reinterpret_cast<const hip_bfloat16*>(x), rows, cols, granularity, bits, pk, packed_nbytes, scales,
                      amax, st);
   }
+}
+
+int mxk_vector_quantize(const void* x, int x_type, int64_t rows, int64_t cols, int axis, int bits, int32_t* codes,
+                        float* scales, void* stream) {
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  if (rows <= 0 || cols <= 0) return fail(MXK_EINVAL, "vector_quantize: rows and cols must be positive");
+  if (!x || !codes || !scales) return fail(MXK_EINVAL, "vector_quantize: null buffer");
+  if (axis != 0 && axis != 1) return fail(MXK_EINVAL, "vector_quantize: axis must be 0 or 1");
+  if (bits < 2 || bits > 16) return fail(MXK_EUNSUPPORTED, "vector_quantize: widths 2..16 are implemented");
+  switch (x_type) {
+    case MXK_IN_F32: return vec_run(reinterpret_cast<const float*>(x), rows, cols, axis, bits, codes, scales, st);
+    case MXK_IN_F16: return vec_run(reinterpret_cast<const __half*>(x), rows, cols, axis, bits, codes, scales, st);
+    case MXK_IN_BF16:
+      return vec_run(reinterpret_cast<const hip_bfloat16*>(x), rows, cols, axis, bits, codes, scales, st);
+    default: return fail(MXK_EINVAL, "vector_quantize: x_type must be f32, f16 or bf16");
+  }
+}
+
+int mxk_vector_dequantize(const int32_t* codes, const float* scales, int64_t rows, int64_t cols, int axis, float* out,
+                          void* stream) {
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  if (rows <= 0 || cols <= 0) return fail(MXK_EINVAL, "vector_dequantize: rows and cols must be positive");
+  if (!codes || !scales || !out) return fail(MXK_EINVAL, "vector_dequantize: null buffer");
+  if (axis != 0 && axis != 1) return fail(MXK_EINVAL, "vector_dequantize: axis must be 0 or 1");
+  const int64_t n = rows * cols;
+  const dim3 g((unsigned)std::min<int64_t>(ceil_div(n, 256), (int64_t)num_cus() * 32));
+  if (axis == 1) hipLaunchKernelGGL(k_vec_decode<true>, g, dim3(256), 0, st, codes, n, cols, scales, out);
+  else hipLaunchKernelGGL(k_vec_decode<false>, g, dim3(256), 0, st, codes, n, cols, scales, out);
+  return check_launch("vector_dequantize");
 }
 
 }  // extern "C"

@@ -488,7 +488,11 @@ int mxk_qelementwise(int op, const void* a_packed, int64_t a_nbytes, const float
   const int64_t count = nb * block;
   const int64_t pbytes = mxk_packed_nbytes(out_bits, count);
   if (c_nbytes < pbytes) return fail(MXK_EINVAL, "qelementwise: output too small");
-  if ((block == 64 || block == 128 || block == 256) && (bits == 2 || bits == 4 || bits == 8) &&
+  // the fast kernels load every lane's codes whole (8 or 16 bytes), so both
+  // operands must hold the codes of all nb*block elements; buffers that stop
+  // at n codes (GEMM outputs, mxtorch.py:5570) take the byte-checked kernels
+  const bool whole = a_nbytes >= count * bits / 8 && b_nbytes >= count * bits / 8;
+  if (whole && (block == 64 || block == 128 || block == 256) && (bits == 2 || bits == 4 || bits == 8) &&
       (out_bits == 2 || out_bits == 4 || out_bits == 8 || out_bits == 16) && a_nbytes < ((int64_t)1 << 32) &&
       b_nbytes < ((int64_t)1 << 32) && count * bits / 8 < ((int64_t)1 << 32) &&
       (reinterpret_cast<uintptr_t>(c_packed) & 15u) == 0) {

@@ -324,6 +324,22 @@ def _child(ref_dir: str) -> None:
     index["cases"].append({"kind": "encoder_layer", "key": "enc", "dtype": "int8d", "seed": 180, "d_model": 128,
                            "nhead": 4, "ff": 256, "shape": [2, 8, 128]})
 
+    # ---------------- vector_quantize (mxtorch.py:2946-2994) ----------------
+    g = gen(190)
+    xv = torch.randn(16, 300, generator=g)
+    xv[torch.rand(16, 300, generator=g) < 0.01] *= 40
+    xv[3] = 0.0                      # an all-zero row
+    xv[5, ::7] = torch.arange(43, dtype=torch.float32) * 0.5 - 10.5   # exact halves of a step after scaling
+    put("vq/x", xv)
+    for dname, axis in (("int8d", 1), ("int8d", 0), ("int4d", 1), ("int2d", 0), ("int16d", 1)):
+        codes, scales = mx.vector_quantize(xv, dname, axis=axis)
+        key = f"vq/{dname}/axis{axis}"
+        put(key + "/codes", codes)
+        put(key + "/scales", scales)
+        put(key + "/dequant", mx.vector_dequantize(codes, scales, axis=axis))
+        index["cases"].append({"kind": "vector_quantize", "key": key, "dtype": dname, "axis": axis, "seed": 190,
+                               "shape": [16, 300]})
+
     # ---------------- pack KATs (mxtorch_test.py:86-112) ----------------
     vals = torch.tensor([3, -2, 7, -8, 0, 1, -1, 4], dtype=torch.int8)
     put("kat/pack4", mx.bit_packer.pack(vals, 4))

@@ -139,3 +139,26 @@ def test_large_elementwise_roundtrip(qa):
     rp, rs, _ = orc.dispatch_qelementwise("add", pa, sa, "int8d", pb, sb, "int8d", idx.numel(), block)
     assert _bits_eq(C._mx_scales.cpu()[pick], rs)
     assert _bits_eq(C._mx_packed.cpu()[idx], rp)
+
+
+@pytest.mark.parametrize("mkn", [(5, 128, 3), (7, 256, 9), (16, 128, 8)])
+@pytest.mark.parametrize("name", ["int4d", "int8d"])
+def test_elementwise_on_gemm_outputs(qa, mkn, name):
+    """C + C, C - C and C * C where C = qa @ qb holds exactly M*N codes
+    (mxtorch.py:5570), M*N not always a multiple of the block or of a lane's
+    load: bitwise equal to the oracle applied to the oracle's C."""
+    M, K, N = mkn
+    g = torch.Generator()
+    g.manual_seed(M * 1000 + N)
+    A, B = torch.randn(M, K, generator=g), torch.randn(K, N, generator=g)
+    dt = qa.get_mx_dtype(name)
+    qc = qa.mx_tensor.quantize(A.to(dev()), dt, 128) @ qa.mx_tensor.quantize(B.to(dev()), dt, 128)
+    pa, sa, na = orc.quantize(A, name, 128)
+    pb, sb, nb = orc.quantize(B, name, 128)
+    pc, sc, out_name = orc.dispatch_qgemm(pa, sa, name, (M, K), na, pb, sb, name, (K, N), nb, 128)
+    assert _bits_eq(qc._mx_packed, pc) and _bits_eq(qc._mx_scales, sc)
+    for op, r in (("add", qc + qc), ("sub", qc - qc), ("mul", qc * qc)):
+        p_ref, s_ref, o_ref = orc.dispatch_qelementwise(op, pc, sc, out_name, pc, sc, out_name, M * N, 128)
+        assert r._mx_dtype.name == o_ref, op
+        assert _bits_eq(r._mx_packed, p_ref), op
+        assert _bits_eq(r._mx_scales, s_ref), op

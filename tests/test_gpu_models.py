@@ -205,3 +205,31 @@ def test_encoder_layer_matches_reference(qa):
     err = (y - y_ref).abs().max().item()
     print(f"encoder layer max err {err:.3g}, bitwise equal fraction {(y == y_ref).float().mean().item():.4f}")
     assert err <= 1e-4 * y_ref.abs().max().item()
+
+
+VQ = G.cases("vector_quantize")
+
+
+@pytest.mark.parametrize("case", VQ, ids=[c["key"] for c in VQ])
+def test_vector_quantize_matches_reference(qa, case):
+    """vector_quantize / vector_dequantize (mxtorch.py:2946-2994): codes,
+    scales and reconstruction bitwise, including an all-zero row and values
+    on exact half steps."""
+    codes, scales = qa.vector_quantize(G.get("vq/x").to(dev()), case["dtype"], axis=case["axis"])
+    assert codes.dtype == torch.int32 and tuple(codes.shape) == (16, 300)
+    assert torch.equal(codes.cpu(), G.get(case["key"] + "/codes"))
+    assert _bits_eq(scales, G.get(case["key"] + "/scales"))
+    assert _bits_eq(qa.vector_dequantize(codes, scales, axis=case["axis"]), G.get(case["key"] + "/dequant"))
+
+
+@pytest.mark.parametrize("axis", [0, 1])
+@pytest.mark.parametrize("xdt", [torch.float32, torch.float16, torch.bfloat16])
+def test_vector_quantize_vs_oracle(qa, axis, xdt):
+    g = torch.Generator()
+    g.manual_seed(7 + axis)
+    x = (torch.randn(1000, 777, generator=g) * 3).to(xdt)
+    for name in ("int8d", "int4d", "int16d"):
+        codes, scales = qa.vector_quantize(x.to(dev()), name, axis=axis)
+        c_ref, s_ref = orc.vector_quantize(x, name, axis)
+        assert torch.equal(codes.cpu(), c_ref), name
+        assert _bits_eq(scales, s_ref), name

@@ -106,3 +106,26 @@ def test_encoder_layer_oracle_matches_reference():
     y = orc.encoder_layer_forward(G.get("enc/src"), params, "int8d", 128, nhead=case["nhead"])
     y_ref = G.get("enc/y")
     assert G.bits_equal(y, y_ref) or (y - y_ref).abs().max().item() <= 1e-5 * y_ref.abs().max().item()
+
+
+VQ = G.cases("vector_quantize")
+
+
+@pytest.mark.parametrize("case", VQ, ids=[c["key"] for c in VQ])
+def test_vector_quantize_oracle_matches_reference(case):
+    codes, scales = orc.vector_quantize(G.get("vq/x"), case["dtype"], case["axis"])
+    assert torch.equal(codes, G.get(case["key"] + "/codes"))
+    assert G.bits_equal(scales, G.get(case["key"] + "/scales"))
+    assert G.bits_equal(orc.vector_dequantize(codes, scales, case["axis"]), G.get(case["key"] + "/dequant"))
+
+
+def test_vector_quantize_per_row_is_the_v_rule():
+    """Per row, vector_quantize's int codes are the golden-pinned 'v'
+    quantizer's (quant_vector) with the row length as block, for widths whose
+    'v' codes pack into bytes."""
+    x = G.get("vq/x")
+    for name in ("int8d", "int4d", "int2d"):
+        codes, scales = orc.vector_quantize(x, name, 1)
+        p, s, n = orc.quantize(x, name.replace("d", "dv"), 300)
+        assert G.bits_equal(scales, s)
+        assert torch.equal(codes.reshape(-1), orc.unpack_auto(p, orc.parse_dtype(name)[1], n).to(torch.int32))
