@@ -203,18 +203,22 @@ def bench_quant_sweep(qa, reps):
     return out
 
 
-def bench_gemm(qa, M, K, N, reps):
+def bench_gemm(qa, M, K, N, reps, dtype="int8d"):
+    """Packed block-scaled GEMM A @ B (mxtorch.py:5497-5573) of two seeded
+    randn operands quantized with `dtype` block 128: fp32 C out, and the
+    packed int16d output the reference's matmul returns."""
     dev = torch.device("cuda:0")
     A = torch.randn(M, K, generator=gen(5, "cuda"), device=dev)
     B = torch.randn(K, N, generator=gen(6, "cuda"), device=dev)
-    d8 = qa.get_mx_dtype("int8d")
-    pa, sa, _ = qa.ops.quantize(A, d8, 128)
-    pb, sb, _ = qa.ops.quantize(B, d8, 128)
+    dt = qa.get_mx_dtype(dtype)
+    pa, sa, _ = qa.ops.quantize(A, dt, 128)
+    pb, sb, _ = qa.ops.quantize(B, dt, 128)
     del A, B
+    bits = dt.bits
     # the median of 5 replays: back-to-back 8192^3 GEMMs move the clock by +-10% from launch to launch
-    t_c = graph_time(lambda: qa.ops.qscale_gemm(pa, sa, pb, sb, M, K, N, 8, 128, 16, want_packed=False,
+    t_c = graph_time(lambda: qa.ops.qscale_gemm(pa, sa, pb, sb, M, K, N, bits, 128, 16, want_packed=False,
                                                   want_c=True), reps, 1, repeats=5)
-    t_p = graph_time(lambda: qa.ops.qscale_gemm(pa, sa, pb, sb, M, K, N, 8, 128, 16), reps, 1, repeats=5)
+    t_p = graph_time(lambda: qa.ops.qscale_gemm(pa, sa, pb, sb, M, K, N, bits, 128, 16), reps, 1, repeats=5)
     ops = 2.0 * M * K * N
     return {"shape": [M, K, N], "fp32_out_us": round(t_c * 1e6, 2), "fp32_out_TOPS": round(ops / t_c / 1e12, 2),
             "fp32_out_frac_int8_peak": round(ops / t_c / 1e12 / INT8_PEAK_TOPS, 4),
@@ -375,7 +379,7 @@ def main():
     ap.add_argument("--no-extras", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--only", default="",
-                    help="comma list of extras: quant,gemm,kv,kvstream,elementwise,small,dynamic")
+                    help="comma list of extras: quant,gemm,gemm4,kv,kvstream,elementwise,small,dynamic")
     ap.add_argument("--eager", action="store_true", help="no graph capture (for rocprofv3 --pmc runs)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a plain 512 MiB device copy (the reference kernel for HBM counter scaling)")
@@ -431,6 +435,8 @@ def main():
             extras["config1_int8d_gemm_512"] = bench_gemm(qa, 512, 512, 512, 50)
         if not only or "gemm" in only:
             extras["config3_int8d_gemm_8192"] = bench_gemm(qa, 8192, 8192, 8192, 3)
+        if not only or "gemm4" in only:
+            extras["int4d_gemm_8192"] = bench_gemm(qa, 8192, 8192, 8192, 3, "int4d")
         if not only or "quant" in only:
             extras["config4_quant_sweep_2e28"] = bench_quant_sweep(qa, 5)
         if not only or "kv" in only:

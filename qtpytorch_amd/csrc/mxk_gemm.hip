@@ -402,16 +402,83 @@ __device__ __forceinline__ void qg3_lgkm_wait(i32x4& v) {
   asm volatile("s_waitcnt lgkmcnt(%1)" : "+v"(v) : "n"(N));
 }
 
-template <bool WRITE_ACC, bool WRITE_C, bool ROWSCALE = false>
-__global__ __launch_bounds__(512, 1) void k_qgemm_i8_v3(const int8_t* __restrict__ A8, int64_t lda, int64_t Arows,
-                                                        const int8_t* __restrict__ B8, int64_t ldb, int64_t Brows,
-                                                        const float* __restrict__ sa_t,
-                                                        const float* __restrict__ sb_src, int64_t M, int64_t N,
-                                                        int KB, float* __restrict__ C, int32_t* __restrict__ acc_out,
-                                                        int grouped, const float* __restrict__ bias) {
+typedef int32_t i32x2 __attribute__((ext_vector_type(2)));
+
+// Transposed 8-byte LDS read (ds_read_b64_tr_b8).  Within each group of 16
+// lanes, lane i receives byte i % 8 of the 8-byte rows addressed by lanes
+// i / 8 + 2j, j = 0..7, as its bytes j.  When lanes 2j and 2j + 1 address
+// the two halves of a 16-column segment of K row kappa_j of an N-contiguous
+// tile, lane i receives B[kappa_0..7][column i]: eight K values of the i8
+// MFMA B operand of column i.  Same waiting rules as qg3_ds_read.
+template <uint32_t OFF>
+__device__ __forceinline__ i32x2 qg3_ds_read_tr(uint32_t base) {
+  static_assert(OFF < 65536, "ds_read offset field");
+  i32x2 v;
+  asm volatile("ds_read_b64_tr_b8 %0, %1 offset:%2" : "=v"(v) : "v"(base), "n"(OFF) : "memory");
+  return v;
+}
+template <int N>
+__device__ __forceinline__ void qg3_lgkm_wait(i32x2& v) {
+  asm volatile("s_waitcnt lgkmcnt(%1)" : "+v"(v) : "n"(N));
+}
+
+// 16-byte LDS store as inline asm, so that the compiler does not order it
+// after the buffer loads to LDS still filling other stages.  The data
+// registers are read when the store issues; the store's completion is
+// waited for (lgkmcnt 0) before the barrier that publishes the stage.
+template <uint32_t OFF>
+__device__ __forceinline__ void qg3_ds_write(uint32_t addr, u32x4 v) {
+  static_assert(OFF < 65536, "ds_write offset field");
+  asm volatile("ds_write_b128 %0, %1 offset:%2" : : "v"(addr), "v"(v), "n"(OFF) : "memory");
+}
+
+// Slot (16-byte unit) of chunk c in K row r of an N-contiguous B stage:
+// rows r and r + 2 differ in the low two bits of the XOR and rows r and r +
+// 16 in the third, so the 32 rows one transposed read touches (8 rows in
+// each of 4 lane groups, 16 rows apart) spread over every slot.
+__device__ __forceinline__ int qg3_bslot(int r, int c) { return c ^ (((r >> 1) & 3) | ((r >> 2) & 4)); }
+
+// Column (within 16) held at LDS column position l of a B fragment: the
+// int4 stages unpack the nibble pairs of every 8 columns as 0,2,4,6,1,3,5,7;
+// the same map orders K within the int4 A rows and the rows the B reads take.
+template <int MODE>
+__device__ __forceinline__ int qg3_lcol(int l) {
+  return MODE == 2 ? ((l & 8) | ((l & 3) << 1) | ((l >> 2) & 1)) : l;
+}
+
+// Nibbles of 8 int4 codes (w: code 2j in the low nibble of byte j) as 8
+// int8 bytes 16 * code: [even codes | odd codes]
+__device__ __forceinline__ u32x4 qg3_unpack16(uint32_t w0, uint32_t w1) {
+  return u32x4{(w0 << 4) & 0xF0F0F0F0u, w0 & 0xF0F0F0F0u, (w1 << 4) & 0xF0F0F0F0u, w1 & 0xF0F0F0F0u};
+}
+
+#define QG3_LDS_BYTES (QG3_NS * (32768 + 16384 + 2048))
+
+// Operand modes of the v3 tile loop:
+//   0  A8 [Arows][lda] and B8 [Brows][ldb] int8, both K-contiguous (B8 holds
+//      B's columns as rows); fragments by ds_read_b128.
+//   1  A8 as in mode 0; B8 is B as stored, [K][ldb = N] int8, N-contiguous:
+//      its stages are copied as they are and read with transposed LDS reads,
+//      so no pass transposes B.
+//   2  int4 codes as stored: A [Arows][lda = K/2 bytes] packed along K, B
+//      [K][ldb = N/2 bytes] packed along N.  Each thread loads its share of
+//      a stage into VGPRs one K block ahead and unpacks it into the int8 LDS
+//      layouts of mode 0 (A) and mode 1 (B).  Code c becomes the byte 16c
+//      (its nibble moved to the top of the byte: two instructions per four
+//      codes, no sign extension), so the MFMA sums P = sum (16a)(16b), 256
+//      times the code product.  sa_t then holds SA * 2^-8, and
+//      RN(float(P) * SA * 2^-8) = RN(P/256 * SA) when SA * 2^-8 is exact; with
+//      EXACT (some scale is too small for that) sa_t holds SA and P is
+//      scaled by 2^-8 first (exact: an integer below 2^24).
+template <int MODE, bool WRITE_ACC, bool WRITE_C, bool ROWSCALE, bool EXACT>
+__device__ __forceinline__ void qg3_run(int8_t* lds, const int8_t* __restrict__ A8, int64_t lda, int64_t Arows,
+                                        const int8_t* __restrict__ B8, int64_t ldb, int64_t Brows,
+                                        const float* __restrict__ sa_t, const float* __restrict__ sb_src, int64_t M,
+                                        int64_t N, int KB, float* __restrict__ C, int32_t* __restrict__ acc_out,
+                                        int grouped, const float* __restrict__ bias) {
+  static_assert(MODE == 0 || !ROWSCALE, "row scales are a mode-0 epilogue");
   // [A stages 0..2, 32 KiB each][B stages 0..2, 16 KiB each][scale stages 0..2, 2 KiB each]:
   // a stage's scales hold SA rows at floats 0..255 and SB columns at 256..383
-  __shared__ __attribute__((aligned(1024))) int8_t lds[QG3_NS * (32768 + 16384 + 2048)];
   constexpr uint32_t LA = 0, LB = QG3_NS * 32768, LS = QG3_NS * (32768 + 16384);
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -436,17 +503,30 @@ __global__ __launch_bounds__(512, 1) void k_qgemm_i8_v3(const int8_t* __restrict
 
   // Per-lane byte offsets of the stage loads; the K block goes into the
   // scalar offset.  A rows 32w + 8q + (L >> 3), B rows 16w + 8q + (L >> 3),
-  // chunk = slot ^ ((row >> 1) & 7) as in v2; scale float 64w + L.
+  // chunk = slot ^ ((row >> 1) & 7) as in v2 (mode 1: B K rows, chunk =
+  // qg3_bslot(row, slot)); scale float 64w + L.  Mode 2: 16 packed bytes
+  // (32 codes) per thread of A rows tid/4 and 128 + tid/4 and of B K row
+  // tid/4, at byte 16 (tid % 4) of the K block (A) or of the tile's columns (B).
   uint32_t oa[4], ob[2];
+  if constexpr (MODE == 2) {
+    const int r = tid >> 2, pc = tid & 3;
+    oa[0] = (uint32_t)(std::min<int64_t>(m0 + r, Arows - 1) * lda + pc * 16);
+    oa[1] = (uint32_t)(std::min<int64_t>(m0 + 128 + r, Arows - 1) * lda + pc * 16);
+    oa[2] = oa[3] = 0;
+    ob[0] = (uint32_t)(r * ldb + n0 / 2 + pc * 16);
+    ob[1] = 0;
+  } else {
 #pragma unroll
-  for (int q = 0; q < 4; ++q) {
-    const int r = 32 * wave + 8 * q + (lane >> 3);
-    oa[q] = (uint32_t)(std::min<int64_t>(m0 + r, Arows - 1) * lda + qg2_slot(r, lane & 7) * 16);
-  }
+    for (int q = 0; q < 4; ++q) {
+      const int r = 32 * wave + 8 * q + (lane >> 3);
+      oa[q] = (uint32_t)(std::min<int64_t>(m0 + r, Arows - 1) * lda + qg2_slot(r, lane & 7) * 16);
+    }
 #pragma unroll
-  for (int q = 0; q < 2; ++q) {
-    const int r = 16 * wave + 8 * q + (lane >> 3);
-    ob[q] = (uint32_t)(std::min<int64_t>(n0 + r, Brows - 1) * ldb + qg2_slot(r, lane & 7) * 16);
+    for (int q = 0; q < 2; ++q) {
+      const int r = 16 * wave + 8 * q + (lane >> 3);
+      ob[q] = MODE == 0 ? (uint32_t)(std::min<int64_t>(n0 + r, Brows - 1) * ldb + qg2_slot(r, lane & 7) * 16)
+                        : (uint32_t)(r * ldb + n0 + qg3_bslot(r, lane & 7) * 16);
+    }
   }
   const int f = 64 * wave + lane;
   // waves 0-3: SA rows, 4-5: SB columns, 6-7: a harmless load of SA row 0
@@ -454,11 +534,14 @@ __global__ __launch_bounds__(512, 1) void k_qgemm_i8_v3(const int8_t* __restrict
   const float* gsb = is_b ? sb_src : sa_t;
   const int64_t gstride = is_b ? N : M;
   // SB is stored lane-major: float 256 + 64*wn + 4*lr + t holds column
-  // n0 + 64*wn + 16t + lr, so a lane's four SB values are one 16-byte read
+  // n0 + 64*wn + 16t + qg3_lcol(lr), so a lane's four SB values are one 16-byte read
   const int fb = f - 256;  // 0..127 on waves 4-5
-  const uint32_t os = (uint32_t)(4 * (f < 256 ? std::min<int64_t>(m0 + f, M - 1)
-                                              : (f < 384 ? std::min<int64_t>(n0 + (fb & ~63) + (fb & 3) * 16 + ((fb & 63) >> 2), N - 1)
-                                                         : 0)));
+  const uint32_t os =
+      (uint32_t)(4 * (f < 256 ? std::min<int64_t>(m0 + f, M - 1)
+                              : (f < 384 ? std::min<int64_t>(n0 + (fb & ~63) + (fb & 3) * 16 +
+                                                                 qg3_lcol<MODE>((fb & 63) >> 2),
+                                                             N - 1)
+                                         : 0)));
   const __amdgpu_buffer_rsrc_t rA = make_rsrc(A8, (uint32_t)(Arows * lda));
   const __amdgpu_buffer_rsrc_t rB = make_rsrc(B8, (uint32_t)(Brows * ldb));
   const __amdgpu_buffer_rsrc_t rS = make_rsrc(gsb, (uint32_t)((int64_t)KB * gstride * 4));
@@ -471,10 +554,12 @@ __global__ __launch_bounds__(512, 1) void k_qgemm_i8_v3(const int8_t* __restrict
         __builtin_amdgcn_raw_ptr_buffer_load_lds(rA, (lds_ptr)(&lds[LA + buf * 32768 + (32 * wave + 8 * q) * 128]), 16,
                                                  (int)oa[q], kb * 128, 0, 0);
     } else if (part == 2) {
+      // mode 1: the K block is 128 rows of ldb bytes (K * N < 2^31, checked by the host)
+      const int kboff = MODE == 0 ? kb * 128 : kb * 128 * (int)ldb;
 #pragma unroll
       for (int q = 0; q < 2; ++q)
         __builtin_amdgcn_raw_ptr_buffer_load_lds(rB, (lds_ptr)(&lds[LB + buf * 16384 + (16 * wave + 8 * q) * 128]), 16,
-                                                 (int)ob[q], kb * 128, 0, 0);
+                                                 (int)ob[q], kboff, 0, 0);
     } else {
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rS, (lds_ptr)(&lds[LS + buf * 2048 + 256 * wave]), 4, (int)os,
                                                (int)((int64_t)kb * gstride * 4), 0, 0);
@@ -492,6 +577,44 @@ __global__ __launch_bounds__(512, 1) void k_qgemm_i8_v3(const int8_t* __restrict
   const uint32_t bB1 = l0 + LB + (wn * 64 + lr) * 128 + (((4 + lg) ^ sw) * 16);
   const uint32_t bSB = l0 + LS + 4u * (256 + wn * 64 + 4 * lr);
   const uint32_t bSA = l0 + LS + 4u * (wm * 64 + lg * 4);
+  // Modes 1 and 2, transposed B reads: lane (lr, lg) addresses K row 16 lg +
+  // map(lr / 2) (+ 64 per K half, + 8 for the second read: immediates) at the
+  // 8-byte half lr % 2 of column segment 4 wn + t, so that its bytes hold the
+  // K values its A fragment holds, in the same order.  The row's slot XOR
+  // depends only on lr / 2 and lg, not on the half or the read.
+  uint32_t bT[4] = {0u, 0u, 0u, 0u};
+  if constexpr (MODE != 0) {
+    const int kl = 16 * lg + qg3_lcol<MODE>(lr >> 1);
+#pragma unroll
+    for (int t = 0; t < 4; ++t) bT[t] = l0 + LB + kl * 128 + qg3_bslot(kl, 4 * wn + t) * 16 + 8 * (lr & 1);
+  }
+  // Mode 2: the packed codes of one stage in VGPRs, loaded one K block before
+  // they are unpacked; the LDS addresses of the unpacked chunks (A rows r and
+  // r + 128 share a swizzle, 16 KiB apart)
+  u32x4 ra0 = {0u, 0u, 0u, 0u}, ra1 = {0u, 0u, 0u, 0u}, rb = {0u, 0u, 0u, 0u};
+  uint32_t wA0 = 0, wA1 = 0, wB0 = 0, wB1 = 0;
+  if constexpr (MODE == 2) {
+    const int r = tid >> 2, pc = tid & 3;
+    wA0 = l0 + LA + r * 128 + qg2_slot(r, 2 * pc) * 16;
+    wA1 = l0 + LA + r * 128 + qg2_slot(r, 2 * pc + 1) * 16;
+    wB0 = l0 + LB + r * 128 + qg3_bslot(r, 2 * pc) * 16;
+    wB1 = l0 + LB + r * 128 + qg3_bslot(r, 2 * pc + 1) * 16;
+  }
+  auto load4 = [&](int kb) {
+    ra0 = buf_load_b128(rA, oa[0], (uint32_t)kb * 64u);
+    ra1 = buf_load_b128(rA, oa[1], (uint32_t)kb * 64u);
+    rb = buf_load_b128(rB, ob[0], (uint32_t)kb * 128u * (uint32_t)ldb);
+  };
+  auto write4 = [&](int buf) {
+    const uint32_t da = (uint32_t)buf * 32768u, db = (uint32_t)buf * 16384u;
+    qg3_ds_write<0>(wA0 + da, qg3_unpack16(ra0[0], ra0[1]));
+    qg3_ds_write<0>(wA1 + da, qg3_unpack16(ra0[2], ra0[3]));
+    qg3_ds_write<16384>(wA0 + da, qg3_unpack16(ra1[0], ra1[1]));
+    qg3_ds_write<16384>(wA1 + da, qg3_unpack16(ra1[2], ra1[3]));
+    qg3_ds_write<0>(wB0 + db, qg3_unpack16(rb[0], rb[1]));
+    qg3_ds_write<0>(wB1 + db, qg3_unpack16(rb[2], rb[3]));
+  };
+  const int lcol = qg3_lcol<MODE>(lr);
 
   float c[4][4][4];
 #pragma unroll
@@ -511,13 +634,16 @@ __global__ __launch_bounds__(512, 1) void k_qgemm_i8_v3(const int8_t* __restrict
     if constexpr (ROWSCALE) {
       c[a][t][i] = __builtin_fmaf((float)p[t][i], __int_as_float(sbvv[t]), c[a][t][i]);
     } else {
-      const float v = ((float)p[t][i] * __int_as_float(sav[i])) * __int_as_float(sbvv[t]);
+      float pf = (float)p[t][i];
+      if constexpr (MODE == 2 && EXACT) pf = pf * 0.00390625f;
+      const float v = (pf * __int_as_float(sav[i])) * __int_as_float(sbvv[t]);
       c[a][t][i] = c[a][t][i] + v;
     }
     if (WRITE_ACC) {
       const int64_t row = m0 + wm * 64 + a * 16 + lg * 4 + i;
-      const int64_t col = n0 + wn * 64 + t * 16 + lr;
-      if (kbw >= 0 && row < M && col < N) acc_out[((int64_t)kbw * M + row) * N + col] = p[t][i];
+      const int64_t col = n0 + wn * 64 + t * 16 + lcol;
+      if (kbw >= 0 && row < M && col < N)
+        acc_out[((int64_t)kbw * M + row) * N + col] = MODE == 2 ? (p[t][i] >> 8) : p[t][i];
     }
   };
 
@@ -526,30 +652,57 @@ __global__ __launch_bounds__(512, 1) void k_qgemm_i8_v3(const int8_t* __restrict
     const uint32_t b0 = bA0 + (uint32_t)cur * 32768u, b1 = bA1 + (uint32_t)cur * 32768u;
     const uint32_t bb0 = bB0 + (uint32_t)cur * 16384u, bb1 = bB1 + (uint32_t)cur * 16384u;
     const uint32_t bsa = bSA + (uint32_t)cur * 2048u, bsb = bSB + (uint32_t)cur * 2048u;
-    // stage kb has landed once at most the next stage's 7 loads are pending
-    if (kb + 1 < KB) wait_vmcnt<7>();
-    else wait_vmcnt<0>();
+    uint32_t bt[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) bt[t] = bT[t] + (uint32_t)cur * 16384u;
+    // stage kb has landed once at most the next stage's loads are pending
+    // (modes 0/1: its 7 loads; mode 2: the 3 packed loads and the scale load
+    // of stage kb+1); mode 2 also waits for its own LDS stores of stage kb
+    if constexpr (MODE == 2) {
+      if (kb + 1 < KB) wait_vmcnt<4>();
+      else wait_vmcnt<0>();
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    } else {
+      if (kb + 1 < KB) wait_vmcnt<7>();
+      else wait_vmcnt<0>();
+    }
     qg3_barrier();  // stage kb visible; every wave is done with stage kb-1
     const bool ld = kb + 2 < KB;
     const int lbuf = cur == 0 ? 2 : cur - 1;
     // reads in need order, at most 15 in flight (the lgkmcnt limit): A
     // slice 0, B column fragments 0..3, SB, SA0, A slice 1, SA1
     i32x4 af[4][2], bf[2][4], sa[4], sbv;
+    // modes 1/2: B fragment (h, t) is two transposed reads (K rows 0-7 and 8-15 of its lane group)
+    i32x2 btr[4][4];
+    auto issue_b = [&](int t) {
+      btr[t][0] = qg3_ds_read_tr<0>(bt[t]);
+      btr[t][1] = qg3_ds_read_tr<1024>(bt[t]);
+      btr[t][2] = qg3_ds_read_tr<8192>(bt[t]);
+      btr[t][3] = qg3_ds_read_tr<8192 + 1024>(bt[t]);
+    };
     af[0][0] = qg3_ds_read<0>(b0);
     af[0][1] = qg3_ds_read<0>(b1);
-    bf[0][0] = qg3_ds_read<0 * 2048>(bb0);
-    bf[1][0] = qg3_ds_read<0 * 2048>(bb1);
-    bf[0][1] = qg3_ds_read<1 * 2048>(bb0);
-    bf[1][1] = qg3_ds_read<1 * 2048>(bb1);
-    bf[0][2] = qg3_ds_read<2 * 2048>(bb0);
-    bf[1][2] = qg3_ds_read<2 * 2048>(bb1);
-    bf[0][3] = qg3_ds_read<3 * 2048>(bb0);
-    bf[1][3] = qg3_ds_read<3 * 2048>(bb1);
-    sbv = qg3_ds_read<0>(bsb);
-    sa[0] = qg3_ds_read<0>(bsa);
-    af[1][0] = qg3_ds_read<2048>(b0);
-    af[1][1] = qg3_ds_read<2048>(b1);
-    sa[1] = qg3_ds_read<64>(bsa);
+    if constexpr (MODE == 0) {
+      bf[0][0] = qg3_ds_read<0 * 2048>(bb0);
+      bf[1][0] = qg3_ds_read<0 * 2048>(bb1);
+      bf[0][1] = qg3_ds_read<1 * 2048>(bb0);
+      bf[1][1] = qg3_ds_read<1 * 2048>(bb1);
+      bf[0][2] = qg3_ds_read<2 * 2048>(bb0);
+      bf[1][2] = qg3_ds_read<2 * 2048>(bb1);
+      bf[0][3] = qg3_ds_read<3 * 2048>(bb0);
+      bf[1][3] = qg3_ds_read<3 * 2048>(bb1);
+      sbv = qg3_ds_read<0>(bsb);
+      sa[0] = qg3_ds_read<0>(bsa);
+      af[1][0] = qg3_ds_read<2048>(b0);
+      af[1][1] = qg3_ds_read<2048>(b1);
+      sa[1] = qg3_ds_read<64>(bsa);
+    } else {
+      // 2 + 12 reads; column fragment 3, the scales and A slice 1 follow
+      // once the first pairs have been waited for
+      issue_b(0);
+      issue_b(1);
+      issue_b(2);
+    }
     __builtin_amdgcn_sched_barrier(0);
     auto slice_mfma = [&](int a, i32x4 (&p)[4]) {
 #pragma unroll
@@ -595,11 +748,46 @@ __global__ __launch_bounds__(512, 1) void k_qgemm_i8_v3(const int8_t* __restrict
     __builtin_amdgcn_sched_barrier(0);                                                              \
     p0[T] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af[0][1], bf[1][T], p0[T], 0, 0, 0);             \
     __builtin_amdgcn_sched_barrier(0);
-    QG3_SLICE0_PAIR(0, 11)
-    QG3_SLICE0_PAIR(1, 9)
-    QG3_SLICE0_PAIR(2, 7)
-    QG3_SLICE0_PAIR(3, 5)
+// modes 1/2: the pair's B fragments are its 4 transposed reads
+#define QG3_SLICE0_PAIRT(T, WAITN)                                                                  \
+    chunk(2 * T);                                                                                   \
+    __builtin_amdgcn_sched_barrier(0);                                                              \
+    qg3_lgkm_wait<WAITN>(af[0][0]);                                                                 \
+    qg3_lgkm_wait<WAITN>(af[0][1]);                                                                 \
+    qg3_lgkm_wait<WAITN>(btr[T][0]);                                                                \
+    qg3_lgkm_wait<WAITN>(btr[T][1]);                                                                \
+    qg3_lgkm_wait<WAITN>(btr[T][2]);                                                                \
+    qg3_lgkm_wait<WAITN>(btr[T][3]);                                                                \
+    __builtin_amdgcn_sched_barrier(0);                                                              \
+    bf[0][T] = i32x4{btr[T][0][0], btr[T][0][1], btr[T][1][0], btr[T][1][1]};                       \
+    bf[1][T] = i32x4{btr[T][2][0], btr[T][2][1], btr[T][3][0], btr[T][3][1]};                       \
+    p0[T] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af[0][0], bf[0][T], i32x4{0, 0, 0, 0}, 0, 0, 0); \
+    __builtin_amdgcn_sched_barrier(0);                                                              \
+    chunk(2 * T + 1);                                                                               \
+    __builtin_amdgcn_sched_barrier(0);                                                              \
+    p0[T] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af[0][1], bf[1][T], p0[T], 0, 0, 0);             \
+    __builtin_amdgcn_sched_barrier(0);
+    if constexpr (MODE == 0) {
+      QG3_SLICE0_PAIR(0, 11)
+      QG3_SLICE0_PAIR(1, 9)
+      QG3_SLICE0_PAIR(2, 7)
+      QG3_SLICE0_PAIR(3, 5)
+    } else {
+      // in flight: A0 (2), fragments 0-2 (12); pair t needs A0 and fragment t
+      QG3_SLICE0_PAIRT(0, 8)
+      issue_b(3);  // fragments 1-3: 12 in flight
+      QG3_SLICE0_PAIRT(1, 8)
+      sbv = qg3_ds_read<0>(bsb);
+      sa[0] = qg3_ds_read<0>(bsa);
+      af[1][0] = qg3_ds_read<2048>(b0);
+      af[1][1] = qg3_ds_read<2048>(b1);
+      sa[1] = qg3_ds_read<64>(bsa);  // fragments 2-3 and these 5: 13 in flight
+      __builtin_amdgcn_sched_barrier(0);
+      QG3_SLICE0_PAIRT(2, 9)
+      QG3_SLICE0_PAIRT(3, 5)
+    }
 #undef QG3_SLICE0_PAIR
+#undef QG3_SLICE0_PAIRT
     qg3_lgkm_wait<0>(sbv);
     qg3_lgkm_wait<0>(sa[0]);
     qg3_lgkm_wait<0>(af[1][0]);
@@ -611,7 +799,7 @@ __global__ __launch_bounds__(512, 1) void k_qgemm_i8_v3(const int8_t* __restrict
     af[3][0] = qg3_ds_read<3 * 2048>(b0);
     af[3][1] = qg3_ds_read<3 * 2048>(b1);
     sa[3] = qg3_ds_read<192>(bsa);
-    if (ld) load_part(kb + 2, lbuf, 0);
+    if (MODE != 2 && ld) load_part(kb + 2, lbuf, 0);
     __builtin_amdgcn_sched_barrier(0);
     slice_mfma(1, p1);
     slice_epilogue(0, p0, sa[0]);
@@ -620,7 +808,7 @@ __global__ __launch_bounds__(512, 1) void k_qgemm_i8_v3(const int8_t* __restrict
     qg3_lgkm_wait<3>(af[2][0]);
     qg3_lgkm_wait<3>(af[2][1]);
     qg3_lgkm_wait<3>(sa[2]);
-    if (ld) load_part(kb + 2, lbuf, 1);
+    if (MODE != 2 && ld) load_part(kb + 2, lbuf, 1);
     __builtin_amdgcn_sched_barrier(0);
     slice_mfma(2, p0);
     slice_epilogue(1, p1, sa[1]);
@@ -629,7 +817,17 @@ __global__ __launch_bounds__(512, 1) void k_qgemm_i8_v3(const int8_t* __restrict
     qg3_lgkm_wait<0>(af[3][0]);
     qg3_lgkm_wait<0>(af[3][1]);
     qg3_lgkm_wait<0>(sa[3]);
-    if (ld) {
+    if constexpr (MODE == 2) {
+      // every read of this stage has returned: unpack stage kb+1 (loaded
+      // during kb-1) into its buffer, then load stage kb+2 into the VGPRs
+      // and its scales into the stage every wave finished before this
+      // block's barrier
+      if (kb + 1 < KB) write4(cur == 2 ? 0 : cur + 1);
+      if (ld) {
+        load4(kb + 2);
+        load_part(kb + 2, lbuf, 3);
+      }
+    } else if (ld) {
       load_part(kb + 2, lbuf, 2);
       load_part(kb + 2, lbuf, 3);
     }
@@ -643,15 +841,26 @@ __global__ __launch_bounds__(512, 1) void k_qgemm_i8_v3(const int8_t* __restrict
     sb3 = sbv;
   };
 
-  load_part(0, 0, 0);
-  load_part(0, 0, 1);
-  load_part(0, 0, 2);
-  load_part(0, 0, 3);
-  if (KB > 1) {
-    load_part(1, 1, 0);
-    load_part(1, 1, 1);
-    load_part(1, 1, 2);
-    load_part(1, 1, 3);
+  if constexpr (MODE == 2) {
+    // stage 0 unpacked into LDS, stage 1 in flight (packed codes in VGPRs)
+    load4(0);
+    load_part(0, 0, 3);
+    write4(0);
+    if (KB > 1) {
+      load4(1);
+      load_part(1, 1, 3);
+    }
+  } else {
+    load_part(0, 0, 0);
+    load_part(0, 0, 1);
+    load_part(0, 0, 2);
+    load_part(0, 0, 3);
+    if (KB > 1) {
+      load_part(1, 1, 0);
+      load_part(1, 1, 1);
+      load_part(1, 1, 2);
+      load_part(1, 1, 3);
+    }
   }
   int cur = 0;
   for (int kb = 0; kb < KB; ++kb) {
@@ -672,12 +881,44 @@ __global__ __launch_bounds__(512, 1) void k_qgemm_i8_v3(const int8_t* __restrict
         const float rs = ROWSCALE ? sa_t[row] : 1.0f;
 #pragma unroll
         for (int b = 0; b < 4; ++b) {
-          const int64_t col = n0 + wn * 64 + b * 16 + lr;
+          const int64_t col = n0 + wn * 64 + b * 16 + lcol;
           const float v = ROWSCALE ? c[a][b][i] * rs : c[a][b][i];
           if (col < N) C[row * N + col] = bias ? v + bias[col] : v;
         }
       }
   }
+}
+
+template <bool WRITE_ACC, bool WRITE_C, bool ROWSCALE = false>
+__global__ __launch_bounds__(512, 1) void k_qgemm_i8_v3(const int8_t* __restrict__ A8, int64_t lda, int64_t Arows,
+                                                        const int8_t* __restrict__ B8, int64_t ldb, int64_t Brows,
+                                                        const float* __restrict__ sa_t,
+                                                        const float* __restrict__ sb_src, int64_t M, int64_t N,
+                                                        int KB, float* __restrict__ C, int32_t* __restrict__ acc_out,
+                                                        int grouped, const float* __restrict__ bias) {
+  __shared__ __attribute__((aligned(1024))) int8_t lds[QG3_LDS_BYTES];
+  qg3_run<0, WRITE_ACC, WRITE_C, ROWSCALE, false>(lds, A8, lda, Arows, B8, ldb, Brows, sa_t, sb_src, M, N, KB, C,
+                                                  acc_out, grouped, bias);
+}
+
+// The packed GEMM on operands as the caller stores them: mode 1 (int8; B
+// [K][N]) or mode 2 (int4; A [M][K/2], B [K][N/2]), see qg3_run.  Mode 2
+// reads `exact` (written by k_prep_sa4) once: 0 takes sa_s = SA * 2^-8, 1
+// the exact epilogue on sa_u = SA.
+template <int MODE, bool WRITE_ACC, bool WRITE_C>
+__global__ __launch_bounds__(512, 1) void k_qgemm_kn(const int8_t* __restrict__ A, int64_t lda, int64_t Arows,
+                                                     const int8_t* __restrict__ B, int64_t ldb, int64_t Brows,
+                                                     const float* __restrict__ sa_s, const float* __restrict__ sa_u,
+                                                     const int* __restrict__ exact, const float* __restrict__ sb_src,
+                                                     int64_t M, int64_t N, int KB, float* __restrict__ C,
+                                                     int32_t* __restrict__ acc_out, int grouped) {
+  __shared__ __attribute__((aligned(1024))) int8_t lds[QG3_LDS_BYTES];
+  if (MODE == 2 && __builtin_amdgcn_readfirstlane(*exact) != 0)
+    qg3_run<MODE, WRITE_ACC, WRITE_C, false, true>(lds, A, lda, Arows, B, ldb, Brows, sa_u, sb_src, M, N, KB, C,
+                                                   acc_out, grouped, nullptr);
+  else
+    qg3_run<MODE, WRITE_ACC, WRITE_C, false, false>(lds, A, lda, Arows, B, ldb, Brows, sa_s, sb_src, M, N, KB, C,
+                                                    acc_out, grouped, nullptr);
 }
 
 __global__ __launch_bounds__(256) void k_fill_ones(float* __restrict__ p, int64_t n) {
@@ -702,6 +943,37 @@ __global__ __launch_bounds__(256) void k_transpose_sa(const float* __restrict__ 
   }
 }
 
+// The int4 loop's A scales: ts[kb][m] = SA * 2^-8 and tu[kb][m] = SA for SA
+// = s[m * KB + kb] (1 when s is null); *exact becomes 1 when some SA * 2^-8
+// is inexact (an SA below 2^-118 with low bits that the shift drops), which
+// selects the loop's exact epilogue.  *exact is zeroed by k_zero_flag first.
+__global__ __launch_bounds__(256) void k_prep_sa4(const float* __restrict__ s, int64_t M, int64_t KB,
+                                                  float* __restrict__ ts, float* __restrict__ tu,
+                                                  int* __restrict__ exact) {
+  __shared__ float tile[32][33];
+  const int64_t k0 = (int64_t)blockIdx.x * 32, m0 = (int64_t)blockIdx.y * 32;
+  const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;
+  for (int i = ty; i < 32; i += 8) {
+    const int64_t m = m0 + i, k = k0 + tx;
+    tile[i][tx] = (m < M && k < KB) ? (s ? s[m * KB + k] : 1.0f) : 0.0f;
+  }
+  __syncthreads();
+  bool lost = false;
+  for (int i = ty; i < 32; i += 8) {
+    const int64_t k = k0 + i, m = m0 + tx;
+    if (k < KB && m < M) {
+      const float v = tile[tx][i];
+      const float vs = v * 0.00390625f;
+      ts[k * M + m] = vs;
+      tu[k * M + m] = v;
+      lost = lost || (vs * 256.0f != v && v == v);
+    }
+  }
+  if (lost) atomicOr(exact, 1);
+}
+
+__global__ void k_zero_flag(int* __restrict__ p) { *p = 0; }
+
 // t[kb][r] (kb_major) or t[r][kb] = s[(r*K + kb*kblk) / B]: the scale of
 // the kblk-wide K chunk kb of row r of a [R][K] operand whose flat blocks
 // of B elements each carry one scale (0 past the ns scales given).
@@ -721,28 +993,51 @@ struct GemmPlan {
   int KB, BP;
   int64_t KBP, Mpad, Npad;
   bool direct_a, v2, v3;
-  size_t a_bytes, b_bytes, c_bytes, q_bytes, sa_bytes, sb_bytes;
+  int kn;  // 1: int8 with B read as stored, 2: int4 A and B read as stored (k_qgemm_kn), 0: unpacking pre-pass
+  size_t a_bytes, b_bytes, c_bytes, q_bytes, sa_bytes, sb_bytes, su_bytes;
 };
 
-static GemmPlan plan_gemm(int64_t M, int64_t K, int64_t N, int bits, int block, int out_bits) {
+// `aligned`: both packed operands start on 16 bytes (the as-stored loops
+// load 16-byte pieces of them)
+static GemmPlan plan_gemm(int64_t M, int64_t K, int64_t N, int bits, int block, int out_bits, bool aligned = true) {
   GemmPlan p;
   p.KB = (int)ceil_div(K, block);
   p.BP = (int)(ceil_div(block, 64) * 64);
   p.KBP = (int64_t)p.KB * p.BP;
   p.Mpad = ceil_div(M, QG_BM) * QG_BM;
   p.Npad = ceil_div(N, QG_BN) * QG_BN;
-  p.direct_a = (bits == 8 && block % 64 == 0 && K % block == 0);
   auto up = [](size_t v) { return (v + 255) & ~(size_t)255; };
-  p.a_bytes = p.direct_a ? 0 : up((size_t)p.Mpad * (size_t)p.KBP);
-  p.b_bytes = up((size_t)p.Npad * (size_t)p.KBP);
   p.c_bytes = out_bits > 0 ? up((size_t)M * (size_t)N * sizeof(float)) : 0;
   p.q_bytes = out_bits > 0 ? up((size_t)ceil_div(M * N, block) * sizeof(float2)) : 0;
-  p.v2 = p.BP == 128 && p.KB < 65536;
-  // v3 addresses A8, B8 and the scale arrays with 32-bit buffer offsets
   const int64_t lim = (int64_t)1 << 31;
+  const bool big = ceil_div(M, QG3_BM) * ceil_div(N, QG3_BN) >= num_cus();
+  // (and A's scale transpose fits its grid: M/32 workgroup rows)
+  const bool scales32 = (int64_t)p.KB * M * 4 < lim && (int64_t)p.KB * N * 4 < lim && ceil_div(M, 32) < 65536;
+  // the as-stored loops: one K block of 128 codes per stage, 32-bit buffer
+  // offsets, B rows of whole 16-byte pieces
+  p.kn = 0;
+  if (aligned && block == 128 && K % 128 == 0 && big && scales32) {
+    if (bits == 8 && N % 16 == 0 && M * K < lim && K * N < lim) p.kn = 1;
+    if (bits == 4 && N % 32 == 0 && M * K / 2 < lim && K * N / 2 < lim) p.kn = 2;
+  }
+  if (p.kn) {
+    p.direct_a = true;
+    p.v2 = p.v3 = true;
+    p.a_bytes = p.b_bytes = 0;
+    p.sa_bytes = up((size_t)p.KB * (size_t)M * sizeof(float));
+    p.su_bytes = p.kn == 2 ? p.sa_bytes + 256 : 0;  // unscaled SA and the exact flag
+    p.sb_bytes = up((size_t)p.KB * (size_t)N * sizeof(float));
+    return p;
+  }
+  p.su_bytes = 0;
+  p.direct_a = (bits == 8 && block % 64 == 0 && K % block == 0);
+  p.a_bytes = p.direct_a ? 0 : up((size_t)p.Mpad * (size_t)p.KBP);
+  p.b_bytes = up((size_t)p.Npad * (size_t)p.KBP);
+  p.v2 = p.BP == 128 && p.KB < 65536 && ceil_div(M, 32) < 65536;  // (k_transpose_sa's grid)
+  // v3 addresses A8, B8 and the scale arrays with 32-bit buffer offsets
   const int64_t a_span = p.direct_a ? M * K : p.Mpad * p.KBP;
-  const bool fits32 = a_span < lim && p.Npad * p.KBP < lim && (int64_t)p.KB * M * 4 < lim && (int64_t)p.KB * N * 4 < lim;
-  p.v3 = p.v2 && fits32 && ceil_div(M, QG3_BM) * ceil_div(N, QG3_BN) >= num_cus();
+  const bool fits32 = a_span < lim && p.Npad * p.KBP < lim && scales32;
+  p.v3 = p.v2 && fits32 && big;
   p.sa_bytes = p.v2 ? up((size_t)p.KB * (size_t)M * sizeof(float)) : 0;
   p.sb_bytes = p.v3 ? up((size_t)p.KB * (size_t)N * sizeof(float)) : 0;  // ones, when B's scales do not fit
   return p;
@@ -792,7 +1087,7 @@ extern "C" {
 size_t mxk_qgemm_workspace(int64_t M, int64_t K, int64_t N, int bits, int block, int out_bits) {
   if (M <= 0 || K <= 0 || N <= 0 || block <= 0) return 0;
   GemmPlan p = plan_gemm(M, K, N, bits, block, out_bits);
-  return p.a_bytes + p.b_bytes + p.c_bytes + p.q_bytes + p.sa_bytes + p.sb_bytes + 1024;
+  return p.a_bytes + p.b_bytes + p.c_bytes + p.q_bytes + p.sa_bytes + p.sb_bytes + p.su_bytes + 1024;
 }
 
 int mxk_qgemm(const void* a_packed, const float* a_scales, int64_t a_nscales, const void* b_packed,
@@ -809,10 +1104,70 @@ int mxk_qgemm(const void* a_packed, const float* a_scales, int64_t a_nscales, co
     return fail(MXK_EUNSUPPORTED, "qgemm: output width must be 2..8 or 16");
   if (out_bits > 0 && c_packed_nbytes < mxk_packed_nbytes(out_bits, M * N))
     return fail(MXK_EINVAL, "qgemm: packed output too small");
-  GemmPlan p = plan_gemm(M, K, N, bits, block, out_bits);
-  const size_t need = p.a_bytes + p.b_bytes + p.c_bytes + p.q_bytes + p.sa_bytes + p.sb_bytes;
-  if (!workspace || workspace_nbytes < need) return fail(MXK_EINVAL, "qgemm: workspace too small");
+  GemmPlan p = plan_gemm(M, K, N, bits, block, out_bits, aligned16(a_packed) && aligned16(b_packed));
+  const size_t need = p.a_bytes + p.b_bytes + p.c_bytes + p.q_bytes + p.sa_bytes + p.sb_bytes + p.su_bytes;
+  if (!workspace || workspace_nbytes < need)
+    return fail(MXK_EINVAL, (aligned16(a_packed) && aligned16(b_packed))
+                                ? "qgemm: workspace too small"
+                                : "qgemm: workspace too small (operands not 16-byte aligned take the unpacking "
+                                  "path, whose workspace mxk_qgemm_workspace does not count)");
   uint8_t* ws = reinterpret_cast<uint8_t*>(workspace);
+  const int a_ok = a_nscales == M * p.KB;
+  const int b_ok = b_nscales == (int64_t)p.KB * N;
+  if (p.kn) {
+    // operands as stored: no unpacking or transposing pass
+    float* Cb = c_f32 ? c_f32 : (p.c_bytes ? reinterpret_cast<float*>(ws) : nullptr);
+    void* qw = ws + p.c_bytes;
+    float* sa_s = reinterpret_cast<float*>(ws + p.c_bytes + p.q_bytes);
+    float* sb_one = reinterpret_cast<float*>(ws + p.c_bytes + p.q_bytes + p.sa_bytes);
+    float* sa_u = p.kn == 2 ? reinterpret_cast<float*>(ws + p.c_bytes + p.q_bytes + p.sa_bytes + p.sb_bytes)
+                            : nullptr;
+    int* exact = p.kn == 2 ? reinterpret_cast<int*>(reinterpret_cast<uint8_t*>(sa_u) + p.sa_bytes) : nullptr;
+    if (!Cb && !acc_i32) return fail(MXK_EINVAL, "qgemm: no output requested");
+    const int cap = num_cus() * 8;
+    const dim3 tg((unsigned)ceil_div(p.KB, 32), (unsigned)ceil_div(M, 32));
+    if (p.kn == 2) {
+      hipLaunchKernelGGL(k_zero_flag, dim3(1), dim3(1), 0, st, exact);
+      hipLaunchKernelGGL(k_prep_sa4, tg, dim3(256), 0, st, a_ok ? a_scales : nullptr, M, (int64_t)p.KB, sa_s, sa_u,
+                         exact);
+    } else if (a_ok) {
+      hipLaunchKernelGGL(k_transpose_sa, tg, dim3(256), 0, st, a_scales, M, (int64_t)p.KB, sa_s);
+    } else {
+      hipLaunchKernelGGL(k_fill_ones, dim3((unsigned)std::min<int64_t>(ceil_div((int64_t)p.KB * M, 256), cap)),
+                         dim3(256), 0, st, sa_s, (int64_t)p.KB * M);
+    }
+    const float* sbs = b_scales;
+    if (!b_ok) {
+      hipLaunchKernelGGL(k_fill_ones, dim3((unsigned)std::min<int64_t>(ceil_div((int64_t)p.KB * N, 256), cap)),
+                         dim3(256), 0, st, sb_one, (int64_t)p.KB * N);
+      sbs = sb_one;
+    }
+    const int64_t tiles_m = ceil_div(M, QG3_BM), tiles_n = ceil_div(N, QG3_BN);
+    const int grouped = (tiles_m % 8 == 0 && tiles_n % 8 == 0 && (tiles_m * tiles_n) % 512 == 0) ? 1 : 0;
+    const dim3 g1((unsigned)(tiles_m * tiles_n));
+    const int8_t* A = (const int8_t*)a_packed;
+    const int8_t* B = (const int8_t*)b_packed;
+    const int64_t lda = p.kn == 2 ? K / 2 : K, ldb = p.kn == 2 ? N / 2 : N;
+#define QG_KN_LAUNCH(MODE, WA, WC)                                                                                 \
+  hipLaunchKernelGGL((k_qgemm_kn<MODE, WA, WC>), g1, dim3(512), 0, st, A, lda, M, B, ldb, K, sa_s, sa_u, exact, sbs, \
+                     M, N, p.KB, Cb, acc_i32, grouped)
+    if (p.kn == 1) {
+      if (acc_i32 && Cb) QG_KN_LAUNCH(1, true, true);
+      else if (acc_i32) QG_KN_LAUNCH(1, true, false);
+      else QG_KN_LAUNCH(1, false, true);
+    } else {
+      if (acc_i32 && Cb) QG_KN_LAUNCH(2, true, true);
+      else if (acc_i32) QG_KN_LAUNCH(2, true, false);
+      else QG_KN_LAUNCH(2, false, true);
+    }
+#undef QG_KN_LAUNCH
+    int rc = check_launch("qgemm");
+    if (rc != MXK_OK) return rc;
+    if (out_bits > 0)
+      return requant_vec_f32(Cb, M * N, out_bits, block, c_packed, c_packed_nbytes, c_scales, M * N, qw, p.q_bytes,
+                             st);
+    return MXK_OK;
+  }
   int8_t* A8 = p.direct_a ? (int8_t*)a_packed : reinterpret_cast<int8_t*>(ws);
   int8_t* B8 = reinterpret_cast<int8_t*>(ws + p.a_bytes);
   float* Cbuf = c_f32 ? c_f32 : (p.c_bytes ? reinterpret_cast<float*>(ws + p.a_bytes + p.b_bytes) : nullptr);
@@ -837,8 +1192,6 @@ int mxk_qgemm(const void* a_packed, const float* a_scales, int64_t a_nscales, co
     hipLaunchKernelGGL(k_unpack_rows, dim3((int)std::min<int64_t>(ceil_div(total, 256), cap)), dim3(256), 0, st,
                        (const uint8_t*)b_packed, b_bytes_src, bits, N, p.Npad, K, 1, N, block, p.BP, p.KB, B8);
   }
-  const int a_ok = a_nscales == M * p.KB;
-  const int b_ok = b_nscales == (int64_t)p.KB * N;
   dim3 grid((unsigned)ceil_div(N, QG_BN), (unsigned)ceil_div(M, QG_BM));
   const int64_t lda = p.direct_a ? K : p.KBP;
   const int64_t arows = p.direct_a ? M : p.Mpad;

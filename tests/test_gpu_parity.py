@@ -282,36 +282,82 @@ def test_qgemm_seeded_vs_oracle(qa, dtype, shape):
     assert _bits_eq(res["scales"], scales)
 
 
-@pytest.mark.parametrize("shape", [(4096, 384, 2048), (4100, 640, 2050), (4096, 256, 4096), (4096, 128, 2048),
-                                   (4096, 1152, 2048)],
-                         ids=lambda s: "x".join(map(str, s)))
-def test_qgemm_large_tiles_sampled_rows(qa, shape):
+def _large_gemm_vs_oracle(qa, dtype, M, K, N, pa, sa, pb, sb, rows):
+    """C and the int32 accumulators of qscale_gemm on the GPU (all three
+    kernel variants: C and accumulators, C only, accumulators only) against
+    the oracle on a sample of A's rows (output rows are independent).
+    Scale arrays whose counts do not match M*KB / KB*N stand for ones, as in
+    the reference."""
+    bits = qa.get_mx_dtype(dtype).bits
+    res = qa.ops.qscale_gemm(pa, sa, pb, sb, M, K, N, bits, 128, 16, want_packed=False, want_c=True, want_acc=True)
+    c_only = qa.ops.qscale_gemm(pa, sa, pb, sb, M, K, N, bits, 128, 16, want_packed=False, want_c=True)
+    acc_only = qa.ops.qscale_gemm(pa, sa, pb, sb, M, K, N, bits, 128, 16, want_packed=False, want_acc=True)
+    assert _bits_eq(res["c"], c_only["c"])
+    assert torch.equal(res["acc"], acc_only["acc"])
+    KB = -(-K // 128)
+    ac = orc.unpack_auto(pa.cpu(), bits, M * K).to(torch.int32).reshape(M, K)[rows].reshape(-1)
+    bc = orc.unpack_auto(pb.cpu(), bits, K * N).to(torch.int32)
+    sa_rows = sa.cpu().reshape(M, KB)[rows].reshape(-1) if sa.numel() == M * KB else sa.cpu()[:1]
+    _, _, C = orc.qscale_matmul(ac, sa_rows, bc, sb.cpu(), len(rows), K, N, bits, 128, 16, return_c=True)
+    assert _bits_eq(res["c"].cpu()[rows], C.reshape(len(rows), N))
+    acc = orc.int_accumulators(ac, bc, len(rows), K, N, 128)
+    assert torch.equal(res["acc"].cpu()[:, rows], acc)
+    return res
+
+
+LARGE_GEMM_SHAPES = [(4096, 384, 2048), (4100, 640, 2050), (4100, 640, 2080), (4096, 256, 4096), (4096, 128, 2048),
+                     (4096, 1152, 2048)]
+
+
+@pytest.mark.parametrize("dtype", ["int8d", "int4d"])
+@pytest.mark.parametrize("shape", LARGE_GEMM_SHAPES, ids=lambda s: "x".join(map(str, s)))
+def test_qgemm_large_tiles_sampled_rows(qa, dtype, shape):
     """Shapes large enough for the 256x128-tile pipelined kernel (grouped and
     row-major tile orders, one and two K blocks, K blocks past the 3-stage
-    ring, ragged M/N).  Output rows are independent, so the oracle runs on a
-    sample of A's rows and must match those rows of C and of the int32
-    accumulators bitwise.  The three kernel variants (C and accumulators, C
-    only, accumulators only) must agree."""
+    ring, ragged M/N).  N % 16 == 0 (int8) or N % 32 == 0 (int4) takes the
+    loop that reads both operands as stored (int4 unpacked in its load
+    stage); 2050 takes the unpacking pre-pass.  Bitwise against the oracle
+    on sampled rows of C and of the int32 accumulators."""
     M, K, N = shape
-    dt = qa.get_mx_dtype("int8d")
+    dt = qa.get_mx_dtype(dtype)
     A = _randn((M, K), 101 + K)
     B = _randn((K, N), 103 + N)
     pa, sa, _ = qa.ops.quantize(A.to(dev()), dt, 128)
     pb, sb, _ = qa.ops.quantize(B.to(dev()), dt, 128)
-    res = qa.ops.qscale_gemm(pa, sa, pb, sb, M, K, N, 8, 128, 16, want_packed=False, want_c=True, want_acc=True)
-    c_only = qa.ops.qscale_gemm(pa, sa, pb, sb, M, K, N, 8, 128, 16, want_packed=False, want_c=True)
-    acc_only = qa.ops.qscale_gemm(pa, sa, pb, sb, M, K, N, 8, 128, 16, want_packed=False, want_acc=True)
-    assert _bits_eq(res["c"], c_only["c"])
-    assert torch.equal(res["acc"], acc_only["acc"])
-    KB = -(-K // 128)
     rows = sorted({0, 1, 15, 16, 17, 127, 128, 255, 256, 1000, M // 2, M - 2, M - 1})
-    ac = orc.unpack_auto(pa.cpu(), 8, M * K).to(torch.int32).reshape(M, K)[rows].reshape(-1)
-    bc = orc.unpack_auto(pb.cpu(), 8, K * N).to(torch.int32)
-    sa_rows = sa.cpu().reshape(M, KB)[rows].reshape(-1)
-    _, _, C = orc.qscale_matmul(ac, sa_rows, bc, sb.cpu(), len(rows), K, N, 8, 128, 16, return_c=True)
-    assert _bits_eq(res["c"].cpu()[rows], C.reshape(len(rows), N))
-    acc = orc.int_accumulators(ac, bc, len(rows), K, N, 128)
-    assert torch.equal(res["acc"].cpu()[:, rows], acc)
+    _large_gemm_vs_oracle(qa, dtype, M, K, N, pa, sa, pb, sb, rows)
+
+
+@pytest.mark.parametrize("dtype", ["int8d", "int4d"])
+def test_qgemm_large_tiles_scale_counts(qa, dtype):
+    """Scale arrays of the wrong length mean ones (mxtorch.py:1352-1355) on
+    the as-stored loop as well: A's, B's, and both."""
+    M, K, N = 4096, 384, 2048
+    dt = qa.get_mx_dtype(dtype)
+    pa, sa, _ = qa.ops.quantize(_randn((M, K), 211).to(dev()), dt, 128)
+    pb, sb, _ = qa.ops.quantize(_randn((K, N), 213).to(dev()), dt, 128)
+    rows = [0, 5, 255, 256, 2047, 4095]
+    for a_s, b_s in ((sa[:-1], sb), (sa, sb[:-1]), (sa[:-1], sb[:-1])):
+        _large_gemm_vs_oracle(qa, dtype, M, K, N, pa, a_s, pb, b_s, rows)
+
+
+def test_qgemm_int4_tiny_scales(qa):
+    """The int4 loop folds the code unpacking's factor 256 into A's scales
+    (SA * 2^-8) when that is exact; scales below 2^-118 whose low bits the
+    shift would drop switch it to the exact epilogue.  Rows whose scales
+    are scaled by 2^-124 and 2^-140 (subnormal), and normal rows, all
+    bitwise against the oracle."""
+    M, K, N = 4096, 512, 2048
+    dt = qa.get_mx_dtype("int4d")
+    pa, sa, _ = qa.ops.quantize(_randn((M, K), 221).to(dev()), dt, 128)
+    pb, sb, _ = qa.ops.quantize(_randn((K, N), 223).to(dev()), dt, 128)
+    ts = sa.clone().view(M, -1)
+    ts[1::4] *= 2.0 ** -124
+    ts[2::4] *= 2.0 ** -140
+    ts = ts.reshape(-1)
+    assert ((ts * 2.0 ** -8) * 2.0 ** 8 != ts).any(), "the test needs scales the 2^-8 fold cannot carry"
+    rows = [0, 1, 2, 3, 5, 6, 1022, 1023, 4093, 4094]
+    _large_gemm_vs_oracle(qa, "int4d", M, K, N, pa, ts, pb, sb, rows)
 
 
 @pytest.mark.parametrize("dtype", ["int4d", "int8d", "int2d", "float4d", "float8d", "int1d"])
