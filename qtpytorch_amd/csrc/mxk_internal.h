@@ -167,6 +167,19 @@ __device__ __forceinline__ void store_bytes(uint8_t* __restrict__ dst, int64_t o
   }
 }
 
+// Zeroes the fields of codes at positions >= lim (lim may be <= 0) in a
+// lane's NW words of BITS-bit fields (code i at bit i * BITS): the codes a
+// quantizer writes past n_store.  Called only for the lanes that reach the
+// end, so the other lanes skip a per-code comparison.
+template <int NW, int BITS>
+__device__ __forceinline__ void clear_tail(uint32_t (&w)[NW], int64_t lim) {
+#pragma unroll
+  for (int k = 0; k < NW; ++k) {
+    const int64_t keep = lim * BITS - 32 * k;
+    w[k] &= keep >= 32 ? 0xFFFFFFFFu : (keep <= 0 ? 0u : ((1u << keep) - 1u));
+  }
+}
+
 // ---------------------------------------------------------------- float grids
 // Positive grid magnitude of code c (c < 2^(bits-1)), in units of the
 // format's largest value, exactly as _get_minifloat_grid builds it
@@ -269,7 +282,14 @@ __device__ __forceinline__ BlockParams block_params(float ap, float qf) {
 template <int MODE, int BITS>
 __device__ __forceinline__ int encode(float v, const BlockParams& bp, float qf, const float* P) {
   if constexpr (MODE == Q_INT) {
-    return (int)rne(fminf(fmaxf(v * bp.mul, -qf), qf));
+    // rne of the clamped product by the float adder: t + 1.5 * 2^23 (|t| <=
+    // q <= 2^15) is rounded to an integer with ties to even and leaves
+    // 2^22 + 2^23 + rne(t) in the significand, so the integer is the bit
+    // pattern minus that of 1.5 * 2^23 (one add and one subtract in place
+    // of a round and a conversion; callers that mask the low bits lose the
+    // subtract)
+    const float t = fminf(fmaxf(v * bp.mul, -qf), qf);
+    return (int)(__float_as_uint(t + 12582912.0f) - 0x4B400000u);
   } else if constexpr (MODE == Q_INT1) {
     return v >= 0.0f ? 0 : 1;
   } else if constexpr (MODE == Q_VEC) {

@@ -83,11 +83,26 @@ __global__ __launch_bounds__(256) void k_quant_fast(const T* __restrict__ x, int
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int g = lane / LPB, li = lane % LPB;
   const int64_t rstride = (int64_t)gridDim.x * GPB;
+  // The next grid-stride step's elements are loaded before this step is
+  // encoded, so that every wave keeps two steps of loads in flight.
+  float vn[Q][CH];
+  {
+    const int64_t blk = (int64_t)blockIdx.x * GPB + wave * GPW + g;
+#pragma unroll
+    for (int q = 0; q < Q; ++q) load_elems<T, CH>(x, blk * B + q * (B / Q) + (int64_t)li * CH, n, vn[q]);
+  }
   for (int64_t b0 = (int64_t)blockIdx.x * GPB; b0 < nb; b0 += rstride) {
     const int64_t blk = b0 + wave * GPW + g;
     float v[Q][CH];
 #pragma unroll
-    for (int q = 0; q < Q; ++q) load_elems<T, CH>(x, blk * B + q * (B / Q) + (int64_t)li * CH, n, v[q]);
+    for (int q = 0; q < Q; ++q)
+#pragma unroll
+      for (int i = 0; i < CH; ++i) v[q][i] = vn[q][i];
+    if (b0 + rstride < nb) {
+      const int64_t nblk = blk + rstride;
+#pragma unroll
+      for (int q = 0; q < Q; ++q) load_elems<T, CH>(x, nblk * B + q * (B / Q) + (int64_t)li * CH, n, vn[q]);
+    }
     float m = 0.0f;
 #pragma unroll
     for (int q = 0; q < Q; ++q)
@@ -103,10 +118,10 @@ __global__ __launch_bounds__(256) void k_quant_fast(const T* __restrict__ x, int
       for (int k = 0; k < NW; ++k) w[k] = 0u;
 #pragma unroll
       for (int i = 0; i < CH; ++i) {
-        uint32_t f = (uint32_t)encode<MODE, BITS>(v[q][i], bp, qf, sP) & MASK;
-        if (idx + i >= n_store) f = 0u;
+        const uint32_t f = (uint32_t)encode<MODE, BITS>(v[q][i], bp, qf, sP) & MASK;
         w[(i * BITS) >> 5] |= f << ((i * BITS) & 31);
       }
+      if (idx + CH > n_store) clear_tail<NW, BITS>(w, n_store - idx);
       if constexpr (NIB) {
         const uint32_t other = (uint32_t)__builtin_amdgcn_mov_dpp((int)w[0], 0xB1, 0xF, 0xF, true);
         w[0] = (w[0] & 0xFu) | ((other & 0xFu) << 4);
@@ -167,10 +182,10 @@ __global__ __launch_bounds__(256) void k_quant_rows(const T* __restrict__ x, int
       for (int k = 0; k < NW; ++k) w[k] = 0u;
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        uint32_t f = (uint32_t)encode<MODE, BITS>(v[r][e], bp, qf, sP) & MASK;
-        if (idx + e >= n_store) f = 0u;
+        const uint32_t f = (uint32_t)encode<MODE, BITS>(v[r][e], bp, qf, sP) & MASK;
         w[(e * BITS) >> 5] |= f << ((e * BITS) & 31);
       }
+      if (idx + 8 > n_store) clear_tail<NW, BITS>(w, n_store - idx);
       store_bytes<BITS>(packed, idx * BITS / 8, packed_nbytes, w);
     }
     if (threadIdx.x == 0) scales[blk] = bp.s;
@@ -321,29 +336,53 @@ __global__ __launch_bounds__(256) void k_quant_had128(const T* __restrict__ x, i
   for (int i = 0; i < E; ++i) sg[i] = signs[li * 16 + i];
   const float rdiv = 11.3137083f;           // fl32(sqrt(128))
   const float rinv = 1.0f / 11.3137083f;
-  for (int64_t b0 = (int64_t)blockIdx.x * GPB; b0 < nb; b0 += (int64_t)gridDim.x * GPB) {
+  const int64_t rstride = (int64_t)gridDim.x * GPB;
+  // the next grid-stride step's row is loaded before this one is rotated
+  float vn[E];
+  load_elems<T, E>(x, ((int64_t)blockIdx.x * GPB + wave * GPW + g) * 128 + (int64_t)li * E, n, vn);
+  for (int64_t b0 = (int64_t)blockIdx.x * GPB; b0 < nb; b0 += rstride) {
     const int64_t blk = b0 + wave * GPW + g;
     const int64_t idx = blk * 128 + (int64_t)li * E;
     float v[E];
-    load_elems<T, E>(x, idx, n, v);
+#pragma unroll
+    for (int i = 0; i < E; ++i) v[i] = vn[i];
+    if (b0 + rstride < nb) load_elems<T, E>(x, idx + rstride * 128, n, vn);
 #pragma unroll
     for (int i = 0; i < E; ++i) v[i] = v[i] * sg[i];
     fwht128_group(v, row, li);
-    div_rn_all<E>(v, rdiv, rinv);
-    float m = 0.0f;
+    // one pass over the magnitudes gives the block maximum and the wave's
+    // smallest nonzero magnitude (which picks the division path, as in
+    // div_rn_all); the scale comes from the maximum before the division:
+    // a correctly rounded division is monotone, so max RN(|v|/d) = RN(max |v| / d)
+    float mx = 0.0f, mn = __builtin_inff();
 #pragma unroll
-    for (int i = 0; i < E; ++i) m = fmaxf(m, __builtin_fabsf(v[i]));
-    const float ap = fmaxf(group_max<LPB>(m), MXK_AMIN);
+    for (int i = 0; i < E; ++i) {
+      const float t = __builtin_fabsf(v[i]);
+      mx = fmaxf(mx, t);
+      mn = fminf(mn, t == 0.0f ? __builtin_inff() : t);
+    }
+    const float gmx = group_max<LPB>(mx);
+    float am;
+    if (__builtin_expect(__ballot(mn < 0x1p-96f) != 0ull, 0)) {
+#pragma unroll
+      for (int i = 0; i < E; ++i) v[i] = v[i] / rdiv;
+      am = gmx / rdiv;
+    } else {
+#pragma unroll
+      for (int i = 0; i < E; ++i) v[i] = div_rn_nochk(v[i], rdiv, rinv);
+      am = div_rn(gmx, rdiv, rinv);
+    }
+    const float ap = fmaxf(am, MXK_AMIN);
     const BlockParams bp = block_params<MODE>(ap, qf);
     uint32_t w[NW];
 #pragma unroll
     for (int k = 0; k < NW; ++k) w[k] = 0u;
 #pragma unroll
     for (int i = 0; i < E; ++i) {
-      uint32_t f = (uint32_t)encode<MODE, BITS>(v[i], bp, qf, sP) & MASK;
-      if (idx + i >= n_store) f = 0u;
+      const uint32_t f = (uint32_t)encode<MODE, BITS>(v[i], bp, qf, sP) & MASK;
       w[(i * BITS) >> 5] |= f << ((i * BITS) & 31);
     }
+    if (idx + E > n_store) clear_tail<NW, BITS>(w, n_store - idx);
     if (blk < nb) {
       store_bytes<NB>(packed, idx * BITS / 8, packed_nbytes, w);
       if (li == 0) scales[blk] = bp.s;
