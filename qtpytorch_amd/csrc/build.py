@@ -48,6 +48,17 @@ def _compile(src: str, obj: str) -> None:
         raise RuntimeError(f"hipcc failed for {src}:\n{r.stderr[-6000:]}")
 
 
+def _check_waits(src: str) -> None:
+    import importlib.util
+
+    spec = importlib.util.spec_from_file_location("mxk_check_lgkm", os.path.join(HERE, "check_lgkm.py"))
+    check_lgkm = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(check_lgkm)
+    n, problems = check_lgkm.check_source(src, hipcc(), HIPCC_FLAGS)
+    if problems:
+        raise RuntimeError(f"LDS wait check failed for {os.path.basename(src)} ({n} kernels):\n" + "\n".join(problems))
+
+
 def build(jobs: int = 4, verbose: bool = True) -> str:
     objdir = os.path.join(HERE, "_build")
     os.makedirs(objdir, exist_ok=True)
@@ -55,8 +66,11 @@ def build(jobs: int = 4, verbose: bool = True) -> str:
     objs = [os.path.join(objdir, s.replace(".hip", ".o")) for s in srcs]
     with cf.ThreadPoolExecutor(max_workers=max(1, jobs)) as ex:
         futs = [ex.submit(_compile, s, o) for s, o in zip(srcs, objs)]
+        # the GEMM's hand-counted LDS waits, checked on its assembly (check_lgkm.py)
+        chk = ex.submit(_check_waits, os.path.join(HERE, "mxk_gemm.hip"))
         for f in futs:
             f.result()
+        chk.result()
     tmp = OUT + ".tmp"
     cmd = [hipcc(), "--offload-arch=gfx950", "-shared", "-fPIC", "-o", tmp, *objs]
     r = subprocess.run(cmd, capture_output=True, text=True)
