@@ -86,14 +86,18 @@ def test_config4_full_size_sampled_blocks(qa, config4_x, dtype):
 
 
 @pytest.mark.parametrize("dtype", ["int8dv", "int4d"])
-def test_config5_kv_full_size_sampled_rows(qa, dtype):
-    g = torch.Generator(device="cuda").manual_seed(9)
-    k = torch.randn(8, 32, 4096, 128, generator=g, device="cuda").half()
-    rows = k.view(-1, 128)
+@pytest.mark.parametrize("which", ["K", "V"])
+def test_config5_kv_full_size_sampled_rows(qa, dtype, which):
+    """Config 5: fp16 K and V [8, 32, 4096, 128] (the seeds bench.py uses),
+    quantized per row of head_dim and dequantized; sampled blocks bitwise
+    against the oracle."""
+    g = torch.Generator(device="cuda").manual_seed(9 if which == "K" else 10)
+    t = torch.randn(8, 32, 4096, 128, generator=g, device="cuda").half()
+    rows = t.view(-1, 128)
     dt = qa.get_mx_dtype(dtype)
     packed, scales, n = qa.ops.quantize(rows, dt, 128)
     nb = rows.shape[0]
-    blocks = _sample_blocks(nb, 2048, 21)
+    blocks = _sample_blocks(nb, 2048, 21 if which == "K" else 23)
     ks = rows[blocks.to(rows.device)].cpu()
     rp, rs, _ = orc.quantize(ks, dtype, 128)
     assert _bits_eq(_block_codes(packed, dt.bits, blocks), rp.view(torch.uint8))
@@ -102,20 +106,23 @@ def test_config5_kv_full_size_sampled_rows(qa, dtype):
     assert _bits_eq(dq.view(nb, 128)[blocks.to(rows.device)], orc.dequant(rp, rs, dtype, ks.numel(), 128).view(-1, 128))
 
 
-def test_config3_gemm_full_size_sampled_rows(qa):
+@pytest.mark.parametrize("dtype", ["int8d", "int4d"])
+def test_config3_gemm_full_size_sampled_rows(qa, dtype):
+    """8192^3 as bench.py runs it (config 3 for int8d; the int4d GEMM
+    extra): sampled rows of the fp32 C bitwise against the oracle."""
     M = K = N = 8192
-    dt = qa.get_mx_dtype("int8d")
+    dt = qa.get_mx_dtype(dtype)
     A = torch.randn(M, K, generator=torch.Generator(device="cuda").manual_seed(5), device="cuda")
     B = torch.randn(K, N, generator=torch.Generator(device="cuda").manual_seed(6), device="cuda")
     pa, sa, _ = qa.ops.quantize(A, dt, 128)
     pb, sb, _ = qa.ops.quantize(B, dt, 128)
     del A, B
-    res = qa.ops.qscale_gemm(pa, sa, pb, sb, M, K, N, 8, 128, 16, want_packed=False, want_c=True)
+    res = qa.ops.qscale_gemm(pa, sa, pb, sb, M, K, N, dt.bits, 128, 16, want_packed=False, want_c=True)
     rows = sorted({0, 1, 127, 128, 255, 4095, 4096, 8190, 8191})
-    ac = pa.view(M, K)[rows].cpu().to(torch.int32).reshape(-1)
-    bc = pb.cpu().to(torch.int32)
+    ac = orc.unpack_auto(pa.cpu(), dt.bits, M * K).to(torch.int32).view(M, K)[rows].reshape(-1)
+    bc = orc.unpack_auto(pb.cpu(), dt.bits, K * N).to(torch.int32)
     sa_rows = sa.view(M, 64)[rows].cpu().reshape(-1)
-    _, _, C = orc.qscale_matmul(ac, sa_rows, bc, sb.cpu(), len(rows), K, N, 8, 128, 16, return_c=True)
+    _, _, C = orc.qscale_matmul(ac, sa_rows, bc, sb.cpu(), len(rows), K, N, dt.bits, 128, 16, return_c=True)
     assert _bits_eq(res["c"][rows], C.view(len(rows), N))
     del res, pa, pb
     torch.cuda.empty_cache()
