@@ -279,6 +279,28 @@ __device__ __forceinline__ BlockParams block_params(float ap, float qf) {
   return bp;
 }
 
+// bucket<4> without the table: the positive mids of the normalized E2M1
+// grid are constants, RN((g[j-1] + g[j]) * 0.5) with g[c] = RN(v_c / 6) in
+// float32, the values build_tables computes.  #{mids < a} comes from a
+// binary search over them (three comparisons, selects, no LDS); for y <= 0
+// the count of mids <= |y| is the count of mids < nextup(|y|).  Equal to
+// bucket<4> for every finite y (checked exhaustively over all float32
+// patterns); a NaN takes the last index, as torch.bucketize gives it.
+__device__ __forceinline__ int bucket_fp4(float y) {
+  constexpr float g1 = 0.5f / 6.0f, g2 = 1.0f / 6.0f, g3 = 1.5f / 6.0f, g4 = 2.0f / 6.0f, g5 = 3.0f / 6.0f,
+                  g6 = 4.0f / 6.0f, g7 = 6.0f / 6.0f;
+  constexpr float P1 = (0.0f + g1) * 0.5f, P2 = (g1 + g2) * 0.5f, P3 = (g2 + g3) * 0.5f, P4 = (g3 + g4) * 0.5f,
+                  P5 = (g4 + g5) * 0.5f, P6 = (g5 + g6) * 0.5f, P7 = (g6 + g7) * 0.5f;
+  const float a0 = __builtin_fabsf(y);
+  const bool pos = !(y <= 0.0f);
+  const float a = pos ? a0 : __uint_as_float(__float_as_uint(a0) + 1u);
+  // !(a <= P) is a > P for numbers and true for a NaN
+  int c = !(a <= P4) ? 4 : 0;
+  c += !(a <= (c ? P6 : P2)) ? 2 : 0;
+  c += !(a <= (c == 6 ? P7 : (c == 4 ? P5 : (c == 2 ? P3 : P1)))) ? 1 : 0;
+  return pos ? 8 + c : 7 - c;
+}
+
 template <int MODE, int BITS>
 __device__ __forceinline__ int encode(float v, const BlockParams& bp, float qf, const float* P) {
   if constexpr (MODE == Q_INT) {
@@ -294,6 +316,8 @@ __device__ __forceinline__ int encode(float v, const BlockParams& bp, float qf, 
     return v >= 0.0f ? 0 : 1;
   } else if constexpr (MODE == Q_VEC) {
     return (int)rne(fminf(fmaxf(div_rn(v, bp.s, bp.mul), -qf), qf));
+  } else if constexpr (BITS == 4) {
+    return bucket_fp4(div_rn(v, bp.s, bp.mul));
   } else {
     return bucket<BITS>(div_rn(v, bp.s, bp.mul), P);
   }
