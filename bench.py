@@ -131,7 +131,7 @@ def bench_linear(args, qa):
     m = layers[0]
     x = x_cpu.to(dev)
     y = m(x)
-    for layer in layers:  # each layer makes its block-major scale copy once, outside the timed graph
+    for layer in layers:  # each layer makes its block-major scale and tiled weight copies once, outside the timed graph
         layer(x)
     torch.cuda.synchronize()
     it = [0]

@@ -36,7 +36,7 @@
 extern "C" {
 #endif
 
-#define MXK_ABI_VERSION 4
+#define MXK_ABI_VERSION 5
 
 typedef enum {
   MXK_OK = 0,
@@ -152,7 +152,7 @@ int mxk_qgemm(const void* a_packed, const float* a_scales, int64_t a_nscales, co
  * sums, then room for block-major scales when w_scales_t is NULL) must be
  * zero-filled before first use, and every call, of any shape, leaves the
  * counter prefix ready for the next one.  Calls sharing a workspace must
- * not overlap. */
+ * not overlap.  The size also covers mxk_linear_wq_tiled. */
 size_t mxk_linear_workspace(int64_t M, int64_t K, int64_t N, int bits, int block);
 
 /* Block-major copy of a weight's scales for the decode path: w_scales_t[b][k]
@@ -191,6 +191,31 @@ int mxk_linear_wq(const void* x, int x_type, int64_t M, int64_t K, const void* w
 int mxk_linear_wq_noalloc(const void* x, int x_type, int64_t M, int64_t K, const void* w_packed,
                           const float* w_scales, const float* w_scales_t, int64_t N, int kind, int bits, int block,
                           const float* bias, float* out, void* stream);
+
+/* Tiled copy of an int4 weight for mxk_linear_wq_tiled: w_packed is the
+ * [K][N] packing of quantize(weight.t()) (mxtorch.py:7447), bits 4, block
+ * 128, K a multiple of 32, N of 128; w_tiled receives the same K*N/2 bytes
+ * reordered so that the decode kernel reads each wave's rows as contiguous
+ * 16-byte loads and builds its MFMA operands without byte permutes (2 KiB per
+ * 128-column block and 32-row step).  No reference counterpart: the
+ * reference dequantizes the whole weight instead (mxtorch.py:7454-7473).
+ * Weights are static, so callers make this copy once per weight.
+ * w_packed 4-byte aligned, w_tiled 16-byte aligned. */
+int mxk_linear_prepack_weight(const void* w_packed, int64_t K, int64_t N, int bits, int block, void* w_tiled,
+                              void* stream);
+
+/* mx_linear.forward (mxtorch.py:7454-7473) for int4 weights, block 128, from
+ * the prepacked copies: out[M,N] = x[M,K] @ dequant(W) (+ bias), the same
+ * product as mxk_linear_wq's decode path, float32 accumulation in another
+ * order.  w_tiled = mxk_linear_prepack_weight(), w_scales_t =
+ * mxk_linear_prepack_scales().  Takes M <= 16, K % 32 == 0, N % 128 == 0,
+ * 16-byte aligned x, w_tiled, w_scales_t, bias and out; other shapes return
+ * MXK_EUNSUPPORTED (call mxk_linear_wq).  workspace: as for mxk_linear_wq
+ * (mxk_linear_workspace() bytes, zero-filled before first use, left ready
+ * for the next call; calls sharing it must not overlap). */
+int mxk_linear_wq_tiled(const void* x, int x_type, int64_t M, int64_t K, const void* w_tiled,
+                        const float* w_scales_t, int64_t N, const float* bias, float* out, void* workspace,
+                        size_t workspace_nbytes, void* stream);
 
 /* One step of kv_cache_quantizer.append_kv (mxtorch.py:3039-3067) written
  * into a caller-owned ring slot (the reference appends a new mx_tensor to a

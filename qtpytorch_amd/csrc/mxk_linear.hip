@@ -501,6 +501,329 @@ __global__ __launch_bounds__(DEC_THREADS, 1) void k_linear_w4_decode(
   }
 }
 
+// ---------------------------------------------------------------- int4 decode, tiled weight copy
+// The same product as k_linear_w4_decode, y[m, n] = sum_k x[m,k] *
+// RN(code[k,n] * s[k, n/128]), read from a tiled copy of the weight
+// (mxk_linear_prepack_weight) laid out so that every 16-byte load of a wave
+// is contiguous and every MFMA B operand comes out of the loaded words with
+// one v_bitop3 (no byte permutes):
+//   chunk (block nb, 32-row step ks): 2048 bytes at (nb * K/32 + ks) * 2048;
+//   lane l = j + 16 g reads 16 bytes at +16 l (words 0..3) and +1024 + 16 l
+//   (words 4..7).  Word 2p + e holds the byte of columns 8j + 2p, 8j + 2p + 1
+//   (low nibble = even column) of rows 8g + 4e + {0, 2, 1, 3} in its bytes
+//   0..3.  So (w & 0x000F000F) is the f16 pair of rows 8g+4e, +1 of column
+//   8j + 2p as denormals code * 2^-24, (w >> 8) & 0x000F000F the pair of
+//   rows +2, +3, and the masks 0x00F000F0 give column 8j + 2p + 1 as
+//   code * 2^-20; xor with 8 per nibble turns the two's complement code into
+//   code + 8, removed by the correction tile as in k_linear_w4_decode.
+//
+// Work split: one 128-column block per workgroup (the tiled rows are whole
+// lines at any width), 16 waves of RPW = 32 * STEPS rows each, so K splits
+// S = ceil(K / (16 * RPW)) ways.  Each wave reads its own x rows
+// row-contiguously (one load covering 16 rows 32 KiB apart would put every
+// request on one memory channel), turns them into the A-fragment order
+// through its own LDS slot (no workgroup barrier), scales them per row into
+// [1, 2), and only then requests its weights, so that x is not queued behind
+// the weight stream.  The partial reduction and the split-K hand-off are
+// those of k_linear_w4_decode.
+template <typename T, int STEPS>
+__global__ __launch_bounds__(DEC_THREADS, 1) void k_linear_w4_decode_tiled(
+    const T* __restrict__ x, int M, int64_t K, int64_t N, const uint32_t* __restrict__ wt,
+    const float* __restrict__ scales_t, const float* __restrict__ bias, float* __restrict__ out,
+    float* __restrict__ partials, unsigned long long* __restrict__ counters, int S, int xcd_map) {
+  using G = DecGeom<STEPS, 1>;
+  constexpr int RPW = G::RPW, R = G::R, TPB = G::TPB, RT = G::RT, CPT = G::CPT;
+  constexpr int EPL = 16 / (int)sizeof(T);   // x elements per 16-byte load
+  constexpr int LPR = RPW / EPL;             // lanes per x row in one load
+  constexpr int RPL = 64 / LPR;              // x rows per load
+  constexpr int XLD = 16 / RPL;              // x loads per lane
+  static_assert(LPR >= 1 && RPL * LPR == 64 && XLD * RPL == 16, "x loads");
+  static_assert(RPW / 4 <= 64 && RPW <= DEC_RS, "scales and x rows of a wave");
+  static_assert(CPT % 4 == 0 && TPB * CPT == 2048, "reduction split");
+  // each wave's slot of 16 x DEC_RS floats holds its x rows, then its partial
+  __shared__ __attribute__((aligned(16))) float sR[DEC_WAVES * 16 * DEC_RS];
+  __shared__ __attribute__((aligned(16))) float sS[DEC_WAVES * RPW];
+  __shared__ int sXe[DEC_WAVES * 16];
+  __shared__ int s_flags;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int j = lane & 15, g = lane >> 4;
+  const int64_t NB = N / 128;
+  int64_t nb;
+  int ks;
+  if (xcd_map) {
+    const int i = (int)(blockIdx.x >> 3);
+    nb = (int64_t)(i / S) * 8 + (blockIdx.x & 7);
+    ks = i % S;
+  } else {
+    nb = blockIdx.x / S;
+    ks = blockIdx.x % S;
+  }
+  const int64_t kw = (int64_t)ks * R + (int64_t)wave * RPW;  // this wave's first row
+
+  // ---- x rows and scales of this wave
+  const __amdgpu_buffer_rsrc_t rx = make_rsrc(x, (uint32_t)((int64_t)M * K * sizeof(T)));
+  const __amdgpu_buffer_rsrc_t rs = make_rsrc(scales_t, (uint32_t)(K * NB * 4));
+  u32x4 xr[XLD];
+#pragma unroll
+  for (int q = 0; q < XLD; ++q) {
+    const int m = q * RPL + lane / LPR;
+    const int64_t kk = kw + (int64_t)EPL * (lane % LPR);
+    const bool ok = m < M && kk < K;  // K % 32 == 0: a load is wholly in or out
+    xr[q] = buf_load_b128(rx, ok ? (uint32_t)(((int64_t)m * K + kk) * sizeof(T)) : DEC_OOB, 0u);
+  }
+  const int64_t r4 = kw + 4 * lane;
+  const u32x4 sst = buf_load_b128(rs, (lane < RPW / 4 && r4 < K) ? (uint32_t)((nb * K + r4) * 4) : DEC_OOB, 0u);
+  __builtin_amdgcn_sched_barrier(0);
+
+  // ---- x into the A-fragment order (lane (j, g): row j, columns
+  // 32 st + 8 g .. +7) through the wave's slot; LDS runs a wave's accesses in
+  // order, so only the compiler needs holding back.  Range as in
+  // k_linear_w4_decode: row j's largest |x| in this wave to [1, 2), the
+  // wave's largest scale to [2^13, 2^14).
+  float* xs = sR + wave * 16 * DEC_RS;
+#pragma unroll
+  for (int q = 0; q < XLD; ++q) {
+    const int m = q * RPL + lane / LPR;
+    const int c = EPL * (lane % LPR);
+    float v[EPL];
+    if constexpr (EPL == 4) {
+#pragma unroll
+      for (int u = 0; u < 4; ++u) v[u] = __uint_as_float(xr[q][u]);
+    } else {
+      const T* tt = reinterpret_cast<const T*>(&xr[q]);
+#pragma unroll
+      for (int u = 0; u < EPL; ++u) v[u] = ElemT<T>::cvt(tt[u]);
+    }
+#pragma unroll
+    for (int u = 0; u < EPL; u += 4)
+      *reinterpret_cast<f32x4*>(xs + m * DEC_RS + c + u) = f32x4{v[u], v[u + 1], v[u + 2], v[u + 3]};
+  }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  float xv[STEPS * 8];
+#pragma unroll
+  for (int st = 0; st < STEPS; ++st)
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const f32x4 t = *reinterpret_cast<const f32x4*>(xs + j * DEC_RS + 32 * st + 8 * g + 4 * h);
+#pragma unroll
+      for (int u = 0; u < 4; ++u) xv[8 * st + 4 * h + u] = t[u];
+    }
+  float mx = 0.0f;
+#pragma unroll
+  for (int u = 0; u < STEPS * 8; ++u) mx = fmaxf(mx, __builtin_fabsf(xv[u]));
+  // row j sits in lanes j, j + 16, j + 32, j + 48
+  mx = fmaxf(mx, __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(mx), 0x401F)));
+  mx = fmaxf(mx, __shfl_xor(mx, 32));
+  const int be = (int)((__float_as_uint(mx) >> 23) & 0xFFu);
+  const int xe = be == 0xFF ? 0 : 127 - (be == 0 ? 1 : be);  // zero rows: any shift
+#pragma unroll
+  for (int u = 0; u < STEPS * 8; ++u) xv[u] = __builtin_ldexpf(xv[u], xe);
+  if (g == 0) sXe[wave * 16 + j] = xe;
+  float sv[4];
+  float smx = 0.0f;
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    sv[u] = __uint_as_float(sst[u]);
+    smx = fmaxf(smx, __builtin_fabsf(sv[u]));
+  }
+  smx = group_max<64>(smx);
+  const int sbe = (int)((__float_as_uint(smx) >> 23) & 0xFFu);
+  const int se = sbe == 0xFF ? 0 : 140 - (sbe == 0 ? 1 : sbe);  // largest scale to [2^13, 2^14)
+  float* wS = sS + wave * RPW;
+  if (lane < RPW / 4)
+    *reinterpret_cast<f32x4*>(wS + 4 * lane) = f32x4{__builtin_ldexpf(sv[0], se), __builtin_ldexpf(sv[1], se),
+                                                     __builtin_ldexpf(sv[2], se), __builtin_ldexpf(sv[3], se)};
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+
+  // ---- weights of every step, requested once this wave's x is in.  A step
+  // past K (only in the last split) re-reads chunk 0 of the block; its x rows
+  // and scales are zeros.
+  const __amdgpu_buffer_rsrc_t rw = make_rsrc(wt, (uint32_t)(K * N / 2));
+  u32x4 wq[STEPS][2];
+#pragma unroll
+  for (int st = 0; st < STEPS; ++st) {
+    const int64_t k0 = kw + (int64_t)st * 32;
+    const uint32_t kr = k0 < K ? (uint32_t)k0 : 0u;  // wave-uniform
+    const uint32_t cbase = (uint32_t)((nb * (K / 32) + kr / 32) * 2048);
+    wq[st][0] = buf_load_b128(rw, 16u * lane, cbase);
+    wq[st][1] = buf_load_b128(rw, 16u * lane, cbase + 1024u);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+
+  f32x4 acc[8];
+#pragma unroll
+  for (int t = 0; t < 8; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+  f32x4 corr = f32x4{0.f, 0.f, 0.f, 0.f};
+  const f16x8 b8 = __builtin_bit_cast(f16x8, u32x4v{0x00800080u, 0x00800080u, 0x00800080u, 0x00800080u});
+  const float* srow = wS + 8 * g;
+#pragma unroll
+  for (int st = 0; st < STEPS; ++st) {
+    const f32x4 x0 = f32x4{xv[8 * st], xv[8 * st + 1], xv[8 * st + 2], xv[8 * st + 3]};
+    const f32x4 x1 = f32x4{xv[8 * st + 4], xv[8 * st + 5], xv[8 * st + 6], xv[8 * st + 7]};
+    const f32x4 s0 = *reinterpret_cast<const f32x4*>(srow + st * 32);
+    const f32x4 s1 = *reinterpret_cast<const f32x4*>(srow + st * 32 + 4);
+    f16x8 ahi, alo;
+    split_hi_lo(x0, x1, s0, s1, ahi, alo);
+    uint32_t wr[8], w8[8];
+#pragma unroll
+    for (int r = 0; r < 8; ++r) {
+      wr[r] = r < 4 ? wq[st][0][r] : wq[st][1][r - 4];
+      w8[r] = wr[r] >> 8;
+    }
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+      // tile t: column 8j + t; even tiles the low nibbles (code * 2^-24),
+      // odd tiles the high nibbles (code * 2^-20)
+      const int p = t >> 1;
+      const uint32_t msk = (t & 1) ? 0x00F000F0u : 0x000F000Fu;
+      const uint32_t off8 = (t & 1) ? 0x00800080u : 0x00080008u;
+      const u32x4v bq = {(wr[2 * p] & msk) ^ off8, (w8[2 * p] & msk) ^ off8, (wr[2 * p + 1] & msk) ^ off8,
+                         (w8[2 * p + 1] & msk) ^ off8};
+      const f16x8 bt = __builtin_bit_cast(f16x8, bq);
+      acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi, bt, acc[t], 0, 0, 0);
+      acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo, bt, acc[t], 0, 0, 0);
+    }
+    corr = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi, b8, corr, 0, 0, 0);
+    corr = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo, b8, corr, 0, 0, 0);
+  }
+
+  // ---- wave partial (rows 4g+i, columns 8j+t) into its own slot: no
+  // barrier first, nothing else uses the slot
+  float* rwv = sR + wave * 16 * DEC_RS;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int sh = -sXe[wave * 16 + 4 * g + i] - se;
+    float v[8];
+#pragma unroll
+    for (int t = 0; t < 8; ++t)
+      v[t] = (t & 1) ? __builtin_ldexpf(acc[t][i] - corr[i], 20 + sh)
+                     : __builtin_ldexpf(acc[t][i] - corr[i] * 0.0625f, 24 + sh);
+    float* dst = rwv + (4 * g + i) * DEC_RS + 8 * j;
+    *reinterpret_cast<f32x4*>(dst) = f32x4{v[0], v[1], v[2], v[3]};
+    *reinterpret_cast<f32x4*>(dst + 4) = f32x4{v[4], v[5], v[6], v[7]};
+  }
+  __syncthreads();
+  // thread (< RT): row m, columns c .. c+CPT-1, summed over the waves in order
+  const bool rt = threadIdx.x < RT;
+  const int r = threadIdx.x % TPB;
+  const int m = r / (128 / CPT), c = CPT * (r % (128 / CPT));
+  f32x4 sum[CPT / 4];
+#pragma unroll
+  for (int h = 0; h < CPT / 4; ++h) {
+    sum[h] = *reinterpret_cast<const f32x4*>(sR + m * DEC_RS + c + 4 * h);
+#pragma unroll
+    for (int q = 1; q < DEC_WAVES; ++q) sum[h] += *reinterpret_cast<const f32x4*>(sR + (q * 16 + m) * DEC_RS + c + 4 * h);
+  }
+  const int64_t col = nb * 128 + c;
+  if (S == 1) {
+    if (rt && m < M) {
+#pragma unroll
+      for (int h = 0; h < CPT / 4; ++h) {
+        f32x4 o = sum[h];
+        if (bias) o += *reinterpret_cast<const f32x4*>(bias + col + 4 * h);
+        *reinterpret_cast<f32x4*>(out + (int64_t)m * N + col + 4 * h) = o;
+      }
+    }
+    return;
+  }
+  // split-K hand-off as in k_linear_w4_decode: partials [S][N/128][16][128]
+  // written through, arrivals counted per XCC, the last arrival sums in
+  // split order
+  const __amdgpu_buffer_rsrc_t rp = make_rsrc(partials, (uint32_t)((int64_t)S * NB * 16 * 128 * 4));
+  const uint32_t poff = (uint32_t)(((nb * 16 + m) * 128 + c) * 4);
+  const uint32_t split_stride = (uint32_t)(NB * 16 * 128 * 4);
+  if (rt) {
+#pragma unroll
+    for (int h = 0; h < CPT / 4; ++h)
+      __builtin_amdgcn_raw_buffer_store_b128(sum[h], rp, poff + 16u * h, (uint32_t)ks * split_stride, 16);
+  }
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    unsigned xcc;
+    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
+    xcc &= 7u;
+    const unsigned long long inc = 1ull << (8 * xcc);
+    const unsigned long long now =
+        __hip_atomic_fetch_add(&counters[nb], inc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + inc;
+    unsigned total = 0;
+#pragma unroll
+    for (int q = 0; q < 8; ++q) total += (unsigned)((now >> (8 * q)) & 0xFFull);
+    const bool same = ((now >> (8 * xcc)) & 0xFFull) == (unsigned long long)S;
+    const bool last = total == (unsigned)S;
+    if (last) __hip_atomic_store(&counters[nb], 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    s_flags = (last ? 1 : 0) | (same ? 2 : 0);
+  }
+  __syncthreads();
+  const int fl = s_flags;
+  if (!(fl & 1) || !rt) return;
+  f32x4 tot[CPT / 4];
+  for (int sb = 0; sb < S; sb += 8) {
+    f32x4 part[8][CPT / 4];
+#pragma unroll
+    for (int u = 0; u < 8; ++u)
+#pragma unroll
+      for (int h = 0; h < CPT / 4; ++h) {
+        const bool ld = sb + u < S && sb + u != ks;
+        const uint32_t soff = ld ? (uint32_t)(sb + u) * split_stride : 0u;
+        if (!ld)
+          part[u][h] = sum[h];
+        else if (fl & 2)
+          part[u][h] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rp, poff + 16u * h, soff, 1));
+        else
+          part[u][h] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rp, poff + 16u * h, soff, 16));
+      }
+#pragma unroll
+    for (int u = 0; u < 8; ++u)
+      if (sb + u < S)
+#pragma unroll
+        for (int h = 0; h < CPT / 4; ++h) tot[h] = (sb + u == 0) ? part[u][h] : tot[h] + part[u][h];
+  }
+  if (m < M) {
+#pragma unroll
+    for (int h = 0; h < CPT / 4; ++h) {
+      f32x4 o = tot[h];
+      if (bias) o += *reinterpret_cast<const f32x4*>(bias + col + 4 * h);
+      *reinterpret_cast<f32x4*>(out + (int64_t)m * N + col + 4 * h) = o;
+    }
+  }
+}
+
+// The tiled copy of an int4 [K][N] weight (layout above): thread (block nb,
+// 32-row step ks, lane j + 16 g) reads the 4-byte word of columns 8j..8j+7
+// from rows 8g..8g+7 and writes its 32 bytes of the chunk.
+__global__ __launch_bounds__(256) void k_tile_w4(const uint32_t* __restrict__ w, int64_t K, int64_t N,
+                                                 uint32_t* __restrict__ wt) {
+  const int64_t tid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t steps = K / 32, NB = N / 128;
+  if (tid >= NB * steps * 64) return;
+  const int lane = (int)(tid & 63);
+  const int64_t chunk = tid >> 6;  // nb * steps + ks
+  const int64_t nb = chunk / steps, ks = chunk % steps;
+  const int j = lane & 15, g = lane >> 4;
+  const int64_t words = N / 8;  // 4-byte words per row
+  uint32_t rw[8];
+#pragma unroll
+  for (int r = 0; r < 8; ++r) rw[r] = w[(ks * 32 + 8 * g + r) * words + nb * 16 + j];
+  uint32_t o[8];
+#pragma unroll
+  for (int p = 0; p < 4; ++p)
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+      const uint32_t b0 = (rw[4 * e + 0] >> (8 * p)) & 0xFFu, b1 = (rw[4 * e + 2] >> (8 * p)) & 0xFFu;
+      const uint32_t b2 = (rw[4 * e + 1] >> (8 * p)) & 0xFFu, b3 = (rw[4 * e + 3] >> (8 * p)) & 0xFFu;
+      o[2 * p + e] = b0 | (b1 << 8) | (b2 << 16) | (b3 << 24);
+    }
+  uint32_t* dst = wt + chunk * 512 + 4 * lane;
+  *reinterpret_cast<u32x4v*>(dst) = u32x4v{o[0], o[1], o[2], o[3]};
+  *reinterpret_cast<u32x4v*>(dst + 256) = u32x4v{o[4], o[5], o[6], o[7]};
+}
+
 // sT[b][k] = s[k][b]: the reference's scales of a [K, N] weight with blocks
 // of 128 along N ([K][NB] row-major) to the block-major order the decode
 // kernel reads ([NB][K]).  32x32 tiles through LDS, both sides coalesced.
@@ -876,6 +1199,53 @@ static void launch_decode(const DecodePlan& p, hipStream_t st, const void* x, in
 #undef MXK_DEC
 }
 
+// The tiled kernel: one block per workgroup, the longest waves that still
+// give every CU a workgroup, else the shape with the most workgroups.
+static DecodePlan plan_decode_tiled(int64_t K, int64_t N) {
+  DecodePlan p;
+  const int64_t NB = N / 128;
+  const int64_t target = num_cus();
+  p.nbw = 1;
+  p.steps = 1;
+  int64_t best = -1;
+  for (const int steps : {4, 2, 1}) {
+    const int64_t S = ceil_div(K, dec_rows(1, steps));
+    if (S > 255) continue;  // 8-bit arrival counts per XCC
+    const int64_t grid = NB * S;
+    if (grid > best) {
+      best = grid;
+      p.steps = steps;
+    }
+    if (grid >= target) {
+      p.steps = steps;
+      break;
+    }
+  }
+  p.S = (int)ceil_div(K, dec_rows(1, p.steps));
+  p.xcd_map = NB % 8 == 0 ? 1 : 0;
+  p.partial_bytes = p.S > 1 ? (((size_t)p.S * (size_t)NB * 8192 + 255) & ~(size_t)255) : 0;
+  p.counter_bytes = DEC_COUNTER_BYTES;
+  p.scales_t_bytes = 0;  // the tiled path takes prepacked scales only
+  return p;
+}
+
+template <typename T>
+static void launch_decode_tiled(const DecodePlan& p, hipStream_t st, const void* x, int64_t M, int64_t K, int64_t N,
+                                const uint32_t* wt, const float* scales_t, const float* bias, float* out,
+                                float* partials, unsigned long long* counters) {
+  const dim3 grid((unsigned)((N / 128) * p.S));
+#define MXK_DECT(STEPS)                                                                                  \
+  if (p.steps == STEPS) {                                                                               \
+    hipLaunchKernelGGL((k_linear_w4_decode_tiled<T, STEPS>), grid, dim3(DEC_THREADS), 0, st, (const T*)x, \
+                       (int)M, K, N, wt, scales_t, bias, out, partials, counters, p.S, p.xcd_map);      \
+    return;                                                                                             \
+  }
+  MXK_DECT(4)
+  MXK_DECT(2)
+  MXK_DECT(1)
+#undef MXK_DECT
+}
+
 static bool decode_eligible(int64_t M, int64_t K, int64_t N, int kind, int bits, int block, const void* x,
                             int x_type, const void* w) {
   if (kind != MXK_KIND_INT || bits != 4 || block != 128) return false;
@@ -891,6 +1261,21 @@ static bool decode_eligible(int64_t M, int64_t K, int64_t N, int kind, int bits,
   if ((K / 32 + 1) * (N / 128) * 8192 >= (int64_t(1) << 31)) return false;
   // each XCC's arrival count is 8 bits of a 64-bit counter: at most 255 splits
   return plan_decode(K, N).S <= 255;
+}
+
+// The tiled path: the decode path's shapes with a 16-byte aligned tiled
+// weight and prepacked scales.
+static bool decode_tiled_eligible(int64_t M, int64_t K, int64_t N, const void* x, int x_type, const void* wt,
+                                  const float* scales_t) {
+  if (M < 1 || M > 16 || K % 32 != 0 || N % 128 != 0) return false;
+  if (N / 128 > DEC_COUNTER_BYTES / 8 || K / 32 >= 65536) return false;
+  if (!aligned16(x) || !aligned16(wt) || !aligned16(scales_t)) return false;
+  const int esz = x_type == MXK_IN_F32 ? 4 : 2;
+  if ((K * esz) % 16 != 0) return false;
+  if (K * N / 2 >= (int64_t(1) << 31) || K * (N / 128) * 4 >= (int64_t(1) << 31) || 16 * K * esz >= (int64_t(1) << 31))
+    return false;
+  if ((K / 32 + 1) * (N / 128) * 8192 >= (int64_t(1) << 31)) return false;
+  return plan_decode_tiled(K, N).S <= 255;
 }
 
 template <bool WT, typename T, int MODE, int BITS>
@@ -977,9 +1362,53 @@ extern "C" {
 
 size_t mxk_linear_workspace(int64_t M, int64_t K, int64_t N, int bits, int block) {
   if (M < 1 || M > 16 || bits != 4 || block != 128 || K <= 0 || N <= 0 || K % 32 != 0 || N % 128 != 0) return 0;
-  DecodePlan p = plan_decode(K, N);
-  if (p.S > 255) return 0;  // the generic kernel takes these shapes
-  return p.counter_bytes + p.partial_bytes + p.scales_t_bytes;
+  // enough for mxk_linear_wq's decode path and for mxk_linear_wq_tiled
+  const DecodePlan p = plan_decode(K, N), q = plan_decode_tiled(K, N);
+  const size_t a = p.S <= 255 ? p.counter_bytes + p.partial_bytes + p.scales_t_bytes : 0;  // else generic kernel
+  const size_t b = q.S <= 255 ? q.counter_bytes + q.partial_bytes : 0;
+  return std::max(a, b);
+}
+
+int mxk_linear_prepack_weight(const void* w_packed, int64_t K, int64_t N, int bits, int block, void* w_tiled,
+                              void* stream) {
+  if (!w_packed || !w_tiled) return fail(MXK_EINVAL, "linear_prepack_weight: null pointer");
+  if (bits != 4 || block != 128 || K <= 0 || N <= 0 || K % 32 != 0 || N % 128 != 0)
+    return fail(MXK_EINVAL, "linear_prepack_weight: needs int4 codes, block 128, K a multiple of 32 and N of 128");
+  if ((reinterpret_cast<uintptr_t>(w_packed) & 3u) != 0 || !aligned16(w_tiled))
+    return fail(MXK_EINVAL, "linear_prepack_weight: w_packed must be 4-byte and w_tiled 16-byte aligned");
+  const int64_t threads = (N / 128) * (K / 32) * 64;
+  if (ceil_div(threads, 256) >= (int64_t(1) << 31)) return fail(MXK_EUNSUPPORTED, "linear_prepack_weight: too large");
+  hipLaunchKernelGGL(k_tile_w4, dim3((unsigned)ceil_div(threads, 256)), dim3(256), 0,
+                     reinterpret_cast<hipStream_t>(stream), reinterpret_cast<const uint32_t*>(w_packed), K, N,
+                     reinterpret_cast<uint32_t*>(w_tiled));
+  return check_launch("linear_prepack_weight");
+}
+
+int mxk_linear_wq_tiled(const void* x, int x_type, int64_t M, int64_t K, const void* w_tiled, const float* w_scales_t,
+                        int64_t N, const float* bias, float* out, void* workspace, size_t workspace_nbytes,
+                        void* stream) {
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  if (M <= 0 || K <= 0 || N <= 0) return fail(MXK_EINVAL, "linear_wq_tiled: sizes must be positive");
+  if (!x || !w_tiled || !w_scales_t || !out) return fail(MXK_EINVAL, "linear_wq_tiled: null pointer");
+  if (x_type != MXK_IN_F32 && x_type != MXK_IN_F16 && x_type != MXK_IN_BF16)
+    return fail(MXK_EINVAL, "linear_wq_tiled: bad input type");
+  if ((bias && !aligned16(bias)) || !aligned16(out))
+    return fail(MXK_EINVAL, "linear_wq_tiled: bias and out must be 16-byte aligned");
+  if (!decode_tiled_eligible(M, K, N, x, x_type, w_tiled, w_scales_t))
+    return fail(MXK_EUNSUPPORTED, "linear_wq_tiled: needs M <= 16, K % 32 == 0, N % 128 == 0, 16-byte aligned "
+                                  "x, w_tiled and w_scales_t (use mxk_linear_wq)");
+  const DecodePlan p = plan_decode_tiled(K, N);
+  const size_t need = p.counter_bytes + p.partial_bytes;
+  if (p.S > 1 && (!workspace || workspace_nbytes < need))
+    return fail(MXK_EINVAL, "linear_wq_tiled: needs a zero-initialised workspace of mxk_linear_workspace() bytes");
+  uint8_t* ws = reinterpret_cast<uint8_t*>(workspace);
+  unsigned long long* counters = p.S > 1 ? reinterpret_cast<unsigned long long*>(ws) : nullptr;
+  float* partials = p.S > 1 ? reinterpret_cast<float*>(ws + p.counter_bytes) : nullptr;
+  const uint32_t* wt = reinterpret_cast<const uint32_t*>(w_tiled);
+  if (x_type == MXK_IN_F32) launch_decode_tiled<float>(p, st, x, M, K, N, wt, w_scales_t, bias, out, partials, counters);
+  else if (x_type == MXK_IN_F16) launch_decode_tiled<__half>(p, st, x, M, K, N, wt, w_scales_t, bias, out, partials, counters);
+  else launch_decode_tiled<hip_bfloat16>(p, st, x, M, K, N, wt, w_scales_t, bias, out, partials, counters);
+  return check_launch("linear_wq_tiled");
 }
 
 int mxk_linear_prepack_scales(const float* w_scales, int64_t K, int64_t N, int block, float* w_scales_t,

@@ -85,11 +85,33 @@ class mx_linear(nn.Module):
         bias = None
         if self.apply_bias and self._mx_bias is not None:
             bias = self._mx_bias.dequantize()
+        rows = x.numel() // max(self.in_features, 1)
+        wt = self._decode_weight(w) if rows <= 16 else None
         if torch.is_grad_enabled() and x.requires_grad:
             # the reference's F.linear(x, W_dq) carries the input gradient grad @ W_dq^T
-            return _LinearWQ.apply(x, w, bias, self.in_features, self.out_features, self._decode_scales(w))
+            return _LinearWQ.apply(x, w, bias, self.in_features, self.out_features, self._decode_scales(w), wt)
         return ops.linear_wq(x, w._mx_packed, w._mx_scales, w._mx_dtype, self.in_features, self.out_features,
-                             w._mx_block, bias=bias, w_scales_t=self._decode_scales(w))
+                             w._mx_block, bias=bias, w_scales_t=self._decode_scales(w), w_tiled=wt)
+
+    # Whether decode-shaped forwards (at most 16 rows of x) keep a tiled copy
+    # of an int4 weight's packed codes (in*out/2 bytes, made on the first
+    # such forward) for the faster decode kernel; False saves that memory.
+    tiled_decode = True
+
+    def _decode_weight(self, w) -> Optional[Tensor]:
+        """Tiled copy of the packed int4 weight for the decode kernel, made
+        once per weight tensor and rebuilt when the packed codes are replaced
+        or modified in place."""
+        if not self.tiled_decode or not ops.decode_prepack_eligible(w._mx_dtype, w._mx_block, self.in_features,
+                                                                   self.out_features):
+            return None
+        pk = w._mx_packed
+        key = (pk.data_ptr(), str(pk.device), pk._version)
+        cached = self.__dict__.get("_w_tiled_cache")
+        if cached is None or cached[0] != key:
+            cached = (key, ops.prepack_weight(pk, self.in_features, self.out_features, w._mx_block))
+            self.__dict__["_w_tiled_cache"] = cached
+        return cached[1]
 
     def _decode_scales(self, w) -> Optional[Tensor]:
         """Block-major copy of the weight's scales for the int4 decode kernel,
@@ -124,11 +146,11 @@ class _LinearWQ(torch.autograd.Function):
     differentiates to that); the packed weight gets no gradient."""
 
     @staticmethod
-    def forward(ctx, x, w, bias, in_features, out_features, w_scales_t):
+    def forward(ctx, x, w, bias, in_features, out_features, w_scales_t, w_tiled=None):
         ctx.w, ctx.w_scales_t = w, w_scales_t
         ctx.in_features, ctx.out_features = in_features, out_features
         return ops.linear_wq(x.detach(), w._mx_packed, w._mx_scales, w._mx_dtype, in_features, out_features,
-                             w._mx_block, bias=bias, w_scales_t=w_scales_t)
+                             w._mx_block, bias=bias, w_scales_t=w_scales_t, w_tiled=w_tiled)
 
     @staticmethod
     def backward(ctx, grad):
@@ -137,7 +159,7 @@ class _LinearWQ(torch.autograd.Function):
         # scales of the transposed product
         gi = ops.linear_wq_nt(grad.contiguous(), w._mx_packed, w._mx_scales, w._mx_dtype, ctx.in_features,
                               ctx.out_features, w._mx_block, w_scales_t=ctx.w_scales_t)
-        return gi, None, None, None, None, None
+        return gi, None, None, None, None, None, None
 
 
 class _LinearWQNT(torch.autograd.Function):

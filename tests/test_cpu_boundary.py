@@ -93,6 +93,22 @@ def test_bad_arguments_return_errors_without_gpu():
     assert rc == -22
     rc = h.mxk_linear_prepack_scales(8, 256, 256, 64, 8, None)
     assert rc == -22
+    rc = h.mxk_linear_prepack_weight(None, 256, 256, 4, 128, 16, None)
+    assert rc == -22 and b"null" in h.mxk_last_error()
+    rc = h.mxk_linear_prepack_weight(16, 256, 200, 4, 128, 16, None)   # N not a multiple of 128
+    assert rc == -22
+    rc = h.mxk_linear_prepack_weight(16, 256, 256, 8, 128, 16, None)   # int8 codes
+    assert rc == -22
+    rc = h.mxk_linear_prepack_weight(16, 256, 256, 4, 128, 8, None)    # w_tiled not 16-byte aligned
+    assert rc == -22
+    rc = h.mxk_linear_wq_tiled(16, 0, 16, 256, None, 16, 256, None, 16, None, 0, None)
+    assert rc == -22 and b"null" in h.mxk_last_error()
+    rc = h.mxk_linear_wq_tiled(16, 7, 16, 256, 16, 16, 256, None, 16, None, 0, None)   # bad x type
+    assert rc == -22
+    rc = h.mxk_linear_wq_tiled(16, 0, 17, 256, 16, 16, 256, None, 16, None, 0, None)   # M > 16
+    assert rc == -95
+    rc = h.mxk_linear_wq_tiled(16, 0, 16, 256, 16, 16, 200, None, 16, None, 0, None)   # N % 128
+    assert rc == -95
 
 
 def test_decode_workspace_limits():
