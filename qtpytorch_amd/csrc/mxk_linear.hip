@@ -518,32 +518,36 @@ __global__ __launch_bounds__(DEC_THREADS, 1) void k_linear_w4_decode(
 //   code + 8, removed by the correction tile as in k_linear_w4_decode.
 //
 // Work split: one 128-column block per workgroup (the tiled rows are whole
-// lines at any width), 16 waves of RPW = 32 * STEPS rows each, so K splits
-// S = ceil(K / (16 * RPW)) ways.  Each wave reads its own x rows
+// lines at any width), W waves of RPW = 32 * STEPS rows each, so K splits
+// S = ceil(K / (W * RPW)) ways.  Long waves (8 waves of 8 steps, two per
+// SIMD) cost less than 16 waves of 4 steps over the same rows: each wave's
+// fixed work (scale range, epilogue, its partial in the LDS reduction) is
+// paid half as often.  Each wave reads its own x rows
 // row-contiguously (one load covering 16 rows 32 KiB apart would put every
 // request on one memory channel), turns them into the A-fragment order
 // through its own LDS slot (no workgroup barrier), scales them per row into
 // [1, 2), and only then requests its weights, so that x is not queued behind
 // the weight stream.  The partial reduction and the split-K hand-off are
 // those of k_linear_w4_decode.
-template <typename T, int STEPS>
-__global__ __launch_bounds__(DEC_THREADS, 1) void k_linear_w4_decode_tiled(
+template <typename T, int STEPS, int W>
+__global__ __launch_bounds__(W * 64, 1) void k_linear_w4_decode_tiled(
     const T* __restrict__ x, int M, int64_t K, int64_t N, const uint32_t* __restrict__ wt,
     const float* __restrict__ scales_t, const float* __restrict__ bias, float* __restrict__ out,
     float* __restrict__ partials, unsigned long long* __restrict__ counters, int S, int xcd_map) {
-  using G = DecGeom<STEPS, 1>;
-  constexpr int RPW = G::RPW, R = G::R, TPB = G::TPB, RT = G::RT, CPT = G::CPT;
+  constexpr int RPW = 32 * STEPS, R = W * RPW;
+  constexpr int TPB = W * 64 > 512 ? 512 : W * 64, RT = TPB, CPT = 2048 / TPB;
+  constexpr int XS = (RPW > 128 ? RPW : 128) + 4;  // row stride of a wave's LDS slot (floats)
   constexpr int EPL = 16 / (int)sizeof(T);   // x elements per 16-byte load
   constexpr int LPR = RPW / EPL;             // lanes per x row in one load
   constexpr int RPL = 64 / LPR;              // x rows per load
   constexpr int XLD = 16 / RPL;              // x loads per lane
   static_assert(LPR >= 1 && RPL * LPR == 64 && XLD * RPL == 16, "x loads");
-  static_assert(RPW / 4 <= 64 && RPW <= DEC_RS, "scales and x rows of a wave");
+  static_assert(RPW / 4 <= 64 && XS >= DEC_RS, "scales and x rows of a wave");
   static_assert(CPT % 4 == 0 && TPB * CPT == 2048, "reduction split");
-  // each wave's slot of 16 x DEC_RS floats holds its x rows, then its partial
-  __shared__ __attribute__((aligned(16))) float sR[DEC_WAVES * 16 * DEC_RS];
-  __shared__ __attribute__((aligned(16))) float sS[DEC_WAVES * RPW];
-  __shared__ int sXe[DEC_WAVES * 16];
+  // each wave's slot of 16 rows of XS floats holds its x rows, then its partial
+  __shared__ __attribute__((aligned(16))) float sR[W * 16 * XS];
+  __shared__ __attribute__((aligned(16))) float sS[W * RPW];
+  __shared__ int sXe[W * 16];
   __shared__ int s_flags;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -581,7 +585,7 @@ __global__ __launch_bounds__(DEC_THREADS, 1) void k_linear_w4_decode_tiled(
   // order, so only the compiler needs holding back.  Range as in
   // k_linear_w4_decode: row j's largest |x| in this wave to [1, 2), the
   // wave's largest scale to [2^13, 2^14).
-  float* xs = sR + wave * 16 * DEC_RS;
+  float* xs = sR + wave * 16 * XS;
 #pragma unroll
   for (int q = 0; q < XLD; ++q) {
     const int m = q * RPL + lane / LPR;
@@ -597,7 +601,7 @@ __global__ __launch_bounds__(DEC_THREADS, 1) void k_linear_w4_decode_tiled(
     }
 #pragma unroll
     for (int u = 0; u < EPL; u += 4)
-      *reinterpret_cast<f32x4*>(xs + m * DEC_RS + c + u) = f32x4{v[u], v[u + 1], v[u + 2], v[u + 3]};
+      *reinterpret_cast<f32x4*>(xs + m * XS + c + u) = f32x4{v[u], v[u + 1], v[u + 2], v[u + 3]};
   }
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
   __builtin_amdgcn_wave_barrier();
@@ -607,7 +611,7 @@ __global__ __launch_bounds__(DEC_THREADS, 1) void k_linear_w4_decode_tiled(
   for (int st = 0; st < STEPS; ++st)
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
-      const f32x4 t = *reinterpret_cast<const f32x4*>(xs + j * DEC_RS + 32 * st + 8 * g + 4 * h);
+      const f32x4 t = *reinterpret_cast<const f32x4*>(xs + j * XS + 32 * st + 8 * g + 4 * h);
 #pragma unroll
       for (int u = 0; u < 4; ++u) xv[8 * st + 4 * h + u] = t[u];
     }
@@ -694,7 +698,7 @@ __global__ __launch_bounds__(DEC_THREADS, 1) void k_linear_w4_decode_tiled(
 
   // ---- wave partial (rows 4g+i, columns 8j+t) into its own slot: no
   // barrier first, nothing else uses the slot
-  float* rwv = sR + wave * 16 * DEC_RS;
+  float* rwv = sR + wave * 16 * XS;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int sh = -sXe[wave * 16 + 4 * g + i] - se;
@@ -703,7 +707,7 @@ __global__ __launch_bounds__(DEC_THREADS, 1) void k_linear_w4_decode_tiled(
     for (int t = 0; t < 8; ++t)
       v[t] = (t & 1) ? __builtin_ldexpf(acc[t][i] - corr[i], 20 + sh)
                      : __builtin_ldexpf(acc[t][i] - corr[i] * 0.0625f, 24 + sh);
-    float* dst = rwv + (4 * g + i) * DEC_RS + 8 * j;
+    float* dst = rwv + (4 * g + i) * XS + 8 * j;
     *reinterpret_cast<f32x4*>(dst) = f32x4{v[0], v[1], v[2], v[3]};
     *reinterpret_cast<f32x4*>(dst + 4) = f32x4{v[4], v[5], v[6], v[7]};
   }
@@ -715,9 +719,9 @@ __global__ __launch_bounds__(DEC_THREADS, 1) void k_linear_w4_decode_tiled(
   f32x4 sum[CPT / 4];
 #pragma unroll
   for (int h = 0; h < CPT / 4; ++h) {
-    sum[h] = *reinterpret_cast<const f32x4*>(sR + m * DEC_RS + c + 4 * h);
+    sum[h] = *reinterpret_cast<const f32x4*>(sR + m * XS + c + 4 * h);
 #pragma unroll
-    for (int q = 1; q < DEC_WAVES; ++q) sum[h] += *reinterpret_cast<const f32x4*>(sR + (q * 16 + m) * DEC_RS + c + 4 * h);
+    for (int q = 1; q < W; ++q) sum[h] += *reinterpret_cast<const f32x4*>(sR + (q * 16 + m) * XS + c + 4 * h);
   }
   const int64_t col = nb * 128 + c;
   if (S == 1) {
@@ -1200,7 +1204,11 @@ static void launch_decode(const DecodePlan& p, hipStream_t st, const void* x, in
 }
 
 // The tiled kernel: one block per workgroup, the longest waves that still
-// give every CU a workgroup, else the shape with the most workgroups.
+// give every CU a workgroup, else the shape with the most workgroups.  Waves
+// of 8 steps come 8 to a workgroup (two per SIMD, 169 VGPRs), shorter ones 16.
+static int tiled_waves(int steps) { return steps == 8 ? 8 : 16; }
+static int64_t tiled_rows(int steps) { return (int64_t)tiled_waves(steps) * 32 * steps; }
+
 static DecodePlan plan_decode_tiled(int64_t K, int64_t N) {
   DecodePlan p;
   const int64_t NB = N / 128;
@@ -1208,8 +1216,8 @@ static DecodePlan plan_decode_tiled(int64_t K, int64_t N) {
   p.nbw = 1;
   p.steps = 1;
   int64_t best = -1;
-  for (const int steps : {4, 2, 1}) {
-    const int64_t S = ceil_div(K, dec_rows(1, steps));
+  for (const int steps : {8, 2, 1}) {
+    const int64_t S = ceil_div(K, tiled_rows(steps));
     if (S > 255) continue;  // 8-bit arrival counts per XCC
     const int64_t grid = NB * S;
     if (grid > best) {
@@ -1221,7 +1229,7 @@ static DecodePlan plan_decode_tiled(int64_t K, int64_t N) {
       break;
     }
   }
-  p.S = (int)ceil_div(K, dec_rows(1, p.steps));
+  p.S = (int)ceil_div(K, tiled_rows(p.steps));
   p.xcd_map = NB % 8 == 0 ? 1 : 0;
   p.partial_bytes = p.S > 1 ? (((size_t)p.S * (size_t)NB * 8192 + 255) & ~(size_t)255) : 0;
   p.counter_bytes = DEC_COUNTER_BYTES;
@@ -1234,15 +1242,15 @@ static void launch_decode_tiled(const DecodePlan& p, hipStream_t st, const void*
                                 const uint32_t* wt, const float* scales_t, const float* bias, float* out,
                                 float* partials, unsigned long long* counters) {
   const dim3 grid((unsigned)((N / 128) * p.S));
-#define MXK_DECT(STEPS)                                                                                  \
-  if (p.steps == STEPS) {                                                                               \
-    hipLaunchKernelGGL((k_linear_w4_decode_tiled<T, STEPS>), grid, dim3(DEC_THREADS), 0, st, (const T*)x, \
-                       (int)M, K, N, wt, scales_t, bias, out, partials, counters, p.S, p.xcd_map);      \
-    return;                                                                                             \
+#define MXK_DECT(STEPS, W)                                                                                  \
+  if (p.steps == STEPS) {                                                                                  \
+    hipLaunchKernelGGL((k_linear_w4_decode_tiled<T, STEPS, W>), grid, dim3(W * 64), 0, st, (const T*)x,    \
+                       (int)M, K, N, wt, scales_t, bias, out, partials, counters, p.S, p.xcd_map);         \
+    return;                                                                                                \
   }
-  MXK_DECT(4)
-  MXK_DECT(2)
-  MXK_DECT(1)
+  MXK_DECT(8, 8)
+  MXK_DECT(2, 16)
+  MXK_DECT(1, 16)
 #undef MXK_DECT
 }
 
