@@ -7,7 +7,10 @@ weight-only linear at decode shape — x fp32 [16, 8192] ~ N(0,1), W
 [8192 (out), 8192 (in)] ~ 0.02 N(0,1) with 0.1% outliers x20, stored as
 quantize(W.t()) int4d block 128 — one step = one mx_linear forward (one
 fused kernel).  `value` = algorithmic bytes per step (packed weights 32 MiB +
-scales 2 MiB + x + y = 36,700,160 B) / time per step, in GB/s.
+scales 2 MiB + x + y = 36,700,160 B) / time per step, in GB/s.  The
+kernel reads the tiled copy of the packed weight (same 32 MiB) and the
+block-major scales that each layer makes once, on its first forward, before
+the timed region.
 
 Timing: W warm-up steps, then K steps captured into one HIP graph and
 replayed between two HIP events recorded on the stream the kernels run on
