@@ -31,7 +31,7 @@ __global__ __launch_bounds__(256) void k_kv_append(const T* __restrict__ k, cons
   constexpr uint32_t MASK = (1u << BITS) - 1u;
   constexpr int H = MODE == Q_FP ? (1 << (BITS - 1)) : 1;
   __shared__ float sP[H + 1];
-  if constexpr (MODE == Q_FP) build_tables<BITS>(sP, nullptr);
+  if constexpr (MODE == Q_FP && BITS != 4) build_tables<BITS>(sP, nullptr);  // FP4 buckets by constants
 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int g = lane / LPB, li = lane % LPB;

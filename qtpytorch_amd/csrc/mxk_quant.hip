@@ -78,7 +78,7 @@ __global__ __launch_bounds__(256) void k_quant_fast(const T* __restrict__ x, int
   constexpr uint32_t MASK = BITS == 32 ? 0xFFFFFFFFu : ((1u << BITS) - 1u);
   constexpr int H = MODE == Q_FP ? (1 << (BITS - 1)) : 1;
   __shared__ float sP[H + 1];
-  if constexpr (MODE == Q_FP) build_tables<BITS>(sP, nullptr);
+  if constexpr (MODE == Q_FP && BITS != 4) build_tables<BITS>(sP, nullptr);  // FP4 buckets by constants
 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int g = lane / LPB, li = lane % LPB;
@@ -149,7 +149,7 @@ __global__ __launch_bounds__(256) void k_quant_rows(const T* __restrict__ x, int
   constexpr int H = MODE == Q_FP ? (1 << (BITS - 1)) : 1;
   __shared__ float sP[H + 1];
   __shared__ float s_max[4];
-  if constexpr (MODE == Q_FP) build_tables<BITS>(sP, nullptr);
+  if constexpr (MODE == Q_FP && BITS != 4) build_tables<BITS>(sP, nullptr);  // FP4 buckets by constants
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int chunks = block / 8;
   for (int64_t blk = blockIdx.x; blk < nb; blk += gridDim.x) {
@@ -226,7 +226,7 @@ __global__ __launch_bounds__(256) void k_pack_generic(const T* __restrict__ x, i
                                                       int64_t packed_nbytes) {
   constexpr int H = MODE == Q_FP ? (1 << (BITS - 1)) : 1;
   __shared__ float sP[H + 1];
-  if constexpr (MODE == Q_FP) build_tables<BITS>(sP, nullptr);
+  if constexpr (MODE == Q_FP && BITS != 4) build_tables<BITS>(sP, nullptr);  // FP4 buckets by constants
   const bool words = !(bits == 1 || bits == 2 || bits == 4 || bits == 8);
   const int per = words ? 32 / bits : 8 / bits;
   const int64_t units = words ? packed_nbytes / 4 : packed_nbytes;
@@ -327,7 +327,7 @@ __global__ __launch_bounds__(256) void k_quant_had128(const T* __restrict__ x, i
   constexpr int H = MODE == Q_FP ? (1 << (BITS - 1)) : 1;
   __shared__ float sP[H + 1];
   __shared__ __attribute__((aligned(16))) float srow[GPB * MXK_ROWPAD];
-  if constexpr (MODE == Q_FP) build_tables<BITS>(sP, nullptr);
+  if constexpr (MODE == Q_FP && BITS != 4) build_tables<BITS>(sP, nullptr);  // FP4 buckets by constants
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int g = lane / LPB, li = lane % LPB;
   float* row = srow + (wave * GPW + g) * MXK_ROWPAD;
@@ -694,6 +694,32 @@ static int grid_for(int64_t work_items, int per_block) {
   return (int)std::max<int64_t>(1, std::min<int64_t>(blocks, cap));
 }
 
+// Workgroups for a streaming kernel: one per `per_block` items, at most
+// cap_per_cu per CU (0: no cap, every workgroup makes one pass of the
+// grid-stride loop).  Measured at 2^28 elements (outputs identical at every
+// setting): the light integer quantizers from fp32 stream best uncapped
+// (int8d 0.69 -> 0.81 of 8 TB/s), kernels with per-workgroup setup (LDS
+// tables) or heavy per-element work at 32-128 per CU.
+static int grid_capped(int64_t work_items, int per_block, int cap_per_cu) {
+  const int64_t blocks = std::max<int64_t>(1, ceil_div(work_items, per_block));
+  if (cap_per_cu <= 0) return (int)std::min<int64_t>(blocks, (int64_t)0x7FFFFFFF);
+  return (int)std::min<int64_t>(blocks, (int64_t)num_cus() * cap_per_cu);
+}
+// k_quant_fast: fp32 int codes uncapped; 16-bit int codes 128; 'v' from
+// 16-bit 32; float codes and the rest 64.
+template <typename T, int MODE>
+constexpr int quant_fast_cap() {
+  return (sizeof(T) == 4 && (MODE == Q_INT || MODE == Q_INT1)) ? 0
+         : (sizeof(T) == 2 && (MODE == Q_INT || MODE == Q_INT1)) ? 128
+         : (sizeof(T) == 2 && MODE == Q_VEC) ? 32 : 64;
+}
+// k_dequant_fast: codes decoded without a table (int8, FP8) uncapped; the
+// LDS-table widths (int 1-4 bits, FP4) 64.
+template <int MODE, int BITS>
+constexpr int dequant_fast_cap() {
+  return (MODE == Q_INT || MODE == Q_FP) && BITS == 8 ? 0 : 64;
+}
+
 // mx_dtype.max_val (mxtorch.py:509-523): q for int widths (1 for int1),
 // the format maximum for float widths.  Only the 'v' rule uses it for
 // float dtypes.
@@ -720,7 +746,7 @@ static void launch_fast_b(const T* x, int64_t n, int64_t nb, int block, uint8_t*
   auto go = [&](auto lpb_tag) {
     constexpr int LPB = decltype(lpb_tag)::value;
     constexpr int GPB = 4 * (64 / LPB);
-    hipLaunchKernelGGL((k_quant_fast<T, E, LPB, MODE, BITS>), dim3(grid_for(nb, GPB)), dim3(256), 0, st, x, n, nb,
+    hipLaunchKernelGGL((k_quant_fast<T, E, LPB, MODE, BITS>), dim3(grid_capped(nb, GPB, quant_fast_cap<T, MODE>())), dim3(256), 0, st, x, n, nb,
                        packed, pbytes, n_store, scales, qf);
     *done = true;
   };
@@ -847,7 +873,7 @@ static bool try_had128(const T* x, int64_t n, int mode, int bits, const float* s
                        int64_t pbytes, int64_t n_store, float* scales, float qf, hipStream_t st) {
   if (!aligned16(x)) return false;
   const int64_t nb = ceil_div(n, 128);
-  const int grid = grid_for(nb, 32);
+  const int grid = grid_capped(nb, 32, 128);
 #define MXK_HAD_CASE(MODE, BITS)                                                                               \
   if (mode == MODE && bits == BITS) {                                                                          \
     hipLaunchKernelGGL((k_quant_had128<T, MODE, BITS>), dim3(grid), dim3(256), 0, st, x, n, nb, signs, packed, \
@@ -907,7 +933,7 @@ static int launch_dequant(const void* packed, int64_t pbytes, const float* scale
     if (block % 4 == 0 && (reinterpret_cast<uintptr_t>(packed) & 3u) == 0 &&
         (reinterpret_cast<uintptr_t>(out) & 15u) == 0) {
       const int64_t slots = ceil_div(n, 4);
-      const int grid = (int)std::max<int64_t>(1, std::min<int64_t>(ceil_div(slots, 256 * 4), (int64_t)num_cus() * 8));
+      const int grid = grid_capped(slots, 256 * 4, dequant_fast_cap<MODE, BITS>());
       hipLaunchKernelGGL((k_dequant_fast<MODE, BITS>), dim3(grid), dim3(256), 0, st,
                          reinterpret_cast<const uint8_t*>(packed), pbytes, scales, nb, n, block, out);
       return check_launch("dequantize");
