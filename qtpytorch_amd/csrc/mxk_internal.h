@@ -310,7 +310,7 @@ __device__ __forceinline__ int encode(float v, const BlockParams& bp, float qf, 
     // pattern minus that of 1.5 * 2^23 (one add and one subtract in place
     // of a round and a conversion; callers that mask the low bits lose the
     // subtract)
-    const float t = fminf(fmaxf(v * bp.mul, -qf), qf);
+    const float t = __builtin_amdgcn_fmed3f(v * bp.mul, -qf, qf);  // the clamp, one instruction
     return (int)(__float_as_uint(t + 12582912.0f) - 0x4B400000u);
   } else if constexpr (MODE == Q_INT1) {
     return v >= 0.0f ? 0 : 1;

@@ -488,10 +488,13 @@ def dynamic_quantize(x: Tensor, dtype="int8d", granularity: str = "per_token", b
     shape = x.shape
     packed, scales, (rows, cols) = ops.dynamic_quantize(x, dt, granularity)
     n = rows * cols
+    # The reference builds the 2-D mx_tensor and reshapes it to x's shape,
+    # which clones the codes it has just made; the fresh buffers are handed
+    # over directly here (same shape, block and values, no copy).
     if granularity == "per_token":
-        return mx_tensor(packed, scales, dt, torch.Size([rows, cols]), n, cols).reshape(*shape)
+        return mx_tensor(packed, scales, dt, torch.Size(shape), n, cols)
     if granularity == "per_channel":
-        return mx_tensor(packed, scales, dt, torch.Size([rows, cols]), n, rows).reshape(*shape)
+        return mx_tensor(packed, scales, dt, torch.Size(shape), n, rows)
     return mx_tensor(packed, scales, dt, torch.Size(shape), n, n)
 
 
