@@ -83,44 +83,60 @@ __global__ __launch_bounds__(256) void k_kv_append(const T* __restrict__ k, cons
 // tiles on grid-y, both looped): each thread writes float4s (4 codes, read
 // from the 32-bit word holding them); a tile reads KV_RT consecutive rows of
 // each of its slots and writes KV_RT runs of KV_JT * D contiguous floats.
+// D = 4 << LQ.  A thread issues the loads of all its IT items of a tile
+// (code word, scale, zero point) before it decodes and stores any of them.
 // rows * D * BITS < 2^35 and T < 2^31 (host-checked).
 #define KV_RT 4
 #define KV_JT 8
-template <int MODE, int BITS>
+template <int MODE, int BITS, int LQ>
 __global__ __launch_bounds__(256) void k_kv_gather(const uint8_t* __restrict__ codes, const float* __restrict__ scales,
-                                                   const float* __restrict__ zp, int64_t rows, int D, int64_t cap,
+                                                   const float* __restrict__ zp, int64_t rows, int64_t cap,
                                                    int64_t start, int64_t T, float* __restrict__ out) {
   constexpr int H = (MODE == Q_FP && BITS == 4) ? 16 : 1;
+  constexpr int QPR = 1 << LQ;            // float4s per (row, step): 16, 32 or 64
+  constexpr int LJQ = LQ + 3;             // log2(KV_JT * QPR)
+  constexpr int IT = KV_RT * KV_JT * QPR / 256;
+  constexpr int D = 4 * QPR;
   __shared__ float sG[H];
   if constexpr (MODE == Q_FP && BITS == 4) build_tables<4>(nullptr, sG);
-  const uint32_t qpr = (uint32_t)D / 4;  // float4s per (row, step): 16, 32 or 64
-  const int lq = 31 - __builtin_clz(qpr);
-  const int ljq = lq + 3;                // log2(KV_JT * qpr)
-  const uint32_t tile = KV_RT * KV_JT * qpr;
-  const int64_t row_bytes = (int64_t)D * BITS / 8, slot_bytes = rows * row_bytes;
+  const int64_t slot_bytes = rows * (D * BITS / 8);
   const int64_t ntr = (rows + KV_RT - 1) / KV_RT, ntj = (T + KV_JT - 1) / KV_JT;
   for (int64_t tj = blockIdx.y; tj < ntj; tj += gridDim.y) {
     for (int64_t tr = blockIdx.x; tr < ntr; tr += gridDim.x) {
-      for (uint32_t t = threadIdx.x; t < tile; t += blockDim.x) {
-        const uint32_t rr = t >> ljq, jj = (t >> lq) & (KV_JT - 1), q = t & (qpr - 1);
+      uint32_t word[IT];
+      float s[IT], z[IT];
+      int64_t dst[IT];
+#pragma unroll
+      for (int it = 0; it < IT; ++it) {
+        const uint32_t t = threadIdx.x + 256u * it;
+        const uint32_t rr = t >> LJQ, jj = (t >> LQ) & (KV_JT - 1), q = t & (QPR - 1);
         const int64_t r = tr * KV_RT + rr, j = tj * KV_JT + jj;
-        if (r >= rows || j >= T) continue;
-        int64_t slot = start + j;
-        if (slot >= cap) slot -= cap;
-        const int64_t bit0 = ((int64_t)r * D + 4 * q) * BITS;
-        const uint32_t word = *reinterpret_cast<const uint32_t*>(codes + slot * slot_bytes + (bit0 >> 5) * 4);
-        const int sh0 = (int)(bit0 & 31);
-        const float s = scales[slot * rows + r];
+        word[it] = 0u;
+        s[it] = 0.0f;
+        z[it] = 0.0f;
+        dst[it] = -1;
+        if (r < rows && j < T) {
+          int64_t slot = start + j;
+          if (slot >= cap) slot -= cap;
+          const int64_t bit0 = ((int64_t)r * D + 4 * q) * BITS;
+          word[it] = *reinterpret_cast<const uint32_t*>(codes + slot * slot_bytes + (bit0 >> 5) * 4);
+          s[it] = scales[slot * rows + r];
+          if (zp) z[it] = zp[slot * rows + r];
+          dst[it] = ((r * T + j) << (LQ + 2)) + q * 4;
+        }
+      }
+#pragma unroll
+      for (int it = 0; it < IT; ++it) {
+        if (dst[it] < 0) continue;
+        const int sh0 = (int)((((threadIdx.x + 256u * it) & (QPR - 1)) * 4 * BITS) & 31);
         float o[4];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) o[e] = decode_field<MODE, BITS>(word, sh0 + e * BITS, s, sG);
+        for (int e = 0; e < 4; ++e) o[e] = decode_field<MODE, BITS>(word[it], sh0 + e * BITS, s[it], sG);
         if (zp) {
-          const float z = zp[slot * rows + r];
 #pragma unroll
-          for (int e = 0; e < 4; ++e) o[e] = o[e] + z;
+          for (int e = 0; e < 4; ++e) o[e] = o[e] + z[it];
         }
-        __builtin_nontemporal_store(f32x4v{o[0], o[1], o[2], o[3]},
-                                    reinterpret_cast<f32x4v*>(out + ((r * T + j) << (lq + 2)) + q * 4));
+        __builtin_nontemporal_store(f32x4v{o[0], o[1], o[2], o[3]}, reinterpret_cast<f32x4v*>(out + dst[it]));
       }
     }
   }
@@ -233,8 +249,17 @@ int mxk_kv_gather(const void* codes, const float* scales, const float* zero_poin
   const dim3 grid((unsigned)std::min<int64_t>(ceil_div(rows, KV_RT), 65535),
                   (unsigned)std::min<int64_t>(ceil_div(count, KV_JT), 65535));
 #define MXK_KVG(MODE, BITS)                                                                                       \
-  hipLaunchKernelGGL((k_kv_gather<MODE, BITS>), grid, dim3(256), 0, st, c, scales, zero_point, rows, head_dim, \
-                     capacity, start, count, out)
+  do {                                                                                                            \
+    if (head_dim == 64)                                                                                           \
+      hipLaunchKernelGGL((k_kv_gather<MODE, BITS, 4>), grid, dim3(256), 0, st, c, scales, zero_point, rows,     \
+                         capacity, start, count, out);                                                            \
+    else if (head_dim == 128)                                                                                     \
+      hipLaunchKernelGGL((k_kv_gather<MODE, BITS, 5>), grid, dim3(256), 0, st, c, scales, zero_point, rows,     \
+                         capacity, start, count, out);                                                            \
+    else                                                                                                          \
+      hipLaunchKernelGGL((k_kv_gather<MODE, BITS, 6>), grid, dim3(256), 0, st, c, scales, zero_point, rows,     \
+                         capacity, start, count, out);                                                            \
+  } while (0)
   if (mode == Q_FP) {
     if (bits == 4) MXK_KVG(Q_FP, 4);
     else MXK_KVG(Q_FP, 8);
