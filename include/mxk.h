@@ -36,7 +36,7 @@
 extern "C" {
 #endif
 
-#define MXK_ABI_VERSION 5
+#define MXK_ABI_VERSION 6
 
 typedef enum {
   MXK_OK = 0,
@@ -292,6 +292,33 @@ int mxk_linear_wq_nt(const void* x, int x_type, int64_t M, int64_t K, const void
  * and every call leaves the counters zero again.  Calls sharing a workspace
  * must not overlap. */
 size_t mxk_linear_nt_workspace(int64_t M, int64_t K, int64_t N, int bits, int block);
+
+/* Tiled copy of an int4 [N][K] weight for mxk_linear_wq_nt_tiled: w_packed
+ * is the packing of quantize(weight) of mx_dynamic_linear
+ * (mxtorch.py:8870-8968, flat blocks of 128 along K), bits 4, block 128, K
+ * and N multiples of 128; w_tiled receives the same N*K/2 bytes reordered so
+ * that each 16-row tile of a K block is 1 KiB contiguous and every MFMA
+ * operand comes out of its words with masks (no byte permutes).  No
+ * reference counterpart: the reference dequantizes the weight instead
+ * (mxtorch.py:8949-8962).  Weights are static, so callers make this copy
+ * once per weight.  w_packed and w_tiled 16-byte aligned. */
+int mxk_linear_prepack_weight_nt(const void* w_packed, int64_t N, int64_t K, int bits, int block, void* w_tiled,
+                                 void* stream);
+
+/* mx_dynamic_linear.forward (mxtorch.py:8949-8962) for int4 weights, block
+ * 128, from the prepacked copies: out[M,N] = x[M,K] @ dequant(W)^T (+ bias),
+ * the product of mxk_linear_wq_nt's decode path, float32 accumulation in
+ * another order.  w_tiled = mxk_linear_prepack_weight_nt(), w_scales_t =
+ * the K-block-major scales [K/128][N] (mxk_linear_prepack_scales(w_scales,
+ * N, K, 128, w_scales_t)).  Takes M <= 16, K and N multiples of 128, 16-byte
+ * aligned x, w_tiled, w_scales_t, bias and out; other shapes return
+ * MXK_EUNSUPPORTED (call mxk_linear_wq_nt).  workspace: as for
+ * mxk_linear_wq_nt (mxk_linear_nt_workspace() bytes, zero-filled before
+ * first use, left ready for the next call; calls sharing it must not
+ * overlap). */
+int mxk_linear_wq_nt_tiled(const void* x, int x_type, int64_t M, int64_t K, const void* w_tiled,
+                           const float* w_scales_t, int64_t N, const float* bias, float* out, void* workspace,
+                           size_t workspace_nbytes, void* stream);
 
 /* Workspace bytes mxk_linear_i8 needs (0 when the shapes are not covered). */
 size_t mxk_linear_i8_workspace(int64_t M, int64_t K, int64_t N, int x_bits, int w_bits, int64_t x_block,

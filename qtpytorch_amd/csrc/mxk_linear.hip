@@ -1096,6 +1096,367 @@ __global__ __launch_bounds__(NT_THREADS, 1) void k_linear_w4t_decode(
   if (threadIdx.x == 0) __hip_atomic_store(counters + cg, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// ---------------------------------------------------------------- int4 decode, [N][K] weight, long waves
+// The product of k_linear_w4t_decode with the work split of
+// k_linear_w4_decode_tiled: one 128-column block (rows n0 .. n0+127 of W) per
+// workgroup, W waves of KBW = 4 * STEPS / 16 blocks of K each (STEPS steps of
+// 32 rows), so K splits S = ceil(K / (W * 32 * STEPS)) ways.  Each wave reads
+// its own x rows row-contiguously, turns them into the A-fragment order of
+// k_linear_w4t_decode through its own LDS slot (lane (j, g) of step st of
+// block b: row j, codes 128 b + 32 g + 8 st .. +7), scales each row's
+// largest |x| of the wave into [2^14, 2^15) (the power of two returns in the
+// epilogue), and only then requests its scales and weights, so that x is not
+// queued behind them.  Tile t of block b: lane (j, g) loads the 16 bytes at
+// byte 64 b + 16 g of row n0 + 16 t + j (codes 128 b + 32 g .. +31), as
+// stored (the B operand and the correction tile of k_linear_w4t_decode), or
+// (TILED) the same codes from the tiled copy of mxk_linear_prepack_weight_nt,
+// where the 16 lanes of a tile read 1 KiB contiguously and every B operand
+// comes out of the words with masks (k_tile_w4t).  Each block's tile sums are
+// scaled by that block's scale of the column before they are added.  The
+// partial reduction and the split-K hand-off are those of
+// k_linear_w4_decode_tiled.
+template <typename T, int STEPS, int W, bool TILED>
+__global__ __launch_bounds__(W * 64, 1) void k_linear_w4t_decode_long(
+    const T* __restrict__ x, int M, int64_t K, int64_t N, const uint8_t* __restrict__ w,
+    const float* __restrict__ scales, int scales_kb_major, const float* __restrict__ bias, float* __restrict__ out,
+    float* __restrict__ partials, unsigned long long* __restrict__ counters, int S, int xcd_map) {
+  constexpr int RPW = 32 * STEPS, R = W * RPW, KBW = RPW / 128;
+  constexpr int TPB = W * 64 > 512 ? 512 : W * 64, RT = TPB, CPT = 2048 / TPB;
+  constexpr int XS = RPW + 4;                // row stride of a wave's LDS slot (floats)
+  constexpr int EPL = 16 / (int)sizeof(T);   // x elements per 16-byte load
+  constexpr int LPR = RPW / EPL;             // lanes per x row in one load
+  constexpr int RPL = 64 / LPR;              // x rows per load
+  constexpr int XLD = 16 / RPL;              // x loads per lane
+  static_assert(RPW % 128 == 0 && LPR >= 1 && RPL * LPR == 64 && XLD * RPL == 16, "x loads");
+  static_assert(XS >= DEC_RS, "a wave's slot holds its partial");
+  static_assert(CPT % 4 == 0 && TPB * CPT == 2048, "reduction split");
+  __shared__ __attribute__((aligned(16))) float sR[W * 16 * XS];
+  __shared__ int sXe[W * 16];
+  __shared__ int s_flags;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int j = lane & 15, g = lane >> 4;
+  const int64_t NB = N / 128, KB = K / 128;
+  int64_t nb;
+  int ks;
+  if (xcd_map) {
+    const int i = (int)(blockIdx.x >> 3);
+    nb = (int64_t)(i / S) * 8 + (blockIdx.x & 7);
+    ks = i % S;
+  } else {
+    nb = blockIdx.x / S;
+    ks = blockIdx.x % S;
+  }
+  const int64_t kw = (int64_t)ks * R + (int64_t)wave * RPW;  // this wave's first row of K
+  const int64_t n0 = nb * 128;
+
+  // ---- x rows of this wave
+  const __amdgpu_buffer_rsrc_t rx = make_rsrc(x, (uint32_t)((int64_t)M * K * sizeof(T)));
+  u32x4 xr[XLD];
+#pragma unroll
+  for (int q = 0; q < XLD; ++q) {
+    const int m = q * RPL + lane / LPR;
+    const int64_t kk = kw + (int64_t)EPL * (lane % LPR);
+    const bool ok = m < M && kk < K;  // K % 128 == 0: a load is wholly in or out
+    xr[q] = buf_load_b128(rx, ok ? (uint32_t)(((int64_t)m * K + kk) * sizeof(T)) : DEC_OOB, 0u);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+
+  float* xs = sR + wave * 16 * XS;
+#pragma unroll
+  for (int q = 0; q < XLD; ++q) {
+    const int m = q * RPL + lane / LPR;
+    const int c = EPL * (lane % LPR);
+    float v[EPL];
+    if constexpr (EPL == 4) {
+#pragma unroll
+      for (int u = 0; u < 4; ++u) v[u] = __uint_as_float(xr[q][u]);
+    } else {
+      const T* tt = reinterpret_cast<const T*>(&xr[q]);
+#pragma unroll
+      for (int u = 0; u < EPL; ++u) v[u] = ElemT<T>::cvt(tt[u]);
+    }
+#pragma unroll
+    for (int u = 0; u < EPL; u += 4)
+      *reinterpret_cast<f32x4*>(xs + m * XS + c + u) = f32x4{v[u], v[u + 1], v[u + 2], v[u + 3]};
+  }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  // xv[8 (4 b + st) + e]: row j, codes 128 b + 32 g + 8 st + e of the wave's rows
+  float xv[STEPS * 8];
+#pragma unroll
+  for (int b = 0; b < KBW; ++b)
+#pragma unroll
+    for (int st = 0; st < 4; ++st)
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const f32x4 t = *reinterpret_cast<const f32x4*>(xs + j * XS + 128 * b + 32 * g + 8 * st + 4 * h);
+#pragma unroll
+        for (int u = 0; u < 4; ++u) xv[8 * (4 * b + st) + 4 * h + u] = t[u];
+      }
+  float mx = 0.0f;
+#pragma unroll
+  for (int u = 0; u < STEPS * 8; ++u) mx = fmaxf(mx, __builtin_fabsf(xv[u]));
+  // row j sits in lanes j, j + 16, j + 32, j + 48
+  mx = fmaxf(mx, __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(mx), 0x401F)));
+  mx = fmaxf(mx, __shfl_xor(mx, 32));
+  const int be = (int)((__float_as_uint(mx) >> 23) & 0xFFu);
+  const int xe = be == 0xFF ? 0 : 141 - (be == 0 ? 1 : be);  // largest |x| to [2^14, 2^15); zero rows: any
+  f16x8 ahi[STEPS], alo[STEPS];
+#pragma unroll
+  for (int s8 = 0; s8 < STEPS; ++s8) {
+    uint32_t hw[4], lw[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float a = __builtin_ldexpf(xv[8 * s8 + 2 * e], xe), b = __builtin_ldexpf(xv[8 * s8 + 2 * e + 1], xe);
+      auto hp = __builtin_amdgcn_cvt_pkrtz(a, b);
+      auto lp = __builtin_amdgcn_cvt_pkrtz(a - (float)hp[0], b - (float)hp[1]);
+      hw[e] = __builtin_bit_cast(uint32_t, hp);
+      lw[e] = __builtin_bit_cast(uint32_t, lp);
+    }
+    ahi[s8] = __builtin_bit_cast(f16x8, u32x4v{hw[0], hw[1], hw[2], hw[3]});
+    alo[s8] = __builtin_bit_cast(f16x8, u32x4v{lw[0], lw[1], lw[2], lw[3]});
+  }
+  if (g == 0) sXe[wave * 16 + j] = xe;
+
+  // ---- scales and weights, requested once this wave's x is in.  A block
+  // past K (only in the last split) re-reads block 0; its x rows are zeros.
+  const __amdgpu_buffer_rsrc_t rw = make_rsrc(w, (uint32_t)(N * K / 2));
+  const __amdgpu_buffer_rsrc_t rs = make_rsrc(scales, (uint32_t)(N * KB * 4));
+  float sc[KBW][8];
+  u32x4 wv[KBW][8];
+#pragma unroll
+  for (int b = 0; b < KBW; ++b) {
+    const int64_t kb0 = kw / 128 + b;
+    const int64_t kb = kb0 < KB ? kb0 : 0;  // wave-uniform
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+      const int64_t n = n0 + 16 * t + j;
+      const int64_t si = scales_kb_major ? kb * N + n : n * KB + kb;
+      sc[b][t] = __uint_as_float(buf_load_b32(rs, (uint32_t)(si * 4), 0u));
+    }
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+      if constexpr (TILED)
+        wv[b][t] = buf_load_b128(rw, 16u * lane, (uint32_t)(((nb * 8 + t) * KB + kb) * 1024));
+      else
+        wv[b][t] = buf_load_b128(rw, (uint32_t)((n0 + 16 * t + j) * (K / 2) + 16 * g), (uint32_t)(kb * 64));
+    }
+  }
+  __builtin_amdgcn_sched_barrier(0);
+
+  // ---- MFMA per block and tile; each block's sums scaled by its column scale
+  f32x4 res[8];
+#pragma unroll
+  for (int t = 0; t < 8; ++t) res[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+  if constexpr (TILED) {
+    // steps 0 and 2 from the low nibbles (code + 8) * 2^-24, steps 1 and 3
+    // from the high nibbles (code + 8) * 2^-20, summed apart: word 2 sp + h,
+    // byte q holds codes (step 2 sp, i) | (step 2 sp + 1, i) << 4 with
+    // i = 4 h + {0, 2, 1, 3}[q], so (w & 0x000F000F) and ((w >> 8) &
+    // 0x000F000F) are the f16 pairs (i, i + 1) of the low step, the masks
+    // 0x00F000F0 those of the high step
+    const f16x8 bl = __builtin_bit_cast(f16x8, u32x4v{0x00080008u, 0x00080008u, 0x00080008u, 0x00080008u});
+    const f16x8 bh = __builtin_bit_cast(f16x8, u32x4v{0x00800080u, 0x00800080u, 0x00800080u, 0x00800080u});
+#pragma unroll
+    for (int b = 0; b < KBW; ++b) {
+      f32x4 corl = f32x4{0.f, 0.f, 0.f, 0.f}, corh = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int sp = 0; sp < 2; ++sp) {
+        corl = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi[4 * b + 2 * sp], bl, corl, 0, 0, 0);
+        corl = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo[4 * b + 2 * sp], bl, corl, 0, 0, 0);
+        corh = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi[4 * b + 2 * sp + 1], bh, corh, 0, 0, 0);
+        corh = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo[4 * b + 2 * sp + 1], bh, corh, 0, 0, 0);
+      }
+#pragma unroll
+      for (int t = 0; t < 8; ++t) {
+        f32x4 accl = f32x4{0.f, 0.f, 0.f, 0.f}, acch = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int sp = 0; sp < 2; ++sp) {
+          const uint32_t w0 = wv[b][t][2 * sp], w1 = wv[b][t][2 * sp + 1];
+          const uint32_t s0 = w0 >> 8, s1 = w1 >> 8;
+          const f16x8 btl = __builtin_bit_cast(
+              f16x8, u32x4v{(w0 & 0x000F000Fu) ^ 0x00080008u, (s0 & 0x000F000Fu) ^ 0x00080008u,
+                            (w1 & 0x000F000Fu) ^ 0x00080008u, (s1 & 0x000F000Fu) ^ 0x00080008u});
+          const f16x8 bth = __builtin_bit_cast(
+              f16x8, u32x4v{(w0 & 0x00F000F0u) ^ 0x00800080u, (s0 & 0x00F000F0u) ^ 0x00800080u,
+                            (w1 & 0x00F000F0u) ^ 0x00800080u, (s1 & 0x00F000F0u) ^ 0x00800080u});
+          accl = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi[4 * b + 2 * sp], btl, accl, 0, 0, 0);
+          accl = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo[4 * b + 2 * sp], btl, accl, 0, 0, 0);
+          acch = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi[4 * b + 2 * sp + 1], bth, acch, 0, 0, 0);
+          acch = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo[4 * b + 2 * sp + 1], bth, acch, 0, 0, 0);
+        }
+        const float sf = sc[b][t] * 16777216.0f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) res[t][i] += sf * ((accl[i] - corl[i]) + (acch[i] - corh[i]) * 0.0625f);
+      }
+    }
+  } else {
+    const f16x8 b8 = __builtin_bit_cast(f16x8, u32x4v{0x00080008u, 0x00080008u, 0x00080008u, 0x00080008u});
+#pragma unroll
+    for (int b = 0; b < KBW; ++b) {
+      f32x4 corr = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int st = 0; st < 4; ++st) {
+        corr = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi[4 * b + st], b8, corr, 0, 0, 0);
+        corr = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo[4 * b + st], b8, corr, 0, 0, 0);
+      }
+#pragma unroll
+      for (int t = 0; t < 8; ++t) {
+        f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int st = 0; st < 4; ++st) {
+          const uint32_t wd = wv[b][t][st];
+          const uint32_t lo = (wd & 0x0F0F0F0Fu) ^ 0x08080808u;
+          const uint32_t hi = ((wd >> 4) & 0x0F0F0F0Fu) ^ 0x08080808u;
+          const uint32_t d0 = __builtin_amdgcn_perm(hi, lo, 0x0C040C00u);
+          const uint32_t d1 = __builtin_amdgcn_perm(hi, lo, 0x0C050C01u);
+          const uint32_t d2 = __builtin_amdgcn_perm(hi, lo, 0x0C060C02u);
+          const uint32_t d3 = __builtin_amdgcn_perm(hi, lo, 0x0C070C03u);
+          const f16x8 bt = __builtin_bit_cast(f16x8, u32x4v{d0, d1, d2, d3});
+          acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi[4 * b + st], bt, acc, 0, 0, 0);
+          acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo[4 * b + st], bt, acc, 0, 0, 0);
+        }
+        const float sf = sc[b][t] * 16777216.0f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) res[t][i] += sf * (acc[i] - corr[i]);
+      }
+    }
+  }
+
+  // ---- wave partial (rows 4g+i, columns 16t+j) into its own slot: no
+  // barrier first, nothing else uses the slot
+  float* rwv = sR + wave * 16 * XS;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int sh = -sXe[wave * 16 + 4 * g + i];
+#pragma unroll
+    for (int t = 0; t < 8; ++t) rwv[(4 * g + i) * XS + 16 * t + j] = __builtin_ldexpf(res[t][i], sh);
+  }
+  __syncthreads();
+  // thread (< RT): row m, columns c .. c+CPT-1, summed over the waves in order
+  const bool rt = threadIdx.x < RT;
+  const int r = threadIdx.x % TPB;
+  const int m = r / (128 / CPT), c = CPT * (r % (128 / CPT));
+  f32x4 sum[CPT / 4];
+#pragma unroll
+  for (int h = 0; h < CPT / 4; ++h) {
+    sum[h] = *reinterpret_cast<const f32x4*>(sR + m * XS + c + 4 * h);
+#pragma unroll
+    for (int q = 1; q < W; ++q) sum[h] += *reinterpret_cast<const f32x4*>(sR + (q * 16 + m) * XS + c + 4 * h);
+  }
+  const int64_t col = nb * 128 + c;
+  if (S == 1) {
+    if (rt && m < M) {
+#pragma unroll
+      for (int h = 0; h < CPT / 4; ++h) {
+        f32x4 o = sum[h];
+        if (bias) o += *reinterpret_cast<const f32x4*>(bias + col + 4 * h);
+        *reinterpret_cast<f32x4*>(out + (int64_t)m * N + col + 4 * h) = o;
+      }
+    }
+    return;
+  }
+  // split-K hand-off as in k_linear_w4_decode: partials [S][N/128][16][128]
+  // written through, arrivals counted per XCC, the last arrival sums in
+  // split order
+  const __amdgpu_buffer_rsrc_t rp = make_rsrc(partials, (uint32_t)((int64_t)S * NB * 16 * 128 * 4));
+  const uint32_t poff = (uint32_t)(((nb * 16 + m) * 128 + c) * 4);
+  const uint32_t split_stride = (uint32_t)(NB * 16 * 128 * 4);
+  if (rt) {
+#pragma unroll
+    for (int h = 0; h < CPT / 4; ++h)
+      __builtin_amdgcn_raw_buffer_store_b128(sum[h], rp, poff + 16u * h, (uint32_t)ks * split_stride, 16);
+  }
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    unsigned xcc;
+    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
+    xcc &= 7u;
+    const unsigned long long inc = 1ull << (8 * xcc);
+    const unsigned long long now =
+        __hip_atomic_fetch_add(&counters[nb], inc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + inc;
+    unsigned total = 0;
+#pragma unroll
+    for (int q = 0; q < 8; ++q) total += (unsigned)((now >> (8 * q)) & 0xFFull);
+    const bool same = ((now >> (8 * xcc)) & 0xFFull) == (unsigned long long)S;
+    const bool last = total == (unsigned)S;
+    if (last) __hip_atomic_store(&counters[nb], 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    s_flags = (last ? 1 : 0) | (same ? 2 : 0);
+  }
+  __syncthreads();
+  const int fl = s_flags;
+  if (!(fl & 1) || !rt) return;
+  f32x4 tot[CPT / 4];
+  for (int sb = 0; sb < S; sb += 8) {
+    f32x4 part[8][CPT / 4];
+#pragma unroll
+    for (int u = 0; u < 8; ++u)
+#pragma unroll
+      for (int h = 0; h < CPT / 4; ++h) {
+        const bool ld = sb + u < S && sb + u != ks;
+        const uint32_t soff = ld ? (uint32_t)(sb + u) * split_stride : 0u;
+        if (!ld)
+          part[u][h] = sum[h];
+        else if (fl & 2)
+          part[u][h] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rp, poff + 16u * h, soff, 1));
+        else
+          part[u][h] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rp, poff + 16u * h, soff, 16));
+      }
+#pragma unroll
+    for (int u = 0; u < 8; ++u)
+      if (sb + u < S)
+#pragma unroll
+        for (int h = 0; h < CPT / 4; ++h) tot[h] = (sb + u == 0) ? part[u][h] : tot[h] + part[u][h];
+  }
+  if (m < M) {
+#pragma unroll
+    for (int h = 0; h < CPT / 4; ++h) {
+      f32x4 o = tot[h];
+      if (bias) o += *reinterpret_cast<const f32x4*>(bias + col + 4 * h);
+      *reinterpret_cast<f32x4*>(out + (int64_t)m * N + col + 4 * h) = o;
+    }
+  }
+}
+
+
+// The tiled copy of an int4 [N][K] weight (k_linear_w4t_decode_long<.., true>):
+// chunk (16-row group nt, block kb of K): 1024 bytes at (nt * K/128 + kb) *
+// 1024.  Its 16 bytes at +16 l (l = j + 16 g) hold the codes of row
+// 16 nt + j at k = 128 kb + 32 g + 8 st + i (st < 4, i < 8), the 16 bytes
+// the plain kernel's lane (j, g) loads, rearranged: word 2 sp + h, byte q is
+// code (2 sp, i) | code (2 sp + 1, i) << 4 with i = 4 h + {0, 2, 1, 3}[q].
+// One thread per 16-byte unit.
+__global__ __launch_bounds__(256) void k_tile_w4t(const u32x4v* __restrict__ w, int64_t K, int64_t N,
+                                                  u32x4v* __restrict__ wt) {
+  const int64_t u = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int64_t KB = K / 128;
+  if (u >= N * K / 32) return;
+  const int64_t nt = u / (KB * 64), rem = u % (KB * 64);
+  const int64_t kb = rem / 64;
+  const int l = (int)(rem % 64);
+  const int64_t n = 16 * nt + (l & 15);
+  const u32x4v src = w[(n * (K / 2) + kb * 64 + 16 * (l >> 4)) / 16];
+  // code c of the unit (c = 8 st + i): nibble c & 1 of byte c >> 1
+  auto code = [&](int c) -> uint32_t { return (src[c >> 3] >> (4 * (c & 7))) & 0xFu; };
+  constexpr int ord[4] = {0, 2, 1, 3};
+  u32x4v o;
+#pragma unroll
+  for (int wd = 0; wd < 4; ++wd) {
+    const int sp = wd >> 1, h = wd & 1;
+    uint32_t word = 0u;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int i = 4 * h + ord[q];
+      word |= (code(16 * sp + i) | (code(16 * sp + 8 + i) << 4)) << (8 * q);
+    }
+    o[wd] = word;
+  }
+  wt[u] = o;
+}
+
 static int nt_splits(int64_t K) { return (int)ceil_div(K / 128, NT_BLKS); }
 
 static bool nt_decode_eligible(int64_t M, int64_t K, int64_t N, int kind, int bits, int block, const void* x,
@@ -1111,16 +1472,47 @@ static bool nt_decode_eligible(int64_t M, int64_t K, int64_t N, int kind, int bi
 }
 
 
-// workspace: arrival counters (one per 256-column group, DEC_COUNTER_BYTES,
-// zero between calls), then the partials [S][16][N]
+// The long-wave kernel: 8 waves of 8 steps (two blocks of K) per workgroup,
+// 2048 rows of K per split.
+#define NT_LONG_ROWS 2048
+static int nt_long_splits(int64_t K) { return (int)ceil_div(K, NT_LONG_ROWS); }
+
+static bool nt_long_eligible(int64_t K, int64_t N) {
+  if (N % 128 != 0 || N / 128 > DEC_COUNTER_BYTES / 8) return false;
+  const int64_t S = nt_long_splits(K);
+  return S <= 255 && S * (N / 128) * 8192 < (int64_t(1) << 31);
+}
+
+// workspace: arrival counters (DEC_COUNTER_BYTES, zero between calls: one
+// 32-bit count per 256-column group, or one 64-bit count of 8 per-XCC bytes
+// per 128-column block for the long-wave kernel), then the partials:
+// [S][16][N] or [S][N/128][16][128]
 static size_t nt_workspace_bytes(int64_t K, int64_t N) {
   const int S = nt_splits(K);
-  return S > 1 ? DEC_COUNTER_BYTES + (size_t)S * 16 * (size_t)N * 4 : 0;
+  size_t need = S > 1 ? DEC_COUNTER_BYTES + (size_t)S * 16 * (size_t)N * 4 : 0;
+  if (nt_long_eligible(K, N)) {
+    const int SL = nt_long_splits(K);
+    if (SL > 1) need = std::max(need, (size_t)DEC_COUNTER_BYTES + (size_t)SL * (size_t)(N / 128) * 8192);
+  }
+  return need;
+}
+
+template <typename T, bool TILED>
+static int launch_nt_long(const T* x, int64_t M, int64_t K, int64_t N, const uint8_t* w, const float* scales,
+                          int scales_kb_major, const float* bias, float* out, uint8_t* ws, hipStream_t st) {
+  const int SL = nt_long_splits(K);
+  const int64_t NB = N / 128;
+  unsigned long long* lc = SL > 1 ? reinterpret_cast<unsigned long long*>(ws) : nullptr;
+  float* lp = SL > 1 ? reinterpret_cast<float*>(ws + DEC_COUNTER_BYTES) : nullptr;
+  hipLaunchKernelGGL((k_linear_w4t_decode_long<T, 8, 8, TILED>), dim3((unsigned)(NB * SL)), dim3(512), 0, st, x,
+                     (int)M, K, N, w, scales, scales_kb_major, bias, out, lp, lc, SL, NB % 8 == 0 ? 1 : 0);
+  return check_launch(TILED ? "linear_wq_nt_tiled" : "linear_wq_nt(decode)");
 }
 
 template <typename T>
 static int launch_nt_decode(const T* x, int64_t M, int64_t K, int64_t N, const uint8_t* w, const float* scales,
                             int scales_kb_major, const float* bias, float* out, uint8_t* ws, hipStream_t st) {
+  if (nt_long_eligible(K, N)) return launch_nt_long<T, false>(x, M, K, N, w, scales, scales_kb_major, bias, out, ws, st);
   const int S = nt_splits(K);
   const int64_t groups = ceil_div(N, NT_COLS);
   unsigned int* counters = S > 1 ? reinterpret_cast<unsigned int*>(ws) : nullptr;
@@ -1529,6 +1921,49 @@ int mxk_linear_wq_nt(const void* x, int x_type, int64_t M, int64_t K, const void
     return linear_t<true, hip_bfloat16>((const hip_bfloat16*)x, M, K, N, pk, w_nbytes, w_scales, kind, bits, block,
                                         bias, out, st);
   return fail(MXK_EINVAL, "linear_wq_nt: bad input type");
+}
+
+int mxk_linear_prepack_weight_nt(const void* w_packed, int64_t N, int64_t K, int bits, int block, void* w_tiled,
+                                 void* stream) {
+  if (!w_packed || !w_tiled) return fail(MXK_EINVAL, "linear_prepack_weight_nt: null pointer");
+  if (bits != 4 || block != 128 || K <= 0 || N <= 0 || K % 128 != 0 || N % 128 != 0)
+    return fail(MXK_EINVAL, "linear_prepack_weight_nt: needs int4 codes, block 128, K and N multiples of 128");
+  if (!aligned16(w_packed) || !aligned16(w_tiled))
+    return fail(MXK_EINVAL, "linear_prepack_weight_nt: w_packed and w_tiled must be 16-byte aligned");
+  const int64_t units = N * K / 32;
+  if (ceil_div(units, 256) >= (int64_t(1) << 31)) return fail(MXK_EUNSUPPORTED, "linear_prepack_weight_nt: too large");
+  hipLaunchKernelGGL(k_tile_w4t, dim3((unsigned)ceil_div(units, 256)), dim3(256), 0,
+                     reinterpret_cast<hipStream_t>(stream), reinterpret_cast<const u32x4v*>(w_packed), K, N,
+                     reinterpret_cast<u32x4v*>(w_tiled));
+  return check_launch("linear_prepack_weight_nt");
+}
+
+int mxk_linear_wq_nt_tiled(const void* x, int x_type, int64_t M, int64_t K, const void* w_tiled,
+                           const float* w_scales_t, int64_t N, const float* bias, float* out, void* workspace,
+                           size_t workspace_nbytes, void* stream) {
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  if (M <= 0 || K <= 0 || N <= 0) return fail(MXK_EINVAL, "linear_wq_nt_tiled: sizes must be positive");
+  if (!x || !w_tiled || !w_scales_t || !out) return fail(MXK_EINVAL, "linear_wq_nt_tiled: null pointer");
+  if (x_type != MXK_IN_F32 && x_type != MXK_IN_F16 && x_type != MXK_IN_BF16)
+    return fail(MXK_EINVAL, "linear_wq_nt_tiled: bad input type");
+  if ((bias && !aligned16(bias)) || !aligned16(out))
+    return fail(MXK_EINVAL, "linear_wq_nt_tiled: bias and out must be 16-byte aligned");
+  const int esz = x_type == MXK_IN_F32 ? 4 : 2;
+  const int64_t lim = int64_t(1) << 31;
+  if (M > 16 || K % 128 != 0 || N % 128 != 0 || !nt_long_eligible(K, N) || !aligned16(x) || !aligned16(w_tiled) ||
+      !aligned16(w_scales_t) || N * K / 2 >= lim || N * (K / 128) * 4 >= lim || 16 * K * esz >= lim)
+    return fail(MXK_EUNSUPPORTED, "linear_wq_nt_tiled: needs M <= 16, K and N multiples of 128, 16-byte aligned "
+                                  "x, w_tiled and w_scales_t (use mxk_linear_wq_nt)");
+  const size_t need = nt_workspace_bytes(K, N);
+  if (nt_long_splits(K) > 1 && (!workspace || workspace_nbytes < need))
+    return fail(MXK_EINVAL, "linear_wq_nt_tiled: needs a zero-initialised workspace of mxk_linear_nt_workspace() bytes");
+  uint8_t* ws = reinterpret_cast<uint8_t*>(workspace);
+  const uint8_t* wt = reinterpret_cast<const uint8_t*>(w_tiled);
+  if (x_type == MXK_IN_F32)
+    return launch_nt_long<float, true>((const float*)x, M, K, N, wt, w_scales_t, 1, bias, out, ws, st);
+  if (x_type == MXK_IN_F16)
+    return launch_nt_long<__half, true>((const __half*)x, M, K, N, wt, w_scales_t, 1, bias, out, ws, st);
+  return launch_nt_long<hip_bfloat16, true>((const hip_bfloat16*)x, M, K, N, wt, w_scales_t, 1, bias, out, ws, st);
 }
 
 }  // extern "C"

@@ -168,18 +168,18 @@ class _LinearWQNT(torch.autograd.Function):
     of ops.linear_wq with the roles of the two dimensions exchanged."""
 
     @staticmethod
-    def forward(ctx, x, w, bias, in_features, out_features, w_scales_t):
+    def forward(ctx, x, w, bias, in_features, out_features, w_scales_t, w_tiled=None):
         ctx.w, ctx.w_scales_t = w, w_scales_t
         ctx.in_features, ctx.out_features = in_features, out_features
         return ops.linear_wq_nt(x.detach(), w._mx_packed, w._mx_scales, w._mx_dtype, out_features, in_features,
-                                w._mx_block, bias=bias, w_scales_t=w_scales_t)
+                                w._mx_block, bias=bias, w_scales_t=w_scales_t, w_tiled=w_tiled)
 
     @staticmethod
     def backward(ctx, grad):
         w = ctx.w
         gi = ops.linear_wq(grad.contiguous(), w._mx_packed, w._mx_scales, w._mx_dtype, ctx.out_features,
                            ctx.in_features, w._mx_block, w_scales_t=ctx.w_scales_t)
-        return gi, None, None, None, None, None
+        return gi, None, None, None, None, None, None
 
 
 class mx_dynamic_linear(nn.Module):
@@ -240,10 +240,32 @@ class mx_dynamic_linear(nn.Module):
             out = out.reshape(*x_f.shape[:-1], self.out_features)
             return out + b if b is not None else out
         st = self._block_major_scales(w)
+        rows = x_f.numel() // max(self.in_features, 1)
+        wt = self._decode_weight(w) if rows <= 16 else None
         if torch.is_grad_enabled() and x_f.requires_grad:
-            return _LinearWQNT.apply(x_f, w, b, self.in_features, self.out_features, st)
+            return _LinearWQNT.apply(x_f, w, b, self.in_features, self.out_features, st, wt)
         return ops.linear_wq_nt(x_f, w._mx_packed, w._mx_scales, w._mx_dtype, self.out_features, self.in_features,
-                                w._mx_block, bias=b, w_scales_t=st)
+                                w._mx_block, bias=b, w_scales_t=st, w_tiled=wt)
+
+    # Whether decode-shaped forwards (at most 16 rows of x) keep a tiled copy
+    # of an int4 weight's packed codes (in*out/2 bytes, made on the first
+    # such forward) for the faster decode kernel; False saves that memory.
+    tiled_decode = True
+
+    def _decode_weight(self, w) -> Optional[Tensor]:
+        """Tiled copy of the packed int4 [out, in] weight for the decode
+        kernel, made once per weight tensor and rebuilt when the packed codes
+        are replaced or modified in place."""
+        if not self.tiled_decode or not ops.decode_prepack_nt_eligible(w._mx_dtype, w._mx_block, self.in_features,
+                                                                      self.out_features):
+            return None
+        pk = w._mx_packed
+        key = (pk.data_ptr(), str(pk.device), pk._version)
+        cached = self.__dict__.get("_w_tiled_cache")
+        if cached is None or cached[0] != key:
+            cached = (key, ops.prepack_weight_nt(pk, self.out_features, self.in_features, w._mx_block))
+            self.__dict__["_w_tiled_cache"] = cached
+        return cached[1]
 
     def _block_major_scales(self, w) -> Optional[Tensor]:
         """K-block-major copy [in/128, out] of the [out, in] weight's scales,
