@@ -1207,9 +1207,12 @@ __global__ __launch_bounds__(W * 64, 1) void k_linear_w4t_decode_long(
 #pragma unroll
   for (int s8 = 0; s8 < STEPS; ++s8) {
     uint32_t hw[4], lw[4];
+    // TILED: the odd steps meet B operands 16 times larger (high nibbles), so
+    // their A is built at 2^-4 and every step sums into one accumulator
+    const int xs8 = (TILED && (s8 & 1)) ? xe - 4 : xe;
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      const float a = __builtin_ldexpf(xv[8 * s8 + 2 * e], xe), b = __builtin_ldexpf(xv[8 * s8 + 2 * e + 1], xe);
+      const float a = __builtin_ldexpf(xv[8 * s8 + 2 * e], xs8), b = __builtin_ldexpf(xv[8 * s8 + 2 * e + 1], xs8);
       auto hp = __builtin_amdgcn_cvt_pkrtz(a, b);
       auto lp = __builtin_amdgcn_cvt_pkrtz(a - (float)hp[0], b - (float)hp[1]);
       hw[e] = __builtin_bit_cast(uint32_t, hp);
@@ -1252,26 +1255,26 @@ __global__ __launch_bounds__(W * 64, 1) void k_linear_w4t_decode_long(
   for (int t = 0; t < 8; ++t) res[t] = f32x4{0.f, 0.f, 0.f, 0.f};
   if constexpr (TILED) {
     // steps 0 and 2 from the low nibbles (code + 8) * 2^-24, steps 1 and 3
-    // from the high nibbles (code + 8) * 2^-20, summed apart: word 2 sp + h,
-    // byte q holds codes (step 2 sp, i) | (step 2 sp + 1, i) << 4 with
-    // i = 4 h + {0, 2, 1, 3}[q], so (w & 0x000F000F) and ((w >> 8) &
+    // from the high nibbles (code + 8) * 2^-20 against A at 2^-4: word
+    // 2 sp + h, byte q holds codes (step 2 sp, i) | (step 2 sp + 1, i) << 4
+    // with i = 4 h + {0, 2, 1, 3}[q], so (w & 0x000F000F) and ((w >> 8) &
     // 0x000F000F) are the f16 pairs (i, i + 1) of the low step, the masks
     // 0x00F000F0 those of the high step
     const f16x8 bl = __builtin_bit_cast(f16x8, u32x4v{0x00080008u, 0x00080008u, 0x00080008u, 0x00080008u});
     const f16x8 bh = __builtin_bit_cast(f16x8, u32x4v{0x00800080u, 0x00800080u, 0x00800080u, 0x00800080u});
 #pragma unroll
     for (int b = 0; b < KBW; ++b) {
-      f32x4 corl = f32x4{0.f, 0.f, 0.f, 0.f}, corh = f32x4{0.f, 0.f, 0.f, 0.f};
+      f32x4 corr = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int sp = 0; sp < 2; ++sp) {
-        corl = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi[4 * b + 2 * sp], bl, corl, 0, 0, 0);
-        corl = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo[4 * b + 2 * sp], bl, corl, 0, 0, 0);
-        corh = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi[4 * b + 2 * sp + 1], bh, corh, 0, 0, 0);
-        corh = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo[4 * b + 2 * sp + 1], bh, corh, 0, 0, 0);
+        corr = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi[4 * b + 2 * sp], bl, corr, 0, 0, 0);
+        corr = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo[4 * b + 2 * sp], bl, corr, 0, 0, 0);
+        corr = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi[4 * b + 2 * sp + 1], bh, corr, 0, 0, 0);
+        corr = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo[4 * b + 2 * sp + 1], bh, corr, 0, 0, 0);
       }
 #pragma unroll
       for (int t = 0; t < 8; ++t) {
-        f32x4 accl = f32x4{0.f, 0.f, 0.f, 0.f}, acch = f32x4{0.f, 0.f, 0.f, 0.f};
+        f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int sp = 0; sp < 2; ++sp) {
           const uint32_t w0 = wv[b][t][2 * sp], w1 = wv[b][t][2 * sp + 1];
@@ -1282,14 +1285,14 @@ __global__ __launch_bounds__(W * 64, 1) void k_linear_w4t_decode_long(
           const f16x8 bth = __builtin_bit_cast(
               f16x8, u32x4v{(w0 & 0x00F000F0u) ^ 0x00800080u, (s0 & 0x00F000F0u) ^ 0x00800080u,
                             (w1 & 0x00F000F0u) ^ 0x00800080u, (s1 & 0x00F000F0u) ^ 0x00800080u});
-          accl = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi[4 * b + 2 * sp], btl, accl, 0, 0, 0);
-          accl = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo[4 * b + 2 * sp], btl, accl, 0, 0, 0);
-          acch = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi[4 * b + 2 * sp + 1], bth, acch, 0, 0, 0);
-          acch = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo[4 * b + 2 * sp + 1], bth, acch, 0, 0, 0);
+          acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi[4 * b + 2 * sp], btl, acc, 0, 0, 0);
+          acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo[4 * b + 2 * sp], btl, acc, 0, 0, 0);
+          acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi[4 * b + 2 * sp + 1], bth, acc, 0, 0, 0);
+          acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo[4 * b + 2 * sp + 1], bth, acc, 0, 0, 0);
         }
         const float sf = sc[b][t] * 16777216.0f;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) res[t][i] += sf * ((accl[i] - corl[i]) + (acch[i] - corh[i]) * 0.0625f);
+        for (int i = 0; i < 4; ++i) res[t][i] += sf * (acc[i] - corr[i]);
       }
     }
   } else {
