@@ -329,7 +329,10 @@ def bench_dynamic(qa, steps, reps):
       * fused_int8_linear with per-token int8 activations [8192, 8192] and int8d
         weights [8192, 8192] block 128: 2*8192^3 int8 ops on MFMA;
       * dynamic_quantize per token of fp32 [8192, 8192] to int8: 4 B read +
-        1 B written per element + 4 B per row."""
+        1 B written per element + 4 B per row;
+      * the same tensor per channel and per tensor: two passes (the absmax,
+        then the codes), bytes counted as one read of x + the codes + the
+        scales, so 0.5 is the ceiling of a two-read kernel pair."""
     dev = torch.device("cuda:0")
     out = {}
     x_cpu, W_cpu = config2_inputs()
@@ -371,6 +374,12 @@ def bench_dynamic(qa, steps, reps):
     out["dynamic_quantize_per_token_8192x8192"] = {
         "us": round(t * 1e6, 2), "GBs": round(algo / t / 1e9, 1), "frac": round(algo / t / 1e9 / HBM_PEAK_GBS, 4),
         "bytes": algo}
+    for gran, ns in (("per_channel", K), ("per_tensor", 1)):
+        t = graph_time(lambda: qa.dynamic_quantize(xa, "int8d", gran), reps, 1, repeats=3)
+        algo = M * K * 5 + ns * 4
+        out[f"dynamic_quantize_{gran}_8192x8192"] = {
+            "us": round(t * 1e6, 2), "GBs": round(algo / t / 1e9, 1),
+            "frac": round(algo / t / 1e9 / HBM_PEAK_GBS, 4), "bytes": algo}
     return out
 
 

@@ -78,6 +78,231 @@ __global__ __launch_bounds__(256) void k_dyn_encode(const T* __restrict__ x, int
   }
 }
 
+// ---- vector paths (x 16-byte aligned; see dyn_run for the shapes).  A
+// wave's load q covers 64 * EPL consecutive elements (lane l: EPL at
+// EPL * l), so every load instruction reads whole lines.
+template <typename T>
+__device__ __forceinline__ void load16(const T* __restrict__ p, float (&v)[16 / sizeof(T)]) {
+  constexpr int EPL = 16 / (int)sizeof(T);
+  const u32x4 w = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+  const T* t = reinterpret_cast<const T*>(&w);
+#pragma unroll
+  for (int e = 0; e < EPL; ++e) v[e] = ElemT<T>::cvt(t[e]);
+}
+
+// part[blockIdx.x] = max |x| over the workgroup's share of x (n % 16 == 0):
+// four wave loads in flight, wave maximum, then across the 4 waves in LDS.
+template <typename T>
+__global__ __launch_bounds__(256) void k_absmax_all_v(const T* __restrict__ x, int64_t n, float* __restrict__ part) {
+  constexpr int EPL = 16 / (int)sizeof(T), U = 4, WCH = 64 * EPL;
+  __shared__ float sm[4];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int64_t stride = (int64_t)gridDim.x * 4 * WCH * U;
+  float m = 0.0f;
+  for (int64_t b0 = ((int64_t)blockIdx.x * 4 + wave) * WCH * U; b0 < n; b0 += stride) {
+    float v[U][EPL];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t i = b0 + (int64_t)u * WCH + EPL * lane;
+      if (i < n) {
+        load16<T>(x + i, v[u]);
+      } else {
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) v[u][e] = 0.0f;
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+#pragma unroll
+      for (int e = 0; e < EPL; ++e) m = fmaxf(m, __builtin_fabsf(v[u][e]));
+  }
+  m = group_max<64>(m);
+  if (lane == 0) sm[wave] = m;
+  __syncthreads();
+  if (threadIdx.x == 0) part[blockIdx.x] = fmaxf(fmaxf(sm[0], sm[1]), fmaxf(sm[2], sm[3]));
+}
+
+// part[blockIdx.y][c] = max over the workgroup's rows of |x[r][c]| (C a
+// multiple of 16 / sizeof(T)): thread t takes the EPL columns at
+// EPL * (blockIdx.x * 256 + t), one 16-byte load per row, eight rows in flight.
+template <typename T>
+__global__ __launch_bounds__(256) void k_absmax_cols_v(const T* __restrict__ x, int64_t R, int64_t C,
+                                                       int64_t rows_per, float* __restrict__ part) {
+  constexpr int EPL = 16 / (int)sizeof(T), U = 8;
+  const int64_t c0 = ((int64_t)blockIdx.x * 256 + threadIdx.x) * EPL;
+  if (c0 >= C) return;
+  const int64_t r0 = (int64_t)blockIdx.y * rows_per;
+  const int64_t r1 = std::min<int64_t>(R, r0 + rows_per);
+  float m[EPL];
+#pragma unroll
+  for (int e = 0; e < EPL; ++e) m[e] = 0.0f;
+  for (int64_t r = r0; r < r1; r += U) {
+    float v[U][EPL];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      if (r + u < r1) {
+        load16<T>(x + (r + u) * C + c0, v[u]);
+      } else {
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) v[u][e] = 0.0f;
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+#pragma unroll
+      for (int e = 0; e < EPL; ++e) m[e] = fmaxf(m[e], __builtin_fabsf(v[u][e]));
+  }
+  float* dst = part + (int64_t)blockIdx.y * C + c0;
+#pragma unroll
+  for (int e = 0; e < EPL; e += 4) *reinterpret_cast<f32x4v*>(dst + e) = f32x4v{m[e], m[e + 1], m[e + 2], m[e + 3]};
+}
+
+// scales[i] = RN(max(amax_i, fl32(1e-12)) / max_int), rcp[i] = RN(1 / scales[i]),
+// amax_i the maximum of part[k * cnt + i] over k < parts.
+__global__ __launch_bounds__(256) void k_dyn_scales_parts(const float* __restrict__ part, int64_t parts, int64_t cnt,
+                                                          float q, float* __restrict__ scales,
+                                                          float* __restrict__ rcp) {
+  if (cnt == 1) {  // one workgroup: the maximum over all parts
+    __shared__ float sm[4];
+    float m = 0.0f;
+    for (int64_t k = threadIdx.x; k < parts; k += 256) m = fmaxf(m, part[k]);
+    m = group_max<64>(m);
+    if ((threadIdx.x & 63) == 0) sm[threadIdx.x >> 6] = m;
+    __syncthreads();
+    if (threadIdx.x == 0 && blockIdx.x == 0) {
+      const float sc = fmaxf(fmaxf(fmaxf(sm[0], sm[1]), fmaxf(sm[2], sm[3])), MXK_AMIN) / q;
+      scales[0] = sc;
+      rcp[0] = 1.0f / sc;
+    }
+    return;
+  }
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < cnt; i += (int64_t)gridDim.x * blockDim.x) {
+    float m = 0.0f;
+    for (int64_t k0 = 0; k0 < parts; k0 += 8) {
+      float t[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) t[u] = k0 + u < parts ? part[(k0 + u) * cnt + i] : 0.0f;
+#pragma unroll
+      for (int u = 0; u < 8; ++u) m = fmaxf(m, t[u]);
+    }
+    const float sc = fmaxf(m, MXK_AMIN) / q;
+    scales[i] = sc;
+    rcp[i] = 1.0f / sc;
+  }
+}
+
+// Encode, a wave taking 1024 consecutive elements per step (n % 16 == 0;
+// per channel C % 1024 == 0, so a step stays in one row): load q of lane l
+// is the EPL elements at 64 * EPL * q + EPL * l.  RN(x / s) by Markstein's
+// correction with y = RN(1 / s), or the hardware divide for a lane holding
+// a nonzero |x| below 2^-96; clamp, round to nearest even, and each load's
+// EPL codes stored together (one store instruction of the wave covers
+// 64 * EPL * BITS / 8 contiguous bytes).
+template <typename T, int BITS, bool PER_CHANNEL, bool FIXED>
+__global__ __launch_bounds__(256) void k_dyn_encode_v(const T* __restrict__ x, int64_t n, int64_t C,
+                                                      const float* __restrict__ scales, const float* __restrict__ rcp,
+                                                      float q, uint8_t* __restrict__ packed) {
+  constexpr int EPL = 16 / (int)sizeof(T), QL = 16 / EPL, WCH = 64 * EPL, STEP = 1024;
+  constexpr int GB = EPL * BITS / 8;  // packed bytes of one load's codes
+  constexpr uint32_t MASK = (1u << BITS) - 1u;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int64_t stride = (int64_t)gridDim.x * 4 * STEP;
+  const float s_all = PER_CHANNEL ? 0.0f : scales[0], y_all = PER_CHANNEL ? 0.0f : rcp[0];
+  // FIXED (the grid's stride a multiple of C): a wave's columns are the same
+  // at every step, so its scales are loaded once
+  float sf[QL][EPL], yf[QL][EPL];
+  if constexpr (PER_CHANNEL && FIXED) {
+    const int64_t cb = (((int64_t)blockIdx.x * 4 + wave) * STEP) % C;
+#pragma unroll
+    for (int ql = 0; ql < QL; ++ql)
+#pragma unroll
+      for (int e = 0; e < EPL; e += 4) {
+        const int64_t c = cb + (int64_t)ql * WCH + EPL * lane + e;
+        const f32x4v a = *reinterpret_cast<const f32x4v*>(scales + c);
+        const f32x4v b = *reinterpret_cast<const f32x4v*>(rcp + c);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) { sf[ql][e + k] = a[k]; yf[ql][e + k] = b[k]; }
+      }
+  }
+  for (int64_t b0 = ((int64_t)blockIdx.x * 4 + wave) * STEP; b0 < n; b0 += stride) {
+    float v[QL][EPL];
+#pragma unroll
+    for (int ql = 0; ql < QL; ++ql) {
+      const int64_t i = b0 + (int64_t)ql * WCH + EPL * lane;
+      if (i < n) {
+        load16<T>(x + i, v[ql]);
+      } else {
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) v[ql][e] = 0.0f;
+      }
+    }
+    float sv[QL][EPL], yv[QL][EPL];
+    if constexpr (PER_CHANNEL && FIXED) {
+#pragma unroll
+      for (int ql = 0; ql < QL; ++ql)
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) { sv[ql][e] = sf[ql][e]; yv[ql][e] = yf[ql][e]; }
+    } else if constexpr (PER_CHANNEL) {
+      const int64_t cb = b0 % C;  // wave-uniform
+#pragma unroll
+      for (int ql = 0; ql < QL; ++ql)
+#pragma unroll
+        for (int e = 0; e < EPL; e += 4) {
+          const int64_t c = cb + (int64_t)ql * WCH + EPL * lane + e;
+          const f32x4v a = *reinterpret_cast<const f32x4v*>(scales + c);
+          const f32x4v b = *reinterpret_cast<const f32x4v*>(rcp + c);
+#pragma unroll
+          for (int k = 0; k < 4; ++k) { sv[ql][e + k] = a[k]; yv[ql][e + k] = b[k]; }
+        }
+    } else {
+#pragma unroll
+      for (int ql = 0; ql < QL; ++ql)
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) { sv[ql][e] = s_all; yv[ql][e] = y_all; }
+    }
+    uint32_t mnb = 0xFFFFFFFFu;  // (bits << 1) - 1: both zeros map to the maximum
+#pragma unroll
+    for (int ql = 0; ql < QL; ++ql)
+#pragma unroll
+      for (int e = 0; e < EPL; ++e) mnb = min(mnb, (__float_as_uint(v[ql][e]) << 1) - 1u);
+    if (__builtin_expect(mnb < 2u * 0x0F800000u - 1u, 0)) {
+#pragma unroll
+      for (int ql = 0; ql < QL; ++ql)
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) v[ql][e] = v[ql][e] / sv[ql][e];
+    } else {
+#pragma unroll
+      for (int ql = 0; ql < QL; ++ql)
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) {
+          const float q0 = v[ql][e] * yv[ql][e];
+          v[ql][e] = __builtin_fmaf(__builtin_fmaf(-q0, sv[ql][e], v[ql][e]), yv[ql][e], q0);
+        }
+    }
+#pragma unroll
+    for (int ql = 0; ql < QL; ++ql) {
+      const int64_t i = b0 + (int64_t)ql * WCH + EPL * lane;
+      uint32_t w[(GB + 3) / 4];
+#pragma unroll
+      for (int k = 0; k < (GB + 3) / 4; ++k) w[k] = 0u;
+#pragma unroll
+      for (int e = 0; e < EPL; ++e) {
+        // rne of the clamped quotient by the float adder (|t| <= q < 2^22)
+        const float t = __builtin_amdgcn_fmed3f(v[ql][e], -q, q);
+        const uint32_t code = __float_as_uint(t + 12582912.0f) & MASK;
+        w[(e * BITS) >> 5] |= code << ((e * BITS) & 31);
+      }
+      if (i < n) {
+        uint8_t* dst = packed + i * BITS / 8;
+        if constexpr (GB == 8) *reinterpret_cast<u32x2*>(dst) = u32x2{w[0], w[1]};
+        else if constexpr (GB == 4) *reinterpret_cast<uint32_t*>(dst) = w[0];
+        else if constexpr (GB == 2) *reinterpret_cast<uint16_t*>(dst) = (uint16_t)w[0];
+        else *dst = (uint8_t)w[0];
+      }
+    }
+  }
+}
+
 // amax[r] = max over row r of |x[r][:]|, as float bits: one workgroup per
 // row (grid-stride over the rows), a wave maximum, then across the 4 waves.
 template <typename T>
@@ -147,9 +372,85 @@ static int vec_run(const T* x, int64_t rows, int64_t cols, int axis, int bits, i
   return check_launch("vector_quantize");
 }
 
+// The vector kernels take 16-byte aligned x, n % 16 == 0 and, per channel,
+// cols % 1024 == 0; other shapes run the element-wise kernels.
+template <typename T>
+static bool dyn_vector_ok(const T* x, int64_t rows, int64_t cols, int granularity, const uint8_t* packed, int bits) {
+  const int64_t n = rows * cols;
+  if (!aligned16(x) || n % 16 != 0) return false;
+  constexpr int EPL = 16 / (int)sizeof(T);
+  if ((reinterpret_cast<uintptr_t>(packed) % (uintptr_t)std::max(1, EPL * bits / 8)) != 0) return false;
+  return granularity != MXK_DYN_PER_CHANNEL || cols % 1024 == 0;
+}
+
+// workspace of the vector path: scales' reciprocals (cnt words, padded to
+// 64), then the absmax parts: DYN_PARTS maxima per tensor, or DYN_COL_PARTS
+// rows of cols maxima per channel
+#define DYN_PARTS 1024
+#define DYN_COL_PARTS 128
+static int64_t dyn_pad(int64_t c) { return (c + 63) & ~(int64_t)63; }
+
+template <typename T>
+static int dyn_run_vector(const T* x, int64_t rows, int64_t cols, int granularity, int bits, uint8_t* packed,
+                          float* scales, float* ws, hipStream_t st) {
+  constexpr int EPL = 16 / (int)sizeof(T);
+  const int64_t n = rows * cols;
+  const float q = (float)((1u << (bits - 1)) - 1u);
+  const int64_t cus = num_cus();
+  const bool pc = granularity == MXK_DYN_PER_CHANNEL;
+  const int64_t cnt = pc ? cols : 1;
+  float* rcp = ws;
+  float* part = ws + dyn_pad(cnt);
+  int64_t parts;
+  if (pc) {
+    const int64_t col_blocks = ceil_div(cols / EPL, 256);
+    const int64_t chunks = std::max<int64_t>(
+        1, std::min<int64_t>({(int64_t)DYN_COL_PARTS, ceil_div(rows, 8), ceil_div(cus * 8, col_blocks)}));
+    const int64_t rows_per = ceil_div(rows, chunks);
+    parts = ceil_div(rows, rows_per);
+    hipLaunchKernelGGL((k_absmax_cols_v<T>), dim3((unsigned)col_blocks, (unsigned)parts), dim3(256), 0, st, x, rows,
+                       cols, rows_per, part);
+  } else {
+    parts = std::max<int64_t>(1, std::min<int64_t>(ceil_div(n, 4 * 64 * EPL * 4), (int64_t)DYN_PARTS));
+    hipLaunchKernelGGL((k_absmax_all_v<T>), dim3((unsigned)parts), dim3(256), 0, st, x, n, part);
+  }
+  hipLaunchKernelGGL(k_dyn_scales_parts, dim3(pc ? (unsigned)std::min<int64_t>(ceil_div(cnt, 256), cus * 8) : 1u),
+                     dim3(256), 0, st, part, parts, cnt, q, scales, rcp);
+  int64_t g = std::max<int64_t>(1, std::min<int64_t>(ceil_div(n, 4 * 1024), cus * 16));
+  // per channel, a grid whose stride (4096 elements per workgroup) is a
+  // multiple of cols keeps every wave on the same columns
+  bool fixed = false;
+  if (pc) {
+    const int64_t c1 = cols / 1024, m = c1 / std::__gcd<int64_t>(c1, 4);
+    if (m <= cus * 64) {
+      g = std::max<int64_t>(m, (g / m) * m);
+      fixed = true;
+    }
+  }
+#define MXK_DYNV(BITS)                                                                                             \
+  if (pc && fixed)                                                                                                 \
+    hipLaunchKernelGGL((k_dyn_encode_v<T, BITS, true, true>), dim3((unsigned)g), dim3(256), 0, st, x, n, cols,     \
+                       scales, rcp, q, packed);                                                                    \
+  else if (pc)                                                                                                     \
+    hipLaunchKernelGGL((k_dyn_encode_v<T, BITS, true, false>), dim3((unsigned)g), dim3(256), 0, st, x, n, cols,    \
+                       scales, rcp, q, packed);                                                                    \
+  else                                                                                                             \
+    hipLaunchKernelGGL((k_dyn_encode_v<T, BITS, false, false>), dim3((unsigned)g), dim3(256), 0, st, x, n, cols,   \
+                       scales, rcp, q, packed)
+  switch (bits) {
+    case 2: MXK_DYNV(2); break;
+    case 4: MXK_DYNV(4); break;
+    default: MXK_DYNV(8); break;
+  }
+#undef MXK_DYNV
+  return check_launch("dynamic_quantize");
+}
+
 template <typename T>
 static int dyn_run(const T* x, int64_t rows, int64_t cols, int granularity, int bits, uint8_t* packed,
                    int64_t pbytes, float* scales, uint32_t* amax, hipStream_t st) {
+  if (dyn_vector_ok(x, rows, cols, granularity, packed, bits))
+    return dyn_run_vector(x, rows, cols, granularity, bits, packed, scales, reinterpret_cast<float*>(amax), st);
   const int64_t n = rows * cols;
   const float q = (float)((1u << (bits - 1)) - 1u);
   const int cap = num_cus() * 8;
@@ -189,8 +490,12 @@ size_t mxk_dynamic_quantize_workspace(int64_t rows, int64_t cols, int granularit
   if (rows <= 0 || cols <= 0) return 0;
   if (granularity == MXK_DYN_PER_TOKEN)
     return mxk_quantize_workspace(rows * cols, MXK_KIND_INT, bits, MXK_VAR_VECTOR, (int)cols, 0);
-  const int64_t cnt = granularity == MXK_DYN_PER_CHANNEL ? cols : 1;
-  return (size_t)((cnt * 4 + 255) & ~(int64_t)255);
+  // the element-wise path: absmax bits (cnt words); the vector path:
+  // reciprocal scales (cnt words, padded to 64), then the absmax parts
+  const bool pc = granularity == MXK_DYN_PER_CHANNEL;
+  const int64_t cnt = pc ? cols : 1;
+  const int64_t words = std::max<int64_t>(cnt, dyn_pad(cnt) + (pc ? (int64_t)DYN_COL_PARTS * cols : DYN_PARTS));
+  return (size_t)((words * 4 + 255) & ~(int64_t)255);
 }
 
 int mxk_dynamic_quantize(const void* x, int x_type, int64_t rows, int64_t cols, int granularity, int bits,

@@ -63,6 +63,28 @@ def test_dynamic_quantize_matches_oracle(qa, gran, name, shape, src):
     assert G.bits_equal(q._mx_scales.cpu(), s), "scales differ"
 
 
+@pytest.mark.parametrize("gran", ["per_channel", "per_tensor"])
+@pytest.mark.parametrize("name", ["int2d", "int4d", "int8d"])
+@pytest.mark.parametrize("shape", [(64, 3072), (33, 5120), (8, 1024, 2), (2048, 1024)])
+@pytest.mark.parametrize("src", ["f32", "bf16"])
+def test_dynamic_quantize_vector_paths(qa, gran, name, shape, src):
+    """The vectorised kernels (16-byte loads, per channel when a row is a
+    multiple of 1024 columns, with the fixed-column grid for 3, 5 and 1 x
+    1024 columns and several grid steps): codes and scales bit for bit,
+    with values below 2^-96 and columns of zeros mixed in (the exact-divide
+    branch of the encode)."""
+    x = _x(shape, 5, 3.0)
+    flat = x.view(-1)
+    flat[::97] *= 1e-33
+    x.view(x.shape[0], -1)[:, 5] = 0.0
+    x = {"f32": x, "bf16": x.bfloat16()}[src]
+    q = qa.dynamic_quantize(x.to(dev()), name, gran)
+    p, s, sh, n, blk = orc.dynamic_quantize(x, name, gran)
+    assert tuple(q.shape) == sh and q._mx_n == n and q._mx_block == blk
+    assert G.bits_equal(q._mx_packed.cpu(), p), "packed codes differ"
+    assert G.bits_equal(q._mx_scales.cpu(), s), "scales differ"
+
+
 @pytest.mark.parametrize("name", ["int3d", "int16d"])
 def test_dynamic_quantize_per_token_word_widths(qa, name):
     x = _x((9, 200), 2)
