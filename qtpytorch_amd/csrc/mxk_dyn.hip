@@ -17,6 +17,7 @@
 #include "mxk_internal.h"
 
 #include <algorithm>
+#include <type_traits>
 
 namespace mxk {
 
@@ -77,6 +78,13 @@ __global__ __launch_bounds__(256) void k_dyn_encode(const T* __restrict__ x, int
     packed[u] = (uint8_t)w;
   }
 }
+
+// workspace of the vector path: scales' reciprocals (cnt words, padded to
+// 64), then the absmax parts: DYN_PARTS maxima per tensor, or DYN_COL_PARTS
+// rows of cols maxima per channel
+#define DYN_PARTS 1024
+#define DYN_COL_PARTS 128
+static int64_t dyn_pad(int64_t c) { return (c + 63) & ~(int64_t)63; }
 
 // ---- vector paths (x 16-byte aligned; see dyn_run for the shapes).  A
 // wave's load q covers 64 * EPL consecutive elements (lane l: EPL at
@@ -172,7 +180,7 @@ __global__ __launch_bounds__(256) void k_dyn_scales_parts(const float* __restric
     if (threadIdx.x == 0 && blockIdx.x == 0) {
       const float sc = fmaxf(fmaxf(fmaxf(sm[0], sm[1]), fmaxf(sm[2], sm[3])), MXK_AMIN) / q;
       scales[0] = sc;
-      rcp[0] = 1.0f / sc;
+      if (rcp) rcp[0] = 1.0f / sc;
     }
     return;
   }
@@ -187,7 +195,76 @@ __global__ __launch_bounds__(256) void k_dyn_scales_parts(const float* __restric
     }
     const float sc = fmaxf(m, MXK_AMIN) / q;
     scales[i] = sc;
-    rcp[i] = 1.0f / sc;
+    if (rcp) rcp[i] = 1.0f / sc;
+  }
+}
+
+// int32 codes of vector_quantize per column (C % 1024 == 0): the load layout
+// of k_dyn_encode_v, RN(x / s) by the hardware divide, clamp, round to
+// nearest even; each load's EPL codes in one or two 16-byte stores.
+template <typename T, bool FIXED>
+__global__ __launch_bounds__(256) void k_vec_encode_cols_v(const T* __restrict__ x, int64_t n, int64_t C,
+                                                           const float* __restrict__ scales, float q,
+                                                           int32_t* __restrict__ codes) {
+  constexpr int EPL = 16 / (int)sizeof(T), QL = 16 / EPL, WCH = 64 * EPL, STEP = 1024;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int64_t stride = (int64_t)gridDim.x * 4 * STEP;
+  float sf[QL][EPL];
+  if constexpr (FIXED) {
+    const int64_t cb = (((int64_t)blockIdx.x * 4 + wave) * STEP) % C;
+#pragma unroll
+    for (int ql = 0; ql < QL; ++ql)
+#pragma unroll
+      for (int e = 0; e < EPL; e += 4) {
+        const f32x4v a = *reinterpret_cast<const f32x4v*>(scales + cb + (int64_t)ql * WCH + EPL * lane + e);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) sf[ql][e + k] = a[k];
+      }
+  }
+  for (int64_t b0 = ((int64_t)blockIdx.x * 4 + wave) * STEP; b0 < n; b0 += stride) {
+    float v[QL][EPL];
+#pragma unroll
+    for (int ql = 0; ql < QL; ++ql) {
+      const int64_t i = b0 + (int64_t)ql * WCH + EPL * lane;
+      if (i < n) {
+        load16<T>(x + i, v[ql]);
+      } else {
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) v[ql][e] = 0.0f;
+      }
+    }
+    float sv[QL][EPL];
+    if constexpr (FIXED) {
+#pragma unroll
+      for (int ql = 0; ql < QL; ++ql)
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) sv[ql][e] = sf[ql][e];
+    } else {
+      const int64_t cb = b0 % C;  // wave-uniform
+#pragma unroll
+      for (int ql = 0; ql < QL; ++ql)
+#pragma unroll
+        for (int e = 0; e < EPL; e += 4) {
+          const f32x4v a = *reinterpret_cast<const f32x4v*>(scales + cb + (int64_t)ql * WCH + EPL * lane + e);
+#pragma unroll
+          for (int k = 0; k < 4; ++k) sv[ql][e + k] = a[k];
+        }
+    }
+#pragma unroll
+    for (int ql = 0; ql < QL; ++ql) {
+      const int64_t i = b0 + (int64_t)ql * WCH + EPL * lane;
+      uint32_t c[EPL];
+#pragma unroll
+      for (int e = 0; e < EPL; ++e) {
+        const float t = __builtin_amdgcn_fmed3f(v[ql][e] / sv[ql][e], -q, q);
+        c[e] = __float_as_uint(t + 12582912.0f) - 0x4B400000u;  // rne(t) as an int32 (|t| <= q < 2^22)
+      }
+      if (i < n) {
+#pragma unroll
+        for (int e = 0; e < EPL; e += 4)
+          *reinterpret_cast<u32x4*>(codes + i + e) = u32x4{c[e], c[e + 1], c[e + 2], c[e + 3]};
+      }
+    }
   }
 }
 
@@ -346,6 +423,37 @@ static int vec_run(const T* x, int64_t rows, int64_t cols, int axis, int bits, i
   const int64_t n = rows * cols;
   const float q = (float)((1u << (bits - 1)) - 1u);
   const int cap = num_cus() * 8;
+  constexpr int x_type = sizeof(T) == 4 ? MXK_IN_F32 : (std::is_same<T, __half>::value ? MXK_IN_F16 : MXK_IN_BF16);
+  // per row: the long-block row quantizer, one pass over x
+  if (axis == 1 && vec_rows_i32(x, x_type, rows, cols, bits, codes, scales, st)) return check_launch("vector_quantize");
+  // per column, whole 1024-column steps: column maxima in parts (held in
+  // the codes buffer, which the encode overwrites afterwards), then a
+  // vector encode
+  if (axis == 0 && aligned16(x) && cols % 1024 == 0 && (reinterpret_cast<uintptr_t>(codes) & 15u) == 0) {
+    constexpr int EPL = 16 / (int)sizeof(T);
+    const int64_t cus = num_cus();
+    float* part = reinterpret_cast<float*>(codes);
+    const int64_t col_blocks = ceil_div(cols / EPL, 256);
+    const int64_t chunks = std::max<int64_t>(
+        1, std::min<int64_t>({(int64_t)DYN_COL_PARTS, ceil_div(rows, 8), ceil_div(cus * 8, col_blocks)}));
+    const int64_t rows_per = ceil_div(rows, chunks);
+    const int64_t parts = ceil_div(rows, rows_per);
+    hipLaunchKernelGGL((k_absmax_cols_v<T>), dim3((unsigned)col_blocks, (unsigned)parts), dim3(256), 0, st, x, rows,
+                       cols, rows_per, part);
+    hipLaunchKernelGGL(k_dyn_scales_parts, dim3((unsigned)std::min<int64_t>(ceil_div(cols, 256), cus * 8)), dim3(256),
+                       0, st, part, parts, cols, q, scales, nullptr);
+    int64_t g = std::max<int64_t>(1, std::min<int64_t>(ceil_div(n, 4 * 1024), cus * 16));
+    const int64_t c1 = cols / 1024, m = c1 / std::__gcd<int64_t>(c1, 4);
+    if (m <= cus * 64) {
+      g = std::max<int64_t>(m, (g / m) * m);
+      hipLaunchKernelGGL((k_vec_encode_cols_v<T, true>), dim3((unsigned)g), dim3(256), 0, st, x, n, cols, scales, q,
+                         codes);
+    } else {
+      hipLaunchKernelGGL((k_vec_encode_cols_v<T, false>), dim3((unsigned)g), dim3(256), 0, st, x, n, cols, scales, q,
+                         codes);
+    }
+    return check_launch("vector_quantize");
+  }
   // the absmax bits accumulate in the scales buffer, which k_dyn_scales then
   // turns into the scales in place
   uint32_t* amax = reinterpret_cast<uint32_t*>(scales);
@@ -383,12 +491,6 @@ static bool dyn_vector_ok(const T* x, int64_t rows, int64_t cols, int granularit
   return granularity != MXK_DYN_PER_CHANNEL || cols % 1024 == 0;
 }
 
-// workspace of the vector path: scales' reciprocals (cnt words, padded to
-// 64), then the absmax parts: DYN_PARTS maxima per tensor, or DYN_COL_PARTS
-// rows of cols maxima per channel
-#define DYN_PARTS 1024
-#define DYN_COL_PARTS 128
-static int64_t dyn_pad(int64_t c) { return (c + 63) & ~(int64_t)63; }
 
 template <typename T>
 static int dyn_run_vector(const T* x, int64_t rows, int64_t cols, int granularity, int bits, uint8_t* packed,

@@ -161,6 +161,10 @@ __device__ __forceinline__ void store_bytes(uint8_t* __restrict__ dst, int64_t o
     else if constexpr (NB == 8) *reinterpret_cast<u32x2*>(dst + off) = u32x2{w[0], w[1]};
     else if constexpr (NB == 16)
       *reinterpret_cast<u32x4*>(dst + off) = u32x4{w[0], w[1], w[2], w[3]};
+    else if constexpr (NB == 32) {
+      *reinterpret_cast<u32x4*>(dst + off) = u32x4{w[0], w[1], w[2], w[3]};
+      *reinterpret_cast<u32x4*>(dst + off + 16) = u32x4{w[4], w[5], w[6], w[7]};
+    }
   } else {
     for (int b = 0; b < NB; ++b)
       if (off + b < limit) dst[off + b] = static_cast<uint8_t>(w[b >> 2] >> ((b & 3) * 8));
@@ -339,6 +343,13 @@ __device__ __forceinline__ float decode_field(uint32_t word, int sh, float s, co
     return (float)c * s;
   }
 }
+
+// vector_quantize per row (mxtorch.py:2946-2987: the 'v' rule with block =
+// row, int32 codes unpacked): launches the long-block row quantizer with
+// 32-bit fields when the shape suits it (16-byte aligned x and codes, rows
+// of 264..8192 elements, a multiple of 8); returns false otherwise.
+bool vec_rows_i32(const void* x, int x_type, int64_t rows, int64_t cols, int bits, int32_t* codes, float* scales,
+                  hipStream_t st);
 
 // 'v'-rule requantization of a float32 buffer (GEMM outputs), mxtorch.py:1372-1385.
 int requant_vec_f32(const float* x, int64_t n, int bits, int block, void* packed, int64_t packed_nbytes,

@@ -1035,6 +1035,20 @@ static int launch_dequant_had128(const void* packed, int64_t pbytes, const float
   return check_launch("dequantize(hadamard128)");
 }
 
+bool vec_rows_i32(const void* x, int x_type, int64_t rows, int64_t cols, int bits, int32_t* codes, float* scales,
+                  hipStream_t st) {
+  if ((reinterpret_cast<uintptr_t>(codes) & 15u) != 0) return false;
+  const float qf = (float)((1u << (bits - 1)) - 1u);
+  const int64_t n = rows * cols;
+  if (cols > 8192) return false;
+  uint8_t* pk = reinterpret_cast<uint8_t*>(codes);
+  if (x_type == MXK_IN_F32)
+    return try_rows<float, Q_VEC, 32>((const float*)x, n, rows, (int)cols, pk, n * 4, n, scales, qf, st);
+  if (x_type == MXK_IN_F16)
+    return try_rows<__half, Q_VEC, 32>((const __half*)x, n, rows, (int)cols, pk, n * 4, n, scales, qf, st);
+  return try_rows<hip_bfloat16, Q_VEC, 32>((const hip_bfloat16*)x, n, rows, (int)cols, pk, n * 4, n, scales, qf, st);
+}
+
 int requant_vec_f32(const float* x, int64_t n, int bits, int block, void* packed, int64_t packed_nbytes,
                     float* scales, int64_t n_store, void* ws, size_t ws_bytes, hipStream_t st) {
   return quantize_t<float>(x, n, MXK_KIND_INT, bits, MXK_VAR_VECTOR, block, reinterpret_cast<uint8_t*>(packed),

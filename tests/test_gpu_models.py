@@ -222,6 +222,28 @@ def test_vector_quantize_matches_reference(qa, case):
     assert _bits_eq(qa.vector_dequantize(codes, scales, axis=case["axis"]), G.get(case["key"] + "/dequant"))
 
 
+@pytest.mark.parametrize("shape,axis", [((256, 1024), 1), ((64, 8192), 1), ((33, 4104), 1), ((2048, 3072), 0),
+                                        ((100, 2048), 0), ((7, 1024), 0)])
+@pytest.mark.parametrize("xdt", [torch.float32, torch.bfloat16, torch.float16])
+def test_vector_quantize_fast_paths(qa, shape, axis, xdt):
+    """Rows of 264..8192 elements (a multiple of 8) take the row quantizer
+    with 32-bit codes; rows of a multiple of 1024 columns take the column
+    maxima and vector encode per column: codes and scales bit for bit, with
+    an all-zero row and column and values below 2^-96 mixed in."""
+    g = torch.Generator()
+    g.manual_seed(11 + shape[1])
+    x = torch.randn(*shape, generator=g) * 3
+    x.view(-1)[::89] *= 1e-33
+    x[1] = 0.0
+    x[:, 3] = 0.0
+    x = x.to(xdt)
+    for name in ("int8d", "int4d", "int16d"):
+        codes, scales = qa.vector_quantize(x.to(dev()), name, axis=axis)
+        c_ref, s_ref = orc.vector_quantize(x, name, axis)
+        assert torch.equal(codes.cpu(), c_ref), name
+        assert _bits_eq(scales, s_ref), name
+
+
 @pytest.mark.parametrize("axis", [0, 1])
 @pytest.mark.parametrize("xdt", [torch.float32, torch.float16, torch.bfloat16])
 def test_vector_quantize_vs_oracle(qa, axis, xdt):
