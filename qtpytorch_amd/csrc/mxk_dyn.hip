@@ -417,6 +417,41 @@ __global__ __launch_bounds__(256) void k_vec_decode(const int32_t* __restrict__ 
     out[j] = (float)codes[j] * scales[PER_ROW ? j / C : j % C];
 }
 
+// vector_dequantize with cols % 4 == 0 and 16-byte aligned buffers: a wave
+// takes 1024 consecutive codes per step (load q of lane l: the 4 codes at
+// 256 q + 4 l, so each load and store instruction covers whole lines); the
+// 4 codes of a load share a row and lie in consecutive columns.
+template <bool PER_ROW>
+__global__ __launch_bounds__(256) void k_vec_decode_v(const int32_t* __restrict__ codes, int64_t n, int64_t C,
+                                                      const float* __restrict__ scales, float* __restrict__ out) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int64_t stride = (int64_t)gridDim.x * 4 * 1024;
+  for (int64_t b0 = ((int64_t)blockIdx.x * 4 + wave) * 1024; b0 < n; b0 += stride) {
+    u32x4 cv[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int64_t i = b0 + 256 * q + 4 * lane;
+      cv[q] = i < n ? __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(codes + i)) : u32x4{0u, 0u, 0u, 0u};
+    }
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int64_t i = b0 + 256 * q + 4 * lane;
+      if (i >= n) continue;
+      const int64_t r = i / C, c = i - r * C;
+      f32x4v sv;
+      if constexpr (PER_ROW) {
+        const float sc = scales[r];
+        sv = f32x4v{sc, sc, sc, sc};
+      } else {
+        sv = *reinterpret_cast<const f32x4v*>(scales + c);
+      }
+      const f32x4v o = {(float)(int32_t)cv[q][0] * sv[0], (float)(int32_t)cv[q][1] * sv[1],
+                        (float)(int32_t)cv[q][2] * sv[2], (float)(int32_t)cv[q][3] * sv[3]};
+      __builtin_nontemporal_store(o, reinterpret_cast<f32x4v*>(out + i));
+    }
+  }
+}
+
 template <typename T>
 static int vec_run(const T* x, int64_t rows, int64_t cols, int axis, int bits, int32_t* codes, float* scales,
                    hipStream_t st) {
@@ -661,6 +696,12 @@ int mxk_vector_dequantize(const int32_t* codes, const float* scales, int64_t row
   if (!codes || !scales || !out) return fail(MXK_EINVAL, "vector_dequantize: null buffer");
   if (axis != 0 && axis != 1) return fail(MXK_EINVAL, "vector_dequantize: axis must be 0 or 1");
   const int64_t n = rows * cols;
+  if (cols % 4 == 0 && aligned16(codes) && aligned16(out) && aligned16(scales)) {
+    const dim3 gv((unsigned)std::max<int64_t>(1, std::min<int64_t>(ceil_div(n, 4 * 1024), (int64_t)num_cus() * 16)));
+    if (axis == 1) hipLaunchKernelGGL(k_vec_decode_v<true>, gv, dim3(256), 0, st, codes, n, cols, scales, out);
+    else hipLaunchKernelGGL(k_vec_decode_v<false>, gv, dim3(256), 0, st, codes, n, cols, scales, out);
+    return check_launch("vector_dequantize");
+  }
   const dim3 g((unsigned)std::min<int64_t>(ceil_div(n, 256), (int64_t)num_cus() * 32));
   if (axis == 1) hipLaunchKernelGGL(k_vec_decode<true>, g, dim3(256), 0, st, codes, n, cols, scales, out);
   else hipLaunchKernelGGL(k_vec_decode<false>, g, dim3(256), 0, st, codes, n, cols, scales, out);

@@ -242,6 +242,7 @@ def test_vector_quantize_fast_paths(qa, shape, axis, xdt):
         c_ref, s_ref = orc.vector_quantize(x, name, axis)
         assert torch.equal(codes.cpu(), c_ref), name
         assert _bits_eq(scales, s_ref), name
+        assert _bits_eq(qa.vector_dequantize(codes, scales, axis=axis), orc.vector_dequantize(c_ref, s_ref, axis)), name
 
 
 @pytest.mark.parametrize("axis", [0, 1])
