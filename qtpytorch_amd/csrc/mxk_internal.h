@@ -60,15 +60,20 @@ __device__ __forceinline__ float div_rn_nochk(float a, float b, float y) {
 // v[i] = RN(v[i] / b) for E values and b > 0: one wave-wide vote on the
 // smallest nonzero magnitude picks the Markstein path for the whole wave, or
 // the hardware divide when any lane holds a nonzero value below 2^-96.
+// (bits << 1) - 1 orders the nonzero magnitudes and sends both zeros to
+// 0xFFFFFFFF, so its minimum is below 2 * bits(2^-96) - 1 exactly when some
+// value has 0 < |v| < 2^-96; true when any lane of the wave holds one.
+template <int E>
+__device__ __forceinline__ bool any_tiny(const float (&v)[E]) {
+  uint32_t mnb = 0xFFFFFFFFu;
+#pragma unroll
+  for (int i = 0; i < E; ++i) mnb = min(mnb, (__float_as_uint(v[i]) << 1) - 1u);
+  return __ballot(mnb < 2u * 0x0F800000u - 1u) != 0ull;
+}
+
 template <int E>
 __device__ __forceinline__ void div_rn_all(float (&v)[E], float b, float y) {
-  float mn = __builtin_inff();
-#pragma unroll
-  for (int i = 0; i < E; ++i) {
-    const float t = __builtin_fabsf(v[i]);
-    mn = fminf(mn, t == 0.0f ? __builtin_inff() : t);
-  }
-  if (__builtin_expect(__ballot(mn < 0x1p-96f) != 0ull, 0)) {
+  if (__builtin_expect(any_tiny<E>(v), 0)) {
 #pragma unroll
     for (int i = 0; i < E; ++i) v[i] = v[i] / b;
   } else {
@@ -325,6 +330,14 @@ __device__ __forceinline__ int encode(float v, const BlockParams& bp, float qf, 
   } else {
     return bucket<BITS>(div_rn(v, bp.s, bp.mul), P);
   }
+}
+
+// The 'v' rule over E values of a block at once: the quotients RN(v / s)
+// with one wave-wide vote for the division path (div_rn_all), then
+// encode_vec_q encodes a quotient exactly as encode<Q_VEC> encodes the value.
+__device__ __forceinline__ int encode_vec_q(float u, float qf) {
+  const float t = __builtin_amdgcn_fmed3f(u, -qf, qf);
+  return (int)(__float_as_uint(t + 12582912.0f) - 0x4B400000u);
 }
 
 // ---------------------------------------------------------------- decode
