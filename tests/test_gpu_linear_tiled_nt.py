@@ -206,3 +206,36 @@ def test_tiled_nt_fallback_for_other_shapes(qa):
         assert x.shape[0] > 16 or x.data_ptr() % 16 != 0
         y = qa.ops.linear_wq_nt(x, wpg, wsg, "int4d", N, K, 128, w_scales_t=st, w_tiled=wt).cpu()
         assert _rowwise_ok(y, orc.dynamic_linear_forward(x.cpu(), wp, ws, "int4d", K, N, 128))[0]
+
+
+def _sweep_shapes(seed, count):
+    g = np.random.default_rng(seed)
+    out = []
+    for _ in range(count):
+        M = int(g.integers(1, 17))
+        K = int(g.integers(1, 49)) * 128
+        N = int(g.integers(1, 17)) * 128
+        out.append((M, K, N))
+    return out
+
+
+@pytest.mark.parametrize("M,K,N", _sweep_shapes(2024, 12))
+def test_tiled_decodes_random_shapes(qa, M, K, N):
+    """Seeded random decode shapes (M 1..16, K and N multiples of 128) through
+    both tiled kernels: mx_linear's [K][N] path (x @ dequant(W)) and the
+    [N][K] path (x @ dequant(W)^T), each within the bar of the oracle."""
+    print(f"random tiled shapes M={M} K={K} N={N}", flush=True)
+    x = _randn((M, K), 97 + M + K)
+    # [N][K] weight, blocks along K
+    wp, ws, wpg, wsg, st, wt = _weights(qa, N, K, 101 + N)
+    y = qa.ops.linear_wq_nt(x.to(dev()), wpg, wsg, "int4d", N, K, 128, w_scales_t=st, w_tiled=wt).cpu()
+    ok, worst = _rowwise_ok(y, orc.dynamic_linear_forward(x, wp, ws, "int4d", K, N, 128))
+    assert ok, f"[N][K] tiled: worst row error {worst:.3g} x the bar"
+    # [K][N] weight of quantize(W.t()), blocks along N
+    W = _randn((N, K), 103 + K, outliers=1e-3) * 0.02
+    fp, fs, _ = orc.linear_from_weight(W, "int4d", 128)
+    fpg, fsg = fp.to(dev()), fs.to(dev())
+    y2 = qa.ops.linear_wq(x.to(dev()), fpg, fsg, "int4d", K, N, 128, w_scales_t=qa.ops.prepack_scales(fsg, K, N, 128),
+                          w_tiled=qa.ops.prepack_weight(fpg, K, N, 128)).cpu()
+    ok, worst = _rowwise_ok(y2, orc.linear_forward(x, fp, fs, "int4d", K, N, 128))
+    assert ok, f"[K][N] tiled: worst row error {worst:.3g} x the bar"
