@@ -209,7 +209,8 @@ def test_hadamard_rows128_dequant(qa, dtype):
     assert _bits_eq(dq, rdq)
 
 
-@pytest.mark.parametrize("dtype", ["float8d", "float4d", "int8d", "int4d", "int2d", "int1d", "float8dh"])
+@pytest.mark.parametrize("dtype", ["float8d", "float4d", "int8d", "int4d", "int2d", "int1d", "float8dh", "int8dh",
+                                   "int4dh"])
 def test_dequant_every_code(qa, dtype):
     """Every byte value 0..255 (so every code of every width, and every pair
     of 4-bit codes) in every position of a slot, against the oracle's grid
