@@ -288,18 +288,22 @@ __device__ __forceinline__ BlockParams block_params(float ap, float qf) {
   return bp;
 }
 
-// bucket<4> without the table: the positive mids of the normalized E2M1
-// grid are constants, RN((g[j-1] + g[j]) * 0.5) with g[c] = RN(v_c / 6) in
-// float32, the values build_tables computes.  #{mids < a} comes from a
-// binary search over them (three comparisons, selects, no LDS); for y <= 0
-// the count of mids <= |y| is the count of mids < nextup(|y|).  Equal to
+// The positive mids of the normalized E2M1 grid: RN((g[j-1] + g[j]) * 0.5)
+// with g[c] = RN(v_c / 6) in float32, the values build_tables computes.
+namespace fp4c {
+constexpr float g1 = 0.5f / 6.0f, g2 = 1.0f / 6.0f, g3 = 1.5f / 6.0f, g4 = 2.0f / 6.0f, g5 = 3.0f / 6.0f,
+                g6 = 4.0f / 6.0f, g7 = 6.0f / 6.0f;
+constexpr float P1 = (0.0f + g1) * 0.5f, P2 = (g1 + g2) * 0.5f, P3 = (g2 + g3) * 0.5f, P4 = (g3 + g4) * 0.5f,
+                P5 = (g4 + g5) * 0.5f, P6 = (g5 + g6) * 0.5f, P7 = (g6 + g7) * 0.5f;
+}  // namespace fp4c
+
+// bucket<4> without the table: #{mids < a} comes from a binary search over
+// the constant mids (three comparisons, selects, no LDS); for y <= 0 the
+// count of mids <= |y| is the count of mids < nextup(|y|).  Equal to
 // bucket<4> for every finite y (checked exhaustively over all float32
 // patterns); a NaN takes the last index, as torch.bucketize gives it.
 __device__ __forceinline__ int bucket_fp4(float y) {
-  constexpr float g1 = 0.5f / 6.0f, g2 = 1.0f / 6.0f, g3 = 1.5f / 6.0f, g4 = 2.0f / 6.0f, g5 = 3.0f / 6.0f,
-                  g6 = 4.0f / 6.0f, g7 = 6.0f / 6.0f;
-  constexpr float P1 = (0.0f + g1) * 0.5f, P2 = (g1 + g2) * 0.5f, P3 = (g2 + g3) * 0.5f, P4 = (g3 + g4) * 0.5f,
-                  P5 = (g4 + g5) * 0.5f, P6 = (g5 + g6) * 0.5f, P7 = (g6 + g7) * 0.5f;
+  using namespace fp4c;
   const float a0 = __builtin_fabsf(y);
   const bool pos = !(y <= 0.0f);
   const float a = pos ? a0 : __uint_as_float(__float_as_uint(a0) + 1u);
@@ -308,6 +312,43 @@ __device__ __forceinline__ int bucket_fp4(float y) {
   c += !(a <= (c ? P6 : P2)) ? 2 : 0;
   c += !(a <= (c == 6 ? P7 : (c == 4 ? P5 : (c == 2 ? P3 : P1)))) ? 1 : 0;
   return pos ? 8 + c : 7 - c;
+}
+
+// bucket<4> through a 32-entry LDS table keyed by the top 11 bits of the
+// magnitude: key k = clamp((bits >> 21) - 488, 0, 31) is a quarter binade
+// from 2^-5 on ([0, 1.25 * 2^-5) for k = 0, [7, inf] and NaN for k = 31),
+// and each key's interval holds at most one mid, so #{mids < a} =
+// T[k].x + (a > T[k].y) with T[k] = (#mids below the interval, the mid
+// inside it or +inf).  For y <= 0 it counts the mids below nextup(|y|), and
+// 8 + c / 7 - c are c ^ 8 / c ^ 7.  One LDS read and ~10 VALU per element
+// against ~15 for the search above (float4d quantize at 2^28: 265 -> 228 us).
+// Equal to bucket_fp4 for every float32 pattern (checked exhaustively).
+constexpr int FP4_KEYS = 32;
+__device__ __forceinline__ void build_fp4_keys(int2* T) {
+  using namespace fp4c;
+  const float P[7] = {P1, P2, P3, P4, P5, P6, P7};
+  for (int k = threadIdx.x; k < FP4_KEYS; k += blockDim.x) {
+    const float lo = k == 0 ? 0.0f : __uint_as_float((uint32_t)(k + 488) << 21);
+    const float hi = k == FP4_KEYS - 1 ? __builtin_inff() : __uint_as_float((uint32_t)(k + 489) << 21);
+    int cnt = 0;
+    float mid = __builtin_inff();
+#pragma unroll
+    for (int j = 0; j < 7; ++j) {
+      if (P[j] < lo) ++cnt;
+      else if (P[j] < hi) mid = P[j];
+    }
+    T[k] = make_int2(cnt, __float_as_int(mid));
+  }
+  __syncthreads();
+}
+
+__device__ __forceinline__ int bucket_fp4_keyed(float y, const int2* __restrict__ T) {
+  const bool pos = !(y <= 0.0f);
+  const uint32_t ab = (__float_as_uint(y) & 0x7FFFFFFFu) + (pos ? 0u : 1u);
+  const int k = min(max((int)(ab >> 21) - 488, 0), FP4_KEYS - 1);
+  const int2 e = T[k];
+  const int c = e.x + (__uint_as_float(ab) > __int_as_float(e.y) ? 1 : 0);
+  return c ^ (pos ? 8 : 7);
 }
 
 template <int MODE, int BITS>
@@ -330,6 +371,14 @@ __device__ __forceinline__ int encode(float v, const BlockParams& bp, float qf, 
   } else {
     return bucket<BITS>(div_rn(v, bp.s, bp.mul), P);
   }
+}
+
+// encode<> with FP4 codes through the key table of build_fp4_keys (T
+// unused for the other formats)
+template <int MODE, int BITS>
+__device__ __forceinline__ int encode_keyed(float v, const BlockParams& bp, float qf, const float* P, const int2* T) {
+  if constexpr (MODE == Q_FP && BITS == 4) return bucket_fp4_keyed(div_rn(v, bp.s, bp.mul), T);
+  else return encode<MODE, BITS>(v, bp, qf, P);
 }
 
 // The 'v' rule over E values of a block at once: the quotients RN(v / s)

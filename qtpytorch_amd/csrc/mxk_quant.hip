@@ -78,7 +78,9 @@ __global__ __launch_bounds__(256) void k_quant_fast(const T* __restrict__ x, int
   constexpr uint32_t MASK = BITS == 32 ? 0xFFFFFFFFu : ((1u << BITS) - 1u);
   constexpr int H = MODE == Q_FP ? (1 << (BITS - 1)) : 1;
   __shared__ float sP[H + 1];
-  if constexpr (MODE == Q_FP && BITS != 4) build_tables<BITS>(sP, nullptr);  // FP4 buckets by constants
+  __shared__ int2 sK[MODE == Q_FP && BITS == 4 ? FP4_KEYS : 1];
+  if constexpr (MODE == Q_FP && BITS != 4) build_tables<BITS>(sP, nullptr);
+  if constexpr (MODE == Q_FP && BITS == 4) build_fp4_keys(sK);
 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int g = lane / LPB, li = lane % LPB;
@@ -126,7 +128,7 @@ __global__ __launch_bounds__(256) void k_quant_fast(const T* __restrict__ x, int
 #pragma unroll
       for (int i = 0; i < CH; ++i) {
         const uint32_t f =
-            (uint32_t)(VOTE ? encode_vec_q(v[q][i], qf) : encode<MODE, BITS>(v[q][i], bp, qf, sP)) & MASK;
+            (uint32_t)(VOTE ? encode_vec_q(v[q][i], qf) : encode_keyed<MODE, BITS>(v[q][i], bp, qf, sP, sK)) & MASK;
         w[(i * BITS) >> 5] |= f << ((i * BITS) & 31);
       }
       if (idx + CH > n_store) clear_tail<NW, BITS>(w, n_store - idx);
@@ -380,7 +382,9 @@ __global__ __launch_bounds__(256) void k_quant_had128(const T* __restrict__ x, i
   constexpr int H = MODE == Q_FP ? (1 << (BITS - 1)) : 1;
   __shared__ float sP[H + 1];
   __shared__ __attribute__((aligned(16))) float srow[GPB * MXK_ROWPAD];
-  if constexpr (MODE == Q_FP && BITS != 4) build_tables<BITS>(sP, nullptr);  // FP4 buckets by constants
+  if constexpr (MODE == Q_FP && BITS != 4) build_tables<BITS>(sP, nullptr);
+  __shared__ int2 sK[MODE == Q_FP && BITS == 4 ? FP4_KEYS : 1];
+  if constexpr (MODE == Q_FP && BITS == 4) build_fp4_keys(sK);
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int g = lane / LPB, li = lane % LPB;
   float* row = srow + (wave * GPW + g) * MXK_ROWPAD;
@@ -440,7 +444,7 @@ __global__ __launch_bounds__(256) void k_quant_had128(const T* __restrict__ x, i
     for (int k = 0; k < NW; ++k) w[k] = 0u;
 #pragma unroll
     for (int i = 0; i < E; ++i) {
-      const uint32_t f = (uint32_t)encode<MODE, BITS>(v[i], bp, qf, sP) & MASK;
+      const uint32_t f = (uint32_t)encode_keyed<MODE, BITS>(v[i], bp, qf, sP, sK) & MASK;
       w[(i * BITS) >> 5] |= f << ((i * BITS) & 31);
     }
     if (idx + E > n_store) clear_tail<NW, BITS>(w, n_store - idx);
