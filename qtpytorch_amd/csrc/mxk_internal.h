@@ -314,41 +314,68 @@ __device__ __forceinline__ int bucket_fp4(float y) {
   return pos ? 8 + c : 7 - c;
 }
 
-// bucket<4> through a 32-entry LDS table keyed by the top 11 bits of the
-// magnitude: key k = clamp((bits >> 21) - 488, 0, 31) is a quarter binade
-// from 2^-5 on ([0, 1.25 * 2^-5) for k = 0, [7, inf] and NaN for k = 31),
-// and each key's interval holds at most one mid, so #{mids < a} =
-// T[k].x + (a > T[k].y) with T[k] = (#mids below the interval, the mid
-// inside it or +inf).  For y <= 0 it counts the mids below nextup(|y|), and
-// 8 + c / 7 - c are c ^ 8 / c ^ 7.  One LDS read and ~10 VALU per element
-// against ~15 for the search above (float4d quantize at 2^28: 265 -> 228 us).
-// Equal to bucket_fp4 for every float32 pattern (checked exhaustively).
-constexpr int FP4_KEYS = 32;
-__device__ __forceinline__ void build_fp4_keys(int2* T) {
-  using namespace fp4c;
-  const float P[7] = {P1, P2, P3, P4, P5, P6, P7};
-  for (int k = threadIdx.x; k < FP4_KEYS; k += blockDim.x) {
-    const float lo = k == 0 ? 0.0f : __uint_as_float((uint32_t)(k + 488) << 21);
-    const float hi = k == FP4_KEYS - 1 ? __builtin_inff() : __uint_as_float((uint32_t)(k + 489) << 21);
+// bucket<BITS> through an LDS table keyed by the top bits of the
+// magnitude.  FP4: key k = clamp((bits >> 21) - 488, 0, 31), a quarter
+// binade from 2^-5 on ([0, 1.25 * 2^-5) for k = 0, [7, inf] and NaN for
+// k = 31).  FP8: k = clamp((bits >> 19) - 1728, 0, 304), a sixteenth of a
+// binade from 2^-19 on (below the smallest mid, 2^-9 / 960) up to [1, inf]
+// and NaN.  Each key's interval holds at most one mid (consecutive mids are
+// more than one key apart), so #{mids < a} = T[k].x + (a > T[k].y) with
+// T[k] = (#mids below the interval, the mid inside it or +inf).  For y <= 0
+// it counts the mids below nextup(|y|), and H + c / H - 1 - c are c ^ H /
+// c ^ (H - 1).  One LDS read and ~10 VALU per element against ~15 (FP4
+// search over constant mids) or ~18 (FP8 candidate and two mids); float4d
+// quantize at 2^28: 265 -> 228 us.  Equal to torch.bucketize over the mids
+// for every float32 pattern, NaN included (last index), checked exhaustively.
+template <int BITS> struct FpKeys;
+template <> struct FpKeys<4> { static constexpr int N = 32, SHIFT = 21, BASE = 488; };
+template <> struct FpKeys<8> { static constexpr int N = 305, SHIFT = 19, BASE = 1728; };
+
+// P: the positive mids at P[1..H-1] (build_tables<8>'s table; FP4 uses its
+// constants and ignores P)
+template <int BITS>
+__device__ __forceinline__ void build_fp_keys(int2* T, const float* P) {
+  constexpr int H = 1 << (BITS - 1);
+  using K = FpKeys<BITS>;
+  for (int k = threadIdx.x; k < K::N; k += blockDim.x) {
+    const float lo = k == 0 ? 0.0f : __uint_as_float((uint32_t)(k + K::BASE) << K::SHIFT);
+    const float hi = k == K::N - 1 ? __builtin_inff() : __uint_as_float((uint32_t)(k + K::BASE + 1) << K::SHIFT);
     int cnt = 0;
     float mid = __builtin_inff();
+    if constexpr (BITS == 4) {
+      using namespace fp4c;
+      const float Q[7] = {P1, P2, P3, P4, P5, P6, P7};
 #pragma unroll
-    for (int j = 0; j < 7; ++j) {
-      if (P[j] < lo) ++cnt;
-      else if (P[j] < hi) mid = P[j];
+      for (int j = 0; j < 7; ++j) {
+        if (Q[j] < lo) ++cnt;
+        else if (Q[j] < hi) mid = Q[j];
+      }
+    } else {
+      // cnt = #{P[1..H-1] < lo} by bisection over the sorted mids
+      int a = 0, b = H - 1;
+      while (a < b) {
+        const int m = (a + b + 1) >> 1;
+        if (P[m] < lo) a = m;
+        else b = m - 1;
+      }
+      cnt = a;
+      if (cnt + 1 <= H - 1 && P[cnt + 1] < hi) mid = P[cnt + 1];
     }
     T[k] = make_int2(cnt, __float_as_int(mid));
   }
   __syncthreads();
 }
 
-__device__ __forceinline__ int bucket_fp4_keyed(float y, const int2* __restrict__ T) {
+template <int BITS>
+__device__ __forceinline__ int bucket_keyed(float y, const int2* __restrict__ T) {
+  constexpr int H = 1 << (BITS - 1);
+  using K = FpKeys<BITS>;
   const bool pos = !(y <= 0.0f);
   const uint32_t ab = (__float_as_uint(y) & 0x7FFFFFFFu) + (pos ? 0u : 1u);
-  const int k = min(max((int)(ab >> 21) - 488, 0), FP4_KEYS - 1);
+  const int k = min(max((int)(ab >> K::SHIFT) - K::BASE, 0), K::N - 1);
   const int2 e = T[k];
   const int c = e.x + (__uint_as_float(ab) > __int_as_float(e.y) ? 1 : 0);
-  return c ^ (pos ? 8 : 7);
+  return c ^ (pos ? H : H - 1);
 }
 
 template <int MODE, int BITS>
@@ -373,12 +400,19 @@ __device__ __forceinline__ int encode(float v, const BlockParams& bp, float qf, 
   }
 }
 
-// encode<> with FP4 codes through the key table of build_fp4_keys (T
+// encode<> with float codes through the key table of build_fp_keys (T
 // unused for the other formats)
 template <int MODE, int BITS>
 __device__ __forceinline__ int encode_keyed(float v, const BlockParams& bp, float qf, const float* P, const int2* T) {
-  if constexpr (MODE == Q_FP && BITS == 4) return bucket_fp4_keyed(div_rn(v, bp.s, bp.mul), T);
+  if constexpr (MODE == Q_FP) return bucket_keyed<BITS>(div_rn(v, bp.s, bp.mul), T);
   else return encode<MODE, BITS>(v, bp, qf, P);
+}
+
+// LDS entries of a kernel's key table (1 when it encodes no float codes)
+template <int MODE, int BITS>
+constexpr int fp_keys_n() {
+  if constexpr (MODE == Q_FP) return FpKeys<BITS>::N;
+  else return 1;
 }
 
 // The 'v' rule over E values of a block at once: the quotients RN(v / s)

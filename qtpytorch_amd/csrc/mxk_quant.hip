@@ -78,9 +78,9 @@ __global__ __launch_bounds__(256) void k_quant_fast(const T* __restrict__ x, int
   constexpr uint32_t MASK = BITS == 32 ? 0xFFFFFFFFu : ((1u << BITS) - 1u);
   constexpr int H = MODE == Q_FP ? (1 << (BITS - 1)) : 1;
   __shared__ float sP[H + 1];
-  __shared__ int2 sK[MODE == Q_FP && BITS == 4 ? FP4_KEYS : 1];
+  __shared__ int2 sK[fp_keys_n<MODE, BITS>()];
   if constexpr (MODE == Q_FP && BITS != 4) build_tables<BITS>(sP, nullptr);
-  if constexpr (MODE == Q_FP && BITS == 4) build_fp4_keys(sK);
+  if constexpr (MODE == Q_FP) build_fp_keys<BITS>(sK, sP);
 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int g = lane / LPB, li = lane % LPB;
@@ -383,8 +383,8 @@ __global__ __launch_bounds__(256) void k_quant_had128(const T* __restrict__ x, i
   __shared__ float sP[H + 1];
   __shared__ __attribute__((aligned(16))) float srow[GPB * MXK_ROWPAD];
   if constexpr (MODE == Q_FP && BITS != 4) build_tables<BITS>(sP, nullptr);
-  __shared__ int2 sK[MODE == Q_FP && BITS == 4 ? FP4_KEYS : 1];
-  if constexpr (MODE == Q_FP && BITS == 4) build_fp4_keys(sK);
+  __shared__ int2 sK[fp_keys_n<MODE, BITS>()];
+  if constexpr (MODE == Q_FP) build_fp_keys<BITS>(sK, sP);
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int g = lane / LPB, li = lane % LPB;
   float* row = srow + (wave * GPW + g) * MXK_ROWPAD;

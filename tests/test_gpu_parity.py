@@ -537,18 +537,21 @@ def test_quantize_long_blocks(qa, name, block, n, src):
 
 
 @pytest.mark.parametrize("src", [torch.float32, torch.float16])
-def test_float4_bucket_boundaries(qa, src):
-    """float4d codes at every float32 within 2^13 ulps of each grid mid and of
-    each boundary of the keyed FP4 bucket (a quarter binade from 2^-5 on), in
-    both signs, plus zeros and subnormals.  Each block of 128 starts with 1.0,
-    so its scale is 1 and the bucket sees the value itself; codes and scales
-    bit-exact against the oracle's bucketize.  fp16 input covers the 16-bit
-    load path on the values fp16 can hold."""
-    mids = orc.float_mids(4).numpy()
+@pytest.mark.parametrize("bits", [4, 8])
+def test_float_bucket_boundaries(qa, src, bits):
+    """float4d/float8d codes at every float32 within 2^13 (FP4) or 2^9 (FP8)
+    ulps of each grid mid and of each key boundary of the keyed bucket, in
+    both signs, plus zeros and subnormals.  Each block of 128 starts with
+    1.0, so its scale is 1 and the bucket sees the value itself; codes and
+    scales bit-exact against the oracle's bucketize.  fp16 input covers the
+    16-bit load path on the values fp16 can hold."""
+    n_keys, shift, base = {4: (32, 21, 488), 8: (305, 19, 1728)}[bits]
+    mids = orc.float_mids(bits).numpy()
     pm = mids[mids > 0].astype(np.float32)
-    bounds = (((np.arange(1, 21, dtype=np.uint64) + 488) << 21).astype(np.uint32))
+    bounds = ((np.arange(1, n_keys, dtype=np.uint64) + base) << shift).astype(np.uint32)
     centers = np.concatenate([pm.view(np.uint32), bounds]).astype(np.int64)
-    off = np.arange(-(1 << 13), 1 << 13, dtype=np.int64)
+    radius = 1 << 13 if bits == 4 else 1 << 9
+    off = np.arange(-radius, radius, dtype=np.int64)
     near = (centers[:, None] + off[None, :]).reshape(-1)
     near = near[(near >= 0) & (near <= 0x3F800000)].astype(np.uint32)
     special = np.array([0, 1, 2, 0x007FFFFF, 0x00800000, 0x3F800000], dtype=np.uint32)
@@ -560,9 +563,10 @@ def test_float4_bucket_boundaries(qa, src):
     body[:vals.size] = vals
     x = np.concatenate([np.ones((nblk, 1), dtype=np.float32), body.reshape(nblk, per)], axis=1)
     xin = torch.from_numpy(x).to(src)
-    dt = qa.get_mx_dtype("float4d")
+    name = f"float{bits}d"
+    dt = qa.get_mx_dtype(name)
     packed, scales, n = qa.ops.quantize(xin.to(dev()), dt, 128)
-    rp, rs, rn = orc.quantize(xin, "float4d", 128)
+    rp, rs, rn = orc.quantize(xin, name, 128)
     assert n == rn
     assert _bits_eq(scales, rs), "scales differ"
     assert _bits_eq(packed, rp), "packed codes differ"
