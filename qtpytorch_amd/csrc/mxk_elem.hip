@@ -179,6 +179,23 @@ __device__ __forceinline__ void load_codes(__amdgpu_buffer_rsrc_t r, uint32_t of
   }
 }
 
+// RN(a / b) by Markstein's correction with y = RN(1/b), for callers whose
+// quotient is only rounded to an integer code afterwards: a zero quotient
+// may come out with either sign, which codes the same.  Exact unless
+// 0 < |a| < 2^-96 (the callers state why that cannot change a code).
+__device__ __forceinline__ float markstein(float a, float b, float y) {
+  const float q0 = a * y;
+  return __builtin_fmaf(__builtin_fmaf(-q0, b, a), y, q0);
+}
+
+// Bit pattern whose low bits are rne(clamp(q, -qf, qf)) in two's
+// complement: the float adder rounds t + 1.5 * 2^23 (|t| <= qf <= 2^15) to
+// an integer with ties to even, leaving 2^22 + 2^23 + rne(t) in the
+// significand.
+__device__ __forceinline__ uint32_t rne_clamped_bits(float q, float qf) {
+  return __float_as_uint(__builtin_amdgcn_fmed3f(q, -qf, qf) + 12582912.0f);
+}
+
 template <int OP, int BITS, int OB, int LPB, int E>
 __global__ __launch_bounds__(256) void k_qelem_fast(const uint8_t* __restrict__ a, int64_t a_nbytes,
                                                     const float* __restrict__ sa_, const uint8_t* __restrict__ b,
@@ -217,6 +234,7 @@ __global__ __launch_bounds__(256) void k_qelem_fast(const uint8_t* __restrict__ 
       }
     }
     float ac[E], bc[E], cv[E];
+    uint32_t cu[E];  // code bits (the low OB bits are the two's complement code)
 #pragma unroll
     for (int i = 0; i < E; ++i) {
       const int32_t ca = (int32_t)((uint32_t)(wa[(i * BITS) >> 6] >> ((i * BITS) & 63)) << (32 - BITS)) >> (32 - BITS);
@@ -230,7 +248,7 @@ __global__ __launch_bounds__(256) void k_qelem_fast(const uint8_t* __restrict__ 
       // the products are 0 or at least 1 in magnitude
       const float qinv = 1.0f / qf;
 #pragma unroll
-      for (int i = 0; i < E; ++i) cv[i] = rne(fminf(fmaxf(div_rn_nochk(ac[i] * bc[i], qf, qinv), -qf), qf));
+      for (int i = 0; i < E; ++i) cu[i] = rne_clamped_bits(markstein(ac[i] * bc[i], qf, qinv), qf);
       scale = (sa * sb) * qf;
     } else {
       const float hi = fmaxf(sa, sb);
@@ -260,7 +278,7 @@ __global__ __launch_bounds__(256) void k_qelem_fast(const uint8_t* __restrict__ 
           for (int i = 0; i < E; ++i) cv[i] = rne(ac[i] * ra_) + rne(bc[i] * rb_);
         }
 #pragma unroll
-        for (int i = 0; i < E; ++i) cv[i] = fminf(fmaxf(cv[i], -qf), qf);
+        for (int i = 0; i < E; ++i) cu[i] = (uint32_t)(int32_t)__builtin_amdgcn_fmed3f(cv[i], -qf, qf);
       } else {
         sc = fmaxf(m, MXK_AMIN) / qf;
         // RN(sum / sc) by Markstein's correction for every element, without
@@ -269,9 +287,7 @@ __global__ __launch_bounds__(256) void k_qelem_fast(const uint8_t* __restrict__ 
         // rounds to code 0 below
         const float y = 1.0f / sc;
 #pragma unroll
-        for (int i = 0; i < E; ++i) cv[i] = div_rn_nochk(cv[i], sc, y);
-#pragma unroll
-        for (int i = 0; i < E; ++i) cv[i] = rne(fminf(fmaxf(cv[i], -qf), qf));
+        for (int i = 0; i < E; ++i) cu[i] = rne_clamped_bits(markstein(cv[i], sc, y), qf);
       }
       scale = sc;
     }
@@ -279,7 +295,7 @@ __global__ __launch_bounds__(256) void k_qelem_fast(const uint8_t* __restrict__ 
 #pragma unroll
     for (int q = 0; q < (ONB + 3) / 4; ++q) w[q] = 0u;
 #pragma unroll
-    for (int i = 0; i < E; ++i) w[(i * OB) >> 5] |= ((uint32_t)(int32_t)cv[i] & OMASK) << ((i * OB) & 31);
+    for (int i = 0; i < E; ++i) w[(i * OB) >> 5] |= (cu[i] & OMASK) << ((i * OB) & 31);
     if (live) {
       store_bytes<ONB>(out, e0 * OB / 8, out_nbytes, w);
       if (li == 0) out_scales[blk] = scale;
