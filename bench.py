@@ -3,8 +3,9 @@
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-extras] [--no-cpu]
 
 Headline (the JSON line's `value`): config 2 of the benchmark
-configurations, the int4d weight-only linear at decode shape — x fp32 [16, 8192] ~ N(0,1), W
-[8192 (out), 8192 (in)] ~ 0.02 N(0,1) with 0.1% outliers x20, stored as
+configurations, the int4d weight-only linear at decode shape — x fp32
+[16, 8192] ~ N(0,1), W [8192 (out), 8192 (in)] ~ 0.02 N(0,1) with 0.1%
+outliers x20, stored as
 quantize(W.t()) int4d block 128 — one step = one mx_linear forward (one
 fused kernel).  `value` = algorithmic bytes per step (packed weights 32 MiB +
 scales 2 MiB + x + y = 36,700,160 B) / time per step, in GB/s.  The
@@ -15,8 +16,9 @@ the timed region.
 Timing: W warm-up steps, then K steps captured into one HIP graph, untimed
 warm replays of it (at least 3, for at least 50 ms), then one replay
 between two HIP events recorded on the stream the kernels run on (torch's
-current stream), synchronize on both sides; inputs are resident in HBM.  ms_per_step = elapsed / K.  Step i runs layer i % 12 of twelve
-identical quantized layers (12 x 34 MiB of weights and scales, more than the
+current stream), synchronize on both sides; inputs are resident in HBM.
+ms_per_step = elapsed / K.  Step i runs layer i % 12 of twelve identical
+quantized layers (12 x 34 MiB of weights and scales, more than the
 256 MiB last-level cache), so every step streams its weights from HBM rather
 than from the previous step's cache lines.
 
