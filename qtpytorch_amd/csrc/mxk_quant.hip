@@ -692,7 +692,9 @@ __global__ __launch_bounds__(256) void k_dequant_had128(const uint8_t* __restric
   constexpr int H = MODE == Q_FP ? (1 << (BITS - 1)) : 1;
   __shared__ float sG[2 * H];
   __shared__ __attribute__((aligned(16))) float srow[GPB * MXK_ROWPAD];
-  if constexpr (MODE == Q_FP && BITS != 8) build_tables<BITS>(nullptr, sG);
+  // FP8 grid values from the table here (the arithmetic decode costs ~14
+  // VALU per code, a quarter of this kernel's work per element)
+  if constexpr (MODE == Q_FP) build_tables<BITS>(nullptr, sG);
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int g = lane / LPB, li = lane % LPB;
   float* row = srow + (wave * GPW + g) * MXK_ROWPAD;
@@ -739,8 +741,13 @@ __global__ __launch_bounds__(256) void k_dequant_had128(const uint8_t* __restric
       wave_lds_sync();
 #pragma unroll
       for (int c = 0; c < 8; ++c) {
-        v[2 * c] = decode_field<MODE, BITS>(hw[c], 0, s, sG);
-        v[2 * c + 1] = decode_field<MODE, BITS>(hw[c], 8, s, sG);
+        if constexpr (MODE == Q_FP) {
+          v[2 * c] = sG[hw[c] & 0xFFu] * s;
+          v[2 * c + 1] = sG[(hw[c] >> 8) & 0xFFu] * s;
+        } else {
+          v[2 * c] = decode_field<MODE, BITS>(hw[c], 0, s, sG);
+          v[2 * c + 1] = decode_field<MODE, BITS>(hw[c], 8, s, sG);
+        }
       }
     } else {
       // word (8j * BITS) / 32 of the row holds position li + 8j; every lane
