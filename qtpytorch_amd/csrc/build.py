@@ -21,7 +21,7 @@ import sys
 HERE = os.path.dirname(os.path.abspath(__file__))
 PKG = os.path.dirname(HERE)
 OUT = os.path.join(PKG, "libmxk.so")
-SOURCES = ["mxk_quant.hip", "mxk_gemm.hip", "mxk_linear.hip", "mxk_kv.hip", "mxk_elem.hip", "mxk_dyn.hip"]
+SOURCES = ["mxk_quant.hip", "mxk_gemm.hip", "mxk_linear.hip", "mxk_linear_mfma.hip", "mxk_kv.hip", "mxk_elem.hip", "mxk_dyn.hip"]
 
 HIPCC_FLAGS = [
     "--offload-arch=gfx950",

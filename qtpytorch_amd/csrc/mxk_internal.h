@@ -447,6 +447,19 @@ __device__ __forceinline__ float decode_field(uint32_t word, int sh, float s, co
 bool vec_rows_i32(const void* x, int x_type, int64_t rows, int64_t cols, int bits, int32_t* codes, float* scales,
                   hipStream_t st);
 
+// MFMA weight-only linear (mxk_linear_mfma.hip) for int4/int8 weights with
+// blocks of 128 and N a multiple of 128: [K][N] weights (mx_linear) and
+// [N][K] weights (K a multiple of 128).  Workspace bytes (0 when the shape is
+// not taken; the first 64 KiB are left untouched), and the products, which
+// return MXK_EUNSUPPORTED with nothing launched for shapes they do not take.
+size_t linear_mfma_workspace(int64_t M, int64_t K, int64_t N, int bits, int block, bool nk);
+int linear_mfma_kn(const void* x, int x_type, int64_t M, int64_t K, const void* w_packed, const float* w_scales,
+                   const float* w_scales_t, int64_t N, int kind, int bits, int block, const float* bias, float* out,
+                   void* workspace, size_t workspace_nbytes, hipStream_t st);
+int linear_mfma_nk(const void* x, int x_type, int64_t M, int64_t K, const void* w_packed, const float* w_scales,
+                   const float* w_scales_t, int64_t N, int kind, int bits, int block, const float* bias, float* out,
+                   void* workspace, size_t workspace_nbytes, hipStream_t st);
+
 // 'v'-rule requantization of a float32 buffer (GEMM outputs), mxtorch.py:1372-1385.
 int requant_vec_f32(const float* x, int64_t n, int bits, int block, void* packed, int64_t packed_nbytes,
                     float* scales, int64_t n_store, void* ws, size_t ws_bytes, hipStream_t st);

@@ -1764,12 +1764,14 @@ using namespace mxk;
 extern "C" {
 
 size_t mxk_linear_workspace(int64_t M, int64_t K, int64_t N, int bits, int block) {
-  if (M < 1 || M > 16 || bits != 4 || block != 128 || K <= 0 || N <= 0 || K % 32 != 0 || N % 128 != 0) return 0;
+  // the MFMA path (any M, int4/int8 codes); its buffers start past the decode counters
+  const size_t c = M > 0 && K > 0 && N > 0 ? linear_mfma_workspace(M, K, N, bits, block, false) : 0;
+  if (M < 1 || M > 16 || bits != 4 || block != 128 || K <= 0 || N <= 0 || K % 32 != 0 || N % 128 != 0) return c;
   // enough for mxk_linear_wq's decode path and for mxk_linear_wq_tiled
   const DecodePlan p = plan_decode(K, N), q = plan_decode_tiled(K, N);
   const size_t a = p.S <= 255 ? p.counter_bytes + p.partial_bytes + p.scales_t_bytes : 0;  // else generic kernel
   const size_t b = q.S <= 255 ? q.counter_bytes + q.partial_bytes : 0;
-  return std::max(a, b);
+  return std::max(std::max(a, b), c);
 }
 
 int mxk_linear_prepack_weight(const void* w_packed, int64_t K, int64_t N, int bits, int block, void* w_tiled,
@@ -1824,9 +1826,12 @@ int mxk_linear_prepack_scales(const float* w_scales, int64_t K, int64_t N, int b
   return check_launch("linear_prepack_scales");
 }
 
-int mxk_linear_wq(const void* x, int x_type, int64_t M, int64_t K, const void* w_packed, const float* w_scales,
-                  const float* w_scales_t, int64_t N, int kind, int bits, int block, const float* bias, float* out,
-                  void* workspace, size_t workspace_nbytes, void* stream) {
+// mxk_linear_wq with the MFMA path switched on or off (off: the
+// allocation-free entry when its scratch is too small for that path)
+static int linear_wq_impl(const void* x, int x_type, int64_t M, int64_t K, const void* w_packed,
+                          const float* w_scales, const float* w_scales_t, int64_t N, int kind, int bits, int block,
+                          const float* bias, float* out, void* workspace, size_t workspace_nbytes, void* stream,
+                          bool mfma) {
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   if (M <= 0 || K <= 0 || N <= 0 || block <= 0) return fail(MXK_EINVAL, "linear_wq: sizes must be positive");
   if (!x || !w_packed || !w_scales || !out) return fail(MXK_EINVAL, "linear_wq: null pointer");
@@ -1850,6 +1855,11 @@ int mxk_linear_wq(const void* x, int x_type, int64_t M, int64_t K, const void* w
     else launch_decode<hip_bfloat16>(p, st, x, M, K, N, wq, sT, bias, out, partials, counters);
     return check_launch("linear_wq(decode)");
   }
+  if (mfma) {
+    const int rc = linear_mfma_kn(x, x_type, M, K, w_packed, w_scales, w_scales_t, N, kind, bits, block, bias, out,
+                                  workspace, workspace_nbytes, st);
+    if (rc != MXK_EUNSUPPORTED) return rc;
+  }
   const int64_t nb = ceil_div(K * N, block);
   const int64_t pbytes = mxk_packed_nbytes(bits, nb * block);
   const uint8_t* pk = reinterpret_cast<const uint8_t*>(w_packed);
@@ -1863,6 +1873,13 @@ int mxk_linear_wq(const void* x, int x_type, int64_t M, int64_t K, const void* w
   return fail(MXK_EINVAL, "linear_wq: bad input type");
 }
 
+int mxk_linear_wq(const void* x, int x_type, int64_t M, int64_t K, const void* w_packed, const float* w_scales,
+                  const float* w_scales_t, int64_t N, int kind, int bits, int block, const float* bias, float* out,
+                  void* workspace, size_t workspace_nbytes, void* stream) {
+  return linear_wq_impl(x, x_type, M, K, w_packed, w_scales, w_scales_t, N, kind, bits, block, bias, out, workspace,
+                        workspace_nbytes, stream, true);
+}
+
 int mxk_linear_wq_noalloc(const void* x, int x_type, int64_t M, int64_t K, const void* w_packed,
                           const float* w_scales, const float* w_scales_t, int64_t N, int kind, int bits, int block,
                           const float* bias, float* out, void* stream) {
@@ -1870,24 +1887,33 @@ int mxk_linear_wq_noalloc(const void* x, int x_type, int64_t M, int64_t K, const
   if (M <= 0 || K <= 0 || N <= 0 || block <= 0) return fail(MXK_EINVAL, "linear_wq_noalloc: sizes must be positive");
   if (!x || !w_packed || !w_scales || !out) return fail(MXK_EINVAL, "linear_wq_noalloc: null pointer");
   size_t need = 0;
+  bool mfma = false;
   if (decode_eligible(M, K, N, kind, bits, block, x, x_type, w_packed)) {
     const DecodePlan p = plan_decode(K, N);
     need = p.counter_bytes + p.partial_bytes + (w_scales_t ? 0 : p.scales_t_bytes);
+    if (need > NOALLOC_SCRATCH_BYTES)
+      return fail(MXK_EINVAL, "linear_wq_noalloc: this shape needs " + std::to_string(need) +
+                                  " bytes of split-K workspace, more than the " +
+                                  std::to_string(NOALLOC_SCRATCH_BYTES) +
+                                  "-byte static scratch (pass w_scales_t, or use mxk_linear_wq with a workspace)");
+  } else if (kind == MXK_KIND_INT) {
+    // the MFMA path when its buffers fit the scratch; the generic kernel otherwise
+    const size_t m = linear_mfma_workspace(M, K, N, bits, block, false);
+    if (m > 0 && m <= NOALLOC_SCRATCH_BYTES) {
+      need = m;
+      mfma = true;
+    }
   }
-  if (need > NOALLOC_SCRATCH_BYTES)
-    return fail(MXK_EINVAL, "linear_wq_noalloc: this shape needs " + std::to_string(need) +
-                                " bytes of split-K workspace, more than the " +
-                                std::to_string(NOALLOC_SCRATCH_BYTES) +
-                                "-byte static scratch (pass w_scales_t, or use mxk_linear_wq with a workspace)");
   void* ws = nullptr;
   if (need > 0 && !(ws = noalloc_scratch(st))) return MXK_ELAUNCH;
-  return mxk_linear_wq(x, x_type, M, K, w_packed, w_scales, w_scales_t, N, kind, bits, block, bias, out, ws,
-                       need > 0 ? NOALLOC_SCRATCH_BYTES : 0, stream);
+  return linear_wq_impl(x, x_type, M, K, w_packed, w_scales, w_scales_t, N, kind, bits, block, bias, out, ws,
+                        need > 0 ? NOALLOC_SCRATCH_BYTES : 0, stream, mfma);
 }
 
 size_t mxk_linear_nt_workspace(int64_t M, int64_t K, int64_t N, int bits, int block) {
-  if (M < 1 || M > 16 || bits != 4 || block != 128 || K <= 0 || N <= 0 || K % 128 != 0 || N % 16 != 0) return 0;
-  return nt_workspace_bytes(K, N);
+  const size_t c = M > 0 && K > 0 && N > 0 ? linear_mfma_workspace(M, K, N, bits, block, true) : 0;
+  if (M < 1 || M > 16 || bits != 4 || block != 128 || K <= 0 || N <= 0 || K % 128 != 0 || N % 16 != 0) return c;
+  return std::max(nt_workspace_bytes(K, N), c);
 }
 
 int mxk_linear_wq_nt(const void* x, int x_type, int64_t M, int64_t K, const void* w_packed, int64_t w_nbytes,
@@ -1914,6 +1940,11 @@ int mxk_linear_wq_nt(const void* x, int x_type, int64_t M, int64_t K, const void
       return launch_nt_decode((const __half*)x, M, K, N, pk, sc, kbm, bias, out, part, st);
     if (x_type == MXK_IN_BF16)
       return launch_nt_decode((const hip_bfloat16*)x, M, K, N, pk, sc, kbm, bias, out, part, st);
+  }
+  {
+    const int rc = linear_mfma_nk(x, x_type, M, K, w_packed, w_scales, w_scales_t, N, kind, bits, block, bias, out,
+                                  workspace, workspace_nbytes, st);
+    if (rc != MXK_EUNSUPPORTED) return rc;
   }
   if (x_type == MXK_IN_F32)
     return linear_t<true, float>((const float*)x, M, K, N, pk, w_nbytes, w_scales, kind, bits, block, bias, out, st);

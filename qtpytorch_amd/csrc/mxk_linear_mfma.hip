@@ -1,0 +1,722 @@
+// MFMA weight-only linear for gfx950: the shapes the int4 decode kernels do
+// not take (more than 16 rows of x, int8 weights).
+//
+//   mx_linear.forward (mxtorch.py:7454-7473), weight [K][N] as
+//   quantize(W.t()) with blocks of 128 along N:
+//       y[m,n] = sum_k x[m,k] * RN(c[k,n] * s[k, n/128])
+//   mx_dynamic_linear.forward (mxtorch.py:8945-8962) and the input
+//   gradients of _MXLinearAutograd / mx_linear (mxtorch.py:6729-6746,
+//   7473), weight [N][K] with blocks of 128 along K:
+//       y[m,n] = sum_k x[m,k] * RN(c[n,k] * s[n, k/128])
+//
+// Both products run on v_mfma_f32_16x16x32_f16 with fp32 accumulation.  The
+// codes themselves are the B operand: integers |c| <= 127 are exact f16
+// values.  The x side is an f16 pair hi + lo (22 significant bits), so each
+// term x * s * c carries a relative error of about 2^-22 and sums in fp32;
+// the reference rounds RN(c * s) and runs an fp32 sgemm (about 2^-24 per
+// term, in a library-defined order).
+//
+// [K][N] weights.  The scale changes along the contraction, so it goes into
+// the A operand: a workgroup owns one 128-column block nb and builds
+// A = x * s[., nb] per k step as hi + lo (two v_fma_mix per element).
+//
+// [N][K] weights.  The scale is constant over each block of 128 along K, so
+// A is x itself, split into hi + lo once by the prepass, and each block's
+// tile sums P are scaled in the epilogue: acc = fma(P, s[n, kb], acc).
+//
+// Range.  A prepass scales each row of x by the power of two 2^ex[m] that
+// puts its largest |x| in [1, 2) and, for [K][N], each column block's scales
+// by 2^es[nb] that puts the largest in [2^13, 2^14).  Every A value then lies
+// below 2^15, inside f16's range, whatever the input magnitudes; the
+// epilogue multiplies by 2^-(ex + es).  Terms far below a row's largest
+// keep an absolute error of at most 2^-25 of the scaled units.
+//
+// Work split.  A workgroup of 8 waves owns 128 output columns, BM = 32 WM
+// rows and a range of K in stages of 256 rows.  Per stage the 8 waves decode
+// the stage's 256 x 128 codes once into LDS as f16 B fragments (64 KiB; two
+// stages in flight), then wave (wm, wk) runs the k steps wk, wk + WK, ... of
+// the stage on rows 32 wm .. +31 (WK = 8 / WM): 2 row tiles x 8 column
+// tiles x (hi, lo) = 32 MFMAs per k step.  Column tile t, MFMA column j is
+// output column 128 nb + 8 j + t, so a lane's 8 tiles are 8 consecutive
+// columns.  Waves that split K meet in LDS at the end, in wk order; K
+// splits across workgroups (few rows) write partials that a second kernel
+// sums in split order.  Every reduction order is fixed, so results are
+// deterministic.
+#include "mxk_internal.h"
+
+#include <algorithm>
+#include <type_traits>
+
+namespace mxk {
+
+namespace {
+
+typedef _Float16 h8v __attribute__((ext_vector_type(8)));
+typedef _Float16 h2v __attribute__((ext_vector_type(2)));
+typedef float f4v __attribute__((ext_vector_type(4)));
+typedef uint32_t u4v __attribute__((ext_vector_type(4)));
+typedef uint32_t u2v __attribute__((ext_vector_type(2)));
+
+constexpr int LM_THREADS = 512;
+constexpr int LM_STAGE = 256;                  // rows of K per LDS stage
+constexpr int LM_FRAG = 1024;                  // one B fragment: 64 lanes x 8 f16
+constexpr int LM_STAGE_BYTES = 64 * LM_FRAG;   // 8 k steps x 8 column tiles
+constexpr uint32_t LM_OOB = 0x80000000u;       // past every buffer: loads return zeros
+constexpr size_t LM_WS_BASE = 65536;           // workspace bytes left to the decode kernels' counters
+
+// Slot of MFMA lane `lane` in the fragment of k step `ks`: a permutation of
+// the 16 slots of each 16-lane group, so that the fragment reads (16 lanes
+// per LDS cycle) stay conflict-free and the decoders' stores, whose 16-lane
+// groups span k steps, spread over every bank.
+__device__ __forceinline__ int lm_slot(int lane, int ks) { return lane ^ ((2 * ks + (lane >> 5)) & 15); }
+__device__ __forceinline__ uint32_t lm_frag_off(int ks, int t, int lane) {
+  return (uint32_t)((ks * 8 + t) * LM_FRAG + lm_slot(lane, ks) * 16);
+}
+
+// Two int4 codes at bits 0-3 and 16-19 of d (other bits ignored) as an f16
+// pair: 0x6400 | (c ^ 8) is the f16 1024 + (c + 8), exact, less 1032.
+__device__ __forceinline__ uint32_t lm_i4pair(uint32_t d) {
+  const uint32_t e = (d & 0x000F000Fu) ^ 0x64086408u;
+  const h2v r = __builtin_bit_cast(h2v, e) - h2v{(_Float16)1032.0f, (_Float16)1032.0f};
+  return __builtin_bit_cast(uint32_t, r);
+}
+// Two int8 codes at bits 0-7 and 16-23 of d (bits 8-15, 24-31 zero):
+// 0x6400 | (c ^ 0x80) is 1024 + (c + 128), less 1152.
+__device__ __forceinline__ uint32_t lm_i8pair(uint32_t d) {
+  const uint32_t e = d ^ 0x64806480u;
+  const h2v r = __builtin_bit_cast(h2v, e) - h2v{(_Float16)1152.0f, (_Float16)1152.0f};
+  return __builtin_bit_cast(uint32_t, r);
+}
+// v_perm_b32 selector: byte a of s1 into byte 0, byte b of s0 into byte 2, zeros in bytes 1 and 3
+__host__ __device__ constexpr uint32_t lm_sel(int a, int b) {
+  return (uint32_t)a | 0x0C00u | ((uint32_t)(4 + b) << 16) | 0x0C000000u;
+}
+
+// p = x * s as f16 hi + lo for two elements: hi = RN16(x*s), lo =
+// RN16(x*s - hi), each one v_fma_mix (fp32 product, f16 result), so
+// |x*s - hi - lo| <= 2^-22 |x*s| (less for values whose lo is subnormal:
+// at most 2^-25 absolute).
+__device__ __forceinline__ void lm_split2(float x0, float s0, float x1, float s1, uint32_t& hi, uint32_t& lo) {
+  uint32_t h, l;
+  asm("v_fma_mixlo_f16 %0, %1, %2, 0 op_sel_hi:[0,0,0]" : "=v"(h) : "v"(x0), "v"(s0));
+  asm("v_fma_mixhi_f16 %0, %1, %2, 0 op_sel_hi:[0,0,0]" : "+v"(h) : "v"(x1), "v"(s1));
+  asm("v_fma_mixlo_f16 %0, %1, %2, -%3 op_sel_hi:[0,0,1]" : "=v"(l) : "v"(x0), "v"(s0), "v"(h));
+  asm("v_fma_mixhi_f16 %0, %1, %2, -%3 op_sel:[0,0,1] op_sel_hi:[0,0,1]" : "+v"(l) : "v"(x1), "v"(s1), "v"(h));
+  hi = h;
+  lo = l;
+}
+
+// s_barrier after this wave's LDS stores are done; global loads still in
+// flight (prefetches) stay in flight.
+__device__ __forceinline__ void lm_barrier() {
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+// ---------------------------------------------------------------- [K][N] stage decode
+// Thread (r8 = tid / 16, c8 = tid % 16) decodes rows 8 r8 .. +7 and columns
+// 8 c8 .. +7 of the stage: for column tile t the 8 codes of column 8 c8 + t,
+// which are the B fragment of MFMA lane c8 + 16 (r8 % 4) in k step r8 / 4.
+// A wave's threads are k step w, lanes 0..63 in order.
+template <int BITS>
+struct KnCodes {
+  uint32_t w[BITS == 4 ? 8 : 16];
+};
+
+template <int BITS>
+__device__ __forceinline__ void kn_load(KnCodes<BITS>& c, __amdgpu_buffer_rsrc_t rw, int64_t k0, int64_t N,
+                                        int64_t nb, int tid) {
+  const int r8 = tid >> 4, c8 = tid & 15;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int64_t row = k0 + 8 * r8 + i;
+    if constexpr (BITS == 4) {
+      c.w[i] = buf_load_b32(rw, (uint32_t)(row * (N / 2) + nb * 64 + 4 * c8), 0u);
+    } else {
+      const auto v = __builtin_amdgcn_raw_buffer_load_b64(rw, (int)(row * N + nb * 128 + 8 * c8), 0, 0);
+      c.w[2 * i] = v[0];
+      c.w[2 * i + 1] = v[1];
+    }
+  }
+}
+
+template <int BITS>
+__device__ __forceinline__ void kn_store(const KnCodes<BITS>& c, uint8_t* sB, int tid) {
+  const int ks = tid >> 6, lane = tid & 63;
+#pragma unroll
+  for (int t = 0; t < 8; ++t) {
+    u4v f;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      if constexpr (BITS == 4) {
+        // byte t/2 of rows 2q and 2q+1: the low nibbles are column 8 c8 + t for even t
+        const uint32_t d = __builtin_amdgcn_perm(c.w[2 * q + 1], c.w[2 * q], lm_sel(t >> 1, t >> 1));
+        f[q] = lm_i4pair((t & 1) ? d >> 4 : d);
+      } else {
+        const int h = t >> 2, u = t & 3;
+        f[q] = lm_i8pair(__builtin_amdgcn_perm(c.w[2 * (2 * q + 1) + h], c.w[2 * (2 * q) + h], lm_sel(u, u)));
+      }
+    }
+    *reinterpret_cast<u4v*>(sB + lm_frag_off(ks, t, lane)) = f;
+  }
+}
+
+// ---------------------------------------------------------------- [N][K] stage decode
+// int4: lanes 8a .. 8a+7 read the 128-byte line of one column (k steps
+// 0..7 of the stage, 16 bytes each); each 16 bytes are the four k octets of
+// MFMA lanes j + 16 v.  The local column of pair index p = tid / 8 + 64 h is
+// 16 (p / 16) + 8 (p % 2) + (p / 2) % 8, so the two columns of a 16-lane
+// store group share a tile and differ in j (no bank conflicts).
+// int8: 16 lanes read one column's 256 bytes; 16 bytes are two k octets.
+template <int BITS>
+struct NkCodes {
+  u4v w[BITS == 4 ? 2 : 4];
+};
+
+__device__ __forceinline__ int nk4_col(int p) { return 16 * (p >> 4) + 8 * (p & 1) + ((p >> 1) & 7); }
+
+template <int BITS>
+__device__ __forceinline__ void nk_load(NkCodes<BITS>& c, __amdgpu_buffer_rsrc_t rw, int64_t k0, int64_t K,
+                                        int64_t nb, int tid) {
+  if constexpr (BITS == 4) {
+    const int q = tid & 7;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int64_t n = nb * 128 + nk4_col((tid >> 3) + 64 * h);
+      c.w[h] = buf_load_b128(rw, (uint32_t)(n * (K / 2) + k0 / 2 + 16 * q), 0u);
+    }
+  } else {
+    const int h8 = tid & 15;
+#pragma unroll
+    for (int h = 0; h < 4; ++h) {
+      const int64_t n = nb * 128 + (tid >> 4) + 32 * h;
+      c.w[h] = buf_load_b128(rw, (uint32_t)(n * K + k0 + 16 * h8), 0u);
+    }
+  }
+}
+
+template <int BITS>
+__device__ __forceinline__ void nk_store(const NkCodes<BITS>& c, uint8_t* sB, int tid) {
+  if constexpr (BITS == 4) {
+    const int ks = tid & 7;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int col = nk4_col((tid >> 3) + 64 * h);
+      const int t = col & 7, j = col >> 3;
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const uint32_t lo4 = c.w[h][v] & 0x0F0F0F0Fu, hi4 = (c.w[h][v] >> 4) & 0x0F0F0F0Fu;
+        u4v f;
+#pragma unroll
+        for (int p = 0; p < 4; ++p) f[p] = lm_i4pair(__builtin_amdgcn_perm(hi4, lo4, lm_sel(p, p)));
+        *reinterpret_cast<u4v*>(sB + lm_frag_off(ks, t, j + 16 * v)) = f;
+      }
+    }
+  } else {
+    const int h8 = tid & 15, ks = h8 >> 1;
+#pragma unroll
+    for (int h = 0; h < 4; ++h) {
+      const int col = (tid >> 4) + 32 * h;
+      const int t = col & 7, j = col >> 3;
+#pragma unroll
+      for (int e = 0; e < 2; ++e) {
+        const int g = 2 * (h8 & 1) + e;
+        u4v f;
+#pragma unroll
+        for (int p = 0; p < 4; ++p) {
+          const uint32_t wd = c.w[h][2 * e + (p >> 1)];
+          const int b = 2 * (p & 1);
+          f[p] = lm_i8pair(__builtin_amdgcn_perm(wd, wd, lm_sel(b, b + 1)));
+        }
+        *reinterpret_cast<u4v*>(sB + lm_frag_off(ks, t, j + 16 * g)) = f;
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------- the MFMA kernel
+// A-operand registers of one k step: [K][N] x' (2 row tiles x 8 fp32) and
+// 8 scales; [N][K] hi and lo (2 row tiles x 8 f16 each)
+struct KnA {
+  u4v x[2][2];
+  u4v s[2];
+};
+struct NkA {
+  u4v h[2];
+  u4v l[2];
+};
+
+template <int BITS, int WM, bool NK>
+__global__ __launch_bounds__(LM_THREADS, 1) void k_linear_mfma(
+    const float* __restrict__ xs,        // [K][N]: x' [M][Kp] fp32
+    const _Float16* __restrict__ xh,     // [N][K]: hi of x' [M][Kp]
+    const _Float16* __restrict__ xl,     // [N][K]: lo of x' [M][Kp]
+    const float* __restrict__ sc,        // [K][N]: scales' [NB][Kp]; [N][K]: scales [KB][N] or [N][KB]
+    int sc_kb_major, const int* __restrict__ ex, const int* __restrict__ es, const uint8_t* __restrict__ w,
+    int M, int64_t K, int64_t Kp, int64_t N, int sps, const float* __restrict__ bias, float* __restrict__ out,
+    float* __restrict__ part) {
+  constexpr int WK = 8 / WM, KPW = 8 / WK;
+  using A = typename std::conditional<NK, NkA, KnA>::type;
+  using Codes = typename std::conditional<NK, NkCodes<BITS>, KnCodes<BITS>>::type;
+  __shared__ __attribute__((aligned(1024))) uint8_t sB[2 * LM_STAGE_BYTES];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave % WM, wk = wave / WM;
+  const int j = lane & 15, g = lane >> 4;
+  const int64_t nb = blockIdx.x, NB = N / 128, KB = K / 128;
+  const int64_t m0 = (int64_t)blockIdx.y * (32 * WM);
+  const int z = blockIdx.z;
+  const int nst = (int)(Kp / LM_STAGE);
+  const int st0 = z * sps, st1 = min(st0 + sps, nst);
+  const int rows = (int64_t)M - m0 < 32 * WM ? (int)((int64_t)M - m0) : 32 * WM;
+  const __amdgpu_buffer_rsrc_t rw = make_rsrc(w, (uint32_t)(K * N * BITS / 8));
+
+  // A-operand loads of k step (st, jj): rows 32 wm + 16 i + j, columns
+  // kg + 8 g .. +7 (rows past M read zeros)
+  __amdgpu_buffer_rsrc_t ra, rb;
+  if constexpr (NK) {
+    ra = make_rsrc(xh + m0 * Kp, (uint32_t)(rows * Kp * 2));
+    rb = make_rsrc(xl + m0 * Kp, (uint32_t)(rows * Kp * 2));
+  } else {
+    ra = make_rsrc(xs + m0 * Kp, (uint32_t)(rows * Kp * 4));
+    rb = make_rsrc(sc + nb * Kp, (uint32_t)(Kp * 4));
+  }
+  auto load_a = [&](A& a, int st, int jj) {
+    const int64_t kg = (int64_t)st * LM_STAGE + 32 * (wk + WK * jj) + 8 * g;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int64_t r = 32 * wm + 16 * i + j;
+      if constexpr (NK) {
+        a.h[i] = buf_load_b128(ra, (uint32_t)((r * Kp + kg) * 2), 0u);
+        a.l[i] = buf_load_b128(rb, (uint32_t)((r * Kp + kg) * 2), 0u);
+      } else {
+        a.x[i][0] = buf_load_b128(ra, (uint32_t)((r * Kp + kg) * 4), 0u);
+        a.x[i][1] = buf_load_b128(ra, (uint32_t)((r * Kp + kg) * 4 + 16), 0u);
+      }
+    }
+    if constexpr (!NK) {
+      a.s[0] = buf_load_b128(rb, (uint32_t)(kg * 4), 0u);
+      a.s[1] = buf_load_b128(rb, (uint32_t)(kg * 4 + 16), 0u);
+    }
+  };
+  auto load_codes = [&](Codes& c, int st) {
+    if constexpr (NK) nk_load<BITS>(c, rw, (int64_t)st * LM_STAGE, K, nb, tid);
+    else kn_load<BITS>(c, rw, (int64_t)st * LM_STAGE, N, nb, tid);
+  };
+  auto store_codes = [&](const Codes& c, uint8_t* dst) {
+    if constexpr (NK) nk_store<BITS>(c, dst, tid);
+    else kn_store<BITS>(c, dst, tid);
+  };
+
+  f4v acc[2][8], P[2][8];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+      acc[i][t] = f4v{0.f, 0.f, 0.f, 0.f};
+      P[i][t] = f4v{0.f, 0.f, 0.f, 0.f};
+    }
+
+  // [N][K] scales of block kb for this lane's 8 columns (8 j .. 8 j + 7 of the block)
+  const __amdgpu_buffer_rsrc_t rsc = make_rsrc(sc, (uint32_t)(NK ? N * KB * 4 : 4));
+  auto block_scales = [&](int64_t kb, float (&s8)[8]) {
+    const int64_t n0 = nb * 128 + 8 * j;
+    if (sc_kb_major) {
+      const u4v a0 = buf_load_b128(rsc, (uint32_t)((kb * N + n0) * 4), 0u);
+      const u4v a1 = buf_load_b128(rsc, (uint32_t)((kb * N + n0) * 4 + 16), 0u);
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        s8[u] = __uint_as_float(a0[u]);
+        s8[4 + u] = __uint_as_float(a1[u]);
+      }
+    } else {
+#pragma unroll
+      for (int t = 0; t < 8; ++t) s8[t] = __uint_as_float(buf_load_b32(rsc, (uint32_t)(((n0 + t) * KB + kb) * 4), 0u));
+    }
+  };
+  // fold the block sums of kb into acc (the block's scale for each column)
+  auto fold = [&](int64_t kb) {
+    if (kb >= KB) return;  // padding rows past K: P holds exact zeros
+    float s8[8];
+    block_scales(kb, s8);
+#pragma unroll
+    for (int t = 0; t < 8; ++t)
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          acc[i][t][r] = __builtin_fmaf(P[i][t][r], s8[t], acc[i][t][r]);
+          P[i][t][r] = 0.0f;
+        }
+  };
+
+  auto compute = [&](const A& a, const uint8_t* b, int ks) {
+    h8v ahi[2], alo[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      if constexpr (NK) {
+        ahi[i] = __builtin_bit_cast(h8v, a.h[i]);
+        alo[i] = __builtin_bit_cast(h8v, a.l[i]);
+      } else {
+        u4v hv, lv;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int e = 2 * q;
+          const float x0 = __uint_as_float(a.x[i][e >> 2][e & 3]), x1 = __uint_as_float(a.x[i][e >> 2][(e & 3) + 1]);
+          const float s0 = __uint_as_float(a.s[e >> 2][e & 3]), s1 = __uint_as_float(a.s[e >> 2][(e & 3) + 1]);
+          uint32_t hh, ll;
+          lm_split2(x0, s0, x1, s1, hh, ll);
+          hv[q] = hh;
+          lv[q] = ll;
+        }
+        ahi[i] = __builtin_bit_cast(h8v, hv);
+        alo[i] = __builtin_bit_cast(h8v, lv);
+      }
+    }
+    // fragments in two groups of four (register pressure of the [N][K] kernel)
+#pragma unroll
+    for (int t0 = 0; t0 < 8; t0 += 4) {
+      h8v bt[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) bt[u] = *reinterpret_cast<const h8v*>(b + lm_frag_off(ks, t0 + u, lane));
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+          f4v& d = NK ? P[i][t0 + u] : acc[i][t0 + u];
+          d = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi[i], bt[u], d, 0, 0, 0);
+          d = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo[i], bt[u], d, 0, 0, 0);
+        }
+      if (NK && t0 == 0) __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+
+  if (st0 < st1) {
+    Codes cc;
+    load_codes(cc, st0);
+    A a_cur, a_nxt;
+    load_a(a_cur, st0, 0);
+    store_codes(cc, sB);
+    lm_barrier();
+    for (int st = st0; st < st1; ++st) {
+      const int buf = (st - st0) & 1;
+      const bool more = st + 1 < st1;
+      if (more) load_codes(cc, st + 1);
+      const uint8_t* b = sB + buf * LM_STAGE_BYTES;
+#pragma unroll(NK ? 1 : 8)
+      for (int jj = 0; jj < KPW; ++jj) {
+        const int ks = wk + WK * jj;
+        if (jj + 1 < KPW) load_a(a_nxt, st, jj + 1);
+        else if (more) load_a(a_nxt, st + 1, 0);
+        compute(a_cur, b, ks);
+        if constexpr (NK) {
+          // the k steps of this wave in block kb = 2 st + ks / 4 end here
+          if (jj + 1 == KPW || (ks >> 2) != ((wk + WK * (jj + 1)) >> 2)) fold(2 * (int64_t)st + (ks >> 2));
+        }
+        a_cur = a_nxt;
+      }
+      if (more) store_codes(cc, sB + (buf ^ 1) * LM_STAGE_BYTES);
+      lm_barrier();
+    }
+  }
+
+  // ---- waves that split K meet in LDS, in wk order (the stage buffers are
+  // free: every wave has passed the barrier after its last fragment reads)
+  if constexpr (WK > 1) {
+    f4v* red = reinterpret_cast<f4v*>(sB);
+    if (wk > 0) {
+      f4v* slot = red + (size_t)(wm * (WK - 1) + wk - 1) * 16 * 64;
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int t = 0; t < 8; ++t) slot[(i * 8 + t) * 64 + lane] = acc[i][t];
+    }
+    lm_barrier();
+    if (wk > 0) return;
+#pragma unroll 1
+    for (int u = 1; u < WK; ++u) {
+      const f4v* slot = red + (size_t)(wm * (WK - 1) + u - 1) * 16 * 64;
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+          const f4v v = slot[(i * 8 + t) * 64 + lane];
+#pragma unroll
+          for (int r = 0; r < 4; ++r) acc[i][t][r] += v[r];
+        }
+    }
+  }
+
+  // ---- store: rows 4 g + r of row tile i, columns 128 nb + 8 j + t
+  const int64_t n0 = nb * 128 + 8 * j;
+  float bv[8];
+#pragma unroll
+  for (int t = 0; t < 8; ++t) bv[t] = (bias && !part) ? bias[n0 + t] : 0.0f;
+  const int esb = (es && !part) ? es[nb] : 0;
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int64_t m = m0 + 32 * wm + 16 * i + 4 * g + r;
+      if (m >= M) continue;
+      float v[8];
+      if (part) {
+#pragma unroll
+        for (int t = 0; t < 8; ++t) v[t] = acc[i][t][r];
+        float* dst = part + ((int64_t)z * M + m) * N + n0;
+        *reinterpret_cast<f4v*>(dst) = f4v{v[0], v[1], v[2], v[3]};
+        *reinterpret_cast<f4v*>(dst + 4) = f4v{v[4], v[5], v[6], v[7]};
+      } else {
+        const int e = -(ex[m] + esb);
+#pragma unroll
+        for (int t = 0; t < 8; ++t) v[t] = __builtin_ldexpf(acc[i][t][r], e) + bv[t];
+        float* dst = out + m * N + n0;
+        *reinterpret_cast<f4v*>(dst) = f4v{v[0], v[1], v[2], v[3]};
+        *reinterpret_cast<f4v*>(dst + 4) = f4v{v[4], v[5], v[6], v[7]};
+      }
+    }
+}
+
+// y = 2^-(ex[m] + es[n / 128]) * sum over the S splits in order (+ bias)
+__global__ __launch_bounds__(256) void k_linear_mfma_reduce(const float* __restrict__ part, int S, int64_t M,
+                                                            int64_t N, const int* __restrict__ ex,
+                                                            const int* __restrict__ es, const float* __restrict__ bias,
+                                                            float* __restrict__ out) {
+  const int64_t q = (int64_t)blockIdx.x * 256 + threadIdx.x;  // float4 index
+  if (q >= M * N / 4) return;
+  const int64_t m = (4 * q) / N, n = (4 * q) % N;
+  f4v s = *reinterpret_cast<const f4v*>(part + 4 * q);
+  for (int z = 1; z < S; ++z) {
+    const f4v v = *reinterpret_cast<const f4v*>(part + (int64_t)z * M * N + 4 * q);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) s[r] += v[r];
+  }
+  const int e = -(ex[m] + (es ? es[n / 128] : 0));
+  f4v y;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) y[r] = __builtin_ldexpf(s[r], e) + (bias ? bias[n + r] : 0.0f);
+  *reinterpret_cast<f4v*>(out + 4 * q) = y;
+}
+
+// ---------------------------------------------------------------- prepasses
+// Row m of x: ex[m] such that its largest |x| times 2^ex lies in [1, 2)
+// (0 for a zero row), and x * 2^ex zero-padded to Kp columns, as fp32
+// (SPLIT false) or as f16 hi + lo (SPLIT true: hi = RN16(v), lo = RN16(v - hi),
+// v - hi exact in fp32).
+template <typename T, bool SPLIT>
+__global__ __launch_bounds__(256) void k_linear_mfma_prep_rows(const T* __restrict__ x, int64_t K, int64_t Kp,
+                                                               float* __restrict__ xs, _Float16* __restrict__ xh,
+                                                               _Float16* __restrict__ xl, int* __restrict__ ex) {
+  __shared__ float red[4];
+  const int64_t m = blockIdx.x;
+  const T* row = x + m * K;
+  float mx = 0.0f;
+  for (int64_t k = threadIdx.x; k < K; k += 256) mx = fmaxf(mx, __builtin_fabsf(ElemT<T>::cvt(row[k])));
+  mx = group_max<64>(mx);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = mx;
+  __syncthreads();
+  mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  const int be = (int)((__float_as_uint(mx) >> 23) & 0xFFu);
+  const int e = (be == 0xFF || mx == 0.0f) ? 0 : 127 - (be == 0 ? 1 : be);
+  if (threadIdx.x == 0) ex[m] = e;
+  for (int64_t k = threadIdx.x; k < Kp; k += 256) {
+    const float v = k < K ? __builtin_ldexpf(ElemT<T>::cvt(row[k]), e) : 0.0f;
+    if constexpr (SPLIT) {
+      const _Float16 h = (_Float16)v;
+      xh[m * Kp + k] = h;
+      xl[m * Kp + k] = (_Float16)(v - (float)h);
+    } else {
+      xs[m * Kp + k] = v;
+    }
+  }
+}
+
+// Column block nb of a [K][N] weight's scales (block-major sT[nb][k] when
+// kb_major, else s[k][nb]): es[nb] such that the largest scale times 2^es
+// lies in [2^13, 2^14), and sc[nb][k] = s * 2^es zero-padded to Kp.
+__global__ __launch_bounds__(256) void k_linear_mfma_prep_scales(const float* __restrict__ s, int kb_major,
+                                                                 int64_t K, int64_t Kp, int64_t NB,
+                                                                 float* __restrict__ sc, int* __restrict__ es) {
+  __shared__ float red[4];
+  const int64_t nb = blockIdx.x;
+  auto at = [&](int64_t k) { return kb_major ? s[nb * K + k] : s[k * NB + nb]; };
+  float mx = 0.0f;
+  for (int64_t k = threadIdx.x; k < K; k += 256) mx = fmaxf(mx, __builtin_fabsf(at(k)));
+  mx = group_max<64>(mx);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = mx;
+  __syncthreads();
+  mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  const int be = (int)((__float_as_uint(mx) >> 23) & 0xFFu);
+  const int e = (be == 0xFF || mx == 0.0f) ? 0 : 140 - (be == 0 ? 1 : be);
+  if (threadIdx.x == 0) es[nb] = e;
+  for (int64_t k = threadIdx.x; k < Kp; k += 256) sc[nb * Kp + k] = k < K ? __builtin_ldexpf(at(k), e) : 0.0f;
+}
+
+// ---------------------------------------------------------------- plan
+struct LmPlan {
+  int wm = 0, S = 1, sps = 0;
+  int64_t Kp = 0;
+  size_t off_ex = 0, off_es = 0, off_x = 0, off_s = 0, off_p = 0, bytes = 0;
+};
+
+inline size_t lm_round(size_t v) { return (v + 255) & ~(size_t)255; }
+
+// Row tile: the largest WM (32 WM rows) that still gives every CU a
+// workgroup; when none does, the fewest row tiles, and K splits across
+// workgroups to fill the CUs.
+LmPlan lm_plan(int64_t M, int64_t K, int64_t N, bool nk) {
+  LmPlan p;
+  p.Kp = ceil_div(K, LM_STAGE) * LM_STAGE;
+  const int nst = (int)(p.Kp / LM_STAGE);
+  const int64_t NB = N / 128, target = num_cus();
+  const int64_t m32 = ceil_div(M, 32);
+  int wm = 1;
+  while (wm < 8 && wm * 2 <= m32) wm *= 2;
+  int pick = 0;
+  for (int c = wm; c >= 1; c /= 2)
+    if (NB * ceil_div(M, 32 * c) >= target) {
+      pick = c;
+      break;
+    }
+  int S = 1;
+  if (pick) {
+    wm = pick;
+  } else {
+    S = (int)std::min<int64_t>(nst, ceil_div(target, NB * ceil_div(M, 32 * wm)));
+  }
+  p.wm = wm;
+  p.sps = (int)ceil_div(nst, S);
+  p.S = (int)ceil_div(nst, p.sps);
+  size_t o = LM_WS_BASE;
+  p.off_ex = o;
+  o += lm_round((size_t)M * 4);
+  p.off_es = o;
+  o += lm_round((size_t)NB * 4);
+  p.off_x = o;
+  o += lm_round((size_t)M * (size_t)p.Kp * 4);  // fp32 x', or f16 hi + lo
+  p.off_s = o;
+  if (!nk) o += lm_round((size_t)NB * (size_t)p.Kp * 4);
+  p.off_p = o;
+  if (p.S > 1) o += lm_round((size_t)p.S * (size_t)M * (size_t)N * 4);
+  p.bytes = o;
+  return p;
+}
+
+template <int BITS, int WM, bool NK>
+void lm_launch_t(const LmPlan& p, hipStream_t st, const float* xs, const _Float16* xh, const _Float16* xl,
+                 const float* sc, int sc_kbm, const int* ex, const int* es, const uint8_t* w, int64_t M, int64_t K,
+                 int64_t N, const float* bias, float* out, float* part) {
+  const dim3 grid((unsigned)(N / 128), (unsigned)ceil_div(M, 32 * WM), (unsigned)p.S);
+  hipLaunchKernelGGL((k_linear_mfma<BITS, WM, NK>), grid, dim3(LM_THREADS), 0, st, xs, xh, xl, sc, sc_kbm, ex, es, w,
+                     (int)M, K, p.Kp, N, p.sps, bias, out, p.S > 1 ? part : nullptr);
+}
+
+template <int BITS, bool NK>
+void lm_launch_w(const LmPlan& p, hipStream_t st, const float* xs, const _Float16* xh, const _Float16* xl,
+                 const float* sc, int sc_kbm, const int* ex, const int* es, const uint8_t* w, int64_t M, int64_t K,
+                 int64_t N, const float* bias, float* out, float* part) {
+  switch (p.wm) {
+    case 8: lm_launch_t<BITS, 8, NK>(p, st, xs, xh, xl, sc, sc_kbm, ex, es, w, M, K, N, bias, out, part); break;
+    case 4: lm_launch_t<BITS, 4, NK>(p, st, xs, xh, xl, sc, sc_kbm, ex, es, w, M, K, N, bias, out, part); break;
+    case 2: lm_launch_t<BITS, 2, NK>(p, st, xs, xh, xl, sc, sc_kbm, ex, es, w, M, K, N, bias, out, part); break;
+    default: lm_launch_t<BITS, 1, NK>(p, st, xs, xh, xl, sc, sc_kbm, ex, es, w, M, K, N, bias, out, part); break;
+  }
+}
+
+template <bool SPLIT>
+void lm_prep_rows(const void* x, int x_type, int64_t M, int64_t K, int64_t Kp, float* xs, _Float16* xh, _Float16* xl,
+                  int* ex, hipStream_t st) {
+  const dim3 grid((unsigned)M);
+  if (x_type == MXK_IN_F32)
+    hipLaunchKernelGGL((k_linear_mfma_prep_rows<float, SPLIT>), grid, dim3(256), 0, st, (const float*)x, K, Kp, xs, xh,
+                       xl, ex);
+  else if (x_type == MXK_IN_F16)
+    hipLaunchKernelGGL((k_linear_mfma_prep_rows<__half, SPLIT>), grid, dim3(256), 0, st, (const __half*)x, K, Kp, xs,
+                       xh, xl, ex);
+  else
+    hipLaunchKernelGGL((k_linear_mfma_prep_rows<hip_bfloat16, SPLIT>), grid, dim3(256), 0, st,
+                       (const hip_bfloat16*)x, K, Kp, xs, xh, xl, ex);
+}
+
+bool lm_common_ok(int64_t M, int64_t K, int64_t N, int kind, int bits, int block, int x_type, const float* out) {
+  if (kind != MXK_KIND_INT || (bits != 4 && bits != 8) || block != 128) return false;
+  if (M < 1 || K < 1 || N < 128 || N % 128 != 0 || M >= (int64_t(1) << 31)) return false;
+  if (x_type != MXK_IN_F32 && x_type != MXK_IN_F16 && x_type != MXK_IN_BF16) return false;
+  if (!aligned16(out)) return false;
+  const int64_t Kp = ceil_div(K, LM_STAGE) * LM_STAGE, lim = int64_t(1) << 31;
+  // 32-bit buffer offsets: codes (with the padded stage rows), one row tile of x', the scales
+  if ((Kp + LM_STAGE) * N * bits / 8 >= lim || 256 * Kp * 4 >= lim || (N / 128) * Kp * 4 >= lim) return false;
+  if (ceil_div(M, 32) >= 65536 || N / 128 >= (int64_t(1) << 31)) return false;
+  return true;
+}
+
+}  // namespace
+
+// ---------------------------------------------------------------- internal entry points
+// Bytes of workspace the MFMA path needs for this product (0 when it does
+// not take the shape); the first LM_WS_BASE bytes are left untouched.
+size_t linear_mfma_workspace(int64_t M, int64_t K, int64_t N, int bits, int block, bool nk) {
+  if ((bits != 4 && bits != 8) || block != 128 || M < 1 || K < 1 || N < 128 || N % 128 != 0) return 0;
+  if (nk && K % 128 != 0) return 0;
+  return lm_plan(M, K, N, nk).bytes;
+}
+
+// [K][N] weight (mx_linear).  Returns MXK_EUNSUPPORTED, with nothing
+// launched, for shapes it does not take.
+int linear_mfma_kn(const void* x, int x_type, int64_t M, int64_t K, const void* w_packed, const float* w_scales,
+                   const float* w_scales_t, int64_t N, int kind, int bits, int block, const float* bias, float* out,
+                   void* workspace, size_t workspace_nbytes, hipStream_t st) {
+  if (!lm_common_ok(M, K, N, kind, bits, block, x_type, out)) return MXK_EUNSUPPORTED;
+  if ((reinterpret_cast<uintptr_t>(w_packed) & (bits == 8 ? 7u : 3u)) != 0) return MXK_EUNSUPPORTED;
+  const LmPlan p = lm_plan(M, K, N, false);
+  if (!workspace || workspace_nbytes < p.bytes)
+    return fail(MXK_EINVAL, "linear_wq: needs a workspace of mxk_linear_workspace() bytes");
+  uint8_t* ws = reinterpret_cast<uint8_t*>(workspace);
+  int* ex = reinterpret_cast<int*>(ws + p.off_ex);
+  int* es = reinterpret_cast<int*>(ws + p.off_es);
+  float* xs = reinterpret_cast<float*>(ws + p.off_x);
+  float* sc = reinterpret_cast<float*>(ws + p.off_s);
+  float* part = reinterpret_cast<float*>(ws + p.off_p);
+  const int64_t NB = N / 128;
+  lm_prep_rows<false>(x, x_type, M, K, p.Kp, xs, nullptr, nullptr, ex, st);
+  hipLaunchKernelGGL(k_linear_mfma_prep_scales, dim3((unsigned)NB), dim3(256), 0, st,
+                     w_scales_t ? w_scales_t : w_scales, w_scales_t ? 1 : 0, K, p.Kp, NB, sc, es);
+  const uint8_t* w = reinterpret_cast<const uint8_t*>(w_packed);
+  if (bits == 4) lm_launch_w<4, false>(p, st, xs, nullptr, nullptr, sc, 1, ex, es, w, M, K, N, bias, out, part);
+  else lm_launch_w<8, false>(p, st, xs, nullptr, nullptr, sc, 1, ex, es, w, M, K, N, bias, out, part);
+  if (p.S > 1)
+    hipLaunchKernelGGL(k_linear_mfma_reduce, dim3((unsigned)ceil_div(M * N / 4, 256)), dim3(256), 0, st, part, p.S,
+                       M, N, ex, es, bias, out);
+  return check_launch("linear_wq(mfma)");
+}
+
+// [N][K] weight (mx_dynamic_linear, input gradients).  `w_scales_t` is the
+// K-block-major copy [K/128][N] when given, else the scales [N][K/128].
+int linear_mfma_nk(const void* x, int x_type, int64_t M, int64_t K, const void* w_packed, const float* w_scales,
+                   const float* w_scales_t, int64_t N, int kind, int bits, int block, const float* bias, float* out,
+                   void* workspace, size_t workspace_nbytes, hipStream_t st) {
+  if (!lm_common_ok(M, K, N, kind, bits, block, x_type, out) || K % 128 != 0) return MXK_EUNSUPPORTED;
+  if (!aligned16(w_packed)) return MXK_EUNSUPPORTED;
+  if (N * K * bits / 8 >= (int64_t(1) << 31) || N * (K / 128) * 4 >= (int64_t(1) << 31)) return MXK_EUNSUPPORTED;
+  const LmPlan p = lm_plan(M, K, N, true);
+  if (!workspace || workspace_nbytes < p.bytes)
+    return fail(MXK_EINVAL, "linear_wq_nt: needs a workspace of mxk_linear_nt_workspace() bytes");
+  uint8_t* ws = reinterpret_cast<uint8_t*>(workspace);
+  int* ex = reinterpret_cast<int*>(ws + p.off_ex);
+  _Float16* xh = reinterpret_cast<_Float16*>(ws + p.off_x);
+  _Float16* xl = xh + (size_t)M * (size_t)p.Kp;
+  float* part = reinterpret_cast<float*>(ws + p.off_p);
+  lm_prep_rows<true>(x, x_type, M, K, p.Kp, nullptr, xh, xl, ex, st);
+  const float* sc = w_scales_t ? w_scales_t : w_scales;
+  const int kbm = w_scales_t ? 1 : 0;
+  const uint8_t* w = reinterpret_cast<const uint8_t*>(w_packed);
+  if (bits == 4) lm_launch_w<4, true>(p, st, nullptr, xh, xl, sc, kbm, ex, nullptr, w, M, K, N, bias, out, part);
+  else lm_launch_w<8, true>(p, st, nullptr, xh, xl, sc, kbm, ex, nullptr, w, M, K, N, bias, out, part);
+  if (p.S > 1)
+    hipLaunchKernelGGL(k_linear_mfma_reduce, dim3((unsigned)ceil_div(M * N / 4, 256)), dim3(256), 0, st, part, p.S,
+                       M, N, ex, nullptr, bias, out);
+  return check_launch("linear_wq_nt(mfma)");
+}
+
+}  // namespace mxk

@@ -138,13 +138,21 @@ def test_bad_arguments_return_errors_without_gpu():
 
 def test_decode_workspace_limits():
     """The int4 decode path counts split arrivals in 8 bits per XCC, so it
-    takes no shape that would need more than 255 splits: for those the
-    workspace query returns 0 (the generic kernel runs instead).  Covered
-    shapes get a workspace with the 64 KiB counter prefix."""
+    takes no shape that would need more than 255 splits.  Covered shapes get
+    a workspace with the 64 KiB counter prefix."""
     from qtpytorch_amd import _lib as L
     h = L.lib()
     assert h.mxk_linear_workspace(16, 8192, 8192, 4, 128) >= 65536
-    # one 128-column block: at most 2048 rows of K per split -> K = 600000 needs 293 splits
-    assert h.mxk_linear_workspace(1, 600000, 128, 4, 128) == 0
     assert h.mxk_linear_workspace(1, 2048 * 255, 128, 4, 128) > 0
-    assert h.mxk_linear_workspace(17, 8192, 8192, 4, 128) == 0     # M > 16: generic kernel
+    # past the decode kernels' limits (more than 16 rows, 293 splits, int8
+    # codes) the MFMA path takes int4 and int8 codes: its row exponents,
+    # scaled x (fp32), scaled scales and any split partials follow the 64 KiB
+    # counter prefix, which it leaves alone
+    for M, K, N, bits in ((17, 8192, 8192, 4), (1, 600000, 128, 4), (512, 8192, 8192, 8), (16, 4096, 256, 8)):
+        Kp = -(-K // 256) * 256
+        assert h.mxk_linear_workspace(M, K, N, bits, 128) >= 65536 + M * Kp * 4 + (N // 128) * Kp * 4
+    assert h.mxk_linear_workspace(64, 8192, 8192, 2, 128) == 0     # other widths: generic kernel, no workspace
+    assert h.mxk_linear_workspace(64, 8192, 8000, 4, 128) == 0     # N not whole 128-column blocks
+    # [out, in] weights: K must be whole blocks of 128; x as f16 hi + lo
+    assert h.mxk_linear_nt_workspace(64, 8192, 8192, 4, 128) >= 65536 + 64 * 8192 * 4
+    assert h.mxk_linear_nt_workspace(64, 8000, 8192, 4, 128) == 0
