@@ -252,8 +252,8 @@ __global__ __launch_bounds__(LM_THREADS, 1) void k_linear_mfma(
     const float* __restrict__ xs,        // [K][N]: x' [M][Kp] fp32
     const _Float16* __restrict__ xh,     // [N][K]: hi of x' [M][Kp]
     const _Float16* __restrict__ xl,     // [N][K]: lo of x' [M][Kp]
-    const float* __restrict__ sc,        // [K][N]: scales' [NB][Kp]; [N][K]: scales [KB][N] or [N][KB]
-    int sc_kb_major, const int* __restrict__ ex, const int* __restrict__ es, const uint8_t* __restrict__ w,
+    const float* __restrict__ sc,        // [K][N]: block-major scales [NB][K]; [N][K]: [KB][N] or [N][KB]
+    int sc_kb_major, const int* __restrict__ ex, int* __restrict__ es, const uint8_t* __restrict__ w,
     int M, int64_t K, int64_t Kp, int64_t N, int sps, const float* __restrict__ bias, float* __restrict__ out,
     float* __restrict__ part) {
   constexpr int WK = 8 / WM, KPW = 8 / WK;
@@ -280,7 +280,30 @@ __global__ __launch_bounds__(LM_THREADS, 1) void k_linear_mfma(
     rb = make_rsrc(xl + m0 * Kp, (uint32_t)(rows * Kp * 2));
   } else {
     ra = make_rsrc(xs + m0 * Kp, (uint32_t)(rows * Kp * 4));
-    rb = make_rsrc(sc + nb * Kp, (uint32_t)(Kp * 4));
+    rb = make_rsrc(sc + nb * K, (uint32_t)(K * 4));  // scales past K read zeros
+  }
+  // [K][N]: the block's scales go to the binade of 2^13 by 2^es (the
+  // largest in [2^13, 2^14)); the epilogue takes 2^-es back out
+  int es_nb = 0;
+  if constexpr (!NK) {
+    __shared__ float s_red[8];
+    float mx = 0.0f;
+    for (int64_t k = tid; k < K; k += 4 * LM_THREADS) {
+      float v[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) v[u] = __uint_as_float(buf_load_b32(rb, (uint32_t)((k + u * LM_THREADS) * 4), 0u));
+#pragma unroll
+      for (int u = 0; u < 4; ++u) mx = fmaxf(mx, __builtin_fabsf(v[u]));
+    }
+    mx = group_max<64>(mx);
+    if (lane == 0) s_red[wave] = mx;
+    lm_barrier();
+#pragma unroll
+    for (int u = 0; u < 8; ++u) mx = fmaxf(mx, s_red[u]);
+    const int be = (int)((__float_as_uint(mx) >> 23) & 0xFFu);
+    es_nb = (be == 0xFF || mx == 0.0f) ? 0 : 140 - (be == 0 ? 1 : be);
+    // the split reduction applies 2^-es after summing the partials
+    if (part && es && blockIdx.y == 0 && blockIdx.z == 0 && tid == 0) es[nb] = es_nb;
   }
   auto load_a = [&](A& a, int st, int jj) {
     const int64_t kg = (int64_t)st * LM_STAGE + 32 * (wk + WK * jj) + 8 * g;
@@ -322,7 +345,10 @@ __global__ __launch_bounds__(LM_THREADS, 1) void k_linear_mfma(
   const __amdgpu_buffer_rsrc_t rsc = make_rsrc(sc, (uint32_t)(NK ? N * KB * 4 : 4));
   auto block_scales = [&](int64_t kb, float (&s8)[8]) {
     const int64_t n0 = nb * 128 + 8 * j;
-    if (sc_kb_major) {
+    if (kb >= KB) {
+#pragma unroll
+      for (int t = 0; t < 8; ++t) s8[t] = 0.0f;
+    } else if (sc_kb_major) {
       const u4v a0 = buf_load_b128(rsc, (uint32_t)((kb * N + n0) * 4), 0u);
       const u4v a1 = buf_load_b128(rsc, (uint32_t)((kb * N + n0) * 4 + 16), 0u);
 #pragma unroll
@@ -335,11 +361,9 @@ __global__ __launch_bounds__(LM_THREADS, 1) void k_linear_mfma(
       for (int t = 0; t < 8; ++t) s8[t] = __uint_as_float(buf_load_b32(rsc, (uint32_t)(((n0 + t) * KB + kb) * 4), 0u));
     }
   };
-  // fold the block sums of kb into acc (the block's scale for each column)
-  auto fold = [&](int64_t kb) {
-    if (kb >= KB) return;  // padding rows past K: P holds exact zeros
-    float s8[8];
-    block_scales(kb, s8);
+  // fold the block sums into acc with the block's scale of each column
+  // (blocks past K: padding rows, P holds exact zeros and s8 zeros)
+  auto fold = [&](const float (&s8)[8]) {
 #pragma unroll
     for (int t = 0; t < 8; ++t)
 #pragma unroll
@@ -351,8 +375,7 @@ __global__ __launch_bounds__(LM_THREADS, 1) void k_linear_mfma(
         }
   };
 
-  auto compute = [&](const A& a, const uint8_t* b, int ks) {
-    h8v ahi[2], alo[2];
+  auto build = [&](const A& a, h8v (&ahi)[2], h8v (&alo)[2]) {
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
       if constexpr (NK) {
@@ -364,7 +387,8 @@ __global__ __launch_bounds__(LM_THREADS, 1) void k_linear_mfma(
         for (int q = 0; q < 4; ++q) {
           const int e = 2 * q;
           const float x0 = __uint_as_float(a.x[i][e >> 2][e & 3]), x1 = __uint_as_float(a.x[i][e >> 2][(e & 3) + 1]);
-          const float s0 = __uint_as_float(a.s[e >> 2][e & 3]), s1 = __uint_as_float(a.s[e >> 2][(e & 3) + 1]);
+          const float s0 = __builtin_ldexpf(__uint_as_float(a.s[e >> 2][e & 3]), es_nb);
+          const float s1 = __builtin_ldexpf(__uint_as_float(a.s[e >> 2][(e & 3) + 1]), es_nb);
           uint32_t hh, ll;
           lm_split2(x0, s0, x1, s1, hh, ll);
           hv[q] = hh;
@@ -374,29 +398,32 @@ __global__ __launch_bounds__(LM_THREADS, 1) void k_linear_mfma(
         alo[i] = __builtin_bit_cast(h8v, lv);
       }
     }
-    // fragments in two groups of four (register pressure of the [N][K] kernel)
+  };
+  // column tiles T0 .. T0 + NT - 1
+  auto mfmas = [&](const h8v (&ahi)[2], const h8v (&alo)[2], const h8v* bt, int T0, int NT) {
 #pragma unroll
-    for (int t0 = 0; t0 < 8; t0 += 4) {
-      h8v bt[4];
+    for (int u = 0; u < NT; ++u)
 #pragma unroll
-      for (int u = 0; u < 4; ++u) bt[u] = *reinterpret_cast<const h8v*>(b + lm_frag_off(ks, t0 + u, lane));
-#pragma unroll
-      for (int u = 0; u < 4; ++u)
-#pragma unroll
-        for (int i = 0; i < 2; ++i) {
-          f4v& d = NK ? P[i][t0 + u] : acc[i][t0 + u];
-          d = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi[i], bt[u], d, 0, 0, 0);
-          d = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo[i], bt[u], d, 0, 0, 0);
-        }
-      if (NK && t0 == 0) __builtin_amdgcn_sched_barrier(0);
-    }
+      for (int i = 0; i < 2; ++i) {
+        f4v& d = NK ? P[i][T0 + u] : acc[i][T0 + u];
+        d = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi[i], bt[u], d, 0, 0, 0);
+        d = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo[i], bt[u], d, 0, 0, 0);
+      }
   };
 
+  // Per k step: request the next step's A operands (a whole step ahead)
+  // and this step's 8 B fragments, then build A and run the 32 MFMAs.  The
+  // scheduling barriers keep every request at the top of its step.
+  // A operands of this wave's k step gs (0 .. nsteps-1 over the split)
+  const int nsteps = (st1 - st0) * KPW;
+  auto load_step = [&](A& a, int gs) { load_a(a, st0 + gs / KPW, gs % KPW); };
   if (st0 < st1) {
     Codes cc;
+    A ar[2];
+    float s8[8];
     load_codes(cc, st0);
-    A a_cur, a_nxt;
-    load_a(a_cur, st0, 0);
+    load_step(ar[0], 0);
+    if (nsteps > 1) load_step(ar[1], 1);
     store_codes(cc, sB);
     lm_barrier();
     for (int st = st0; st < st1; ++st) {
@@ -404,17 +431,38 @@ __global__ __launch_bounds__(LM_THREADS, 1) void k_linear_mfma(
       const bool more = st + 1 < st1;
       if (more) load_codes(cc, st + 1);
       const uint8_t* b = sB + buf * LM_STAGE_BYTES;
-#pragma unroll(NK ? 1 : 8)
+#pragma unroll
       for (int jj = 0; jj < KPW; ++jj) {
-        const int ks = wk + WK * jj;
-        if (jj + 1 < KPW) load_a(a_nxt, st, jj + 1);
-        else if (more) load_a(a_nxt, st + 1, 0);
-        compute(a_cur, b, ks);
-        if constexpr (NK) {
-          // the k steps of this wave in block kb = 2 st + ks / 4 end here
-          if (jj + 1 == KPW || (ks >> 2) != ((wk + WK * (jj + 1)) >> 2)) fold(2 * (int64_t)st + (ks >> 2));
+        // slot p holds step gs, the other slot step gs + 1 (KPW even: p = gs % 2)
+        const int p = (KPW & 1) ? 0 : (jj & 1), ks = wk + WK * jj;
+        const int gs = (st - st0) * KPW + jj;
+        // [N][K]: this wave's k steps of block kb = 2 st + ks / 4 start here / end here
+        const bool kb_first = jj == 0 || (ks >> 2) != ((ks - WK) >> 2);
+        const bool kb_last = jj + 1 == KPW || (ks >> 2) != ((ks + WK) >> 2);
+        if (NK && kb_first) block_scales(2 * (int64_t)st + (ks >> 2), s8);
+        // [N][K] (two accumulator sets) reads its fragments in two halves
+        constexpr int BT = NK ? 4 : 8;
+        h8v bt[BT];
+#pragma unroll
+        for (int t = 0; t < BT; ++t) bt[t] = *reinterpret_cast<const h8v*>(b + lm_frag_off(ks, t, lane));
+        h8v ahi[2], alo[2];
+        build(ar[p], ahi, alo);
+        // slot p is free: step gs + 2 goes there, about two steps ahead of its use
+        if constexpr ((KPW & 1) != 0) {
+          ar[0] = ar[1];
+          if (gs + 2 < nsteps) load_step(ar[1], gs + 2);
+        } else {
+          if (gs + 2 < nsteps) load_step(ar[p], gs + 2);
         }
-        a_cur = a_nxt;
+        __builtin_amdgcn_sched_barrier(0);
+        mfmas(ahi, alo, bt, 0, BT);
+        if constexpr (NK) {
+#pragma unroll
+          for (int t = 0; t < 4; ++t) bt[t] = *reinterpret_cast<const h8v*>(b + lm_frag_off(ks, 4 + t, lane));
+          mfmas(ahi, alo, bt, 4, 4);
+          if (kb_last) fold(s8);
+        }
+        __builtin_amdgcn_sched_barrier(0);
       }
       if (more) store_codes(cc, sB + (buf ^ 1) * LM_STAGE_BYTES);
       lm_barrier();
@@ -453,7 +501,7 @@ __global__ __launch_bounds__(LM_THREADS, 1) void k_linear_mfma(
   float bv[8];
 #pragma unroll
   for (int t = 0; t < 8; ++t) bv[t] = (bias && !part) ? bias[n0 + t] : 0.0f;
-  const int esb = (es && !part) ? es[nb] : 0;
+  const int esb = part ? 0 : es_nb;
 #pragma unroll
   for (int i = 0; i < 2; ++i)
 #pragma unroll
@@ -503,54 +551,107 @@ __global__ __launch_bounds__(256) void k_linear_mfma_reduce(const float* __restr
 // Row m of x: ex[m] such that its largest |x| times 2^ex lies in [1, 2)
 // (0 for a zero row), and x * 2^ex zero-padded to Kp columns, as fp32
 // (SPLIT false) or as f16 hi + lo (SPLIT true: hi = RN16(v), lo = RN16(v - hi),
-// v - hi exact in fp32).
+// v - hi exact in fp32).  VEC: 16-byte rows (K * sizeof(T) % 16 == 0, x
+// 16-byte aligned); rows of up to 2048 16-byte chunks stay in registers
+// between the maximum and the scaled copy, longer ones are read twice.
 template <typename T, bool SPLIT>
+__device__ __forceinline__ void lm_put(float* __restrict__ xs, _Float16* __restrict__ xh, _Float16* __restrict__ xl,
+                                       int64_t at, float v) {
+  if constexpr (SPLIT) {
+    const _Float16 h = (_Float16)v;
+    xh[at] = h;
+    xl[at] = (_Float16)(v - (float)h);
+  } else {
+    xs[at] = v;
+  }
+}
+
+template <typename T, bool SPLIT, bool VEC>
 __global__ __launch_bounds__(256) void k_linear_mfma_prep_rows(const T* __restrict__ x, int64_t K, int64_t Kp,
                                                                float* __restrict__ xs, _Float16* __restrict__ xh,
                                                                _Float16* __restrict__ xl, int* __restrict__ ex) {
+  constexpr int E = 16 / (int)sizeof(T), NCH = 8;
   __shared__ float red[4];
   const int64_t m = blockIdx.x;
+  const int tid = threadIdx.x;
   const T* row = x + m * K;
+  const int64_t nch = K / E;
+  const bool cached = VEC && nch <= (int64_t)NCH * 256;
+  u4v c[NCH];
+  auto elems = [&](const u4v& w, float (&v)[E]) {
+    const T* t = reinterpret_cast<const T*>(&w);
+#pragma unroll
+    for (int e = 0; e < E; ++e) v[e] = ElemT<T>::cvt(t[e]);
+  };
   float mx = 0.0f;
-  for (int64_t k = threadIdx.x; k < K; k += 256) mx = fmaxf(mx, __builtin_fabsf(ElemT<T>::cvt(row[k])));
+  if (cached) {
+#pragma unroll
+    for (int q = 0; q < NCH; ++q) {
+      const int64_t ch = tid + 256 * q;
+      c[q] = ch < nch ? *reinterpret_cast<const u4v*>(row + ch * E) : u4v{0u, 0u, 0u, 0u};
+    }
+#pragma unroll
+    for (int q = 0; q < NCH; ++q) {
+      float v[E];
+      elems(c[q], v);
+#pragma unroll
+      for (int e = 0; e < E; ++e) mx = fmaxf(mx, __builtin_fabsf(v[e]));
+    }
+  } else {
+    for (int64_t k = tid; k < K; k += 256) mx = fmaxf(mx, __builtin_fabsf(ElemT<T>::cvt(row[k])));
+  }
   mx = group_max<64>(mx);
-  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = mx;
+  if ((tid & 63) == 0) red[tid >> 6] = mx;
   __syncthreads();
   mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
   const int be = (int)((__float_as_uint(mx) >> 23) & 0xFFu);
   const int e = (be == 0xFF || mx == 0.0f) ? 0 : 127 - (be == 0 ? 1 : be);
-  if (threadIdx.x == 0) ex[m] = e;
-  for (int64_t k = threadIdx.x; k < Kp; k += 256) {
-    const float v = k < K ? __builtin_ldexpf(ElemT<T>::cvt(row[k]), e) : 0.0f;
-    if constexpr (SPLIT) {
-      const _Float16 h = (_Float16)v;
-      xh[m * Kp + k] = h;
-      xl[m * Kp + k] = (_Float16)(v - (float)h);
-    } else {
-      xs[m * Kp + k] = v;
+  if (tid == 0) ex[m] = e;
+  const int64_t base = m * Kp;
+  if (cached) {
+#pragma unroll
+    for (int q = 0; q < NCH; ++q) {
+      const int64_t ch = tid + 256 * q;
+      if (ch >= nch) break;
+      float v[E];
+      elems(c[q], v);
+#pragma unroll
+      for (int u = 0; u < E; ++u) v[u] = __builtin_ldexpf(v[u], e);
+      const int64_t at = base + ch * E;
+      if constexpr (SPLIT) {
+        _Float16 h[E], l[E];
+#pragma unroll
+        for (int u = 0; u < E; ++u) {
+          h[u] = (_Float16)v[u];
+          l[u] = (_Float16)(v[u] - (float)h[u]);
+        }
+        if constexpr (E == 4) {
+          *reinterpret_cast<u2v*>(xh + at) = __builtin_bit_cast(u2v, h);
+          *reinterpret_cast<u2v*>(xl + at) = __builtin_bit_cast(u2v, l);
+        } else {
+          *reinterpret_cast<u4v*>(xh + at) = __builtin_bit_cast(u4v, h);
+          *reinterpret_cast<u4v*>(xl + at) = __builtin_bit_cast(u4v, l);
+        }
+      } else {
+#pragma unroll
+        for (int u = 0; u < E; u += 4) *reinterpret_cast<f4v*>(xs + at + u) = f4v{v[u], v[u + 1], v[u + 2], v[u + 3]};
+      }
     }
+    for (int64_t k = K + tid; k < Kp; k += 256) lm_put<T, SPLIT>(xs, xh, xl, base + k, 0.0f);
+  } else {
+    for (int64_t k = tid; k < Kp; k += 256)
+      lm_put<T, SPLIT>(xs, xh, xl, base + k, k < K ? __builtin_ldexpf(ElemT<T>::cvt(row[k]), e) : 0.0f);
   }
 }
 
-// Column block nb of a [K][N] weight's scales (block-major sT[nb][k] when
-// kb_major, else s[k][nb]): es[nb] such that the largest scale times 2^es
-// lies in [2^13, 2^14), and sc[nb][k] = s * 2^es zero-padded to Kp.
-__global__ __launch_bounds__(256) void k_linear_mfma_prep_scales(const float* __restrict__ s, int kb_major,
-                                                                 int64_t K, int64_t Kp, int64_t NB,
-                                                                 float* __restrict__ sc, int* __restrict__ es) {
-  __shared__ float red[4];
-  const int64_t nb = blockIdx.x;
-  auto at = [&](int64_t k) { return kb_major ? s[nb * K + k] : s[k * NB + nb]; };
-  float mx = 0.0f;
-  for (int64_t k = threadIdx.x; k < K; k += 256) mx = fmaxf(mx, __builtin_fabsf(at(k)));
-  mx = group_max<64>(mx);
-  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = mx;
-  __syncthreads();
-  mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-  const int be = (int)((__float_as_uint(mx) >> 23) & 0xFFu);
-  const int e = (be == 0xFF || mx == 0.0f) ? 0 : 140 - (be == 0 ? 1 : be);
-  if (threadIdx.x == 0) es[nb] = e;
-  for (int64_t k = threadIdx.x; k < Kp; k += 256) sc[nb * Kp + k] = k < K ? __builtin_ldexpf(at(k), e) : 0.0f;
+// Block-major copy sT[nb][k] = s[k][nb] of a [K][N] weight's scales (when
+// the caller has none)
+__global__ __launch_bounds__(256) void k_linear_mfma_scales_t(const float* __restrict__ s, int64_t K, int64_t NB,
+                                                              float* __restrict__ sT) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= K * NB) return;
+  const int64_t nb = i / K, k = i % K;
+  sT[i] = s[k * NB + nb];
 }
 
 // ---------------------------------------------------------------- plan
@@ -562,17 +663,21 @@ struct LmPlan {
 
 inline size_t lm_round(size_t v) { return (v + 255) & ~(size_t)255; }
 
+// Largest row tile (WM) per kernel: the [N][K] kernel holds a second set of
+// accumulators (the block sums), so its wider tiles would spill registers.
+constexpr int lm_max_wm(bool nk, int bits) { return nk ? (bits == 8 ? 2 : 4) : 8; }
+
 // Row tile: the largest WM (32 WM rows) that still gives every CU a
 // workgroup; when none does, the fewest row tiles, and K splits across
 // workgroups to fill the CUs.
-LmPlan lm_plan(int64_t M, int64_t K, int64_t N, bool nk) {
+LmPlan lm_plan(int64_t M, int64_t K, int64_t N, bool nk, int bits) {
   LmPlan p;
   p.Kp = ceil_div(K, LM_STAGE) * LM_STAGE;
   const int nst = (int)(p.Kp / LM_STAGE);
   const int64_t NB = N / 128, target = num_cus();
   const int64_t m32 = ceil_div(M, 32);
   int wm = 1;
-  while (wm < 8 && wm * 2 <= m32) wm *= 2;
+  while (wm < lm_max_wm(nk, bits) && wm * 2 <= m32) wm *= 2;
   int pick = 0;
   for (int c = wm; c >= 1; c /= 2)
     if (NB * ceil_div(M, 32 * c) >= target) {
@@ -595,8 +700,8 @@ LmPlan lm_plan(int64_t M, int64_t K, int64_t N, bool nk) {
   o += lm_round((size_t)NB * 4);
   p.off_x = o;
   o += lm_round((size_t)M * (size_t)p.Kp * 4);  // fp32 x', or f16 hi + lo
-  p.off_s = o;
-  if (!nk) o += lm_round((size_t)NB * (size_t)p.Kp * 4);
+  p.off_s = o;  // [K][N]: room for a block-major copy of the scales when the caller has none
+  if (!nk) o += lm_round((size_t)NB * (size_t)K * 4);
   p.off_p = o;
   if (p.S > 1) o += lm_round((size_t)p.S * (size_t)M * (size_t)N * 4);
   p.bytes = o;
@@ -605,7 +710,7 @@ LmPlan lm_plan(int64_t M, int64_t K, int64_t N, bool nk) {
 
 template <int BITS, int WM, bool NK>
 void lm_launch_t(const LmPlan& p, hipStream_t st, const float* xs, const _Float16* xh, const _Float16* xl,
-                 const float* sc, int sc_kbm, const int* ex, const int* es, const uint8_t* w, int64_t M, int64_t K,
+                 const float* sc, int sc_kbm, const int* ex, int* es, const uint8_t* w, int64_t M, int64_t K,
                  int64_t N, const float* bias, float* out, float* part) {
   const dim3 grid((unsigned)(N / 128), (unsigned)ceil_div(M, 32 * WM), (unsigned)p.S);
   hipLaunchKernelGGL((k_linear_mfma<BITS, WM, NK>), grid, dim3(LM_THREADS), 0, st, xs, xh, xl, sc, sc_kbm, ex, es, w,
@@ -614,29 +719,33 @@ void lm_launch_t(const LmPlan& p, hipStream_t st, const float* xs, const _Float1
 
 template <int BITS, bool NK>
 void lm_launch_w(const LmPlan& p, hipStream_t st, const float* xs, const _Float16* xh, const _Float16* xl,
-                 const float* sc, int sc_kbm, const int* ex, const int* es, const uint8_t* w, int64_t M, int64_t K,
+                 const float* sc, int sc_kbm, const int* ex, int* es, const uint8_t* w, int64_t M, int64_t K,
                  int64_t N, const float* bias, float* out, float* part) {
+  constexpr int MW = lm_max_wm(NK, BITS);
   switch (p.wm) {
-    case 8: lm_launch_t<BITS, 8, NK>(p, st, xs, xh, xl, sc, sc_kbm, ex, es, w, M, K, N, bias, out, part); break;
-    case 4: lm_launch_t<BITS, 4, NK>(p, st, xs, xh, xl, sc, sc_kbm, ex, es, w, M, K, N, bias, out, part); break;
+    case 8: lm_launch_t<BITS, MW < 8 ? MW : 8, NK>(p, st, xs, xh, xl, sc, sc_kbm, ex, es, w, M, K, N, bias, out, part); break;
+    case 4: lm_launch_t<BITS, MW < 4 ? MW : 4, NK>(p, st, xs, xh, xl, sc, sc_kbm, ex, es, w, M, K, N, bias, out, part); break;
     case 2: lm_launch_t<BITS, 2, NK>(p, st, xs, xh, xl, sc, sc_kbm, ex, es, w, M, K, N, bias, out, part); break;
     default: lm_launch_t<BITS, 1, NK>(p, st, xs, xh, xl, sc, sc_kbm, ex, es, w, M, K, N, bias, out, part); break;
   }
 }
 
+template <typename T, bool SPLIT>
+void lm_prep_rows_t(const T* x, int64_t M, int64_t K, int64_t Kp, float* xs, _Float16* xh, _Float16* xl, int* ex,
+                    hipStream_t st) {
+  const dim3 grid((unsigned)M);
+  if (aligned16(x) && (K * (int64_t)sizeof(T)) % 16 == 0)
+    hipLaunchKernelGGL((k_linear_mfma_prep_rows<T, SPLIT, true>), grid, dim3(256), 0, st, x, K, Kp, xs, xh, xl, ex);
+  else
+    hipLaunchKernelGGL((k_linear_mfma_prep_rows<T, SPLIT, false>), grid, dim3(256), 0, st, x, K, Kp, xs, xh, xl, ex);
+}
+
 template <bool SPLIT>
 void lm_prep_rows(const void* x, int x_type, int64_t M, int64_t K, int64_t Kp, float* xs, _Float16* xh, _Float16* xl,
                   int* ex, hipStream_t st) {
-  const dim3 grid((unsigned)M);
-  if (x_type == MXK_IN_F32)
-    hipLaunchKernelGGL((k_linear_mfma_prep_rows<float, SPLIT>), grid, dim3(256), 0, st, (const float*)x, K, Kp, xs, xh,
-                       xl, ex);
-  else if (x_type == MXK_IN_F16)
-    hipLaunchKernelGGL((k_linear_mfma_prep_rows<__half, SPLIT>), grid, dim3(256), 0, st, (const __half*)x, K, Kp, xs,
-                       xh, xl, ex);
-  else
-    hipLaunchKernelGGL((k_linear_mfma_prep_rows<hip_bfloat16, SPLIT>), grid, dim3(256), 0, st,
-                       (const hip_bfloat16*)x, K, Kp, xs, xh, xl, ex);
+  if (x_type == MXK_IN_F32) lm_prep_rows_t<float, SPLIT>((const float*)x, M, K, Kp, xs, xh, xl, ex, st);
+  else if (x_type == MXK_IN_F16) lm_prep_rows_t<__half, SPLIT>((const __half*)x, M, K, Kp, xs, xh, xl, ex, st);
+  else lm_prep_rows_t<hip_bfloat16, SPLIT>((const hip_bfloat16*)x, M, K, Kp, xs, xh, xl, ex, st);
 }
 
 bool lm_common_ok(int64_t M, int64_t K, int64_t N, int kind, int bits, int block, int x_type, const float* out) {
@@ -659,7 +768,7 @@ bool lm_common_ok(int64_t M, int64_t K, int64_t N, int kind, int bits, int block
 size_t linear_mfma_workspace(int64_t M, int64_t K, int64_t N, int bits, int block, bool nk) {
   if ((bits != 4 && bits != 8) || block != 128 || M < 1 || K < 1 || N < 128 || N % 128 != 0) return 0;
   if (nk && K % 128 != 0) return 0;
-  return lm_plan(M, K, N, nk).bytes;
+  return lm_plan(M, K, N, nk, bits).bytes;
 }
 
 // [K][N] weight (mx_linear).  Returns MXK_EUNSUPPORTED, with nothing
@@ -669,7 +778,7 @@ int linear_mfma_kn(const void* x, int x_type, int64_t M, int64_t K, const void* 
                    void* workspace, size_t workspace_nbytes, hipStream_t st) {
   if (!lm_common_ok(M, K, N, kind, bits, block, x_type, out)) return MXK_EUNSUPPORTED;
   if ((reinterpret_cast<uintptr_t>(w_packed) & (bits == 8 ? 7u : 3u)) != 0) return MXK_EUNSUPPORTED;
-  const LmPlan p = lm_plan(M, K, N, false);
+  const LmPlan p = lm_plan(M, K, N, false, bits);
   if (!workspace || workspace_nbytes < p.bytes)
     return fail(MXK_EINVAL, "linear_wq: needs a workspace of mxk_linear_workspace() bytes");
   uint8_t* ws = reinterpret_cast<uint8_t*>(workspace);
@@ -680,11 +789,15 @@ int linear_mfma_kn(const void* x, int x_type, int64_t M, int64_t K, const void* 
   float* part = reinterpret_cast<float*>(ws + p.off_p);
   const int64_t NB = N / 128;
   lm_prep_rows<false>(x, x_type, M, K, p.Kp, xs, nullptr, nullptr, ex, st);
-  hipLaunchKernelGGL(k_linear_mfma_prep_scales, dim3((unsigned)NB), dim3(256), 0, st,
-                     w_scales_t ? w_scales_t : w_scales, w_scales_t ? 1 : 0, K, p.Kp, NB, sc, es);
+  const float* sT = w_scales_t;
+  if (!sT) {
+    hipLaunchKernelGGL(k_linear_mfma_scales_t, dim3((unsigned)ceil_div(K * NB, 256)), dim3(256), 0, st, w_scales, K,
+                       NB, sc);
+    sT = sc;
+  }
   const uint8_t* w = reinterpret_cast<const uint8_t*>(w_packed);
-  if (bits == 4) lm_launch_w<4, false>(p, st, xs, nullptr, nullptr, sc, 1, ex, es, w, M, K, N, bias, out, part);
-  else lm_launch_w<8, false>(p, st, xs, nullptr, nullptr, sc, 1, ex, es, w, M, K, N, bias, out, part);
+  if (bits == 4) lm_launch_w<4, false>(p, st, xs, nullptr, nullptr, sT, 1, ex, es, w, M, K, N, bias, out, part);
+  else lm_launch_w<8, false>(p, st, xs, nullptr, nullptr, sT, 1, ex, es, w, M, K, N, bias, out, part);
   if (p.S > 1)
     hipLaunchKernelGGL(k_linear_mfma_reduce, dim3((unsigned)ceil_div(M * N / 4, 256)), dim3(256), 0, st, part, p.S,
                        M, N, ex, es, bias, out);
@@ -699,7 +812,7 @@ int linear_mfma_nk(const void* x, int x_type, int64_t M, int64_t K, const void* 
   if (!lm_common_ok(M, K, N, kind, bits, block, x_type, out) || K % 128 != 0) return MXK_EUNSUPPORTED;
   if (!aligned16(w_packed)) return MXK_EUNSUPPORTED;
   if (N * K * bits / 8 >= (int64_t(1) << 31) || N * (K / 128) * 4 >= (int64_t(1) << 31)) return MXK_EUNSUPPORTED;
-  const LmPlan p = lm_plan(M, K, N, true);
+  const LmPlan p = lm_plan(M, K, N, true, bits);
   if (!workspace || workspace_nbytes < p.bytes)
     return fail(MXK_EINVAL, "linear_wq_nt: needs a workspace of mxk_linear_nt_workspace() bytes");
   uint8_t* ws = reinterpret_cast<uint8_t*>(workspace);
