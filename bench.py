@@ -27,7 +27,10 @@ path restated with the same torch ops) on the full config-2 workload, 2
 warm-ups then the median of 5, on this host's cores.
 
 `extras`: configs 1, 3, 4 and 5 measured the same way, each with its
-roofline fraction (HBM 8.0 TB/s, dense int8 MFMA 5.0 POP/s).
+roofline fraction (HBM 8.0 TB/s, dense int8 MFMA 5.0 POP/s, dense f16 MFMA
+2.5 PFLOP/s), config 2 with bfloat16 activations, config 1 with its two
+quantizes, mx_linear beyond the decode shape, and the CPU oracle on bounded
+samples of configs 1, 3, 4 and 5.
 """
 from __future__ import annotations
 
@@ -46,6 +49,7 @@ if ROOT not in sys.path:
 
 HBM_PEAK_GBS = 8000.0
 INT8_PEAK_TOPS = 5000.0
+F16_PEAK_TFLOPS = 2500.0
 PROFILES = os.path.join(ROOT, "profiles")
 
 
@@ -158,6 +162,18 @@ def bench_linear(args, qa):
     res = {"sec": sec, "algo_bytes": algo_bytes, "gbs": gbs, "y": y.cpu(),
            "w_packed": m._mx_weight._mx_packed.cpu(), "w_scales": m._mx_weight._mx_scales.cpu(),
            "x": x_cpu}
+    # the same step with config 2's bfloat16 activations (x.float() is exact)
+    xb = x.bfloat16()
+    it[0] = 0
+
+    def step_bf16():
+        layers[it[0] % N_LAYERS](xb)
+        it[0] += 1
+
+    sec_b = graph_time(step_bf16, args.steps, args.warmup)
+    algo_b = K * N // 2 + (K * N // 128) * 4 + 16 * K * 2 + 16 * N * 4
+    res["bf16"] = {"us": round(sec_b * 1e6, 3), "GBs": round(algo_b / sec_b / 1e9, 1),
+                   "frac": round(algo_b / sec_b / 1e9 / HBM_PEAK_GBS, 4), "bytes": algo_b}
     return res
 
 
@@ -235,6 +251,130 @@ def bench_gemm(qa, M, K, N, reps, dtype="int8d"):
     return {"shape": [M, K, N], "fp32_out_us": round(t_c * 1e6, 2), "fp32_out_TOPS": round(ops / t_c / 1e12, 2),
             "fp32_out_frac_int8_peak": round(ops / t_c / 1e12 / INT8_PEAK_TOPS, 4),
             "packed_int16d_out_us": round(t_p * 1e6, 2), "packed_TOPS": round(ops / t_p / 1e12, 2)}
+
+
+def bench_config1_full(qa, reps):
+    """Config 1 end to end: quantize the fp32 512x512 A and B (int8d block
+    128), then the packed GEMM A_q @ B_q with the reference's int16d output
+    (mxtorch.py:1684-1763, 5497-5573): three launches of quantize + the GEMM
+    kernels per step."""
+    dev = torch.device("cuda:0")
+    A = torch.randn(512, 512, generator=gen(0)).to(dev)
+    B = torch.randn(512, 512, generator=gen(1)).to(dev)
+    dt = qa.get_mx_dtype("int8d")
+
+    def step():
+        qa.mx_tensor.quantize(A, dt, 128) @ qa.mx_tensor.quantize(B, dt, 128)
+
+    t = graph_time(step, reps, 2, repeats=3)
+    ops = 2.0 * 512 ** 3
+    return {"us": round(t * 1e6, 2), "TOPS": round(ops / t / 1e12, 3),
+            "note": "quantize A and B + packed GEMM + int16d requantization per step"}
+
+
+def bench_linear_mfma(qa, reps):
+    """mx_linear beyond the decode shape (mxtorch.py:7454-7473): x fp32 [M,
+    8192] @ dequant(W [8192, 8192] stored as quantize(W.t())), M = 512 and
+    8192, int4d and int8d weights.  The kernel issues two f16 MFMAs per
+    product (x*s as hi + lo against the exact codes), so the f16 MFMA work is
+    twice 2*M*K*N; frac_f16_peak is that work over 2.5 PFLOP/s dense f16."""
+    dev = torch.device("cuda:0")
+    K = N = 8192
+    _, W_cpu = config2_inputs()
+    lin = torch.nn.Linear(K, N, bias=False)
+    with torch.no_grad():
+        lin.weight.copy_(W_cpu)
+    lin = lin.to(dev)
+    out = {}
+    for name in ("int4d", "int8d"):
+        m = qa.mx_linear.from_linear(lin, qa.get_mx_dtype(name), 128)
+        for M in (512, 8192):
+            x = torch.randn(M, K, generator=gen(20 + M, "cuda"), device=dev)
+            with torch.no_grad():
+                m(x)
+                t = graph_time(lambda: m(x), reps if M <= 512 else max(2, reps // 4), 1, repeats=3)
+            flops = 2.0 * M * K * N
+            out[f"{name}_{M}x{K}x{N}"] = {"us": round(t * 1e6, 2), "TFLOPS": round(flops / t / 1e12, 1),
+                                          "f16_mfma_TFLOPS": round(2 * flops / t / 1e12, 1),
+                                          "frac_f16_peak": round(2 * flops / t / 1e12 / F16_PEAK_TFLOPS, 4)}
+            del x
+        del m
+        torch.cuda.empty_cache()
+    return out
+
+
+def cpu_baselines_extra():
+    """The CPU oracle (the reference's CPU path restated) on bounded
+    samples of configs 1, 3, 4 and 5, 2 warm-ups then the median of 5, on
+    this host's cores; each entry states its sample."""
+    from oracle import mx_oracle as orc
+
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+
+    def timed(f, runs=5):
+        for _ in range(2):
+            f()
+        ts = []
+        for _ in range(runs):
+            t0 = time.perf_counter()
+            f()
+            ts.append(time.perf_counter() - t0)
+        return statistics.median(ts)
+
+    out = {}
+    A = torch.randn(512, 512, generator=gen(0))
+    B = torch.randn(512, 512, generator=gen(1))
+
+    def c1():
+        pa, sa, na = orc.quantize(A, "int8d", 128)
+        pb, sb, nb = orc.quantize(B, "int8d", 128)
+        orc.dispatch_qgemm(pa, sa, "int8d", (512, 512), na, pb, sb, "int8d", (512, 512), nb, 128)
+
+    t = timed(c1)
+    out["config1"] = {"value": round(2 * 512 ** 3 / t / 1e12, 5), "unit": "TOPS", "cores": cores, "kind": "port",
+                      "sample": "full config 1: quantize A, B (int8d) + _dispatch_qgemm 512^3", "sec": round(t, 5)}
+    # config 3: the first 512 rows of A against all of B (the product's rows are independent)
+    Mr, K, N = 512, 8192, 8192
+    a = torch.randint(-127, 128, (Mr * K,), generator=gen(5), dtype=torch.int32)
+    b = torch.randint(-127, 128, (K * N,), generator=gen(6), dtype=torch.int32)
+    sa = torch.rand(Mr * K // 128, generator=gen(7)) * 0.02
+    sb = torch.rand(K * N // 128, generator=gen(8)) * 0.02
+    t = timed(lambda: orc.qscale_matmul(a, sa, b, sb, Mr, K, N, 8, 128, 16, return_c=True), runs=3)
+    out["config3"] = {"value": round(2.0 * Mr * K * N / t / 1e12, 5), "unit": "TOPS", "cores": cores,
+                      "kind": "port", "sample": "512 of the 8192 rows of the 8192^3 _qscale_matmul "
+                                                "(64 K-block mm + epilogue + int16 requant), median of 3",
+                      "sec": round(t, 4)}
+    del a, b
+    # config 4: 2^24 elements of the seeded fp32 tensor, quantize then dequantize
+    n = 1 << 24
+    x = torch.randn(n, generator=gen(7))
+    x[torch.rand(n, generator=gen(8)) < 1e-3] *= 50
+    x = x.view(-1, 128)
+    c4 = {}
+    for name in ("int8d", "int4d", "float4d"):
+        bits = 8 if name.endswith("8d") else 4
+        algo = n * 4 + n * bits // 8 + (n // 128) * 4
+        tq = timed(lambda: orc.quantize(x, name, 128))
+        pk, sc, _ = orc.quantize(x, name, 128)
+        td = timed(lambda: orc.dequant(pk, sc, name, n, 128))
+        c4[name] = {"quantize_GBs": round(algo / tq / 1e9, 3), "dequantize_GBs": round(algo / td / 1e9, 3)}
+    out["config4"] = {"value": c4["int4d"]["quantize_GBs"], "unit": "GB/s", "cores": cores, "kind": "port",
+                      "sample": "2^24 of the 2^28 elements (int4d quantize is `value`)", "dtypes": c4}
+    # config 5: 2^17 rows of 128 fp16 (2^24 elements) of K, int8dv and int4d
+    kx = torch.randn(1 << 17, 128, generator=gen(9)).half()
+    c5 = {}
+    for name in ("int8dv", "int4d"):
+        bits = 8 if name.startswith("int8") else 4
+        nq = kx.numel()
+        tq = timed(lambda: orc.quantize(kx, name, 128))
+        pk, sc, _ = orc.quantize(kx, name, 128)
+        td = timed(lambda: orc.dequant(pk, sc, name, nq, 128))
+        c5[name] = {"quantize_GBs": round((nq * 2 + nq * bits // 8 + nq // 128 * 4) / tq / 1e9, 3),
+                    "dequantize_GBs": round((nq * 4 + nq * bits // 8 + nq // 128 * 4) / td / 1e9, 3)}
+    out["config5"] = {"value": c5["int8dv"]["quantize_GBs"], "unit": "GB/s", "cores": cores, "kind": "port",
+                      "sample": "2^17 rows x 128 of the fp16 K tensor (int8dv quantize is `value`)", "dtypes": c5}
+    return out
 
 
 def bench_kv(qa, reps):
@@ -400,7 +540,7 @@ def main():
     ap.add_argument("--no-extras", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--only", default="",
-                    help="comma list of extras: quant,gemm,gemm4,kv,kvstream,elementwise,small,dynamic")
+                    help="comma list of extras: quant,gemm,gemm4,kv,kvstream,elementwise,small,mfma,dynamic,cpu")
     ap.add_argument("--eager", action="store_true", help="no graph capture (for rocprofv3 --pmc runs)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a plain 512 MiB device copy (the reference kernel for HBM counter scaling)")
@@ -452,8 +592,12 @@ def main():
     if not args.no_extras:
         only = set(filter(None, args.only.split(",")))
         extras = {}
+        extras["config2_bf16_x"] = res["bf16"]
         if not only or "small" in only:
             extras["config1_int8d_gemm_512"] = bench_gemm(qa, 512, 512, 512, 50)
+            extras["config1_with_quantize_512"] = bench_config1_full(qa, 50)
+        if not only or "mfma" in only:
+            extras["mx_linear_mfma"] = bench_linear_mfma(qa, 20)
         if not only or "gemm" in only:
             extras["config3_int8d_gemm_8192"] = bench_gemm(qa, 8192, 8192, 8192, 3)
         if not only or "gemm4" in only:
@@ -468,6 +612,8 @@ def main():
             extras["kv_ring_stream_8x32x128_T4096"] = bench_kv_stream(qa, 64)
         if not only or "dynamic" in only:
             extras["dynamic_int8"] = bench_dynamic(qa, 120, 5)
+        if not args.no_cpu and (not only or "cpu" in only):
+            extras["cpu_baselines"] = cpu_baselines_extra()
         line["extras"] = extras
     print(json.dumps(line))
 

@@ -102,6 +102,29 @@ __device__ __forceinline__ float group_max(float v) {
   return v;
 }
 
+// NaN-propagating block maxima.  torch's amax returns NaN for a block that
+// holds a NaN and clamp(min=1e-12) keeps it (mxtorch.py:1456-1457, 1497,
+// 1748), so that block's scale is NaN.  Magnitudes compared as unsigned
+// integers order like floats, and every NaN (sign cleared) sorts above
+// +inf, so an integer maximum over the magnitude bits propagates it.
+__device__ __forceinline__ uint32_t mag_bits(float v) { return __float_as_uint(v) & 0x7FFFFFFFu; }
+
+template <int G>
+__device__ __forceinline__ uint32_t group_max_u(uint32_t v) {
+  if constexpr (G >= 2) v = max(v, (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0xB1, 0xF, 0xF, true));
+  if constexpr (G >= 4) v = max(v, (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x4E, 0xF, 0xF, true));
+  if constexpr (G >= 8) v = max(v, (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x141, 0xF, 0xF, true));
+  if constexpr (G >= 16) v = max(v, (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x140, 0xF, 0xF, true));
+  if constexpr (G >= 32) v = max(v, (uint32_t)__builtin_amdgcn_ds_swizzle((int)v, 0x401F));
+  if constexpr (G >= 64) v = max(v, (uint32_t)__shfl_xor((int)v, 32));
+  return v;
+}
+
+// max(a, fl32(1e-12)) of a magnitude given by its bits, keeping a NaN
+__device__ __forceinline__ float amax_clamped(uint32_t m) {
+  return __uint_as_float(max(m, __float_as_uint(MXK_AMIN)));
+}
+
 // ---------------------------------------------------------------- element loads
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
@@ -285,6 +308,8 @@ __device__ __forceinline__ BlockParams block_params(float ap, float qf) {
     bp.s = ap;
     bp.mul = 1.0f / ap;
   }
+  // a NaN scale is stored as the reference's host makes it: 0x7FC00000
+  if (!(bp.s == bp.s)) bp.s = __uint_as_float(0x7FC00000u);
   return bp;
 }
 
@@ -399,6 +424,30 @@ __device__ __forceinline__ int encode(float v, const BlockParams& bp, float qf, 
     return bucket<BITS>(div_rn(v, bp.s, bp.mul), P);
   }
 }
+
+// Codes of a block whose scale is not finite (a NaN in the block makes it
+// NaN, an infinity makes it +inf), as the reference's CPU path computes
+// them: the quotient by a true division (the multiplier of Q_INT is then
+// NaN or 0); a NaN quotient converts to INT_MIN on the reference's host,
+// whose stored field is 0, and a float code is bucketize's last index for
+// it; int1 codes take the sign rule as always.  Out of the hot loops:
+// kernels branch here per block.
+template <int MODE, int BITS>
+__device__ __forceinline__ int encode_nonfinite(float v, const BlockParams& bp, float qf, const float* P) {
+  if constexpr (MODE == Q_INT1) {
+    return v >= 0.0f ? 0 : 1;
+  } else if constexpr (MODE == Q_FP) {
+    const float y = v / bp.s;
+    if (!(y == y)) return (1 << BITS) - 1;
+    if constexpr (BITS == 4) return bucket_fp4(y);
+    else return bucket<BITS>(y, P);
+  } else {
+    const float y = MODE == Q_INT ? v * bp.mul : v / bp.s;
+    if (!(y == y)) return 0;
+    return (int)rne(fminf(fmaxf(y, -qf), qf));
+  }
+}
+__device__ __forceinline__ bool finite_scale(float s) { return __builtin_fabsf(s) < __builtin_inff(); }
 
 // encode<> with float codes through the key table of build_fp_keys (T
 // unused for the other formats)

@@ -105,19 +105,23 @@ __global__ __launch_bounds__(256) void k_quant_fast(const T* __restrict__ x, int
 #pragma unroll
       for (int q = 0; q < Q; ++q) load_elems<T, CH>(x, nblk * B + q * (B / Q) + (int64_t)li * CH, n, vn[q]);
     }
-    float m = 0.0f;
+    uint32_t mb = 0u;
 #pragma unroll
     for (int q = 0; q < Q; ++q)
 #pragma unroll
-      for (int i = 0; i < CH; ++i) m = fmaxf(m, __builtin_fabsf(v[q][i]));
-    const float ap = fmaxf(group_max<LPB>(m), MXK_AMIN);
+      for (int i = 0; i < CH; ++i) mb = max(mb, mag_bits(v[q][i]));
+    const float ap = amax_clamped(group_max_u<LPB>(mb));
     const BlockParams bp = block_params<MODE>(ap, qf);
+    // a NaN or an infinity in the block: its codes take encode_nonfinite
+    const bool nf = MODE != Q_INT1 && !finite_scale(bp.s);
     // the 'v' rule from 16-bit input divides a lane's values after one wave
     // vote (fp16 int8dv 0.66 -> 0.71 of 8 TB/s; per-element checks elsewhere)
     constexpr bool VOTE = MODE == Q_VEC && sizeof(T) == 2;
     if constexpr (VOTE) {
+      if (!nf) {
 #pragma unroll
-      for (int q = 0; q < Q; ++q) div_rn_all<CH>(v[q], bp.s, bp.mul);
+        for (int q = 0; q < Q; ++q) div_rn_all<CH>(v[q], bp.s, bp.mul);
+      }
     }
 #pragma unroll
     for (int q = 0; q < Q; ++q) {
@@ -125,11 +129,19 @@ __global__ __launch_bounds__(256) void k_quant_fast(const T* __restrict__ x, int
       uint32_t w[NW];
 #pragma unroll
       for (int k = 0; k < NW; ++k) w[k] = 0u;
+      if (__builtin_expect(nf, 0)) {
 #pragma unroll
-      for (int i = 0; i < CH; ++i) {
-        const uint32_t f =
-            (uint32_t)(VOTE ? encode_vec_q(v[q][i], qf) : encode_keyed<MODE, BITS>(v[q][i], bp, qf, sP, sK)) & MASK;
-        w[(i * BITS) >> 5] |= f << ((i * BITS) & 31);
+        for (int i = 0; i < CH; ++i) {
+          const uint32_t f = (uint32_t)encode_nonfinite<MODE, BITS>(v[q][i], bp, qf, sP) & MASK;
+          w[(i * BITS) >> 5] |= f << ((i * BITS) & 31);
+        }
+      } else {
+#pragma unroll
+        for (int i = 0; i < CH; ++i) {
+          const uint32_t f = (uint32_t)(VOTE ? encode_vec_q(v[q][i], qf)
+                                             : encode_keyed<MODE, BITS>(v[q][i], bp, qf, sP, sK)) & MASK;
+          w[(i * BITS) >> 5] |= f << ((i * BITS) & 31);
+        }
       }
       if (idx + CH > n_store) clear_tail<NW, BITS>(w, n_store - idx);
       if constexpr (NIB) {
@@ -158,13 +170,13 @@ __global__ __launch_bounds__(NT) void k_quant_rows(const T* __restrict__ x, int6
   constexpr uint32_t MASK = BITS == 32 ? 0xFFFFFFFFu : ((1u << BITS) - 1u);
   constexpr int H = MODE == Q_FP ? (1 << (BITS - 1)) : 1;
   __shared__ float sP[H + 1];
-  __shared__ float s_max[NT / 64];
+  __shared__ uint32_t s_max[NT / 64];
   if constexpr (MODE == Q_FP && BITS != 4) build_tables<BITS>(sP, nullptr);  // FP4 buckets by constants
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int chunks = block / 8;
   for (int64_t blk = blockIdx.x; blk < nb; blk += gridDim.x) {
     float v[R][8];
-    float m = 0.0f;
+    uint32_t m = 0u;
 #pragma unroll
     for (int r = 0; r < R; ++r) {
       const int c = threadIdx.x + NT * r;
@@ -175,16 +187,17 @@ __global__ __launch_bounds__(NT) void k_quant_rows(const T* __restrict__ x, int6
         for (int e = 0; e < 8; ++e) v[r][e] = 0.0f;
       }
 #pragma unroll
-      for (int e = 0; e < 8; ++e) m = fmaxf(m, __builtin_fabsf(v[r][e]));
+      for (int e = 0; e < 8; ++e) m = max(m, mag_bits(v[r][e]));
     }
-    m = group_max<64>(m);
+    m = group_max_u<64>(m);
     if (lane == 0) s_max[wave] = m;
     __syncthreads();
-    float am = s_max[0];
+    uint32_t am = s_max[0];
 #pragma unroll
-    for (int q = 1; q < NT / 64; ++q) am = fmaxf(am, s_max[q]);
-    const float ap = fmaxf(am, MXK_AMIN);
+    for (int q = 1; q < NT / 64; ++q) am = max(am, s_max[q]);
+    const float ap = amax_clamped(am);
     const BlockParams bp = block_params<MODE>(ap, qf);
+    const bool nf = MODE != Q_INT1 && !finite_scale(bp.s);
 #pragma unroll
     for (int r = 0; r < R; ++r) {
       const int c = threadIdx.x + NT * r;
@@ -195,7 +208,8 @@ __global__ __launch_bounds__(NT) void k_quant_rows(const T* __restrict__ x, int6
       for (int k = 0; k < NW; ++k) w[k] = 0u;
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        const uint32_t f = (uint32_t)encode<MODE, BITS>(v[r][e], bp, qf, sP) & MASK;
+        const uint32_t f = (uint32_t)(nf ? encode_nonfinite<MODE, BITS>(v[r][e], bp, qf, sP)
+                                         : encode<MODE, BITS>(v[r][e], bp, qf, sP)) & MASK;
         w[(e * BITS) >> 5] |= f << ((e * BITS) & 31);
       }
       if (idx + 8 > n_store) clear_tail<NW, BITS>(w, n_store - idx);
@@ -218,12 +232,12 @@ __global__ __launch_bounds__(256) void k_block_params(const T* __restrict__ x, i
   const int64_t wave0 = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
   const int64_t nwaves = ((int64_t)gridDim.x * blockDim.x) >> 6;
   for (int64_t blk = wave0; blk < nb; blk += nwaves) {
-    float m = 0.0f;
+    uint32_t m = 0u;
     for (int i = lane; i < block; i += 64) {
       int64_t j = blk * block + i;
-      if (j < n) m = fmaxf(m, __builtin_fabsf(ElemT<T>::cvt(x[j])));
+      if (j < n) m = max(m, mag_bits(ElemT<T>::cvt(x[j])));
     }
-    const float ap = fmaxf(group_max<64>(m), MXK_AMIN);
+    const float ap = amax_clamped(group_max_u<64>(m));
     const BlockParams bp = block_params<MODE>(ap, qf);
     if (lane == 0) {
       scales[blk] = bp.s;
@@ -253,7 +267,8 @@ __global__ __launch_bounds__(256) void k_pack_generic(const T* __restrict__ x, i
       float v = j < n ? ElemT<T>::cvt(x[j]) : 0.0f;
       float2 p = params[j / block];
       BlockParams bp{p.x, p.y};
-      uint32_t code = (uint32_t)encode<MODE, BITS>(v, bp, qf, sP) & mask;
+      const bool nf = MODE != Q_INT1 && !finite_scale(bp.s);
+      uint32_t code = (uint32_t)(nf ? encode_nonfinite<MODE, BITS>(v, bp, qf, sP) : encode<MODE, BITS>(v, bp, qf, sP)) & mask;
       word |= code << (f * bits);
     }
     if (words) reinterpret_cast<uint32_t*>(packed)[u] = word;
@@ -414,14 +429,14 @@ __global__ __launch_bounds__(256) void k_quant_had128(const T* __restrict__ x, i
     // (bits << 1) - 1 orders the nonzero magnitudes and sends both zeros to
     // 0xFFFFFFFF, so its minimum is below 2 * bits(2^-96) - 1 exactly when
     // some lane holds 0 < |v| < 2^-96.
-    float mx = 0.0f;
+    uint32_t mxb = 0u;
     uint32_t mnb = 0xFFFFFFFFu;
 #pragma unroll
     for (int i = 0; i < E; ++i) {
-      mx = fmaxf(mx, __builtin_fabsf(v[i]));
+      mxb = max(mxb, mag_bits(v[i]));
       mnb = min(mnb, (__float_as_uint(v[i]) << 1) - 1u);
     }
-    const float gmx = group_max<LPB>(mx);
+    const float gmx = __uint_as_float(group_max_u<LPB>(mxb));
     float am;
     if (__builtin_expect(__ballot(mnb < 2u * 0x0F800000u - 1u) != 0ull, 0)) {
 #pragma unroll
@@ -435,17 +450,26 @@ __global__ __launch_bounds__(256) void k_quant_had128(const T* __restrict__ x, i
         const float q0 = v[i] * rinv;
         v[i] = __builtin_fmaf(__builtin_fmaf(-q0, rdiv, v[i]), rinv, q0);
       }
-      am = div_rn(gmx, rdiv, rinv);
+      am = finite_scale(gmx) ? div_rn(gmx, rdiv, rinv) : gmx;  // inf / d = inf, NaN / d = NaN
     }
-    const float ap = fmaxf(am, MXK_AMIN);
+    const float ap = amax_clamped(mag_bits(am));
     const BlockParams bp = block_params<MODE>(ap, qf);
+    const bool nf = MODE != Q_INT1 && !finite_scale(bp.s);
     uint32_t w[NW];
 #pragma unroll
     for (int k = 0; k < NW; ++k) w[k] = 0u;
+    if (__builtin_expect(nf, 0)) {
 #pragma unroll
-    for (int i = 0; i < E; ++i) {
-      const uint32_t f = (uint32_t)encode_keyed<MODE, BITS>(v[i], bp, qf, sP, sK) & MASK;
-      w[(i * BITS) >> 5] |= f << ((i * BITS) & 31);
+      for (int i = 0; i < E; ++i) {
+        const uint32_t f = (uint32_t)encode_nonfinite<MODE, BITS>(v[i], bp, qf, sP) & MASK;
+        w[(i * BITS) >> 5] |= f << ((i * BITS) & 31);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < E; ++i) {
+        const uint32_t f = (uint32_t)encode_keyed<MODE, BITS>(v[i], bp, qf, sP, sK) & MASK;
+        w[(i * BITS) >> 5] |= f << ((i * BITS) & 31);
+      }
     }
     if (idx + E > n_store) clear_tail<NW, BITS>(w, n_store - idx);
     if (blk < nb) {

@@ -114,10 +114,11 @@ class mx_linear(nn.Module):
         return cached[1]
 
     def _decode_scales(self, w) -> Optional[Tensor]:
-        """Block-major copy of the weight's scales for the int4 decode kernel,
-        made once per weight tensor and rebuilt when the weight's scales are
-        replaced or modified in place."""
-        if not ops.decode_prepack_eligible(w._mx_dtype, w._mx_block, self.in_features, self.out_features):
+        """Block-major copy of the weight's scales (1/16 of an int4 weight's
+        packed bytes) for the int4 decode and the MFMA kernels, made once per
+        weight tensor and rebuilt when the weight's scales are replaced or
+        modified in place."""
+        if not ops.scales_prepack_eligible(w._mx_dtype, w._mx_block, self.in_features, self.out_features):
             return None
         sc = w._mx_scales
         key = (sc.data_ptr(), str(sc.device), sc._version)
@@ -269,9 +270,10 @@ class mx_dynamic_linear(nn.Module):
 
     def _block_major_scales(self, w) -> Optional[Tensor]:
         """K-block-major copy [in/128, out] of the [out, in] weight's scales,
-        read by both int4 decode kernels (this forward and its input
-        gradient); made once per weight and rebuilt when the scales change."""
-        if not ops.decode_prepack_eligible(w._mx_dtype, w._mx_block, self.out_features, self.in_features):
+        read by the int4 decode kernels and the MFMA kernels (this forward and
+        its input gradient); made once per weight and rebuilt when the scales
+        change."""
+        if not ops.scales_prepack_eligible(w._mx_dtype, w._mx_block, self.out_features, self.in_features):
             return None
         sc = w._mx_scales
         key = (sc.data_ptr(), str(sc.device), sc._version)

@@ -166,33 +166,39 @@ _ZEROED_WS = {}
 # buffers replaced by larger ones: a captured HIP graph keeps the address of
 # the buffer it was captured with, so none is ever freed
 _RETIRED_WS = []
+# data pointers of workspaces whose counter prefix an eager (not captured)
+# fill has cleared; every call leaves the counters zero after that
+_WS_CLEARED = set()
 
 
 def _zeroed_workspace(nbytes: int, device, stream: int) -> Optional[Tensor]:
     """The split-K workspace of `stream` on `device`, at least `nbytes` long.
 
-    A new (or larger) buffer is allocated when needed.  Outside a graph
-    capture it is zero-filled at once; inside one its counter prefix is
-    cleared by a fill kernel that becomes part of the graph, so that every
-    replay starts from zeroed counters whatever ran before.  Calls that
+    A new (or larger) buffer is allocated when needed.  The counter prefix
+    must be zero when a call starts, and every call leaves it zero, so it
+    needs clearing once, outside any capture.  A buffer made inside a graph
+    capture holds whatever its memory held: until an eager call has cleared
+    it, every capture that uses it records a fill kernel of the prefix
+    (no memset node), so that each replay of each such graph starts from
+    zeroed counters, and the first eager call clears it for good.  Calls that
     overlap on one stream cannot happen; graphs captured on the same stream
     share its buffer, so their replays must not overlap either."""
     if nbytes <= 0:
         return None
     key = (str(device), int(stream))
     ws = _ZEROED_WS.get(key)
-    if ws is not None and ws.numel() >= nbytes:
-        return ws
-    size = int(max(nbytes, 2 * ws.numel() if ws is not None else 0))
-    new = torch.empty(size, dtype=torch.uint8, device=device)
-    if torch.cuda.is_current_stream_capturing():
-        new[:min(size, COUNTER_BYTES)].zero_()
-    else:
-        new.zero_()
-    if ws is not None:
-        _RETIRED_WS.append(ws)
-    _ZEROED_WS[key] = new
-    return new
+    capturing = torch.cuda.is_current_stream_capturing()
+    if ws is None or ws.numel() < nbytes:
+        size = int(max(nbytes, 2 * ws.numel() if ws is not None else 0))
+        new = torch.empty(size, dtype=torch.uint8, device=device)
+        if ws is not None:
+            _RETIRED_WS.append(ws)
+        _ZEROED_WS[key] = ws = new
+    if ws.data_ptr() not in _WS_CLEARED:
+        ws[:min(ws.numel(), COUNTER_BYTES)].zero_()
+        if not capturing:
+            _WS_CLEARED.add(ws.data_ptr())
+    return ws
 
 
 def quantize(x: Tensor, dt, block: int = 128, *, seed: Optional[int] = None,
@@ -327,6 +333,15 @@ def decode_prepack_eligible(dt, block: int, in_features: int, out_features: int)
     dt = get_mx_dtype(dt)
     return (not dt.is_float and dt.bits == 4 and not dt.is_hadamard and not dt.is_vector and block == 128
             and out_features % 128 == 0 and in_features % 32 == 0)
+
+
+def scales_prepack_eligible(dt, block: int, in_features: int, out_features: int) -> bool:
+    """Whether linear_wq's kernels read block-major scales for this weight:
+    the int4 decode kernels and the MFMA kernels (int4 and int8 base codes,
+    block 128, whole 128-column blocks)."""
+    dt = get_mx_dtype(dt)
+    return (not dt.is_float and dt.bits in (4, 8) and not dt.is_hadamard and not dt.is_vector and block == 128
+            and out_features % 128 == 0)
 
 
 def prepack_scales(w_scales: Tensor, in_features: int, out_features: int, block: int = 128) -> Tensor:

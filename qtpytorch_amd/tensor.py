@@ -30,6 +30,26 @@ from .dtypes import get_mx_dtype, matmul_output_dtype, mx_dtype, qmul_output_dty
 Tensor = torch.Tensor
 
 
+def _as_mx_dtype(v) -> Optional[mx_dtype]:
+    """The MX dtype v names (an mx_dtype or a registered name), else None."""
+    if isinstance(v, mx_dtype):
+        return v
+    if isinstance(v, str) and _is_mx_name(v):
+        return get_mx_dtype(v)
+    return None
+
+
+def _names_device(v) -> bool:
+    if isinstance(v, (torch.device, int)) and not isinstance(v, bool):
+        return True
+    return isinstance(v, str) and (v in ("cpu", "cuda") or v.startswith(("cuda:", "cpu:")))
+
+
+def _as_device(v) -> torch.device:
+    """torch.device of a device spec; a bare index is a CUDA ordinal."""
+    return torch.device("cuda", v) if isinstance(v, int) else torch.device(v)
+
+
 class mx_tensor(torch.Tensor):
     """A quantized tensor that is a torch.Tensor (mxtorch.py:6028)."""
 
@@ -203,64 +223,58 @@ class mx_tensor(torch.Tensor):
     def bfloat16(self):
         return self.dequantize().bfloat16()
 
-    # ---- moves and re-quantization (mxtorch.py:6215-6307) ----
+    # ---- moves, re-quantization and shape (mxtorch.py:6215-6331) ----
+    # The accepted forms follow torch.Tensor.to: an MX dtype (name or
+    # mx_dtype) re-quantizes, a device (torch.device, "cpu", "cuda[:i]" or a
+    # bare index) moves the packed storage, dtype= with an MX dtype moves
+    # (device=) then re-quantizes, anything else dequantizes and hands the
+    # arguments to the float tensor's .to.
     def to(self, *args, **kwargs):
-        kw_device = kwargs.get("device", None)
-        kw_dtype = kwargs.get("dtype", None)
-        target = args[0] if args else None
-
-        def _is_device(v):
-            if isinstance(v, torch.device) or isinstance(v, int):
-                return True
-            if isinstance(v, str):
-                return v in ("cpu", "cuda") or v.startswith("cuda:") or v.startswith("cpu:")
-            return False
-
-        def _to_dev(v):
-            return torch.device("cuda", v) if isinstance(v, int) else torch.device(v)
-
-        if isinstance(target, mx_dtype) or (isinstance(target, str) and _is_mx_name(target)):
-            return mx_tensor.quantize(self.dequantize(), get_mx_dtype(target), self._mx_block)
-        if isinstance(kw_dtype, mx_dtype) or (isinstance(kw_dtype, str) and _is_mx_name(kw_dtype)):
-            base = self._move_device(_to_dev(kw_device)) if kw_device is not None else self
-            return mx_tensor.quantize(base.dequantize(), get_mx_dtype(kw_dtype), self._mx_block)
-        dev = kw_device if kw_device is not None else (target if _is_device(target) else None)
-        if dev is not None:
-            return self._move_device(_to_dev(dev))
+        first = args[0] if args else None
+        device, dtype = kwargs.get("device"), kwargs.get("dtype")
+        for want in (first, dtype):
+            mx = _as_mx_dtype(want)
+            if mx is not None:
+                src = self if want is first or device is None else self._move_device(_as_device(device))
+                return mx_tensor.quantize(src.dequantize(), mx, self._mx_block)
+        if device is None and _names_device(first):
+            device = first
+        if device is not None:
+            return self._move_device(_as_device(device))
         return self.dequantize().to(*args, **kwargs)
 
+    def _derived(self, packed: Tensor, scales: Tensor, shape=None) -> "mx_tensor":
+        """Same dtype, element count, block and rotation seed over other storage (or shape)."""
+        return mx_tensor(packed, scales, self._mx_dtype, self._mx_orig_shape if shape is None else shape,
+                         self._mx_n, self._mx_block, seed=self._mx_seed)
+
     def _move_device(self, device: torch.device) -> "mx_tensor":
-        return mx_tensor(self._mx_packed.to(device), self._mx_scales.to(device), self._mx_dtype,
-                         self._mx_orig_shape, self._mx_n, self._mx_block, seed=self._mx_seed)
+        return self._derived(self._mx_packed.to(device), self._mx_scales.to(device))
 
     def cuda(self, device=None):
+        """.cuda() / .cuda(i) / .cuda("cuda:i") / .cuda("i"); other strings mean device 0."""
         if device is None:
             return self._move_device(torch.device("cuda"))
-        if isinstance(device, int):
-            return self._move_device(torch.device("cuda", device))
-        if isinstance(device, str) and ":" in device:
-            return self._move_device(torch.device(device))
-        return self._move_device(torch.device("cuda", int(device) if str(device).isdigit() else 0))
+        if isinstance(device, (int, torch.device)) or (isinstance(device, str) and ":" in device):
+            return self._move_device(_as_device(device))
+        text = str(device)
+        return self._move_device(torch.device("cuda", int(text) if text.isdigit() else 0))
 
     def cpu(self):
         return self._move_device(torch.device("cpu"))
 
     def clone(self):
-        return mx_tensor(self._mx_packed.clone(), self._mx_scales.clone(), self._mx_dtype, self._mx_orig_shape,
-                         self._mx_n, self._mx_block, seed=self._mx_seed)
+        return self._derived(self._mx_packed.clone(), self._mx_scales.clone())
 
     def detach(self):
-        return mx_tensor(self._mx_packed.detach(), self._mx_scales.detach(), self._mx_dtype,
-                         self._mx_orig_shape, self._mx_n, self._mx_block, seed=self._mx_seed)
+        return self._derived(self._mx_packed.detach(), self._mx_scales.detach())
 
     def reshape(self, *shape):
-        if len(shape) == 1 and isinstance(shape[0], (tuple, list, torch.Size)):
-            shape = tuple(shape[0])
-        known = math.prod(s for s in shape if s != -1)
-        shape = tuple(self._mx_n // known if s == -1 else s for s in shape)
-        t = self.clone()
-        t._mx_orig_shape = torch.Size(shape)
-        return t
+        """A copy with another logical shape over the same flat blocks (one -1 is inferred)."""
+        dims = tuple(shape[0]) if len(shape) == 1 and isinstance(shape[0], (tuple, list, torch.Size)) else shape
+        fixed = math.prod(d for d in dims if d != -1)
+        dims = tuple(self._mx_n // fixed if d == -1 else d for d in dims)
+        return self._derived(self._mx_packed.clone(), self._mx_scales.clone(), torch.Size(dims))
 
     def view(self, *shape):
         return self.reshape(*shape)
@@ -361,7 +375,13 @@ def _dispatch_qelementwise(op: str, a: "mx_tensor", b: "mx_tensor") -> "mx_tenso
     out_dt = qmul_output_dtype(a._mx_dtype) if op == "mul" else resolve_mixed(a._mx_dtype, b._mx_dtype)
     packed, scales = ops.qelementwise(op, a._mx_packed, a._mx_scales, b._mx_packed, b._mx_scales, a._mx_n,
                                       a._mx_block, bits, out_dt.bits)
-    return mx_tensor(packed, scales, out_dt, a._mx_orig_shape, a._mx_n, a._mx_block)
+    # codes of 'h' operands live in their rotated domain: the result keeps
+    # the operands' Hadamard seed (callers route operands of different seeds
+    # through dequantize / requantize instead)
+    seed = None
+    if out_dt.is_hadamard:
+        seed = a._mx_seed if a._mx_seed is not None else b._mx_seed
+    return mx_tensor(packed, scales, out_dt, a._mx_orig_shape, a._mx_n, a._mx_block, seed=seed)
 
 
 def _binary_op(a, b, fn):
@@ -371,7 +391,8 @@ def _binary_op(a, b, fn):
     taken); otherwise dequantize, apply fn, requantize (two mx_tensors: with
     _resolve_mixed of their dtypes; one: with its dtype)."""
     if isinstance(a, mx_tensor) and isinstance(b, mx_tensor):
-        if a._mx_orig_shape == b._mx_orig_shape and a._mx_block == b._mx_block:
+        same_rotation = not (a._mx_dtype.is_hadamard and b._mx_dtype.is_hadamard and a._mx_seed != b._mx_seed)
+        if a._mx_orig_shape == b._mx_orig_shape and a._mx_block == b._mx_block and same_rotation:
             name = getattr(fn, "__name__", "") or str(fn)
             if "add" in name or fn is torch.add:
                 return _dispatch_qelementwise("add", a, b)

@@ -51,6 +51,19 @@ def cases(kind):
     return [c for c in index()["cases"] if c["kind"] == kind]
 
 
+def nan_aware_equal(a: torch.Tensor, b: torch.Tensor) -> bool:
+    """Bitwise equality of float32 tensors where every NaN matches any NaN
+    (a NaN's payload and sign depend on the hardware that made it)."""
+    a = a.contiguous().reshape(-1)
+    b = b.contiguous().reshape(-1)
+    if a.shape != b.shape or a.dtype != b.dtype:
+        return False
+    na, nb = torch.isnan(a), torch.isnan(b)
+    if not torch.equal(na, nb):
+        return False
+    return torch.equal(a[~na].view(torch.int32), b[~nb].view(torch.int32))
+
+
 def bits_equal(a: torch.Tensor, b: torch.Tensor) -> bool:
     """Bitwise equality (tells -0.0 from 0.0)."""
     a = a.contiguous()

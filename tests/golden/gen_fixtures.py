@@ -23,7 +23,8 @@ Vectors written (all through the reference's public entry points):
   * ``_QGemmSTE.apply`` forward output;
   * ``mx_linear.from_linear(...)(x)`` with and without bias;
   * ``kv_cache_quantizer`` append/get with asymmetric V;
-  * the int4dh hash seed under PYTHONHASHSEED=0.
+  * the int4dh hash seed under PYTHONHASHSEED=0;
+  * quantize of blocks holding NaN and infinities (NaN / infinite scales).
 """
 from __future__ import annotations
 
@@ -114,6 +115,27 @@ def _child(ref_dir: str) -> None:
         put(f"in/{iname}", xin)
         index["cases"].append({"kind": "input", "key": f"in/{iname}", "dtype": str(xin.dtype),
                                "shape": list(xin.shape), "seed": seed})
+
+    # non-finite blocks: torch's amax propagates NaN, so a block holding a
+    # NaN gets a NaN scale; an infinity gives an infinite scale (its codes
+    # come from NaN and zero quotients)
+    nf = torch.randn(5, 128, generator=gen(140))
+    nf[1, 2] = float("nan")
+    nf[2, 44] = float("inf")
+    nf[3, 16] = float("nan")
+    nf[3, 17] = float("-inf")
+    nf[4, 100] = float("-inf")
+    put("in/nonfinite_5x128", nf)
+    for dname in ("int8d", "int4d", "int2d", "int1d", "float4d", "float8d", "int8dv", "int4dh"):
+        dt = mx.get_mx_dtype(dname)
+        q = mx.mx_tensor.quantize(nf, dt, 128)
+        key = f"qnf/nonfinite_5x128/{dname}/128"
+        put(key + "/packed", q._mx_packed)
+        put(key + "/scales", q._mx_scales)
+        put(key + "/dequant", q.dequantize())
+        index["cases"].append({"kind": "quantize_nonfinite", "key": key, "input": "nonfinite_5x128",
+                               "dtype": dname, "block": 128, "n": int(q._mx_n), "shape": [5, 128],
+                               "seed": 140, "packed_dtype": str(q._mx_packed.dtype)})
 
     # int4dh: the seed is hash(name) % 2**31, fixed here by PYTHONHASHSEED
     index["hash_seed"]["int4dh"] = hash("int4dh") % (2 ** 31)

@@ -162,3 +162,32 @@ def test_elementwise_on_gemm_outputs(qa, mkn, name):
         assert r._mx_dtype.name == o_ref, op
         assert _bits_eq(r._mx_packed, p_ref), op
         assert _bits_eq(r._mx_scales, s_ref), op
+
+
+def test_hadamard_add_keeps_seed(qa):
+    """add / sub of two 'h' tensors quantized with a non-default seed stay
+    in the code domain and keep that seed, so the result dequantizes with the
+    rotation its codes were made in; operands of different seeds go through
+    dequantize -> add -> requantize."""
+    dev = torch.device("cuda:0")
+    g = torch.Generator()
+    g.manual_seed(91)
+    x = torch.randn(64, 128, generator=g)
+    y = torch.randn(64, 128, generator=g) * 0.5
+    dt = qa.get_mx_dtype("int4dh")
+    a = qa.mx_tensor.quantize(x.to(dev), dt, 128, seed=777)
+    b = qa.mx_tensor.quantize(y.to(dev), dt, 128, seed=777)
+    for op, ref in (("add", x + y), ("sub", x - y)):
+        c = a + b if op == "add" else a - b
+        assert c._mx_seed == 777
+        err = (c.dequantize().cpu() - ref).abs().max().item()
+        assert err < 0.35 * ref.abs().max().item(), f"{op}: {err}"
+        # the same codes read with the default seed are another rotation's
+        wrong = qa.mx_tensor(c._mx_packed, c._mx_scales, dt, c._mx_orig_shape, c._mx_n, 128)
+        assert wrong._mx_seed != 777
+        err_wrong = (wrong.dequantize().cpu() - ref).abs().max().item()
+        assert err_wrong > 2 * err, f"{op}: {err_wrong} vs {err}"
+    b2 = qa.mx_tensor.quantize(y.to(dev), dt, 128, seed=778)
+    c2 = a + b2
+    err2 = (c2.dequantize().cpu() - (x + y)).abs().max().item()
+    assert err2 < 0.35 * (x + y).abs().max().item()

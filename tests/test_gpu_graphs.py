@@ -130,3 +130,42 @@ def test_graph_gemm_and_kv_append(qa):
     # the ring is full: every append evicts the oldest step, and the newest
     # step is the last one get() returns
     _replays(lambda: step(k1, v1)[0][:, :, -1:], lambda: step(k2, v2)[0][:, :, -1:])
+
+
+def test_two_graphs_one_stream_second_replayed_first(qa):
+    """Two decode-linear graphs captured one after the other on one new
+    stream share its split-K workspace, which the first capture creates in
+    graph memory.  Replaying the second graph first (and eager calls on that
+    stream before any replay of the first) must still see zeroed arrival
+    counters: every capture records the counter clear until an eager call
+    has made it."""
+    dev = torch.device("cuda:0")
+    lin = torch.nn.Linear(8192, 2048, bias=False)
+    with torch.no_grad():
+        lin.weight.copy_(_x((2048, 8192), 21, 0.02))
+    m = qa.mx_linear.from_linear(lin.to(dev), qa.get_mx_dtype("int4d"), 128)
+    x1, x2 = _x((16, 8192), 22).to(dev), _x((8, 8192), 23).to(dev)
+    ref1, ref2 = m(x1).clone(), m(x2).clone()   # eager, on the default stream
+    torch.cuda.synchronize()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    g1, g2 = torch.cuda.CUDAGraph(), torch.cuda.CUDAGraph()
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(g1, stream=s):
+            o1 = m(x1)
+        with torch.cuda.graph(g2, stream=s):
+            o2 = m(x2)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    for rep in range(3):
+        g2.replay()
+        torch.cuda.synchronize()
+        assert _same(o2, ref2), f"second graph, replay {rep}"
+        with torch.cuda.stream(s):
+            e2 = m(x2)   # eager on the capture stream
+        torch.cuda.synchronize()
+        assert _same(e2, ref2), f"eager call on the capture stream, round {rep}"
+        g1.replay()
+        torch.cuda.synchronize()
+        assert _same(o1, ref1), f"first graph, replay {rep}"
+    del g1, g2

@@ -55,6 +55,62 @@ def test_quantize_golden(qa, case):
     assert _bits_eq(dq.reshape(case["shape"]), G.get(case["key"] + "/dequant")), "dequantized values differ"
 
 
+NFCASES = G.cases("quantize_nonfinite")
+
+
+@pytest.mark.parametrize("case", NFCASES, ids=[c["key"] for c in NFCASES])
+def test_quantize_nonfinite_golden(qa, case):
+    """Blocks holding NaN or +-inf, against the reference-written codes and
+    scales (bitwise: NaN scales 0x7FC00000, infinite scales +inf, codes of
+    NaN quotients 0, float codes of NaN the last index); dequantized values
+    with any NaN for a NaN."""
+    x = G.input_tensor(case["input"]).to(dev())
+    dt = qa.get_mx_dtype(case["dtype"])
+    seed = G.index()["hash_seed"].get(case["dtype"]) if dt.is_hadamard else None
+    packed, scales, n = qa.ops.quantize(x, dt, case["block"], seed=seed)
+    assert _bits_eq(packed, G.get(case["key"] + "/packed")), "packed codes differ"
+    assert _bits_eq(scales, G.get(case["key"] + "/scales")), "scales differ"
+    dq = qa.ops._dequant(packed, scales, dt, n, case["block"], orig_shape=tuple(case["shape"]), seed=seed,
+                         hadamard_mode="reference")
+    assert G.nan_aware_equal(dq.reshape(case["shape"]).cpu(), G.get(case["key"] + "/dequant"))
+
+
+@pytest.mark.parametrize("name", ["int8d", "int4d", "int2d", "int1d", "float4d", "float8d", "int8dv", "int4dh",
+                                  "float8dh"])
+@pytest.mark.parametrize("src", ["f32", "f16", "long", "generic"])
+def test_quantize_nonfinite_kernels(qa, name, src):
+    """NaN and +-inf through every quantize kernel (the fused kernel from
+    fp32 and from fp16, the one-workgroup-per-block kernel for blocks above
+    512, the generic two-pass kernel for other block sizes) against the
+    oracle, which restates the reference's torch ops: codes and scales
+    bitwise."""
+    dt = qa.get_mx_dtype(name)
+    if dt.is_hadamard and src in ("long", "generic"):
+        pytest.skip("'h' rotates rows of the last dimension; covered at 128")
+    block = {"long": 1024, "generic": 96}.get(src, 128)
+    g = torch.Generator()
+    g.manual_seed(77)
+    x = torch.randn(24, 1024, generator=g)
+    flat = x.view(-1)
+    flat[5] = float("nan")
+    flat[1500] = float("inf")
+    flat[3000] = float("-inf")
+    flat[3001] = float("nan")
+    flat[9000] = float("inf")
+    flat[9001] = float("-inf")
+    flat[20000] = float("-nan")
+    if src == "f16":
+        x = x.half()
+    if dt.is_hadamard:
+        x = x.reshape(-1, 128)
+    seed = 1534857261 if dt.is_hadamard else None
+    packed, scales, n = qa.ops.quantize(x.to(dev()), dt, block, seed=seed)
+    rp, rs, rn = orc.quantize(x, name, block, seed=seed) if seed is not None else orc.quantize(x, name, block)
+    assert n == rn
+    assert _bits_eq(packed, rp), "packed codes differ"
+    assert _bits_eq(scales, rs), "scales differ"
+
+
 MCASES = G.cases("matmul")
 
 

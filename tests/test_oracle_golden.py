@@ -30,6 +30,26 @@ def test_quantize_matches_reference(case):
     assert G.bits_equal(dq.reshape(case["shape"]), G.get(case["key"] + "/dequant"))
 
 
+NFCASES = G.cases("quantize_nonfinite")
+
+
+@pytest.mark.parametrize("case", NFCASES, ids=[c["key"] for c in NFCASES])
+def test_quantize_nonfinite_matches_reference(case):
+    """Blocks holding NaN or +-inf (mxtorch.py:1456-1460, 1497-1524): the
+    reference's amax gives NaN or inf scales, and its codes come from NaN
+    and zero quotients.  Codes and scales bitwise (the reference's NaN
+    scales are 0x7FC00000); dequantized values with any NaN for a NaN."""
+    x = G.input_tensor(case["input"])
+    seed = G.index()["hash_seed"][case["dtype"]] if case["dtype"].endswith("h") else None
+    packed, scales, n = orc.quantize(x, case["dtype"], case["block"], seed=seed)
+    assert G.bits_equal(packed, G.get(case["key"] + "/packed"))
+    assert G.bits_equal(scales, G.get(case["key"] + "/scales"))
+    assert torch.isnan(scales).any() and torch.isinf(scales).any()
+    dq = orc.dequant(packed, scales, case["dtype"], n, case["block"], seed=seed,
+                     orig_shape=tuple(case["shape"]), hadamard_mode="reference")
+    assert G.nan_aware_equal(dq.reshape(case["shape"]), G.get(case["key"] + "/dequant"))
+
+
 MCASES = G.cases("matmul")
 
 
