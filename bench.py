@@ -246,11 +246,13 @@ def bench_gemm(qa, M, K, N, reps, dtype="int8d"):
     # the median of 5 replays: back-to-back 8192^3 GEMMs move the clock by +-10% from launch to launch
     t_c = graph_time(lambda: qa.ops.qscale_gemm(pa, sa, pb, sb, M, K, N, bits, 128, 16, want_packed=False,
                                                   want_c=True), reps, 1, repeats=5)
-    t_p = graph_time(lambda: qa.ops.qscale_gemm(pa, sa, pb, sb, M, K, N, bits, 128, 16), reps, 1, repeats=5)
+    # the packed output of qa @ qb: int16d for int8 operands, int8d for int4 (mxtorch.py:1393-1418)
+    ob = qa.matmul_output_dtype(dt, dt).bits
+    t_p = graph_time(lambda: qa.ops.qscale_gemm(pa, sa, pb, sb, M, K, N, bits, 128, ob), reps, 1, repeats=5)
     ops = 2.0 * M * K * N
     return {"shape": [M, K, N], "fp32_out_us": round(t_c * 1e6, 2), "fp32_out_TOPS": round(ops / t_c / 1e12, 2),
             "fp32_out_frac_int8_peak": round(ops / t_c / 1e12 / INT8_PEAK_TOPS, 4),
-            "packed_int16d_out_us": round(t_p * 1e6, 2), "packed_TOPS": round(ops / t_p / 1e12, 2)}
+            f"packed_int{ob}d_out_us": round(t_p * 1e6, 2), "packed_TOPS": round(ops / t_p / 1e12, 2)}
 
 
 def bench_config1_full(qa, reps):

@@ -36,7 +36,7 @@
 extern "C" {
 #endif
 
-#define MXK_ABI_VERSION 6
+#define MXK_ABI_VERSION 7
 
 typedef enum {
   MXK_OK = 0,
@@ -116,9 +116,16 @@ int mxk_dequantize(const void* packed, int64_t packed_nbytes, const float* scale
 /* Workspace bytes mxk_dequantize needs (0 if none). */
 size_t mxk_dequantize_workspace(int64_t n, int variant, int64_t rot_dim);
 
-/* Workspace bytes mxk_qgemm needs; out_bits = 0 when no packed output is
- * requested. */
+/* Workspace bytes mxk_qgemm needs for packed operands that start on 16
+ * bytes; out_bits = 0 when no packed output is requested.  With block 128,
+ * K % 128 == 0 and N a multiple of 128, int8 x int8 -> 16-bit and int4 x int4
+ * -> 8-bit packed outputs are requantized in the GEMM's epilogue and need no
+ * M*N float32 buffer. */
 size_t mxk_qgemm_workspace(int64_t M, int64_t K, int64_t N, int bits, int block, int out_bits);
+
+/* Workspace bytes mxk_qgemm needs for packed operands at any alignment
+ * (those not on 16 bytes are unpacked into the workspace first). */
+size_t mxk_qgemm_workspace_any(int64_t M, int64_t K, int64_t N, int bits, int block, int out_bits);
 
 /* Packed block-scaled GEMM: the CPU branch of _dispatch_qgemm
  * (mxtorch.py:5563-5573) around _qscale_matmul (mxtorch.py:1299-1385).
@@ -152,7 +159,11 @@ int mxk_qgemm(const void* a_packed, const float* a_scales, int64_t a_nscales, co
  * sums, then room for block-major scales when w_scales_t is NULL) must be
  * zero-filled before first use, and every call, of any shape, leaves the
  * counter prefix ready for the next one.  Calls sharing a workspace must
- * not overlap.  The size also covers mxk_linear_wq_tiled. */
+ * not overlap.  The size also covers mxk_linear_wq_tiled and the MFMA path
+ * (int4 / int8 weights, block 128, N % 128 == 0, any M): its row exponents,
+ * x scaled by them (M * roundup(K, 256) floats), a block-major copy of the
+ * scales when w_scales_t is NULL and any K-split partials, all after the
+ * counter prefix, which it leaves alone. */
 size_t mxk_linear_workspace(int64_t M, int64_t K, int64_t N, int bits, int block);
 
 /* Block-major copy of a weight's scales for the decode path: w_scales_t[b][k]
@@ -290,7 +301,10 @@ int mxk_linear_wq_nt(const void* x, int x_type, int64_t M, int64_t K, const void
  * workgroups of 1024 rows of K; its workspace (a 64 KiB prefix of arrival
  * counters, then the partial sums) must be zero-filled before first use,
  * and every call leaves the counters zero again.  Calls sharing a workspace
- * must not overlap. */
+ * must not overlap.  The size also covers the MFMA path (int4 / int8 codes,
+ * block 128, K and N multiples of 128, any M): row exponents, x as f16 hi +
+ * lo (M * roundup(K, 256) * 4 bytes) and any K-split partials after the
+ * counter prefix. */
 size_t mxk_linear_nt_workspace(int64_t M, int64_t K, int64_t N, int bits, int block);
 
 /* Tiled copy of an int4 [N][K] weight for mxk_linear_wq_nt_tiled: w_packed

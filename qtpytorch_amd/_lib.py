@@ -20,7 +20,7 @@ MXK_IN_F32, MXK_IN_F16, MXK_IN_BF16 = 0, 1, 2
 MXK_KIND_INT, MXK_KIND_FLOAT = 0, 1
 MXK_VAR_BASE, MXK_VAR_HADAMARD, MXK_VAR_VECTOR = 0, 1, 2
 MXK_DYN_PER_TOKEN, MXK_DYN_PER_CHANNEL, MXK_DYN_PER_TENSOR = 0, 1, 2
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 _lock = threading.Lock()
 _lib = None
@@ -43,6 +43,7 @@ SIGNATURES = {
                                c_vp, c_vp, c_sz, c_vp]),
     "mxk_dequantize_workspace": (c_sz, [c_i64, c_int, c_i64]),
     "mxk_qgemm_workspace": (c_sz, [c_i64, c_i64, c_i64, c_int, c_int, c_int]),
+    "mxk_qgemm_workspace_any": (c_sz, [c_i64, c_i64, c_i64, c_int, c_int, c_int]),
     "mxk_qgemm": (c_int, [c_vp, c_vp, c_i64, c_vp, c_vp, c_i64, c_i64, c_i64, c_i64, c_int, c_int, c_int,
                           c_vp, c_i64, c_vp, c_vp, c_vp, c_vp, c_sz, c_vp]),
     "mxk_linear_workspace": (c_sz, [c_i64, c_i64, c_i64, c_int, c_int]),

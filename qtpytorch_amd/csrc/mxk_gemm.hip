@@ -470,12 +470,22 @@ __device__ __forceinline__ u32x4 qg3_unpack16(uint32_t w0, uint32_t w1) {
 //      RN(float(P) * SA * 2^-8) = RN(P/256 * SA) when SA * 2^-8 is exact; with
 //      EXACT (some scale is too small for that) sa_t holds SA and P is
 //      scaled by 2^-8 first (exact: an integer below 2^24).
-template <int MODE, bool WRITE_ACC, bool WRITE_C, bool ROWSCALE, bool EXACT>
+//
+// REQ (16 or 8): the requantization of C to REQ-bit codes by the 'v' rule
+// (mxtorch.py:1372-1385) runs in the epilogue, for N a multiple of 128:
+// every 128-element block of the flat C is then one row of a tile, whose
+// two 64-column halves belong to waves (wm, 0) and (wm, 1).  The row's
+// maximum meets in LDS, s = RN(max(a, 1e-12) / q) and the codes
+// rne(clamp(RN(C / s))) use the same functions as the two-pass kernel
+// (requant_vec_f32), and the codes go out through an LDS tile as whole
+// packed rows.  No fp32 C reaches memory unless WRITE_C asks for it.
+template <int MODE, bool WRITE_ACC, bool WRITE_C, bool ROWSCALE, bool EXACT, int REQ = 0>
 __device__ __forceinline__ void qg3_run(int8_t* lds, const int8_t* __restrict__ A8, int64_t lda, int64_t Arows,
                                         const int8_t* __restrict__ B8, int64_t ldb, int64_t Brows,
                                         const float* __restrict__ sa_t, const float* __restrict__ sb_src, int64_t M,
                                         int64_t N, int KB, float* __restrict__ C, int32_t* __restrict__ acc_out,
-                                        int grouped, const float* __restrict__ bias) {
+                                        int grouped, const float* __restrict__ bias, uint8_t* __restrict__ cq = nullptr,
+                                        float* __restrict__ cq_scales = nullptr) {
   static_assert(MODE == 0 || !ROWSCALE, "row scales are a mode-0 epilogue");
   // [A stages 0..2, 32 KiB each][B stages 0..2, 16 KiB each][scale stages 0..2, 2 KiB each]:
   // a stage's scales hold SA rows at floats 0..255 and SB columns at 256..383
@@ -887,6 +897,51 @@ __device__ __forceinline__ void qg3_run(int8_t* lds, const int8_t* __restrict__ 
         }
       }
   }
+  if constexpr (REQ > 0) {
+    constexpr int RB = 128 * REQ / 8;  // bytes of one packed row of the tile
+    static_assert(2048 + 256 * RB <= QG3_LDS_BYTES, "requant tile");
+    __syncthreads();  // every wave is done with the stage buffers
+    uint32_t* smax = reinterpret_cast<uint32_t*>(lds);  // [wn][256 rows] maxima (magnitude bits)
+    uint8_t* tile = reinterpret_cast<uint8_t*>(lds) + 2048;
+#pragma unroll
+    for (int a = 0; a < 4; ++a)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        uint32_t m = 0u;
+#pragma unroll
+        for (int b = 0; b < 4; ++b) m = max(m, mag_bits(c[a][b][i]));
+        m = group_max_u<16>(m);  // the 16 lanes of lane group lg hold the wave's 64 columns of the row
+        if (lr == 0) smax[wn * 256 + wm * 64 + a * 16 + lg * 4 + i] = m;
+      }
+    __syncthreads();
+    constexpr float qf = (float)((1 << (REQ - 1)) - 1);
+#pragma unroll
+    for (int a = 0; a < 4; ++a)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int rl = wm * 64 + a * 16 + lg * 4 + i;
+        const BlockParams bp = block_params<Q_VEC>(amax_clamped(max(smax[rl], smax[256 + rl])), qf);
+        const bool nf = !finite_scale(bp.s);
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+          const int cl = wn * 64 + b * 16 + lcol;
+          const int code = nf ? encode_nonfinite<Q_VEC, REQ>(c[a][b][i], bp, qf, nullptr)
+                              : encode<Q_VEC, REQ>(c[a][b][i], bp, qf, nullptr);
+          if constexpr (REQ == 16) reinterpret_cast<int16_t*>(tile + rl * RB)[cl] = (int16_t)code;
+          else tile[rl * RB + cl] = (uint8_t)code;
+        }
+        const int64_t row = m0 + rl;
+        if (wn == 0 && lr == 0 && row < M) cq_scales[row * (N / 128) + n0 / 128] = bp.s;
+      }
+    __syncthreads();
+    for (int idx = tid; idx < 256 * RB / 16; idx += 512) {
+      const int rl = idx / (RB / 16), ch = idx % (RB / 16);
+      const int64_t row = m0 + rl;
+      if (row < M)
+        *reinterpret_cast<u32x4*>(cq + (row * N + n0) * REQ / 8 + ch * 16) =
+            *reinterpret_cast<const u32x4*>(tile + rl * RB + ch * 16);
+    }
+  }
 }
 
 template <bool WRITE_ACC, bool WRITE_C, bool ROWSCALE = false>
@@ -905,20 +960,21 @@ __global__ __launch_bounds__(512, 1) void k_qgemm_i8_v3(const int8_t* __restrict
 // [K][N]) or mode 2 (int4; A [M][K/2], B [K][N/2]), see qg3_run.  Mode 2
 // reads `exact` (written by k_prep_sa4) once: 0 takes sa_s = SA * 2^-8, 1
 // the exact epilogue on sa_u = SA.
-template <int MODE, bool WRITE_ACC, bool WRITE_C>
+template <int MODE, bool WRITE_ACC, bool WRITE_C, int REQ = 0>
 __global__ __launch_bounds__(512, 1) void k_qgemm_kn(const int8_t* __restrict__ A, int64_t lda, int64_t Arows,
                                                      const int8_t* __restrict__ B, int64_t ldb, int64_t Brows,
                                                      const float* __restrict__ sa_s, const float* __restrict__ sa_u,
                                                      const int* __restrict__ exact, const float* __restrict__ sb_src,
                                                      int64_t M, int64_t N, int KB, float* __restrict__ C,
-                                                     int32_t* __restrict__ acc_out, int grouped) {
+                                                     int32_t* __restrict__ acc_out, int grouped,
+                                                     uint8_t* __restrict__ cq, float* __restrict__ cq_scales) {
   __shared__ __attribute__((aligned(1024))) int8_t lds[QG3_LDS_BYTES];
   if (MODE == 2 && __builtin_amdgcn_readfirstlane(*exact) != 0)
-    qg3_run<MODE, WRITE_ACC, WRITE_C, false, true>(lds, A, lda, Arows, B, ldb, Brows, sa_u, sb_src, M, N, KB, C,
-                                                   acc_out, grouped, nullptr);
+    qg3_run<MODE, WRITE_ACC, WRITE_C, false, true, REQ>(lds, A, lda, Arows, B, ldb, Brows, sa_u, sb_src, M, N, KB, C,
+                                                        acc_out, grouped, nullptr, cq, cq_scales);
   else
-    qg3_run<MODE, WRITE_ACC, WRITE_C, false, false>(lds, A, lda, Arows, B, ldb, Brows, sa_s, sb_src, M, N, KB, C,
-                                                    acc_out, grouped, nullptr);
+    qg3_run<MODE, WRITE_ACC, WRITE_C, false, false, REQ>(lds, A, lda, Arows, B, ldb, Brows, sa_s, sb_src, M, N, KB,
+                                                         C, acc_out, grouped, nullptr, cq, cq_scales);
 }
 
 __global__ __launch_bounds__(256) void k_fill_ones(float* __restrict__ p, int64_t n) {
@@ -994,6 +1050,7 @@ struct GemmPlan {
   int64_t KBP, Mpad, Npad;
   bool direct_a, v2, v3;
   int kn;  // 1: int8 with B read as stored, 2: int4 A and B read as stored (k_qgemm_kn), 0: unpacking pre-pass
+  int req;  // output width requantized in the GEMM's epilogue (kn, N % 128 == 0), 0: a second pass
   size_t a_bytes, b_bytes, c_bytes, q_bytes, sa_bytes, sb_bytes, su_bytes;
 };
 
@@ -1020,7 +1077,13 @@ static GemmPlan plan_gemm(int64_t M, int64_t K, int64_t N, int bits, int block, 
     if (bits == 8 && N % 16 == 0 && M * K < lim && K * N < lim) p.kn = 1;
     if (bits == 4 && N % 32 == 0 && M * K / 2 < lim && K * N / 2 < lim) p.kn = 2;
   }
+  p.req = 0;
   if (p.kn) {
+    // int8 x int8 -> int16d and int4 x int4 -> int8d codes straight from the epilogue
+    if (out_bits > 0 && N % 128 == 0 && out_bits == (p.kn == 1 ? 16 : 8)) {
+      p.req = out_bits;
+      p.c_bytes = p.q_bytes = 0;
+    }
     p.direct_a = true;
     p.v2 = p.v3 = true;
     p.a_bytes = p.b_bytes = 0;
@@ -1084,10 +1147,20 @@ using namespace mxk;
 
 extern "C" {
 
-size_t mxk_qgemm_workspace(int64_t M, int64_t K, int64_t N, int bits, int block, int out_bits) {
+static size_t qgemm_workspace(int64_t M, int64_t K, int64_t N, int bits, int block, int out_bits, bool aligned) {
   if (M <= 0 || K <= 0 || N <= 0 || block <= 0) return 0;
-  GemmPlan p = plan_gemm(M, K, N, bits, block, out_bits);
+  const GemmPlan p = plan_gemm(M, K, N, bits, block, out_bits, aligned);
   return p.a_bytes + p.b_bytes + p.c_bytes + p.q_bytes + p.sa_bytes + p.sb_bytes + p.su_bytes + 1024;
+}
+
+size_t mxk_qgemm_workspace(int64_t M, int64_t K, int64_t N, int bits, int block, int out_bits) {
+  return qgemm_workspace(M, K, N, bits, block, out_bits, true);
+}
+
+size_t mxk_qgemm_workspace_any(int64_t M, int64_t K, int64_t N, int bits, int block, int out_bits) {
+  // operands not on 16 bytes take the unpacking path, whose buffers the aligned plan leaves out
+  return std::max(qgemm_workspace(M, K, N, bits, block, out_bits, true),
+                  qgemm_workspace(M, K, N, bits, block, out_bits, false));
 }
 
 int mxk_qgemm(const void* a_packed, const float* a_scales, int64_t a_nscales, const void* b_packed,
@@ -1105,12 +1178,19 @@ int mxk_qgemm(const void* a_packed, const float* a_scales, int64_t a_nscales, co
   if (out_bits > 0 && c_packed_nbytes < mxk_packed_nbytes(out_bits, M * N))
     return fail(MXK_EINVAL, "qgemm: packed output too small");
   GemmPlan p = plan_gemm(M, K, N, bits, block, out_bits, aligned16(a_packed) && aligned16(b_packed));
+  // the fused requantization stores whole 16-byte pieces of packed rows
+  // (else: two passes, with the buffers mxk_qgemm_workspace_any counts)
+  if (p.req && !aligned16(c_packed)) {
+    p.req = 0;
+    p.c_bytes = (((size_t)M * (size_t)N * sizeof(float)) + 255) & ~(size_t)255;
+    p.q_bytes = (((size_t)ceil_div(M * N, block) * sizeof(float2)) + 255) & ~(size_t)255;
+  }
   const size_t need = p.a_bytes + p.b_bytes + p.c_bytes + p.q_bytes + p.sa_bytes + p.sb_bytes + p.su_bytes;
   if (!workspace || workspace_nbytes < need)
     return fail(MXK_EINVAL, (aligned16(a_packed) && aligned16(b_packed))
                                 ? "qgemm: workspace too small"
-                                : "qgemm: workspace too small (operands not 16-byte aligned take the unpacking "
-                                  "path, whose workspace mxk_qgemm_workspace does not count)");
+                                : "qgemm: workspace too small (packed operands not on 16 bytes take the unpacking "
+                                  "path: size the workspace with mxk_qgemm_workspace_any)");
   uint8_t* ws = reinterpret_cast<uint8_t*>(workspace);
   const int a_ok = a_nscales == M * p.KB;
   const int b_ok = b_nscales == (int64_t)p.KB * N;
@@ -1123,7 +1203,7 @@ int mxk_qgemm(const void* a_packed, const float* a_scales, int64_t a_nscales, co
     float* sa_u = p.kn == 2 ? reinterpret_cast<float*>(ws + p.c_bytes + p.q_bytes + p.sa_bytes + p.sb_bytes)
                             : nullptr;
     int* exact = p.kn == 2 ? reinterpret_cast<int*>(reinterpret_cast<uint8_t*>(sa_u) + p.sa_bytes) : nullptr;
-    if (!Cb && !acc_i32) return fail(MXK_EINVAL, "qgemm: no output requested");
+    if (!Cb && !acc_i32 && !p.req) return fail(MXK_EINVAL, "qgemm: no output requested");
     const int cap = num_cus() * 8;
     const dim3 tg((unsigned)ceil_div(p.KB, 32), (unsigned)ceil_div(M, 32));
     if (p.kn == 2) {
@@ -1148,17 +1228,32 @@ int mxk_qgemm(const void* a_packed, const float* a_scales, int64_t a_nscales, co
     const int8_t* A = (const int8_t*)a_packed;
     const int8_t* B = (const int8_t*)b_packed;
     const int64_t lda = p.kn == 2 ? K / 2 : K, ldb = p.kn == 2 ? N / 2 : N;
-#define QG_KN_LAUNCH(MODE, WA, WC)                                                                                 \
-  hipLaunchKernelGGL((k_qgemm_kn<MODE, WA, WC>), g1, dim3(512), 0, st, A, lda, M, B, ldb, K, sa_s, sa_u, exact, sbs, \
-                     M, N, p.KB, Cb, acc_i32, grouped)
+#define QG_KN_LAUNCH(MODE, WA, WC, REQ)                                                                         \
+  hipLaunchKernelGGL((k_qgemm_kn<MODE, WA, WC, REQ>), g1, dim3(512), 0, st, A, lda, M, B, ldb, K, sa_s, sa_u, exact, \
+                     sbs, M, N, p.KB, Cb, acc_i32, grouped, (uint8_t*)c_packed, c_scales)
+    if (p.req) {
+      // c_f32 and acc_i32 (when asked for) are written as well; no workspace C, no second pass
+      if (p.kn == 1) {
+        if (acc_i32 && c_f32) QG_KN_LAUNCH(1, true, true, 16);
+        else if (acc_i32) QG_KN_LAUNCH(1, true, false, 16);
+        else if (c_f32) QG_KN_LAUNCH(1, false, true, 16);
+        else QG_KN_LAUNCH(1, false, false, 16);
+      } else {
+        if (acc_i32 && c_f32) QG_KN_LAUNCH(2, true, true, 8);
+        else if (acc_i32) QG_KN_LAUNCH(2, true, false, 8);
+        else if (c_f32) QG_KN_LAUNCH(2, false, true, 8);
+        else QG_KN_LAUNCH(2, false, false, 8);
+      }
+      return check_launch("qgemm");
+    }
     if (p.kn == 1) {
-      if (acc_i32 && Cb) QG_KN_LAUNCH(1, true, true);
-      else if (acc_i32) QG_KN_LAUNCH(1, true, false);
-      else QG_KN_LAUNCH(1, false, true);
+      if (acc_i32 && Cb) QG_KN_LAUNCH(1, true, true, 0);
+      else if (acc_i32) QG_KN_LAUNCH(1, true, false, 0);
+      else QG_KN_LAUNCH(1, false, true, 0);
     } else {
-      if (acc_i32 && Cb) QG_KN_LAUNCH(2, true, true);
-      else if (acc_i32) QG_KN_LAUNCH(2, true, false);
-      else QG_KN_LAUNCH(2, false, true);
+      if (acc_i32 && Cb) QG_KN_LAUNCH(2, true, true, 0);
+      else if (acc_i32) QG_KN_LAUNCH(2, true, false, 0);
+      else QG_KN_LAUNCH(2, false, true, 0);
     }
 #undef QG_KN_LAUNCH
     int rc = check_launch("qgemm");

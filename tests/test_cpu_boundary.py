@@ -156,3 +156,24 @@ def test_decode_workspace_limits():
     # [out, in] weights: K must be whole blocks of 128; x as f16 hi + lo
     assert h.mxk_linear_nt_workspace(64, 8192, 8192, 4, 128) >= 65536 + 64 * 8192 * 4
     assert h.mxk_linear_nt_workspace(64, 8000, 8192, 4, 128) == 0
+
+
+def test_qgemm_workspace_queries():
+    """mxk_qgemm_workspace sizes the workspace for packed operands on 16
+    bytes; mxk_qgemm_workspace_any for any alignment (misaligned operands
+    are unpacked into it first).  With N a multiple of 128 the int16 / int8
+    requantization runs in the GEMM's epilogue: no M*N float32 buffer."""
+    from qtpytorch_amd import _lib as L
+    h = L.lib()
+    M = K = N = 8192
+    for bits, ob in ((8, 16), (4, 8)):
+        fused = h.mxk_qgemm_workspace(M, K, N, bits, 128, ob)
+        c_only = h.mxk_qgemm_workspace(M, K, N, bits, 128, 0)
+        assert fused == c_only < M * N * 4          # no C buffer for the packed output
+        assert h.mxk_qgemm_workspace_any(M, K, N, bits, 128, ob) >= fused + M * N * 4
+    # N not whole 128-column blocks: a second pass over an fp32 C buffer
+    assert h.mxk_qgemm_workspace(M, K, 8160, 8, 128, 16) >= M * 8160 * 4
+    # the misaligned call names the other query
+    rc = h.mxk_qgemm(8, 8, M * (K // 128), 24, 8, (K // 128) * N, M, K, N, 8, 128, 16, 16, M * N * 2, 16, None,
+                     None, 16, h.mxk_qgemm_workspace(M, K, N, 8, 128, 16), None)
+    assert rc == -22 and b"mxk_qgemm_workspace_any" in h.mxk_last_error()

@@ -124,7 +124,15 @@ def test_config3_gemm_full_size_sampled_rows(qa, dtype):
     sa_rows = sa.view(M, 64)[rows].cpu().reshape(-1)
     _, _, C = orc.qscale_matmul(ac, sa_rows, bc, sb.cpu(), len(rows), K, N, dt.bits, 128, 16, return_c=True)
     assert _bits_eq(res["c"][rows], C.view(len(rows), N))
-    del res, pa, pb
+    del res
+    # qa @ qb's packed output (int16d / int8d), requantized in the GEMM's epilogue
+    ob = qa.matmul_output_dtype(dt, dt).bits
+    pk = qa.ops.qscale_gemm(pa, sa, pb, sb, M, K, N, dt.bits, 128, ob)
+    codes, scales = orc.qscale_matmul(ac, sa_rows, bc, sb.cpu(), len(rows), K, N, dt.bits, 128, ob)
+    got = orc.unpack_auto(pk["packed"].cpu(), ob, M * N).view(M, N)[rows].to(torch.int32)
+    assert torch.equal(got, codes.view(len(rows), N))
+    assert _bits_eq(pk["scales"].cpu().view(M, N // 128)[rows], scales.view(len(rows), N // 128))
+    del pk, pa, pb
     torch.cuda.empty_cache()
 
 

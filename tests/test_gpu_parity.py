@@ -387,6 +387,41 @@ def test_qgemm_large_tiles_sampled_rows(qa, dtype, shape):
 
 
 @pytest.mark.parametrize("dtype", ["int8d", "int4d"])
+@pytest.mark.parametrize("shape", [(4096, 384, 2048), (4100, 640, 2048), (4096, 1152, 4096), (4100, 256, 2176)],
+                         ids=lambda s: "x".join(map(str, s)))
+def test_qgemm_fused_requant(qa, dtype, shape):
+    """N a multiple of 128: qa @ qb's int16d (int8d for int4 operands)
+    codes and scales come from the GEMM's epilogue (mxtorch.py:1372-1385 on
+    each row segment of 128).  They equal the two-pass result (fp32 C, then
+    the requantization kernel) bit for bit, with and without the fp32 C
+    asked for as well, and the oracle's on sampled rows."""
+    M, K, N = shape
+    dt = qa.get_mx_dtype(dtype)
+    ob = qa.matmul_output_dtype(dt, dt).bits
+    pa, sa, _ = qa.ops.quantize(_randn((M, K), 301 + K).to(dev()), dt, 128)
+    pb, sb, _ = qa.ops.quantize(_randn((K, N), 303 + N).to(dev()), dt, 128)
+    fused = qa.ops.qscale_gemm(pa, sa, pb, sb, M, K, N, dt.bits, 128, ob)
+    fused_c = qa.ops.qscale_gemm(pa, sa, pb, sb, M, K, N, dt.bits, 128, ob, want_c=True, want_acc=True)
+    # the two-pass path: fp32 C, then the requantization kernel over it
+    c_only = qa.ops.qscale_gemm(pa, sa, pb, sb, M, K, N, dt.bits, 128, ob, want_packed=False, want_c=True)
+    pk2, sc2, _ = qa.ops.quantize(c_only["c"], qa.get_mx_dtype(f"int{ob}dv"), 128)
+    for r in (fused, fused_c):
+        assert _bits_eq(r["packed"], pk2), "packed codes differ from the two-pass result"
+        assert _bits_eq(r["scales"], sc2), "scales differ from the two-pass result"
+    assert _bits_eq(fused_c["c"], c_only["c"])
+    rows = sorted({0, 1, 127, 128, 255, 256, M // 2, M - 1})
+    bits = dt.bits
+    KB = K // 128
+    ac = orc.unpack_auto(pa.cpu(), bits, M * K).to(torch.int32).reshape(M, K)[rows].reshape(-1)
+    bc = orc.unpack_auto(pb.cpu(), bits, K * N).to(torch.int32)
+    sa_rows = sa.cpu().reshape(M, KB)[rows].reshape(-1)
+    codes, scales = orc.qscale_matmul(ac, sa_rows, bc, sb.cpu(), len(rows), K, N, bits, 128, ob)
+    got = orc.unpack_auto(fused["packed"].cpu(), ob, M * N).reshape(M, N)[rows]
+    assert torch.equal(got.to(torch.int32), codes.reshape(len(rows), N)), "codes differ from the oracle"
+    assert _bits_eq(fused["scales"].cpu().reshape(M, N // 128)[rows], scales.reshape(len(rows), N // 128))
+
+
+@pytest.mark.parametrize("dtype", ["int8d", "int4d"])
 def test_qgemm_large_tiles_scale_counts(qa, dtype):
     """Scale arrays of the wrong length mean ones (mxtorch.py:1352-1355) on
     the as-stored loop as well: A's, B's, and both."""
