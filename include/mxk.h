@@ -36,7 +36,7 @@
 extern "C" {
 #endif
 
-#define MXK_ABI_VERSION 7
+#define MXK_ABI_VERSION 8
 
 typedef enum {
   MXK_OK = 0,
@@ -215,12 +215,21 @@ int mxk_linear_wq_noalloc(const void* x, int x_type, int64_t M, int64_t K, const
 int mxk_linear_prepack_weight(const void* w_packed, int64_t K, int64_t N, int bits, int block, void* w_tiled,
                               void* stream);
 
+/* The inverse of mxk_linear_prepack_weight: w_packed receives the K*N/2
+ * bytes of the [K][N] packing back from the tiled copy, so that a caller may
+ * keep the tiled copy only and rebuild the packed codes when something else
+ * needs them (dequantize, checkpoints).  No reference counterpart.  Same
+ * arguments and alignment as mxk_linear_prepack_weight. */
+int mxk_linear_unpack_weight(const void* w_tiled, int64_t K, int64_t N, int bits, int block, void* w_packed,
+                             void* stream);
+
 /* mx_linear.forward (mxtorch.py:7454-7473) for int4 weights, block 128, from
- * the prepacked copies: out[M,N] = x[M,K] @ dequant(W) (+ bias), the same
- * product as mxk_linear_wq's decode path, float32 accumulation in another
- * order.  w_tiled = mxk_linear_prepack_weight(), w_scales_t =
- * mxk_linear_prepack_scales().  Takes M <= 16, K % 32 == 0, N % 128 == 0,
- * 16-byte aligned x, w_tiled, w_scales_t, bias and out; other shapes return
+ * the prepacked copies: out[M,N] = x[M,K] @ dequant(W) (+ bias), the product
+ * of mxk_linear_wq, float32 accumulation in another order.  w_tiled =
+ * mxk_linear_prepack_weight(), w_scales_t = mxk_linear_prepack_scales().
+ * K % 32 == 0, N % 128 == 0, 16-byte aligned w_tiled, w_scales_t, bias and
+ * out.  M <= 16 with 16-byte aligned x runs the decode kernel, any other M
+ * the MFMA path on the same tiled copy; other shapes return
  * MXK_EUNSUPPORTED (call mxk_linear_wq).  workspace: as for mxk_linear_wq
  * (mxk_linear_workspace() bytes, zero-filled before first use, left ready
  * for the next call; calls sharing it must not overlap). */

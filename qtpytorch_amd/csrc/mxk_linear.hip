@@ -828,6 +828,33 @@ __global__ __launch_bounds__(256) void k_tile_w4(const uint32_t* __restrict__ w,
   *reinterpret_cast<u32x4v*>(dst + 256) = u32x4v{o[4], o[5], o[6], o[7]};
 }
 
+// The inverse of k_tile_w4: thread (block nb, step ks, lane j + 16 g) reads
+// its 32 bytes of the chunk and writes the 4-byte words of columns
+// 8j..8j+7 of rows 8g..8g+7 (byte q of word 2p + e is row 4e + {0,2,1,3}[q],
+// a permutation that is its own inverse).
+__global__ __launch_bounds__(256) void k_untile_w4(const uint32_t* __restrict__ wt, int64_t K, int64_t N,
+                                                   uint32_t* __restrict__ w) {
+  const int64_t tid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t steps = K / 32, NB = N / 128;
+  if (tid >= NB * steps * 64) return;
+  const int lane = (int)(tid & 63);
+  const int64_t chunk = tid >> 6;
+  const int64_t nb = chunk / steps, ks = chunk % steps;
+  const int j = lane & 15, g = lane >> 4;
+  const uint32_t* src = wt + chunk * 512 + 4 * lane;
+  const u32x4v lo = *reinterpret_cast<const u32x4v*>(src), hi = *reinterpret_cast<const u32x4v*>(src + 256);
+  const uint32_t o[8] = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+  constexpr int inv[4] = {0, 2, 1, 3};
+  const int64_t words = N / 8;
+#pragma unroll
+  for (int r = 0; r < 8; ++r) {
+    uint32_t v = 0u;
+#pragma unroll
+    for (int p = 0; p < 4; ++p) v |= ((o[2 * p + (r >> 2)] >> (8 * inv[r & 3])) & 0xFFu) << (8 * p);
+    w[(ks * 32 + 8 * g + r) * words + nb * 16 + j] = v;
+  }
+}
+
 // sT[b][k] = s[k][b]: the reference's scales of a [K, N] weight with blocks
 // of 128 along N ([K][NB] row-major) to the block-major order the decode
 // kernel reads ([NB][K]).  32x32 tiles through LDS, both sides coalesced.
@@ -1789,6 +1816,21 @@ int mxk_linear_prepack_weight(const void* w_packed, int64_t K, int64_t N, int bi
   return check_launch("linear_prepack_weight");
 }
 
+int mxk_linear_unpack_weight(const void* w_tiled, int64_t K, int64_t N, int bits, int block, void* w_packed,
+                             void* stream) {
+  if (!w_packed || !w_tiled) return fail(MXK_EINVAL, "linear_unpack_weight: null pointer");
+  if (bits != 4 || block != 128 || K <= 0 || N <= 0 || K % 32 != 0 || N % 128 != 0)
+    return fail(MXK_EINVAL, "linear_unpack_weight: needs int4 codes, block 128, K a multiple of 32 and N of 128");
+  if ((reinterpret_cast<uintptr_t>(w_packed) & 3u) != 0 || !aligned16(w_tiled))
+    return fail(MXK_EINVAL, "linear_unpack_weight: w_packed must be 4-byte and w_tiled 16-byte aligned");
+  const int64_t threads = (N / 128) * (K / 32) * 64;
+  if (ceil_div(threads, 256) >= (int64_t(1) << 31)) return fail(MXK_EUNSUPPORTED, "linear_unpack_weight: too large");
+  hipLaunchKernelGGL(k_untile_w4, dim3((unsigned)ceil_div(threads, 256)), dim3(256), 0,
+                     reinterpret_cast<hipStream_t>(stream), reinterpret_cast<const uint32_t*>(w_tiled), K, N,
+                     reinterpret_cast<uint32_t*>(w_packed));
+  return check_launch("linear_unpack_weight");
+}
+
 int mxk_linear_wq_tiled(const void* x, int x_type, int64_t M, int64_t K, const void* w_tiled, const float* w_scales_t,
                         int64_t N, const float* bias, float* out, void* workspace, size_t workspace_nbytes,
                         void* stream) {
@@ -1799,9 +1841,16 @@ int mxk_linear_wq_tiled(const void* x, int x_type, int64_t M, int64_t K, const v
     return fail(MXK_EINVAL, "linear_wq_tiled: bad input type");
   if ((bias && !aligned16(bias)) || !aligned16(out))
     return fail(MXK_EINVAL, "linear_wq_tiled: bias and out must be 16-byte aligned");
-  if (!decode_tiled_eligible(M, K, N, x, x_type, w_tiled, w_scales_t))
-    return fail(MXK_EUNSUPPORTED, "linear_wq_tiled: needs M <= 16, K % 32 == 0, N % 128 == 0, 16-byte aligned "
-                                  "x, w_tiled and w_scales_t (use mxk_linear_wq)");
+  if (!decode_tiled_eligible(M, K, N, x, x_type, w_tiled, w_scales_t)) {
+    // more than 16 rows (or x not on 16 bytes): the MFMA path reads the tiled copy too
+    if (K % 32 == 0 && aligned16(w_tiled) && aligned16(w_scales_t)) {
+      const int rc = linear_mfma_kn_tiled(x, x_type, M, K, w_tiled, w_scales_t, N, bias, out, workspace,
+                                          workspace_nbytes, st);
+      if (rc != MXK_EUNSUPPORTED) return rc;
+    }
+    return fail(MXK_EUNSUPPORTED, "linear_wq_tiled: needs K % 32 == 0, N % 128 == 0, 16-byte aligned w_tiled "
+                                  "and w_scales_t (use mxk_linear_wq)");
+  }
   const DecodePlan p = plan_decode_tiled(K, N);
   const size_t need = p.counter_bytes + p.partial_bytes;
   if (p.S > 1 && (!workspace || workspace_nbytes < need))

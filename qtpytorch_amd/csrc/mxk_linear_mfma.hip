@@ -162,6 +162,38 @@ __device__ __forceinline__ void kn_store(const KnCodes<BITS>& c, uint8_t* sB, in
   }
 }
 
+// The same 8 x 8 blocks from the tiled copy of mxk_linear_prepack_weight:
+// chunk (nb, 32-row step) of 2 KiB, whose lane c8 + 16 (r8 % 4) holds the
+// block as two 16-byte pieces (at +16 L and +1024 + 16 L).  Word 2p + e,
+// byte q is the byte of columns 8 c8 + 2p, +1 of row 4e + {0,2,1,3}[q], so
+// rows 2q', 2q'+1 of column pair p sit at bits 0-7 and 16-23 of word
+// 2p + q'/2 shifted right by 8 (q' % 2): no byte permutes.
+struct KnTiled {
+  u4v w[2];
+};
+
+__device__ __forceinline__ void kn_load_tiled(KnTiled& c, __amdgpu_buffer_rsrc_t rw, int64_t k0, int64_t K,
+                                              int64_t nb, int tid) {
+  const int r8 = tid >> 4, c8 = tid & 15;
+  const int64_t chunk = nb * (K / 32) + (k0 + 8 * r8) / 32;
+  const uint32_t off = (uint32_t)(chunk * 2048 + 16 * (c8 + 16 * (r8 & 3)));
+  c.w[0] = buf_load_b128(rw, off, 0u);
+  c.w[1] = buf_load_b128(rw, off + 1024u, 0u);
+}
+
+__device__ __forceinline__ void kn_store_tiled(const KnTiled& c, uint8_t* sB, int tid) {
+  const int ks = tid >> 6, lane = tid & 63;
+  const uint32_t o[8] = {c.w[0][0], c.w[0][1], c.w[0][2], c.w[0][3], c.w[1][0], c.w[1][1], c.w[1][2], c.w[1][3]};
+#pragma unroll
+  for (int t = 0; t < 8; ++t) {
+    const int p = t >> 1;
+    u4v f;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) f[q] = lm_i4pair(o[2 * p + (q >> 1)] >> (8 * (q & 1) + 4 * (t & 1)));
+    *reinterpret_cast<u4v*>(sB + lm_frag_off(ks, t, lane)) = f;
+  }
+}
+
 // ---------------------------------------------------------------- [N][K] stage decode
 // int4: lanes 8a .. 8a+7 read the 128-byte line of one column (k steps
 // 0..7 of the stage, 16 bytes each); each 16 bytes are the four k octets of
@@ -247,7 +279,7 @@ struct NkA {
   u4v l[2];
 };
 
-template <int BITS, int WM, bool NK>
+template <int BITS, int WM, bool NK, bool TILED = false>
 __global__ __launch_bounds__(LM_THREADS, 1) void k_linear_mfma(
     const float* __restrict__ xs,        // [K][N]: x' [M][Kp] fp32
     const _Float16* __restrict__ xh,     // [N][K]: hi of x' [M][Kp]
@@ -258,7 +290,9 @@ __global__ __launch_bounds__(LM_THREADS, 1) void k_linear_mfma(
     float* __restrict__ part) {
   constexpr int WK = 8 / WM, KPW = 8 / WK;
   using A = typename std::conditional<NK, NkA, KnA>::type;
-  using Codes = typename std::conditional<NK, NkCodes<BITS>, KnCodes<BITS>>::type;
+  static_assert(!TILED || (!NK && BITS == 4), "the tiled copy holds int4 [K][N] weights");
+  using Codes = typename std::conditional<NK, NkCodes<BITS>,
+                                          typename std::conditional<TILED, KnTiled, KnCodes<BITS>>::type>::type;
   __shared__ __attribute__((aligned(1024))) uint8_t sB[2 * LM_STAGE_BYTES];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -325,10 +359,12 @@ __global__ __launch_bounds__(LM_THREADS, 1) void k_linear_mfma(
   };
   auto load_codes = [&](Codes& c, int st) {
     if constexpr (NK) nk_load<BITS>(c, rw, (int64_t)st * LM_STAGE, K, nb, tid);
+    else if constexpr (TILED) kn_load_tiled(c, rw, (int64_t)st * LM_STAGE, K, nb, tid);
     else kn_load<BITS>(c, rw, (int64_t)st * LM_STAGE, N, nb, tid);
   };
   auto store_codes = [&](const Codes& c, uint8_t* dst) {
     if constexpr (NK) nk_store<BITS>(c, dst, tid);
+    else if constexpr (TILED) kn_store_tiled(c, dst, tid);
     else kn_store<BITS>(c, dst, tid);
   };
 
@@ -708,25 +744,29 @@ LmPlan lm_plan(int64_t M, int64_t K, int64_t N, bool nk, int bits) {
   return p;
 }
 
-template <int BITS, int WM, bool NK>
+template <int BITS, int WM, bool NK, bool TILED>
 void lm_launch_t(const LmPlan& p, hipStream_t st, const float* xs, const _Float16* xh, const _Float16* xl,
                  const float* sc, int sc_kbm, const int* ex, int* es, const uint8_t* w, int64_t M, int64_t K,
                  int64_t N, const float* bias, float* out, float* part) {
   const dim3 grid((unsigned)(N / 128), (unsigned)ceil_div(M, 32 * WM), (unsigned)p.S);
-  hipLaunchKernelGGL((k_linear_mfma<BITS, WM, NK>), grid, dim3(LM_THREADS), 0, st, xs, xh, xl, sc, sc_kbm, ex, es, w,
-                     (int)M, K, p.Kp, N, p.sps, bias, out, p.S > 1 ? part : nullptr);
+  hipLaunchKernelGGL((k_linear_mfma<BITS, WM, NK, TILED>), grid, dim3(LM_THREADS), 0, st, xs, xh, xl, sc, sc_kbm, ex,
+                     es, w, (int)M, K, p.Kp, N, p.sps, bias, out, p.S > 1 ? part : nullptr);
 }
 
-template <int BITS, bool NK>
+template <int BITS, bool NK, bool TILED = false>
 void lm_launch_w(const LmPlan& p, hipStream_t st, const float* xs, const _Float16* xh, const _Float16* xl,
                  const float* sc, int sc_kbm, const int* ex, int* es, const uint8_t* w, int64_t M, int64_t K,
                  int64_t N, const float* bias, float* out, float* part) {
   constexpr int MW = lm_max_wm(NK, BITS);
   switch (p.wm) {
-    case 8: lm_launch_t<BITS, MW < 8 ? MW : 8, NK>(p, st, xs, xh, xl, sc, sc_kbm, ex, es, w, M, K, N, bias, out, part); break;
-    case 4: lm_launch_t<BITS, MW < 4 ? MW : 4, NK>(p, st, xs, xh, xl, sc, sc_kbm, ex, es, w, M, K, N, bias, out, part); break;
-    case 2: lm_launch_t<BITS, 2, NK>(p, st, xs, xh, xl, sc, sc_kbm, ex, es, w, M, K, N, bias, out, part); break;
-    default: lm_launch_t<BITS, 1, NK>(p, st, xs, xh, xl, sc, sc_kbm, ex, es, w, M, K, N, bias, out, part); break;
+    case 8:
+      lm_launch_t<BITS, MW < 8 ? MW : 8, NK, TILED>(p, st, xs, xh, xl, sc, sc_kbm, ex, es, w, M, K, N, bias, out, part);
+      break;
+    case 4:
+      lm_launch_t<BITS, MW < 4 ? MW : 4, NK, TILED>(p, st, xs, xh, xl, sc, sc_kbm, ex, es, w, M, K, N, bias, out, part);
+      break;
+    case 2: lm_launch_t<BITS, 2, NK, TILED>(p, st, xs, xh, xl, sc, sc_kbm, ex, es, w, M, K, N, bias, out, part); break;
+    default: lm_launch_t<BITS, 1, NK, TILED>(p, st, xs, xh, xl, sc, sc_kbm, ex, es, w, M, K, N, bias, out, part); break;
   }
 }
 
@@ -802,6 +842,29 @@ int linear_mfma_kn(const void* x, int x_type, int64_t M, int64_t K, const void* 
     hipLaunchKernelGGL(k_linear_mfma_reduce, dim3((unsigned)ceil_div(M * N / 4, 256)), dim3(256), 0, st, part, p.S,
                        M, N, ex, es, bias, out);
   return check_launch("linear_wq(mfma)");
+}
+
+// [K][N] int4 weight in the tiled layout (block-major scales required)
+int linear_mfma_kn_tiled(const void* x, int x_type, int64_t M, int64_t K, const void* w_tiled,
+                         const float* w_scales_t, int64_t N, const float* bias, float* out, void* workspace,
+                         size_t workspace_nbytes, hipStream_t st) {
+  if (!lm_common_ok(M, K, N, MXK_KIND_INT, 4, 128, x_type, out) || K % 32 != 0) return MXK_EUNSUPPORTED;
+  if (!aligned16(w_tiled) || !w_scales_t) return MXK_EUNSUPPORTED;
+  const LmPlan p = lm_plan(M, K, N, false, 4);
+  if (!workspace || workspace_nbytes < p.bytes)
+    return fail(MXK_EINVAL, "linear_wq_tiled: needs a workspace of mxk_linear_workspace() bytes");
+  uint8_t* ws = reinterpret_cast<uint8_t*>(workspace);
+  int* ex = reinterpret_cast<int*>(ws + p.off_ex);
+  int* es = reinterpret_cast<int*>(ws + p.off_es);
+  float* xs = reinterpret_cast<float*>(ws + p.off_x);
+  float* part = reinterpret_cast<float*>(ws + p.off_p);
+  lm_prep_rows<false>(x, x_type, M, K, p.Kp, xs, nullptr, nullptr, ex, st);
+  lm_launch_w<4, false, true>(p, st, xs, nullptr, nullptr, w_scales_t, 1, ex, es,
+                              reinterpret_cast<const uint8_t*>(w_tiled), M, K, N, bias, out, part);
+  if (p.S > 1)
+    hipLaunchKernelGGL(k_linear_mfma_reduce, dim3((unsigned)ceil_div(M * N / 4, 256)), dim3(256), 0, st, part, p.S,
+                       M, N, ex, es, bias, out);
+  return check_launch("linear_wq_tiled(mfma)");
 }
 
 // [N][K] weight (mx_dynamic_linear, input gradients).  `w_scales_t` is the

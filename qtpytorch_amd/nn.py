@@ -75,7 +75,7 @@ class mx_linear(nn.Module):
             # Module.half(), which dequantizes floating buffers): quantize it again
             w = mx_tensor.quantize(w.float(), self.mx_dtype, self.block)
             self._mx_weight = w
-        if w._mx_packed.device != x.device:
+        if w._mx_storage().device != x.device:
             w = w._move_device(x.device)
             self._mx_weight = w
             if self._mx_bias is not None:
@@ -85,33 +85,30 @@ class mx_linear(nn.Module):
         bias = None
         if self.apply_bias and self._mx_bias is not None:
             bias = self._mx_bias.dequantize()
-        rows = x.numel() // max(self.in_features, 1)
-        wt = self._decode_weight(w) if rows <= 16 else None
+        wt = self._tiled_weight(w)
         if torch.is_grad_enabled() and x.requires_grad:
             # the reference's F.linear(x, W_dq) carries the input gradient grad @ W_dq^T
             return _LinearWQ.apply(x, w, bias, self.in_features, self.out_features, self._decode_scales(w), wt)
-        return ops.linear_wq(x, w._mx_packed, w._mx_scales, w._mx_dtype, self.in_features, self.out_features,
-                             w._mx_block, bias=bias, w_scales_t=self._decode_scales(w), w_tiled=wt)
+        return ops.linear_wq(x, w._mx_packed if wt is None else None, w._mx_scales, w._mx_dtype, self.in_features,
+                             self.out_features, w._mx_block, bias=bias, w_scales_t=self._decode_scales(w), w_tiled=wt)
 
-    # Whether decode-shaped forwards (at most 16 rows of x) keep a tiled copy
-    # of an int4 weight's packed codes (in*out/2 bytes, made on the first
-    # such forward) for the faster decode kernel; False saves that memory.
+    # Whether an int4 weight (block 128, whole 128-column blocks) is held as
+    # its tiled copy only, from the first forward on: the layout the decode
+    # kernel (at most 16 rows of x) and the MFMA kernel (more rows) read, the
+    # same in*out/2 bytes as the packed codes, which are freed and rebuilt
+    # on demand (dequantize, state_dict, checkpoints).  False keeps the
+    # packed codes and runs the kernels that read them.
     tiled_decode = True
 
-    def _decode_weight(self, w) -> Optional[Tensor]:
-        """Tiled copy of the packed int4 weight for the decode kernel, made
-        once per weight tensor and rebuilt when the packed codes are replaced
-        or modified in place."""
+    def _tiled_weight(self, w) -> Optional[Tensor]:
+        """The tiled copy of an eligible int4 weight, made on the first
+        forward in place of its packed codes (mx_tensor._mx_tile_); an
+        in-place change of the codes (copy_, load_state_dict) turns the
+        weight back to packed storage, and the next forward tiles it again."""
         if not self.tiled_decode or not ops.decode_prepack_eligible(w._mx_dtype, w._mx_block, self.in_features,
                                                                    self.out_features):
             return None
-        pk = w._mx_packed
-        key = (pk.data_ptr(), str(pk.device), pk._version)
-        cached = self.__dict__.get("_w_tiled_cache")
-        if cached is None or cached[0] != key:
-            cached = (key, ops.prepack_weight(pk, self.in_features, self.out_features, w._mx_block))
-            self.__dict__["_w_tiled_cache"] = cached
-        return cached[1]
+        return w._mx_tile_(self.in_features, self.out_features)
 
     def _decode_scales(self, w) -> Optional[Tensor]:
         """Block-major copy of the weight's scales (1/16 of an int4 weight's
@@ -150,8 +147,9 @@ class _LinearWQ(torch.autograd.Function):
     def forward(ctx, x, w, bias, in_features, out_features, w_scales_t, w_tiled=None):
         ctx.w, ctx.w_scales_t = w, w_scales_t
         ctx.in_features, ctx.out_features = in_features, out_features
-        return ops.linear_wq(x.detach(), w._mx_packed, w._mx_scales, w._mx_dtype, in_features, out_features,
-                             w._mx_block, bias=bias, w_scales_t=w_scales_t, w_tiled=w_tiled)
+        return ops.linear_wq(x.detach(), w._mx_packed if w_tiled is None else None, w._mx_scales, w._mx_dtype,
+                             in_features, out_features, w._mx_block, bias=bias, w_scales_t=w_scales_t,
+                             w_tiled=w_tiled)
 
     @staticmethod
     def backward(ctx, grad):

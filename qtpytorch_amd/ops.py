@@ -377,7 +377,23 @@ def prepack_weight(w_packed: Tensor, in_features: int, out_features: int, block:
     return out
 
 
-def linear_wq(x: Tensor, w_packed: Tensor, w_scales: Tensor, dt, in_features: int, out_features: int,
+def unpack_weight(w_tiled: Tensor, in_features: int, out_features: int, block: int = 128) -> Tensor:
+    """The packed int4 [in, out] codes (uint8, in*out/2 bytes) rebuilt from
+    their tiled copy (mxk_linear_unpack_weight), the inverse of
+    prepack_weight."""
+    dev = L.require_gpu(w_tiled)
+    K, N = in_features, out_features
+    if w_tiled.numel() * w_tiled.element_size() != K * N // 2:
+        raise L.MXKError(f"unpack_weight: {w_tiled.numel()} bytes for a {K}x{N} int4 weight")
+    out = torch.empty(K * N // 2, dtype=torch.uint8, device=dev)
+    with torch.cuda.device(dev):
+        rc = L.lib().mxk_linear_unpack_weight(w_tiled.data_ptr(), K, N, 4, block, out.data_ptr(),
+                                               L.stream_of(w_tiled))
+    L.check(rc, f"unpack_weight({K}x{N})")
+    return out
+
+
+def linear_wq(x: Tensor, w_packed: Optional[Tensor], w_scales: Tensor, dt, in_features: int, out_features: int,
               block: int = 128, bias: Optional[Tensor] = None, w_scales_t: Optional[Tensor] = None,
               w_tiled: Optional[Tensor] = None) -> Tensor:
     """y = x.float() @ dequant(W) (+ bias) for W stored as quantize(weight.t())
@@ -386,9 +402,14 @@ def linear_wq(x: Tensor, w_packed: Tensor, w_scales: Tensor, dt, in_features: in
     `w_scales_t` is an optional prepack_scales() copy; without it the int4
     decode path transposes the scales into its workspace on every call.
     With `w_tiled` (prepack_weight()) and `w_scales_t` as well, the int4
-    decode shapes run the tiled decode kernel (mxk_linear_wq_tiled)."""
+    decode shapes run the tiled decode kernel and the other shapes the MFMA
+    kernel on the same tiled copy (mxk_linear_wq_tiled); `w_packed` may then
+    be None (a weight held as its tiled copy only), and shapes the tiled
+    entry point does not take rebuild the packed codes for one call."""
     dt = get_mx_dtype(dt)
-    dev = L.require_gpu(x, w_packed, w_scales)
+    if w_packed is None and w_tiled is None:
+        raise L.MXKError("linear_wq: needs the packed weight or its tiled copy")
+    dev = L.require_gpu(x, w_packed if w_packed is not None else w_tiled, w_scales)
     kind, var = _kind_variant(dt)
     if var != L.MXK_VAR_BASE:
         raise L.MXKError(f"linear_wq: {dt.name} weights need the base variant")
@@ -423,13 +444,13 @@ def linear_wq(x: Tensor, w_packed: Tensor, w_scales: Tensor, dt, in_features: in
     ws = _zeroed_workspace(ws_bytes, dev, stream)
     with torch.cuda.device(dev):
         rc = L.MXK_EUNSUPPORTED
-        if (w_tiled is not None and w_scales_t is not None and decode_prepack_eligible(dt, block, K, N)
-                and M <= 16 and xc.data_ptr() % 16 == 0):
+        if w_tiled is not None and w_scales_t is not None and decode_prepack_eligible(dt, block, K, N):
             rc = lib.mxk_linear_wq_tiled(xc.data_ptr(), L.elem_type(xc.dtype), M, K, w_tiled.data_ptr(),
                                          w_scales_t.data_ptr(), N, L.ptr(b), out.data_ptr(), L.ptr(ws), ws_bytes,
                                          stream)
         if rc == L.MXK_EUNSUPPORTED:
-            rc = lib.mxk_linear_wq(xc.data_ptr(), L.elem_type(xc.dtype), M, K, w_packed.contiguous().data_ptr(),
+            wp = w_packed.contiguous() if w_packed is not None else unpack_weight(w_tiled, K, N, block)
+            rc = lib.mxk_linear_wq(xc.data_ptr(), L.elem_type(xc.dtype), M, K, wp.data_ptr(),
                                    w_scales.contiguous().data_ptr(), L.ptr(w_scales_t), N, kind, dt.bits, block,
                                    L.ptr(b), out.data_ptr(), L.ptr(ws), ws_bytes, stream)
     L.check(rc, f"linear_wq({dt.name}, M={M}, K={K}, N={N})")

@@ -74,6 +74,46 @@ class mx_tensor(torch.Tensor):
     def __init__(self, packed, scales, mx_dtype, orig_shape, n, block=128, requires_grad=False, seed=None):
         pass
 
+    # ---- code storage: the packed codes, or, for an int4 [in, out] weight
+    # that mx_linear tiles, the tiled copy its kernels read and nothing else
+    # (one copy of the weight); the packed codes are then rebuilt on demand
+    # (ops.unpack_weight) for whatever else reads them.
+    @property
+    def _mx_packed(self) -> Tensor:
+        d = self.__dict__
+        t = d.get("_mx_tiled")
+        if t is not None:
+            K, N, dtype = d["_mx_tiled_meta"]
+            return ops.unpack_weight(t, K, N, self._mx_block).view(dtype)
+        return d["_mx_packed_store"]
+
+    @_mx_packed.setter
+    def _mx_packed(self, v: Tensor) -> None:
+        self.__dict__["_mx_packed_store"] = v
+        self.__dict__["_mx_tiled"] = None
+
+    def _mx_storage(self) -> Tensor:
+        """The tensor holding the codes (packed, or the tiled copy), without rebuilding anything."""
+        t = self.__dict__.get("_mx_tiled")
+        return t if t is not None else self.__dict__["_mx_packed_store"]
+
+    def _mx_tile_(self, in_features: int, out_features: int) -> Tensor:
+        """Hold the codes of this int4 [in, out] weight as their tiled copy
+        only (ops.prepack_weight) and return it; the packed bytes are freed."""
+        d = self.__dict__
+        if d.get("_mx_tiled") is None:
+            pk = d["_mx_packed_store"]
+            d["_mx_tiled_meta"] = (int(in_features), int(out_features), pk.dtype)
+            d["_mx_tiled"] = ops.prepack_weight(pk, in_features, out_features, self._mx_block)
+            d["_mx_packed_store"] = None
+        return d["_mx_tiled"]
+
+    def _mx_untile_(self) -> "mx_tensor":
+        """Back to packed storage (before an in-place change of the codes)."""
+        if self.__dict__.get("_mx_tiled") is not None:
+            self._mx_packed = self._mx_packed
+        return self
+
     # ---- tensor-subclass protocol (mxtorch.py:6058-6085) ----
     def __tensor_flatten__(self):
         meta = {"mx_dtype": self._mx_dtype, "orig_shape": self._mx_orig_shape,
@@ -140,7 +180,7 @@ class mx_tensor(torch.Tensor):
 
     @property
     def nbytes_packed(self) -> int:
-        return self._mx_packed.nbytes + self._mx_scales.nbytes
+        return self._mx_storage().nbytes + self._mx_scales.nbytes
 
     @property
     def compression_ratio(self) -> float:
@@ -208,7 +248,7 @@ class mx_tensor(torch.Tensor):
 
     def __repr__(self):
         return (f"mx_tensor({self._mx_dtype.name}, shape={tuple(self._mx_orig_shape)}, "
-                f"device={self._mx_packed.device}, {self.compression_ratio:.1f}x compression, "
+                f"device={self._mx_storage().device}, {self.compression_ratio:.1f}x compression, "
                 f"{self.nbytes_packed / 1024:.2f} KB packed)")
 
     def __len__(self):
@@ -302,6 +342,7 @@ class mx_tensor(torch.Tensor):
     def copy_(self, src, non_blocking: bool = False):
         """In-place copy of another mx_tensor's packed data (Module.load_state_dict
         copies saved buffers into the module's own this way)."""
+        self._mx_untile_()
         if not isinstance(src, mx_tensor):
             src = mx_tensor.quantize(src.float().to(self._mx_packed.device), self._mx_dtype, self._mx_block)
         if (src._mx_dtype != self._mx_dtype or src._mx_n != self._mx_n or src._mx_block != self._mx_block
@@ -335,8 +376,8 @@ def _is_mx_name(s: str) -> bool:
 
 
 _GETTERS = {
-    "device": lambda t: t._mx_packed.device,
-    "is_cuda": lambda t: t._mx_packed.is_cuda,
+    "device": lambda t: t._mx_storage().device,
+    "is_cuda": lambda t: t._mx_storage().is_cuda,
     "requires_grad": lambda t: False,
     "dtype": lambda t: torch.float32,
     "ndim": lambda t: len(t._mx_orig_shape),

@@ -117,26 +117,59 @@ def test_tiled_linear_vs_oracle(qa, M, K, N, xdt, use_bias):
 
 
 def test_mx_linear_keeps_one_tiled_copy(qa):
-    """mx_linear makes the tiled copy on the first decode-shaped forward,
-    reuses it, rebuilds it when the packed codes change, and skips it for
-    more than 16 rows or with tiled_decode = False."""
+    """mx_linear holds an eligible int4 weight as its tiled copy only, from
+    the first forward (any row count) on: one copy of the weight's bytes.
+    The packed codes come back bit for bit on demand (dequantize,
+    state_dict), the decode and MFMA kernels read the tiled copy, an
+    in-place copy_ turns the weight back to packed storage (and the next
+    forward tiles the new codes), and tiled_decode = False keeps the packed
+    codes."""
     K, N = 1024, 256
+    W = _randn((N, K), 61) * 0.03
     lin = torch.nn.Linear(K, N, bias=False)
+    with torch.no_grad():
+        lin.weight.copy_(W)
     m = qa.mx_linear.from_linear(lin.to(dev()), qa.get_mx_dtype("int4d"), 128)
-    x = torch.randn(4, K, device=dev())
-    y0 = m(x)
-    c0 = m.__dict__["_w_tiled_cache"][1]
-    y1 = m(x)
-    assert m.__dict__["_w_tiled_cache"][1] is c0 and G.bits_equal(y0.cpu(), y1.cpu())
-    m._mx_weight._mx_packed.bitwise_xor_(torch.tensor(0x11, dtype=torch.uint8, device=dev()))
-    m(x)
-    assert m.__dict__["_w_tiled_cache"][1] is not c0
-    m2 = qa.mx_linear.from_linear(lin.to(dev()), qa.get_mx_dtype("int4d"), 128)
-    m2(torch.randn(32, K, device=dev()))
-    assert "_w_tiled_cache" not in m2.__dict__
-    m2.tiled_decode = False
-    m2(x)
-    assert "_w_tiled_cache" not in m2.__dict__
+    wp, ws, _ = orc.linear_from_weight(W, "int4d", 128)
+    w = m._mx_weight
+    for M in (4, 40):
+        x = _randn((M, K), 63 + M)
+        y = m(x.to(dev())).cpu()
+        assert w.__dict__["_mx_tiled"] is not None and w.__dict__["_mx_packed_store"] is None
+        assert _rowwise_ok(y, orc.linear_forward(x, wp, ws, "int4d", K, N, 128))[0]
+    assert w.nbytes_packed == K * N // 2 + ws.numel() * 4          # one copy of the codes
+    assert G.bits_equal(w._mx_packed.cpu(), wp)                       # rebuilt on demand
+    assert w._mx_packed.dtype == wp.dtype
+    assert G.bits_equal(w.dequantize().cpu().reshape(-1), orc.dequant(wp, ws, "int4d", K * N, 128))
+    sd = {k: v for k, v in m.state_dict().items()}
+    m2 = qa.mx_linear.from_linear(torch.nn.Linear(K, N, bias=False).to(dev()), qa.get_mx_dtype("int4d"), 128)
+    m2.load_state_dict(sd)
+    x = _randn((9, K), 65).to(dev())
+    assert G.bits_equal(m2(x).cpu(), m(x).cpu())
+    # an in-place change of the codes
+    W2 = _randn((N, K), 67) * 0.03
+    q2 = qa.mx_tensor.quantize(W2.t().contiguous().to(dev()), qa.get_mx_dtype("int4d"), 128)
+    w.copy_(q2)
+    assert w.__dict__["_mx_tiled"] is None
+    wp2, ws2, _ = orc.linear_from_weight(W2, "int4d", 128)
+    y2 = m(x).cpu()
+    assert w.__dict__["_mx_tiled"] is not None
+    assert _rowwise_ok(y2, orc.linear_forward(x.cpu(), wp2, ws2, "int4d", K, N, 128))[0]
+    m3 = qa.mx_linear.from_linear(lin.to(dev()), qa.get_mx_dtype("int4d"), 128)
+    m3.tiled_decode = False
+    m3(x)
+    assert m3._mx_weight.__dict__["_mx_tiled"] is None
+
+
+@pytest.mark.parametrize("K,N", [(32, 128), (96, 384), (1024, 256), (8192, 8192)])
+def test_unpack_weight_inverts_prepack(qa, K, N):
+    """mxk_linear_unpack_weight gives back the packed bytes of any codes."""
+    g = torch.Generator()
+    g.manual_seed(K + N)
+    pk = torch.randint(0, 256, (K * N // 2,), generator=g, dtype=torch.uint8).to(dev())
+    t = qa.ops.prepack_weight(pk, K, N, 128)
+    assert not torch.equal(t, pk) or K * N <= 4096
+    assert torch.equal(qa.ops.unpack_weight(t, K, N, 128), pk)
 
 
 def test_tiled_two_streams_concurrently(qa):
