@@ -181,8 +181,15 @@ int mxk_linear_prepack_scales(const float* w_scales, int64_t K, int64_t N, int b
  * blocks of `block` flat elements (mxtorch.py:7447).  The dequantized
  * weight RN(code*s) (mxtorch.py:1573-1575) is formed in registers only.
  * kind/bits as for mxk_quantize (base variant).  Float32 accumulation.
+ * Int4 weights with x of at most 16 rows run the decode kernel; int4 and
+ * int8 weights (block 128, N % 128 == 0) with any other x run on f16 MFMAs,
+ * x * s as an f16 hi + lo pair against the exact codes (each term within
+ * 2^-22 of x * RN(code * s), after a power-of-two scaling of every row of
+ * x and every block of scales into f16's range); other widths and shapes a
+ * scalar fallback.
  * w_scales_t: optional mxk_linear_prepack_scales() copy of w_scales, read
- * by the int4 decode path (NULL: that path transposes into the workspace). */
+ * by the int4 decode path and the MFMA path (NULL: they transpose into the
+ * workspace). */
 int mxk_linear_wq(const void* x, int x_type, int64_t M, int64_t K, const void* w_packed,
                   const float* w_scales, const float* w_scales_t, int64_t N, int kind, int bits,
                   int block, const float* bias, float* out, void* workspace,
@@ -195,7 +202,8 @@ int mxk_linear_wq(const void* x, int x_type, int64_t M, int64_t K, const void* w
  * workspace is a static 8 MiB device array of the library (one per GPU,
  * held until the process ends), so shapes that need more (for example
  * N = 16384, K = 8192) return MXK_EINVAL: pass w_scales_t or use
- * mxk_linear_wq.  The call allocates nothing; the first call on a device
+ * mxk_linear_wq.  Other shapes take the MFMA path when its buffers fit the
+ * array and the scalar fallback otherwise.  The call allocates nothing; the first call on a device
  * clears the array's counters with a fill kernel on `stream`.  All calls on
  * one GPU share the array: calls that overlap on one GPU (other streams,
  * concurrent graph replays) race and must not be issued. */
