@@ -141,25 +141,29 @@ __device__ __forceinline__ void kn_load(KnCodes<BITS>& c, __amdgpu_buffer_rsrc_t
   }
 }
 
+// the B fragment of column tile t (column 8 c8 + t) from the thread's block
+template <int BITS>
+__device__ __forceinline__ u4v kn_frag(const KnCodes<BITS>& c, int t) {
+  u4v f;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    if constexpr (BITS == 4) {
+      // byte t/2 of rows 2q and 2q+1: the low nibbles are column 8 c8 + t for even t
+      const uint32_t d = __builtin_amdgcn_perm(c.w[2 * q + 1], c.w[2 * q], lm_sel(t >> 1, t >> 1));
+      f[q] = lm_i4pair((t & 1) ? d >> 4 : d);
+    } else {
+      const int h = t >> 2, u = t & 3;
+      f[q] = lm_i8pair(__builtin_amdgcn_perm(c.w[2 * (2 * q + 1) + h], c.w[2 * (2 * q) + h], lm_sel(u, u)));
+    }
+  }
+  return f;
+}
+
 template <int BITS>
 __device__ __forceinline__ void kn_store(const KnCodes<BITS>& c, uint8_t* sB, int tid) {
   const int ks = tid >> 6, lane = tid & 63;
 #pragma unroll
-  for (int t = 0; t < 8; ++t) {
-    u4v f;
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      if constexpr (BITS == 4) {
-        // byte t/2 of rows 2q and 2q+1: the low nibbles are column 8 c8 + t for even t
-        const uint32_t d = __builtin_amdgcn_perm(c.w[2 * q + 1], c.w[2 * q], lm_sel(t >> 1, t >> 1));
-        f[q] = lm_i4pair((t & 1) ? d >> 4 : d);
-      } else {
-        const int h = t >> 2, u = t & 3;
-        f[q] = lm_i8pair(__builtin_amdgcn_perm(c.w[2 * (2 * q + 1) + h], c.w[2 * (2 * q) + h], lm_sel(u, u)));
-      }
-    }
-    *reinterpret_cast<u4v*>(sB + lm_frag_off(ks, t, lane)) = f;
-  }
+  for (int t = 0; t < 8; ++t) *reinterpret_cast<u4v*>(sB + lm_frag_off(ks, t, lane)) = kn_frag<BITS>(c, t);
 }
 
 // The same 8 x 8 blocks from the tiled copy of mxk_linear_prepack_weight:
@@ -181,17 +185,19 @@ __device__ __forceinline__ void kn_load_tiled(KnTiled& c, __amdgpu_buffer_rsrc_t
   c.w[1] = buf_load_b128(rw, off + 1024u, 0u);
 }
 
+__device__ __forceinline__ u4v kn_frag_tiled(const KnTiled& c, int t) {
+  const uint32_t o[8] = {c.w[0][0], c.w[0][1], c.w[0][2], c.w[0][3], c.w[1][0], c.w[1][1], c.w[1][2], c.w[1][3]};
+  const int p = t >> 1;
+  u4v f;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) f[q] = lm_i4pair(o[2 * p + (q >> 1)] >> (8 * (q & 1) + 4 * (t & 1)));
+  return f;
+}
+
 __device__ __forceinline__ void kn_store_tiled(const KnTiled& c, uint8_t* sB, int tid) {
   const int ks = tid >> 6, lane = tid & 63;
-  const uint32_t o[8] = {c.w[0][0], c.w[0][1], c.w[0][2], c.w[0][3], c.w[1][0], c.w[1][1], c.w[1][2], c.w[1][3]};
 #pragma unroll
-  for (int t = 0; t < 8; ++t) {
-    const int p = t >> 1;
-    u4v f;
-#pragma unroll
-    for (int q = 0; q < 4; ++q) f[q] = lm_i4pair(o[2 * p + (q >> 1)] >> (8 * (q & 1) + 4 * (t & 1)));
-    *reinterpret_cast<u4v*>(sB + lm_frag_off(ks, t, lane)) = f;
-  }
+  for (int t = 0; t < 8; ++t) *reinterpret_cast<u4v*>(sB + lm_frag_off(ks, t, lane)) = kn_frag_tiled(c, t);
 }
 
 // ---------------------------------------------------------------- [N][K] stage decode
@@ -318,8 +324,11 @@ __global__ __launch_bounds__(LM_THREADS, 1) void k_linear_mfma(
   }
   // [K][N]: the block's scales go to the binade of 2^13 by 2^es (the
   // largest in [2^13, 2^14)); the epilogue takes 2^-es back out
+  // (called once the first stages' loads are in flight, so their
+  // latencies overlap)
   int es_nb = 0;
-  if constexpr (!NK) {
+  auto scan_es = [&]() {
+    if constexpr (NK) return;
     __shared__ float s_red[8];
     float mx = 0.0f;
     for (int64_t k = tid; k < K; k += 4 * LM_THREADS) {
@@ -338,7 +347,7 @@ __global__ __launch_bounds__(LM_THREADS, 1) void k_linear_mfma(
     es_nb = (be == 0xFF || mx == 0.0f) ? 0 : 140 - (be == 0 ? 1 : be);
     // the split reduction applies 2^-es after summing the partials
     if (part && es && blockIdx.y == 0 && blockIdx.z == 0 && tid == 0) es[nb] = es_nb;
-  }
+  };
   auto load_a = [&](A& a, int st, int jj) {
     const int64_t kg = (int64_t)st * LM_STAGE + 32 * (wk + WK * jj) + 8 * g;
 #pragma unroll
@@ -453,13 +462,54 @@ __global__ __launch_bounds__(LM_THREADS, 1) void k_linear_mfma(
   // A operands of this wave's k step gs (0 .. nsteps-1 over the split)
   const int nsteps = (st1 - st0) * KPW;
   auto load_step = [&](A& a, int gs) { load_a(a, st0 + gs / KPW, gs % KPW); };
-  if (st0 < st1) {
+  // One row tile ([K][N], WM = 1): wave w runs k step w of every stage, and
+  // the fragments its lanes decode are exactly the ones they feed to the
+  // MFMAs, so the codes skip LDS (and every barrier): each wave keeps DS
+  // stages of its codes in flight in registers.
+  if (st0 >= st1) scan_es();
+  constexpr bool DIRECT = !NK && WM == 1;
+  constexpr int DS = BITS == 8 ? 2 : 4;
+  if constexpr (DIRECT) {
+   if (st0 < st1) {
+    Codes cq[DS];
+    A ar[2];
+#pragma unroll
+    for (int i = 0; i < DS; ++i)
+      if (st0 + i < st1) load_codes(cq[i], st0 + i);
+    load_step(ar[0], 0);
+    if (nsteps > 1) load_step(ar[1], 1);
+    scan_es();
+    for (int sb = st0; sb < st1; sb += DS) {
+#pragma unroll
+      for (int i = 0; i < DS; ++i) {
+        const int st = sb + i;
+        if (st < st1) {
+          const int gs = st - st0, p = i & 1;  // DS is even, so gs % 2 = i % 2
+          h8v bt[8];
+#pragma unroll
+          for (int t = 0; t < 8; ++t) {
+            if constexpr (TILED) bt[t] = __builtin_bit_cast(h8v, kn_frag_tiled(cq[i], t));
+            else bt[t] = __builtin_bit_cast(h8v, kn_frag<BITS>(cq[i], t));
+          }
+          if (st + DS < st1) load_codes(cq[i], st + DS);
+          h8v ahi[2], alo[2];
+          build(ar[p], ahi, alo);
+          if (gs + 2 < nsteps) load_step(ar[p], gs + 2);
+          __builtin_amdgcn_sched_barrier(0);
+          mfmas(ahi, alo, bt, 0, 8);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      }
+    }
+   }
+  } else if (st0 < st1) {
     Codes cc;
     A ar[2];
     float s8[8];
     load_codes(cc, st0);
     load_step(ar[0], 0);
     if (nsteps > 1) load_step(ar[1], 1);
+    scan_es();
     store_codes(cc, sB);
     lm_barrier();
     for (int st = st0; st < st1; ++st) {
