@@ -263,7 +263,7 @@ __global__ __launch_bounds__(DEC_THREADS, 1) void k_linear_w4_decode(
     xst[i] = buf_load_b128(rx, ok ? (uint32_t)(((int64_t)m * K + k0w + (int64_t)c * EPL) * sizeof(T)) : DEC_OOB, 0u);
   }
   const int64_t r4 = kw + 4 * lane;  // K % 4 == 0: a 16-byte group is wholly in or out
-  const u32x4 sst = buf_load_b128(rs, (lane < RPW / 4 && r4 < K) ? (uint32_t)((nb * K + r4) * 4) : DEC_OOB, 0u);
+  const u32x4 sst = buf_load_b128_nt(rs, (lane < RPW / 4 && r4 < K) ? (uint32_t)((nb * K + r4) * 4) : DEC_OOB, 0u);
   // every wave's x and scale requests are issued before any wave's weight
   // requests: the CU returns data in request order, so x arrives first while
   // the weight stream is already queued behind it
@@ -285,7 +285,7 @@ __global__ __launch_bounds__(DEC_THREADS, 1) void k_linear_w4_decode(
     const int64_t k0 = kw + (int64_t)st * 32;
     const uint32_t kr = k0 < K ? (uint32_t)k0 : 0u;  // wave-uniform
 #pragma unroll
-    for (int r = 0; r < 8; ++r) wv[slot][r] = buf_load_b32(rw, vw, (kr + r) * row_bytes);
+    for (int r = 0; r < 8; ++r) wv[slot][r] = buf_load_b32_nt(rw, vw, (kr + r) * row_bytes);
   };
   issue(0, 0);
   // keep the loads where they are written (the scheduler would otherwise
@@ -577,7 +577,7 @@ __global__ __launch_bounds__(W * 64, 1) void k_linear_w4_decode_tiled(
     xr[q] = buf_load_b128(rx, ok ? (uint32_t)(((int64_t)m * K + kk) * sizeof(T)) : DEC_OOB, 0u);
   }
   const int64_t r4 = kw + 4 * lane;
-  const u32x4 sst = buf_load_b128(rs, (lane < RPW / 4 && r4 < K) ? (uint32_t)((nb * K + r4) * 4) : DEC_OOB, 0u);
+  const u32x4 sst = buf_load_b128_nt(rs, (lane < RPW / 4 && r4 < K) ? (uint32_t)((nb * K + r4) * 4) : DEC_OOB, 0u);
   __builtin_amdgcn_sched_barrier(0);
 
   // ---- x into the A-fragment order (lane (j, g): row j, columns
@@ -654,8 +654,8 @@ __global__ __launch_bounds__(W * 64, 1) void k_linear_w4_decode_tiled(
     const int64_t k0 = kw + (int64_t)st * 32;
     const uint32_t kr = k0 < K ? (uint32_t)k0 : 0u;  // wave-uniform
     const uint32_t cbase = (uint32_t)((nb * (K / 32) + kr / 32) * 2048);
-    wq[st][0] = buf_load_b128(rw, 16u * lane, cbase);
-    wq[st][1] = buf_load_b128(rw, 16u * lane, cbase + 1024u);
+    wq[st][0] = buf_load_b128_nt(rw, 16u * lane, cbase);
+    wq[st][1] = buf_load_b128_nt(rw, 16u * lane, cbase + 1024u);
   }
   __builtin_amdgcn_sched_barrier(0);
 
@@ -958,7 +958,7 @@ __global__ __launch_bounds__(NT_THREADS, 1) void k_linear_w4t_decode(
   float sc[8];
   auto load_tile = [&](int t) {
     const int64_t n = std::min<int64_t>(n0 + 16 * t + j, N - 1);
-    wv[t] = buf_load_b128(rw, (uint32_t)(n * (K / 2) + kb * 64 + 16 * g), 0u);
+    wv[t] = buf_load_b128_nt(rw, (uint32_t)(n * (K / 2) + kb * 64 + 16 * g), 0u);
   };
   // only the first tile before x is staged: requests queued ahead of x delay it
   if (live) load_tile(0);
@@ -1021,7 +1021,7 @@ __global__ __launch_bounds__(NT_THREADS, 1) void k_linear_w4t_decode(
     for (int t = 0; t < 8; ++t) {
       const int64_t n = std::min<int64_t>(n0 + 16 * t + j, N - 1);
       const int64_t si = scales_kb_major ? kb * N + n : n * KB + kb;
-      sc[t] = __uint_as_float(buf_load_b32(rs, (uint32_t)(si * 4), 0u));
+      sc[t] = __uint_as_float(buf_load_b32_nt(rs, (uint32_t)(si * 4), 0u));
     }
 #pragma unroll
     for (int t = 1; t < 8; ++t) load_tile(t);
@@ -1264,14 +1264,14 @@ __global__ __launch_bounds__(W * 64, 1) void k_linear_w4t_decode_long(
     for (int t = 0; t < 8; ++t) {
       const int64_t n = n0 + 16 * t + j;
       const int64_t si = scales_kb_major ? kb * N + n : n * KB + kb;
-      sc[b][t] = __uint_as_float(buf_load_b32(rs, (uint32_t)(si * 4), 0u));
+      sc[b][t] = __uint_as_float(buf_load_b32_nt(rs, (uint32_t)(si * 4), 0u));
     }
 #pragma unroll
     for (int t = 0; t < 8; ++t) {
       if constexpr (TILED)
-        wv[b][t] = buf_load_b128(rw, 16u * lane, (uint32_t)(((nb * 8 + t) * KB + kb) * 1024));
+        wv[b][t] = buf_load_b128_nt(rw, 16u * lane, (uint32_t)(((nb * 8 + t) * KB + kb) * 1024));
       else
-        wv[b][t] = buf_load_b128(rw, (uint32_t)((n0 + 16 * t + j) * (K / 2) + 16 * g), (uint32_t)(kb * 64));
+        wv[b][t] = buf_load_b128_nt(rw, (uint32_t)((n0 + 16 * t + j) * (K / 2) + 16 * g), (uint32_t)(kb * 64));
     }
   }
   __builtin_amdgcn_sched_barrier(0);
