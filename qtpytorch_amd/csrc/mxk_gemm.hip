@@ -977,6 +977,156 @@ __global__ __launch_bounds__(512, 1) void k_qgemm_kn(const int8_t* __restrict__ 
                                                          C, acc_out, grouped, nullptr, cq, cq_scales);
 }
 
+// ---------------------------------------------------------------- small GEMMs
+// int8 codes, block 128, operands and scales as stored, for shapes whose
+// 256x128 tiles do not give every CU a workgroup (config 1: 512^3), in one
+// launch.  One 32x32 output tile per workgroup of 4 waves; the K blocks go
+// round-robin to the waves (wave w: blocks w, w + 4, ...).  For its block a
+// wave
+//  - loads its A operands straight from A (rows m0 + 16i + lr, bytes
+//    16 lg .. 16 lg + 15 of each 64-wide half of the block),
+//  - copies the block's 128x32 slab of B (as stored, N-contiguous) into its
+//    own LDS slot and takes the B operands out with ds_read_b64_tr_b8 (K
+//    rows 16 lg + 8 rd + lr / 2, half lr % 2 of each 16-column segment:
+//    lane lr then holds 8 K values of column lr),
+//  - runs 8 v_mfma_i32_16x16x64_i8 and forms v = RN(RN(P*SA)*SB) for its
+//    16 outputs per lane (v does not depend on C).
+// The waves' v meet in LDS, where each thread adds those of its 4 outputs
+// to C in K-block order, C = RN(C + v) for kb ascending from C = +0, the
+// reference's sum (mxtorch.py:1357-1370).  The B slot is the wave's own, and
+// LDS runs one wave's accesses in order: no barrier between the copy and
+// the transposed reads.
+#define QGS_TILE 32
+template <bool WRITE_ACC, bool WRITE_C>
+__global__ __launch_bounds__(256) void k_qgemm_small(const int8_t* __restrict__ A, const int8_t* __restrict__ B,
+                                                     const float* __restrict__ sa, const float* __restrict__ sb,
+                                                     int sa_ok, int sb_ok, int64_t M, int64_t K, int64_t N, int KB,
+                                                     float* __restrict__ C, int32_t* __restrict__ acc_out) {
+  __shared__ __attribute__((aligned(16))) int8_t sB[4 * 128 * QGS_TILE];
+  __shared__ __attribute__((aligned(16))) float sV[4 * 64 * 16];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lr = lane & 15, lg = lane >> 4;
+  const int64_t m0 = (int64_t)blockIdx.y * QGS_TILE, n0 = (int64_t)blockIdx.x * QGS_TILE;
+  const __amdgpu_buffer_rsrc_t rA = make_rsrc(A, (uint32_t)(M * K));
+  const __amdgpu_buffer_rsrc_t rB = make_rsrc(B, (uint32_t)(K * N));
+  const __amdgpu_buffer_rsrc_t rSA = make_rsrc(sa, sa_ok ? (uint32_t)(M * KB * 4) : 0u);
+  const __amdgpu_buffer_rsrc_t rSB = make_rsrc(sb, sb_ok ? (uint32_t)((int64_t)KB * N * 4) : 0u);
+  constexpr uint32_t OOB = 0x80000000u;  // past every range: the load returns zeros
+  // per-lane offsets that do not depend on the K block
+  uint32_t oa[2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int64_t m = m0 + 16 * i + lr;
+    oa[i] = m < M ? (uint32_t)(m * K + 16 * lg) : OOB;
+  }
+  uint32_t ob[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int c = lane + 64 * q, rr = c >> 1, hh = c & 1;
+    ob[q] = n0 + 16 * hh < N ? (uint32_t)(rr * N + n0 + 16 * hh) : OOB;
+  }
+  int8_t* slot = sB + wave * 128 * QGS_TILE;
+  const uint32_t tr_base = (uint32_t)(uintptr_t)slot + (uint32_t)((16 * lg + (lr >> 1)) * QGS_TILE + 8 * (lr & 1));
+  float cacc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  const int own = tid >> 6;  // this thread's (row tile, column tile) of lane `lane` in the sums
+
+  for (int kb0 = 0; kb0 < KB; kb0 += 4) {
+    const int kb = kb0 + wave;
+    if (kb < KB) {
+      u32x4 af[2][2], bl[4];
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+          af[i][h] = buf_load_b128(rA, oa[i] == OOB ? OOB : oa[i] + 64u * h, (uint32_t)kb * 128u);
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        bl[q] = buf_load_b128(rB, ob[q] == OOB ? OOB : ob[q], (uint32_t)((int64_t)kb * 128 * N));
+      float sav[2][4], sbv[2];
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int64_t m = m0 + 16 * i + 4 * lg + r;
+          sav[i][r] = sa_ok ? __uint_as_float(buf_load_b32(rSA, m < M ? (uint32_t)((m * KB + kb) * 4) : OOB, 0u))
+                            : 1.0f;
+        }
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        const int64_t n = n0 + 16 * t + lr;
+        sbv[t] = sb_ok ? __uint_as_float(buf_load_b32(rSB, n < N ? (uint32_t)(((int64_t)kb * N + n) * 4) : OOB, 0u))
+                       : 1.0f;
+      }
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int c = lane + 64 * q;
+        *reinterpret_cast<u32x4*>(slot + (c >> 1) * QGS_TILE + 16 * (c & 1)) = bl[q];
+      }
+      // B operands: column tile t, K half h, K rows 16 lg + 8 rd + 0..7
+      i32x2 btr[2][2][2];
+      btr[0][0][0] = qg3_ds_read_tr<0>(tr_base);
+      btr[0][0][1] = qg3_ds_read_tr<8 * QGS_TILE>(tr_base);
+      btr[0][1][0] = qg3_ds_read_tr<64 * QGS_TILE>(tr_base);
+      btr[0][1][1] = qg3_ds_read_tr<72 * QGS_TILE>(tr_base);
+      btr[1][0][0] = qg3_ds_read_tr<16>(tr_base);
+      btr[1][0][1] = qg3_ds_read_tr<8 * QGS_TILE + 16>(tr_base);
+      btr[1][1][0] = qg3_ds_read_tr<64 * QGS_TILE + 16>(tr_base);
+      btr[1][1][1] = qg3_ds_read_tr<72 * QGS_TILE + 16>(tr_base);
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+          for (int rd = 0; rd < 2; ++rd) qg3_lgkm_wait<0>(btr[t][h][rd]);
+      i32x4 bf[2][2];
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+          bf[t][h] = i32x4{btr[t][h][0][0], btr[t][h][0][1], btr[t][h][1][0], btr[t][h][1][1]};
+      f32x4v* vout = reinterpret_cast<f32x4v*>(sV + (wave * 64 + lane) * 16);
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+          i32x4 p = __builtin_amdgcn_mfma_i32_16x16x64_i8(__builtin_bit_cast(i32x4, af[i][0]), bf[t][0],
+                                                          i32x4{0, 0, 0, 0}, 0, 0, 0);
+          p = __builtin_amdgcn_mfma_i32_16x16x64_i8(__builtin_bit_cast(i32x4, af[i][1]), bf[t][1], p, 0, 0, 0);
+          f32x4v v;
+#pragma unroll
+          for (int r = 0; r < 4; ++r) v[r] = ((float)p[r] * sav[i][r]) * sbv[t];
+          vout[i * 2 + t] = v;
+          if constexpr (WRITE_ACC) {
+            const int64_t n = n0 + 16 * t + lr;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              const int64_t m = m0 + 16 * i + 4 * lg + r;
+              if (m < M && n < N) acc_out[((int64_t)kb * M + m) * N + n] = p[r];
+            }
+          }
+        }
+    }
+    __syncthreads();
+    const int nk = KB - kb0 < 4 ? KB - kb0 : 4;
+    for (int u = 0; u < nk; ++u) {
+      const f32x4v v = *reinterpret_cast<const f32x4v*>(sV + (u * 64 + lane) * 16 + own * 4);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) cacc[r] = cacc[r] + v[r];
+    }
+    __syncthreads();
+  }
+  if constexpr (WRITE_C) {
+    const int i = own >> 1, t = own & 1;
+    const int64_t n = n0 + 16 * t + lr;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int64_t m = m0 + 16 * i + 4 * lg + r;
+      if (m < M && n < N) C[m * N + n] = cacc[r];
+    }
+  }
+}
+
 __global__ __launch_bounds__(256) void k_fill_ones(float* __restrict__ p, int64_t n) {
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
     p[i] = 1.0f;
@@ -1049,6 +1199,7 @@ struct GemmPlan {
   int KB, BP;
   int64_t KBP, Mpad, Npad;
   bool direct_a, v2, v3;
+  bool small = false;  // k_qgemm_small: int8, block 128, grids of 256x128 tiles below the CU count
   int kn;  // 1: int8 with B read as stored, 2: int4 A and B read as stored (k_qgemm_kn), 0: unpacking pre-pass
   int req;  // output width requantized in the GEMM's epilogue (kn, N % 128 == 0), 0: a second pass
   size_t a_bytes, b_bytes, c_bytes, q_bytes, sa_bytes, sb_bytes, su_bytes;
@@ -1090,6 +1241,16 @@ static GemmPlan plan_gemm(int64_t M, int64_t K, int64_t N, int bits, int block, 
     p.sa_bytes = up((size_t)p.KB * (size_t)M * sizeof(float));
     p.su_bytes = p.kn == 2 ? p.sa_bytes + 256 : 0;  // unscaled SA and the exact flag
     p.sb_bytes = up((size_t)p.KB * (size_t)N * sizeof(float));
+    return p;
+  }
+  // small int8 shapes: one launch on the operands and scales as stored
+  p.small = aligned && bits == 8 && block == 128 && K % 128 == 0 && N % 16 == 0 && !big && M * K < lim &&
+            K * N < lim && (int64_t)p.KB * M * 4 < lim && (int64_t)p.KB * N * 4 < lim &&
+            ceil_div(M, QGS_TILE) < 65536;
+  if (p.small) {
+    p.direct_a = true;
+    p.v2 = p.v3 = false;
+    p.a_bytes = p.b_bytes = p.sa_bytes = p.sb_bytes = p.su_bytes = 0;
     return p;
   }
   p.su_bytes = 0;
@@ -1262,6 +1423,26 @@ int mxk_qgemm(const void* a_packed, const float* a_scales, int64_t a_nscales, co
       return requant_vec_f32(Cb, M * N, out_bits, block, c_packed, c_packed_nbytes, c_scales, M * N, qw, p.q_bytes,
                              st);
     return MXK_OK;
+  }
+  if (p.small) {
+    float* Cb = c_f32 ? c_f32 : (p.c_bytes ? reinterpret_cast<float*>(ws) : nullptr);
+    if (!Cb && !acc_i32) return fail(MXK_EINVAL, "qgemm: no output requested");
+    const dim3 grid((unsigned)ceil_div(N, QGS_TILE), (unsigned)ceil_div(M, QGS_TILE));
+    const int8_t* A = (const int8_t*)a_packed;
+    const int8_t* B = (const int8_t*)b_packed;
+    if (acc_i32 && Cb)
+      hipLaunchKernelGGL((k_qgemm_small<true, true>), grid, dim3(256), 0, st, A, B, a_scales, b_scales, a_ok, b_ok, M,
+                         K, N, p.KB, Cb, acc_i32);
+    else if (acc_i32)
+      hipLaunchKernelGGL((k_qgemm_small<true, false>), grid, dim3(256), 0, st, A, B, a_scales, b_scales, a_ok, b_ok,
+                         M, K, N, p.KB, Cb, acc_i32);
+    else
+      hipLaunchKernelGGL((k_qgemm_small<false, true>), grid, dim3(256), 0, st, A, B, a_scales, b_scales, a_ok, b_ok,
+                         M, K, N, p.KB, Cb, acc_i32);
+    const int rc = check_launch("qgemm");
+    if (rc != MXK_OK || out_bits <= 0) return rc;
+    return requant_vec_f32(Cb, M * N, out_bits, block, c_packed, c_packed_nbytes, c_scales, M * N, ws + p.c_bytes,
+                           p.q_bytes, st);
   }
   int8_t* A8 = p.direct_a ? (int8_t*)a_packed : reinterpret_cast<int8_t*>(ws);
   int8_t* B8 = reinterpret_cast<int8_t*>(ws + p.a_bytes);

@@ -308,6 +308,13 @@ def qscale_gemm(a_packed: Tensor, a_scales: Tensor, b_packed: Tensor, b_scales: 
         out["acc"] = acc
     ap, asc = a_packed.contiguous(), a_scales.contiguous().float()
     bp, bsc = b_packed.contiguous(), b_scales.contiguous().float()
+    # an empty scale array is one of the wrong length (ones, as the reference
+    # reads it); the C-ABI takes a non-null pointer with a count of 0
+    n_asc, n_bsc = asc.numel(), bsc.numel()
+    if n_asc == 0:
+        asc = torch.ones(1, dtype=torch.float32, device=dev)
+    if n_bsc == 0:
+        bsc = torch.ones(1, dtype=torch.float32, device=dev)
     # the kernels that read the packed operands as stored load them in
     # 16-byte pieces (the workspace size assumes so): realign views that
     # start inside an allocation
@@ -319,7 +326,7 @@ def qscale_gemm(a_packed: Tensor, a_scales: Tensor, b_packed: Tensor, b_scales: 
     ws_bytes = lib.mxk_qgemm_workspace(M, K, N, bits, block, out_bits if want_packed else 0)
     ws = _workspace(ws_bytes, dev)
     with torch.cuda.device(dev):
-        rc = lib.mxk_qgemm(ap.data_ptr(), asc.data_ptr(), asc.numel(), bp.data_ptr(), bsc.data_ptr(), bsc.numel(),
+        rc = lib.mxk_qgemm(ap.data_ptr(), asc.data_ptr(), n_asc, bp.data_ptr(), bsc.data_ptr(), n_bsc,
                            M, K, N, bits, block, out_bits if want_packed else 0,
                            L.ptr(cp), 0 if cp is None else cp.numel() * cp.element_size(), L.ptr(cs), L.ptr(cf),
                            L.ptr(acc), L.ptr(ws), ws_bytes, L.stream_of(ap))

@@ -434,6 +434,45 @@ def test_qgemm_large_tiles_scale_counts(qa, dtype):
         _large_gemm_vs_oracle(qa, dtype, M, K, N, pa, a_s, pb, b_s, rows)
 
 
+SMALL_GEMM_SHAPES = [(40, 384, 48), (16, 1024, 16), (64, 1152, 96), (1, 128, 32), (72, 256, 4080), (300, 512, 208)]
+
+
+@pytest.mark.parametrize("shape", SMALL_GEMM_SHAPES, ids=lambda s: "x".join(map(str, s)))
+def test_qgemm_small_tiles(qa, shape):
+    """The one-launch int8 kernel for grids below the CU count: 32x32 tiles,
+    K blocks round-robin over 4 waves (9 blocks: a short last round), M and
+    N tails inside a tile, N below the tile; C, the int32 accumulators (all
+    three kernel variants) and the int16d requantization bitwise against the
+    oracle, then scale arrays of the wrong length as ones."""
+    M, K, N = shape
+    dt = qa.get_mx_dtype("int8d")
+    A = _randn((M, K), 401 + M)
+    B = _randn((K, N), 409 + N)
+    pa, sa, _ = qa.ops.quantize(A.to(dev()), dt, 128)
+    pb, sb, _ = qa.ops.quantize(B.to(dev()), dt, 128)
+    res = qa.ops.qscale_gemm(pa, sa, pb, sb, M, K, N, 8, 128, 16, want_c=True, want_acc=True)
+    c_only = qa.ops.qscale_gemm(pa, sa, pb, sb, M, K, N, 8, 128, 16, want_packed=False, want_c=True)
+    acc_only = qa.ops.qscale_gemm(pa, sa, pb, sb, M, K, N, 8, 128, 16, want_packed=False, want_acc=True)
+    rpa, rsa, _ = orc.quantize(A, "int8d", 128)
+    rpb, rsb, _ = orc.quantize(B, "int8d", 128)
+    ac = orc.unpack_auto(rpa, 8, M * K).to(torch.int32)
+    bc = orc.unpack_auto(rpb, 8, K * N).to(torch.int32)
+    codes, scales, C = orc.qscale_matmul(ac, rsa, bc, rsb, M, K, N, 8, 128, 16, return_c=True)
+    acc = orc.int_accumulators(ac, bc, M, K, N, 128)
+    assert torch.equal(res["acc"].cpu(), acc), "int32 accumulators differ"
+    assert torch.equal(acc_only["acc"].cpu(), acc)
+    assert _bits_eq(res["c"], C), "fp32 accumulator C differs"
+    assert _bits_eq(c_only["c"], C)
+    assert _bits_eq(res["packed"], orc.pack_auto(codes, 16))
+    assert _bits_eq(res["scales"], scales)
+    for a_s, b_s in ((sa[:-1], sb), (sa, sb[:-1]), (sa[:-1], sb[:-1])):
+        got = qa.ops.qscale_gemm(pa, a_s, pb, b_s, M, K, N, 8, 128, 16, want_packed=False, want_c=True)
+        ra = rsa[:-1] if a_s.numel() < sa.numel() else rsa
+        rb = rsb[:-1] if b_s.numel() < sb.numel() else rsb
+        _, _, Cw = orc.qscale_matmul(ac, ra, bc, rb, M, K, N, 8, 128, 16, return_c=True)
+        assert _bits_eq(got["c"], Cw), "C with ones for a mis-sized scale array differs"
+
+
 def test_qgemm_int4_tiny_scales(qa):
     """The int4 loop folds the code unpacking's factor 256 into A's scales
     (SA * 2^-8) when that is exact; scales below 2^-118 whose low bits the
