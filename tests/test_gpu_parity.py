@@ -434,7 +434,8 @@ def test_qgemm_large_tiles_scale_counts(qa, dtype):
         _large_gemm_vs_oracle(qa, dtype, M, K, N, pa, a_s, pb, b_s, rows)
 
 
-SMALL_GEMM_SHAPES = [(40, 384, 48), (16, 1024, 16), (64, 1152, 96), (1, 128, 32), (72, 256, 4080), (300, 512, 208)]
+SMALL_GEMM_SHAPES = [(40, 384, 48), (16, 1024, 16), (64, 1152, 96), (1, 128, 32), (72, 256, 4080), (300, 512, 208),
+                     (40, 384, 256), (300, 1152, 384), (1, 128, 128)]
 
 
 @pytest.mark.parametrize("shape", SMALL_GEMM_SHAPES, ids=lambda s: "x".join(map(str, s)))
@@ -443,7 +444,8 @@ def test_qgemm_small_tiles(qa, shape):
     K blocks round-robin over 4 waves (9 blocks: a short last round), M and
     N tails inside a tile, N below the tile; C, the int32 accumulators (all
     three kernel variants) and the int16d requantization bitwise against the
-    oracle, then scale arrays of the wrong length as ones."""
+    oracle (with and without C and the accumulators), then scale arrays of
+    the wrong length as ones."""
     M, K, N = shape
     dt = qa.get_mx_dtype("int8d")
     A = _randn((M, K), 401 + M)
@@ -465,6 +467,9 @@ def test_qgemm_small_tiles(qa, shape):
     assert _bits_eq(c_only["c"], C)
     assert _bits_eq(res["packed"], orc.pack_auto(codes, 16))
     assert _bits_eq(res["scales"], scales)
+    pk_only = qa.ops.qscale_gemm(pa, sa, pb, sb, M, K, N, 8, 128, 16)
+    assert _bits_eq(pk_only["packed"], orc.pack_auto(codes, 16))
+    assert _bits_eq(pk_only["scales"], scales)
     for a_s, b_s in ((sa[:-1], sb), (sa, sb[:-1]), (sa[:-1], sb[:-1])):
         got = qa.ops.qscale_gemm(pa, a_s, pb, b_s, M, K, N, 8, 128, 16, want_packed=False, want_c=True)
         ra = rsa[:-1] if a_s.numel() < sa.numel() else rsa
