@@ -36,7 +36,7 @@
 extern "C" {
 #endif
 
-#define MXK_ABI_VERSION 8
+#define MXK_ABI_VERSION 9
 
 typedef enum {
   MXK_OK = 0,
@@ -336,16 +336,26 @@ size_t mxk_linear_nt_workspace(int64_t M, int64_t K, int64_t N, int bits, int bl
 int mxk_linear_prepack_weight_nt(const void* w_packed, int64_t N, int64_t K, int bits, int block, void* w_tiled,
                                  void* stream);
 
+/* The inverse of mxk_linear_prepack_weight_nt: w_packed receives the N*K/2
+ * bytes of the [N][K] packing back from the tiled copy (a caller may keep
+ * the tiled copy only).  No reference counterpart.  Same arguments and
+ * alignment as mxk_linear_prepack_weight_nt. */
+int mxk_linear_unpack_weight_nt(const void* w_tiled, int64_t N, int64_t K, int bits, int block, void* w_packed,
+                                void* stream);
+
 /* mx_dynamic_linear.forward (mxtorch.py:8949-8962) for int4 weights, block
  * 128, from the prepacked copies: out[M,N] = x[M,K] @ dequant(W)^T (+ bias),
  * the product of mxk_linear_wq_nt's decode path, float32 accumulation in
  * another order.  w_tiled = mxk_linear_prepack_weight_nt(), w_scales_t =
  * the K-block-major scales [K/128][N] (mxk_linear_prepack_scales(w_scales,
- * N, K, 128, w_scales_t)).  Takes M <= 16, K and N multiples of 128, 16-byte
- * aligned x, w_tiled, w_scales_t, bias and out; other shapes return
- * MXK_EUNSUPPORTED (call mxk_linear_wq_nt).  workspace: as for
- * mxk_linear_wq_nt (mxk_linear_nt_workspace() bytes, zero-filled before
- * first use, left ready for the next call; calls sharing it must not
+ * N, K, 128, w_scales_t)).  K and N multiples of 128, 16-byte aligned
+ * w_tiled, w_scales_t, bias and out.  M <= 16 with 16-byte aligned x runs
+ * the tiled decode kernel; any other M runs the MFMA kernel on the same
+ * tiled copy (the product of mxk_linear_wq_nt's MFMA path), so a weight may
+ * be held as its tiled copy only.  Shapes neither takes return
+ * MXK_EUNSUPPORTED (call mxk_linear_wq_nt on the packed codes).  workspace:
+ * as for mxk_linear_wq_nt (mxk_linear_nt_workspace() bytes, zero-filled
+ * before first use, left ready for the next call; calls sharing it must not
  * overlap). */
 int mxk_linear_wq_nt_tiled(const void* x, int x_type, int64_t M, int64_t K, const void* w_tiled,
                            const float* w_scales_t, int64_t N, const float* bias, float* out, void* workspace,

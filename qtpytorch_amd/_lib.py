@@ -20,7 +20,7 @@ MXK_IN_F32, MXK_IN_F16, MXK_IN_BF16 = 0, 1, 2
 MXK_KIND_INT, MXK_KIND_FLOAT = 0, 1
 MXK_VAR_BASE, MXK_VAR_HADAMARD, MXK_VAR_VECTOR = 0, 1, 2
 MXK_DYN_PER_TOKEN, MXK_DYN_PER_CHANNEL, MXK_DYN_PER_TENSOR = 0, 1, 2
-ABI_VERSION = 8
+ABI_VERSION = 9
 
 _lock = threading.Lock()
 _lib = None
@@ -66,6 +66,7 @@ SIGNATURES = {
                                  c_int, c_vp, c_vp, c_vp, c_sz, c_vp]),
     "mxk_linear_nt_workspace": (c_sz, [c_i64, c_i64, c_i64, c_int, c_int]),
     "mxk_linear_prepack_weight_nt": (c_int, [c_vp, c_i64, c_i64, c_int, c_int, c_vp, c_vp]),
+    "mxk_linear_unpack_weight_nt": (c_int, [c_vp, c_i64, c_i64, c_int, c_int, c_vp, c_vp]),
     "mxk_linear_wq_nt_tiled": (c_int, [c_vp, c_int, c_i64, c_i64, c_vp, c_vp, c_i64, c_vp, c_vp, c_vp, c_sz, c_vp]),
     "mxk_linear_i8_workspace": (c_sz, [c_i64, c_i64, c_i64, c_int, c_int, c_i64, c_i64]),
     "mxk_linear_i8": (c_int, [c_vp, c_i64, c_vp, c_i64, c_i64, c_int, c_vp, c_i64, c_vp, c_i64, c_i64, c_int,

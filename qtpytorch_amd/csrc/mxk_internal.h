@@ -522,6 +522,11 @@ int linear_mfma_kn_tiled(const void* x, int x_type, int64_t M, int64_t K, const 
 int linear_mfma_nk(const void* x, int x_type, int64_t M, int64_t K, const void* w_packed, const float* w_scales,
                    const float* w_scales_t, int64_t N, int kind, int bits, int block, const float* bias, float* out,
                    void* workspace, size_t workspace_nbytes, hipStream_t st);
+// [N][K] int4 weights as their tiled copy (k_tile_w4t's layout) with
+// K-block-major scales [K/128][N]: the MFMA path of mxk_linear_wq_nt_tiled
+int linear_mfma_nk_tiled(const void* x, int x_type, int64_t M, int64_t K, const void* w_tiled,
+                         const float* w_scales_t, int64_t N, const float* bias, float* out, void* workspace,
+                         size_t workspace_nbytes, hipStream_t st);
 
 // 'v'-rule requantization of a float32 buffer (GEMM outputs), mxtorch.py:1372-1385.
 int requant_vec_f32(const float* x, int64_t n, int bits, int block, void* packed, int64_t packed_nbytes,

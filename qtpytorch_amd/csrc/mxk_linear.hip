@@ -1487,6 +1487,36 @@ __global__ __launch_bounds__(256) void k_tile_w4t(const u32x4v* __restrict__ w, 
   wt[u] = o;
 }
 
+// The inverse of k_tile_w4t: the packed [N][K] codes of a tiled copy.  Code
+// c = 8 st + i of a unit sits in word 2 (c >> 4) + (i >> 2), byte
+// {0, 2, 1, 3}[i & 3] (the order is its own inverse), nibble (c >> 3) & 1.
+// One thread per 16-byte unit.
+__global__ __launch_bounds__(256) void k_untile_w4t(const u32x4v* __restrict__ wt, int64_t K, int64_t N,
+                                                    u32x4v* __restrict__ w) {
+  const int64_t u = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int64_t KB = K / 128;
+  if (u >= N * K / 32) return;
+  const int64_t nt = u / (KB * 64), rem = u % (KB * 64);
+  const int64_t kb = rem / 64;
+  const int l = (int)(rem % 64);
+  const int64_t n = 16 * nt + (l & 15);
+  const u32x4v t = wt[u];
+  constexpr int ord[4] = {0, 2, 1, 3};
+  auto code = [&](int c) -> uint32_t {
+    const int i = c & 7;
+    return (t[2 * (c >> 4) + (i >> 2)] >> (8 * ord[i & 3] + 4 * ((c >> 3) & 1))) & 0xFu;
+  };
+  u32x4v o;
+#pragma unroll
+  for (int wd = 0; wd < 4; ++wd) {
+    uint32_t word = 0u;
+#pragma unroll
+    for (int b = 0; b < 4; ++b) word |= (code(8 * wd + 2 * b) | (code(8 * wd + 2 * b + 1) << 4)) << (8 * b);
+    o[wd] = word;
+  }
+  w[(n * (K / 2) + kb * 64 + 16 * (l >> 4)) / 16] = o;
+}
+
 static int nt_splits(int64_t K) { return (int)ceil_div(K / 128, NT_BLKS); }
 
 static bool nt_decode_eligible(int64_t M, int64_t K, int64_t N, int kind, int bits, int block, const void* x,
@@ -2021,6 +2051,21 @@ int mxk_linear_prepack_weight_nt(const void* w_packed, int64_t N, int64_t K, int
   return check_launch("linear_prepack_weight_nt");
 }
 
+int mxk_linear_unpack_weight_nt(const void* w_tiled, int64_t N, int64_t K, int bits, int block, void* w_packed,
+                                void* stream) {
+  if (!w_packed || !w_tiled) return fail(MXK_EINVAL, "linear_unpack_weight_nt: null pointer");
+  if (bits != 4 || block != 128 || K <= 0 || N <= 0 || K % 128 != 0 || N % 128 != 0)
+    return fail(MXK_EINVAL, "linear_unpack_weight_nt: needs int4 codes, block 128, K and N multiples of 128");
+  if (!aligned16(w_packed) || !aligned16(w_tiled))
+    return fail(MXK_EINVAL, "linear_unpack_weight_nt: w_packed and w_tiled must be 16-byte aligned");
+  const int64_t units = N * K / 32;
+  if (ceil_div(units, 256) >= (int64_t(1) << 31)) return fail(MXK_EUNSUPPORTED, "linear_unpack_weight_nt: too large");
+  hipLaunchKernelGGL(k_untile_w4t, dim3((unsigned)ceil_div(units, 256)), dim3(256), 0,
+                     reinterpret_cast<hipStream_t>(stream), reinterpret_cast<const u32x4v*>(w_tiled), K, N,
+                     reinterpret_cast<u32x4v*>(w_packed));
+  return check_launch("linear_unpack_weight_nt");
+}
+
 int mxk_linear_wq_nt_tiled(const void* x, int x_type, int64_t M, int64_t K, const void* w_tiled,
                            const float* w_scales_t, int64_t N, const float* bias, float* out, void* workspace,
                            size_t workspace_nbytes, void* stream) {
@@ -2033,10 +2078,17 @@ int mxk_linear_wq_nt_tiled(const void* x, int x_type, int64_t M, int64_t K, cons
     return fail(MXK_EINVAL, "linear_wq_nt_tiled: bias and out must be 16-byte aligned");
   const int esz = x_type == MXK_IN_F32 ? 4 : 2;
   const int64_t lim = int64_t(1) << 31;
-  if (M > 16 || K % 128 != 0 || N % 128 != 0 || !nt_long_eligible(K, N) || !aligned16(x) || !aligned16(w_tiled) ||
-      !aligned16(w_scales_t) || N * K / 2 >= lim || N * (K / 128) * 4 >= lim || 16 * K * esz >= lim)
-    return fail(MXK_EUNSUPPORTED, "linear_wq_nt_tiled: needs M <= 16, K and N multiples of 128, 16-byte aligned "
-                                  "x, w_tiled and w_scales_t (use mxk_linear_wq_nt)");
+  if (K % 128 != 0 || N % 128 != 0 || !aligned16(w_tiled) || !aligned16(w_scales_t))
+    return fail(MXK_EUNSUPPORTED, "linear_wq_nt_tiled: needs K and N multiples of 128 and 16-byte aligned w_tiled "
+                                  "and w_scales_t (use mxk_linear_wq_nt)");
+  if (M > 16 || !nt_long_eligible(K, N) || !aligned16(x) || N * K / 2 >= lim || N * (K / 128) * 4 >= lim ||
+      16 * K * esz >= lim) {
+    // the other shapes: the MFMA kernel on the same tiled copy
+    const int rc = linear_mfma_nk_tiled(x, x_type, M, K, w_tiled, w_scales_t, N, bias, out, workspace,
+                                        workspace_nbytes, st);
+    if (rc != MXK_EUNSUPPORTED) return rc;
+    return fail(MXK_EUNSUPPORTED, "linear_wq_nt_tiled: shape not supported on the tiled copy (use mxk_linear_wq_nt)");
+  }
   const size_t need = nt_workspace_bytes(K, N);
   if (nt_long_splits(K) > 1 && (!workspace || workspace_nbytes < need))
     return fail(MXK_EINVAL, "linear_wq_nt_tiled: needs a zero-initialised workspace of mxk_linear_nt_workspace() bytes");

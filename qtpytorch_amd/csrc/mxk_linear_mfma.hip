@@ -273,6 +273,42 @@ __device__ __forceinline__ void nk_store(const NkCodes<BITS>& c, uint8_t* sB, in
   }
 }
 
+// [N][K] int4 codes from the tiled copy of k_tile_w4t: the 16-byte unit of
+// row n and K segment k .. k + 31 (k = 32 q within a block of 128) sits at
+// ((n / 16) * K/128 + k / 128) * 1024 + 16 * (n % 16 + 16 * (k % 128) / 32),
+// and word 2 sp + h, byte b of a unit holds the codes (8 st + i) with
+// st = 2 sp (low nibble) and 2 sp + 1 (high nibble), i = 4 h + {0, 2, 1, 3}[b].
+__device__ __forceinline__ void nk_load_tiled(NkCodes<4>& c, __amdgpu_buffer_rsrc_t rw, int64_t k0, int64_t K,
+                                              int64_t nb, int tid) {
+  const int q = tid & 7;
+  const int64_t k = k0 + 32 * q, KB = K / 128;
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int64_t n = nb * 128 + nk4_col((tid >> 3) + 64 * h);
+    c.w[h] = buf_load_b128(rw, (uint32_t)(((n >> 4) * KB + (k >> 7)) * 1024 + 16 * ((n & 15) + 16 * ((k >> 5) & 3))),
+                           0u);
+  }
+}
+
+// nk_store's fragments from tiled units: the pair (i, i + 1) of step st is
+// (word 2 (st / 2) + i / 4) >> (8 ((i / 2) & 1) + 4 (st & 1)) under the mask
+// of lm_i4pair
+__device__ __forceinline__ void nk_store_tiled(const NkCodes<4>& c, uint8_t* sB, int tid) {
+  const int ks = tid & 7;
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int col = nk4_col((tid >> 3) + 64 * h);
+    const int t = col & 7, j = col >> 3;
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      u4v f;
+#pragma unroll
+      for (int p = 0; p < 4; ++p) f[p] = lm_i4pair(c.w[h][2 * (v >> 1) + (p >> 1)] >> (8 * (p & 1) + 4 * (v & 1)));
+      *reinterpret_cast<u4v*>(sB + lm_frag_off(ks, t, j + 16 * v)) = f;
+    }
+  }
+}
+
 // ---------------------------------------------------------------- the MFMA kernel
 // A-operand registers of one k step: [K][N] x' (2 row tiles x 8 fp32) and
 // 8 scales; [N][K] hi and lo (2 row tiles x 8 f16 each)
@@ -296,7 +332,7 @@ __global__ __launch_bounds__(LM_THREADS, 1) void k_linear_mfma(
     float* __restrict__ part) {
   constexpr int WK = 8 / WM, KPW = 8 / WK;
   using A = typename std::conditional<NK, NkA, KnA>::type;
-  static_assert(!TILED || (!NK && BITS == 4), "the tiled copy holds int4 [K][N] weights");
+  static_assert(!TILED || BITS == 4, "the tiled copies hold int4 weights");
   using Codes = typename std::conditional<NK, NkCodes<BITS>,
                                           typename std::conditional<TILED, KnTiled, KnCodes<BITS>>::type>::type;
   __shared__ __attribute__((aligned(1024))) uint8_t sB[2 * LM_STAGE_BYTES];
@@ -367,12 +403,14 @@ __global__ __launch_bounds__(LM_THREADS, 1) void k_linear_mfma(
     }
   };
   auto load_codes = [&](Codes& c, int st) {
-    if constexpr (NK) nk_load<BITS>(c, rw, (int64_t)st * LM_STAGE, K, nb, tid);
+    if constexpr (NK && TILED) nk_load_tiled(c, rw, (int64_t)st * LM_STAGE, K, nb, tid);
+    else if constexpr (NK) nk_load<BITS>(c, rw, (int64_t)st * LM_STAGE, K, nb, tid);
     else if constexpr (TILED) kn_load_tiled(c, rw, (int64_t)st * LM_STAGE, K, nb, tid);
     else kn_load<BITS>(c, rw, (int64_t)st * LM_STAGE, N, nb, tid);
   };
   auto store_codes = [&](const Codes& c, uint8_t* dst) {
-    if constexpr (NK) nk_store<BITS>(c, dst, tid);
+    if constexpr (NK && TILED) nk_store_tiled(c, dst, tid);
+    else if constexpr (NK) nk_store<BITS>(c, dst, tid);
     else if constexpr (TILED) kn_store_tiled(c, dst, tid);
     else kn_store<BITS>(c, dst, tid);
   };
@@ -943,6 +981,29 @@ int linear_mfma_nk(const void* x, int x_type, int64_t M, int64_t K, const void* 
     hipLaunchKernelGGL(k_linear_mfma_reduce, dim3((unsigned)ceil_div(M * N / 4, 256)), dim3(256), 0, st, part, p.S,
                        M, N, ex, nullptr, bias, out);
   return check_launch("linear_wq_nt(mfma)");
+}
+
+int linear_mfma_nk_tiled(const void* x, int x_type, int64_t M, int64_t K, const void* w_tiled,
+                         const float* w_scales_t, int64_t N, const float* bias, float* out, void* workspace,
+                         size_t workspace_nbytes, hipStream_t st) {
+  if (!lm_common_ok(M, K, N, MXK_KIND_INT, 4, 128, x_type, out) || K % 128 != 0) return MXK_EUNSUPPORTED;
+  if (!aligned16(w_tiled) || !w_scales_t) return MXK_EUNSUPPORTED;
+  if (N * K / 2 >= (int64_t(1) << 31) || N * (K / 128) * 4 >= (int64_t(1) << 31)) return MXK_EUNSUPPORTED;
+  const LmPlan p = lm_plan(M, K, N, true, 4);
+  if (!workspace || workspace_nbytes < p.bytes)
+    return fail(MXK_EINVAL, "linear_wq_nt_tiled: needs a workspace of mxk_linear_nt_workspace() bytes");
+  uint8_t* ws = reinterpret_cast<uint8_t*>(workspace);
+  int* ex = reinterpret_cast<int*>(ws + p.off_ex);
+  _Float16* xh = reinterpret_cast<_Float16*>(ws + p.off_x);
+  _Float16* xl = xh + (size_t)M * (size_t)p.Kp;
+  float* part = reinterpret_cast<float*>(ws + p.off_p);
+  lm_prep_rows<true>(x, x_type, M, K, p.Kp, nullptr, xh, xl, ex, st);
+  lm_launch_w<4, true, true>(p, st, nullptr, xh, xl, w_scales_t, 1, ex, nullptr,
+                             reinterpret_cast<const uint8_t*>(w_tiled), M, K, N, bias, out, part);
+  if (p.S > 1)
+    hipLaunchKernelGGL(k_linear_mfma_reduce, dim3((unsigned)ceil_div(M * N / 4, 256)), dim3(256), 0, st, part, p.S,
+                       M, N, ex, nullptr, bias, out);
+  return check_launch("linear_wq_nt_tiled(mfma)");
 }
 
 }  // namespace mxk

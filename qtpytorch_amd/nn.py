@@ -170,8 +170,9 @@ class _LinearWQNT(torch.autograd.Function):
     def forward(ctx, x, w, bias, in_features, out_features, w_scales_t, w_tiled=None):
         ctx.w, ctx.w_scales_t = w, w_scales_t
         ctx.in_features, ctx.out_features = in_features, out_features
-        return ops.linear_wq_nt(x.detach(), w._mx_packed, w._mx_scales, w._mx_dtype, out_features, in_features,
-                                w._mx_block, bias=bias, w_scales_t=w_scales_t, w_tiled=w_tiled)
+        return ops.linear_wq_nt(x.detach(), w._mx_packed if w_tiled is None else None, w._mx_scales, w._mx_dtype,
+                                out_features, in_features, w._mx_block, bias=bias, w_scales_t=w_scales_t,
+                                w_tiled=w_tiled)
 
     @staticmethod
     def backward(ctx, grad):
@@ -228,7 +229,7 @@ class mx_dynamic_linear(nn.Module):
         w = self.weight
         if not isinstance(w, mx_tensor):
             w = mx_tensor.quantize(w, self.weight_dtype, self.weight_block)
-        if w._mx_packed.device != x_f.device:
+        if w._mx_storage().device != x_f.device:
             w = w._move_device(x_f.device)
             self.weight = w
         b = self.bias
@@ -239,32 +240,25 @@ class mx_dynamic_linear(nn.Module):
             out = out.reshape(*x_f.shape[:-1], self.out_features)
             return out + b if b is not None else out
         st = self._block_major_scales(w)
-        rows = x_f.numel() // max(self.in_features, 1)
-        wt = self._decode_weight(w) if rows <= 16 else None
+        wt = self._tiled_weight(w)
         if torch.is_grad_enabled() and x_f.requires_grad:
             return _LinearWQNT.apply(x_f, w, b, self.in_features, self.out_features, st, wt)
-        return ops.linear_wq_nt(x_f, w._mx_packed, w._mx_scales, w._mx_dtype, self.out_features, self.in_features,
-                                w._mx_block, bias=b, w_scales_t=st, w_tiled=wt)
+        return ops.linear_wq_nt(x_f, w._mx_packed if wt is None else None, w._mx_scales, w._mx_dtype,
+                                self.out_features, self.in_features, w._mx_block, bias=b, w_scales_t=st, w_tiled=wt)
 
-    # Whether decode-shaped forwards (at most 16 rows of x) keep a tiled copy
-    # of an int4 weight's packed codes (in*out/2 bytes, made on the first
-    # such forward) for the faster decode kernel; False saves that memory.
+    # Whether an eligible int4 weight is held as its tiled copy (made on the
+    # first forward, any row count; the packed bytes are then freed and
+    # rebuilt on demand), which the decode and MFMA kernels read; False keeps
+    # the packed codes and runs the kernels that read them.
     tiled_decode = True
 
-    def _decode_weight(self, w) -> Optional[Tensor]:
-        """Tiled copy of the packed int4 [out, in] weight for the decode
-        kernel, made once per weight tensor and rebuilt when the packed codes
-        are replaced or modified in place."""
+    def _tiled_weight(self, w) -> Optional[Tensor]:
+        """The tiled copy the weight is held as (one copy of its codes), or
+        None when the weight keeps its packed codes."""
         if not self.tiled_decode or not ops.decode_prepack_nt_eligible(w._mx_dtype, w._mx_block, self.in_features,
                                                                       self.out_features):
             return None
-        pk = w._mx_packed
-        key = (pk.data_ptr(), str(pk.device), pk._version)
-        cached = self.__dict__.get("_w_tiled_cache")
-        if cached is None or cached[0] != key:
-            cached = (key, ops.prepack_weight_nt(pk, self.out_features, self.in_features, w._mx_block))
-            self.__dict__["_w_tiled_cache"] = cached
-        return cached[1]
+        return w._mx_tile_(self.in_features, self.out_features, "nt")
 
     def _block_major_scales(self, w) -> Optional[Tensor]:
         """K-block-major copy [in/128, out] of the [out, in] weight's scales,

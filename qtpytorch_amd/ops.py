@@ -582,9 +582,25 @@ def prepack_weight_nt(w_packed: Tensor, out_features: int, in_features: int, blo
     return out
 
 
-def linear_wq_nt(x: Tensor, w_packed: Tensor, w_scales: Tensor, dt, out_features: int, in_features: int,
-                 block: int = 128, bias: Optional[Tensor] = None, w_scales_t: Optional[Tensor] = None,
-                 w_tiled: Optional[Tensor] = None) -> Tensor:
+def unpack_weight_nt(w_tiled: Tensor, out_features: int, in_features: int, block: int = 128) -> Tensor:
+    """The packed int4 [out, in] codes (uint8, out*in/2 bytes) rebuilt from
+    their tiled copy (mxk_linear_unpack_weight_nt), the inverse of
+    prepack_weight_nt."""
+    dev = L.require_gpu(w_tiled)
+    N, K = out_features, in_features
+    if w_tiled.numel() * w_tiled.element_size() != K * N // 2:
+        raise L.MXKError(f"unpack_weight_nt: {w_tiled.numel()} bytes for a {N}x{K} int4 weight")
+    out = torch.empty(K * N // 2, dtype=torch.uint8, device=dev)
+    with torch.cuda.device(dev):
+        rc = L.lib().mxk_linear_unpack_weight_nt(w_tiled.data_ptr(), N, K, 4, block, out.data_ptr(),
+                                                  L.stream_of(w_tiled))
+    L.check(rc, f"unpack_weight_nt({N}x{K})")
+    return out
+
+
+def linear_wq_nt(x: Tensor, w_packed: Optional[Tensor], w_scales: Tensor, dt, out_features: int,
+                 in_features: int, block: int = 128, bias: Optional[Tensor] = None,
+                 w_scales_t: Optional[Tensor] = None, w_tiled: Optional[Tensor] = None) -> Tensor:
     """y = x.float() @ dequant(W).t() (+ bias) for a weight stored [out, in]
     (mx_dynamic_linear.forward, mxtorch.py:8949-8962, and the input gradient
     of _MXLinearAutograd, mxtorch.py:6729-6740); the weight is decoded in
@@ -592,9 +608,14 @@ def linear_wq_nt(x: Tensor, w_packed: Tensor, w_scales: Tensor, dt, out_features
     K-block-major copy [in/128, out] of the scales (prepack_scales(w_scales,
     out, in)), read by the int4 decode path.  With `w_tiled`
     (prepack_weight_nt()) and `w_scales_t` as well, the int4 decode shapes
-    run the tiled kernel (mxk_linear_wq_nt_tiled)."""
+    run the tiled decode kernel and the other shapes the MFMA kernel on the
+    same tiled copy (mxk_linear_wq_nt_tiled); `w_packed` may then be None (a
+    weight held as its tiled copy only), and shapes the tiled entry point does
+    not take rebuild the packed codes for one call."""
     dt = get_mx_dtype(dt)
-    dev = L.require_gpu(x, w_packed, w_scales)
+    if w_packed is None and w_tiled is None:
+        raise L.MXKError("linear_wq_nt: needs the packed codes or their tiled copy")
+    dev = L.require_gpu(x, w_packed if w_packed is not None else w_tiled, w_scales)
     kind, var = _kind_variant(dt)
     if var != L.MXK_VAR_BASE:
         raise L.MXKError(f"linear_wq_nt: {dt.name} weights need the base variant")
@@ -616,7 +637,7 @@ def linear_wq_nt(x: Tensor, w_packed: Tensor, w_scales: Tensor, dt, out_features
             out += bias.to(device=dev, dtype=torch.float32)
         return out.reshape(*lead, N)
     b = None if bias is None else bias.to(device=dev, dtype=torch.float32).contiguous()
-    wp, ws = w_packed.contiguous(), w_scales.contiguous().float()
+    ws = w_scales.contiguous().float()
     if w_scales_t is not None:
         if (w_scales_t.device != dev or w_scales_t.dtype != torch.float32 or not w_scales_t.is_contiguous()
                 or w_scales_t.numel() != ws.numel()):
@@ -632,13 +653,13 @@ def linear_wq_nt(x: Tensor, w_packed: Tensor, w_scales: Tensor, dt, out_features
     wk = _zeroed_workspace(ws_bytes, dev, stream)
     with torch.cuda.device(dev):
         rc = L.MXK_EUNSUPPORTED
-        if (w_tiled is not None and w_scales_t is not None and decode_prepack_nt_eligible(dt, block, K, N)
-                and M <= 16 and xc.data_ptr() % 16 == 0):
+        if w_tiled is not None and w_scales_t is not None and decode_prepack_nt_eligible(dt, block, K, N):
             bt = b if b is None or b.data_ptr() % 16 == 0 else b.clone()
             rc = lib.mxk_linear_wq_nt_tiled(xc.data_ptr(), L.elem_type(xc.dtype), M, K, w_tiled.data_ptr(),
                                             w_scales_t.data_ptr(), N, L.ptr(bt), out.data_ptr(), L.ptr(wk), ws_bytes,
                                             stream)
         if rc == L.MXK_EUNSUPPORTED:
+            wp = (w_packed if w_packed is not None else unpack_weight_nt(w_tiled, N, K, block)).contiguous()
             rc = lib.mxk_linear_wq_nt(xc.data_ptr(), L.elem_type(xc.dtype), M, K, wp.data_ptr(),
                                       wp.numel() * wp.element_size(), ws.data_ptr(), ws.numel(), L.ptr(w_scales_t),
                                       N, kind, dt.bits, block, L.ptr(b), out.data_ptr(), L.ptr(wk), ws_bytes, stream)

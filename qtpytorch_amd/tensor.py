@@ -74,16 +74,19 @@ class mx_tensor(torch.Tensor):
     def __init__(self, packed, scales, mx_dtype, orig_shape, n, block=128, requires_grad=False, seed=None):
         pass
 
-    # ---- code storage: the packed codes, or, for an int4 [in, out] weight
-    # that mx_linear tiles, the tiled copy its kernels read and nothing else
-    # (one copy of the weight); the packed codes are then rebuilt on demand
-    # (ops.unpack_weight) for whatever else reads them.
+    # ---- code storage: the packed codes, or, for an int4 weight that
+    # mx_linear ([in, out]) or mx_dynamic_linear ([out, in]) tiles, the tiled
+    # copy its kernels read and nothing else (one copy of the weight); the
+    # packed codes are then rebuilt on demand (ops.unpack_weight /
+    # ops.unpack_weight_nt) for whatever else reads them.
     @property
     def _mx_packed(self) -> Tensor:
         d = self.__dict__
         t = d.get("_mx_tiled")
         if t is not None:
-            K, N, dtype = d["_mx_tiled_meta"]
+            K, N, dtype, layout = d["_mx_tiled_meta"]
+            if layout == "nt":
+                return ops.unpack_weight_nt(t, N, K, self._mx_block).view(dtype)
             return ops.unpack_weight(t, K, N, self._mx_block).view(dtype)
         return d["_mx_packed_store"]
 
@@ -97,15 +100,24 @@ class mx_tensor(torch.Tensor):
         t = self.__dict__.get("_mx_tiled")
         return t if t is not None else self.__dict__["_mx_packed_store"]
 
-    def _mx_tile_(self, in_features: int, out_features: int) -> Tensor:
-        """Hold the codes of this int4 [in, out] weight as their tiled copy
-        only (ops.prepack_weight) and return it; the packed bytes are freed."""
+    def _mx_tile_(self, in_features: int, out_features: int, layout: str = "kn") -> Tensor:
+        """Hold the codes of this int4 weight as their tiled copy only and
+        return it; the packed bytes are freed.  layout "kn": an [in, out]
+        weight (mx_linear, ops.prepack_weight); "nt": an [out, in] weight
+        (mx_dynamic_linear, ops.prepack_weight_nt)."""
         d = self.__dict__
-        if d.get("_mx_tiled") is None:
-            pk = d["_mx_packed_store"]
-            d["_mx_tiled_meta"] = (int(in_features), int(out_features), pk.dtype)
+        t = d.get("_mx_tiled")
+        if t is not None:
+            if d["_mx_tiled_meta"][3] != layout:
+                raise ValueError(f"mx_tensor: the codes are tiled as {d['_mx_tiled_meta'][3]!r}, not {layout!r}")
+            return t
+        pk = d["_mx_packed_store"]
+        d["_mx_tiled_meta"] = (int(in_features), int(out_features), pk.dtype, layout)
+        if layout == "nt":
+            d["_mx_tiled"] = ops.prepack_weight_nt(pk, out_features, in_features, self._mx_block)
+        else:
             d["_mx_tiled"] = ops.prepack_weight(pk, in_features, out_features, self._mx_block)
-            d["_mx_packed_store"] = None
+        d["_mx_packed_store"] = None
         return d["_mx_tiled"]
 
     def _mx_untile_(self) -> "mx_tensor":

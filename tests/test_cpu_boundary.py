@@ -126,8 +126,15 @@ def test_bad_arguments_return_errors_without_gpu():
     assert rc == -22
     rc = h.mxk_linear_wq_nt_tiled(16, 0, 16, 256, 16, 16, 256, 8, 16, None, 0, None)     # misaligned bias
     assert rc == -22
-    rc = h.mxk_linear_wq_nt_tiled(16, 0, 17, 256, 16, 16, 256, None, 16, None, 0, None)  # M > 16
-    assert rc == -95
+    # M > 16 runs the MFMA path on the tiled copy, which needs its workspace
+    rc = h.mxk_linear_wq_nt_tiled(16, 0, 17, 256, 16, 16, 256, None, 16, None, 0, None)
+    assert rc == -22 and b"workspace" in h.mxk_last_error()
+    rc = h.mxk_linear_unpack_weight_nt(None, 256, 256, 4, 128, 16, None)
+    assert rc == -22 and b"null" in h.mxk_last_error()
+    rc = h.mxk_linear_unpack_weight_nt(16, 256, 192, 4, 128, 16, None)   # K not a multiple of 128
+    assert rc == -22
+    rc = h.mxk_linear_unpack_weight_nt(16, 256, 256, 4, 128, 8, None)    # w_packed not 16-byte aligned
+    assert rc == -22
     rc = h.mxk_linear_wq_nt_tiled(16, 0, 16, 192, 16, 16, 256, None, 16, None, 0, None)  # K % 128
     assert rc == -95
     rc = h.mxk_linear_wq_nt_tiled(16, 0, 16, 256, 16, 16, 200, None, 16, None, 0, None)  # N % 128

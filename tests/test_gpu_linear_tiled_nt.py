@@ -14,8 +14,10 @@ kernel mxk_linear_wq_nt runs on the weight as stored for the same shapes.
     same bar;
   * two streams at once, each with its own workspace, give the results of
     the calls alone, bit for bit;
-  * mx_dynamic_linear keeps one tiled copy and rebuilds it when the codes
-    change; shapes the tiled kernel does not take fall back.
+  * mx_dynamic_linear holds an int4 weight as its tiled copy only (the
+    packed codes rebuilt on demand, bit for bit), more than 16 rows run the
+    MFMA kernel on the tiled copy (bitwise equal to the packed-code MFMA
+    kernel); shapes the tiled kernels do not take fall back.
 """
 import numpy as np
 import pytest
@@ -172,29 +174,77 @@ def test_tiled_nt_two_streams_concurrently(qa):
 
 
 def test_mx_dynamic_linear_keeps_one_tiled_copy(qa):
-    """mx_dynamic_linear makes the tiled copy on the first decode-shaped
-    forward, reuses it, rebuilds it when the packed codes change, and skips it
-    for more than 16 rows or with tiled_decode = False."""
+    """mx_dynamic_linear holds an eligible int4 weight as its tiled copy only,
+    from the first forward (any row count) on: one copy of the weight's
+    bytes.  The packed codes come back bit for bit on demand (dequantize,
+    state_dict), the decode and MFMA kernels read the tiled copy, an in-place
+    copy_ turns the weight back to packed storage (and the next forward tiles
+    the new codes), the input gradient matches the oracle's, and
+    tiled_decode = False keeps the packed codes."""
     K, N = 1024, 256
     lin = torch.nn.Linear(K, N, bias=True)
     m = qa.mx_dynamic_linear.from_linear(lin.to(dev()), "int4d", "int8d")
-    x = torch.randn(4, K, device=dev())
-    y0 = m(x)
-    c0 = m.__dict__["_w_tiled_cache"][1]
-    y1 = m(x)
-    assert m.__dict__["_w_tiled_cache"][1] is c0 and G.bits_equal(y0.cpu(), y1.cpu())
     wp, ws, _ = orc.dynamic_linear_from_weight(lin.weight.data.cpu(), "int4d", 128)
-    ref = orc.dynamic_linear_forward(x.cpu(), wp, ws, "int4d", K, N, 128, lin.bias.data.cpu())
-    assert _rowwise_ok(y0.cpu(), ref)[0]
-    m.weight._mx_packed.bitwise_xor_(torch.tensor(0x11, dtype=torch.int8, device=dev()))
-    m(x)
-    assert m.__dict__["_w_tiled_cache"][1] is not c0
-    m2 = qa.mx_dynamic_linear.from_linear(lin.to(dev()), "int4d", "int8d")
-    m2(torch.randn(32, K, device=dev()))
-    assert "_w_tiled_cache" not in m2.__dict__
-    m2.tiled_decode = False
-    m2(x)
-    assert "_w_tiled_cache" not in m2.__dict__
+    bias = lin.bias.data.cpu()
+    w = m.weight
+    for M in (4, 40):
+        x = _randn((M, K), 171 + M).to(dev())
+        y = m(x).cpu()
+        assert w.__dict__["_mx_tiled"] is not None and w.__dict__["_mx_packed_store"] is None
+        assert _rowwise_ok(y, orc.dynamic_linear_forward(x.cpu(), wp, ws, "int4d", K, N, 128, bias))[0]
+    assert w.nbytes_packed == K * N // 2 + ws.numel() * 4          # one copy of the codes
+    assert G.bits_equal(w._mx_packed.cpu(), wp)                       # rebuilt on demand
+    assert w._mx_packed.dtype == wp.dtype
+    assert G.bits_equal(w.dequantize().cpu().reshape(-1), orc.dequant(wp, ws, "int4d", K * N, 128))
+    # the input gradient (the [in, out] product on the rebuilt codes)
+    x = _randn((24, K), 181).to(dev()).requires_grad_(True)
+    g = _randn((24, N), 183).to(dev())
+    m(x).backward(g)
+    gi_ref = g.cpu() @ orc.dequant(wp, ws, "int4d", K * N, 128).reshape(N, K)
+    assert _rowwise_ok(x.grad.cpu(), gi_ref)[0]
+    sd = {k: v for k, v in m.state_dict().items()}
+    m2 = qa.mx_dynamic_linear.from_linear(torch.nn.Linear(K, N, bias=True).to(dev()), "int4d", "int8d")
+    m2.load_state_dict(sd)
+    x = _randn((9, K), 185).to(dev())
+    assert G.bits_equal(m2(x).cpu(), m(x).cpu())
+    # an in-place change of the codes
+    W2 = _randn((N, K), 187) * 0.03
+    q2 = qa.mx_tensor.quantize(W2.to(dev()), qa.get_mx_dtype("int4d"), 128)
+    w.copy_(q2)
+    assert w.__dict__["_mx_tiled"] is None
+    wp2, ws2, _ = orc.dynamic_linear_from_weight(W2, "int4d", 128)
+    y2 = m(x).cpu()
+    assert w.__dict__["_mx_tiled"] is not None
+    assert _rowwise_ok(y2, orc.dynamic_linear_forward(x.cpu(), wp2, ws2, "int4d", K, N, 128, bias))[0]
+    m3 = qa.mx_dynamic_linear.from_linear(lin.to(dev()), "int4d", "int8d")
+    m3.tiled_decode = False
+    m3(x)
+    assert m3.weight.__dict__.get("_mx_tiled") is None
+
+
+@pytest.mark.parametrize("N,K", [(128, 128), (384, 2176), (1024, 4096)])
+def test_unpack_weight_nt_inverts_prepack(qa, N, K):
+    """unpack_weight_nt(prepack_weight_nt(p)) == p byte for byte."""
+    wp, ws, wpg, wsg, st, wt = _weights(qa, N, K, 191 + N)
+    assert G.bits_equal(qa.ops.unpack_weight_nt(wt, N, K, 128).cpu(), wp.view(torch.uint8))
+
+
+@pytest.mark.parametrize("M", [17, 64, 300])
+@pytest.mark.parametrize("xdt", [torch.float32, torch.bfloat16])
+def test_tiled_nt_mfma_vs_oracle(qa, M, xdt):
+    """More than 16 rows on the tiled copy alone (w_packed None): the MFMA
+    kernel reading the tiled [N][K] layout, within the bar of the oracle, and
+    equal to the MFMA kernel on the packed codes bit for bit."""
+    N, K = 384, 2176
+    wp, ws, wpg, wsg, st, wt = _weights(qa, N, K, 193 + M)
+    x = _randn((M, K), 197 + M).to(xdt)
+    b = _randn((N,), 199)
+    y = qa.ops.linear_wq_nt(x.to(dev()), None, wsg, "int4d", N, K, 128, bias=b.to(dev()), w_scales_t=st,
+                            w_tiled=wt).cpu()
+    ok, worst = _rowwise_ok(y, orc.dynamic_linear_forward(x.float(), wp, ws, "int4d", K, N, 128, b))
+    assert ok, f"worst row error {worst:.3g} x the bar"
+    y_packed = qa.ops.linear_wq_nt(x.to(dev()), wpg, wsg, "int4d", N, K, 128, bias=b.to(dev()), w_scales_t=st).cpu()
+    assert G.bits_equal(y, y_packed)
 
 
 def test_tiled_nt_fallback_for_other_shapes(qa):
