@@ -309,6 +309,18 @@ __device__ __forceinline__ void nk_store_tiled(const NkCodes<4>& c, uint8_t* sB,
   }
 }
 
+// x' (and its f16 hi / lo) in HBM as tiles of 16 rows x 8 columns of K,
+// tile (m / 16, k / 8) at element ((m / 16) * Kp/8 + k / 8) * 128 and
+// element (m % 16) * 8 + k % 8 inside it, so that the 64 lanes of an A
+// operand load (rows j of a row tile, columns 8 g .. 8 g + 7 of a k step)
+// read one contiguous 2 KiB (fp32) or 1 KiB (f16): with x' row-major the 16
+// rows of one load are Kp elements apart and land on one memory channel.
+__host__ __device__ __forceinline__ int64_t lm_xoff(int64_t m, int64_t k, int64_t Kp) {
+  return ((m >> 4) * (Kp >> 3) + (k >> 3)) * 128 + (m & 15) * 8 + (k & 7);
+}
+// rows of x' the tiled layout holds (whole row tiles)
+__host__ __device__ __forceinline__ int64_t lm_rows16(int64_t M) { return (M + 15) & ~(int64_t)15; }
+
 // ---------------------------------------------------------------- the MFMA kernel
 // A-operand registers of one k step: [K][N] x' (2 row tiles x 8 fp32) and
 // 8 scales; [N][K] hi and lo (2 row tiles x 8 f16 each)
@@ -345,7 +357,9 @@ __global__ __launch_bounds__(LM_THREADS, 1) void k_linear_mfma(
   const int z = blockIdx.z;
   const int nst = (int)(Kp / LM_STAGE);
   const int st0 = z * sps, st1 = min(st0 + sps, nst);
-  const int rows = (int64_t)M - m0 < 32 * WM ? (int)((int64_t)M - m0) : 32 * WM;
+  // whole row tiles: x' rows past M (within the last tile) hold anything,
+  // and only their own output rows, never stored, see them
+  const int rows = lm_rows16((int64_t)M - m0) < 32 * WM ? (int)lm_rows16((int64_t)M - m0) : 32 * WM;
   const __amdgpu_buffer_rsrc_t rw = make_rsrc(w, (uint32_t)(K * N * BITS / 8));
 
   // A-operand loads of k step (st, jj): rows 32 wm + 16 i + j, columns
@@ -388,13 +402,13 @@ __global__ __launch_bounds__(LM_THREADS, 1) void k_linear_mfma(
     const int64_t kg = (int64_t)st * LM_STAGE + 32 * (wk + WK * jj) + 8 * g;
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
-      const int64_t r = 32 * wm + 16 * i + j;
+      const int64_t at = lm_xoff(32 * wm + 16 * i + j, kg, Kp);
       if constexpr (NK) {
-        a.h[i] = buf_load_b128(ra, (uint32_t)((r * Kp + kg) * 2), 0u);
-        a.l[i] = buf_load_b128(rb, (uint32_t)((r * Kp + kg) * 2), 0u);
+        a.h[i] = buf_load_b128(ra, (uint32_t)(at * 2), 0u);
+        a.l[i] = buf_load_b128(rb, (uint32_t)(at * 2), 0u);
       } else {
-        a.x[i][0] = buf_load_b128(ra, (uint32_t)((r * Kp + kg) * 4), 0u);
-        a.x[i][1] = buf_load_b128(ra, (uint32_t)((r * Kp + kg) * 4 + 16), 0u);
+        a.x[i][0] = buf_load_b128(ra, (uint32_t)(at * 4), 0u);
+        a.x[i][1] = buf_load_b128(ra, (uint32_t)(at * 4 + 16), 0u);
       }
     }
     if constexpr (!NK) {
@@ -731,7 +745,6 @@ __global__ __launch_bounds__(256) void k_linear_mfma_prep_rows(const T* __restri
   const int be = (int)((__float_as_uint(mx) >> 23) & 0xFFu);
   const int e = (be == 0xFF || mx == 0.0f) ? 0 : 127 - (be == 0 ? 1 : be);
   if (tid == 0) ex[m] = e;
-  const int64_t base = m * Kp;
   if (cached) {
 #pragma unroll
     for (int q = 0; q < NCH; ++q) {
@@ -741,7 +754,7 @@ __global__ __launch_bounds__(256) void k_linear_mfma_prep_rows(const T* __restri
       elems(c[q], v);
 #pragma unroll
       for (int u = 0; u < E; ++u) v[u] = __builtin_ldexpf(v[u], e);
-      const int64_t at = base + ch * E;
+      const int64_t at = lm_xoff(m, ch * E, Kp);  // E <= 8 values within one 8-column group
       if constexpr (SPLIT) {
         _Float16 h[E], l[E];
 #pragma unroll
@@ -761,10 +774,10 @@ __global__ __launch_bounds__(256) void k_linear_mfma_prep_rows(const T* __restri
         for (int u = 0; u < E; u += 4) *reinterpret_cast<f4v*>(xs + at + u) = f4v{v[u], v[u + 1], v[u + 2], v[u + 3]};
       }
     }
-    for (int64_t k = K + tid; k < Kp; k += 256) lm_put<T, SPLIT>(xs, xh, xl, base + k, 0.0f);
+    for (int64_t k = K + tid; k < Kp; k += 256) lm_put<T, SPLIT>(xs, xh, xl, lm_xoff(m, k, Kp), 0.0f);
   } else {
     for (int64_t k = tid; k < Kp; k += 256)
-      lm_put<T, SPLIT>(xs, xh, xl, base + k, k < K ? __builtin_ldexpf(ElemT<T>::cvt(row[k]), e) : 0.0f);
+      lm_put<T, SPLIT>(xs, xh, xl, lm_xoff(m, k, Kp), k < K ? __builtin_ldexpf(ElemT<T>::cvt(row[k]), e) : 0.0f);
   }
 }
 
@@ -823,7 +836,7 @@ LmPlan lm_plan(int64_t M, int64_t K, int64_t N, bool nk, int bits) {
   p.off_es = o;
   o += lm_round((size_t)NB * 4);
   p.off_x = o;
-  o += lm_round((size_t)M * (size_t)p.Kp * 4);  // fp32 x', or f16 hi + lo
+  o += lm_round((size_t)lm_rows16(M) * (size_t)p.Kp * 4);  // fp32 x', or f16 hi + lo, in whole row tiles
   p.off_s = o;  // [K][N]: room for a block-major copy of the scales when the caller has none
   if (!nk) o += lm_round((size_t)NB * (size_t)K * 4);
   p.off_p = o;
@@ -969,7 +982,7 @@ int linear_mfma_nk(const void* x, int x_type, int64_t M, int64_t K, const void* 
   uint8_t* ws = reinterpret_cast<uint8_t*>(workspace);
   int* ex = reinterpret_cast<int*>(ws + p.off_ex);
   _Float16* xh = reinterpret_cast<_Float16*>(ws + p.off_x);
-  _Float16* xl = xh + (size_t)M * (size_t)p.Kp;
+  _Float16* xl = xh + (size_t)lm_rows16(M) * (size_t)p.Kp;
   float* part = reinterpret_cast<float*>(ws + p.off_p);
   lm_prep_rows<true>(x, x_type, M, K, p.Kp, nullptr, xh, xl, ex, st);
   const float* sc = w_scales_t ? w_scales_t : w_scales;
@@ -995,7 +1008,7 @@ int linear_mfma_nk_tiled(const void* x, int x_type, int64_t M, int64_t K, const 
   uint8_t* ws = reinterpret_cast<uint8_t*>(workspace);
   int* ex = reinterpret_cast<int*>(ws + p.off_ex);
   _Float16* xh = reinterpret_cast<_Float16*>(ws + p.off_x);
-  _Float16* xl = xh + (size_t)M * (size_t)p.Kp;
+  _Float16* xl = xh + (size_t)lm_rows16(M) * (size_t)p.Kp;
   float* part = reinterpret_cast<float*>(ws + p.off_p);
   lm_prep_rows<true>(x, x_type, M, K, p.Kp, nullptr, xh, xl, ex, st);
   lm_launch_w<4, true, true>(p, st, nullptr, xh, xl, w_scales_t, 1, ex, nullptr,
