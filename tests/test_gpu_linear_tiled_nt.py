@@ -247,6 +247,23 @@ def test_tiled_nt_mfma_vs_oracle(qa, M, xdt):
     assert G.bits_equal(y, y_packed)
 
 
+def _mfma_nt_shapes(seed, count):
+    g = np.random.default_rng(seed)
+    return [(int(g.integers(17, 400)), int(g.integers(1, 13)) * 128, int(g.integers(1, 9)) * 128) for _ in range(count)]
+
+
+@pytest.mark.parametrize("M,K,N", _mfma_nt_shapes(777, 8))
+def test_tiled_nt_mfma_random_shapes(qa, M, K, N):
+    """Seeded random shapes beyond the decode (M 17..399, K and N multiples
+    of 128) on the tiled [N][K] copy alone, within the bar of the oracle."""
+    print(f"tiled nt mfma M={M} K={K} N={N}", flush=True)
+    wp, ws, wpg, wsg, st, wt = _weights(qa, N, K, 211 + N + K)
+    x = _randn((M, K), 223 + M)
+    y = qa.ops.linear_wq_nt(x.to(dev()), None, wsg, "int4d", N, K, 128, w_scales_t=st, w_tiled=wt).cpu()
+    ok, worst = _rowwise_ok(y, orc.dynamic_linear_forward(x, wp, ws, "int4d", K, N, 128))
+    assert ok, f"worst row error {worst:.3g} x the bar"
+
+
 def test_tiled_nt_fallback_for_other_shapes(qa):
     """x with 17 rows, or a misaligned x view, takes mxk_linear_wq_nt."""
     N, K = 256, 1024

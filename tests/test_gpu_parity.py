@@ -478,6 +478,35 @@ def test_qgemm_small_tiles(qa, shape):
         assert _bits_eq(got["c"], Cw), "C with ones for a mis-sized scale array differs"
 
 
+def _small_gemm_shapes(seed, count):
+    g = np.random.default_rng(seed)
+    return [(int(g.integers(1, 300)), int(g.integers(1, 13)) * 128, int(g.integers(1, 41)) * 16) for _ in range(count)]
+
+
+@pytest.mark.parametrize("shape", _small_gemm_shapes(4242, 10), ids=lambda s: "x".join(map(str, s)))
+def test_qgemm_small_random_shapes(qa, shape):
+    """Seeded random shapes through the one-launch int8 kernel (M 1..299, K a
+    multiple of 128 up to 1536, N a multiple of 16 up to 640): C, the int32
+    accumulators and the int16d codes bitwise against the oracle."""
+    M, K, N = shape
+    print(f"small gemm M={M} K={K} N={N}", flush=True)
+    dt = qa.get_mx_dtype("int8d")
+    A = _randn((M, K), 503 + M)
+    B = _randn((K, N), 509 + N)
+    pa, sa, _ = qa.ops.quantize(A.to(dev()), dt, 128)
+    pb, sb, _ = qa.ops.quantize(B.to(dev()), dt, 128)
+    res = qa.ops.qscale_gemm(pa, sa, pb, sb, M, K, N, 8, 128, 16, want_c=True, want_acc=True)
+    rpa, rsa, _ = orc.quantize(A, "int8d", 128)
+    rpb, rsb, _ = orc.quantize(B, "int8d", 128)
+    ac = orc.unpack_auto(rpa, 8, M * K).to(torch.int32)
+    bc = orc.unpack_auto(rpb, 8, K * N).to(torch.int32)
+    codes, scales, C = orc.qscale_matmul(ac, rsa, bc, rsb, M, K, N, 8, 128, 16, return_c=True)
+    assert torch.equal(res["acc"].cpu(), orc.int_accumulators(ac, bc, M, K, N, 128))
+    assert _bits_eq(res["c"], C)
+    assert _bits_eq(res["packed"], orc.pack_auto(codes, 16))
+    assert _bits_eq(res["scales"], scales)
+
+
 def test_qgemm_int4_tiny_scales(qa):
     """The int4 loop folds the code unpacking's factor 256 into A's scales
     (SA * 2^-8) when that is exact; scales below 2^-118 whose low bits the
