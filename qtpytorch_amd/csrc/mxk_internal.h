@@ -407,8 +407,10 @@ __device__ __forceinline__ int bucket_keyed(float y, const int2* __restrict__ T)
   using K = FpKeys<BITS>;
   const bool pos = !(y <= 0.0f);
   const uint32_t ab = (__float_as_uint(y) & 0x7FFFFFFFu) + (pos ? 0u : 1u);
-  const int k = min(max((int)(ab >> K::SHIFT) - K::BASE, 0), K::N - 1);
-  const int2 e = T[k];
+  // the key clamped before the base is taken off (one v_med3_u32; the
+  // subtraction folds into the table address)
+  const uint32_t kc = min(max(ab >> K::SHIFT, (uint32_t)K::BASE), (uint32_t)(K::BASE + K::N - 1));
+  const int2 e = T[kc - (uint32_t)K::BASE];
   const int c = e.x + (__uint_as_float(ab) > __int_as_float(e.y) ? 1 : 0);
   return c ^ (pos ? H : H - 1);
 }
