@@ -145,20 +145,26 @@ template <> struct ElemT<hip_bfloat16> {
 // Load E consecutive elements starting at `idx` as float; elements at or
 // beyond n read as +0.0 (the reference zero-pads the last block).  A full
 // in-range group uses 16-byte loads (the caller guarantees alignment).
+// E in-range elements at p (16-byte aligned) as float, no range check
+template <typename T, int E>
+__device__ __forceinline__ void load_whole(const T* __restrict__ p, float (&v)[E]) {
+  constexpr int PER16 = 16 / sizeof(T);
+  static_assert(E % PER16 == 0, "E must cover whole 16-byte vectors");
+  const u32x4* p4 = reinterpret_cast<const u32x4*>(p);
+#pragma unroll
+  for (int q = 0; q < E / PER16; ++q) {
+    u32x4 w = __builtin_nontemporal_load(p4 + q);
+    const T* t = reinterpret_cast<const T*>(&w);
+#pragma unroll
+    for (int i = 0; i < PER16; ++i) v[q * PER16 + i] = ElemT<T>::cvt(t[i]);
+  }
+}
+
 template <typename T, int E>
 __device__ __forceinline__ void load_elems(const T* __restrict__ x, int64_t idx, int64_t n,
                                            float (&v)[E]) {
-  constexpr int PER16 = 16 / sizeof(T);
-  static_assert(E % PER16 == 0, "E must cover whole 16-byte vectors");
   if (idx + E <= n) {
-    const u32x4* p = reinterpret_cast<const u32x4*>(x + idx);
-#pragma unroll
-    for (int q = 0; q < E / PER16; ++q) {
-      u32x4 w = __builtin_nontemporal_load(p + q);
-      const T* t = reinterpret_cast<const T*>(&w);
-#pragma unroll
-      for (int i = 0; i < PER16; ++i) v[q * PER16 + i] = ElemT<T>::cvt(t[i]);
-    }
+    load_whole<T, E>(x + idx, v);
   } else {
 #pragma unroll
     for (int i = 0; i < E; ++i) v[i] = (idx + i < n) ? ElemT<T>::cvt(x[idx + i]) : 0.0f;
@@ -185,6 +191,50 @@ __device__ __forceinline__ uint32_t buf_load_b32_nt(__amdgpu_buffer_rsrc_t r, ui
 }
 __device__ __forceinline__ u32x4 buf_load_b128_nt(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
   return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)voff, (int)soff, 2));
+}
+
+// Store `NB` bytes from `w` at byte voff of a buffer resource (aligned to NB)
+template <int NB>
+__device__ __forceinline__ void buf_store(__amdgpu_buffer_rsrc_t r, uint32_t voff, const uint32_t* w) {
+  if constexpr (NB == 1) __builtin_amdgcn_raw_buffer_store_b8((uint8_t)w[0], r, (int)voff, 0, 0);
+  else if constexpr (NB == 2) __builtin_amdgcn_raw_buffer_store_b16((uint16_t)w[0], r, (int)voff, 0, 0);
+  else if constexpr (NB == 4) __builtin_amdgcn_raw_buffer_store_b32(w[0], r, (int)voff, 0, 0);
+  else if constexpr (NB == 8) __builtin_amdgcn_raw_buffer_store_b64(u32x2{w[0], w[1]}, r, (int)voff, 0, 0);
+  else if constexpr (NB == 16)
+    __builtin_amdgcn_raw_buffer_store_b128(u32x4{w[0], w[1], w[2], w[3]}, r, (int)voff, 0, 0);
+  else if constexpr (NB == 32) {
+    __builtin_amdgcn_raw_buffer_store_b128(u32x4{w[0], w[1], w[2], w[3]}, r, (int)voff, 0, 0);
+    __builtin_amdgcn_raw_buffer_store_b128(u32x4{w[4], w[5], w[6], w[7]}, r, (int)voff + 16, 0, 0);
+  }
+}
+
+// E elements at byte voff of a buffer resource (16-byte aligned) as float,
+// non-temporal
+template <typename T, int E>
+__device__ __forceinline__ void buf_load_elems(__amdgpu_buffer_rsrc_t r, uint32_t voff, float (&v)[E]) {
+  constexpr int PER16 = 16 / sizeof(T);
+  static_assert(E % PER16 == 0, "E must cover whole 16-byte vectors");
+#pragma unroll
+  for (int q = 0; q < E / PER16; ++q) {
+    u32x4 w = buf_load_b128_nt(r, voff + 16 * q, 0);
+    const T* t = reinterpret_cast<const T*>(&w);
+#pragma unroll
+    for (int i = 0; i < PER16; ++i) v[q * PER16 + i] = ElemT<T>::cvt(t[i]);
+  }
+}
+
+// Store `NB` bytes from `w` at dst (aligned to NB), no range check
+template <int NB>
+__device__ __forceinline__ void store_whole(uint8_t* __restrict__ dst, const uint32_t* w) {
+  if constexpr (NB == 1) *dst = static_cast<uint8_t>(w[0]);
+  else if constexpr (NB == 2) *reinterpret_cast<uint16_t*>(dst) = static_cast<uint16_t>(w[0]);
+  else if constexpr (NB == 4) *reinterpret_cast<uint32_t*>(dst) = w[0];
+  else if constexpr (NB == 8) *reinterpret_cast<u32x2*>(dst) = u32x2{w[0], w[1]};
+  else if constexpr (NB == 16) *reinterpret_cast<u32x4*>(dst) = u32x4{w[0], w[1], w[2], w[3]};
+  else if constexpr (NB == 32) {
+    *reinterpret_cast<u32x4*>(dst) = u32x4{w[0], w[1], w[2], w[3]};
+    *reinterpret_cast<u32x4*>(dst + 16) = u32x4{w[4], w[5], w[6], w[7]};
+  }
 }
 
 // Store `NB` bytes from `w` at dst+off when they fit below `limit`; bytes at
@@ -349,71 +399,134 @@ __device__ __forceinline__ int bucket_fp4(float y) {
   return pos ? 8 + c : 7 - c;
 }
 
-// bucket<BITS> through an LDS table keyed by the top bits of the
-// magnitude.  FP4: key k = clamp((bits >> 21) - 488, 0, 31), a quarter
-// binade from 2^-5 on ([0, 1.25 * 2^-5) for k = 0, [7, inf] and NaN for
-// k = 31).  FP8: k = clamp((bits >> 19) - 1728, 0, 304), a sixteenth of a
-// binade from 2^-19 on (below the smallest mid, 2^-9 / 960) up to [1, inf]
-// and NaN.  Each key's interval holds at most one mid (consecutive mids are
-// more than one key apart), so #{mids < a} = T[k].x + (a > T[k].y) with
-// T[k] = (#mids below the interval, the mid inside it or +inf).  For y <= 0
-// it counts the mids below nextup(|y|), and H + c / H - 1 - c are c ^ H /
-// c ^ (H - 1).  One LDS read and ~10 VALU per element against ~15 (FP4
-// search over constant mids) or ~18 (FP8 candidate and two mids); float4d
-// quantize at 2^28: 265 -> 228 us.  Equal to torch.bucketize over the mids
-// for every float32 pattern, NaN included (last index), checked exhaustively.
+// bucket<BITS> of a finite y through an LDS table keyed by the sign and
+// the top bits of the clamped magnitude.  Magnitude key k = (bits(c) >>
+// SHIFT) - BASE of c = clamp(|y|, LO, HI): FP4 a quarter binade from 2^-5
+// on (N 32, SHIFT 21, BASE 488; key 0 = [0, 1.25 * 2^-5), key 31 = [7,
+// inf)), FP8 a sixteenth of a binade from 2^-19 on (N 305, SHIFT 19, BASE
+// 1728; key 304 = [1, inf)).  Each key's interval holds at most one
+// positive mid m_k (consecutive mids are more than one key apart) and key
+// 0 none (it ends below the smallest mid); c_k counts the mids below the
+// interval.  With torch.bucketize's count of mids < y:
+//   y > 0:   H + c_k + (y > m_k)
+//   y <= 0:  H - 1 - #{mids <= |y|} = (H - 2 - c_k) + (y > -m_k)
+// so every (sign, key) entry is a base and a threshold, code = base +
+// (y > thr): positive (H + c_k, m_k), negative (H - 2 - c_k, -m_k), a key
+// without a mid (H + c_k, +inf) / (H - 1 - c_k, +inf), and positive key 0
+// (H - 1, +0) so that +0 takes the code of -0.  The sign selects a half of
+// the table: FP4 as bit 10 of the key itself (bits(c) with y's sign bit,
+// shifted), the table indexed by that key unreduced (entries from BASE on,
+// the negative half 1024 entries further, 12 KB of LDS) so that the address
+// is two VALU; FP8 by selecting the half's base address (305 entries on).  ~7 VALU and one LDS
+// read per element against ~11 for the unsigned key (count, nextup of |y|
+// for y <= 0, then c ^ H or c ^ (H - 1)).  Equal to torch.bucketize over
+// the mids for every finite float32 and +-inf (checked over every pattern
+// near a mid or a key boundary and a stride through all of them).
 template <int BITS> struct FpKeys;
-template <> struct FpKeys<4> { static constexpr int N = 32, SHIFT = 21, BASE = 488; };
-template <> struct FpKeys<8> { static constexpr int N = 305, SHIFT = 19, BASE = 1728; };
+// OFF: the index of positive key 0's entry; NEG: the negative half's
+// distance from the positive one
+template <> struct FpKeys<4> { static constexpr int N = 32, SHIFT = 21, BASE = 488, NEG = 1 << 10, OFF = 488; };
+template <> struct FpKeys<8> { static constexpr int N = 305, SHIFT = 19, BASE = 1728, NEG = 305, OFF = 0; };
 
-// P: the positive mids at P[1..H-1] (build_tables<8>'s table; FP4 uses its
-// constants and ignores P)
+// The tables are made by the compiler (constant evaluation is IEEE float32
+// arithmetic, rounded to nearest, the operations build_tables performs at
+// run time) and live in device memory; a workgroup copies the 2 * N key
+// entries into LDS (load_fp_keys) instead of building them: float8d
+// quantize spent ~100 VALU per wave on the build (a division per grid value,
+// a bisection per key) against ~2.7 steps of ~220.
+namespace fpt {
+constexpr float pow2(int e) {
+  float r = 1.0f;
+  for (int i = 0; i < e; ++i) r *= 2.0f;
+  for (int i = 0; i < -e; ++i) r *= 0.5f;
+  return r;
+}
+// fmt_value(bits, c) / fmt_max(bits)
+constexpr float grid(int bits, int c) {
+  if (bits == 4) {
+    const int e = c >> 1, m = c & 1;
+    return (e == 0 ? 0.5f * (float)m : (float)(2 + m) * pow2(e - 2)) / 6.0f;
+  }
+  const int e = c >> 3, m = c & 7;
+  return (e == 0 ? (float)m * pow2(-9) : (float)(8 + m) * pow2(e - 10)) / 480.0f;
+}
 template <int BITS>
-__device__ __forceinline__ void build_fp_keys(int2* T, const float* P) {
-  constexpr int H = 1 << (BITS - 1);
+struct Tables {
+  static constexpr int H = 1 << (BITS - 1), N = FpKeys<BITS>::N;
+  float P[H + 1];     // build_tables' P: -inf, the positive mids, +inf
+  int key[2 * N][2];  // positive keys 0..N-1, then negative keys 0..N-1
+};
+template <int BITS>
+constexpr Tables<BITS> make_tables() {
   using K = FpKeys<BITS>;
-  for (int k = threadIdx.x; k < K::N; k += blockDim.x) {
-    const float lo = k == 0 ? 0.0f : __uint_as_float((uint32_t)(k + K::BASE) << K::SHIFT);
-    const float hi = k == K::N - 1 ? __builtin_inff() : __uint_as_float((uint32_t)(k + K::BASE + 1) << K::SHIFT);
+  constexpr int H = 1 << (BITS - 1);
+  Tables<BITS> t{};
+  t.P[0] = -__builtin_inff();
+  t.P[H] = __builtin_inff();
+  for (int j = 1; j < H; ++j) t.P[j] = (grid(BITS, j - 1) + grid(BITS, j)) * 0.5f;
+  for (int k = 0; k < K::N; ++k) {
+    const float lo = k == 0 ? 0.0f : __builtin_bit_cast(float, (uint32_t)(k + K::BASE) << K::SHIFT);
+    const float hi =
+        k == K::N - 1 ? __builtin_inff() : __builtin_bit_cast(float, (uint32_t)(k + K::BASE + 1) << K::SHIFT);
     int cnt = 0;
     float mid = __builtin_inff();
-    if constexpr (BITS == 4) {
-      using namespace fp4c;
-      const float Q[7] = {P1, P2, P3, P4, P5, P6, P7};
-#pragma unroll
-      for (int j = 0; j < 7; ++j) {
-        if (Q[j] < lo) ++cnt;
-        else if (Q[j] < hi) mid = Q[j];
-      }
-    } else {
-      // cnt = #{P[1..H-1] < lo} by bisection over the sorted mids
-      int a = 0, b = H - 1;
-      while (a < b) {
-        const int m = (a + b + 1) >> 1;
-        if (P[m] < lo) a = m;
-        else b = m - 1;
-      }
-      cnt = a;
-      if (cnt + 1 <= H - 1 && P[cnt + 1] < hi) mid = P[cnt + 1];
+    for (int j = 1; j < H; ++j) {
+      if (t.P[j] < lo) ++cnt;
+      else if (t.P[j] < hi && mid == __builtin_inff()) mid = t.P[j];
     }
-    T[k] = make_int2(cnt, __float_as_int(mid));
+    const bool has = mid < __builtin_inff();
+    t.key[k][0] = k == 0 ? H - 1 : H + cnt;
+    t.key[k][1] = __builtin_bit_cast(int, k == 0 ? 0.0f : mid);
+    t.key[K::N + k][0] = has ? H - 2 - cnt : H - 1 - cnt;
+    t.key[K::N + k][1] = __builtin_bit_cast(int, has ? -mid : mid);
   }
+  return t;
+}
+}  // namespace fpt
+
+template <int BITS> struct FpTables;
+template <> struct FpTables<4> { static __device__ const fpt::Tables<4> t; };
+template <> struct FpTables<8> { static __device__ const fpt::Tables<8> t; };
+inline __device__ const fpt::Tables<4> FpTables<4>::t = fpt::make_tables<4>();
+inline __device__ const fpt::Tables<8> FpTables<8>::t = fpt::make_tables<8>();
+
+// build_tables<BITS>' P (FP4's is its constants), in device memory
+template <int BITS>
+__device__ __forceinline__ const float* fp_mids() { return FpTables<BITS>::t.P; }
+
+// Copies the 2 * N key entries into T's layout (FP4 leaves the entries below
+// OFF and between the halves unwritten) and waits for the workgroup.
+template <int BITS>
+__device__ __forceinline__ void load_fp_keys(int2* T) {
+  using K = FpKeys<BITS>;
+  const int2* src = reinterpret_cast<const int2*>(FpTables<BITS>::t.key);
+  for (int t = threadIdx.x; t < 2 * K::N; t += blockDim.x)
+    T[K::OFF + (t < K::N ? t : K::NEG + t - K::N)] = src[t];
   __syncthreads();
 }
 
+// The code of a finite y (or +-inf) in [0, 2H - 1]; T is load_fp_keys'
+// table.
 template <int BITS>
-__device__ __forceinline__ int bucket_keyed(float y, const int2* __restrict__ T) {
-  constexpr int H = 1 << (BITS - 1);
+__device__ __forceinline__ int bucket_signed(float y, const int2* __restrict__ T) {
   using K = FpKeys<BITS>;
-  const bool pos = !(y <= 0.0f);
-  const uint32_t ab = (__float_as_uint(y) & 0x7FFFFFFFu) + (pos ? 0u : 1u);
-  // the key clamped before the base is taken off (one v_med3_u32; the
-  // subtraction folds into the table address)
-  const uint32_t kc = min(max(ab >> K::SHIFT, (uint32_t)K::BASE), (uint32_t)(K::BASE + K::N - 1));
-  const int2 e = T[kc - (uint32_t)K::BASE];
-  const int c = e.x + (__uint_as_float(ab) > __int_as_float(e.y) ? 1 : 0);
-  return c ^ (pos ? H : H - 1);
+  const float c = __builtin_amdgcn_fmed3f(__builtin_fabsf(y), __uint_as_float((uint32_t)K::BASE << K::SHIFT),
+                                          __uint_as_float((uint32_t)(K::BASE + K::N - 1) << K::SHIFT));
+  int2 e;
+  if constexpr (K::NEG == (1 << (31 - K::SHIFT))) {
+    static_assert(K::OFF == K::BASE, "the key indexes the table unreduced");
+    const uint32_t u = __float_as_uint(c) | (__float_as_uint(y) & 0x80000000u);
+    e = T[u >> K::SHIFT];
+  } else {
+    const int2* Th = (int)__float_as_uint(y) < 0 ? T + K::OFF + K::NEG : T + K::OFF;
+    e = Th[(__float_as_uint(c) >> K::SHIFT) - (uint32_t)K::BASE];
+  }
+  return e.x + (y > __int_as_float(e.y) ? 1 : 0);
 }
+
+// LDS entries of load_fp_keys' table
+template <int BITS>
+constexpr int fp_keys_size() { return FpKeys<BITS>::OFF + FpKeys<BITS>::NEG + FpKeys<BITS>::N; }
 
 template <int MODE, int BITS>
 __device__ __forceinline__ int encode(float v, const BlockParams& bp, float qf, const float* P) {
@@ -461,18 +574,18 @@ __device__ __forceinline__ int encode_nonfinite(float v, const BlockParams& bp, 
 }
 __device__ __forceinline__ bool finite_scale(float s) { return __builtin_fabsf(s) < __builtin_inff(); }
 
-// encode<> with float codes through the key table of build_fp_keys (T
+// encode<> with float codes through the key table of load_fp_keys (T
 // unused for the other formats)
 template <int MODE, int BITS>
 __device__ __forceinline__ int encode_keyed(float v, const BlockParams& bp, float qf, const float* P, const int2* T) {
-  if constexpr (MODE == Q_FP) return bucket_keyed<BITS>(div_rn(v, bp.s, bp.mul), T);
+  if constexpr (MODE == Q_FP) return bucket_signed<BITS>(div_rn(v, bp.s, bp.mul), T);
   else return encode<MODE, BITS>(v, bp, qf, P);
 }
 
 // LDS entries of a kernel's key table (1 when it encodes no float codes)
 template <int MODE, int BITS>
 constexpr int fp_keys_n() {
-  if constexpr (MODE == Q_FP) return FpKeys<BITS>::N;
+  if constexpr (MODE == Q_FP) return fp_keys_size<BITS>();
   else return 1;
 }
 

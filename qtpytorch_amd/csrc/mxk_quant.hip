@@ -21,6 +21,7 @@
 #include <cmath>
 #include <cstring>
 #include <mutex>
+#include <type_traits>
 #include <vector>
 
 namespace mxk {
@@ -55,10 +56,30 @@ int num_cus() {
 }
 
 // ---------------------------------------------------------------- fast quantize
+// A workgroup's step count for the grid-stride loops over steps of GPB
+// blocks: the workgroup whose first block is b makes q_all + (b < r_all)
+// steps in all, and q_whole + (b <= r_whole) steps that end at or below
+// both n and n_store.
+struct QuantSteps {
+  int64_t q_all, r_all, q_whole, r_whole;
+};
+static QuantSteps quant_steps(int grid, int gpb, int block, int64_t n, int64_t nb, int64_t n_store) {
+  const int64_t rstride = (int64_t)grid * gpb;
+  QuantSteps s;
+  s.q_all = nb / rstride;
+  s.r_all = nb % rstride;
+  // step s0 is whole when s0 + gpb <= floor(min(n, n_store) / block)
+  const int64_t last = std::min(n, n_store) / block - gpb;
+  s.q_whole = last < 0 ? 0 : last / rstride;
+  s.r_whole = last < 0 ? -1 : last % rstride;
+  return s;
+}
+
 template <typename T, int E, int LPB, int MODE, int BITS>
 __global__ __launch_bounds__(256) void k_quant_fast(const T* __restrict__ x, int64_t n, int64_t nb,
                                                     uint8_t* __restrict__ packed, int64_t packed_nbytes,
-                                                    int64_t n_store, float* __restrict__ scales, float qf) {
+                                                    int64_t n_store, float* __restrict__ scales, float qf,
+                                                    QuantSteps st) {
   constexpr int B = E * LPB;
   constexpr int GPW = 64 / LPB;
   constexpr int GPB = 4 * GPW;
@@ -77,34 +98,37 @@ __global__ __launch_bounds__(256) void k_quant_fast(const T* __restrict__ x, int
   constexpr int NB = NIB ? 1 : CH * BITS / 8;
   constexpr uint32_t MASK = BITS == 32 ? 0xFFFFFFFFu : ((1u << BITS) - 1u);
   constexpr int H = MODE == Q_FP ? (1 << (BITS - 1)) : 1;
-  __shared__ float sP[H + 1];
+  const float* sP = fp_mids<MODE == Q_FP ? BITS : 4>();  // read only by the non-finite path
   __shared__ int2 sK[fp_keys_n<MODE, BITS>()];
-  if constexpr (MODE == Q_FP && BITS != 4) build_tables<BITS>(sP, nullptr);
-  if constexpr (MODE == Q_FP) build_fp_keys<BITS>(sK, sP);
 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int g = lane / LPB, li = lane % LPB;
   const int64_t rstride = (int64_t)gridDim.x * GPB;
-  // The next grid-stride step's elements are loaded before this step is
-  // encoded, so that every wave keeps two steps of loads in flight.
-  float vn[Q][CH];
-  {
-    const int64_t blk = (int64_t)blockIdx.x * GPB + wave * GPW + g;
+  // A step is the workgroup's GPB consecutive blocks; the workgroup's steps
+  // are grid-stride.  The steps that end at or below both n and n_store
+  // ("whole": every step but those reaching the end of the data) read and
+  // write through buffer resources based at the step, at the lane's fixed
+  // offset: no per-lane range checks and no 64-bit lane addresses.  Their
+  // loop is unrolled twice over two register sets, so that the next step's
+  // loads are in flight while this one is encoded without copying
+  // registers.  The remaining steps check each lane.  Step counts come from
+  // the host as quotients and remainders so that the loop tests are scalar.
+  // (With the signed key tables: float4d at 2^28 220 -> 198 us, float8d 243
+  // -> 229 us, fp16 int8dv 149 -> 136 us.)
+  const int64_t b_first = (int64_t)blockIdx.x * GPB;
+  const int steps = (int)(st.q_all + (b_first < st.r_all ? 1 : 0));
+  const int wholes = (int)(st.q_whole + (b_first <= st.r_whole ? 1 : 0));
+  const int lo = (wave * GPW + g) * B + li * CH;  // the lane's first element in a step
+  auto load_whole_step = [&](int t, float (&v)[Q][CH]) {
+    const int64_t s0 = b_first + (int64_t)t * rstride;
+    const __amdgpu_buffer_rsrc_t r = make_rsrc(x + s0 * B, (uint32_t)(GPB * B * sizeof(T)));
 #pragma unroll
-    for (int q = 0; q < Q; ++q) load_elems<T, CH>(x, blk * B + q * (B / Q) + (int64_t)li * CH, n, vn[q]);
-  }
-  for (int64_t b0 = (int64_t)blockIdx.x * GPB; b0 < nb; b0 += rstride) {
-    const int64_t blk = b0 + wave * GPW + g;
-    float v[Q][CH];
-#pragma unroll
-    for (int q = 0; q < Q; ++q)
-#pragma unroll
-      for (int i = 0; i < CH; ++i) v[q][i] = vn[q][i];
-    if (b0 + rstride < nb) {
-      const int64_t nblk = blk + rstride;
-#pragma unroll
-      for (int q = 0; q < Q; ++q) load_elems<T, CH>(x, nblk * B + q * (B / Q) + (int64_t)li * CH, n, vn[q]);
-    }
+    for (int q = 0; q < Q; ++q) buf_load_elems<T, CH>(r, (uint32_t)((lo + q * (B / Q)) * sizeof(T)), v[q]);
+  };
+  auto encode_step = [&](auto whole_c, int t, float (&v)[Q][CH]) {
+    constexpr bool WHOLE = decltype(whole_c)::value;
+    const int64_t s0 = b_first + (int64_t)t * rstride;
+    const int64_t blk = s0 + wave * GPW + g;
     uint32_t mb = 0u;
 #pragma unroll
     for (int q = 0; q < Q; ++q)
@@ -123,6 +147,8 @@ __global__ __launch_bounds__(256) void k_quant_fast(const T* __restrict__ x, int
         for (int q = 0; q < Q; ++q) div_rn_all<CH>(v[q], bp.s, bp.mul);
       }
     }
+    __amdgpu_buffer_rsrc_t rp;
+    if constexpr (WHOLE) rp = make_rsrc(packed + s0 * (B * BITS / 8), (uint32_t)(GPB * B * BITS / 8));
 #pragma unroll
     for (int q = 0; q < Q; ++q) {
       const int64_t idx = blk * B + q * (B / Q) + (int64_t)li * CH;
@@ -138,21 +164,54 @@ __global__ __launch_bounds__(256) void k_quant_fast(const T* __restrict__ x, int
       } else {
 #pragma unroll
         for (int i = 0; i < CH; ++i) {
-          const uint32_t f = (uint32_t)(VOTE ? encode_vec_q(v[q][i], qf)
-                                             : encode_keyed<MODE, BITS>(v[q][i], bp, qf, sP, sK)) & MASK;
+          // float codes come out of the table in [0, 2^BITS) and need no mask
+          const int c = VOTE ? encode_vec_q(v[q][i], qf) : encode_keyed<MODE, BITS>(v[q][i], bp, qf, sP, sK);
+          const uint32_t f = MODE == Q_FP ? (uint32_t)c : (uint32_t)c & MASK;
           w[(i * BITS) >> 5] |= f << ((i * BITS) & 31);
         }
       }
-      if (idx + CH > n_store) clear_tail<NW, BITS>(w, n_store - idx);
+      if (!WHOLE && idx + CH > n_store) clear_tail<NW, BITS>(w, n_store - idx);
       if constexpr (NIB) {
         const uint32_t other = (uint32_t)__builtin_amdgcn_mov_dpp((int)w[0], 0xB1, 0xF, 0xF, true);
         w[0] = (w[0] & 0xFu) | ((other & 0xFu) << 4);
-        if (blk < nb && (li & 1) == 0) store_bytes<1>(packed, idx / 8, packed_nbytes, w);
+        if ((li & 1) == 0) {
+          if constexpr (WHOLE) buf_store<1>(rp, (uint32_t)((lo + q * (B / Q)) / 8), w);
+          else if (blk < nb) store_bytes<1>(packed, idx / 8, packed_nbytes, w);
+        }
       } else {
-        if (blk < nb) store_bytes<NB>(packed, idx * BITS / 8, packed_nbytes, w);
+        if constexpr (WHOLE) buf_store<NB>(rp, (uint32_t)((lo + q * (B / Q)) * BITS / 8), w);
+        else if (blk < nb) store_bytes<NB>(packed, idx * BITS / 8, packed_nbytes, w);
       }
     }
-    if (blk < nb && li == 0) scales[blk] = bp.s;
+    if constexpr (WHOLE) {
+      if (li == 0) {
+        const uint32_t sb = __float_as_uint(bp.s);
+        buf_store<4>(make_rsrc(scales + s0, (uint32_t)(GPB * 4)), (uint32_t)((wave * GPW + g) * 4), &sb);
+      }
+    } else {
+      if (li == 0 && blk < nb) scales[blk] = bp.s;
+    }
+  };
+  float va[Q][CH], vb[Q][CH];
+  int t = 0;
+  // the first step's loads are in flight while the float key table is copied
+  if (wholes > 0) load_whole_step(0, va);
+  if constexpr (MODE == Q_FP) load_fp_keys<BITS>(sK);
+  for (; t + 1 < wholes; t += 2) {
+    load_whole_step(t + 1, vb);
+    encode_step(std::true_type(), t, va);
+    if (t + 2 < wholes) load_whole_step(t + 2, va);
+    encode_step(std::true_type(), t + 1, vb);
+  }
+  if (t < wholes) {
+    encode_step(std::true_type(), t, va);
+    ++t;
+  }
+  for (; t < steps; ++t) {
+    const int64_t blk = b_first + (int64_t)t * rstride + wave * GPW + g;
+#pragma unroll
+    for (int q = 0; q < Q; ++q) load_elems<T, CH>(x, blk * B + q * (B / Q) + (int64_t)li * CH, n, va[q]);
+    encode_step(std::false_type(), t, va);
   }
 }
 
@@ -395,11 +454,11 @@ __global__ __launch_bounds__(256) void k_quant_had128(const T* __restrict__ x, i
   constexpr int NB = E * BITS / 8;
   constexpr uint32_t MASK = (1u << BITS) - 1u;
   constexpr int H = MODE == Q_FP ? (1 << (BITS - 1)) : 1;
-  __shared__ float sP[H + 1];
+  const float* sP = fp_mids<MODE == Q_FP ? BITS : 4>();  // read only by the non-finite path
   __shared__ __attribute__((aligned(16))) float srow[GPB * MXK_ROWPAD];
-  if constexpr (MODE == Q_FP && BITS != 4) build_tables<BITS>(sP, nullptr);
+
   __shared__ int2 sK[fp_keys_n<MODE, BITS>()];
-  if constexpr (MODE == Q_FP) build_fp_keys<BITS>(sK, sP);
+  if constexpr (MODE == Q_FP) load_fp_keys<BITS>(sK);
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int g = lane / LPB, li = lane % LPB;
   float* row = srow + (wave * GPW + g) * MXK_ROWPAD;
@@ -851,13 +910,15 @@ static int grid_capped(int64_t work_items, int per_block, int cap_per_cu) {
   return (int)std::min<int64_t>(blocks, (int64_t)num_cus() * cap_per_cu);
 }
 // k_quant_fast: fp32 int codes uncapped; 16-bit int codes 128; 'v' from
-// 16-bit 32; float codes 128 (keyed buckets: float4d 221 -> 216 us against
-// 64, 225 at 32); the rest 64.
-template <typename T, int MODE>
+// 16-bit 32; FP4 codes 384 (float4d at 2^28: 196 us against 212 at 128, 198
+// at 256 and 512, 197 uncapped), FP8 codes 192 (float8d 228 us against 233
+// at 128, 231 at 160, 238 at 256, 240 at 96); the rest 64.
+template <typename T, int MODE, int BITS>
 constexpr int quant_fast_cap() {
   return (sizeof(T) == 4 && (MODE == Q_INT || MODE == Q_INT1)) ? 0
          : (sizeof(T) == 2 && (MODE == Q_INT || MODE == Q_INT1)) ? 128
-         : (sizeof(T) == 2 && MODE == Q_VEC) ? 32 : MODE == Q_FP ? 128 : 64;
+         : (sizeof(T) == 2 && MODE == Q_VEC) ? 32
+         : MODE == Q_FP ? (BITS == 4 ? 384 : 192) : 64;
 }
 // k_dequant_fast: codes decoded without a table (int8, FP8) uncapped; the
 // LDS-table widths (int 1-4 bits, FP4) 64.
@@ -892,8 +953,10 @@ static void launch_fast_b(const T* x, int64_t n, int64_t nb, int block, uint8_t*
   auto go = [&](auto lpb_tag) {
     constexpr int LPB = decltype(lpb_tag)::value;
     constexpr int GPB = 4 * (64 / LPB);
-    hipLaunchKernelGGL((k_quant_fast<T, E, LPB, MODE, BITS>), dim3(grid_capped(nb, GPB, quant_fast_cap<T, MODE>())), dim3(256), 0, st, x, n, nb,
-                       packed, pbytes, n_store, scales, qf);
+    const int grid = grid_capped(nb, GPB, quant_fast_cap<T, MODE, BITS>());
+    const QuantSteps qs = quant_steps(grid, GPB, E * LPB, n, nb, n_store);
+    hipLaunchKernelGGL((k_quant_fast<T, E, LPB, MODE, BITS>), dim3(grid), dim3(256), 0, st, x, n, nb, packed, pbytes,
+                       n_store, scales, qf, qs);
     *done = true;
   };
   switch (block / E) {
