@@ -125,6 +125,30 @@ __device__ __forceinline__ float amax_clamped(uint32_t m) {
   return __uint_as_float(max(m, __float_as_uint(MXK_AMIN)));
 }
 
+// Unsigned 32-bit division by an invariant d >= 1 (Granlund and Montgomery,
+// "Division by Invariant Integers using Multiplication", PLDI 1994, fig.
+// 4.1): with l = ceil(log2 d), m = floor(2^32 (2^l - d) / d) + 1, sh1 =
+// min(l, 1), sh2 = max(l - 1, 0), t = mulhi(m, n):
+// n / d = (t + ((n - t) >> sh1)) >> sh2 for every 0 <= n < 2^32.  Five VALU
+// in place of a 64-bit division (~66 VALU and ~67 SALU).
+struct DivU32 {
+  uint32_t m;
+  int sh1, sh2;
+};
+inline DivU32 make_divu32(uint32_t d) {
+  int l = 0;
+  while (l < 32 && (1ull << l) < (uint64_t)d) ++l;
+  DivU32 r;
+  r.m = (uint32_t)((((1ull << l) - (uint64_t)d) << 32) / (uint64_t)d + 1ull);
+  r.sh1 = l < 1 ? l : 1;
+  r.sh2 = l - 1 > 0 ? l - 1 : 0;
+  return r;
+}
+__device__ __forceinline__ uint32_t divu32(uint32_t n, const DivU32& d) {
+  const uint32_t t = __umulhi(d.m, n);
+  return (t + ((n - t) >> d.sh1)) >> d.sh2;
+}
+
 // ---------------------------------------------------------------- element loads
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));

@@ -379,19 +379,25 @@ __device__ __forceinline__ void wave_lds_sync() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-// Forward rotation of one row without the division.  In: line layout,
-// v[PER16 * q + k] at position 8 * PER16 * q + PER16 * li + k (PER16 elements
-// of the input type per 16 bytes).  Out: natural layout, v[i] at position
-// li * 16 + i.  Bit j of smask is the sign of position li + 8j; the signs
+// Forward rotation of one row without the division.  In (fwht128_stage):
+// line layout, v[PER16 * q + k] at position 8 * PER16 * q + PER16 * li + k
+// (PER16 elements of the input type per 16 bytes).  Out (fwht128_rest):
+// natural layout, v[i] at position li * 16 + i.  Bit j of smask is the sign of position li + 8j; the signs
 // flip sign bits (exact) before level 64.  row: 128(+pad) floats of LDS.
+// fwht128_stage writes the row (line layout) to LDS; fwht128_rest reads it
+// back transposed and runs the levels.  Between the two the caller may
+// reuse the registers of the input (the next row's loads).
 template <int PER16>
-__device__ __forceinline__ void fwht128_group(float (&v)[16], float* __restrict__ row, int li, uint32_t smask) {
+__device__ __forceinline__ void fwht128_stage(const float (&v)[16], float* __restrict__ row, int li) {
 #pragma unroll
   for (int q = 0; q < 16 / PER16; ++q)
 #pragma unroll
     for (int h = 0; h < PER16 / 4; ++h)
       *reinterpret_cast<float4*>(row + 8 * PER16 * q + PER16 * li + 4 * h) =
           make_float4(v[PER16 * q + 4 * h], v[PER16 * q + 4 * h + 1], v[PER16 * q + 4 * h + 2], v[PER16 * q + 4 * h + 3]);
+}
+
+__device__ __forceinline__ void fwht128_rest(float (&v)[16], float* __restrict__ row, int li, uint32_t smask) {
   wave_lds_sync();
 #pragma unroll
   for (int j = 0; j < 16; ++j) v[j] = row[li + 8 * j];
@@ -448,56 +454,69 @@ template <typename T, int MODE, int BITS>
 __global__ __launch_bounds__(256) void k_quant_had128(const T* __restrict__ x, int64_t n, int64_t nb,
                                                       const float* __restrict__ signs,
                                                       uint8_t* __restrict__ packed, int64_t packed_nbytes,
-                                                      int64_t n_store, float* __restrict__ scales, float qf) {
+                                                      int64_t n_store, float* __restrict__ scales, float qf,
+                                                      QuantSteps st) {
   constexpr int E = 16, LPB = 8, GPW = 8, GPB = 32;
   constexpr int NW = (E * BITS + 31) / 32;
   constexpr int NB = E * BITS / 8;
   constexpr uint32_t MASK = (1u << BITS) - 1u;
-  constexpr int H = MODE == Q_FP ? (1 << (BITS - 1)) : 1;
+  constexpr int P16 = 16 / (int)sizeof(T);
   const float* sP = fp_mids<MODE == Q_FP ? BITS : 4>();  // read only by the non-finite path
   __shared__ __attribute__((aligned(16))) float srow[GPB * MXK_ROWPAD];
-
   __shared__ int2 sK[fp_keys_n<MODE, BITS>()];
-  if constexpr (MODE == Q_FP) load_fp_keys<BITS>(sK);
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int g = lane / LPB, li = lane % LPB;
   float* row = srow + (wave * GPW + g) * MXK_ROWPAD;
-  uint32_t smask = 0u;  // bit j: the sign of position li + 8j is negative
-#pragma unroll
-  for (int j = 0; j < E; ++j) smask |= (signs[li + 8 * j] < 0.0f ? 1u : 0u) << j;
   const float rdiv = 11.3137083f;           // fl32(sqrt(128))
   const float rinv = 1.0f / 11.3137083f;
   const int64_t rstride = (int64_t)gridDim.x * GPB;
-  // the next grid-stride step's row is loaded before this one is rotated
-  constexpr int P16 = 16 / (int)sizeof(T);
-  float vn[E];
-  load_line<T>(x, ((int64_t)blockIdx.x * GPB + wave * GPW + g) * 128, li, n, vn);
-  for (int64_t b0 = (int64_t)blockIdx.x * GPB; b0 < nb; b0 += rstride) {
-    const int64_t blk = b0 + wave * GPW + g;
-    const int64_t idx = blk * 128 + (int64_t)li * E;
-    float v[E];
+  // Steps of GPB rows as in k_quant_fast: the whole ones load and store
+  // through buffer resources based at the step; the next row is loaded into
+  // the registers this row leaves once it is staged in LDS (no copy).
+  const int64_t b_first = (int64_t)blockIdx.x * GPB;
+  const int steps = (int)(st.q_all + (b_first < st.r_all ? 1 : 0));
+  const int wholes = (int)(st.q_whole + (b_first <= st.r_whole ? 1 : 0));
+  const int r0 = (wave * GPW + g) * 128;  // the row's first element in a step
+  auto load_whole_step = [&](int t, float (&v)[E]) {
+    const int64_t s0 = b_first + (int64_t)t * rstride;
+    const __amdgpu_buffer_rsrc_t r = make_rsrc(x + s0 * 128, (uint32_t)(GPB * 128 * sizeof(T)));
 #pragma unroll
-    for (int i = 0; i < E; ++i) v[i] = vn[i];
-    if (b0 + rstride < nb) load_line<T>(x, (blk + rstride) * 128, li, n, vn);
-    asm volatile("" : "+v"(smask));  // keeps the sign words out of loop-invariant registers
-    fwht128_group<P16>(v, row, li, smask);
-    // one pass over the magnitudes gives the block maximum and the wave's
-    // smallest nonzero magnitude (which picks the division path, as in
-    // div_rn_all); the scale comes from the maximum before the division:
-    // a correctly rounded division is monotone, so max RN(|v|/d) = RN(max |v| / d).
-    // (bits << 1) - 1 orders the nonzero magnitudes and sends both zeros to
-    // 0xFFFFFFFF, so its minimum is below 2 * bits(2^-96) - 1 exactly when
-    // some lane holds 0 < |v| < 2^-96.
+    for (int q = 0; q < 16 / P16; ++q) {
+      const u32x4 w = buf_load_b128_nt(r, (uint32_t)((r0 + 8 * P16 * q + P16 * li) * sizeof(T)), 0);
+      const T* tv = reinterpret_cast<const T*>(&w);
+#pragma unroll
+      for (int k = 0; k < P16; ++k) v[P16 * q + k] = ElemT<T>::cvt(tv[k]);
+    }
+  };
+  // The division by d of every element: the Markstein quotient, unless some
+  // lane holds a nonzero value below 2^-96 (one wave-wide vote, below) and
+  // the codes read the quotient's low bits: 1-bit codes its sign, float
+  // codes whether it is above 2^-150.  Integer codes of 2+ bits need no
+  // vote: the block scale comes from the maximum before the division (a
+  // correctly rounded division is monotone, so max RN(|v|/d) = RN(max |v| /
+  // d)), and below 2^-96 a quotient (< 2^-99) times the largest multiplier
+  // (q / 1e-12 < 2^55) or over the smallest 'v' scale (1e-12 / q > 2^-55)
+  // is below 2^-44 on either path: code 0.
+  constexpr bool VOTE = MODE == Q_INT1 || MODE == Q_FP;
+  auto encode_step = [&](auto whole_c, int t, float (&v)[E]) {
+    constexpr bool WHOLE = decltype(whole_c)::value;
+    const int64_t s0 = b_first + (int64_t)t * rstride;
+    const int64_t blk = s0 + wave * GPW + g;
+    const int64_t idx = blk * 128 + (int64_t)li * E;
+    // one pass over the magnitudes gives the block maximum and (VOTE) the
+    // wave's smallest nonzero magnitude: (bits << 1) - 1 orders the nonzero
+    // magnitudes and sends both zeros to 0xFFFFFFFF, so its minimum is below
+    // 2 * bits(2^-96) - 1 exactly when some lane holds 0 < |v| < 2^-96.
     uint32_t mxb = 0u;
     uint32_t mnb = 0xFFFFFFFFu;
 #pragma unroll
     for (int i = 0; i < E; ++i) {
       mxb = max(mxb, mag_bits(v[i]));
-      mnb = min(mnb, (__float_as_uint(v[i]) << 1) - 1u);
+      if constexpr (VOTE) mnb = min(mnb, (__float_as_uint(v[i]) << 1) - 1u);
     }
     const float gmx = __uint_as_float(group_max_u<LPB>(mxb));
     float am;
-    if (__builtin_expect(__ballot(mnb < 2u * 0x0F800000u - 1u) != 0ull, 0)) {
+    if (VOTE && __builtin_expect(__ballot(mnb < 2u * 0x0F800000u - 1u) != 0ull, 0)) {
 #pragma unroll
       for (int i = 0; i < E; ++i) v[i] = v[i] / rdiv;
       am = gmx / rdiv;
@@ -530,11 +549,41 @@ __global__ __launch_bounds__(256) void k_quant_had128(const T* __restrict__ x, i
         w[(i * BITS) >> 5] |= f << ((i * BITS) & 31);
       }
     }
-    if (idx + E > n_store) clear_tail<NW, BITS>(w, n_store - idx);
-    if (blk < nb) {
-      store_bytes<NB>(packed, idx * BITS / 8, packed_nbytes, w);
-      if (li == 0) scales[blk] = bp.s;
+    if constexpr (WHOLE) {
+      buf_store<NB>(make_rsrc(packed + s0 * (128 * BITS / 8), (uint32_t)(GPB * 128 * BITS / 8)),
+                    (uint32_t)((r0 + li * E) * BITS / 8), w);
+      if (li == 0) {
+        const uint32_t sb = __float_as_uint(bp.s);
+        buf_store<4>(make_rsrc(scales + s0, (uint32_t)(GPB * 4)), (uint32_t)((wave * GPW + g) * 4), &sb);
+      }
+    } else {
+      if (idx + E > n_store) clear_tail<NW, BITS>(w, n_store - idx);
+      if (blk < nb) {
+        store_bytes<NB>(packed, idx * BITS / 8, packed_nbytes, w);
+        if (li == 0) scales[blk] = bp.s;
+      }
     }
+  };
+  float vn[E], v[E];
+  int t = 0;
+  if (wholes > 0) load_whole_step(0, vn);
+  uint32_t smask = 0u;  // bit j: the sign of position li + 8j is negative
+#pragma unroll
+  for (int j = 0; j < E; ++j) smask |= (signs[li + 8 * j] < 0.0f ? 1u : 0u) << j;
+  if constexpr (MODE == Q_FP) load_fp_keys<BITS>(sK);
+  for (; t < wholes; ++t) {
+    fwht128_stage<P16>(vn, row, li);
+    if (t + 1 < wholes) load_whole_step(t + 1, vn);
+    asm volatile("" : "+v"(smask));  // keeps the sign words out of loop-invariant registers
+    fwht128_rest(v, row, li, smask);
+    encode_step(std::true_type(), t, v);
+  }
+  for (; t < steps; ++t) {
+    load_line<T>(x, (b_first + (int64_t)t * rstride + wave * GPW + g) * 128, li, n, vn);
+    fwht128_stage<P16>(vn, row, li);
+    asm volatile("" : "+v"(smask));
+    fwht128_rest(v, row, li, smask);
+    encode_step(std::false_type(), t, v);
   }
 }
 
@@ -694,7 +743,8 @@ __global__ __launch_bounds__(256) void k_dequant(const uint8_t* __restrict__ pac
 template <int MODE, int BITS>
 __global__ __launch_bounds__(256) void k_dequant_fast(const uint8_t* __restrict__ packed, int64_t packed_nbytes,
                                                       const float* __restrict__ scales, int64_t nb, int64_t n,
-                                                      int block, float* __restrict__ out) {
+                                                      int block, float* __restrict__ out, DivU32 slots_per_block,
+                                                      bool div32) {
   constexpr int U = 4;
   constexpr int H = MODE == Q_FP ? (1 << (BITS - 1)) : 1;
   // int codes of up to 4 bits decode through a table of their values as
@@ -730,7 +780,10 @@ __global__ __launch_bounds__(256) void k_dequant_fast(const uint8_t* __restrict_
         else if constexpr (BITS == 2) w[u] = packed[j0 / 4];
         else w[u] = (uint32_t)packed[j0 / 8] >> (j0 & 4);
       }
-      const int64_t b = j0 / block;
+      // the slot's block: slot / (block / 4) (all 4 of its outputs share it),
+      // by multiplication when slot indices fit 32 bits (dequantize at 2^28:
+      // int4d 180 -> 174 us, float8d 218 -> 212 us)
+      const int64_t b = div32 ? (int64_t)divu32((uint32_t)sl, slots_per_block) : j0 / block;
       sc[u] = (sl < slots && b < nb) ? scales[b] : 0.0f;
     }
 #pragma unroll
@@ -1084,11 +1137,14 @@ static bool try_had128(const T* x, int64_t n, int mode, int bits, const float* s
                        int64_t pbytes, int64_t n_store, float* scales, float qf, hipStream_t st) {
   if (!aligned16(x)) return false;
   const int64_t nb = ceil_div(n, 128);
-  const int grid = grid_capped(nb, 32, 128);
+  // 256 workgroups per CU: int4dh at 2^28 193 us against 199 at 128, 210
+  // at 64, 195 uncapped
+  const int grid = grid_capped(nb, 32, 256);
+  const QuantSteps qs = quant_steps(grid, 32, 128, n, nb, n_store);
 #define MXK_HAD_CASE(MODE, BITS)                                                                               \
   if (mode == MODE && bits == BITS) {                                                                          \
     hipLaunchKernelGGL((k_quant_had128<T, MODE, BITS>), dim3(grid), dim3(256), 0, st, x, n, nb, signs, packed, \
-                       pbytes, n_store, scales, qf);                                                           \
+                       pbytes, n_store, scales, qf, qs);                                                       \
     return true;                                                                                               \
   }
   MXK_HAD_CASE(Q_INT, 2)
@@ -1145,8 +1201,11 @@ static int launch_dequant(const void* packed, int64_t pbytes, const float* scale
         (reinterpret_cast<uintptr_t>(out) & 15u) == 0) {
       const int64_t slots = ceil_div(n, 4);
       const int grid = grid_capped(slots, 256 * 4, dequant_fast_cap<MODE, BITS>());
+      // every slot index a thread forms (sl + u * stride) stays below 2^32
+      const bool div32 = slots + 4ll * grid * 256 < (1ll << 32);
       hipLaunchKernelGGL((k_dequant_fast<MODE, BITS>), dim3(grid), dim3(256), 0, st,
-                         reinterpret_cast<const uint8_t*>(packed), pbytes, scales, nb, n, block, out);
+                         reinterpret_cast<const uint8_t*>(packed), pbytes, scales, nb, n, block, out,
+                         make_divu32((uint32_t)(block / 4)), div32);
       return check_launch("dequantize");
     }
   }

@@ -208,6 +208,55 @@ def test_quantize_seeded_vs_oracle(qa, dtype, block):
     assert _bits_eq(dq, rdq), f"{dtype}/{block}: dequantized values differ"
 
 
+@pytest.mark.parametrize("dtype", ["int8d", "int4d", "int2d", "int1d", "float4d", "float8d"])
+@pytest.mark.parametrize("block", [4, 12, 20, 36, 100, 132, 252, 1000, 4096])
+def test_dequantize_block_sizes(qa, dtype, block):
+    """The 4-output-slot dequantizer finds each slot's block by a
+    multiplicative division by block / 4 (an invariant divisor, Granlund and
+    Montgomery): blocks that are not powers of two, ragged n, against the
+    oracle bit for bit."""
+    n = 9 * block * 37 + 4 * (block // 4 // 2 + 1) + 3
+    x = _randn((n,), 4000 + block, outliers=1e-3)
+    dt = qa.get_mx_dtype(dtype)
+    packed, scales, nn = qa.ops.quantize(x.to(dev()), dt, block)
+    rp, rs, rn = orc.quantize(x, dtype, block)
+    assert nn == rn and _bits_eq(packed, rp) and _bits_eq(scales, rs)
+    dq = qa.ops._dequant(packed, scales, dt, nn, block, orig_shape=(n,))
+    rdq = orc.dequant(rp, rs, dtype, rn, block, orig_shape=(n,))
+    assert _bits_eq(dq, rdq), f"{dtype}/{block}: dequantized values differ"
+
+
+@pytest.mark.parametrize("dtype", ["int4dh", "int8dh", "int2dh", "int1dh", "float4dh", "float8dh"])
+def test_quantize_had_tiny_values(qa, dtype):
+    """'h' quantize of rows holding values below 2^-96 (subnormals, 2^-100,
+    1e-35, zeros of both signs) next to normal ones, and rows of tiny values
+    only.  The integer widths of 2+ bits divide by sqrt(128) without the
+    small-value vote (their codes of such values are 0 on either path, the
+    scale comes from the maximum before the division); int1dh and the float
+    widths keep it.  Codes and scales bit-exact against the oracle."""
+    g = torch.Generator()
+    g.manual_seed(91)
+    rows = []
+    tiny = torch.tensor([1e-45, -1e-45, 3e-45, 2.0 ** -100, -(2.0 ** -100), 1e-35, -1e-38, 0.0, -0.0, 2.0 ** -126])
+    for r in range(64):
+        v = torch.randn(128, generator=g)
+        if r % 4 == 0:
+            v = tiny[torch.randint(0, tiny.numel(), (128,), generator=g)]
+        elif r % 4 == 1:
+            m = torch.rand(128, generator=g) < 0.5
+            v[m] = tiny[torch.randint(0, tiny.numel(), (int(m.sum()),), generator=g)]
+        elif r % 4 == 2:
+            v = v * 1e-30
+        rows.append(v)
+    x = torch.stack(rows)
+    dt = qa.get_mx_dtype(dtype)
+    packed, scales, n = qa.ops.quantize(x.to(dev()), dt, 128, seed=777)
+    rp, rs, rn = orc.quantize(x, dtype, 128, seed=777)
+    assert n == rn
+    assert _bits_eq(scales, rs), f"{dtype}: scales differ"
+    assert _bits_eq(packed, rp), f"{dtype}: packed codes differ"
+
+
 @pytest.mark.parametrize("src", [torch.float16, torch.bfloat16])
 @pytest.mark.parametrize("dtype", ["int8d", "int4d", "int8dv", "float8d", "int4dh", "int1d"])
 def test_quantize_half_inputs(qa, src, dtype):
