@@ -147,6 +147,37 @@ __global__ __launch_bounds__(256) void k_quant_fast(const T* __restrict__ x, int
         for (int q = 0; q < Q; ++q) div_rn_all<CH>(v[q], bp.s, bp.mul);
       }
     }
+    // float codes: the quotients RN(v / s) for the whole step after one
+    // wave vote on subnormal values (a class test and a scalar OR per
+    // element, where div_rn branches per element).  Markstein's correction
+    // is exact for |v| >= 2^-96; between 2^-126 and 2^-96 the quotient is
+    // below 2^-56 (s >= 1e-12), where the bucket reads only whether it is
+    // above 2^-150, which the correction gets right for normal v; for a
+    // subnormal v its residual is rounded and the hardware divide is used.
+    constexpr bool FPVOTE = MODE == Q_FP;
+    if constexpr (FPVOTE) {
+      if (!nf) {
+        uint64_t sub = 0ull;
+#pragma unroll
+        for (int q = 0; q < Q; ++q)
+#pragma unroll
+          for (int i = 0; i < CH; ++i) sub |= __ballot(__builtin_amdgcn_classf(v[q][i], 0x90));
+        if (__builtin_expect(sub != 0ull, 0)) {
+#pragma unroll
+          for (int q = 0; q < Q; ++q)
+#pragma unroll
+            for (int i = 0; i < CH; ++i) v[q][i] = v[q][i] / bp.s;
+        } else {
+#pragma unroll
+          for (int q = 0; q < Q; ++q)
+#pragma unroll
+            for (int i = 0; i < CH; ++i) {
+              const float q0 = v[q][i] * bp.mul;
+              v[q][i] = __builtin_fmaf(__builtin_fmaf(-q0, bp.s, v[q][i]), bp.mul, q0);
+            }
+        }
+      }
+    }
     __amdgpu_buffer_rsrc_t rp;
     if constexpr (WHOLE) rp = make_rsrc(packed + s0 * (B * BITS / 8), (uint32_t)(GPB * B * BITS / 8));
 #pragma unroll
@@ -165,7 +196,9 @@ __global__ __launch_bounds__(256) void k_quant_fast(const T* __restrict__ x, int
 #pragma unroll
         for (int i = 0; i < CH; ++i) {
           // float codes come out of the table in [0, 2^BITS) and need no mask
-          const int c = VOTE ? encode_vec_q(v[q][i], qf) : encode_keyed<MODE, BITS>(v[q][i], bp, qf, sP, sK);
+          int c;
+          if constexpr (FPVOTE) c = bucket_signed<BITS>(v[q][i], sK);
+          else c = VOTE ? encode_vec_q(v[q][i], qf) : encode_keyed<MODE, BITS>(v[q][i], bp, qf, sP, sK);
           const uint32_t f = MODE == Q_FP ? (uint32_t)c : (uint32_t)c & MASK;
           w[(i * BITS) >> 5] |= f << ((i * BITS) & 31);
         }

@@ -226,6 +226,38 @@ def test_dequantize_block_sizes(qa, dtype, block):
     assert _bits_eq(dq, rdq), f"{dtype}/{block}: dequantized values differ"
 
 
+@pytest.mark.parametrize("dtype", ["float4d", "float8d", "float4dh", "float8dh"])
+def test_float_codes_of_subnormals(qa, dtype):
+    """Float codes of subnormal values k * 2^-149 in blocks whose scale lies
+    within 3 ulps of 2k, where RN(x / s) turns zero: Markstein's correction
+    alone rounds some of these to 0 where IEEE division gives 2^-149 (its
+    residual falls on the subnormal grid), so the quantizers divide by the
+    hardware sequence when a wave holds a subnormal.  Blocks of 128: element 0
+    is the scale, the rest subnormals of both signs near k * 2^-149.  Codes
+    and scales bit-exact against the oracle (782 of the values change their
+    zero-ness under the correction alone)."""
+    g = np.random.default_rng(5)
+    rows = []
+    for r in range(256):
+        k = int(g.integers(1, 1 << 22))
+        s = np.float32(2 * k)
+        for _ in range(abs(r % 7 - 3)):
+            s = np.nextafter(s, np.float32(np.inf if r % 7 > 3 else 0.0), dtype=np.float32)
+        ks = np.clip(k + g.integers(-2, 3, 127), 1, (1 << 23) - 1)
+        sub = (ks.astype(np.float64) * 2.0 ** -149).astype(np.float32) * np.where(g.random(127) < 0.5, -1, 1)
+        rows.append(np.concatenate([[s], sub.astype(np.float32)]))
+    x = torch.from_numpy(np.stack(rows).astype(np.float32))
+    # (the 'h' quantizers rotate first, which keeps only part of the values
+    # subnormal; they run the same rows for coverage of their vote)
+    dt = qa.get_mx_dtype(dtype)
+    hseed = 4321 if dt.is_hadamard else None
+    packed, scales, n = qa.ops.quantize(x.to(dev()), dt, 128, seed=hseed)
+    rp, rs, rn = orc.quantize(x, dtype, 128, seed=hseed)
+    assert n == rn
+    assert _bits_eq(scales, rs), f"{dtype}: scales differ"
+    assert _bits_eq(packed, rp), f"{dtype}: packed codes differ"
+
+
 @pytest.mark.parametrize("dtype", ["int4dh", "int8dh", "int2dh", "int1dh", "float4dh", "float8dh"])
 def test_quantize_had_tiny_values(qa, dtype):
     """'h' quantize of rows holding values below 2^-96 (subnormals, 2^-100,
