@@ -196,6 +196,30 @@ __device__ __forceinline__ uint32_t rne_clamped_bits(float q, float qf) {
   return __float_as_uint(__builtin_amdgcn_fmed3f(q, -qf, qf) + 12582912.0f);
 }
 
+// A lane's E codes of BITS in {2, 4, 8} bits (little-endian fields of w,
+// low codes first) as floats of code * 2^(8 - BITS): each word's fields of
+// one sub-position are moved to the tops of its bytes by one shift and one
+// mask, then each byte converts as a sign-extended byte (v_cvt_f32_i32 with
+// an SDWA byte select): ~1.2 VALU per code against ~5 for a 64-bit shift,
+// a field extract and a conversion.  The caller scales its factors by
+// 2^(BITS - 8), which keeps every product exact.
+template <int BITS, int E, int NW>
+__device__ __forceinline__ void codes_scaled(const uint64_t (&w)[NW], float (&c)[E]) {
+  constexpr int PB = 8 / BITS, CW = 32 / BITS;  // fields per byte, codes per 32-bit word
+  constexpr uint32_t TOP = BITS == 8 ? 0xFFFFFFFFu : (BITS == 4 ? 0xF0F0F0F0u : 0xC0C0C0C0u);
+#pragma unroll
+  for (int h = 0; h < (E + CW - 1) / CW; ++h) {
+    const uint32_t x = (uint32_t)(w[h >> 1] >> (32 * (h & 1)));
+#pragma unroll
+    for (int p = 0; p < PB; ++p) {
+      const uint32_t t = (x << (8 - BITS * (p + 1))) & TOP;
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        if (h * CW + j * PB + p < E) c[h * CW + j * PB + p] = (float)(int8_t)(t >> (8 * j));
+    }
+  }
+}
+
 template <int OP, int BITS, int OB, int LPB, int E>
 __global__ __launch_bounds__(256) void k_qelem_fast(const uint8_t* __restrict__ a, int64_t a_nbytes,
                                                     const float* __restrict__ sa_, const uint8_t* __restrict__ b,
@@ -233,22 +257,27 @@ __global__ __launch_bounds__(256) void k_qelem_fast(const uint8_t* __restrict__ 
         wb[k] &= keep;
       }
     }
+    // codes times 2^(8 - BITS) (codes_scaled); factors that multiply them
+    // are scaled by CS = 2^(BITS - 8): exact for every factor >= 2^-100 (a
+    // scale below that takes the codes back to their values instead)
+    constexpr float CS = BITS == 8 ? 1.0f : (BITS == 4 ? 0.0625f : 0.015625f);
     float ac[E], bc[E], cv[E];
     uint32_t cu[E];  // code bits (the low OB bits are the two's complement code)
+    codes_scaled<BITS, E, NW>(wa, ac);
+    codes_scaled<BITS, E, NW>(wb, bc);
+    if constexpr (OP == E_SUB) {
 #pragma unroll
-    for (int i = 0; i < E; ++i) {
-      const int32_t ca = (int32_t)((uint32_t)(wa[(i * BITS) >> 6] >> ((i * BITS) & 63)) << (32 - BITS)) >> (32 - BITS);
-      const int32_t cb = (int32_t)((uint32_t)(wb[(i * BITS) >> 6] >> ((i * BITS) & 63)) << (32 - BITS)) >> (32 - BITS);
-      ac[i] = (float)ca;
-      bc[i] = (float)(OP == E_SUB ? -cb : cb);
+      for (int i = 0; i < E; ++i) bc[i] = -bc[i];
     }
     float scale;
     if constexpr (OP == E_MUL) {
       // RN(prod / max_int) by Markstein's correction with y = RN(1/max_int):
-      // the products are 0 or at least 1 in magnitude
-      const float qinv = 1.0f / qf;
+      // the products are 0 or at least 1 in magnitude; the scaled codes'
+      // product over max_int * 2^(16 - 2 BITS) is the same quotient
+      constexpr float CS2 = CS * CS;
+      const float qs = qf / CS2, qinv = (1.0f / qf) * CS2;
 #pragma unroll
-      for (int i = 0; i < E; ++i) cu[i] = rne_clamped_bits(markstein(ac[i] * bc[i], qf, qinv), qf);
+      for (int i = 0; i < E; ++i) cu[i] = rne_clamped_bits(markstein(ac[i] * bc[i], qs, qinv), qf);
       scale = (sa * sb) * qf;
     } else {
       const float hi = fmaxf(sa, sb);
@@ -256,15 +285,26 @@ __global__ __launch_bounds__(256) void k_qelem_fast(const uint8_t* __restrict__ 
       const bool use_int = ratio <= 2.0f;  // uniform over the LPB lanes of the block
       float sc = hi;
       float ra_ = 1.0f, rb_ = 1.0f, m = 0.0f;
+      float f = CS;  // the factor the codes' products carry
+      if (BITS != 8 && __builtin_expect(!(fminf(sa, sb) >= 0x1p-100f), 0)) {
+#pragma unroll
+        for (int i = 0; i < E; ++i) {
+          ac[i] *= CS;
+          bc[i] *= CS;
+        }
+        f = 1.0f;
+      }
       // one form per block (the lanes of a block agree on use_int)
       if (use_int) {
         ra_ = sa / sc;
         rb_ = sb / sc;
+        const float fa = ra_ * f, fb = rb_ * f;
 #pragma unroll
-        for (int i = 0; i < E; ++i) cv[i] = rne(ac[i] * ra_) + rne(bc[i] * rb_);
+        for (int i = 0; i < E; ++i) cv[i] = rne(ac[i] * fa) + rne(bc[i] * fb);
       } else {
+        const float fa = sa * f, fb = sb * f;
 #pragma unroll
-        for (int i = 0; i < E; ++i) cv[i] = ac[i] * sa + bc[i] * sb;
+        for (int i = 0; i < E; ++i) cv[i] = ac[i] * fa + bc[i] * fb;
       }
 #pragma unroll
       for (int i = 0; i < E; ++i) m = fmaxf(m, __builtin_fabsf(cv[i]));
@@ -274,11 +314,10 @@ __global__ __launch_bounds__(256) void k_qelem_fast(const uint8_t* __restrict__ 
           sc = sc * 2.0f;
           ra_ = sa / sc;
           rb_ = sb / sc;
+          const float fa = ra_ * f, fb = rb_ * f;
 #pragma unroll
-          for (int i = 0; i < E; ++i) cv[i] = rne(ac[i] * ra_) + rne(bc[i] * rb_);
+          for (int i = 0; i < E; ++i) cv[i] = rne(ac[i] * fa) + rne(bc[i] * fb);
         }
-#pragma unroll
-        for (int i = 0; i < E; ++i) cu[i] = (uint32_t)(int32_t)__builtin_amdgcn_fmed3f(cv[i], -qf, qf);
       } else {
         sc = fmaxf(m, MXK_AMIN) / qf;
         // RN(sum / sc) by Markstein's correction for every element, without
@@ -287,8 +326,14 @@ __global__ __launch_bounds__(256) void k_qelem_fast(const uint8_t* __restrict__ 
         // rounds to code 0 below
         const float y = 1.0f / sc;
 #pragma unroll
-        for (int i = 0; i < E; ++i) cu[i] = rne_clamped_bits(markstein(cv[i], sc, y), qf);
+        for (int i = 0; i < E; ++i) cv[i] = markstein(cv[i], sc, y);
       }
+      // both forms end in one tail: the integer sums are already integers,
+      // so clamp + round is their clamp (the integer form used to run its
+      // own clamp and conversion, in every wave: the compiler did not
+      // branch around it)
+#pragma unroll
+      for (int i = 0; i < E; ++i) cu[i] = rne_clamped_bits(cv[i], qf);
       scale = sc;
     }
     uint32_t w[(ONB + 3) / 4];

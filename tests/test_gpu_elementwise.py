@@ -82,6 +82,32 @@ def test_qelementwise_vs_oracle(qa, op, a_name, b_name, block, shape, mode):
     assert _bits_eq(C._mx_packed, rp), "packed codes differ"
 
 
+@pytest.mark.parametrize("op", ["add", "sub", "mul"])
+@pytest.mark.parametrize("name", ["int2d", "int4d", "int8d"])
+@pytest.mark.parametrize("mode", ["near", "far", "mixed"])
+def test_qelementwise_tiny_and_zero_scales(qa, op, name, mode):
+    """The fused kernel multiplies codes scaled by 2^(8 - bits) with scales
+    scaled by 2^(bits - 8), exact for scales >= 2^-100; blocks whose scale
+    is smaller (down to subnormal) or zero take the codes back to their
+    values.  Operands with such scales in some blocks, against the oracle
+    bitwise."""
+    shape, block = (8, 512), 128
+    (pa, sa), (pb, sb), n = _operands(shape, 23, block, name, name, mode)
+    sa = sa.clone()
+    sb = sb.clone()
+    sa[::3] *= 2.0 ** -110
+    sb[1::4] *= 2.0 ** -125
+    sa[5] = 0.0
+    sb[7] = 1e-44
+    A = _mx(qa, pa, sa, name, shape, n, block)
+    B = _mx(qa, pb, sb, name, shape, n, block)
+    C = {"add": A + B, "sub": A - B, "mul": A * B}[op]
+    rp, rs, rname = orc.dispatch_qelementwise(op, pa, sa, name, pb, sb, name, n, block)
+    assert C._mx_dtype.name == rname
+    assert _bits_eq(C._mx_scales, rs), "scales differ"
+    assert _bits_eq(C._mx_packed, rp), "packed codes differ"
+
+
 @pytest.mark.parametrize("name", ["int1d", "int2d", "int3d", "int4d", "int5d", "int8d", "int16d", "float4d",
                                   "float8d", "int4dh"])
 def test_neg_vs_oracle(qa, name):
