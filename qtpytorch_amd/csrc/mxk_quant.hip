@@ -995,15 +995,16 @@ static int grid_capped(int64_t work_items, int per_block, int cap_per_cu) {
   if (cap_per_cu <= 0) return (int)std::min<int64_t>(blocks, (int64_t)0x7FFFFFFF);
   return (int)std::min<int64_t>(blocks, (int64_t)num_cus() * cap_per_cu);
 }
-// k_quant_fast: fp32 int codes uncapped; 16-bit int codes 128; 'v' from
-// 16-bit 32; FP4 codes 384 (float4d at 2^28: 196 us against 212 at 128, 198
+// k_quant_fast: fp32 int codes uncapped; 16-bit int codes 128 (config 5
+// int4d 117 us, 118 uncapped or at 256, 124 at 64); 'v' from 16-bit 64
+// (config 5 int8dv 132-135 us against 137-139 at 32, 143 at 128); FP4 codes 384 (float4d at 2^28: 196 us against 212 at 128, 198
 // at 256 and 512, 197 uncapped), FP8 codes 192 (float8d 228 us against 233
 // at 128, 231 at 160, 238 at 256, 240 at 96); the rest 64.
 template <typename T, int MODE, int BITS>
 constexpr int quant_fast_cap() {
   return (sizeof(T) == 4 && (MODE == Q_INT || MODE == Q_INT1)) ? 0
          : (sizeof(T) == 2 && (MODE == Q_INT || MODE == Q_INT1)) ? 128
-         : (sizeof(T) == 2 && MODE == Q_VEC) ? 32
+         : (sizeof(T) == 2 && MODE == Q_VEC) ? 64
          : MODE == Q_FP ? (BITS == 4 ? 384 : 192) : 64;
 }
 // k_dequant_fast: codes decoded without a table (int8, FP8) uncapped; the
