@@ -338,15 +338,17 @@ __device__ void build_tables(float* P, float* G) {
 // fmt_value(c) / 480 = (m / 15) * 2^(max(e,1) - 15); the power of two scales
 // exactly (the smallest nonzero value, 2^-14 / 15, is normal), so the value
 // is RN(m / 15) scaled, and RN(m / 15) is the exactly rounded quotient of two
-// small integers.  Index 127 gives -0.0, as in the table.
+// small integers.  Index 127 gives -0.0, as in the table.  RN(m / 15) for
+// the 16 numerators is fma(m, A, RN(m * B)) with A = RN(1/15) and B =
+// RN(1/15 - A) (checked against the division for every m; 2 VALU where the
+// Markstein quotient took 4), both scaled by 2^-15 here (exact).
 __device__ __forceinline__ float fp8_grid_value(uint32_t f) {
-  const uint32_t neg = ((f >> 7) & 1u) ^ 1u;
-  const uint32_t c = (f ^ (neg * 0x7Fu)) & 0x7Fu;
+  const uint32_t c = (f ^ ((f >> 7) - 1u)) & 0x7Fu;  // f ^ 0x7F below 128, f - 128 above
   const uint32_t e = c >> 3;
-  const float m = (float)((c & 7u) | (e != 0u ? 8u : 0u));
-  const float q = div_rn_nochk(m, 15.0f, 0x1.111112p-4f);  // RN(1/15)
-  const float g = __builtin_ldexpf(q, (int)(e != 0u ? e : 1u) - 15);
-  return neg ? -g : g;
+  const float m = (float)((c & 7u) | (min(e, 1u) << 3));
+  const float q = __builtin_fmaf(m, 0x1.111112p-19f, m * -0x1.dddddep-44f);  // RN(m / 15) * 2^-15
+  const float g = __builtin_ldexpf(q, (int)max(e, 1u));
+  return f < 128u ? -g : g;
 }
 
 // Index of y in the sorted grid: #{mids < y} (torch.bucketize, right=False).
@@ -478,6 +480,7 @@ template <int BITS>
 struct Tables {
   static constexpr int H = 1 << (BITS - 1), N = FpKeys<BITS>::N;
   float P[H + 1];     // build_tables' P: -inf, the positive mids, +inf
+  float G[2 * H];     // build_tables' G: the sorted grid (G[H - 1] = -0.0)
   int key[2 * N][2];  // positive keys 0..N-1, then negative keys 0..N-1
 };
 template <int BITS>
@@ -488,6 +491,10 @@ constexpr Tables<BITS> make_tables() {
   t.P[0] = -__builtin_inff();
   t.P[H] = __builtin_inff();
   for (int j = 1; j < H; ++j) t.P[j] = (grid(BITS, j - 1) + grid(BITS, j)) * 0.5f;
+  for (int c = 0; c < H; ++c) {
+    t.G[H + c] = grid(BITS, c);
+    t.G[H - 1 - c] = -grid(BITS, c);
+  }
   for (int k = 0; k < K::N; ++k) {
     const float lo = k == 0 ? 0.0f : __builtin_bit_cast(float, (uint32_t)(k + K::BASE) << K::SHIFT);
     const float hi =
@@ -517,6 +524,14 @@ inline __device__ const fpt::Tables<8> FpTables<8>::t = fpt::make_tables<8>();
 // build_tables<BITS>' P (FP4's is its constants), in device memory
 template <int BITS>
 __device__ __forceinline__ const float* fp_mids() { return FpTables<BITS>::t.P; }
+
+// Copies the sorted grid (2H floats) into G and waits for the workgroup.
+template <int BITS>
+__device__ __forceinline__ void load_fp_grid(float* G) {
+  constexpr int H = 1 << (BITS - 1);
+  for (int t = threadIdx.x; t < 2 * H; t += blockDim.x) G[t] = FpTables<BITS>::t.G[t];
+  __syncthreads();
+}
 
 // Copies the 2 * N key entries into T's layout (FP4 leaves the entries below
 // OFF and between the halves unwritten) and waits for the workgroup.

@@ -782,11 +782,17 @@ __global__ __launch_bounds__(256) void k_dequant_fast(const uint8_t* __restrict_
   constexpr int H = MODE == Q_FP ? (1 << (BITS - 1)) : 1;
   // int codes of up to 4 bits decode through a table of their values as
   // floats (the same float(code) * s): measured faster than the bit-field
-  // extract and conversion; a 256-entry table for 8-bit codes was slower
+  // extract and conversion; a 256-entry table for int8 codes was slower.
+  // FP4 codes read the sorted grid, made by the compiler and copied in
+  // (float4d dequantize 182 -> 176-181 us against building it per
+  // workgroup); FP8 values are computed (fp8_grid_value): its 256-entry
+  // grid in LDS measured 220 -> 276-280 us, the random codes' LDS reads
+  // conflicting on the banks
   constexpr bool ITAB = (MODE == Q_INT && BITS <= 4) || MODE == Q_INT1;
+  constexpr bool GTAB = MODE == Q_FP && BITS == 4;
   constexpr int TS = ITAB ? (1 << BITS) : 2 * H;
   __shared__ float sG[TS];
-  if constexpr (MODE == Q_FP && BITS != 8) build_tables<BITS>(nullptr, sG);
+  if constexpr (GTAB) load_fp_grid<BITS>(sG);
   if constexpr (ITAB) {
     // int1: code 0 -> +s, 1 -> -s (mxtorch.py:1553-1557), i.e. (+-1) * s exactly
     for (int c = threadIdx.x; c < TS; c += blockDim.x)
@@ -828,7 +834,7 @@ __global__ __launch_bounds__(256) void k_dequant_fast(const uint8_t* __restrict_
         f32x4v v;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          if constexpr (ITAB) v[i] = sG[(w[u] >> (i * BITS)) & ((1u << BITS) - 1u)] * sc[u];
+          if constexpr (ITAB || GTAB) v[i] = sG[(w[u] >> (i * BITS)) & ((1u << BITS) - 1u)] * sc[u];
           else v[i] = decode_field<MODE, BITS>(w[u], i * BITS, sc[u], sG);
         }
         __builtin_nontemporal_store(v, reinterpret_cast<f32x4v*>(out + j0));
