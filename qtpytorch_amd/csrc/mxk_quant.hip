@@ -83,15 +83,16 @@ __global__ __launch_bounds__(256) void k_quant_fast(const T* __restrict__ x, int
   constexpr int B = E * LPB;
   constexpr int GPW = 64 / LPB;
   constexpr int GPB = 4 * GPW;
-  // fp32: a lane's E elements are Q chunks of CH consecutive elements (one
+  // A lane's E elements are Q chunks of CH consecutive elements (one
   // 16-byte load each), chunk q at offset q * B / Q in the block, so that
   // every load instruction of a wave covers whole lines.  1-bit codes of a
-  // chunk fill half a byte: lanes 2i and 2i+1 swap nibbles (DPP) and the
-  // even lane stores the byte.  16-bit inputs keep one consecutive run
-  // (measured faster).
+  // fp32 chunk fill half a byte: lanes 2i and 2i+1 swap nibbles (DPP) and
+  // the even lane stores the byte.  (16-bit inputs used to keep one
+  // consecutive run of 32 bytes per lane, half of each line per load
+  // instruction: config 5 int4d 117 -> 108 us split, int8dv 136 -> 132.)
   constexpr int PER16 = 16 / (int)sizeof(T);
   constexpr bool NIB = sizeof(T) == 4 && BITS == 1 && E / PER16 > 1;
-  constexpr bool SPLIT = sizeof(T) == 4 && E / PER16 > 1 && ((PER16 * BITS) % 8 == 0 || NIB);
+  constexpr bool SPLIT = E / PER16 > 1 && ((PER16 * BITS) % 8 == 0 || NIB);
   constexpr int Q = SPLIT ? E / PER16 : 1;
   constexpr int CH = E / Q;
   constexpr int NW = (CH * BITS + 31) / 32;
@@ -1068,7 +1069,7 @@ static bool try_fast_e(const T* x, int64_t n, int64_t nb, int block, uint8_t* pa
                        int64_t n_store, float* scales, float qf, hipStream_t st) {
   constexpr int PER16 = 16 / (int)sizeof(T);
   constexpr bool NIB = sizeof(T) == 4 && BITS == 1 && E / PER16 > 1;
-  constexpr bool SPLIT = sizeof(T) == 4 && E / PER16 > 1 && ((PER16 * BITS) % 8 == 0 || NIB);
+  constexpr bool SPLIT = E / PER16 > 1 && ((PER16 * BITS) % 8 == 0 || NIB);
   constexpr int CH = SPLIT ? PER16 : E;
   constexpr int NB = NIB ? 1 : CH * BITS / 8;
   if (block % E != 0 || !is_pow2(block / E) || block / E > 64 || block / E < 2) return false;
