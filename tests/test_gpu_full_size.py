@@ -158,3 +158,46 @@ def test_empty_batch_linear_and_gemm(qa):
     res = qa.ops.qscale_gemm(torch.empty(0, dtype=torch.int8, device=dev()), torch.empty(0, device=dev()), pb, sb,
                              0, 256, 128, 8, 128, 16, want_c=True)
     assert res["packed"].numel() == 0 and res["scales"].numel() == 0 and tuple(res["c"].shape) == (0, 128)
+
+
+@pytest.mark.parametrize("dtype,src,n", [
+    ("float4d", torch.float32, (1 << 28) + 3 * 128 + 5),   # 1-2 steps per workgroup (384 per CU)
+    ("float8d", torch.float32, (1 << 28) + 7 * 128 + 100),  # 2-3 steps (192 per CU): pairs and an odd step
+    ("int4d", torch.float16, (1 << 28) + 128 + 1),          # 2 steps (128 per CU), a pair
+    ("int8dv", torch.float16, (1 << 28) + 9 * 128),         # 4 steps (64 per CU), pairs
+    ("int4dh", torch.float32, (1 << 29) + 5 * 128),          # 2 steps (256 per CU)
+])
+def test_quantize_steps_match_chunked(qa, dtype, src, n):
+    """The quantizers walk a capped grid in steps of whole blocks: steps that
+    end inside the data load and store through buffer resources with the
+    loop unrolled twice, the steps reaching the end check each lane.  Large
+    ragged tensors (several steps per workgroup, odd and even counts, a
+    tail) must give the codes and scales of the same tensor quantized in
+    2^24-element chunks (one step per workgroup, blocks being independent),
+    every block bitwise."""
+    g = torch.Generator(device="cuda").manual_seed(n % 1000)
+    x = torch.randn(n, generator=g, device="cuda").to(src)
+    dt = qa.get_mx_dtype(dtype)
+    seed = 99 if dt.is_hadamard else None
+    if dt.is_hadamard:
+        # the rotation runs along the last dimension: rows of 128, as config 4
+        x = x[: n - n % 128].reshape(-1, 128)
+        n = x.numel()
+    packed, scales, nn = qa.ops.quantize(x, dt, 128, seed=seed)
+    assert nn == n
+    chunk = 1 << 24
+    parts_p, parts_s = [], []
+    for lo in range(0, n, chunk):
+        part = x[lo // 128: (lo + chunk) // 128] if dt.is_hadamard else x[lo: lo + chunk]
+        p, s, _ = qa.ops.quantize(part, dt, 128, seed=seed)
+        parts_p.append(p.view(torch.uint8).reshape(-1))
+        parts_s.append(s.reshape(-1))
+    cp = torch.cat(parts_p)
+    cs = torch.cat(parts_s)
+    pw = packed.view(torch.uint8).reshape(-1)
+    assert pw.numel() == cp.numel() and scales.numel() == cs.numel()
+    assert torch.equal(scales.reshape(-1).view(torch.int32), cs.view(torch.int32)), "scales differ"
+    bad = (pw != cp).nonzero()
+    assert bad.numel() == 0, f"{bad.numel()} packed bytes differ, first at {int(bad[0])}"
+    del x, packed, scales, cp, cs, pw
+    torch.cuda.empty_cache()
