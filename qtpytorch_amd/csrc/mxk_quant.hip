@@ -11,10 +11,12 @@
 // where a' = max(absmax(block), fl32(1e-12)).
 //
 // Layout of work: a "group" of LPB consecutive lanes owns one block of
-// B = E*LPB elements; each lane holds E consecutive elements (16-byte
-// vector loads), the block absmax is a DPP / ds_swizzle reduction across
-// the group, and each lane packs its E codes into E*bits/8 bytes that it
-// stores directly.  A 256-thread workgroup walks blocks grid-stride.
+// B = E*LPB elements; each lane holds E elements as 16-byte chunks (half a
+// block apart when there are two, so that each load instruction covers
+// whole lines), the block absmax is a DPP / ds_swizzle reduction across
+// the group, and each lane packs its codes into E*bits/8 bytes that it
+// stores directly.  A 256-thread workgroup walks steps of blocks
+// grid-stride (k_quant_fast describes the steps).
 #include "mxk_internal.h"
 
 #include <algorithm>
@@ -98,7 +100,6 @@ __global__ __launch_bounds__(256) void k_quant_fast(const T* __restrict__ x, int
   constexpr int NW = (CH * BITS + 31) / 32;
   constexpr int NB = NIB ? 1 : CH * BITS / 8;
   constexpr uint32_t MASK = BITS == 32 ? 0xFFFFFFFFu : ((1u << BITS) - 1u);
-  constexpr int H = MODE == Q_FP ? (1 << (BITS - 1)) : 1;
   const float* sP = fp_mids<MODE == Q_FP ? BITS : 4>();  // read only by the non-finite path
   __shared__ int2 sK[fp_keys_n<MODE, BITS>()];
 
