@@ -179,10 +179,10 @@ __device__ __forceinline__ void load_codes(__amdgpu_buffer_rsrc_t r, uint32_t of
   }
 }
 
-// RN(a / b) by Markstein's correction with y = RN(1/b), for callers whose
-// quotient is only rounded to an integer code afterwards: a zero quotient
-// may come out with either sign, which codes the same.  Exact unless
-// 0 < |a| < 2^-96 (the callers state why that cannot change a code).
+// RN(a / b) by Markstein's correction with y = RN(1/b): correctly rounded
+// unless 0 < |a| < 2^-96 (the callers state why that cannot change their
+// result), and a zero quotient may come out with either sign (callers that
+// round it to an integer code code both zeros the same).
 __device__ __forceinline__ float markstein(float a, float b, float y) {
   const float q0 = a * y;
   return __builtin_fmaf(__builtin_fmaf(-q0, b, a), y, q0);
@@ -232,6 +232,7 @@ __global__ __launch_bounds__(256) void k_qelem_fast(const uint8_t* __restrict__ 
   constexpr int INB = E * BITS / 8, ONB = E * OB / 8;
   constexpr uint32_t OMASK = (1u << OB) - 1u;
   const float qf = (float)((1 << (BITS - 1)) - 1);
+  const float qinv_c = 1.0f / qf;  // RN(1/q)
   const __amdgpu_buffer_rsrc_t ra = make_rsrc(a, (uint32_t)a_nbytes);
   const __amdgpu_buffer_rsrc_t rb = make_rsrc(b, (uint32_t)b_nbytes);
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -281,8 +282,14 @@ __global__ __launch_bounds__(256) void k_qelem_fast(const uint8_t* __restrict__ 
       scale = (sa * sb) * qf;
     } else {
       const float hi = fmaxf(sa, sb);
-      const float ratio = hi / fmaxf(fminf(sa, sb), 1e-30f);
-      const bool use_int = ratio <= 2.0f;  // uniform over the LPB lanes of the block
+      // RN(hi / lo) <= 2 exactly when hi / lo <= 2 + 2^-23 (the midpoint
+      // above 2 rounds to even, to 2): hi - 2 lo <= 2^-23 lo, where the FMA
+      // difference is exact near the boundary (hi and 2 lo within a factor
+      // of 2) and 2^-23 lo is exact (lo >= 1e-30); non-finite scales take
+      // the division's branches (an infinite hi or NaN difference: float
+      // form).  Two VALU in place of a division.
+      const float lo_ = fmaxf(fminf(sa, sb), 1e-30f);
+      const bool use_int = __builtin_fmaf(-2.0f, lo_, hi) <= 0x1p-23f * lo_;  // uniform over the block's lanes
       float sc = hi;
       float ra_ = 1.0f, rb_ = 1.0f, m = 0.0f;
       float f = CS;  // the factor the codes' products carry
@@ -319,7 +326,9 @@ __global__ __launch_bounds__(256) void k_qelem_fast(const uint8_t* __restrict__ 
           for (int i = 0; i < E; ++i) cv[i] = rne(ac[i] * fa) + rne(bc[i] * fb);
         }
       } else {
-        sc = fmaxf(m, MXK_AMIN) / qf;
+        // RN(max / q) by Markstein's correction with RN(1/q): the dividend
+        // is at least fl32(1e-12), so the quotient is correctly rounded
+        sc = markstein(fmaxf(m, MXK_AMIN), qf, qinv_c);
         // RN(sum / sc) by Markstein's correction for every element, without
         // div_rn_all's small-dividend vote: sc >= 1e-12 / 127 > 2^-47, so a
         // dividend below 2^-96 has |quotient| < 2^-49 on either path and
