@@ -1981,7 +1981,7 @@ int mxk_linear_wq_noalloc(const void* x, int x_type, int64_t M, int64_t K, const
                                   " bytes of split-K workspace, more than the " +
                                   std::to_string(NOALLOC_SCRATCH_BYTES) +
                                   "-byte static scratch (pass w_scales_t, or use mxk_linear_wq with a workspace)");
-  } else if (kind == MXK_KIND_INT) {
+  } else {
     // the MFMA path when its buffers fit the scratch; the generic kernel otherwise
     const size_t m = linear_mfma_workspace(M, K, N, bits, block, false);
     if (m > 0 && m <= NOALLOC_SCRATCH_BYTES) {

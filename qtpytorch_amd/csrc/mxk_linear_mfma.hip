@@ -1,5 +1,6 @@
-// MFMA weight-only linear for gfx950: the shapes the int4 decode kernels do
-// not take (more than 16 rows of x, int8 weights).
+// MFMA weight-only linear for gfx950: the shapes and formats the int4
+// decode kernels do not take (more than 16 rows of x; int2d, int8d, float4d
+// and float8d weights at any row count).
 //
 //   mx_linear.forward (mxtorch.py:7454-7473), weight [K][N] as
 //   quantize(W.t()) with blocks of 128 along N:
@@ -11,7 +12,9 @@
 //
 // Both products run on v_mfma_f32_16x16x32_f16 with fp32 accumulation.  The
 // codes themselves are the B operand: integers |c| <= 127 are exact f16
-// values.  The x side is an f16 pair hi + lo (22 significant bits), so each
+// values, and so are the FP4 E2M1 and FP8 E4M3 values v of the float grids,
+// whose grid value RN(v / vmax) takes the factor RN(1 / vmax) in the
+// epilogue instead (vmax 6 or 480).  The x side is an f16 pair hi + lo (22 significant bits), so each
 // term x * s * c carries a relative error of about 2^-22 and sums in fp32;
 // the reference rounds RN(c * s) and runs an fp32 sgemm (about 2^-24 per
 // term, in a library-defined order).
@@ -87,6 +90,58 @@ __device__ __forceinline__ uint32_t lm_i8pair(uint32_t d) {
   const h2v r = __builtin_bit_cast(h2v, e) - h2v{(_Float16)1152.0f, (_Float16)1152.0f};
   return __builtin_bit_cast(uint32_t, r);
 }
+// Two int2 codes at bits 0-1 and 16-17 of d (other bits ignored):
+// 0x6400 | (c ^ 2) is 1024 + (c + 2), less 1026.
+__device__ __forceinline__ uint32_t lm_i2pair(uint32_t d) {
+  const uint32_t e = (d & 0x00030003u) ^ 0x64026402u;
+  const h2v r = __builtin_bit_cast(h2v, e) - h2v{(_Float16)1026.0f, (_Float16)1026.0f};
+  return __builtin_bit_cast(uint32_t, r);
+}
+// Two float codes (indices into the sorted grid of 2^B values: B = 4 FP4
+// E2M1, B = 8 FP8 E4M3 with exponent 15 a normal binade) at bits 0..B-1 and
+// 16..16+B-1 of d (the bits above each code ignored) as the f16 pair of their
+// grid values times vmax (6 or 480): the format's own values v, exact in f16.
+// c ^ 2^(B-1) is the B-bit one's complement of +-m, m the bit pattern of
+// |v| (the grid is symmetric and sorted); moved to the top of a 16-bit half,
+// xor-ed with its sign mask and shifted to f16's mantissa position, m is the
+// f16 of |v| * 2^-14 (FP4) or 2^-8 (FP8), subnormals included, and one f16
+// multiply by the power of two gives v.
+template <int B>
+__device__ __forceinline__ uint32_t lm_fpair(uint32_t d) {
+  typedef short s2v __attribute__((ext_vector_type(2)));
+  // code at the top of each half, its top bit flipped
+  const uint32_t x = (d << (16 - B)) ^ 0x80008000u;
+  const uint32_t sm = __builtin_bit_cast(uint32_t, __builtin_bit_cast(s2v, x) >> (short)15);
+  const uint32_t y = x ^ sm;
+  const uint32_t m = (y >> (B == 4 ? 3 : 1)) & (B == 4 ? 0x0E000E00u : 0x3F803F80u);
+  const uint32_t f = (sm & 0x80008000u) | m;
+  constexpr _Float16 P = (_Float16)(B == 4 ? 16384.0f : 256.0f);
+  const h2v r = __builtin_bit_cast(h2v, f) * h2v{P, P};
+  return __builtin_bit_cast(uint32_t, r);
+}
+
+// Weight formats: the code width in the low 4 bits, 16 for float grids
+enum : int { LM_I2 = 2, LM_I4 = 4, LM_I8 = 8, LM_F4 = 16 + 4, LM_F8 = 16 + 8 };
+__host__ __device__ constexpr int lm_bits(int fmt) { return fmt & 15; }
+// The factor the outputs take for B fragments that hold v instead of the
+// grid value v / vmax: RN(1/6), RN(1/480), or 1 for integer codes.
+__host__ __device__ constexpr float lm_post(int fmt) {
+  return fmt == LM_F4 ? 1.0f / 6.0f : fmt == LM_F8 ? 1.0f / 480.0f : 1.0f;
+}
+inline int lm_format(int kind, int bits) {
+  if (kind == MXK_KIND_INT) return bits == 2 ? LM_I2 : bits == 4 ? LM_I4 : bits == 8 ? LM_I8 : 0;
+  if (kind == MXK_KIND_FLOAT) return bits == 4 ? LM_F4 : bits == 8 ? LM_F8 : 0;
+  return 0;
+}
+// Two codes of a format (layout of its width) as an f16 B-operand pair
+template <int FMT>
+__device__ __forceinline__ uint32_t lm_pair(uint32_t d) {
+  if constexpr (FMT == LM_I4) return lm_i4pair(d);
+  else if constexpr (FMT == LM_I8) return lm_i8pair(d);
+  else if constexpr (FMT == LM_I2) return lm_i2pair(d);
+  else return lm_fpair<lm_bits(FMT)>(d);
+}
+
 // v_perm_b32 selector: byte a of s1 into byte 0, byte b of s0 into byte 2, zeros in bytes 1 and 3
 __host__ __device__ constexpr uint32_t lm_sel(int a, int b) {
   return (uint32_t)a | 0x0C00u | ((uint32_t)(4 + b) << 16) | 0x0C000000u;
@@ -121,7 +176,7 @@ __device__ __forceinline__ void lm_barrier() {
 // A wave's threads are k step w, lanes 0..63 in order.
 template <int BITS>
 struct KnCodes {
-  uint32_t w[BITS == 4 ? 8 : 16];
+  uint32_t w[BITS == 8 ? 16 : 8];
 };
 
 template <int BITS>
@@ -131,7 +186,9 @@ __device__ __forceinline__ void kn_load(KnCodes<BITS>& c, __amdgpu_buffer_rsrc_t
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
     const int64_t row = k0 + 8 * r8 + i;
-    if constexpr (BITS == 4) {
+    if constexpr (BITS == 2) {
+      c.w[i] = __builtin_amdgcn_raw_buffer_load_b16(rw, (int)(row * (N / 4) + nb * 32 + 2 * c8), 0, 0);
+    } else if constexpr (BITS == 4) {
       c.w[i] = buf_load_b32(rw, (uint32_t)(row * (N / 2) + nb * 64 + 4 * c8), 0u);
     } else {
       const auto v = __builtin_amdgcn_raw_buffer_load_b64(rw, (int)(row * N + nb * 128 + 8 * c8), 0, 0);
@@ -142,28 +199,33 @@ __device__ __forceinline__ void kn_load(KnCodes<BITS>& c, __amdgpu_buffer_rsrc_t
 }
 
 // the B fragment of column tile t (column 8 c8 + t) from the thread's block
-template <int BITS>
-__device__ __forceinline__ u4v kn_frag(const KnCodes<BITS>& c, int t) {
+template <int FMT>
+__device__ __forceinline__ u4v kn_frag(const KnCodes<lm_bits(FMT)>& c, int t) {
+  constexpr int BITS = lm_bits(FMT);
   u4v f;
 #pragma unroll
   for (int q = 0; q < 4; ++q) {
-    if constexpr (BITS == 4) {
+    if constexpr (BITS == 2) {
+      // rows 2q and 2q+1 (16 bits each) side by side: column 8 c8 + t at bits 2t, 2t + 1
+      const uint32_t d = c.w[2 * q] | (c.w[2 * q + 1] << 16);
+      f[q] = lm_pair<FMT>(d >> (2 * t));
+    } else if constexpr (BITS == 4) {
       // byte t/2 of rows 2q and 2q+1: the low nibbles are column 8 c8 + t for even t
       const uint32_t d = __builtin_amdgcn_perm(c.w[2 * q + 1], c.w[2 * q], lm_sel(t >> 1, t >> 1));
-      f[q] = lm_i4pair((t & 1) ? d >> 4 : d);
+      f[q] = lm_pair<FMT>((t & 1) ? d >> 4 : d);
     } else {
       const int h = t >> 2, u = t & 3;
-      f[q] = lm_i8pair(__builtin_amdgcn_perm(c.w[2 * (2 * q + 1) + h], c.w[2 * (2 * q) + h], lm_sel(u, u)));
+      f[q] = lm_pair<FMT>(__builtin_amdgcn_perm(c.w[2 * (2 * q + 1) + h], c.w[2 * (2 * q) + h], lm_sel(u, u)));
     }
   }
   return f;
 }
 
-template <int BITS>
-__device__ __forceinline__ void kn_store(const KnCodes<BITS>& c, uint8_t* sB, int tid) {
+template <int FMT>
+__device__ __forceinline__ void kn_store(const KnCodes<lm_bits(FMT)>& c, uint8_t* sB, int tid) {
   const int ks = tid >> 6, lane = tid & 63;
 #pragma unroll
-  for (int t = 0; t < 8; ++t) *reinterpret_cast<u4v*>(sB + lm_frag_off(ks, t, lane)) = kn_frag<BITS>(c, t);
+  for (int t = 0; t < 8; ++t) *reinterpret_cast<u4v*>(sB + lm_frag_off(ks, t, lane)) = kn_frag<FMT>(c, t);
 }
 
 // The same 8 x 8 blocks from the tiled copy of mxk_linear_prepack_weight:
@@ -207,17 +269,23 @@ __device__ __forceinline__ void kn_store_tiled(const KnTiled& c, uint8_t* sB, in
 // 16 (p / 16) + 8 (p % 2) + (p / 2) % 8, so the two columns of a 16-lane
 // store group share a tile and differ in j (no bank conflicts).
 // int8: 16 lanes read one column's 256 bytes; 16 bytes are two k octets.
+// int2: 4 lanes read one column's 64 bytes, each 16 bytes two k steps; the
+// 4 columns of a 16-lane store group share a tile and differ in j.
 template <int BITS>
 struct NkCodes {
-  u4v w[BITS == 4 ? 2 : 4];
+  u4v w[BITS == 4 ? 2 : BITS == 8 ? 4 : 1];
 };
 
 __device__ __forceinline__ int nk4_col(int p) { return 16 * (p >> 4) + 8 * (p & 1) + ((p >> 1) & 7); }
+__device__ __forceinline__ int nk2_col(int p) { return ((p >> 4) & 7) + 8 * (p & 15); }
 
 template <int BITS>
 __device__ __forceinline__ void nk_load(NkCodes<BITS>& c, __amdgpu_buffer_rsrc_t rw, int64_t k0, int64_t K,
                                         int64_t nb, int tid) {
-  if constexpr (BITS == 4) {
+  if constexpr (BITS == 2) {
+    const int64_t n = nb * 128 + nk2_col(tid >> 2);
+    c.w[0] = buf_load_b128(rw, (uint32_t)(n * (K / 4) + k0 / 4 + 16 * (tid & 3)), 0u);
+  } else if constexpr (BITS == 4) {
     const int q = tid & 7;
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
@@ -234,9 +302,31 @@ __device__ __forceinline__ void nk_load(NkCodes<BITS>& c, __amdgpu_buffer_rsrc_t
   }
 }
 
-template <int BITS>
-__device__ __forceinline__ void nk_store(const NkCodes<BITS>& c, uint8_t* sB, int tid) {
-  if constexpr (BITS == 4) {
+template <int FMT>
+__device__ __forceinline__ void nk_store(const NkCodes<lm_bits(FMT)>& c, uint8_t* sB, int tid) {
+  constexpr int BITS = lm_bits(FMT);
+  if constexpr (BITS == 2) {
+    // k step 2q + s is dwords 2s, 2s+1; octet v is bytes 2 (v & 1), +1 of
+    // dword 2s + v / 2.  Byte b of wd beside byte b of wd >> 2 holds the
+    // codes (0, 1) at bits 0-1 and 16-17, and (2, 3) four bits higher.
+    const int q = tid & 3, col = nk2_col(tid >> 2);
+    const int t = col & 7, j = col >> 3;
+#pragma unroll
+    for (int sv = 0; sv < 4; ++sv) {
+      const uint32_t wd = c.w[0][sv], sh = wd >> 2;
+#pragma unroll
+      for (int vl = 0; vl < 2; ++vl) {
+        u4v f;
+#pragma unroll
+        for (int bb = 0; bb < 2; ++bb) {
+          const uint32_t d = __builtin_amdgcn_perm(sh, wd, lm_sel(2 * vl + bb, 2 * vl + bb));
+          f[2 * bb] = lm_pair<FMT>(d);
+          f[2 * bb + 1] = lm_pair<FMT>(d >> 4);
+        }
+        *reinterpret_cast<u4v*>(sB + lm_frag_off(2 * q + (sv >> 1), t, j + 16 * (2 * (sv & 1) + vl))) = f;
+      }
+    }
+  } else if constexpr (BITS == 4) {
     const int ks = tid & 7;
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
@@ -247,7 +337,7 @@ __device__ __forceinline__ void nk_store(const NkCodes<BITS>& c, uint8_t* sB, in
         const uint32_t lo4 = c.w[h][v] & 0x0F0F0F0Fu, hi4 = (c.w[h][v] >> 4) & 0x0F0F0F0Fu;
         u4v f;
 #pragma unroll
-        for (int p = 0; p < 4; ++p) f[p] = lm_i4pair(__builtin_amdgcn_perm(hi4, lo4, lm_sel(p, p)));
+        for (int p = 0; p < 4; ++p) f[p] = lm_pair<FMT>(__builtin_amdgcn_perm(hi4, lo4, lm_sel(p, p)));
         *reinterpret_cast<u4v*>(sB + lm_frag_off(ks, t, j + 16 * v)) = f;
       }
     }
@@ -265,7 +355,7 @@ __device__ __forceinline__ void nk_store(const NkCodes<BITS>& c, uint8_t* sB, in
         for (int p = 0; p < 4; ++p) {
           const uint32_t wd = c.w[h][2 * e + (p >> 1)];
           const int b = 2 * (p & 1);
-          f[p] = lm_i8pair(__builtin_amdgcn_perm(wd, wd, lm_sel(b, b + 1)));
+          f[p] = lm_pair<FMT>(__builtin_amdgcn_perm(wd, wd, lm_sel(b, b + 1)));
         }
         *reinterpret_cast<u4v*>(sB + lm_frag_off(ks, t, j + 16 * g)) = f;
       }
@@ -333,7 +423,7 @@ struct NkA {
   u4v l[2];
 };
 
-template <int BITS, int WM, bool NK, bool TILED = false>
+template <int FMT, int WM, bool NK, bool TILED = false>
 __global__ __launch_bounds__(LM_THREADS, 1) void k_linear_mfma(
     const float* __restrict__ xs,        // [K][N]: x' [M][Kp] fp32
     const _Float16* __restrict__ xh,     // [N][K]: hi of x' [M][Kp]
@@ -342,9 +432,9 @@ __global__ __launch_bounds__(LM_THREADS, 1) void k_linear_mfma(
     int sc_kb_major, const int* __restrict__ ex, int* __restrict__ es, const uint8_t* __restrict__ w,
     int M, int64_t K, int64_t Kp, int64_t N, int sps, const float* __restrict__ bias, float* __restrict__ out,
     float* __restrict__ part) {
-  constexpr int WK = 8 / WM, KPW = 8 / WK;
+  constexpr int BITS = lm_bits(FMT), WK = 8 / WM, KPW = 8 / WK;
   using A = typename std::conditional<NK, NkA, KnA>::type;
-  static_assert(!TILED || BITS == 4, "the tiled copies hold int4 weights");
+  static_assert(!TILED || FMT == LM_I4, "the tiled copies hold int4 weights");
   using Codes = typename std::conditional<NK, NkCodes<BITS>,
                                           typename std::conditional<TILED, KnTiled, KnCodes<BITS>>::type>::type;
   __shared__ __attribute__((aligned(1024))) uint8_t sB[2 * LM_STAGE_BYTES];
@@ -424,9 +514,9 @@ __global__ __launch_bounds__(LM_THREADS, 1) void k_linear_mfma(
   };
   auto store_codes = [&](const Codes& c, uint8_t* dst) {
     if constexpr (NK && TILED) nk_store_tiled(c, dst, tid);
-    else if constexpr (NK) nk_store<BITS>(c, dst, tid);
+    else if constexpr (NK) nk_store<FMT>(c, dst, tid);
     else if constexpr (TILED) kn_store_tiled(c, dst, tid);
-    else kn_store<BITS>(c, dst, tid);
+    else kn_store<FMT>(c, dst, tid);
   };
 
   f4v acc[2][8], P[2][8];
@@ -541,7 +631,7 @@ __global__ __launch_bounds__(LM_THREADS, 1) void k_linear_mfma(
 #pragma unroll
           for (int t = 0; t < 8; ++t) {
             if constexpr (TILED) bt[t] = __builtin_bit_cast(h8v, kn_frag_tiled(cq[i], t));
-            else bt[t] = __builtin_bit_cast(h8v, kn_frag<BITS>(cq[i], t));
+            else bt[t] = __builtin_bit_cast(h8v, kn_frag<FMT>(cq[i], t));
           }
           if (st + DS < st1) load_codes(cq[i], st + DS);
           h8v ahi[2], alo[2];
@@ -656,7 +746,10 @@ __global__ __launch_bounds__(LM_THREADS, 1) void k_linear_mfma(
       } else {
         const int e = -(ex[m] + esb);
 #pragma unroll
-        for (int t = 0; t < 8; ++t) v[t] = __builtin_ldexpf(acc[i][t][r], e) + bv[t];
+        for (int t = 0; t < 8; ++t) {
+          if constexpr (lm_post(FMT) != 1.0f) v[t] = __builtin_ldexpf(acc[i][t][r], e) * lm_post(FMT) + bv[t];
+          else v[t] = __builtin_ldexpf(acc[i][t][r], e) + bv[t];
+        }
         float* dst = out + m * N + n0;
         *reinterpret_cast<f4v*>(dst) = f4v{v[0], v[1], v[2], v[3]};
         *reinterpret_cast<f4v*>(dst + 4) = f4v{v[4], v[5], v[6], v[7]};
@@ -664,11 +757,11 @@ __global__ __launch_bounds__(LM_THREADS, 1) void k_linear_mfma(
     }
 }
 
-// y = 2^-(ex[m] + es[n / 128]) * sum over the S splits in order (+ bias)
+// y = 2^-(ex[m] + es[n / 128]) * sum over the S splits in order * post (+ bias)
 __global__ __launch_bounds__(256) void k_linear_mfma_reduce(const float* __restrict__ part, int S, int64_t M,
                                                             int64_t N, const int* __restrict__ ex,
                                                             const int* __restrict__ es, const float* __restrict__ bias,
-                                                            float* __restrict__ out) {
+                                                            float post, float* __restrict__ out) {
   const int64_t q = (int64_t)blockIdx.x * 256 + threadIdx.x;  // float4 index
   if (q >= M * N / 4) return;
   const int64_t m = (4 * q) / N, n = (4 * q) % N;
@@ -681,7 +774,7 @@ __global__ __launch_bounds__(256) void k_linear_mfma_reduce(const float* __restr
   const int e = -(ex[m] + (es ? es[n / 128] : 0));
   f4v y;
 #pragma unroll
-  for (int r = 0; r < 4; ++r) y[r] = __builtin_ldexpf(s[r], e) + (bias ? bias[n + r] : 0.0f);
+  for (int r = 0; r < 4; ++r) y[r] = __builtin_ldexpf(s[r], e) * post + (bias ? bias[n + r] : 0.0f);
   *reinterpret_cast<f4v*>(out + 4 * q) = y;
 }
 
@@ -845,29 +938,29 @@ LmPlan lm_plan(int64_t M, int64_t K, int64_t N, bool nk, int bits) {
   return p;
 }
 
-template <int BITS, int WM, bool NK, bool TILED>
+template <int FMT, int WM, bool NK, bool TILED>
 void lm_launch_t(const LmPlan& p, hipStream_t st, const float* xs, const _Float16* xh, const _Float16* xl,
                  const float* sc, int sc_kbm, const int* ex, int* es, const uint8_t* w, int64_t M, int64_t K,
                  int64_t N, const float* bias, float* out, float* part) {
   const dim3 grid((unsigned)(N / 128), (unsigned)ceil_div(M, 32 * WM), (unsigned)p.S);
-  hipLaunchKernelGGL((k_linear_mfma<BITS, WM, NK, TILED>), grid, dim3(LM_THREADS), 0, st, xs, xh, xl, sc, sc_kbm, ex,
+  hipLaunchKernelGGL((k_linear_mfma<FMT, WM, NK, TILED>), grid, dim3(LM_THREADS), 0, st, xs, xh, xl, sc, sc_kbm, ex,
                      es, w, (int)M, K, p.Kp, N, p.sps, bias, out, p.S > 1 ? part : nullptr);
 }
 
-template <int BITS, bool NK, bool TILED = false>
+template <int FMT, bool NK, bool TILED = false>
 void lm_launch_w(const LmPlan& p, hipStream_t st, const float* xs, const _Float16* xh, const _Float16* xl,
                  const float* sc, int sc_kbm, const int* ex, int* es, const uint8_t* w, int64_t M, int64_t K,
                  int64_t N, const float* bias, float* out, float* part) {
-  constexpr int MW = lm_max_wm(NK, BITS);
+  constexpr int MW = lm_max_wm(NK, lm_bits(FMT));
   switch (p.wm) {
     case 8:
-      lm_launch_t<BITS, MW < 8 ? MW : 8, NK, TILED>(p, st, xs, xh, xl, sc, sc_kbm, ex, es, w, M, K, N, bias, out, part);
+      lm_launch_t<FMT, MW < 8 ? MW : 8, NK, TILED>(p, st, xs, xh, xl, sc, sc_kbm, ex, es, w, M, K, N, bias, out, part);
       break;
     case 4:
-      lm_launch_t<BITS, MW < 4 ? MW : 4, NK, TILED>(p, st, xs, xh, xl, sc, sc_kbm, ex, es, w, M, K, N, bias, out, part);
+      lm_launch_t<FMT, MW < 4 ? MW : 4, NK, TILED>(p, st, xs, xh, xl, sc, sc_kbm, ex, es, w, M, K, N, bias, out, part);
       break;
-    case 2: lm_launch_t<BITS, 2, NK, TILED>(p, st, xs, xh, xl, sc, sc_kbm, ex, es, w, M, K, N, bias, out, part); break;
-    default: lm_launch_t<BITS, 1, NK, TILED>(p, st, xs, xh, xl, sc, sc_kbm, ex, es, w, M, K, N, bias, out, part); break;
+    case 2: lm_launch_t<FMT, 2, NK, TILED>(p, st, xs, xh, xl, sc, sc_kbm, ex, es, w, M, K, N, bias, out, part); break;
+    default: lm_launch_t<FMT, 1, NK, TILED>(p, st, xs, xh, xl, sc, sc_kbm, ex, es, w, M, K, N, bias, out, part); break;
   }
 }
 
@@ -890,7 +983,7 @@ void lm_prep_rows(const void* x, int x_type, int64_t M, int64_t K, int64_t Kp, f
 }
 
 bool lm_common_ok(int64_t M, int64_t K, int64_t N, int kind, int bits, int block, int x_type, const float* out) {
-  if (kind != MXK_KIND_INT || (bits != 4 && bits != 8) || block != 128) return false;
+  if (lm_format(kind, bits) == 0 || block != 128) return false;
   if (M < 1 || K < 1 || N < 128 || N % 128 != 0 || M >= (int64_t(1) << 31)) return false;
   if (x_type != MXK_IN_F32 && x_type != MXK_IN_F16 && x_type != MXK_IN_BF16) return false;
   if (!aligned16(out)) return false;
@@ -907,7 +1000,7 @@ bool lm_common_ok(int64_t M, int64_t K, int64_t N, int kind, int bits, int block
 // Bytes of workspace the MFMA path needs for this product (0 when it does
 // not take the shape); the first LM_WS_BASE bytes are left untouched.
 size_t linear_mfma_workspace(int64_t M, int64_t K, int64_t N, int bits, int block, bool nk) {
-  if ((bits != 4 && bits != 8) || block != 128 || M < 1 || K < 1 || N < 128 || N % 128 != 0) return 0;
+  if ((bits != 2 && bits != 4 && bits != 8) || block != 128 || M < 1 || K < 1 || N < 128 || N % 128 != 0) return 0;
   if (nk && K % 128 != 0) return 0;
   return lm_plan(M, K, N, nk, bits).bytes;
 }
@@ -918,7 +1011,7 @@ int linear_mfma_kn(const void* x, int x_type, int64_t M, int64_t K, const void* 
                    const float* w_scales_t, int64_t N, int kind, int bits, int block, const float* bias, float* out,
                    void* workspace, size_t workspace_nbytes, hipStream_t st) {
   if (!lm_common_ok(M, K, N, kind, bits, block, x_type, out)) return MXK_EUNSUPPORTED;
-  if ((reinterpret_cast<uintptr_t>(w_packed) & (bits == 8 ? 7u : 3u)) != 0) return MXK_EUNSUPPORTED;
+  if ((reinterpret_cast<uintptr_t>(w_packed) & (bits == 8 ? 7u : bits == 4 ? 3u : 1u)) != 0) return MXK_EUNSUPPORTED;
   const LmPlan p = lm_plan(M, K, N, false, bits);
   if (!workspace || workspace_nbytes < p.bytes)
     return fail(MXK_EINVAL, "linear_wq: needs a workspace of mxk_linear_workspace() bytes");
@@ -937,11 +1030,20 @@ int linear_mfma_kn(const void* x, int x_type, int64_t M, int64_t K, const void* 
     sT = sc;
   }
   const uint8_t* w = reinterpret_cast<const uint8_t*>(w_packed);
-  if (bits == 4) lm_launch_w<4, false>(p, st, xs, nullptr, nullptr, sT, 1, ex, es, w, M, K, N, bias, out, part);
-  else lm_launch_w<8, false>(p, st, xs, nullptr, nullptr, sT, 1, ex, es, w, M, K, N, bias, out, part);
+  const int fmt = lm_format(kind, bits);
+  switch (fmt) {
+#define MXK_LMK(F) \
+  case F: lm_launch_w<F, false>(p, st, xs, nullptr, nullptr, sT, 1, ex, es, w, M, K, N, bias, out, part); break;
+    MXK_LMK(LM_I2)
+    MXK_LMK(LM_I4)
+    MXK_LMK(LM_I8)
+    MXK_LMK(LM_F4)
+    MXK_LMK(LM_F8)
+#undef MXK_LMK
+  }
   if (p.S > 1)
     hipLaunchKernelGGL(k_linear_mfma_reduce, dim3((unsigned)ceil_div(M * N / 4, 256)), dim3(256), 0, st, part, p.S,
-                       M, N, ex, es, bias, out);
+                       M, N, ex, es, bias, lm_post(fmt), out);
   return check_launch("linear_wq(mfma)");
 }
 
@@ -960,11 +1062,11 @@ int linear_mfma_kn_tiled(const void* x, int x_type, int64_t M, int64_t K, const 
   float* xs = reinterpret_cast<float*>(ws + p.off_x);
   float* part = reinterpret_cast<float*>(ws + p.off_p);
   lm_prep_rows<false>(x, x_type, M, K, p.Kp, xs, nullptr, nullptr, ex, st);
-  lm_launch_w<4, false, true>(p, st, xs, nullptr, nullptr, w_scales_t, 1, ex, es,
-                              reinterpret_cast<const uint8_t*>(w_tiled), M, K, N, bias, out, part);
+  lm_launch_w<LM_I4, false, true>(p, st, xs, nullptr, nullptr, w_scales_t, 1, ex, es,
+                                  reinterpret_cast<const uint8_t*>(w_tiled), M, K, N, bias, out, part);
   if (p.S > 1)
     hipLaunchKernelGGL(k_linear_mfma_reduce, dim3((unsigned)ceil_div(M * N / 4, 256)), dim3(256), 0, st, part, p.S,
-                       M, N, ex, es, bias, out);
+                       M, N, ex, es, bias, 1.0f, out);
   return check_launch("linear_wq_tiled(mfma)");
 }
 
@@ -988,11 +1090,20 @@ int linear_mfma_nk(const void* x, int x_type, int64_t M, int64_t K, const void* 
   const float* sc = w_scales_t ? w_scales_t : w_scales;
   const int kbm = w_scales_t ? 1 : 0;
   const uint8_t* w = reinterpret_cast<const uint8_t*>(w_packed);
-  if (bits == 4) lm_launch_w<4, true>(p, st, nullptr, xh, xl, sc, kbm, ex, nullptr, w, M, K, N, bias, out, part);
-  else lm_launch_w<8, true>(p, st, nullptr, xh, xl, sc, kbm, ex, nullptr, w, M, K, N, bias, out, part);
+  const int fmt = lm_format(kind, bits);
+  switch (fmt) {
+#define MXK_LMN(F) \
+  case F: lm_launch_w<F, true>(p, st, nullptr, xh, xl, sc, kbm, ex, nullptr, w, M, K, N, bias, out, part); break;
+    MXK_LMN(LM_I2)
+    MXK_LMN(LM_I4)
+    MXK_LMN(LM_I8)
+    MXK_LMN(LM_F4)
+    MXK_LMN(LM_F8)
+#undef MXK_LMN
+  }
   if (p.S > 1)
     hipLaunchKernelGGL(k_linear_mfma_reduce, dim3((unsigned)ceil_div(M * N / 4, 256)), dim3(256), 0, st, part, p.S,
-                       M, N, ex, nullptr, bias, out);
+                       M, N, ex, nullptr, bias, lm_post(fmt), out);
   return check_launch("linear_wq_nt(mfma)");
 }
 
@@ -1011,11 +1122,11 @@ int linear_mfma_nk_tiled(const void* x, int x_type, int64_t M, int64_t K, const 
   _Float16* xl = xh + (size_t)lm_rows16(M) * (size_t)p.Kp;
   float* part = reinterpret_cast<float*>(ws + p.off_p);
   lm_prep_rows<true>(x, x_type, M, K, p.Kp, nullptr, xh, xl, ex, st);
-  lm_launch_w<4, true, true>(p, st, nullptr, xh, xl, w_scales_t, 1, ex, nullptr,
-                             reinterpret_cast<const uint8_t*>(w_tiled), M, K, N, bias, out, part);
+  lm_launch_w<LM_I4, true, true>(p, st, nullptr, xh, xl, w_scales_t, 1, ex, nullptr,
+                                 reinterpret_cast<const uint8_t*>(w_tiled), M, K, N, bias, out, part);
   if (p.S > 1)
     hipLaunchKernelGGL(k_linear_mfma_reduce, dim3((unsigned)ceil_div(M * N / 4, 256)), dim3(256), 0, st, part, p.S,
-                       M, N, ex, nullptr, bias, out);
+                       M, N, ex, nullptr, bias, 1.0f, out);
   return check_launch("linear_wq_nt_tiled(mfma)");
 }
 

@@ -10,8 +10,11 @@ runs both on f16 MFMAs with x * scale carried as an f16 hi + lo pair and the
 codes as exact f16 operands; every output row must be within 1e-3 of that
 row's largest |y| of the oracle (the reference's CPU path restated:
 quantize, dequantize, fp32 product), for activations and weights from 1e-6
-to 1e6, rows of very different magnitudes in one call, ragged K and the
-verdict's sizes M in {17, 64, 512, 8192} at K = N = 8192."""
+to 1e6, rows of very different magnitudes in one call, ragged K and
+M in {17, 64, 512, 8192} at K = N = 8192.  int2d, float4d and float8d
+weights run on the same kernel with their codes decoded to exact f16 values
+(FP4 / FP8 grid values times 6 / 480, the factor taken back out of the
+outputs); an all-codes test pins every decoded code."""
 import pytest
 import torch
 
@@ -21,6 +24,7 @@ from tests import _golden as G
 pytestmark = pytest.mark.gpu
 
 RTOL = 1e-3
+FMTS = ["int4d", "int8d", "int2d", "float4d", "float8d"]
 
 
 @pytest.fixture(scope="module")
@@ -83,12 +87,14 @@ def big_weights():
     return W
 
 
-@pytest.mark.parametrize("dt", ["int4d", "int8d"])
+@pytest.mark.parametrize("dt", FMTS)
 @pytest.mark.parametrize("M", [17, 64, 512, 8192])
 def test_mfma_linear_8192(qa, big_weights, dt, M):
     """x [M, 8192] in float32 and bfloat16 against W [8192, 8192]; at
     M = 8192 the oracle checks 96 sampled rows (each row's product is
-    independent of the others)."""
+    independent of the others).  int2d / float4d / float8d at M = 17 and 512."""
+    if dt not in ("int4d", "int8d") and M in (64, 8192):
+        pytest.skip("the other formats share the kernel; two sizes bound the test time")
     W = big_weights
     K = N = 8192
     m = _module(qa, W, dt)
@@ -113,7 +119,7 @@ def test_mfma_linear_8192(qa, big_weights, dt, M):
 MAGS = [1e-6, 1e-3, 1.0, 1e4, 1e6]
 
 
-@pytest.mark.parametrize("dt", ["int4d", "int8d"])
+@pytest.mark.parametrize("dt", FMTS)
 @pytest.mark.parametrize("wmag", MAGS)
 @pytest.mark.parametrize("xmag", MAGS)
 def test_mfma_magnitudes(qa, dt, xmag, wmag):
@@ -125,7 +131,7 @@ def test_mfma_magnitudes(qa, dt, xmag, wmag):
 
 
 @pytest.mark.parametrize("xdt", [torch.float32, torch.bfloat16, torch.float16])
-@pytest.mark.parametrize("dt", ["int4d", "int8d"])
+@pytest.mark.parametrize("dt", FMTS)
 def test_mfma_mixed_row_magnitudes(qa, dt, xdt):
     """Rows from 1e-4 to 1e3 (1e-7 to 1e7 for float32 and bfloat16) in one
     call, and a row of zeros, which must give exact zeros."""
@@ -147,7 +153,7 @@ def test_mfma_mixed_row_magnitudes(qa, dt, xdt):
     assert ok, f"worst row error {worst:.3g} x the bar"
 
 
-@pytest.mark.parametrize("dt", ["int4d", "int8d"])
+@pytest.mark.parametrize("dt", FMTS)
 def test_mfma_mixed_k_magnitudes(qa, dt):
     """Magnitudes that change along K inside one row: x large where the
     weights are small and the other way round."""
@@ -160,12 +166,12 @@ def test_mfma_mixed_k_magnitudes(qa, dt):
     _check_linear(qa, x, W, dt)
 
 
-@pytest.mark.parametrize("dt", ["int4d", "int8d"])
+@pytest.mark.parametrize("dt", FMTS)
 @pytest.mark.parametrize("M,K,N", [(16, 1024, 256), (33, 100, 128), (200, 300, 384), (130, 1000, 640),
                                    (300, 2304, 1152), (1, 4096, 128)])
 def test_mfma_ragged_shapes(qa, dt, M, K, N):
     """K not a multiple of the 256-row stage, odd M, single column blocks,
-    and int8d at M <= 16."""
+    and every format but int4d at M <= 16."""
     if dt == "int4d" and M <= 16:
         pytest.skip("int4d at M <= 16 takes the decode kernels")
     print(f"mfma ragged {dt} M={M} K={K} N={N}", flush=True)
@@ -174,7 +180,7 @@ def test_mfma_ragged_shapes(qa, dt, M, K, N):
     _check_linear(qa, x, W, dt)
 
 
-@pytest.mark.parametrize("dt", ["int4d", "int8d"])
+@pytest.mark.parametrize("dt", FMTS)
 def test_mfma_bias(qa, dt):
     """apply_bias adds the dequantized stored bias after the product."""
     M, K, N = 80, 1024, 384
@@ -194,13 +200,15 @@ def test_mfma_bias(qa, dt):
     assert ok, f"worst row error {worst:.3g} x the bar"
 
 
-@pytest.mark.parametrize("dt", ["int4d", "int8d"])
+@pytest.mark.parametrize("dt", FMTS)
 @pytest.mark.parametrize("M,K,N", [(17, 8192, 8192), (64, 8192, 8192), (512, 8192, 8192), (40, 384, 256),
                                    (300, 1280, 640)])
 def test_mfma_linear_nt(qa, dt, M, K, N):
     """[out, in] weights (mx_dynamic_linear.forward, mxtorch.py:8945-8962):
     x.float() @ dequant(W).t() + bias through ops.linear_wq_nt."""
     from qtpytorch_amd import ops
+    if dt not in ("int4d", "int8d") and M == 64:
+        pytest.skip("the other formats share the kernel; 17 and 512 rows bound the test time")
     print(f"mfma linear_nt {dt} M={M} K={K} N={N}", flush=True)
     W = _randn((N, K), 31 + M, outliers=1e-3) * 0.02
     x = _randn((M, K), 37 + N)
@@ -218,7 +226,7 @@ def test_mfma_linear_nt(qa, dt, M, K, N):
         assert torch.equal(y2, y)
 
 
-@pytest.mark.parametrize("dt", ["int4d", "int8d"])
+@pytest.mark.parametrize("dt", FMTS)
 @pytest.mark.parametrize("xmag,wmag", [(1e-6, 1e6), (1e6, 1e-6), (1e-3, 1e-3), (1e4, 1e4)])
 def test_mfma_linear_nt_magnitudes(qa, dt, xmag, wmag):
     from qtpytorch_amd import ops
@@ -233,7 +241,7 @@ def test_mfma_linear_nt_magnitudes(qa, dt, xmag, wmag):
     assert ok, f"worst row error {worst:.3g} x the bar"
 
 
-@pytest.mark.parametrize("dt", ["int4d", "int8d"])
+@pytest.mark.parametrize("dt", FMTS)
 def test_mfma_input_gradient(qa, dt):
     """mx_linear's input gradient at batch 96: grad @ dequant(W)^T
     (F.linear(x, W_dq) of mxtorch.py:7473 differentiated), against float64."""
@@ -276,3 +284,49 @@ def test_mfma_repeat_bitwise(qa):
         m = _module(qa, W, "int4d")
         x = _randn((M, 4096), 73).to(dev())
         assert torch.equal(m(x), m(x))
+
+
+@pytest.mark.parametrize("dt", ["int2d", "int4d", "int8d", "float4d", "float8d"])
+@pytest.mark.parametrize("layout", ["kn", "nk"])
+def test_mfma_every_code(qa, dt, layout):
+    """Every code of the format in every column and k position: codes
+    (k + 3 n) mod 2^bits, scales 2^-6 .. 2^6 around a power of two from
+    2^-20 to 2^20 that changes between column blocks (the [K][N] kernel
+    keeps a block's terms relative to its largest scale), x the identity
+    (M = K = 384 rows, more than the decode kernels take), so that y is the
+    dequantized weight itself, one product term per output.  Each output may
+    differ from the oracle's RN(grid[c] * s) only by the hi + lo split of
+    s (2^-22) and, for the float grids, the factor RN(1/6) or RN(1/480):
+    a code decoded to any other grid value fails by far more."""
+    from qtpytorch_amd import ops
+    bits = {"int2d": 2, "int4d": 4, "int8d": 8, "float4d": 4, "float8d": 8}[dt]
+    K, N = 384, 256
+    k = torch.arange(K)[:, None]
+    n = torch.arange(N)[None, :]
+    codes = (k + 3 * n) % (1 << bits)
+    if dt.startswith("int"):
+        codes = codes - (1 << (bits - 1))  # signed codes, every one of them
+    g = torch.Generator()
+    g.manual_seed(bits)
+    x = torch.eye(K)
+    nsc = K * N // 128
+    off = torch.tensor([-20.0, 20.0, 0.0, 7.0])
+    if layout == "kn":
+        # block (k, nb) at k * N/128 + nb
+        scales = torch.exp2(torch.empty(nsc).uniform_(-6, 6, generator=g) + off[torch.arange(nsc) % (N // 128)])
+        packed = orc.pack(codes.reshape(-1), bits)
+        y = ops.linear_wq(x.to(dev()), packed.to(dev()), scales.to(dev()), dt, K, N, 128).cpu()
+        ref = orc.dequant(packed, scales, dt, K * N, 128).reshape(K, N)
+    else:
+        codes_nk = codes.t().contiguous()  # [N][K]: blocks along K, block (n, kb) at n * K/128 + kb
+        scales = torch.exp2(torch.empty(nsc).uniform_(-6, 6, generator=g) + off[torch.arange(nsc) % 4])
+        packed = orc.pack(codes_nk.reshape(-1), bits)
+        y = ops.linear_wq_nt(x.to(dev()), packed.to(dev()), scales.to(dev()), dt, N, K, 128).cpu()
+        ref = orc.dequant(packed, scales, dt, K * N, 128).reshape(N, K).t()
+    print(f"mfma every code {dt} {layout}", flush=True)
+    assert torch.isfinite(y).all()
+    err = (y - ref).abs()
+    lim = 2.0 ** -20 * ref.abs()
+    bad = err > lim
+    assert not bad.any(), (f"{int(bad.sum())} outputs off, first at {bad.nonzero()[0].tolist()}: "
+                           f"{y[bad][0].item()!r} vs {ref[bad][0].item()!r}")
