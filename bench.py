@@ -305,6 +305,75 @@ def bench_linear_mfma(qa, reps):
     return out
 
 
+# The reference's published rows (README.md:590-595, 599-603, 618-624; RX
+# 7900 XTX, its Triton path), in ms
+README_QUANT_MS = {("int4d", 512): 0.05, ("int4d", 1024): 0.07, ("int8d", 512): 0.05, ("int8d", 1024): 0.06,
+                   ("float4d", 512): 0.24, ("float4d", 1024): 0.30, ("float8d", 512): 0.18, ("float8d", 1024): 0.23}
+README_GEMM_MS = {256: 0.073, 512: 0.085, 1024: 0.190}
+README_LINEAR_MS = {(512, 512): {"int8d": 0.82, "int4d": 1.75}, (1024, 512): {"int8d": 0.83, "int4d": 1.89},
+                    (2048, 1024): {"int8d": 0.82, "int4d": 2.16}}
+
+
+def bench_readme_rows(qa):
+    """The reference's own published benchmark rows, timed the way its
+    benchmark times them (mxtorch_test.py:3474-3496, 3523-3580, 3616-3628):
+    3 eager warm-up calls, then 20 eager calls each bracketed by a pair of
+    events and a synchronize, and the mean in ms.  Rows: quantize 512^2 and
+    1024^2 (block 128) for int4d / int8d / float4d / float8d; the int8d GEMM
+    _dispatch_qgemm of 256^3, 512^3, 1024^3 operands quantized with block 64;
+    mx_linear at batch 32 for 512->512, 1024->512, 2048->1024 (int8d and
+    int4d weights, block 128).  Each row carries the published RX 7900 XTX
+    time and published / ours."""
+    from qtpytorch_amd.tensor import _dispatch_qgemm
+
+    dev = torch.device("cuda:0")
+
+    def ev_mean(fn, warmup=3, runs=20):
+        for _ in range(warmup):
+            fn()
+        torch.cuda.synchronize()
+        ts = []
+        for _ in range(runs):
+            a = torch.cuda.Event(enable_timing=True)
+            b = torch.cuda.Event(enable_timing=True)
+            a.record()
+            fn()
+            b.record()
+            torch.cuda.synchronize()
+            ts.append(a.elapsed_time(b))
+        return statistics.mean(ts)
+
+    def row(ms, pub):
+        return {"ms": round(ms, 4), "published_ms": pub, "published_over_ours": round(pub / ms, 1)}
+
+    out = {"method": "eager calls, event pair per call, mean of 20 after 3 warm-ups (the reference's _bench)"}
+    q = {}
+    for n in (512, 1024):
+        x = torch.randn(n, n, generator=gen(300 + n, "cuda"), device=dev)
+        for name in ("int4d", "int8d", "float4d", "float8d"):
+            dt = qa.get_mx_dtype(name)
+            q[f"{name}_{n}x{n}"] = row(ev_mean(lambda: qa.mx_tensor.quantize(x, dt, 128)), README_QUANT_MS[(name, n)])
+    out["quantize"] = q
+    g = {}
+    for n in (256, 512, 1024):
+        a = qa.mx_tensor.quantize(torch.randn(n, n, generator=gen(310 + n, "cuda"), device=dev),
+                                  qa.get_mx_dtype("int8d"), 64)
+        b = qa.mx_tensor.quantize(torch.randn(n, n, generator=gen(320 + n, "cuda"), device=dev),
+                                  qa.get_mx_dtype("int8d"), 64)
+        g[f"int8d_{n}^3_block64"] = row(ev_mean(lambda: _dispatch_qgemm(a, b)), README_GEMM_MS[n])
+    out["qgemm"] = g
+    lin_rows = {}
+    for (k, n), pubs in README_LINEAR_MS.items():
+        lin = torch.nn.Linear(k, n, device=dev)
+        x = torch.randn(32, k, generator=gen(330 + k, "cuda"), device=dev)
+        for name, pub in pubs.items():
+            m = qa.mx_linear.from_linear(lin, qa.get_mx_dtype(name), 128)
+            with torch.no_grad():
+                lin_rows[f"{name}_{k}->{n}_batch32"] = row(ev_mean(lambda: m(x)), pub)
+    out["mx_linear"] = lin_rows
+    return out
+
+
 def cpu_baselines_extra():
     """The CPU oracle (the reference's CPU path restated) on bounded
     samples of configs 1, 3, 4 and 5, 2 warm-ups then the median of 5, on
@@ -542,7 +611,7 @@ def main():
     ap.add_argument("--no-extras", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--only", default="",
-                    help="comma list of extras: quant,gemm,gemm4,kv,kvstream,elementwise,small,mfma,dynamic,cpu")
+                    help="comma list of extras: quant,gemm,gemm4,kv,kvstream,elementwise,small,mfma,dynamic,readme,cpu")
     ap.add_argument("--eager", action="store_true", help="no graph capture (for rocprofv3 --pmc runs)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a plain 512 MiB device copy (the reference kernel for HBM counter scaling)")
@@ -614,6 +683,8 @@ def main():
             extras["kv_ring_stream_8x32x128_T4096"] = bench_kv_stream(qa, 64)
         if not only or "dynamic" in only:
             extras["dynamic_int8"] = bench_dynamic(qa, 120, 5)
+        if not only or "readme" in only:
+            extras["reference_published_rows"] = bench_readme_rows(qa)
         if not args.no_cpu and (not only or "cpu" in only):
             extras["cpu_baselines"] = cpu_baselines_extra()
         line["extras"] = extras

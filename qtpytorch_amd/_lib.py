@@ -5,6 +5,7 @@ fails loudly when it is missing: the package has no CPU compute path.
 """
 from __future__ import annotations
 
+import contextlib
 import ctypes
 import os
 import threading
@@ -113,9 +114,25 @@ def check(rc: int, what: str) -> None:
         raise MXKError(f"{what} failed ({rc}): {msg.decode() if msg else ''}")
 
 
+_RAW_STREAM = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+_GET_DEVICE = getattr(torch._C, "_cuda_getDevice", None)
+_SAME_DEVICE = contextlib.nullcontext()
+
+
 def stream_of(t: torch.Tensor) -> int:
-    """hipStream_t of torch's current stream on t's device."""
+    """hipStream_t of torch's current stream on t's device (the raw handle
+    query when torch has it: it builds no Stream object)."""
+    if _RAW_STREAM is not None:
+        return _RAW_STREAM(t.device.index if t.device.index is not None else torch.cuda.current_device())
     return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def on_device(dev: torch.device):
+    """Context that makes `dev` the current device for the library's calls:
+    nothing to do when it already is."""
+    if _GET_DEVICE is not None and (dev.index is None or dev.index == _GET_DEVICE()):
+        return _SAME_DEVICE
+    return torch.cuda.device(dev)
 
 
 def ptr(t) -> int:

@@ -179,19 +179,24 @@ struct KnCodes {
   uint32_t w[BITS == 8 ? 16 : 8];
 };
 
+// `dead` is 0 or LM_OOB: every loader's byte offsets are or-ed with it, so
+// that a load the caller does not need still issues (the compiler's wait
+// counts then stay exact across loop iterations) and reads zeros.
 template <int BITS>
 __device__ __forceinline__ void kn_load(KnCodes<BITS>& c, __amdgpu_buffer_rsrc_t rw, int64_t k0, int64_t N,
-                                        int64_t nb, int tid) {
+                                        int64_t nb, int tid, uint32_t dead) {
   const int r8 = tid >> 4, c8 = tid & 15;
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
     const int64_t row = k0 + 8 * r8 + i;
     if constexpr (BITS == 2) {
-      c.w[i] = __builtin_amdgcn_raw_buffer_load_b16(rw, (int)(row * (N / 4) + nb * 32 + 2 * c8), 0, 0);
+      c.w[i] = __builtin_amdgcn_raw_buffer_load_b16(rw, (int)((uint32_t)(row * (N / 4) + nb * 32 + 2 * c8) | dead),
+                                                    0, 0);
     } else if constexpr (BITS == 4) {
-      c.w[i] = buf_load_b32(rw, (uint32_t)(row * (N / 2) + nb * 64 + 4 * c8), 0u);
+      c.w[i] = buf_load_b32(rw, (uint32_t)(row * (N / 2) + nb * 64 + 4 * c8) | dead, 0u);
     } else {
-      const auto v = __builtin_amdgcn_raw_buffer_load_b64(rw, (int)(row * N + nb * 128 + 8 * c8), 0, 0);
+      const auto v =
+          __builtin_amdgcn_raw_buffer_load_b64(rw, (int)((uint32_t)(row * N + nb * 128 + 8 * c8) | dead), 0, 0);
       c.w[2 * i] = v[0];
       c.w[2 * i + 1] = v[1];
     }
@@ -239,10 +244,10 @@ struct KnTiled {
 };
 
 __device__ __forceinline__ void kn_load_tiled(KnTiled& c, __amdgpu_buffer_rsrc_t rw, int64_t k0, int64_t K,
-                                              int64_t nb, int tid) {
+                                              int64_t nb, int tid, uint32_t dead) {
   const int r8 = tid >> 4, c8 = tid & 15;
   const int64_t chunk = nb * (K / 32) + (k0 + 8 * r8) / 32;
-  const uint32_t off = (uint32_t)(chunk * 2048 + 16 * (c8 + 16 * (r8 & 3)));
+  const uint32_t off = (uint32_t)(chunk * 2048 + 16 * (c8 + 16 * (r8 & 3))) | dead;
   c.w[0] = buf_load_b128(rw, off, 0u);
   c.w[1] = buf_load_b128(rw, off + 1024u, 0u);
 }
@@ -281,23 +286,23 @@ __device__ __forceinline__ int nk2_col(int p) { return ((p >> 4) & 7) + 8 * (p &
 
 template <int BITS>
 __device__ __forceinline__ void nk_load(NkCodes<BITS>& c, __amdgpu_buffer_rsrc_t rw, int64_t k0, int64_t K,
-                                        int64_t nb, int tid) {
+                                        int64_t nb, int tid, uint32_t dead) {
   if constexpr (BITS == 2) {
     const int64_t n = nb * 128 + nk2_col(tid >> 2);
-    c.w[0] = buf_load_b128(rw, (uint32_t)(n * (K / 4) + k0 / 4 + 16 * (tid & 3)), 0u);
+    c.w[0] = buf_load_b128(rw, (uint32_t)(n * (K / 4) + k0 / 4 + 16 * (tid & 3)) | dead, 0u);
   } else if constexpr (BITS == 4) {
     const int q = tid & 7;
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
       const int64_t n = nb * 128 + nk4_col((tid >> 3) + 64 * h);
-      c.w[h] = buf_load_b128(rw, (uint32_t)(n * (K / 2) + k0 / 2 + 16 * q), 0u);
+      c.w[h] = buf_load_b128(rw, (uint32_t)(n * (K / 2) + k0 / 2 + 16 * q) | dead, 0u);
     }
   } else {
     const int h8 = tid & 15;
 #pragma unroll
     for (int h = 0; h < 4; ++h) {
       const int64_t n = nb * 128 + (tid >> 4) + 32 * h;
-      c.w[h] = buf_load_b128(rw, (uint32_t)(n * K + k0 + 16 * h8), 0u);
+      c.w[h] = buf_load_b128(rw, (uint32_t)(n * K + k0 + 16 * h8) | dead, 0u);
     }
   }
 }
@@ -369,14 +374,14 @@ __device__ __forceinline__ void nk_store(const NkCodes<lm_bits(FMT)>& c, uint8_t
 // and word 2 sp + h, byte b of a unit holds the codes (8 st + i) with
 // st = 2 sp (low nibble) and 2 sp + 1 (high nibble), i = 4 h + {0, 2, 1, 3}[b].
 __device__ __forceinline__ void nk_load_tiled(NkCodes<4>& c, __amdgpu_buffer_rsrc_t rw, int64_t k0, int64_t K,
-                                              int64_t nb, int tid) {
+                                              int64_t nb, int tid, uint32_t dead) {
   const int q = tid & 7;
   const int64_t k = k0 + 32 * q, KB = K / 128;
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
     const int64_t n = nb * 128 + nk4_col((tid >> 3) + 64 * h);
-    c.w[h] = buf_load_b128(rw, (uint32_t)(((n >> 4) * KB + (k >> 7)) * 1024 + 16 * ((n & 15) + 16 * ((k >> 5) & 3))),
-                           0u);
+    c.w[h] = buf_load_b128(
+        rw, (uint32_t)(((n >> 4) * KB + (k >> 7)) * 1024 + 16 * ((n & 15) + 16 * ((k >> 5) & 3))) | dead, 0u);
   }
 }
 
@@ -429,7 +434,7 @@ __global__ __launch_bounds__(LM_THREADS, 1) void k_linear_mfma(
     const _Float16* __restrict__ xh,     // [N][K]: hi of x' [M][Kp]
     const _Float16* __restrict__ xl,     // [N][K]: lo of x' [M][Kp]
     const float* __restrict__ sc,        // [K][N]: block-major scales [NB][K]; [N][K]: [KB][N] or [N][KB]
-    int sc_kb_major, const int* __restrict__ ex, int* __restrict__ es, const uint8_t* __restrict__ w,
+    int sc_kb_major, const int* __restrict__ ex, const int* __restrict__ es, const uint8_t* __restrict__ w,
     int M, int64_t K, int64_t Kp, int64_t N, int sps, const float* __restrict__ bias, float* __restrict__ out,
     float* __restrict__ part) {
   constexpr int BITS = lm_bits(FMT), WK = 8 / WM, KPW = 8 / WK;
@@ -463,54 +468,39 @@ __global__ __launch_bounds__(LM_THREADS, 1) void k_linear_mfma(
     rb = make_rsrc(sc + nb * K, (uint32_t)(K * 4));  // scales past K read zeros
   }
   // [K][N]: the block's scales go to the binade of 2^13 by 2^es (the
-  // largest in [2^13, 2^14)); the epilogue takes 2^-es back out
-  // (called once the first stages' loads are in flight, so their
-  // latencies overlap)
-  int es_nb = 0;
-  auto scan_es = [&]() {
-    if constexpr (NK) return;
-    __shared__ float s_red[8];
-    float mx = 0.0f;
-    for (int64_t k = tid; k < K; k += 4 * LM_THREADS) {
-      float v[4];
-#pragma unroll
-      for (int u = 0; u < 4; ++u) v[u] = __uint_as_float(buf_load_b32(rb, (uint32_t)((k + u * LM_THREADS) * 4), 0u));
-#pragma unroll
-      for (int u = 0; u < 4; ++u) mx = fmaxf(mx, __builtin_fabsf(v[u]));
-    }
-    mx = group_max<64>(mx);
-    if (lane == 0) s_red[wave] = mx;
-    lm_barrier();
-#pragma unroll
-    for (int u = 0; u < 8; ++u) mx = fmaxf(mx, s_red[u]);
-    const int be = (int)((__float_as_uint(mx) >> 23) & 0xFFu);
-    es_nb = (be == 0xFF || mx == 0.0f) ? 0 : 140 - (be == 0 ? 1 : be);
-    // the split reduction applies 2^-es after summing the partials
-    if (part && es && blockIdx.y == 0 && blockIdx.z == 0 && tid == 0) es[nb] = es_nb;
-  };
-  auto load_a = [&](A& a, int st, int jj) {
+  // largest in [2^13, 2^14), from the row prepass); the epilogue, or the
+  // split reduction, takes 2^-es back out
+  const int es_nb = NK ? 0 : es[nb];
+  // Loads are issued whether or not their data is needed (`live` false:
+  // every offset past its buffer, zeros come back), so that the number of
+  // loads per step is fixed and the compiler's wait counts stay exact; with
+  // conditional loads it waited for every load in flight at each step.  A
+  // dead A operand is all zeros, so a dead step adds exact zeros.
+  auto load_a = [&](A& a, int st, int jj, bool live) {
+    const uint32_t dead = live ? 0u : LM_OOB;
     const int64_t kg = (int64_t)st * LM_STAGE + 32 * (wk + WK * jj) + 8 * g;
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
       const int64_t at = lm_xoff(32 * wm + 16 * i + j, kg, Kp);
       if constexpr (NK) {
-        a.h[i] = buf_load_b128(ra, (uint32_t)(at * 2), 0u);
-        a.l[i] = buf_load_b128(rb, (uint32_t)(at * 2), 0u);
+        a.h[i] = buf_load_b128(ra, (uint32_t)(at * 2) | dead, 0u);
+        a.l[i] = buf_load_b128(rb, (uint32_t)(at * 2) | dead, 0u);
       } else {
-        a.x[i][0] = buf_load_b128(ra, (uint32_t)(at * 4), 0u);
-        a.x[i][1] = buf_load_b128(ra, (uint32_t)(at * 4 + 16), 0u);
+        a.x[i][0] = buf_load_b128(ra, (uint32_t)(at * 4) | dead, 0u);
+        a.x[i][1] = buf_load_b128(ra, (uint32_t)(at * 4 + 16) | dead, 0u);
       }
     }
     if constexpr (!NK) {
-      a.s[0] = buf_load_b128(rb, (uint32_t)(kg * 4), 0u);
-      a.s[1] = buf_load_b128(rb, (uint32_t)(kg * 4 + 16), 0u);
+      a.s[0] = buf_load_b128(rb, (uint32_t)(kg * 4) | dead, 0u);
+      a.s[1] = buf_load_b128(rb, (uint32_t)(kg * 4 + 16) | dead, 0u);
     }
   };
-  auto load_codes = [&](Codes& c, int st) {
-    if constexpr (NK && TILED) nk_load_tiled(c, rw, (int64_t)st * LM_STAGE, K, nb, tid);
-    else if constexpr (NK) nk_load<BITS>(c, rw, (int64_t)st * LM_STAGE, K, nb, tid);
-    else if constexpr (TILED) kn_load_tiled(c, rw, (int64_t)st * LM_STAGE, K, nb, tid);
-    else kn_load<BITS>(c, rw, (int64_t)st * LM_STAGE, N, nb, tid);
+  auto load_codes = [&](Codes& c, int st, bool live) {
+    const uint32_t dead = live ? 0u : LM_OOB;
+    if constexpr (NK && TILED) nk_load_tiled(c, rw, (int64_t)st * LM_STAGE, K, nb, tid, dead);
+    else if constexpr (NK) nk_load<BITS>(c, rw, (int64_t)st * LM_STAGE, K, nb, tid, dead);
+    else if constexpr (TILED) kn_load_tiled(c, rw, (int64_t)st * LM_STAGE, K, nb, tid, dead);
+    else kn_load<BITS>(c, rw, (int64_t)st * LM_STAGE, N, nb, tid, dead);
   };
   auto store_codes = [&](const Codes& c, uint8_t* dst) {
     if constexpr (NK && TILED) nk_store_tiled(c, dst, tid);
@@ -603,12 +593,11 @@ __global__ __launch_bounds__(LM_THREADS, 1) void k_linear_mfma(
   // scheduling barriers keep every request at the top of its step.
   // A operands of this wave's k step gs (0 .. nsteps-1 over the split)
   const int nsteps = (st1 - st0) * KPW;
-  auto load_step = [&](A& a, int gs) { load_a(a, st0 + gs / KPW, gs % KPW); };
+  auto load_step = [&](A& a, int gs) { load_a(a, st0 + gs / KPW, gs % KPW, gs < nsteps); };
   // One row tile ([K][N], WM = 1): wave w runs k step w of every stage, and
   // the fragments its lanes decode are exactly the ones they feed to the
   // MFMAs, so the codes skip LDS (and every barrier): each wave keeps DS
   // stages of its codes in flight in registers.
-  if (st0 >= st1) scan_es();
   constexpr bool DIRECT = !NK && WM == 1;
   constexpr int DS = BITS == 8 ? 2 : 4;
   if constexpr (DIRECT) {
@@ -616,31 +605,29 @@ __global__ __launch_bounds__(LM_THREADS, 1) void k_linear_mfma(
     Codes cq[DS];
     A ar[2];
 #pragma unroll
-    for (int i = 0; i < DS; ++i)
-      if (st0 + i < st1) load_codes(cq[i], st0 + i);
+    for (int i = 0; i < DS; ++i) load_codes(cq[i], st0 + i, st0 + i < st1);
     load_step(ar[0], 0);
-    if (nsteps > 1) load_step(ar[1], 1);
-    scan_es();
+    load_step(ar[1], 1);
+    // whole groups of DS stages: the steps past st1 in the last group run
+    // on zero A operands
     for (int sb = st0; sb < st1; sb += DS) {
 #pragma unroll
       for (int i = 0; i < DS; ++i) {
         const int st = sb + i;
-        if (st < st1) {
-          const int gs = st - st0, p = i & 1;  // DS is even, so gs % 2 = i % 2
-          h8v bt[8];
+        const int gs = st - st0, p = i & 1;  // DS is even, so gs % 2 = i % 2
+        h8v bt[8];
 #pragma unroll
-          for (int t = 0; t < 8; ++t) {
-            if constexpr (TILED) bt[t] = __builtin_bit_cast(h8v, kn_frag_tiled(cq[i], t));
-            else bt[t] = __builtin_bit_cast(h8v, kn_frag<FMT>(cq[i], t));
-          }
-          if (st + DS < st1) load_codes(cq[i], st + DS);
-          h8v ahi[2], alo[2];
-          build(ar[p], ahi, alo);
-          if (gs + 2 < nsteps) load_step(ar[p], gs + 2);
-          __builtin_amdgcn_sched_barrier(0);
-          mfmas(ahi, alo, bt, 0, 8);
-          __builtin_amdgcn_sched_barrier(0);
+        for (int t = 0; t < 8; ++t) {
+          if constexpr (TILED) bt[t] = __builtin_bit_cast(h8v, kn_frag_tiled(cq[i], t));
+          else bt[t] = __builtin_bit_cast(h8v, kn_frag<FMT>(cq[i], t));
         }
+        load_codes(cq[i], st + DS, st + DS < st1);
+        h8v ahi[2], alo[2];
+        build(ar[p], ahi, alo);
+        load_step(ar[p], gs + 2);
+        __builtin_amdgcn_sched_barrier(0);
+        mfmas(ahi, alo, bt, 0, 8);
+        __builtin_amdgcn_sched_barrier(0);
       }
     }
    }
@@ -648,23 +635,24 @@ __global__ __launch_bounds__(LM_THREADS, 1) void k_linear_mfma(
     Codes cc;
     A ar[2];
     float s8[8];
-    load_codes(cc, st0);
+    load_codes(cc, st0, true);
     load_step(ar[0], 0);
-    if (nsteps > 1) load_step(ar[1], 1);
-    scan_es();
+    load_step(ar[1], 1);
     store_codes(cc, sB);
     lm_barrier();
     for (int st = st0; st < st1; ++st) {
       const int buf = (st - st0) & 1;
       const bool more = st + 1 < st1;
-      if (more) load_codes(cc, st + 1);
+      load_codes(cc, st + 1, more);
       const uint8_t* b = sB + buf * LM_STAGE_BYTES;
 #pragma unroll
       for (int jj = 0; jj < KPW; ++jj) {
         // slot p holds step gs, the other slot step gs + 1 (KPW even: p = gs % 2)
         const int p = (KPW & 1) ? 0 : (jj & 1), ks = wk + WK * jj;
         const int gs = (st - st0) * KPW + jj;
-        // [N][K]: this wave's k steps of block kb = 2 st + ks / 4 start here / end here
+        // [N][K]: this wave's k steps of block kb = 2 st + ks / 4 start here
+        // / end here (ks = wk + WK jj with wk < WK and WK dividing 4 or
+        // equal to 8, so a block starts at jj where WK jj is a multiple of 4)
         const bool kb_first = jj == 0 || (ks >> 2) != ((ks - WK) >> 2);
         const bool kb_last = jj + 1 == KPW || (ks >> 2) != ((ks + WK) >> 2);
         if (NK && kb_first) block_scales(2 * (int64_t)st + (ks >> 2), s8);
@@ -678,9 +666,9 @@ __global__ __launch_bounds__(LM_THREADS, 1) void k_linear_mfma(
         // slot p is free: step gs + 2 goes there, about two steps ahead of its use
         if constexpr ((KPW & 1) != 0) {
           ar[0] = ar[1];
-          if (gs + 2 < nsteps) load_step(ar[1], gs + 2);
+          load_step(ar[1], gs + 2);
         } else {
-          if (gs + 2 < nsteps) load_step(ar[p], gs + 2);
+          load_step(ar[p], gs + 2);
         }
         __builtin_amdgcn_sched_barrier(0);
         mfmas(ahi, alo, bt, 0, BT);
@@ -797,14 +785,45 @@ __device__ __forceinline__ void lm_put(float* __restrict__ xs, _Float16* __restr
   }
 }
 
+//
+// Workgroups M .. M + NB - 1 (the [K][N] product) find es[nb] instead: the
+// power of two that puts the largest |scale| of column block nb (row nb of
+// the block-major scales sT [NB][K]) in [2^13, 2^14), 0 for a zero or
+// non-finite maximum.  It depends on the weight alone; computed here, it is
+// ready before the main kernel starts.
 template <typename T, bool SPLIT, bool VEC>
-__global__ __launch_bounds__(256) void k_linear_mfma_prep_rows(const T* __restrict__ x, int64_t K, int64_t Kp,
-                                                               float* __restrict__ xs, _Float16* __restrict__ xh,
-                                                               _Float16* __restrict__ xl, int* __restrict__ ex) {
+__global__ __launch_bounds__(256) void k_linear_mfma_prep_rows(const T* __restrict__ x, int64_t M, int64_t K,
+                                                               int64_t Kp, float* __restrict__ xs,
+                                                               _Float16* __restrict__ xh, _Float16* __restrict__ xl,
+                                                               int* __restrict__ ex, const float* __restrict__ sT,
+                                                               int* __restrict__ es) {
   constexpr int E = 16 / (int)sizeof(T), NCH = 8;
   __shared__ float red[4];
-  const int64_t m = blockIdx.x;
   const int tid = threadIdx.x;
+  if ((int64_t)blockIdx.x >= M) {
+    const int64_t nb = (int64_t)blockIdx.x - M;
+    const float* s = sT + nb * K;
+    float mx = 0.0f;
+    int64_t k = tid;
+    for (; k + 7 * 256 < K; k += 8 * 256) {
+      float v[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) v[u] = s[k + 256 * u];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) mx = fmaxf(mx, __builtin_fabsf(v[u]));
+    }
+    for (; k < K; k += 256) mx = fmaxf(mx, __builtin_fabsf(s[k]));
+    mx = group_max<64>(mx);
+    if ((tid & 63) == 0) red[tid >> 6] = mx;
+    __syncthreads();
+    if (tid == 0) {
+      mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+      const int be = (int)((__float_as_uint(mx) >> 23) & 0xFFu);
+      es[nb] = (be == 0xFF || mx == 0.0f) ? 0 : 140 - (be == 0 ? 1 : be);
+    }
+    return;
+  }
+  const int64_t m = blockIdx.x;
   const T* row = x + m * K;
   const int64_t nch = K / E;
   const bool cached = VEC && nch <= (int64_t)NCH * 256;
@@ -940,7 +959,7 @@ LmPlan lm_plan(int64_t M, int64_t K, int64_t N, bool nk, int bits) {
 
 template <int FMT, int WM, bool NK, bool TILED>
 void lm_launch_t(const LmPlan& p, hipStream_t st, const float* xs, const _Float16* xh, const _Float16* xl,
-                 const float* sc, int sc_kbm, const int* ex, int* es, const uint8_t* w, int64_t M, int64_t K,
+                 const float* sc, int sc_kbm, const int* ex, const int* es, const uint8_t* w, int64_t M, int64_t K,
                  int64_t N, const float* bias, float* out, float* part) {
   const dim3 grid((unsigned)(N / 128), (unsigned)ceil_div(M, 32 * WM), (unsigned)p.S);
   hipLaunchKernelGGL((k_linear_mfma<FMT, WM, NK, TILED>), grid, dim3(LM_THREADS), 0, st, xs, xh, xl, sc, sc_kbm, ex,
@@ -949,7 +968,7 @@ void lm_launch_t(const LmPlan& p, hipStream_t st, const float* xs, const _Float1
 
 template <int FMT, bool NK, bool TILED = false>
 void lm_launch_w(const LmPlan& p, hipStream_t st, const float* xs, const _Float16* xh, const _Float16* xl,
-                 const float* sc, int sc_kbm, const int* ex, int* es, const uint8_t* w, int64_t M, int64_t K,
+                 const float* sc, int sc_kbm, const int* ex, const int* es, const uint8_t* w, int64_t M, int64_t K,
                  int64_t N, const float* bias, float* out, float* part) {
   constexpr int MW = lm_max_wm(NK, lm_bits(FMT));
   switch (p.wm) {
@@ -964,22 +983,26 @@ void lm_launch_w(const LmPlan& p, hipStream_t st, const float* xs, const _Float1
   }
 }
 
+// rows of x (and, with sT, the NB column-block exponents of a [K][N] weight)
 template <typename T, bool SPLIT>
 void lm_prep_rows_t(const T* x, int64_t M, int64_t K, int64_t Kp, float* xs, _Float16* xh, _Float16* xl, int* ex,
-                    hipStream_t st) {
-  const dim3 grid((unsigned)M);
+                    const float* sT, int64_t NB, int* es, hipStream_t st) {
+  const dim3 grid((unsigned)(M + (sT ? NB : 0)));
   if (aligned16(x) && (K * (int64_t)sizeof(T)) % 16 == 0)
-    hipLaunchKernelGGL((k_linear_mfma_prep_rows<T, SPLIT, true>), grid, dim3(256), 0, st, x, K, Kp, xs, xh, xl, ex);
+    hipLaunchKernelGGL((k_linear_mfma_prep_rows<T, SPLIT, true>), grid, dim3(256), 0, st, x, M, K, Kp, xs, xh, xl, ex,
+                       sT, es);
   else
-    hipLaunchKernelGGL((k_linear_mfma_prep_rows<T, SPLIT, false>), grid, dim3(256), 0, st, x, K, Kp, xs, xh, xl, ex);
+    hipLaunchKernelGGL((k_linear_mfma_prep_rows<T, SPLIT, false>), grid, dim3(256), 0, st, x, M, K, Kp, xs, xh, xl,
+                       ex, sT, es);
 }
 
 template <bool SPLIT>
 void lm_prep_rows(const void* x, int x_type, int64_t M, int64_t K, int64_t Kp, float* xs, _Float16* xh, _Float16* xl,
-                  int* ex, hipStream_t st) {
-  if (x_type == MXK_IN_F32) lm_prep_rows_t<float, SPLIT>((const float*)x, M, K, Kp, xs, xh, xl, ex, st);
-  else if (x_type == MXK_IN_F16) lm_prep_rows_t<__half, SPLIT>((const __half*)x, M, K, Kp, xs, xh, xl, ex, st);
-  else lm_prep_rows_t<hip_bfloat16, SPLIT>((const hip_bfloat16*)x, M, K, Kp, xs, xh, xl, ex, st);
+                  int* ex, const float* sT, int64_t NB, int* es, hipStream_t st) {
+  if (x_type == MXK_IN_F32) lm_prep_rows_t<float, SPLIT>((const float*)x, M, K, Kp, xs, xh, xl, ex, sT, NB, es, st);
+  else if (x_type == MXK_IN_F16)
+    lm_prep_rows_t<__half, SPLIT>((const __half*)x, M, K, Kp, xs, xh, xl, ex, sT, NB, es, st);
+  else lm_prep_rows_t<hip_bfloat16, SPLIT>((const hip_bfloat16*)x, M, K, Kp, xs, xh, xl, ex, sT, NB, es, st);
 }
 
 bool lm_common_ok(int64_t M, int64_t K, int64_t N, int kind, int bits, int block, int x_type, const float* out) {
@@ -990,7 +1013,7 @@ bool lm_common_ok(int64_t M, int64_t K, int64_t N, int kind, int bits, int block
   const int64_t Kp = ceil_div(K, LM_STAGE) * LM_STAGE, lim = int64_t(1) << 31;
   // 32-bit buffer offsets: codes (with the padded stage rows), one row tile of x', the scales
   if ((Kp + LM_STAGE) * N * bits / 8 >= lim || 256 * Kp * 4 >= lim || (N / 128) * Kp * 4 >= lim) return false;
-  if (ceil_div(M, 32) >= 65536 || N / 128 >= (int64_t(1) << 31)) return false;
+  if (ceil_div(M, 32) >= 65536 || M + N / 128 >= (int64_t(1) << 31)) return false;
   return true;
 }
 
@@ -1022,13 +1045,13 @@ int linear_mfma_kn(const void* x, int x_type, int64_t M, int64_t K, const void* 
   float* sc = reinterpret_cast<float*>(ws + p.off_s);
   float* part = reinterpret_cast<float*>(ws + p.off_p);
   const int64_t NB = N / 128;
-  lm_prep_rows<false>(x, x_type, M, K, p.Kp, xs, nullptr, nullptr, ex, st);
   const float* sT = w_scales_t;
   if (!sT) {
     hipLaunchKernelGGL(k_linear_mfma_scales_t, dim3((unsigned)ceil_div(K * NB, 256)), dim3(256), 0, st, w_scales, K,
                        NB, sc);
     sT = sc;
   }
+  lm_prep_rows<false>(x, x_type, M, K, p.Kp, xs, nullptr, nullptr, ex, sT, NB, es, st);
   const uint8_t* w = reinterpret_cast<const uint8_t*>(w_packed);
   const int fmt = lm_format(kind, bits);
   switch (fmt) {
@@ -1061,7 +1084,7 @@ int linear_mfma_kn_tiled(const void* x, int x_type, int64_t M, int64_t K, const 
   int* es = reinterpret_cast<int*>(ws + p.off_es);
   float* xs = reinterpret_cast<float*>(ws + p.off_x);
   float* part = reinterpret_cast<float*>(ws + p.off_p);
-  lm_prep_rows<false>(x, x_type, M, K, p.Kp, xs, nullptr, nullptr, ex, st);
+  lm_prep_rows<false>(x, x_type, M, K, p.Kp, xs, nullptr, nullptr, ex, w_scales_t, N / 128, es, st);
   lm_launch_w<LM_I4, false, true>(p, st, xs, nullptr, nullptr, w_scales_t, 1, ex, es,
                                   reinterpret_cast<const uint8_t*>(w_tiled), M, K, N, bias, out, part);
   if (p.S > 1)
@@ -1086,7 +1109,7 @@ int linear_mfma_nk(const void* x, int x_type, int64_t M, int64_t K, const void* 
   _Float16* xh = reinterpret_cast<_Float16*>(ws + p.off_x);
   _Float16* xl = xh + (size_t)lm_rows16(M) * (size_t)p.Kp;
   float* part = reinterpret_cast<float*>(ws + p.off_p);
-  lm_prep_rows<true>(x, x_type, M, K, p.Kp, nullptr, xh, xl, ex, st);
+  lm_prep_rows<true>(x, x_type, M, K, p.Kp, nullptr, xh, xl, ex, nullptr, 0, nullptr, st);
   const float* sc = w_scales_t ? w_scales_t : w_scales;
   const int kbm = w_scales_t ? 1 : 0;
   const uint8_t* w = reinterpret_cast<const uint8_t*>(w_packed);
@@ -1121,7 +1144,7 @@ int linear_mfma_nk_tiled(const void* x, int x_type, int64_t M, int64_t K, const 
   _Float16* xh = reinterpret_cast<_Float16*>(ws + p.off_x);
   _Float16* xl = xh + (size_t)lm_rows16(M) * (size_t)p.Kp;
   float* part = reinterpret_cast<float*>(ws + p.off_p);
-  lm_prep_rows<true>(x, x_type, M, K, p.Kp, nullptr, xh, xl, ex, st);
+  lm_prep_rows<true>(x, x_type, M, K, p.Kp, nullptr, xh, xl, ex, nullptr, 0, nullptr, st);
   lm_launch_w<LM_I4, true, true>(p, st, nullptr, xh, xl, w_scales_t, 1, ex, nullptr,
                                  reinterpret_cast<const uint8_t*>(w_tiled), M, K, N, bias, out, part);
   if (p.S > 1)

@@ -129,7 +129,7 @@ class kv_cache_quantizer:
                 and k2.dtype == v2.dtype:
             kx, vx = k2.contiguous(), v2.contiguous()
             zp = self._zp[slot] if self.asymmetric_v else None
-            with torch.cuda.device(dev):
+            with L.on_device(dev):
                 rc = L.lib().mxk_kv_append(kx.data_ptr(), vx.data_ptr(), L.elem_type(kx.dtype), rows, D, kind,
                                            dt.bits, var, int(self.asymmetric_v), self._kc[slot].data_ptr(),
                                            self._ks[slot].data_ptr(), self._vc[slot].data_ptr(),
@@ -164,7 +164,7 @@ class kv_cache_quantizer:
             outs = []
             for codes, scales, zp in ((self._kc, self._ks, None), (self._vc, self._vs, self._zp)):
                 out = torch.empty(rows, T, D, dtype=torch.float32, device=dev)
-                with torch.cuda.device(dev):
+                with L.on_device(dev):
                     rc = L.lib().mxk_kv_gather(codes.data_ptr(), scales.data_ptr(), L.ptr(zp), rows, D, kind,
                                                dt.bits, var, self._cap, self._start, T, out.data_ptr(),
                                                L.stream_of(out))

@@ -229,7 +229,7 @@ def quantize(x: Tensor, dt, block: int = 128, *, seed: Optional[int] = None,
     lib = L.lib()
     ws_bytes = lib.mxk_quantize_workspace(n, kind, dt.bits, var, block, rot_dim)
     ws = _workspace(ws_bytes, dev)
-    with torch.cuda.device(dev):
+    with L.on_device(dev):
         rc = lib.mxk_quantize(xc.data_ptr(), L.elem_type(xc.dtype), n, kind, dt.bits, var, block,
                               L.ptr(sg), rot_dim, packed.data_ptr(), packed.numel() * packed.element_size(),
                               scales.data_ptr(), n_store, L.ptr(ws), ws_bytes, L.stream_of(xc))
@@ -262,7 +262,7 @@ def _dequant(packed: Tensor, scales: Tensor, dt, n: int, block: int, *, orig_sha
     lib = L.lib()
     ws_bytes = lib.mxk_dequantize_workspace(n, var, rot_dim)
     ws = _workspace(ws_bytes, dev)
-    with torch.cuda.device(dev):
+    with L.on_device(dev):
         rc = lib.mxk_dequantize(pk.data_ptr(), pk.numel() * pk.element_size(), sc.data_ptr(), sc.numel(), n,
                                 kind, dt.bits, var, block, L.ptr(sg), rot_dim, out.data_ptr(), L.ptr(ws),
                                 ws_bytes, L.stream_of(pk))
@@ -325,7 +325,7 @@ def qscale_gemm(a_packed: Tensor, a_scales: Tensor, b_packed: Tensor, b_scales: 
     lib = L.lib()
     ws_bytes = lib.mxk_qgemm_workspace(M, K, N, bits, block, out_bits if want_packed else 0)
     ws = _workspace(ws_bytes, dev)
-    with torch.cuda.device(dev):
+    with L.on_device(dev):
         rc = lib.mxk_qgemm(ap.data_ptr(), asc.data_ptr(), n_asc, bp.data_ptr(), bsc.data_ptr(), n_bsc,
                            M, K, N, bits, block, out_bits if want_packed else 0,
                            L.ptr(cp), 0 if cp is None else cp.numel() * cp.element_size(), L.ptr(cs), L.ptr(cf),
@@ -360,7 +360,7 @@ def prepack_scales(w_scales: Tensor, in_features: int, out_features: int, block:
     if sc.numel() != K * (N // block):
         raise L.MXKError(f"prepack_scales: {sc.numel()} scales for a {K}x{N} weight with block {block}")
     out = torch.empty(N // block, K, dtype=torch.float32, device=dev)
-    with torch.cuda.device(dev):
+    with L.on_device(dev):
         rc = L.lib().mxk_linear_prepack_scales(sc.data_ptr(), K, N, block, out.data_ptr(), L.stream_of(sc))
     L.check(rc, f"prepack_scales({K}x{N})")
     return out
@@ -378,7 +378,7 @@ def prepack_weight(w_packed: Tensor, in_features: int, out_features: int, block:
     if pk.data_ptr() % 4:
         pk = pk.clone()
     out = torch.empty(K * N // 2, dtype=torch.uint8, device=dev)
-    with torch.cuda.device(dev):
+    with L.on_device(dev):
         rc = L.lib().mxk_linear_prepack_weight(pk.data_ptr(), K, N, 4, block, out.data_ptr(), L.stream_of(pk))
     L.check(rc, f"prepack_weight({K}x{N})")
     return out
@@ -393,7 +393,7 @@ def unpack_weight(w_tiled: Tensor, in_features: int, out_features: int, block: i
     if w_tiled.numel() * w_tiled.element_size() != K * N // 2:
         raise L.MXKError(f"unpack_weight: {w_tiled.numel()} bytes for a {K}x{N} int4 weight")
     out = torch.empty(K * N // 2, dtype=torch.uint8, device=dev)
-    with torch.cuda.device(dev):
+    with L.on_device(dev):
         rc = L.lib().mxk_linear_unpack_weight(w_tiled.data_ptr(), K, N, 4, block, out.data_ptr(),
                                                L.stream_of(w_tiled))
     L.check(rc, f"unpack_weight({K}x{N})")
@@ -449,7 +449,7 @@ def linear_wq(x: Tensor, w_packed: Optional[Tensor], w_scales: Tensor, dt, in_fe
     ws_bytes = lib.mxk_linear_workspace(M, K, N, dt.bits, block)
     stream = L.stream_of(xc)
     ws = _zeroed_workspace(ws_bytes, dev, stream)
-    with torch.cuda.device(dev):
+    with L.on_device(dev):
         rc = L.MXK_EUNSUPPORTED
         if w_tiled is not None and w_scales_t is not None and decode_prepack_eligible(dt, block, K, N):
             rc = lib.mxk_linear_wq_tiled(xc.data_ptr(), L.elem_type(xc.dtype), M, K, w_tiled.data_ptr(),
@@ -504,7 +504,7 @@ def qelementwise(op: str, a_packed: Tensor, a_scales: Tensor, b_packed: Optional
     lib = L.lib()
     ws_bytes = lib.mxk_qelementwise_workspace(code, n, nb, block, bits, out_bits)
     ws = _workspace(ws_bytes, dev)
-    with torch.cuda.device(dev):
+    with L.on_device(dev):
         rc = lib.mxk_qelementwise(code, ap.data_ptr(), ap.numel() * ap.element_size(), asc.data_ptr(),
                                   L.ptr(bp), 0 if bp is None else bp.numel() * bp.element_size(), L.ptr(bsc),
                                   n, nb, block, bits, out_bits, out.data_ptr(), out.numel() * out.element_size(),
@@ -547,7 +547,7 @@ def dynamic_quantize(x: Tensor, dt, granularity: str = "per_token") -> Tuple[Ten
     lib = L.lib()
     ws_bytes = lib.mxk_dynamic_quantize_workspace(rows, cols, g, dt.bits)
     ws = _workspace(ws_bytes, dev)
-    with torch.cuda.device(dev):
+    with L.on_device(dev):
         rc = lib.mxk_dynamic_quantize(xs.data_ptr(), L.elem_type(xs.dtype), rows, cols, g, dt.bits, packed.data_ptr(),
                                       packed.numel() * packed.element_size(), scales.data_ptr(), L.ptr(ws), ws_bytes,
                                       L.stream_of(xs))
@@ -576,7 +576,7 @@ def prepack_weight_nt(w_packed: Tensor, out_features: int, in_features: int, blo
     if pk.data_ptr() % 16:
         pk = pk.clone()
     out = torch.empty(K * N // 2, dtype=torch.uint8, device=dev)
-    with torch.cuda.device(dev):
+    with L.on_device(dev):
         rc = L.lib().mxk_linear_prepack_weight_nt(pk.data_ptr(), N, K, 4, block, out.data_ptr(), L.stream_of(pk))
     L.check(rc, f"prepack_weight_nt({N}x{K})")
     return out
@@ -591,7 +591,7 @@ def unpack_weight_nt(w_tiled: Tensor, out_features: int, in_features: int, block
     if w_tiled.numel() * w_tiled.element_size() != K * N // 2:
         raise L.MXKError(f"unpack_weight_nt: {w_tiled.numel()} bytes for a {N}x{K} int4 weight")
     out = torch.empty(K * N // 2, dtype=torch.uint8, device=dev)
-    with torch.cuda.device(dev):
+    with L.on_device(dev):
         rc = L.lib().mxk_linear_unpack_weight_nt(w_tiled.data_ptr(), N, K, 4, block, out.data_ptr(),
                                                   L.stream_of(w_tiled))
     L.check(rc, f"unpack_weight_nt({N}x{K})")
@@ -651,7 +651,7 @@ def linear_wq_nt(x: Tensor, w_packed: Optional[Tensor], w_scales: Tensor, dt, ou
     ws_bytes = lib.mxk_linear_nt_workspace(M, K, N, dt.bits, block)
     stream = L.stream_of(xc)
     wk = _zeroed_workspace(ws_bytes, dev, stream)
-    with torch.cuda.device(dev):
+    with L.on_device(dev):
         rc = L.MXK_EUNSUPPORTED
         if w_tiled is not None and w_scales_t is not None and decode_prepack_nt_eligible(dt, block, K, N):
             bt = b if b is None or b.data_ptr() % 16 == 0 else b.clone()
@@ -700,7 +700,7 @@ def linear_i8(x_packed: Tensor, x_scales: Tensor, x_dt, x_block: int, w_packed: 
     lib = L.lib()
     ws_bytes = lib.mxk_linear_i8_workspace(M, K, N, x_dt.bits, w_dt.bits, x_block, w_block)
     ws = _workspace(ws_bytes, dev)
-    with torch.cuda.device(dev):
+    with L.on_device(dev):
         rc = lib.mxk_linear_i8(xp.data_ptr(), xp.numel() * xp.element_size(), xs.data_ptr(), xs.numel(), x_block,
                                x_dt.bits, wp.data_ptr(), wp.numel() * wp.element_size(), wsc.data_ptr(), wsc.numel(),
                                w_block, w_dt.bits, M, K, N, L.ptr(b), out.data_ptr(), L.ptr(ws), ws_bytes,
@@ -725,7 +725,7 @@ def vector_quantize(x: Tensor, dtype="int8d", axis: int = 1) -> Tuple[Tensor, Te
     rows, cols = xs.shape
     codes = torch.empty(rows, cols, dtype=torch.int32, device=dev)
     scales = torch.empty(rows if axis == 1 else cols, dtype=torch.float32, device=dev)
-    with torch.cuda.device(dev):
+    with L.on_device(dev):
         rc = L.lib().mxk_vector_quantize(xs.data_ptr(), L.elem_type(xs.dtype), rows, cols, axis, dt.bits,
                                          codes.data_ptr(), scales.data_ptr(), L.stream_of(xs))
     L.check(rc, f"vector_quantize({dt.name}, axis={axis}, {rows}x{cols})")
@@ -744,7 +744,7 @@ def vector_dequantize(codes: Tensor, scales: Tensor, axis: int = 1) -> Tensor:
     if sc.numel() != (rows if axis == 1 else cols):
         raise ValueError(f"vector_dequantize: {sc.numel()} scales for {rows}x{cols} codes along axis {axis}")
     out = torch.empty(rows, cols, dtype=torch.float32, device=dev)
-    with torch.cuda.device(dev):
+    with L.on_device(dev):
         rc = L.lib().mxk_vector_dequantize(c.data_ptr(), sc.data_ptr(), rows, cols, axis, out.data_ptr(),
                                            L.stream_of(c))
     L.check(rc, "vector_dequantize")
