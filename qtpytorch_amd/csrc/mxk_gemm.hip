@@ -978,31 +978,35 @@ __global__ __launch_bounds__(512, 1) void k_qgemm_kn(const int8_t* __restrict__ 
 }
 
 // ---------------------------------------------------------------- small GEMMs
-// int8 codes, block 128, operands and scales as stored, for shapes whose
-// 256x128 tiles do not give every CU a workgroup (config 1: 512^3), in one
-// launch.  One 32x32 output tile per workgroup of 4 waves; the K blocks go
-// round-robin to the waves (wave w: blocks w, w + 4, ...).  For its block a
-// wave
+// int8 codes, block BLK = 128 or 64, operands and scales as stored, for
+// shapes whose 256x128 tiles do not give every CU a workgroup (config 1:
+// 512^3), in one launch.  One 32x32 output tile per workgroup of 4 waves;
+// the K blocks go round-robin to the waves (wave w: blocks w, w + 4, ...).
+// For its block a wave
 //  - loads its A operands straight from A (rows m0 + 16i + lr, bytes
-//    16 lg .. 16 lg + 15 of each 64-wide half of the block),
-//  - copies the block's 128x32 slab of B (as stored, N-contiguous) into its
-//    own LDS slot and takes the B operands out with ds_read_b64_tr_b8 (K
+//    16 lg .. 16 lg + 15 of each 64-wide half of the block; one half for
+//    BLK = 64),
+//  - copies the block's BLK x 32 slab of B (as stored, N-contiguous) into
+//    its own LDS slot and takes the B operands out with ds_read_b64_tr_b8 (K
 //    rows 16 lg + 8 rd + lr / 2, half lr % 2 of each 16-column segment:
 //    lane lr then holds 8 K values of column lr),
-//  - runs 8 v_mfma_i32_16x16x64_i8 and forms v = RN(RN(P*SA)*SB) for its
-//    16 outputs per lane (v does not depend on C).
+//  - runs 4 v_mfma_i32_16x16x64_i8 per 64-wide half and forms
+//    v = RN(RN(P*SA)*SB) for its 16 outputs per lane (v does not depend on C).
 // The waves' v meet in LDS, where each thread adds those of its 4 outputs
 // to C in K-block order, C = RN(C + v) for kb ascending from C = +0, the
 // reference's sum (mxtorch.py:1357-1370).  The B slot is the wave's own, and
 // LDS runs one wave's accesses in order: no barrier between the copy and
 // the transposed reads.
 #define QGS_TILE 32
-template <bool WRITE_ACC, bool WRITE_C>
+template <bool WRITE_ACC, bool WRITE_C, int BLK>
 __global__ __launch_bounds__(256) void k_qgemm_small(const int8_t* __restrict__ A, const int8_t* __restrict__ B,
                                                      const float* __restrict__ sa, const float* __restrict__ sb,
                                                      int sa_ok, int sb_ok, int64_t M, int64_t K, int64_t N, int KB,
                                                      float* __restrict__ C, int32_t* __restrict__ acc_out) {
-  __shared__ __attribute__((aligned(16))) int8_t sB[4 * 128 * QGS_TILE];
+  static_assert(BLK == 64 || BLK == 128, "K blocks of one or two MFMA depths");
+  constexpr int H = BLK / 64;         // 64-wide halves of a K block
+  constexpr int NQ = BLK * QGS_TILE / 16 / 64;  // 16-byte pieces of the B slab per lane
+  __shared__ __attribute__((aligned(16))) int8_t sB[4 * BLK * QGS_TILE];
   __shared__ __attribute__((aligned(16))) float sV[4 * 64 * 16];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -1020,13 +1024,13 @@ __global__ __launch_bounds__(256) void k_qgemm_small(const int8_t* __restrict__ 
     const int64_t m = m0 + 16 * i + lr;
     oa[i] = m < M ? (uint32_t)(m * K + 16 * lg) : OOB;
   }
-  uint32_t ob[4];
+  uint32_t ob[NQ];
 #pragma unroll
-  for (int q = 0; q < 4; ++q) {
+  for (int q = 0; q < NQ; ++q) {
     const int c = lane + 64 * q, rr = c >> 1, hh = c & 1;
     ob[q] = n0 + 16 * hh < N ? (uint32_t)(rr * N + n0 + 16 * hh) : OOB;
   }
-  int8_t* slot = sB + wave * 128 * QGS_TILE;
+  int8_t* slot = sB + wave * BLK * QGS_TILE;
   const uint32_t tr_base = (uint32_t)(uintptr_t)slot + (uint32_t)((16 * lg + (lr >> 1)) * QGS_TILE + 8 * (lr & 1));
   float cacc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
   const int own = tid >> 6;  // this thread's (row tile, column tile) of lane `lane` in the sums
@@ -1034,15 +1038,15 @@ __global__ __launch_bounds__(256) void k_qgemm_small(const int8_t* __restrict__ 
   for (int kb0 = 0; kb0 < KB; kb0 += 4) {
     const int kb = kb0 + wave;
     if (kb < KB) {
-      u32x4 af[2][2], bl[4];
+      u32x4 af[2][H], bl[NQ];
 #pragma unroll
       for (int i = 0; i < 2; ++i)
 #pragma unroll
-        for (int h = 0; h < 2; ++h)
-          af[i][h] = buf_load_b128(rA, oa[i] == OOB ? OOB : oa[i] + 64u * h, (uint32_t)kb * 128u);
+        for (int h = 0; h < H; ++h)
+          af[i][h] = buf_load_b128(rA, oa[i] == OOB ? OOB : oa[i] + 64u * h, (uint32_t)kb * (uint32_t)BLK);
 #pragma unroll
-      for (int q = 0; q < 4; ++q)
-        bl[q] = buf_load_b128(rB, ob[q] == OOB ? OOB : ob[q], (uint32_t)((int64_t)kb * 128 * N));
+      for (int q = 0; q < NQ; ++q)
+        bl[q] = buf_load_b128(rB, ob[q] == OOB ? OOB : ob[q], (uint32_t)((int64_t)kb * BLK * N));
       float sav[2][4], sbv[2];
 #pragma unroll
       for (int i = 0; i < 2; ++i)
@@ -1059,31 +1063,33 @@ __global__ __launch_bounds__(256) void k_qgemm_small(const int8_t* __restrict__ 
                        : 1.0f;
       }
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
+      for (int q = 0; q < NQ; ++q) {
         const int c = lane + 64 * q;
         *reinterpret_cast<u32x4*>(slot + (c >> 1) * QGS_TILE + 16 * (c & 1)) = bl[q];
       }
       // B operands: column tile t, K half h, K rows 16 lg + 8 rd + 0..7
-      i32x2 btr[2][2][2];
+      i32x2 btr[2][H][2];
       btr[0][0][0] = qg3_ds_read_tr<0>(tr_base);
       btr[0][0][1] = qg3_ds_read_tr<8 * QGS_TILE>(tr_base);
-      btr[0][1][0] = qg3_ds_read_tr<64 * QGS_TILE>(tr_base);
-      btr[0][1][1] = qg3_ds_read_tr<72 * QGS_TILE>(tr_base);
       btr[1][0][0] = qg3_ds_read_tr<16>(tr_base);
       btr[1][0][1] = qg3_ds_read_tr<8 * QGS_TILE + 16>(tr_base);
-      btr[1][1][0] = qg3_ds_read_tr<64 * QGS_TILE + 16>(tr_base);
-      btr[1][1][1] = qg3_ds_read_tr<72 * QGS_TILE + 16>(tr_base);
+      if constexpr (H == 2) {
+        btr[0][H - 1][0] = qg3_ds_read_tr<64 * QGS_TILE>(tr_base);
+        btr[0][H - 1][1] = qg3_ds_read_tr<72 * QGS_TILE>(tr_base);
+        btr[1][H - 1][0] = qg3_ds_read_tr<64 * QGS_TILE + 16>(tr_base);
+        btr[1][H - 1][1] = qg3_ds_read_tr<72 * QGS_TILE + 16>(tr_base);
+      }
 #pragma unroll
       for (int t = 0; t < 2; ++t)
 #pragma unroll
-        for (int h = 0; h < 2; ++h)
+        for (int h = 0; h < H; ++h)
 #pragma unroll
           for (int rd = 0; rd < 2; ++rd) qg3_lgkm_wait<0>(btr[t][h][rd]);
-      i32x4 bf[2][2];
+      i32x4 bf[2][H];
 #pragma unroll
       for (int t = 0; t < 2; ++t)
 #pragma unroll
-        for (int h = 0; h < 2; ++h)
+        for (int h = 0; h < H; ++h)
           bf[t][h] = i32x4{btr[t][h][0][0], btr[t][h][0][1], btr[t][h][1][0], btr[t][h][1][1]};
       f32x4v* vout = reinterpret_cast<f32x4v*>(sV + (wave * 64 + lane) * 16);
 #pragma unroll
@@ -1092,7 +1098,9 @@ __global__ __launch_bounds__(256) void k_qgemm_small(const int8_t* __restrict__ 
         for (int t = 0; t < 2; ++t) {
           i32x4 p = __builtin_amdgcn_mfma_i32_16x16x64_i8(__builtin_bit_cast(i32x4, af[i][0]), bf[t][0],
                                                           i32x4{0, 0, 0, 0}, 0, 0, 0);
-          p = __builtin_amdgcn_mfma_i32_16x16x64_i8(__builtin_bit_cast(i32x4, af[i][1]), bf[t][1], p, 0, 0, 0);
+          if constexpr (H == 2)
+            p = __builtin_amdgcn_mfma_i32_16x16x64_i8(__builtin_bit_cast(i32x4, af[i][H - 1]), bf[t][H - 1], p, 0, 0,
+                                                      0);
           f32x4v v;
 #pragma unroll
           for (int r = 0; r < 4; ++r) v[r] = ((float)p[r] * sav[i][r]) * sbv[t];
@@ -1199,7 +1207,7 @@ struct GemmPlan {
   int KB, BP;
   int64_t KBP, Mpad, Npad;
   bool direct_a, v2, v3;
-  bool small = false;  // k_qgemm_small: int8, block 128, grids of 256x128 tiles below the CU count
+  bool small = false;  // k_qgemm_small: int8, block 128 or 64, grids of 256x128 tiles below the CU count
   int kn;  // 1: int8 with B read as stored, 2: int4 A and B read as stored (k_qgemm_kn), 0: unpacking pre-pass
   int req;  // output width requantized in the GEMM's epilogue (kn, N % 128 == 0), 0: a second pass
   size_t a_bytes, b_bytes, c_bytes, q_bytes, sa_bytes, sb_bytes, su_bytes;
@@ -1244,7 +1252,8 @@ static GemmPlan plan_gemm(int64_t M, int64_t K, int64_t N, int bits, int block, 
     return p;
   }
   // small int8 shapes: one launch on the operands and scales as stored
-  p.small = aligned && bits == 8 && block == 128 && K % 128 == 0 && N % 16 == 0 && !big && M * K < lim &&
+  p.small = aligned && bits == 8 && (block == 128 || block == 64) && K % block == 0 && N % 16 == 0 && !big &&
+            M * K < lim &&
             K * N < lim && (int64_t)p.KB * M * 4 < lim && (int64_t)p.KB * N * 4 < lim &&
             ceil_div(M, QGS_TILE) < 65536;
   if (p.small) {
@@ -1430,15 +1439,19 @@ int mxk_qgemm(const void* a_packed, const float* a_scales, int64_t a_nscales, co
     const dim3 grid((unsigned)ceil_div(N, QGS_TILE), (unsigned)ceil_div(M, QGS_TILE));
     const int8_t* A = (const int8_t*)a_packed;
     const int8_t* B = (const int8_t*)b_packed;
-    if (acc_i32 && Cb)
-      hipLaunchKernelGGL((k_qgemm_small<true, true>), grid, dim3(256), 0, st, A, B, a_scales, b_scales, a_ok, b_ok, M,
-                         K, N, p.KB, Cb, acc_i32);
-    else if (acc_i32)
-      hipLaunchKernelGGL((k_qgemm_small<true, false>), grid, dim3(256), 0, st, A, B, a_scales, b_scales, a_ok, b_ok,
-                         M, K, N, p.KB, Cb, acc_i32);
-    else
-      hipLaunchKernelGGL((k_qgemm_small<false, true>), grid, dim3(256), 0, st, A, B, a_scales, b_scales, a_ok, b_ok,
-                         M, K, N, p.KB, Cb, acc_i32);
+#define QGS_LAUNCH(WA, WC, BLK)                                                                               \
+  hipLaunchKernelGGL((k_qgemm_small<WA, WC, BLK>), grid, dim3(256), 0, st, A, B, a_scales, b_scales, a_ok, b_ok, M, \
+                     K, N, p.KB, Cb, acc_i32)
+    if (block == 128) {
+      if (acc_i32 && Cb) QGS_LAUNCH(true, true, 128);
+      else if (acc_i32) QGS_LAUNCH(true, false, 128);
+      else QGS_LAUNCH(false, true, 128);
+    } else {
+      if (acc_i32 && Cb) QGS_LAUNCH(true, true, 64);
+      else if (acc_i32) QGS_LAUNCH(true, false, 64);
+      else QGS_LAUNCH(false, true, 64);
+    }
+#undef QGS_LAUNCH
     const int rc = check_launch("qgemm");
     if (rc != MXK_OK || out_bits <= 0) return rc;
     return requant_vec_f32(Cb, M * N, out_bits, block, c_packed, c_packed_nbytes, c_scales, M * N, ws + p.c_bytes,

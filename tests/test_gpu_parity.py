@@ -519,9 +519,11 @@ SMALL_GEMM_SHAPES = [(40, 384, 48), (16, 1024, 16), (64, 1152, 96), (1, 128, 32)
                      (40, 384, 256), (300, 1152, 384), (1, 128, 128)]
 
 
+@pytest.mark.parametrize("block", [128, 64])
 @pytest.mark.parametrize("shape", SMALL_GEMM_SHAPES, ids=lambda s: "x".join(map(str, s)))
-def test_qgemm_small_tiles(qa, shape):
-    """The one-launch int8 kernel for grids below the CU count: 32x32 tiles,
+def test_qgemm_small_tiles(qa, shape, block):
+    """The one-launch int8 kernel for grids below the CU count, with K blocks
+    of 128 and of 64 (the reference's benchmark block): 32x32 tiles,
     K blocks round-robin over 4 waves (9 blocks: a short last round), M and
     N tails inside a tile, N below the tile; C, the int32 accumulators (all
     three kernel variants) and the int16d requantization bitwise against the
@@ -531,58 +533,62 @@ def test_qgemm_small_tiles(qa, shape):
     dt = qa.get_mx_dtype("int8d")
     A = _randn((M, K), 401 + M)
     B = _randn((K, N), 409 + N)
-    pa, sa, _ = qa.ops.quantize(A.to(dev()), dt, 128)
-    pb, sb, _ = qa.ops.quantize(B.to(dev()), dt, 128)
-    res = qa.ops.qscale_gemm(pa, sa, pb, sb, M, K, N, 8, 128, 16, want_c=True, want_acc=True)
-    c_only = qa.ops.qscale_gemm(pa, sa, pb, sb, M, K, N, 8, 128, 16, want_packed=False, want_c=True)
-    acc_only = qa.ops.qscale_gemm(pa, sa, pb, sb, M, K, N, 8, 128, 16, want_packed=False, want_acc=True)
-    rpa, rsa, _ = orc.quantize(A, "int8d", 128)
-    rpb, rsb, _ = orc.quantize(B, "int8d", 128)
+    pa, sa, _ = qa.ops.quantize(A.to(dev()), dt, block)
+    pb, sb, _ = qa.ops.quantize(B.to(dev()), dt, block)
+    res = qa.ops.qscale_gemm(pa, sa, pb, sb, M, K, N, 8, block, 16, want_c=True, want_acc=True)
+    c_only = qa.ops.qscale_gemm(pa, sa, pb, sb, M, K, N, 8, block, 16, want_packed=False, want_c=True)
+    acc_only = qa.ops.qscale_gemm(pa, sa, pb, sb, M, K, N, 8, block, 16, want_packed=False, want_acc=True)
+    rpa, rsa, _ = orc.quantize(A, "int8d", block)
+    rpb, rsb, _ = orc.quantize(B, "int8d", block)
     ac = orc.unpack_auto(rpa, 8, M * K).to(torch.int32)
     bc = orc.unpack_auto(rpb, 8, K * N).to(torch.int32)
-    codes, scales, C = orc.qscale_matmul(ac, rsa, bc, rsb, M, K, N, 8, 128, 16, return_c=True)
-    acc = orc.int_accumulators(ac, bc, M, K, N, 128)
+    codes, scales, C = orc.qscale_matmul(ac, rsa, bc, rsb, M, K, N, 8, block, 16, return_c=True)
+    acc = orc.int_accumulators(ac, bc, M, K, N, block)
     assert torch.equal(res["acc"].cpu(), acc), "int32 accumulators differ"
     assert torch.equal(acc_only["acc"].cpu(), acc)
     assert _bits_eq(res["c"], C), "fp32 accumulator C differs"
     assert _bits_eq(c_only["c"], C)
     assert _bits_eq(res["packed"], orc.pack_auto(codes, 16))
     assert _bits_eq(res["scales"], scales)
-    pk_only = qa.ops.qscale_gemm(pa, sa, pb, sb, M, K, N, 8, 128, 16)
+    pk_only = qa.ops.qscale_gemm(pa, sa, pb, sb, M, K, N, 8, block, 16)
     assert _bits_eq(pk_only["packed"], orc.pack_auto(codes, 16))
     assert _bits_eq(pk_only["scales"], scales)
     for a_s, b_s in ((sa[:-1], sb), (sa, sb[:-1]), (sa[:-1], sb[:-1])):
-        got = qa.ops.qscale_gemm(pa, a_s, pb, b_s, M, K, N, 8, 128, 16, want_packed=False, want_c=True)
+        got = qa.ops.qscale_gemm(pa, a_s, pb, b_s, M, K, N, 8, block, 16, want_packed=False, want_c=True)
         ra = rsa[:-1] if a_s.numel() < sa.numel() else rsa
         rb = rsb[:-1] if b_s.numel() < sb.numel() else rsb
-        _, _, Cw = orc.qscale_matmul(ac, ra, bc, rb, M, K, N, 8, 128, 16, return_c=True)
+        _, _, Cw = orc.qscale_matmul(ac, ra, bc, rb, M, K, N, 8, block, 16, return_c=True)
         assert _bits_eq(got["c"], Cw), "C with ones for a mis-sized scale array differs"
 
 
-def _small_gemm_shapes(seed, count):
+def _small_gemm_shapes(seed, count, block=128):
     g = np.random.default_rng(seed)
-    return [(int(g.integers(1, 300)), int(g.integers(1, 13)) * 128, int(g.integers(1, 41)) * 16) for _ in range(count)]
+    kmax = 1536 // block + 1
+    return [(int(g.integers(1, 300)), int(g.integers(1, kmax)) * block, int(g.integers(1, 41)) * 16, block)
+            for _ in range(count)]
 
 
-@pytest.mark.parametrize("shape", _small_gemm_shapes(4242, 10), ids=lambda s: "x".join(map(str, s)))
+@pytest.mark.parametrize("shape", _small_gemm_shapes(4242, 10) + _small_gemm_shapes(4343, 10, 64),
+                         ids=lambda s: "x".join(map(str, s)))
 def test_qgemm_small_random_shapes(qa, shape):
     """Seeded random shapes through the one-launch int8 kernel (M 1..299, K a
-    multiple of 128 up to 1536, N a multiple of 16 up to 640): C, the int32
-    accumulators and the int16d codes bitwise against the oracle."""
-    M, K, N = shape
-    print(f"small gemm M={M} K={K} N={N}", flush=True)
+    multiple of the block (128, or 64: odd multiples included) up to 1536, N
+    a multiple of 16 up to 640): C, the int32 accumulators and the int16d
+    codes bitwise against the oracle."""
+    M, K, N, block = shape
+    print(f"small gemm M={M} K={K} N={N} block={block}", flush=True)
     dt = qa.get_mx_dtype("int8d")
     A = _randn((M, K), 503 + M)
     B = _randn((K, N), 509 + N)
-    pa, sa, _ = qa.ops.quantize(A.to(dev()), dt, 128)
-    pb, sb, _ = qa.ops.quantize(B.to(dev()), dt, 128)
-    res = qa.ops.qscale_gemm(pa, sa, pb, sb, M, K, N, 8, 128, 16, want_c=True, want_acc=True)
-    rpa, rsa, _ = orc.quantize(A, "int8d", 128)
-    rpb, rsb, _ = orc.quantize(B, "int8d", 128)
+    pa, sa, _ = qa.ops.quantize(A.to(dev()), dt, block)
+    pb, sb, _ = qa.ops.quantize(B.to(dev()), dt, block)
+    res = qa.ops.qscale_gemm(pa, sa, pb, sb, M, K, N, 8, block, 16, want_c=True, want_acc=True)
+    rpa, rsa, _ = orc.quantize(A, "int8d", block)
+    rpb, rsb, _ = orc.quantize(B, "int8d", block)
     ac = orc.unpack_auto(rpa, 8, M * K).to(torch.int32)
     bc = orc.unpack_auto(rpb, 8, K * N).to(torch.int32)
-    codes, scales, C = orc.qscale_matmul(ac, rsa, bc, rsb, M, K, N, 8, 128, 16, return_c=True)
-    assert torch.equal(res["acc"].cpu(), orc.int_accumulators(ac, bc, M, K, N, 128))
+    codes, scales, C = orc.qscale_matmul(ac, rsa, bc, rsb, M, K, N, 8, block, 16, return_c=True)
+    assert torch.equal(res["acc"].cpu(), orc.int_accumulators(ac, bc, M, K, N, block))
     assert _bits_eq(res["c"], C)
     assert _bits_eq(res["packed"], orc.pack_auto(codes, 16))
     assert _bits_eq(res["scales"], scales)
