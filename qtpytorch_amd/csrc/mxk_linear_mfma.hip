@@ -98,35 +98,35 @@ __device__ __forceinline__ uint32_t lm_i2pair(uint32_t d) {
   return __builtin_bit_cast(uint32_t, r);
 }
 // Two float codes (indices into the sorted grid of 2^B values: B = 4 FP4
-// E2M1, B = 8 FP8 E4M3 with exponent 15 a normal binade) at bits 0..B-1 and
-// 16..16+B-1 of d (the bits above each code ignored) as the f16 pair of their
-// grid values times vmax (6 or 480): the format's own values v, exact in f16.
-// c ^ 2^(B-1) is the B-bit one's complement of +-m, m the bit pattern of
-// |v| (the grid is symmetric and sorted); moved to the top of a 16-bit half,
-// xor-ed with its sign mask and shifted to f16's mantissa position, m is the
-// f16 of |v| * 2^-14 (FP4) or 2^-8 (FP8), subnormals included, and one f16
-// multiply by the power of two gives v.
+// E2M1, B = 8 FP8 E4M3 with exponent 15 a normal binade) as the f16 pair of
+// their grid values times vmax · 2^-P (vmax 6 or 480, P = 14 or 8): the
+// format's own values v, scaled by a power of two, exact in f16 (subnormal
+// for the smallest: the MFMA takes f16 subnormals).  FP4 codes sit at bits
+// 0-3 and 16-19 of d (the bits above each code ignored), FP8 codes at bits
+// 8-15 and 24-31 (the callers' byte permutes put them there; the bits below
+// ignored).  c ^ 2^(B-1) is the B-bit one's complement of +-m, m the bit
+// pattern of |v| (the grid is symmetric and sorted); at the top of a 16-bit
+// half, xor-ed with its sign mask and shifted to f16's mantissa position, m
+// is the f16 of |v| * 2^-P.
 template <int B>
 __device__ __forceinline__ uint32_t lm_fpair(uint32_t d) {
   typedef short s2v __attribute__((ext_vector_type(2)));
   // code at the top of each half, its top bit flipped
-  const uint32_t x = (d << (16 - B)) ^ 0x80008000u;
+  const uint32_t x = (B == 4 ? d << 12 : d) ^ 0x80008000u;
   const uint32_t sm = __builtin_bit_cast(uint32_t, __builtin_bit_cast(s2v, x) >> (short)15);
   const uint32_t y = x ^ sm;
   const uint32_t m = (y >> (B == 4 ? 3 : 1)) & (B == 4 ? 0x0E000E00u : 0x3F803F80u);
-  const uint32_t f = (sm & 0x80008000u) | m;
-  constexpr _Float16 P = (_Float16)(B == 4 ? 16384.0f : 256.0f);
-  const h2v r = __builtin_bit_cast(h2v, f) * h2v{P, P};
-  return __builtin_bit_cast(uint32_t, r);
+  return (sm & 0x80008000u) | m;
 }
 
 // Weight formats: the code width in the low 4 bits, 16 for float grids
 enum : int { LM_I2 = 2, LM_I4 = 4, LM_I8 = 8, LM_F4 = 16 + 4, LM_F8 = 16 + 8 };
 __host__ __device__ constexpr int lm_bits(int fmt) { return fmt & 15; }
-// The factor the outputs take for B fragments that hold v instead of the
-// grid value v / vmax: RN(1/6), RN(1/480), or 1 for integer codes.
+// The factor the outputs take for B fragments that hold v * 2^-P instead of
+// the grid value v / vmax: RN(1/6) * 2^14, RN(1/480) * 2^8, or 1 for integer
+// codes.
 __host__ __device__ constexpr float lm_post(int fmt) {
-  return fmt == LM_F4 ? 1.0f / 6.0f : fmt == LM_F8 ? 1.0f / 480.0f : 1.0f;
+  return fmt == LM_F4 ? (1.0f / 6.0f) * 16384.0f : fmt == LM_F8 ? (1.0f / 480.0f) * 256.0f : 1.0f;
 }
 inline int lm_format(int kind, int bits) {
   if (kind == MXK_KIND_INT) return bits == 2 ? LM_I2 : bits == 4 ? LM_I4 : bits == 8 ? LM_I8 : 0;
@@ -145,6 +145,15 @@ __device__ __forceinline__ uint32_t lm_pair(uint32_t d) {
 // v_perm_b32 selector: byte a of s1 into byte 0, byte b of s0 into byte 2, zeros in bytes 1 and 3
 __host__ __device__ constexpr uint32_t lm_sel(int a, int b) {
   return (uint32_t)a | 0x0C00u | ((uint32_t)(4 + b) << 16) | 0x0C000000u;
+}
+// the same bytes into bytes 1 and 3 (FP8 codes at the top of each half), zeros in bytes 0 and 2
+__host__ __device__ constexpr uint32_t lm_selh(int a, int b) {
+  return 0x0Cu | ((uint32_t)a << 8) | 0x0C0000u | ((uint32_t)(4 + b) << 24);
+}
+// the byte-pair selector a format's pair decoder takes
+template <int FMT>
+__host__ __device__ constexpr uint32_t lm_sel_f(int a, int b) {
+  return FMT == LM_F8 ? lm_selh(a, b) : lm_sel(a, b);
 }
 
 // p = x * s as f16 hi + lo for two elements: hi = RN16(x*s), lo =
@@ -220,7 +229,8 @@ __device__ __forceinline__ u4v kn_frag(const KnCodes<lm_bits(FMT)>& c, int t) {
       f[q] = lm_pair<FMT>((t & 1) ? d >> 4 : d);
     } else {
       const int h = t >> 2, u = t & 3;
-      f[q] = lm_pair<FMT>(__builtin_amdgcn_perm(c.w[2 * (2 * q + 1) + h], c.w[2 * (2 * q) + h], lm_sel(u, u)));
+      f[q] = lm_pair<FMT>(
+          __builtin_amdgcn_perm(c.w[2 * (2 * q + 1) + h], c.w[2 * (2 * q) + h], lm_sel_f<FMT>(u, u)));
     }
   }
   return f;
@@ -360,7 +370,7 @@ __device__ __forceinline__ void nk_store(const NkCodes<lm_bits(FMT)>& c, uint8_t
         for (int p = 0; p < 4; ++p) {
           const uint32_t wd = c.w[h][2 * e + (p >> 1)];
           const int b = 2 * (p & 1);
-          f[p] = lm_pair<FMT>(__builtin_amdgcn_perm(wd, wd, lm_sel(b, b + 1)));
+          f[p] = lm_pair<FMT>(__builtin_amdgcn_perm(wd, wd, lm_sel_f<FMT>(b, b + 1)));
         }
         *reinterpret_cast<u4v*>(sB + lm_frag_off(ks, t, j + 16 * g)) = f;
       }
