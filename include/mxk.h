@@ -154,13 +154,13 @@ int mxk_qgemm(const void* a_packed, const float* a_scales, int64_t a_nscales, co
               void* stream);
 
 /* Workspace bytes mxk_linear_wq needs (0 if none).  The decode path
- * (int4 weights, block 128, M <= 16, K % 32 == 0, N % 128 == 0) splits K
+ * (int4 and int8 weights, block 128, M <= 16, K % 32 == 0, N % 128 == 0) splits K
  * across workgroups; its workspace (a 64 KiB counter prefix, the partial
  * sums, then room for block-major scales when w_scales_t is NULL) must be
  * zero-filled before first use, and every call, of any shape, leaves the
  * counter prefix ready for the next one.  Calls sharing a workspace must
  * not overlap.  The size also covers mxk_linear_wq_tiled and the MFMA path
- * (int4 / int8 weights, block 128, N % 128 == 0, any M): its row exponents,
+ * (2-, 4- and 8-bit codes, block 128, N % 128 == 0, any M): its row exponents,
  * x scaled by them (M * roundup(K, 256) floats), a block-major copy of the
  * scales when w_scales_t is NULL and any K-split partials, all after the
  * counter prefix, which it leaves alone. */
@@ -181,14 +181,14 @@ int mxk_linear_prepack_scales(const float* w_scales, int64_t K, int64_t N, int b
  * blocks of `block` flat elements (mxtorch.py:7447).  The dequantized
  * weight RN(code*s) (mxtorch.py:1573-1575) is formed in registers only.
  * kind/bits as for mxk_quantize (base variant).  Float32 accumulation.
- * Int4 weights with x of at most 16 rows run the decode kernel; int4 and
- * int8 weights (block 128, N % 128 == 0) with any other x run on f16 MFMAs,
- * x * s as an f16 hi + lo pair against the exact codes (each term within
- * 2^-22 of x * RN(code * s), after a power-of-two scaling of every row of
- * x and every block of scales into f16's range); other widths and shapes a
- * scalar fallback.
+ * Int4 and int8 weights with x of at most 16 rows run the decode kernel;
+ * int2, int4, int8, FP4 and FP8 weights (block 128, N % 128 == 0) with any
+ * other x run on f16 MFMAs, x * s as an f16 hi + lo pair against the exact
+ * codes or grid values (each term within 2^-22 of x * RN(code * s), after a
+ * power-of-two scaling of every row of x and every block of scales into
+ * f16's range); other widths and shapes a scalar fallback.
  * w_scales_t: optional mxk_linear_prepack_scales() copy of w_scales, read
- * by the int4 decode path and the MFMA path (NULL: they transpose into the
+ * by the decode path and the MFMA path (NULL: they transpose into the
  * workspace). */
 int mxk_linear_wq(const void* x, int x_type, int64_t M, int64_t K, const void* w_packed,
                   const float* w_scales, const float* w_scales_t, int64_t N, int kind, int bits,

@@ -208,7 +208,7 @@ struct DecGeom {
   static constexpr int CPT = 2048 / TPB;
 };
 
-template <typename T, int STEPS, int NBW, int P>
+template <typename T, int STEPS, int NBW, int P, int BITS = 4>
 __global__ __launch_bounds__(DEC_THREADS, 1) void k_linear_w4_decode(
     const T* __restrict__ x, int M, int64_t K, int64_t N, const uint32_t* __restrict__ w,
     const float* __restrict__ scales_t, const float* __restrict__ bias, float* __restrict__ out,
@@ -277,15 +277,27 @@ __global__ __launch_bounds__(DEC_THREADS, 1) void k_linear_w4_decode(
   // valid by construction: a step past K (only in the last split when K is
   // not a multiple of R) re-reads rows 0..31, and its x rows and scales are
   // zeros.
-  const __amdgpu_buffer_rsrc_t rw = make_rsrc(w, (uint32_t)(K * N / 2));
-  const uint32_t row_bytes = (uint32_t)(N / 2);
-  const uint32_t vw = (uint32_t)(8 * g * row_bytes + (nb * 16 + j) * 4);
-  uint32_t wv[P][8];
+  // BITS = 8 (int8 codes): 8 bytes of a row per lane, words 2r and 2r + 1
+  // of row r; the prefetch is P steps deep as for int4 (the caller halves P)
+  static_assert(BITS == 4 || BITS == 8, "int4 or int8 codes");
+  constexpr int WPR = BITS / 4;  // 32-bit words of a lane's 8 columns in one row
+  const __amdgpu_buffer_rsrc_t rw = make_rsrc(w, (uint32_t)(K * N * BITS / 8));
+  const uint32_t row_bytes = (uint32_t)(N * BITS / 8);
+  const uint32_t vw = (uint32_t)(8 * g * row_bytes + (nb * 16 + j) * 4 * WPR);
+  uint32_t wv[P][8 * WPR];
   auto issue = [&](int slot, int st) {
     const int64_t k0 = kw + (int64_t)st * 32;
     const uint32_t kr = k0 < K ? (uint32_t)k0 : 0u;  // wave-uniform
 #pragma unroll
-    for (int r = 0; r < 8; ++r) wv[slot][r] = buf_load_b32_nt(rw, vw, (kr + r) * row_bytes);
+    for (int r = 0; r < 8; ++r) {
+      if constexpr (BITS == 4) {
+        wv[slot][r] = buf_load_b32_nt(rw, vw, (kr + r) * row_bytes);
+      } else {
+        const uint2 v = buf_load_b64_nt(rw, vw, (kr + r) * row_bytes);
+        wv[slot][2 * r] = v.x;
+        wv[slot][2 * r + 1] = v.y;
+      }
+    }
   };
   issue(0, 0);
   // keep the loads where they are written (the scheduler would otherwise
@@ -363,24 +375,37 @@ __global__ __launch_bounds__(DEC_THREADS, 1) void k_linear_w4_decode(
     const f32x4 s1 = *reinterpret_cast<const f32x4*>(srow + st * 32 + 4);
     f16x8 ahi, alo;
     split_hi_lo(x0, x1, s0, s1, ahi, alo);
-    uint32_t lo4[8], hi4[8];
+    // int4: lo4 / hi4 hold the low / high nibbles of each row word xor 8
+    // (c + 8, at bits 0-3 / 4-7 of a byte); int8: the row words themselves
+    uint32_t lo4[8 * WPR], hi4[BITS == 4 ? 8 : 1];
 #pragma unroll
-    for (int r = 0; r < 8; ++r) {
-      lo4[r] = (wv[q][r] & 0x0F0F0F0Fu) ^ 0x08080808u;
-      hi4[r] = (wv[q][r] & 0xF0F0F0F0u) ^ 0x80808080u;
+    for (int r = 0; r < 8 * WPR; ++r) {
+      if constexpr (BITS == 4) {
+        lo4[r] = (wv[q][r] & 0x0F0F0F0Fu) ^ 0x08080808u;
+        hi4[r] = (wv[q][r] & 0xF0F0F0F0u) ^ 0x80808080u;
+      } else {
+        lo4[r] = wv[q][r];
+      }
     }
     if (st + P < STEPS) issue(q, st + P);
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int t = 0; t < 8; ++t) {
-      const uint32_t p = (uint32_t)(t >> 1);
+      // int4: byte t / 2 of rows 2h and 2h + 1; int8: byte t % 4 of word t / 4
+      const uint32_t p = BITS == 4 ? (uint32_t)(t >> 1) : (uint32_t)(t & 3);
       const uint32_t sel = 0x0C000C00u | ((4u + p) << 16) | p;
       uint32_t bq[4];
 #pragma unroll
       for (int h = 0; h < 4; ++h) {
-        const uint32_t a0 = (t & 1) ? hi4[2 * h] : lo4[2 * h];
-        const uint32_t a1 = (t & 1) ? hi4[2 * h + 1] : lo4[2 * h + 1];
-        bq[h] = __builtin_amdgcn_perm(a1, a0, sel);
+        if constexpr (BITS == 4) {
+          const uint32_t a0 = (t & 1) ? hi4[2 * h] : lo4[2 * h];
+          const uint32_t a1 = (t & 1) ? hi4[2 * h + 1] : lo4[2 * h + 1];
+          bq[h] = __builtin_amdgcn_perm(a1, a0, sel);
+        } else {
+          // c ^ 0x80 = c + 128 at bits 0-7 of a half: the f16 (c + 128) * 2^-24
+          const int wd = t >> 2;
+          bq[h] = __builtin_amdgcn_perm(lo4[2 * (2 * h + 1) + wd], lo4[2 * (2 * h) + wd], sel) ^ 0x00800080u;
+        }
       }
       const f16x8 bt = __builtin_bit_cast(f16x8, u32x4v{bq[0], bq[1], bq[2], bq[3]});
       acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi, bt, acc[t], 0, 0, 0);
@@ -402,9 +427,13 @@ __global__ __launch_bounds__(DEC_THREADS, 1) void k_linear_w4_decode(
     const int sh = -sXe[(4 * g + i) * RG + rg] - se;
     float v[8];
 #pragma unroll
-    for (int t = 0; t < 8; ++t)
-      v[t] = (t & 1) ? __builtin_ldexpf(acc[t][i] - corr[i], 20 + sh)
-                     : __builtin_ldexpf(acc[t][i] - corr[i] * 0.0625f, 24 + sh);
+    for (int t = 0; t < 8; ++t) {
+      if constexpr (BITS == 8)  // (c + 128) * 2^-24, corr the sum of 128 * 2^-24 terms
+        v[t] = __builtin_ldexpf(acc[t][i] - corr[i], 24 + sh);
+      else
+        v[t] = (t & 1) ? __builtin_ldexpf(acc[t][i] - corr[i], 20 + sh)
+                       : __builtin_ldexpf(acc[t][i] - corr[i] * 0.0625f, 24 + sh);
+    }
     float* dst = rwv + (4 * g + i) * DEC_RS + 8 * j;
     *reinterpret_cast<f32x4*>(dst) = f32x4{v[0], v[1], v[2], v[3]};
     *reinterpret_cast<f32x4*>(dst + 4) = f32x4{v[4], v[5], v[6], v[7]};
@@ -1629,22 +1658,26 @@ static DecodePlan plan_decode(int64_t K, int64_t N) {
   return p;
 }
 
-template <typename T, int STEPS, int NBW>
+// int8 codes: half the prefetch depth (the same bytes and registers in flight)
+template <typename T, int STEPS, int NBW, int BITS>
 static void launch_decode_t(const DecodePlan& p, hipStream_t st, const void* x, int64_t M, int64_t K, int64_t N,
                             const uint32_t* w, const float* scales, const float* bias, float* out, float* partials,
                             unsigned long long* counters) {
   const dim3 grid((unsigned)((N / 128 / NBW) * p.S));
-  hipLaunchKernelGGL((k_linear_w4_decode<T, STEPS, NBW, 4>), grid, dim3(DEC_THREADS), 0, st, (const T*)x, (int)M, K,
-                     N, w, scales, bias, out, partials, counters, p.S, p.xcd_map);
+  hipLaunchKernelGGL((k_linear_w4_decode<T, STEPS, NBW, BITS == 8 ? 2 : 4, BITS>), grid, dim3(DEC_THREADS), 0, st,
+                     (const T*)x, (int)M, K, N, w, scales, bias, out, partials, counters, p.S, p.xcd_map);
 }
 
 template <typename T>
 static void launch_decode(const DecodePlan& p, hipStream_t st, const void* x, int64_t M, int64_t K, int64_t N,
                           const uint32_t* w, const float* scales, const float* bias, float* out, float* partials,
-                          unsigned long long* counters) {
+                          unsigned long long* counters, int bits) {
 #define MXK_DEC(STEPS, NBW)                                                                          \
   if (p.steps == STEPS && p.nbw == NBW) {                                                           \
-    launch_decode_t<T, STEPS, NBW>(p, st, x, M, K, N, w, scales, bias, out, partials, counters);    \
+    if (bits == 8)                                                                                  \
+      launch_decode_t<T, STEPS, NBW, 8>(p, st, x, M, K, N, w, scales, bias, out, partials, counters); \
+    else                                                                                            \
+      launch_decode_t<T, STEPS, NBW, 4>(p, st, x, M, K, N, w, scales, bias, out, partials, counters); \
     return;                                                                                         \
   }
   MXK_DEC(4, 2)
@@ -1713,14 +1746,15 @@ static void launch_decode_tiled(const DecodePlan& p, hipStream_t st, const void*
 
 static bool decode_eligible(int64_t M, int64_t K, int64_t N, int kind, int bits, int block, const void* x,
                             int x_type, const void* w) {
-  if (kind != MXK_KIND_INT || bits != 4 || block != 128) return false;
+  if (kind != MXK_KIND_INT || (bits != 4 && bits != 8) || block != 128) return false;
   if (M < 1 || M > 16 || K % 32 != 0 || N % 128 != 0) return false;
   if (N / 128 > DEC_COUNTER_BYTES / 8 || K / 32 >= 65536) return false;
-  if (!aligned16(x) || (reinterpret_cast<uintptr_t>(w) & 3u) != 0) return false;
+  if (!aligned16(x) || (reinterpret_cast<uintptr_t>(w) & (bits == 8 ? 7u : 3u)) != 0) return false;
   const int esz = x_type == MXK_IN_F32 ? 4 : 2;
   if ((K * esz) % 16 != 0) return false;
   // 32-bit buffer offsets with headroom
-  if (K * N / 2 >= (int64_t(1) << 31) || K * (N / 128) * 4 >= (int64_t(1) << 31) || 16 * K * esz >= (int64_t(1) << 31))
+  if (K * N * bits / 8 >= (int64_t(1) << 31) || K * (N / 128) * 4 >= (int64_t(1) << 31) ||
+      16 * K * esz >= (int64_t(1) << 31))
     return false;
   // partial buffer: S * (N/128) * 8 KiB, addressed with 32-bit offsets
   if ((K / 32 + 1) * (N / 128) * 8192 >= (int64_t(1) << 31)) return false;
@@ -1828,7 +1862,9 @@ extern "C" {
 size_t mxk_linear_workspace(int64_t M, int64_t K, int64_t N, int bits, int block) {
   // the MFMA path (any M, int4/int8 codes); its buffers start past the decode counters
   const size_t c = M > 0 && K > 0 && N > 0 ? linear_mfma_workspace(M, K, N, bits, block, false) : 0;
-  if (M < 1 || M > 16 || bits != 4 || block != 128 || K <= 0 || N <= 0 || K % 32 != 0 || N % 128 != 0) return c;
+  if (M < 1 || M > 16 || (bits != 4 && bits != 8) || block != 128 || K <= 0 || N <= 0 || K % 32 != 0 ||
+      N % 128 != 0)
+    return c;
   // enough for mxk_linear_wq's decode path and for mxk_linear_wq_tiled
   const DecodePlan p = plan_decode(K, N), q = plan_decode_tiled(K, N, 4), q2 = plan_decode_tiled(K, N, 2);
   const size_t a = p.S <= 255 ? p.counter_bytes + p.partial_bytes + p.scales_t_bytes : 0;  // else generic kernel
@@ -1935,9 +1971,10 @@ static int linear_wq_impl(const void* x, int x_type, int64_t M, int64_t K, const
       sT = tmp;
     }
     const uint32_t* wq = reinterpret_cast<const uint32_t*>(w_packed);
-    if (x_type == MXK_IN_F32) launch_decode<float>(p, st, x, M, K, N, wq, sT, bias, out, partials, counters);
-    else if (x_type == MXK_IN_F16) launch_decode<__half>(p, st, x, M, K, N, wq, sT, bias, out, partials, counters);
-    else launch_decode<hip_bfloat16>(p, st, x, M, K, N, wq, sT, bias, out, partials, counters);
+    if (x_type == MXK_IN_F32) launch_decode<float>(p, st, x, M, K, N, wq, sT, bias, out, partials, counters, bits);
+    else if (x_type == MXK_IN_F16)
+      launch_decode<__half>(p, st, x, M, K, N, wq, sT, bias, out, partials, counters, bits);
+    else launch_decode<hip_bfloat16>(p, st, x, M, K, N, wq, sT, bias, out, partials, counters, bits);
     return check_launch("linear_wq(decode)");
   }
   if (mfma) {

@@ -1,5 +1,6 @@
-"""mx_linear's int4 decode path at any input magnitude (mx_linear.forward,
-mxtorch.py:7454-7473: y = x.float() @ dequant(quantize(W.t()))).
+"""mx_linear's int4 and int8 decode paths (at most 16 rows of x) at any input
+magnitude (mx_linear.forward, mxtorch.py:7454-7473:
+y = x.float() @ dequant(quantize(W.t()))).
 
 The decode kernel feeds x*s to f16 MFMAs as a hi + lo pair; these tests
 check that its power-of-two range scaling keeps every output within 1e-3 of
@@ -48,36 +49,39 @@ def _rowwise_ok(y, y_ref):
     return bool((err <= lim).all()), (err / lim.clamp_min(1e-300)).max().item()
 
 
-def _run(qa, x, W, K, N):
+def _run(qa, x, W, K, N, dt="int4d"):
     lin = torch.nn.Linear(K, N, bias=False)
     with torch.no_grad():
         lin.weight.copy_(W)
-    m = qa.mx_linear.from_linear(lin.to(dev()), qa.get_mx_dtype("int4d"), 128)
-    wp, ws, _ = orc.linear_from_weight(W, "int4d", 128)
+    m = qa.mx_linear.from_linear(lin.to(dev()), qa.get_mx_dtype(dt), 128)
+    wp, ws, _ = orc.linear_from_weight(W, dt, 128)
     assert G.bits_equal(m._mx_weight._mx_packed.cpu(), wp)
     assert G.bits_equal(m._mx_weight._mx_scales.cpu(), ws)
     y = m(x.to(dev())).cpu()
-    y_ref = orc.linear_forward(x, wp, ws, "int4d", K, N, 128)
+    y_ref = orc.linear_forward(x, wp, ws, dt, K, N, 128)
     return y, y_ref
 
 
 MAGS = [1e-6, 1e-3, 1.0, 1e4, 1e6]
+DTS = ["int4d", "int8d"]
 
 
+@pytest.mark.parametrize("dt", DTS)
 @pytest.mark.parametrize("wmag", MAGS)
 @pytest.mark.parametrize("xmag", MAGS)
-def test_decode_magnitudes(qa, xmag, wmag):
+def test_decode_magnitudes(qa, xmag, wmag, dt):
     M, K, N = 16, 2048, 512
-    print(f"decode magnitudes x~{xmag:g} W~{wmag:g}", flush=True)
+    print(f"decode magnitudes {dt} x~{xmag:g} W~{wmag:g}", flush=True)
     W = _randn((N, K), 101, outliers=1e-3) * wmag
     x = _randn((M, K), 103) * xmag
-    y, y_ref = _run(qa, x, W, K, N)
+    y, y_ref = _run(qa, x, W, K, N, dt)
     ok, worst = _rowwise_ok(y, y_ref)
     assert ok, f"worst row error {worst:.3g} x the bar"
 
 
+@pytest.mark.parametrize("dt", DTS)
 @pytest.mark.parametrize("xdt", [torch.float32, torch.bfloat16, torch.float16])
-def test_decode_mixed_row_magnitudes(qa, xdt):
+def test_decode_mixed_row_magnitudes(qa, xdt, dt):
     """Rows from 1e-4 to 1e3 (1e-7 to 1e7 for float32 and bfloat16) in one
     call, and a row of zeros: each row within the bar of its own magnitude."""
     M, K, N = 16, 4096, 1024
@@ -88,13 +92,14 @@ def test_decode_mixed_row_magnitudes(qa, xdt):
     x[: M - 1] *= mags[:, None]
     x[M - 1] = 0.0
     x = x.to(xdt)
-    y, y_ref = _run(qa, x, W, K, N)
+    y, y_ref = _run(qa, x, W, K, N, dt)
     assert torch.equal(y[M - 1], torch.zeros(N))
     ok, worst = _rowwise_ok(y[: M - 1], y_ref[: M - 1])
     assert ok, f"worst row error {worst:.3g} x the bar"
 
 
-def test_decode_mixed_k_magnitudes(qa):
+@pytest.mark.parametrize("dt", DTS)
+def test_decode_mixed_k_magnitudes(qa, dt):
     """Magnitudes that change along K inside one row group of the kernel: x
     large where the weights are small and the other way round."""
     M, K, N = 8, 2048, 256
@@ -102,20 +107,44 @@ def test_decode_mixed_k_magnitudes(qa):
     W[:, ::2] *= 1e-5
     x = _randn((M, K), 117)
     x[:, ::2] *= 1e5
-    y, y_ref = _run(qa, x, W, K, N)
+    y, y_ref = _run(qa, x, W, K, N, dt)
     ok, worst = _rowwise_ok(y, y_ref)
     assert ok, f"worst row error {worst:.3g} x the bar"
 
 
+@pytest.mark.parametrize("dt", DTS)
 @pytest.mark.parametrize("xdt", [torch.float32, torch.bfloat16])
-def test_decode_config2_outliers(qa, xdt):
+def test_decode_config2_outliers(qa, xdt, dt):
     """The benchmark configuration at full size: x [16, 8192] (float32 and
     its bfloat16 copy), W [8192, 8192] ~ 0.02*N(0,1) with 0.1% of the
-    weights at 20x."""
+    weights at 20x (int8d: the same layer with int8 codes)."""
     M = K = N = 8192
     M = 16
     W = _randn((N, K), 3, outliers=1e-3, scale=20.0) * 0.02
     x = _randn((M, K), 2).to(xdt)
-    y, y_ref = _run(qa, x, W, K, N)
+    y, y_ref = _run(qa, x, W, K, N, dt)
     ok, worst = _rowwise_ok(y, y_ref)
     assert ok, f"worst row error {worst:.3g} x the bar"
+
+
+@pytest.mark.parametrize("M,K,N", [(1, 8192, 8192), (5, 4096, 1024), (16, 96, 128), (9, 2080, 384), (16, 16384, 256),
+                                   (3, 32, 128)])
+@pytest.mark.parametrize("xdt", [torch.float32, torch.bfloat16, torch.float16])
+def test_decode_int8_shapes(qa, M, K, N, xdt):
+    """int8 codes through the decode kernel called directly (ops.linear_wq),
+    with the scales as stored (the kernel's own transposed copy in the
+    workspace) and block-major (prepack_scales): one to sixteen rows, K a
+    multiple of 32 down to one step, single and many column blocks, one
+    split and many; both results within the bar of the oracle and equal."""
+    from qtpytorch_amd import ops
+    print(f"int8 decode M={M} K={K} N={N} {xdt}", flush=True)
+    W = _randn((N, K), 7 * K + N, outliers=1e-3) * 0.05
+    x = _randn((M, K), 11 * M + K).to(xdt)
+    wp, ws, _ = orc.linear_from_weight(W, "int8d", 128)
+    y = ops.linear_wq(x.to(dev()), wp.to(dev()), ws.to(dev()), "int8d", K, N, 128).cpu()
+    sT = ops.prepack_scales(ws.to(dev()), K, N, 128)
+    y2 = ops.linear_wq(x.to(dev()), wp.to(dev()), ws.to(dev()), "int8d", K, N, 128, w_scales_t=sT).cpu()
+    y_ref = orc.linear_forward(x, wp, ws, "int8d", K, N, 128)
+    ok, worst = _rowwise_ok(y, y_ref)
+    assert ok, f"worst row error {worst:.3g} x the bar"
+    assert torch.equal(y, y2)
