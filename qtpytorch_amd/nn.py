@@ -85,6 +85,12 @@ class mx_linear(nn.Module):
         bias = None
         if self.apply_bias and self._mx_bias is not None:
             bias = self._mx_bias.dequantize()
+        if not ops.linear_nt_eligible(w._mx_dtype):
+            # weights the kernels do not decode in registers ('h' and 'v'
+            # variants): the reference's own product, dequantize then F.linear
+            # (mxtorch.py:7470-7473), the dequantize (and its 'h' unrotation)
+            # on this library's kernels
+            return torch.nn.functional.linear(x.float(), w.dequantize().t(), bias)
         wt = self._tiled_weight(w)
         if torch.is_grad_enabled() and x.requires_grad:
             # the reference's F.linear(x, W_dq) carries the input gradient grad @ W_dq^T

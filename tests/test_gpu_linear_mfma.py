@@ -330,3 +330,31 @@ def test_mfma_every_code(qa, dt, layout):
     bad = err > lim
     assert not bad.any(), (f"{int(bad.sum())} outputs off, first at {bad.nonzero()[0].tolist()}: "
                            f"{y[bad][0].item()!r} vs {ref[bad][0].item()!r}")
+
+
+@pytest.mark.parametrize("dt", ["int4dh", "int8dh", "float4dh", "int8dv"])
+def test_mx_linear_rotated_and_vector_weights(qa, dt):
+    """'h' and 'v' weights, which no kernel decodes in registers: the
+    reference's own dequantize-then-F.linear (mxtorch.py:7470-7473).  The
+    dequantize undoes the rotation as ops.HADAMARD_DEQUANT_MODE says: the
+    rows quantize rotated (the default), or the reference's whole-tensor
+    unrotation (mxtorch.py:1582-1595)."""
+    from qtpytorch_amd import ops
+    M, K, N = 24, 512, 256
+    W = _randn((N, K), 131, outliers=1e-3) * 0.05
+    x = _randn((M, K), 137)
+    m = _module(qa, W, dt)
+    wp, ws, _ = orc.linear_from_weight(W, dt, 128)
+    assert G.bits_equal(m._mx_weight._mx_packed.cpu(), wp)
+    assert G.bits_equal(m._mx_weight._mx_scales.cpu(), ws)
+    for mode in ("rows", "reference"):
+        print(f"mx_linear {dt} unrotation {mode}", flush=True)
+        old = ops.HADAMARD_DEQUANT_MODE
+        ops.HADAMARD_DEQUANT_MODE = mode
+        try:
+            y = m(x.to(dev())).cpu()
+        finally:
+            ops.HADAMARD_DEQUANT_MODE = old
+        w_f = orc.dequant(wp, ws, dt, K * N, 128, orig_shape=(K, N), hadamard_mode=mode).reshape(K, N)
+        ok, worst = _rowwise(y, x @ w_f)
+        assert ok, f"{dt} ({mode}): worst row error {worst:.3g} x the bar"
