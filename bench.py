@@ -300,16 +300,18 @@ def bench_linear_mfma(qa, reps):
                                           "f16_mfma_TFLOPS": round(2 * flops / t / 1e12, 1),
                                           "frac_f16_peak": round(2 * flops / t / 1e12 / F16_PEAK_TFLOPS, 4)}
             del x
-        if name == "int8d":
-            # int8 codes at decode batch (16 rows): the decode kernel, HBM-bound
+        if name in ("int8d", "float4d", "float8d"):
+            # decode batch (16 rows): the decode kernel on the codes as stored, HBM-bound
             x = torch.randn(16, K, generator=gen(36, "cuda"), device=dev)
             with torch.no_grad():
                 m(x)
                 t = graph_time(lambda: m(x), reps * 5, 1, repeats=3)
-            nbytes = K * N + (K * N // 128) * 4 + 16 * K * 4 + 16 * N * 4  # codes, block scales, x, y (as config 2)
-            out["int8d_decode_16x8192x8192"] = {"us": round(t * 1e6, 2), "GBs": round(nbytes / t / 1e9, 1),
-                                                "frac_hbm": round(nbytes / t / 1e9 / HBM_PEAK_GBS, 4),
-                                                "bytes": nbytes}
+            bits = qa.get_mx_dtype(name).bits
+            # codes, block scales, x, y (as config 2)
+            nbytes = K * N * bits // 8 + (K * N // 128) * 4 + 16 * K * 4 + 16 * N * 4
+            out[f"{name}_decode_16x8192x8192"] = {"us": round(t * 1e6, 2), "GBs": round(nbytes / t / 1e9, 1),
+                                                  "frac_hbm": round(nbytes / t / 1e9 / HBM_PEAK_GBS, 4),
+                                                  "bytes": nbytes}
             del x
         del m
         torch.cuda.empty_cache()

@@ -690,4 +690,27 @@ int linear_mfma_nk_tiled(const void* x, int x_type, int64_t M, int64_t K, const 
 int requant_vec_f32(const float* x, int64_t n, int bits, int block, void* packed, int64_t packed_nbytes,
                     float* scales, int64_t n_store, void* ws, size_t ws_bytes, hipStream_t st);
 
+// ---------------------------------------------------------------- float codes as f16 B operands
+// Two float codes (indices into the sorted grid of 2^B values: B = 4 FP4
+// E2M1, B = 8 FP8 E4M3 with exponent 15 a normal binade) as the f16 pair of
+// their grid values times vmax · 2^-P (vmax 6 or 480, P = 14 or 8): the
+// format's own values v, scaled by a power of two, exact in f16 (subnormal
+// for the smallest: the MFMA takes f16 subnormals).  FP4 codes sit at bits
+// 0-3 and 16-19 of d (the bits above each code ignored), FP8 codes at bits
+// 8-15 and 24-31 (the callers' byte permutes put them there; the bits below
+// ignored).  c ^ 2^(B-1) is the B-bit one's complement of +-m, m the bit
+// pattern of |v| (the grid is symmetric and sorted); at the top of a 16-bit
+// half, xor-ed with its sign mask and shifted to f16's mantissa position, m
+// is the f16 of |v| * 2^-P.
+template <int B>
+__device__ __forceinline__ uint32_t fp_code_pair_f16(uint32_t d) {
+  typedef short s2v __attribute__((ext_vector_type(2)));
+  // code at the top of each half, its top bit flipped
+  const uint32_t x = (B == 4 ? d << 12 : d) ^ 0x80008000u;
+  const uint32_t sm = __builtin_bit_cast(uint32_t, __builtin_bit_cast(s2v, x) >> (short)15);
+  const uint32_t y = x ^ sm;
+  const uint32_t m = (y >> (B == 4 ? 3 : 1)) & (B == 4 ? 0x0E000E00u : 0x3F803F80u);
+  return (sm & 0x80008000u) | m;
+}
+
 }  // namespace mxk

@@ -158,6 +158,7 @@ __global__ __launch_bounds__(256) void k_linear_generic(const T* __restrict__ x,
 // runs on XCD b % 8), all splits of a column group are placed on one XCD;
 // the protocol does not depend on it.
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x2v __attribute__((ext_vector_type(2)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
 
@@ -208,7 +209,7 @@ struct DecGeom {
   static constexpr int CPT = 2048 / TPB;
 };
 
-template <typename T, int STEPS, int NBW, int P, int BITS = 4>
+template <typename T, int STEPS, int NBW, int P, int BITS = 4, bool FP = false>
 __global__ __launch_bounds__(DEC_THREADS, 1) void k_linear_w4_decode(
     const T* __restrict__ x, int M, int64_t K, int64_t N, const uint32_t* __restrict__ w,
     const float* __restrict__ scales_t, const float* __restrict__ bias, float* __restrict__ out,
@@ -277,9 +278,14 @@ __global__ __launch_bounds__(DEC_THREADS, 1) void k_linear_w4_decode(
   // valid by construction: a step past K (only in the last split when K is
   // not a multiple of R) re-reads rows 0..31, and its x rows and scales are
   // zeros.
-  // BITS = 8 (int8 codes): 8 bytes of a row per lane, words 2r and 2r + 1
-  // of row r; the prefetch is P steps deep as for int4 (the caller halves P)
-  static_assert(BITS == 4 || BITS == 8, "int4 or int8 codes");
+  // BITS = 8 (int8 or FP8 codes, exact f16 operands with no offset): 8
+  // bytes of a row per lane, words 2r and 2r + 1 of row r; the prefetch is
+  // P steps deep as for 4-bit codes (the caller halves P).  int4 codes go
+  // in as (c + 8) at bits 0-3 or 4-7 of an f16 half, a denormal, the offset
+  // taken back by one correction MFMA.  FP: sorted-grid float codes (FP4 E2M1, FP8 E4M3),
+  // whose B operands are the format's values v * 2^-E exactly (E = 14 or 8,
+  // no offset), and the epilogue takes 2^E * RN(1 / vmax).
+  static_assert(BITS == 4 || BITS == 8, "4- or 8-bit codes");
   constexpr int WPR = BITS / 4;  // 32-bit words of a lane's 8 columns in one row
   const __amdgpu_buffer_rsrc_t rw = make_rsrc(w, (uint32_t)(K * N * BITS / 8));
   const uint32_t row_bytes = (uint32_t)(N * BITS / 8);
@@ -377,10 +383,10 @@ __global__ __launch_bounds__(DEC_THREADS, 1) void k_linear_w4_decode(
     split_hi_lo(x0, x1, s0, s1, ahi, alo);
     // int4: lo4 / hi4 hold the low / high nibbles of each row word xor 8
     // (c + 8, at bits 0-3 / 4-7 of a byte); int8: the row words themselves
-    uint32_t lo4[8 * WPR], hi4[BITS == 4 ? 8 : 1];
+    uint32_t lo4[8 * WPR], hi4[BITS == 4 && !FP ? 8 : 1];
 #pragma unroll
     for (int r = 0; r < 8 * WPR; ++r) {
-      if constexpr (BITS == 4) {
+      if constexpr (BITS == 4 && !FP) {
         lo4[r] = (wv[q][r] & 0x0F0F0F0Fu) ^ 0x08080808u;
         hi4[r] = (wv[q][r] & 0xF0F0F0F0u) ^ 0x80808080u;
       } else {
@@ -397,22 +403,38 @@ __global__ __launch_bounds__(DEC_THREADS, 1) void k_linear_w4_decode(
       uint32_t bq[4];
 #pragma unroll
       for (int h = 0; h < 4; ++h) {
-        if constexpr (BITS == 4) {
+        if constexpr (FP && BITS == 4) {
+          // byte t / 2 of rows 2h, 2h + 1 at bytes 0 and 2; odd tiles the high nibbles
+          const uint32_t d = __builtin_amdgcn_perm(lo4[2 * h + 1], lo4[2 * h], sel);
+          bq[h] = fp_code_pair_f16<4>((t & 1) ? d >> 4 : d);
+        } else if constexpr (FP) {
+          // byte t % 4 of word t / 4 of rows 2h, 2h + 1 at bytes 1 and 3
+          const int wd = t >> 2;
+          const uint32_t selh = 0x0Cu | (p << 8) | 0x0C0000u | ((4u + p) << 24);
+          bq[h] = fp_code_pair_f16<8>(__builtin_amdgcn_perm(lo4[2 * (2 * h + 1) + wd], lo4[2 * (2 * h) + wd], selh));
+        } else if constexpr (BITS == 4) {
           const uint32_t a0 = (t & 1) ? hi4[2 * h] : lo4[2 * h];
           const uint32_t a1 = (t & 1) ? hi4[2 * h + 1] : lo4[2 * h + 1];
           bq[h] = __builtin_amdgcn_perm(a1, a0, sel);
         } else {
-          // c ^ 0x80 = c + 128 at bits 0-7 of a half: the f16 (c + 128) * 2^-24
+          // 0x6400 | (c ^ 0x80) is the f16 1024 + (c + 128): less 1152, c
+          // itself, exact (an offset taken back after the sum, as for int4,
+          // would leave each sum's rounding relative to 128 * A, not c * A)
           const int wd = t >> 2;
-          bq[h] = __builtin_amdgcn_perm(lo4[2 * (2 * h + 1) + wd], lo4[2 * (2 * h) + wd], sel) ^ 0x00800080u;
+          const uint32_t e =
+              __builtin_amdgcn_perm(lo4[2 * (2 * h + 1) + wd], lo4[2 * (2 * h) + wd], sel) ^ 0x64806480u;
+          const f16x2v r = __builtin_bit_cast(f16x2v, e) - f16x2v{(_Float16)1152.0f, (_Float16)1152.0f};
+          bq[h] = __builtin_bit_cast(uint32_t, r);
         }
       }
       const f16x8 bt = __builtin_bit_cast(f16x8, u32x4v{bq[0], bq[1], bq[2], bq[3]});
       acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi, bt, acc[t], 0, 0, 0);
       acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo, bt, acc[t], 0, 0, 0);
     }
-    corr = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi, b8, corr, 0, 0, 0);
-    corr = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo, b8, corr, 0, 0, 0);
+    if constexpr (!FP && BITS == 4) {
+      corr = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi, b8, corr, 0, 0, 0);
+      corr = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo, b8, corr, 0, 0, 0);
+    }
   }
 
   // ---- wave partial (rows 4g+i, columns 8j+t of block nb) to LDS, after
@@ -428,8 +450,10 @@ __global__ __launch_bounds__(DEC_THREADS, 1) void k_linear_w4_decode(
     float v[8];
 #pragma unroll
     for (int t = 0; t < 8; ++t) {
-      if constexpr (BITS == 8)  // (c + 128) * 2^-24, corr the sum of 128 * 2^-24 terms
-        v[t] = __builtin_ldexpf(acc[t][i] - corr[i], 24 + sh);
+      if constexpr (FP)  // v * 2^-E for the grid value RN(v / vmax)
+        v[t] = __builtin_ldexpf(acc[t][i], (BITS == 4 ? 14 : 8) + sh) * (BITS == 4 ? 1.0f / 6.0f : 1.0f / 480.0f);
+      else if constexpr (BITS == 8)  // exact codes
+        v[t] = __builtin_ldexpf(acc[t][i], sh);
       else
         v[t] = (t & 1) ? __builtin_ldexpf(acc[t][i] - corr[i], 20 + sh)
                        : __builtin_ldexpf(acc[t][i] - corr[i] * 0.0625f, 24 + sh);
@@ -1658,27 +1682,31 @@ static DecodePlan plan_decode(int64_t K, int64_t N) {
   return p;
 }
 
-// int8 codes: half the prefetch depth (the same bytes and registers in flight)
-template <typename T, int STEPS, int NBW, int BITS>
+// 8-bit codes: half the prefetch depth (the same bytes and registers in flight)
+template <typename T, int STEPS, int NBW, int BITS, bool FP>
 static void launch_decode_t(const DecodePlan& p, hipStream_t st, const void* x, int64_t M, int64_t K, int64_t N,
                             const uint32_t* w, const float* scales, const float* bias, float* out, float* partials,
                             unsigned long long* counters) {
   const dim3 grid((unsigned)((N / 128 / NBW) * p.S));
-  hipLaunchKernelGGL((k_linear_w4_decode<T, STEPS, NBW, BITS == 8 ? 2 : 4, BITS>), grid, dim3(DEC_THREADS), 0, st,
-                     (const T*)x, (int)M, K, N, w, scales, bias, out, partials, counters, p.S, p.xcd_map);
+  hipLaunchKernelGGL((k_linear_w4_decode<T, STEPS, NBW, BITS == 8 ? 2 : 4, BITS, FP>), grid, dim3(DEC_THREADS), 0,
+                     st, (const T*)x, (int)M, K, N, w, scales, bias, out, partials, counters, p.S, p.xcd_map);
 }
 
 template <typename T>
 static void launch_decode(const DecodePlan& p, hipStream_t st, const void* x, int64_t M, int64_t K, int64_t N,
                           const uint32_t* w, const float* scales, const float* bias, float* out, float* partials,
-                          unsigned long long* counters, int bits) {
-#define MXK_DEC(STEPS, NBW)                                                                          \
-  if (p.steps == STEPS && p.nbw == NBW) {                                                           \
-    if (bits == 8)                                                                                  \
-      launch_decode_t<T, STEPS, NBW, 8>(p, st, x, M, K, N, w, scales, bias, out, partials, counters); \
-    else                                                                                            \
-      launch_decode_t<T, STEPS, NBW, 4>(p, st, x, M, K, N, w, scales, bias, out, partials, counters); \
-    return;                                                                                         \
+                          unsigned long long* counters, int bits, int kind) {
+#define MXK_DEC_K(STEPS, NBW, B, F) \
+  launch_decode_t<T, STEPS, NBW, B, F>(p, st, x, M, K, N, w, scales, bias, out, partials, counters)
+#define MXK_DEC(STEPS, NBW)                                                          \
+  if (p.steps == STEPS && p.nbw == NBW) {                                           \
+    const bool fp = kind == MXK_KIND_FLOAT;                                         \
+    if (bits == 8) {                                                                \
+      if (fp) MXK_DEC_K(STEPS, NBW, 8, true); else MXK_DEC_K(STEPS, NBW, 8, false); \
+    } else {                                                                        \
+      if (fp) MXK_DEC_K(STEPS, NBW, 4, true); else MXK_DEC_K(STEPS, NBW, 4, false); \
+    }                                                                               \
+    return;                                                                         \
   }
   MXK_DEC(4, 2)
   MXK_DEC(2, 2)
@@ -1686,6 +1714,7 @@ static void launch_decode(const DecodePlan& p, hipStream_t st, const void* x, in
   MXK_DEC(2, 1)
   MXK_DEC(1, 1)
 #undef MXK_DEC
+#undef MXK_DEC_K
 }
 
 // The tiled kernel: one block per workgroup, the longest waves that still
@@ -1746,7 +1775,7 @@ static void launch_decode_tiled(const DecodePlan& p, hipStream_t st, const void*
 
 static bool decode_eligible(int64_t M, int64_t K, int64_t N, int kind, int bits, int block, const void* x,
                             int x_type, const void* w) {
-  if (kind != MXK_KIND_INT || (bits != 4 && bits != 8) || block != 128) return false;
+  if ((kind != MXK_KIND_INT && kind != MXK_KIND_FLOAT) || (bits != 4 && bits != 8) || block != 128) return false;
   if (M < 1 || M > 16 || K % 32 != 0 || N % 128 != 0) return false;
   if (N / 128 > DEC_COUNTER_BYTES / 8 || K / 32 >= 65536) return false;
   if (!aligned16(x) || (reinterpret_cast<uintptr_t>(w) & (bits == 8 ? 7u : 3u)) != 0) return false;
@@ -1971,10 +2000,11 @@ static int linear_wq_impl(const void* x, int x_type, int64_t M, int64_t K, const
       sT = tmp;
     }
     const uint32_t* wq = reinterpret_cast<const uint32_t*>(w_packed);
-    if (x_type == MXK_IN_F32) launch_decode<float>(p, st, x, M, K, N, wq, sT, bias, out, partials, counters, bits);
+    if (x_type == MXK_IN_F32)
+      launch_decode<float>(p, st, x, M, K, N, wq, sT, bias, out, partials, counters, bits, kind);
     else if (x_type == MXK_IN_F16)
-      launch_decode<__half>(p, st, x, M, K, N, wq, sT, bias, out, partials, counters, bits);
-    else launch_decode<hip_bfloat16>(p, st, x, M, K, N, wq, sT, bias, out, partials, counters, bits);
+      launch_decode<__half>(p, st, x, M, K, N, wq, sT, bias, out, partials, counters, bits, kind);
+    else launch_decode<hip_bfloat16>(p, st, x, M, K, N, wq, sT, bias, out, partials, counters, bits, kind);
     return check_launch("linear_wq(decode)");
   }
   if (mfma) {

@@ -97,28 +97,6 @@ __device__ __forceinline__ uint32_t lm_i2pair(uint32_t d) {
   const h2v r = __builtin_bit_cast(h2v, e) - h2v{(_Float16)1026.0f, (_Float16)1026.0f};
   return __builtin_bit_cast(uint32_t, r);
 }
-// Two float codes (indices into the sorted grid of 2^B values: B = 4 FP4
-// E2M1, B = 8 FP8 E4M3 with exponent 15 a normal binade) as the f16 pair of
-// their grid values times vmax · 2^-P (vmax 6 or 480, P = 14 or 8): the
-// format's own values v, scaled by a power of two, exact in f16 (subnormal
-// for the smallest: the MFMA takes f16 subnormals).  FP4 codes sit at bits
-// 0-3 and 16-19 of d (the bits above each code ignored), FP8 codes at bits
-// 8-15 and 24-31 (the callers' byte permutes put them there; the bits below
-// ignored).  c ^ 2^(B-1) is the B-bit one's complement of +-m, m the bit
-// pattern of |v| (the grid is symmetric and sorted); at the top of a 16-bit
-// half, xor-ed with its sign mask and shifted to f16's mantissa position, m
-// is the f16 of |v| * 2^-P.
-template <int B>
-__device__ __forceinline__ uint32_t lm_fpair(uint32_t d) {
-  typedef short s2v __attribute__((ext_vector_type(2)));
-  // code at the top of each half, its top bit flipped
-  const uint32_t x = (B == 4 ? d << 12 : d) ^ 0x80008000u;
-  const uint32_t sm = __builtin_bit_cast(uint32_t, __builtin_bit_cast(s2v, x) >> (short)15);
-  const uint32_t y = x ^ sm;
-  const uint32_t m = (y >> (B == 4 ? 3 : 1)) & (B == 4 ? 0x0E000E00u : 0x3F803F80u);
-  return (sm & 0x80008000u) | m;
-}
-
 // Weight formats: the code width in the low 4 bits, 16 for float grids
 enum : int { LM_I2 = 2, LM_I4 = 4, LM_I8 = 8, LM_F4 = 16 + 4, LM_F8 = 16 + 8 };
 __host__ __device__ constexpr int lm_bits(int fmt) { return fmt & 15; }
@@ -139,7 +117,7 @@ __device__ __forceinline__ uint32_t lm_pair(uint32_t d) {
   if constexpr (FMT == LM_I4) return lm_i4pair(d);
   else if constexpr (FMT == LM_I8) return lm_i8pair(d);
   else if constexpr (FMT == LM_I2) return lm_i2pair(d);
-  else return lm_fpair<lm_bits(FMT)>(d);
+  else return fp_code_pair_f16<lm_bits(FMT)>(d);
 }
 
 // v_perm_b32 selector: byte a of s1 into byte 0, byte b of s0 into byte 2, zeros in bytes 1 and 3

@@ -1,5 +1,5 @@
-"""mx_linear's int4 and int8 decode paths (at most 16 rows of x) at any input
-magnitude (mx_linear.forward, mxtorch.py:7454-7473:
+"""mx_linear's decode paths (at most 16 rows of x; int4, int8, FP4 and FP8
+codes) at any input magnitude (mx_linear.forward, mxtorch.py:7454-7473:
 y = x.float() @ dequant(quantize(W.t()))).
 
 The decode kernel feeds x*s to f16 MFMAs as a hi + lo pair; these tests
@@ -63,7 +63,7 @@ def _run(qa, x, W, K, N, dt="int4d"):
 
 
 MAGS = [1e-6, 1e-3, 1.0, 1e4, 1e6]
-DTS = ["int4d", "int8d"]
+DTS = ["int4d", "int8d", "float4d", "float8d"]
 
 
 @pytest.mark.parametrize("dt", DTS)
@@ -148,3 +148,37 @@ def test_decode_int8_shapes(qa, M, K, N, xdt):
     ok, worst = _rowwise_ok(y, y_ref)
     assert ok, f"worst row error {worst:.3g} x the bar"
     assert torch.equal(y, y2)
+
+
+@pytest.mark.parametrize("dt", ["int4d", "int8d", "float4d", "float8d"])
+def test_decode_every_code(qa, dt):
+    """Every code of the format in every column and k position through the
+    decode kernel: x is 16 rows of the identity at a time, so each output is
+    one dequantized weight.  Codes (k + 3 n) mod 2^bits, scales 2^-6 .. 2^6
+    around a power of two from 2^-20 to 2^20 that changes between column
+    blocks.  Each output may differ from the oracle's RN(grid[c] * s) only
+    by the hi + lo split of s (2^-22) and, for the float grids, the factor
+    RN(1/6) or RN(1/480)."""
+    from qtpytorch_amd import ops
+    bits = {"int4d": 4, "int8d": 8, "float4d": 4, "float8d": 8}[dt]
+    K, N = 384, 256
+    k = torch.arange(K)[:, None]
+    n = torch.arange(N)[None, :]
+    codes = (k + 3 * n) % (1 << bits)
+    if dt.startswith("int"):
+        codes = codes - (1 << (bits - 1))
+    g = torch.Generator()
+    g.manual_seed(bits + 1)
+    nsc = K * N // 128
+    off = torch.tensor([-20.0, 20.0])
+    scales = torch.exp2(torch.empty(nsc).uniform_(-6, 6, generator=g) + off[torch.arange(nsc) % (N // 128)])
+    packed = orc.pack(codes.reshape(-1), bits)
+    ref = orc.dequant(packed, scales, dt, K * N, 128).reshape(K, N)
+    pk, sc = packed.to(dev()), scales.to(dev())
+    eye = torch.eye(K)
+    for r0 in range(0, K, 16):
+        y = ops.linear_wq(eye[r0:r0 + 16].to(dev()), pk, sc, dt, K, N, 128).cpu()
+        want = ref[r0:r0 + 16]
+        bad = (y - want).abs() > 2.0 ** -20 * want.abs()
+        assert not bad.any(), (f"{dt} rows {r0}..{r0 + 15}: {int(bad.sum())} outputs off, first "
+                               f"{y[bad][0].item()!r} vs {want[bad][0].item()!r}")
