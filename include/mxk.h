@@ -36,7 +36,7 @@
 extern "C" {
 #endif
 
-#define MXK_ABI_VERSION 9
+#define MXK_ABI_VERSION 10
 
 typedef enum {
   MXK_OK = 0,
@@ -231,7 +231,8 @@ int mxk_linear_prepack_weight(const void* w_packed, int64_t K, int64_t N, int bi
 int mxk_linear_unpack_weight(const void* w_tiled, int64_t K, int64_t N, int bits, int block, void* w_packed,
                              void* stream);
 
-/* mx_linear.forward (mxtorch.py:7454-7473) for int4 weights, block 128, from
+/* mx_linear.forward (mxtorch.py:7454-7473) for 4-bit weights (kind
+ * MXK_KIND_INT: int4 codes, MXK_KIND_FLOAT: FP4 E2M1 codes), block 128, from
  * the prepacked copies: out[M,N] = x[M,K] @ dequant(W) (+ bias), the product
  * of mxk_linear_wq, float32 accumulation in another order.  w_tiled =
  * mxk_linear_prepack_weight(), w_scales_t = mxk_linear_prepack_scales().
@@ -242,8 +243,8 @@ int mxk_linear_unpack_weight(const void* w_tiled, int64_t K, int64_t N, int bits
  * (mxk_linear_workspace() bytes, zero-filled before first use, left ready
  * for the next call; calls sharing it must not overlap). */
 int mxk_linear_wq_tiled(const void* x, int x_type, int64_t M, int64_t K, const void* w_tiled,
-                        const float* w_scales_t, int64_t N, const float* bias, float* out, void* workspace,
-                        size_t workspace_nbytes, void* stream);
+                        const float* w_scales_t, int64_t N, int kind, const float* bias, float* out,
+                        void* workspace, size_t workspace_nbytes, void* stream);
 
 /* One step of kv_cache_quantizer.append_kv (mxtorch.py:3039-3067) written
  * into a caller-owned ring slot (the reference appends a new mx_tensor to a

@@ -21,7 +21,7 @@ MXK_IN_F32, MXK_IN_F16, MXK_IN_BF16 = 0, 1, 2
 MXK_KIND_INT, MXK_KIND_FLOAT = 0, 1
 MXK_VAR_BASE, MXK_VAR_HADAMARD, MXK_VAR_VECTOR = 0, 1, 2
 MXK_DYN_PER_TOKEN, MXK_DYN_PER_CHANNEL, MXK_DYN_PER_TENSOR = 0, 1, 2
-ABI_VERSION = 9
+ABI_VERSION = 10
 
 _lock = threading.Lock()
 _lib = None
@@ -55,7 +55,8 @@ SIGNATURES = {
                                       c_vp, c_vp]),
     "mxk_linear_prepack_weight": (c_int, [c_vp, c_i64, c_i64, c_int, c_int, c_vp, c_vp]),
     "mxk_linear_unpack_weight": (c_int, [c_vp, c_i64, c_i64, c_int, c_int, c_vp, c_vp]),
-    "mxk_linear_wq_tiled": (c_int, [c_vp, c_int, c_i64, c_i64, c_vp, c_vp, c_i64, c_vp, c_vp, c_vp, c_sz, c_vp]),
+    "mxk_linear_wq_tiled": (c_int, [c_vp, c_int, c_i64, c_i64, c_vp, c_vp, c_i64, c_int, c_vp, c_vp, c_vp, c_sz,
+                                    c_vp]),
     "mxk_kv_append": (c_int, [c_vp, c_vp, c_int, c_i64, c_int, c_int, c_int, c_int, c_int, c_vp, c_vp, c_vp, c_vp,
                               c_vp, c_vp]),
     "mxk_kv_gather": (c_int, [c_vp, c_vp, c_vp, c_i64, c_int, c_int, c_int, c_int, c_i64, c_i64, c_i64, c_vp,

@@ -675,8 +675,8 @@ int linear_mfma_kn(const void* x, int x_type, int64_t M, int64_t K, const void* 
                    void* workspace, size_t workspace_nbytes, hipStream_t st);
 // [K][N] int4 weight in the tiled layout of mxk_linear_prepack_weight (K % 32 == 0)
 int linear_mfma_kn_tiled(const void* x, int x_type, int64_t M, int64_t K, const void* w_tiled,
-                         const float* w_scales_t, int64_t N, const float* bias, float* out, void* workspace,
-                         size_t workspace_nbytes, hipStream_t st);
+                         const float* w_scales_t, int64_t N, int kind, const float* bias, float* out,
+                         void* workspace, size_t workspace_nbytes, hipStream_t st);
 int linear_mfma_nk(const void* x, int x_type, int64_t M, int64_t K, const void* w_packed, const float* w_scales,
                    const float* w_scales_t, int64_t N, int kind, int bits, int block, const float* bias, float* out,
                    void* workspace, size_t workspace_nbytes, hipStream_t st);

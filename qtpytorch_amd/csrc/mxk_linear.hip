@@ -582,7 +582,9 @@ __global__ __launch_bounds__(DEC_THREADS, 1) void k_linear_w4_decode(
 // [1, 2), and only then requests its weights, so that x is not queued behind
 // the weight stream.  The partial reduction and the split-K hand-off are
 // those of k_linear_w4_decode.
-template <typename T, int STEPS, int W>
+// FP: FP4 E2M1 sorted-grid codes instead of int4 (B operands v * 2^-14,
+// exact, no offset; the epilogue takes 2^14 * RN(1/6))
+template <typename T, int STEPS, int W, bool FP = false>
 __global__ __launch_bounds__(W * 64, 1) void k_linear_w4_decode_tiled(
     const T* __restrict__ x, int M, int64_t K, int64_t N, const uint32_t* __restrict__ wt,
     const float* __restrict__ scales_t, const float* __restrict__ bias, float* __restrict__ out,
@@ -737,16 +739,25 @@ __global__ __launch_bounds__(W * 64, 1) void k_linear_w4_decode_tiled(
       // tile t: column 8j + t; even tiles the low nibbles (code * 2^-24),
       // odd tiles the high nibbles (code * 2^-20)
       const int p = t >> 1;
-      const uint32_t msk = (t & 1) ? 0x00F000F0u : 0x000F000Fu;
-      const uint32_t off8 = (t & 1) ? 0x00800080u : 0x00080008u;
-      const u32x4v bq = {(wr[2 * p] & msk) ^ off8, (w8[2 * p] & msk) ^ off8, (wr[2 * p + 1] & msk) ^ off8,
-                         (w8[2 * p + 1] & msk) ^ off8};
+      u32x4v bq;
+      if constexpr (FP) {
+        const int sh = 4 * (t & 1);
+        bq = u32x4v{fp_code_pair_f16<4>(wr[2 * p] >> sh), fp_code_pair_f16<4>(w8[2 * p] >> sh),
+                    fp_code_pair_f16<4>(wr[2 * p + 1] >> sh), fp_code_pair_f16<4>(w8[2 * p + 1] >> sh)};
+      } else {
+        const uint32_t msk = (t & 1) ? 0x00F000F0u : 0x000F000Fu;
+        const uint32_t off8 = (t & 1) ? 0x00800080u : 0x00080008u;
+        bq = u32x4v{(wr[2 * p] & msk) ^ off8, (w8[2 * p] & msk) ^ off8, (wr[2 * p + 1] & msk) ^ off8,
+                    (w8[2 * p + 1] & msk) ^ off8};
+      }
       const f16x8 bt = __builtin_bit_cast(f16x8, bq);
       acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi, bt, acc[t], 0, 0, 0);
       acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo, bt, acc[t], 0, 0, 0);
     }
-    corr = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi, b8, corr, 0, 0, 0);
-    corr = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo, b8, corr, 0, 0, 0);
+    if constexpr (!FP) {
+      corr = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi, b8, corr, 0, 0, 0);
+      corr = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo, b8, corr, 0, 0, 0);
+    }
   }
 
   // ---- wave partial (rows 4g+i, columns 8j+t) into its own slot: no
@@ -757,9 +768,13 @@ __global__ __launch_bounds__(W * 64, 1) void k_linear_w4_decode_tiled(
     const int sh = -sXe[wave * 16 + 4 * g + i] - se;
     float v[8];
 #pragma unroll
-    for (int t = 0; t < 8; ++t)
-      v[t] = (t & 1) ? __builtin_ldexpf(acc[t][i] - corr[i], 20 + sh)
-                     : __builtin_ldexpf(acc[t][i] - corr[i] * 0.0625f, 24 + sh);
+    for (int t = 0; t < 8; ++t) {
+      if constexpr (FP)
+        v[t] = __builtin_ldexpf(acc[t][i], 14 + sh) * (1.0f / 6.0f);
+      else
+        v[t] = (t & 1) ? __builtin_ldexpf(acc[t][i] - corr[i], 20 + sh)
+                       : __builtin_ldexpf(acc[t][i] - corr[i] * 0.0625f, 24 + sh);
+    }
     float* dst = rwv + (4 * g + i) * XS + 8 * j;
     *reinterpret_cast<f32x4*>(dst) = f32x4{v[0], v[1], v[2], v[3]};
     *reinterpret_cast<f32x4*>(dst + 4) = f32x4{v[4], v[5], v[6], v[7]};
@@ -1758,13 +1773,17 @@ static DecodePlan plan_decode_tiled(int64_t K, int64_t N, int esz) {
 template <typename T>
 static void launch_decode_tiled(const DecodePlan& p, hipStream_t st, const void* x, int64_t M, int64_t K, int64_t N,
                                 const uint32_t* wt, const float* scales_t, const float* bias, float* out,
-                                float* partials, unsigned long long* counters) {
+                                float* partials, unsigned long long* counters, bool fp) {
   const dim3 grid((unsigned)((N / 128) * p.S));
-#define MXK_DECT(STEPS, W)                                                                                  \
-  if (p.steps == STEPS) {                                                                                  \
-    hipLaunchKernelGGL((k_linear_w4_decode_tiled<T, STEPS, W>), grid, dim3(W * 64), 0, st, (const T*)x,    \
-                       (int)M, K, N, wt, scales_t, bias, out, partials, counters, p.S, p.xcd_map);         \
-    return;                                                                                                \
+#define MXK_DECT(STEPS, W)                                                                                   \
+  if (p.steps == STEPS) {                                                                                   \
+    if (fp)                                                                                                 \
+      hipLaunchKernelGGL((k_linear_w4_decode_tiled<T, STEPS, W, true>), grid, dim3(W * 64), 0, st,          \
+                         (const T*)x, (int)M, K, N, wt, scales_t, bias, out, partials, counters, p.S, p.xcd_map); \
+    else                                                                                                    \
+      hipLaunchKernelGGL((k_linear_w4_decode_tiled<T, STEPS, W, false>), grid, dim3(W * 64), 0, st,         \
+                         (const T*)x, (int)M, K, N, wt, scales_t, bias, out, partials, counters, p.S, p.xcd_map); \
+    return;                                                                                                 \
   }
   MXK_DECT(8, 8)
   MXK_DECT(4, 8)
@@ -1933,11 +1952,14 @@ int mxk_linear_unpack_weight(const void* w_tiled, int64_t K, int64_t N, int bits
 }
 
 int mxk_linear_wq_tiled(const void* x, int x_type, int64_t M, int64_t K, const void* w_tiled, const float* w_scales_t,
-                        int64_t N, const float* bias, float* out, void* workspace, size_t workspace_nbytes,
+                        int64_t N, int kind, const float* bias, float* out, void* workspace, size_t workspace_nbytes,
                         void* stream) {
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   if (M <= 0 || K <= 0 || N <= 0) return fail(MXK_EINVAL, "linear_wq_tiled: sizes must be positive");
   if (!x || !w_tiled || !w_scales_t || !out) return fail(MXK_EINVAL, "linear_wq_tiled: null pointer");
+  if (kind != MXK_KIND_INT && kind != MXK_KIND_FLOAT)
+    return fail(MXK_EINVAL, "linear_wq_tiled: kind must be int (int4 codes) or float (FP4 codes)");
+  const bool fp = kind == MXK_KIND_FLOAT;
   if (x_type != MXK_IN_F32 && x_type != MXK_IN_F16 && x_type != MXK_IN_BF16)
     return fail(MXK_EINVAL, "linear_wq_tiled: bad input type");
   if ((bias && !aligned16(bias)) || !aligned16(out))
@@ -1945,7 +1967,7 @@ int mxk_linear_wq_tiled(const void* x, int x_type, int64_t M, int64_t K, const v
   if (!decode_tiled_eligible(M, K, N, x, x_type, w_tiled, w_scales_t)) {
     // more than 16 rows (or x not on 16 bytes): the MFMA path reads the tiled copy too
     if (K % 32 == 0 && aligned16(w_tiled) && aligned16(w_scales_t)) {
-      const int rc = linear_mfma_kn_tiled(x, x_type, M, K, w_tiled, w_scales_t, N, bias, out, workspace,
+      const int rc = linear_mfma_kn_tiled(x, x_type, M, K, w_tiled, w_scales_t, N, kind, bias, out, workspace,
                                           workspace_nbytes, st);
       if (rc != MXK_EUNSUPPORTED) return rc;
     }
@@ -1960,9 +1982,11 @@ int mxk_linear_wq_tiled(const void* x, int x_type, int64_t M, int64_t K, const v
   unsigned long long* counters = p.S > 1 ? reinterpret_cast<unsigned long long*>(ws) : nullptr;
   float* partials = p.S > 1 ? reinterpret_cast<float*>(ws + p.counter_bytes) : nullptr;
   const uint32_t* wt = reinterpret_cast<const uint32_t*>(w_tiled);
-  if (x_type == MXK_IN_F32) launch_decode_tiled<float>(p, st, x, M, K, N, wt, w_scales_t, bias, out, partials, counters);
-  else if (x_type == MXK_IN_F16) launch_decode_tiled<__half>(p, st, x, M, K, N, wt, w_scales_t, bias, out, partials, counters);
-  else launch_decode_tiled<hip_bfloat16>(p, st, x, M, K, N, wt, w_scales_t, bias, out, partials, counters);
+  if (x_type == MXK_IN_F32)
+    launch_decode_tiled<float>(p, st, x, M, K, N, wt, w_scales_t, bias, out, partials, counters, fp);
+  else if (x_type == MXK_IN_F16)
+    launch_decode_tiled<__half>(p, st, x, M, K, N, wt, w_scales_t, bias, out, partials, counters, fp);
+  else launch_decode_tiled<hip_bfloat16>(p, st, x, M, K, N, wt, w_scales_t, bias, out, partials, counters, fp);
   return check_launch("linear_wq_tiled");
 }
 

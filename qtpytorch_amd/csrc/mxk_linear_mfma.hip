@@ -240,19 +240,21 @@ __device__ __forceinline__ void kn_load_tiled(KnTiled& c, __amdgpu_buffer_rsrc_t
   c.w[1] = buf_load_b128(rw, off + 1024u, 0u);
 }
 
+template <int FMT>
 __device__ __forceinline__ u4v kn_frag_tiled(const KnTiled& c, int t) {
   const uint32_t o[8] = {c.w[0][0], c.w[0][1], c.w[0][2], c.w[0][3], c.w[1][0], c.w[1][1], c.w[1][2], c.w[1][3]};
   const int p = t >> 1;
   u4v f;
 #pragma unroll
-  for (int q = 0; q < 4; ++q) f[q] = lm_i4pair(o[2 * p + (q >> 1)] >> (8 * (q & 1) + 4 * (t & 1)));
+  for (int q = 0; q < 4; ++q) f[q] = lm_pair<FMT>(o[2 * p + (q >> 1)] >> (8 * (q & 1) + 4 * (t & 1)));
   return f;
 }
 
+template <int FMT>
 __device__ __forceinline__ void kn_store_tiled(const KnTiled& c, uint8_t* sB, int tid) {
   const int ks = tid >> 6, lane = tid & 63;
 #pragma unroll
-  for (int t = 0; t < 8; ++t) *reinterpret_cast<u4v*>(sB + lm_frag_off(ks, t, lane)) = kn_frag_tiled(c, t);
+  for (int t = 0; t < 8; ++t) *reinterpret_cast<u4v*>(sB + lm_frag_off(ks, t, lane)) = kn_frag_tiled<FMT>(c, t);
 }
 
 // ---------------------------------------------------------------- [N][K] stage decode
@@ -427,7 +429,7 @@ __global__ __launch_bounds__(LM_THREADS, 1) void k_linear_mfma(
     float* __restrict__ part) {
   constexpr int BITS = lm_bits(FMT), WK = 8 / WM, KPW = 8 / WK;
   using A = typename std::conditional<NK, NkA, KnA>::type;
-  static_assert(!TILED || FMT == LM_I4, "the tiled copies hold int4 weights");
+  static_assert(!TILED || FMT == LM_I4 || (FMT == LM_F4 && !NK), "the tiled copies hold int4 (or [K][N] FP4) codes");
   using Codes = typename std::conditional<NK, NkCodes<BITS>,
                                           typename std::conditional<TILED, KnTiled, KnCodes<BITS>>::type>::type;
   __shared__ __attribute__((aligned(1024))) uint8_t sB[2 * LM_STAGE_BYTES];
@@ -493,7 +495,7 @@ __global__ __launch_bounds__(LM_THREADS, 1) void k_linear_mfma(
   auto store_codes = [&](const Codes& c, uint8_t* dst) {
     if constexpr (NK && TILED) nk_store_tiled(c, dst, tid);
     else if constexpr (NK) nk_store<FMT>(c, dst, tid);
-    else if constexpr (TILED) kn_store_tiled(c, dst, tid);
+    else if constexpr (TILED) kn_store_tiled<FMT>(c, dst, tid);
     else kn_store<FMT>(c, dst, tid);
   };
 
@@ -606,7 +608,7 @@ __global__ __launch_bounds__(LM_THREADS, 1) void k_linear_mfma(
         h8v bt[8];
 #pragma unroll
         for (int t = 0; t < 8; ++t) {
-          if constexpr (TILED) bt[t] = __builtin_bit_cast(h8v, kn_frag_tiled(cq[i], t));
+          if constexpr (TILED) bt[t] = __builtin_bit_cast(h8v, kn_frag_tiled<FMT>(cq[i], t));
           else bt[t] = __builtin_bit_cast(h8v, kn_frag<FMT>(cq[i], t));
         }
         load_codes(cq[i], st + DS, st + DS < st1);
@@ -1060,9 +1062,9 @@ int linear_mfma_kn(const void* x, int x_type, int64_t M, int64_t K, const void* 
 
 // [K][N] int4 weight in the tiled layout (block-major scales required)
 int linear_mfma_kn_tiled(const void* x, int x_type, int64_t M, int64_t K, const void* w_tiled,
-                         const float* w_scales_t, int64_t N, const float* bias, float* out, void* workspace,
-                         size_t workspace_nbytes, hipStream_t st) {
-  if (!lm_common_ok(M, K, N, MXK_KIND_INT, 4, 128, x_type, out) || K % 32 != 0) return MXK_EUNSUPPORTED;
+                         const float* w_scales_t, int64_t N, int kind, const float* bias, float* out,
+                         void* workspace, size_t workspace_nbytes, hipStream_t st) {
+  if (!lm_common_ok(M, K, N, kind, 4, 128, x_type, out) || K % 32 != 0) return MXK_EUNSUPPORTED;
   if (!aligned16(w_tiled) || !w_scales_t) return MXK_EUNSUPPORTED;
   const LmPlan p = lm_plan(M, K, N, false, 4);
   if (!workspace || workspace_nbytes < p.bytes)
@@ -1073,11 +1075,15 @@ int linear_mfma_kn_tiled(const void* x, int x_type, int64_t M, int64_t K, const 
   float* xs = reinterpret_cast<float*>(ws + p.off_x);
   float* part = reinterpret_cast<float*>(ws + p.off_p);
   lm_prep_rows<false>(x, x_type, M, K, p.Kp, xs, nullptr, nullptr, ex, w_scales_t, N / 128, es, st);
-  lm_launch_w<LM_I4, false, true>(p, st, xs, nullptr, nullptr, w_scales_t, 1, ex, es,
-                                  reinterpret_cast<const uint8_t*>(w_tiled), M, K, N, bias, out, part);
+  const uint8_t* wt = reinterpret_cast<const uint8_t*>(w_tiled);
+  const int fmt = lm_format(kind, 4);
+  if (fmt == LM_F4)
+    lm_launch_w<LM_F4, false, true>(p, st, xs, nullptr, nullptr, w_scales_t, 1, ex, es, wt, M, K, N, bias, out, part);
+  else
+    lm_launch_w<LM_I4, false, true>(p, st, xs, nullptr, nullptr, w_scales_t, 1, ex, es, wt, M, K, N, bias, out, part);
   if (p.S > 1)
     hipLaunchKernelGGL(k_linear_mfma_reduce, dim3((unsigned)ceil_div(M * N / 4, 256)), dim3(256), 0, st, part, p.S,
-                       M, N, ex, es, bias, 1.0f, out);
+                       M, N, ex, es, bias, lm_post(fmt), out);
   return check_launch("linear_wq_tiled(mfma)");
 }
 

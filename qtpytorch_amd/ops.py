@@ -335,10 +335,11 @@ def qscale_gemm(a_packed: Tensor, a_scales: Tensor, b_packed: Tensor, b_scales: 
 
 
 def decode_prepack_eligible(dt, block: int, in_features: int, out_features: int) -> bool:
-    """Whether the int4 decode kernel can use block-major scales for this
-    weight (int4 base codes, block 128, whole 128-column blocks)."""
+    """Whether the tiled decode and MFMA kernels take this weight as its
+    tiled copy (4-bit base codes: int4 or FP4; block 128, whole 128-column
+    blocks)."""
     dt = get_mx_dtype(dt)
-    return (not dt.is_float and dt.bits == 4 and not dt.is_hadamard and not dt.is_vector and block == 128
+    return (dt.bits == 4 and not dt.is_hadamard and not dt.is_vector and block == 128
             and out_features % 128 == 0 and in_features % 32 == 0)
 
 
@@ -453,7 +454,7 @@ def linear_wq(x: Tensor, w_packed: Optional[Tensor], w_scales: Tensor, dt, in_fe
         rc = L.MXK_EUNSUPPORTED
         if w_tiled is not None and w_scales_t is not None and decode_prepack_eligible(dt, block, K, N):
             rc = lib.mxk_linear_wq_tiled(xc.data_ptr(), L.elem_type(xc.dtype), M, K, w_tiled.data_ptr(),
-                                         w_scales_t.data_ptr(), N, L.ptr(b), out.data_ptr(), L.ptr(ws), ws_bytes,
+                                         w_scales_t.data_ptr(), N, kind, L.ptr(b), out.data_ptr(), L.ptr(ws), ws_bytes,
                                          stream)
         if rc == L.MXK_EUNSUPPORTED:
             wp = w_packed.contiguous() if w_packed is not None else unpack_weight(w_tiled, K, N, block)

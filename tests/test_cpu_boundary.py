@@ -101,14 +101,16 @@ def test_bad_arguments_return_errors_without_gpu():
     assert rc == -22
     rc = h.mxk_linear_prepack_weight(16, 256, 256, 4, 128, 8, None)    # w_tiled not 16-byte aligned
     assert rc == -22
-    rc = h.mxk_linear_wq_tiled(16, 0, 16, 256, None, 16, 256, None, 16, None, 0, None)
+    rc = h.mxk_linear_wq_tiled(16, 0, 16, 256, None, 16, 256, 0, None, 16, None, 0, None)
     assert rc == -22 and b"null" in h.mxk_last_error()
-    rc = h.mxk_linear_wq_tiled(16, 7, 16, 256, 16, 16, 256, None, 16, None, 0, None)   # bad x type
+    rc = h.mxk_linear_wq_tiled(16, 7, 16, 256, 16, 16, 256, 0, None, 16, None, 0, None)   # bad x type
     assert rc == -22
+    rc = h.mxk_linear_wq_tiled(16, 0, 16, 256, 16, 16, 256, 5, None, 16, None, 0, None)   # bad kind
+    assert rc == -22 and b"kind" in h.mxk_last_error()
     # M > 16 runs the MFMA path on the tiled copy, which needs its workspace
-    rc = h.mxk_linear_wq_tiled(16, 0, 17, 256, 16, 16, 256, None, 16, None, 0, None)
+    rc = h.mxk_linear_wq_tiled(16, 0, 17, 256, 16, 16, 256, 0, None, 16, None, 0, None)
     assert rc == -22 and b"workspace" in h.mxk_last_error()
-    rc = h.mxk_linear_wq_tiled(16, 0, 16, 256, 16, 16, 200, None, 16, None, 0, None)   # N % 128
+    rc = h.mxk_linear_wq_tiled(16, 0, 16, 256, 16, 16, 200, 0, None, 16, None, 0, None)   # N % 128
     assert rc == -95
     rc = h.mxk_linear_prepack_weight_nt(None, 256, 256, 4, 128, 16, None)
     assert rc == -22 and b"null" in h.mxk_last_error()

@@ -56,9 +56,9 @@ def _rowwise_ok(y, y_ref):
     return bool((err <= lim).all()), (err / lim.clamp_min(1e-300)).max().item()
 
 
-def _weights(qa, K, N, seed):
+def _weights(qa, K, N, seed, name="int4d"):
     W = _randn((N, K), seed, outliers=1e-3) * 0.02
-    wp, ws, _ = orc.linear_from_weight(W, "int4d", 128)
+    wp, ws, _ = orc.linear_from_weight(W, name, 128)
     wpg, wsg = wp.to(dev()), ws.to(dev())
     return wp, ws, wpg, wsg, qa.ops.prepack_scales(wsg, K, N, 128), qa.ops.prepack_weight(wpg, K, N, 128)
 
@@ -93,19 +93,25 @@ CASES = [
     (16, 2048, 256, torch.bfloat16, False),    # one split of 16 x 128 rows
     (9, 96, 128, torch.float32, True),         # short waves, one split
     (16, 12288, 640, torch.float32, False),
+    (40, 2048, 512, torch.float32, True),      # more than 16 rows: the MFMA kernel on the tiled copy
+    (300, 1024, 256, torch.bfloat16, False),
 ]
 
 
+@pytest.mark.parametrize("name", ["int4d", "float4d"])
 @pytest.mark.parametrize("M,K,N,xdt,use_bias", CASES)
-def test_tiled_linear_vs_oracle(qa, M, K, N, xdt, use_bias):
-    print(f"tiled decode M={M} K={K} N={N} {xdt} bias={use_bias}", flush=True)
-    dt = qa.get_mx_dtype("int4d")
-    wp, ws, wpg, wsg, st, wt = _weights(qa, K, N, 31 + K % 97)
+def test_tiled_linear_vs_oracle(qa, M, K, N, xdt, use_bias, name):
+    """int4 and FP4 codes (the same tiled layout) through the tiled decode
+    kernel (at most 16 rows) and the MFMA kernel on the tiled copy (more),
+    and the same product from the packed codes."""
+    print(f"tiled {name} M={M} K={K} N={N} {xdt} bias={use_bias}", flush=True)
+    dt = qa.get_mx_dtype(name)
+    wp, ws, wpg, wsg, st, wt = _weights(qa, K, N, 31 + K % 97, name)
     x = _randn((M, K), 37 + M).to(xdt)
     bias = _randn((N,), 41) if use_bias else None
     y = qa.ops.linear_wq(x.to(dev()), wpg, wsg, dt, K, N, 128, bias=None if bias is None else bias.to(dev()),
                          w_scales_t=st, w_tiled=wt).cpu()
-    y_ref = orc.linear_forward(x, wp, ws, "int4d", K, N, 128)
+    y_ref = orc.linear_forward(x, wp, ws, name, K, N, 128)
     if bias is not None:
         y_ref = y_ref + bias
     ok, worst = _rowwise_ok(y, y_ref)
@@ -210,3 +216,31 @@ def test_tiled_fallback_for_other_shapes(qa):
         y = qa.ops.linear_wq(x, wpg, wsg, dt, K, N, 128, w_scales_t=st, w_tiled=wt).cpu()
         y_ref = orc.linear_forward(x.cpu(), wp, ws, "int4d", K, N, 128)
         assert _rowwise_ok(y, y_ref)[0]
+
+
+def test_mx_linear_float4d_tiled(qa):
+    """An FP4 (float4d) mx_linear weight is held as its tiled copy like int4:
+    forwards at 4 and 40 rows, the input gradient (from the packed codes
+    rebuilt on demand) against float64, and dequantize bit for bit."""
+    K, N = 1024, 256
+    W = _randn((N, K), 71) * 0.03
+    lin = torch.nn.Linear(K, N, bias=False)
+    with torch.no_grad():
+        lin.weight.copy_(W)
+    m = qa.mx_linear.from_linear(lin.to(dev()), qa.get_mx_dtype("float4d"), 128)
+    wp, ws, _ = orc.linear_from_weight(W, "float4d", 128)
+    w = m._mx_weight
+    for M in (4, 40):
+        x = _randn((M, K), 73 + M)
+        y = m(x.to(dev())).cpu()
+        assert w.__dict__["_mx_tiled"] is not None and w.__dict__["_mx_packed_store"] is None
+        ok, worst = _rowwise_ok(y, orc.linear_forward(x, wp, ws, "float4d", K, N, 128))
+        assert ok, f"M={M}: worst row error {worst:.3g} x the bar"
+    xg = _randn((24, K), 79).to(dev()).requires_grad_(True)
+    g = _randn((24, N), 83)
+    m(xg).backward(g.to(dev()))
+    w_dq = orc.dequant(wp, ws, "float4d", K * N, 128).reshape(K, N).double()
+    ok, worst = _rowwise_ok(xg.grad.cpu(), (g.double() @ w_dq.t()).float())
+    assert ok, f"input gradient: worst row error {worst:.3g} x the bar"
+    assert G.bits_equal(w._mx_packed.cpu(), wp)
+    assert G.bits_equal(w.dequantize().cpu().reshape(-1), orc.dequant(wp, ws, "float4d", K * N, 128))
