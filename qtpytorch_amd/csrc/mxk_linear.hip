@@ -285,18 +285,23 @@ __global__ __launch_bounds__(DEC_THREADS, 1) void k_linear_w4_decode(
   // taken back by one correction MFMA.  FP: sorted-grid float codes (FP4 E2M1, FP8 E4M3),
   // whose B operands are the format's values v * 2^-E exactly (E = 14 or 8,
   // no offset), and the epilogue takes 2^E * RN(1 / vmax).
-  static_assert(BITS == 4 || BITS == 8, "4- or 8-bit codes");
-  constexpr int WPR = BITS / 4;  // 32-bit words of a lane's 8 columns in one row
+  // BITS = 2 (int2 codes): 16 bits of a row per lane, as (c + 2) at bits
+  // 0-1 of an f16 half with the int4 correction scaled by 2/128.
+  static_assert(BITS == 2 || BITS == 4 || BITS == 8, "2-, 4- or 8-bit codes");
+  static_assert(!FP || BITS != 2, "no 2-bit float grid");
+  constexpr int WPR = BITS == 8 ? 2 : 1;  // 32-bit words of a lane's 8 columns in one row (int2: 16 bits)
   const __amdgpu_buffer_rsrc_t rw = make_rsrc(w, (uint32_t)(K * N * BITS / 8));
   const uint32_t row_bytes = (uint32_t)(N * BITS / 8);
-  const uint32_t vw = (uint32_t)(8 * g * row_bytes + (nb * 16 + j) * 4 * WPR);
+  const uint32_t vw = (uint32_t)(8 * g * row_bytes + (nb * 16 + j) * BITS);  // a lane's 8 columns: BITS bytes
   uint32_t wv[P][8 * WPR];
   auto issue = [&](int slot, int st) {
     const int64_t k0 = kw + (int64_t)st * 32;
     const uint32_t kr = k0 < K ? (uint32_t)k0 : 0u;  // wave-uniform
 #pragma unroll
     for (int r = 0; r < 8; ++r) {
-      if constexpr (BITS == 4) {
+      if constexpr (BITS == 2) {
+        wv[slot][r] = buf_load_b16_nt(rw, vw, (kr + r) * row_bytes);
+      } else if constexpr (BITS == 4) {
         wv[slot][r] = buf_load_b32_nt(rw, vw, (kr + r) * row_bytes);
       } else {
         const uint2 v = buf_load_b64_nt(rw, vw, (kr + r) * row_bytes);
@@ -389,6 +394,9 @@ __global__ __launch_bounds__(DEC_THREADS, 1) void k_linear_w4_decode(
       if constexpr (BITS == 4 && !FP) {
         lo4[r] = (wv[q][r] & 0x0F0F0F0Fu) ^ 0x08080808u;
         hi4[r] = (wv[q][r] & 0xF0F0F0F0u) ^ 0x80808080u;
+      } else if constexpr (BITS == 2) {
+        // rows 2h and 2h + 1 side by side (odd r: the upper half)
+        lo4[r] = (r & 1) ? wv[q][r] << 16 : wv[q][r];
       } else {
         lo4[r] = wv[q][r];
       }
@@ -412,6 +420,9 @@ __global__ __launch_bounds__(DEC_THREADS, 1) void k_linear_w4_decode(
           const int wd = t >> 2;
           const uint32_t selh = 0x0Cu | (p << 8) | 0x0C0000u | ((4u + p) << 24);
           bq[h] = fp_code_pair_f16<8>(__builtin_amdgcn_perm(lo4[2 * (2 * h + 1) + wd], lo4[2 * (2 * h) + wd], selh));
+        } else if constexpr (BITS == 2) {
+          // column 8j + t at bits 2t of each row's 16 bits: c ^ 2 = c + 2, the denormal (c + 2) * 2^-24
+          bq[h] = (((lo4[2 * h] | lo4[2 * h + 1]) >> (2 * t)) & 0x00030003u) ^ 0x00020002u;
         } else if constexpr (BITS == 4) {
           const uint32_t a0 = (t & 1) ? hi4[2 * h] : lo4[2 * h];
           const uint32_t a1 = (t & 1) ? hi4[2 * h + 1] : lo4[2 * h + 1];
@@ -431,7 +442,7 @@ __global__ __launch_bounds__(DEC_THREADS, 1) void k_linear_w4_decode(
       acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi, bt, acc[t], 0, 0, 0);
       acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo, bt, acc[t], 0, 0, 0);
     }
-    if constexpr (!FP && BITS == 4) {
+    if constexpr (!FP && BITS != 8) {
       corr = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi, b8, corr, 0, 0, 0);
       corr = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo, b8, corr, 0, 0, 0);
     }
@@ -454,6 +465,8 @@ __global__ __launch_bounds__(DEC_THREADS, 1) void k_linear_w4_decode(
         v[t] = __builtin_ldexpf(acc[t][i], (BITS == 4 ? 14 : 8) + sh) * (BITS == 4 ? 1.0f / 6.0f : 1.0f / 480.0f);
       else if constexpr (BITS == 8)  // exact codes
         v[t] = __builtin_ldexpf(acc[t][i], sh);
+      else if constexpr (BITS == 2)  // (c + 2) * 2^-24, corr the sum of 128 * 2^-24 terms
+        v[t] = __builtin_ldexpf(acc[t][i] - corr[i] * 0.015625f, 24 + sh);
       else
         v[t] = (t & 1) ? __builtin_ldexpf(acc[t][i] - corr[i], 20 + sh)
                        : __builtin_ldexpf(acc[t][i] - corr[i] * 0.0625f, 24 + sh);
@@ -1718,6 +1731,8 @@ static void launch_decode(const DecodePlan& p, hipStream_t st, const void* x, in
     const bool fp = kind == MXK_KIND_FLOAT;                                         \
     if (bits == 8) {                                                                \
       if (fp) MXK_DEC_K(STEPS, NBW, 8, true); else MXK_DEC_K(STEPS, NBW, 8, false); \
+    } else if (bits == 2) {                                                         \
+      MXK_DEC_K(STEPS, NBW, 2, false);                                              \
     } else {                                                                        \
       if (fp) MXK_DEC_K(STEPS, NBW, 4, true); else MXK_DEC_K(STEPS, NBW, 4, false); \
     }                                                                               \
@@ -1794,10 +1809,13 @@ static void launch_decode_tiled(const DecodePlan& p, hipStream_t st, const void*
 
 static bool decode_eligible(int64_t M, int64_t K, int64_t N, int kind, int bits, int block, const void* x,
                             int x_type, const void* w) {
-  if ((kind != MXK_KIND_INT && kind != MXK_KIND_FLOAT) || (bits != 4 && bits != 8) || block != 128) return false;
+  if (block != 128) return false;
+  if (!(kind == MXK_KIND_INT && (bits == 2 || bits == 4 || bits == 8)) &&
+      !(kind == MXK_KIND_FLOAT && (bits == 4 || bits == 8)))
+    return false;
   if (M < 1 || M > 16 || K % 32 != 0 || N % 128 != 0) return false;
   if (N / 128 > DEC_COUNTER_BYTES / 8 || K / 32 >= 65536) return false;
-  if (!aligned16(x) || (reinterpret_cast<uintptr_t>(w) & (bits == 8 ? 7u : 3u)) != 0) return false;
+  if (!aligned16(x) || (reinterpret_cast<uintptr_t>(w) & (bits == 8 ? 7u : bits == 4 ? 3u : 1u)) != 0) return false;
   const int esz = x_type == MXK_IN_F32 ? 4 : 2;
   if ((K * esz) % 16 != 0) return false;
   // 32-bit buffer offsets with headroom
@@ -1910,8 +1928,8 @@ extern "C" {
 size_t mxk_linear_workspace(int64_t M, int64_t K, int64_t N, int bits, int block) {
   // the MFMA path (any M, int4/int8 codes); its buffers start past the decode counters
   const size_t c = M > 0 && K > 0 && N > 0 ? linear_mfma_workspace(M, K, N, bits, block, false) : 0;
-  if (M < 1 || M > 16 || (bits != 4 && bits != 8) || block != 128 || K <= 0 || N <= 0 || K % 32 != 0 ||
-      N % 128 != 0)
+  if (M < 1 || M > 16 || (bits != 2 && bits != 4 && bits != 8) || block != 128 || K <= 0 || N <= 0 ||
+      K % 32 != 0 || N % 128 != 0)
     return c;
   // enough for mxk_linear_wq's decode path and for mxk_linear_wq_tiled
   const DecodePlan p = plan_decode(K, N), q = plan_decode_tiled(K, N, 4), q2 = plan_decode_tiled(K, N, 2);

@@ -1,5 +1,5 @@
-"""mx_linear's decode paths (at most 16 rows of x; int4, int8, FP4 and FP8
-codes) at any input magnitude (mx_linear.forward, mxtorch.py:7454-7473:
+"""mx_linear's decode paths (at most 16 rows of x; int4, int8, int2, FP4 and
+FP8 codes) at any input magnitude (mx_linear.forward, mxtorch.py:7454-7473:
 y = x.float() @ dequant(quantize(W.t()))).
 
 The decode kernel feeds x*s to f16 MFMAs as a hi + lo pair; these tests
@@ -63,7 +63,7 @@ def _run(qa, x, W, K, N, dt="int4d"):
 
 
 MAGS = [1e-6, 1e-3, 1.0, 1e4, 1e6]
-DTS = ["int4d", "int8d", "float4d", "float8d"]
+DTS = ["int4d", "int8d", "int2d", "float4d", "float8d"]
 
 
 @pytest.mark.parametrize("dt", DTS)
@@ -150,7 +150,7 @@ def test_decode_int8_shapes(qa, M, K, N, xdt):
     assert torch.equal(y, y2)
 
 
-@pytest.mark.parametrize("dt", ["int4d", "int8d", "float4d", "float8d"])
+@pytest.mark.parametrize("dt", ["int4d", "int8d", "int2d", "float4d", "float8d"])
 def test_decode_every_code(qa, dt):
     """Every code of the format in every column and k position through the
     decode kernel: x is 16 rows of the identity at a time, so each output is
@@ -160,7 +160,7 @@ def test_decode_every_code(qa, dt):
     by the hi + lo split of s (2^-22) and, for the float grids, the factor
     RN(1/6) or RN(1/480)."""
     from qtpytorch_amd import ops
-    bits = {"int4d": 4, "int8d": 8, "float4d": 4, "float8d": 8}[dt]
+    bits = {"int4d": 4, "int8d": 8, "int2d": 2, "float4d": 4, "float8d": 8}[dt]
     K, N = 384, 256
     k = torch.arange(K)[:, None]
     n = torch.arange(N)[None, :]
