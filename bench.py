@@ -300,8 +300,8 @@ def bench_linear_mfma(qa, reps):
                                           "f16_mfma_TFLOPS": round(2 * flops / t / 1e12, 1),
                                           "frac_f16_peak": round(2 * flops / t / 1e12 / F16_PEAK_TFLOPS, 4)}
             del x
-        if name in ("int8d", "float4d", "float8d"):
-            # decode batch (16 rows): the decode kernel on the codes as stored, HBM-bound
+        if name in ("int8d", "int2d", "float4d", "float8d"):
+            # decode batch (16 rows): the decode kernels (float4d on its tiled copy), HBM-bound
             x = torch.randn(16, K, generator=gen(36, "cuda"), device=dev)
             with torch.no_grad():
                 m(x)
