@@ -211,7 +211,8 @@ int mxk_linear_wq_noalloc(const void* x, int x_type, int64_t M, int64_t K, const
                           const float* w_scales, const float* w_scales_t, int64_t N, int kind, int bits, int block,
                           const float* bias, float* out, void* stream);
 
-/* Tiled copy of an int4 weight for mxk_linear_wq_tiled: w_packed is the
+/* Tiled copy of a 4-bit weight (int4 or FP4 codes: the copy only moves
+ * nibbles) for mxk_linear_wq_tiled: w_packed is the
  * [K][N] packing of quantize(weight.t()) (mxtorch.py:7447), bits 4, block
  * 128, K a multiple of 32, N of 128; w_tiled receives the same K*N/2 bytes
  * reordered so that the decode kernel reads each wave's rows as contiguous

@@ -368,9 +368,10 @@ def prepack_scales(w_scales: Tensor, in_features: int, out_features: int, block:
 
 
 def prepack_weight(w_packed: Tensor, in_features: int, out_features: int, block: int = 128) -> Tensor:
-    """Tiled copy (uint8, in*out/2 bytes) of a quantized int4 [in, out]
-    weight's packed codes, the layout linear_wq's tiled decode kernel reads
-    (mxk_linear_prepack_weight)."""
+    """Tiled copy (uint8, in*out/2 bytes) of a quantized 4-bit (int4 or FP4)
+    [in, out] weight's packed codes, the layout linear_wq's tiled decode and
+    MFMA kernels read (mxk_linear_prepack_weight; the copy only moves
+    nibbles)."""
     dev = L.require_gpu(w_packed)
     K, N = in_features, out_features
     pk = w_packed.contiguous()

@@ -101,10 +101,11 @@ class mx_tensor(torch.Tensor):
         return t if t is not None else self.__dict__["_mx_packed_store"]
 
     def _mx_tile_(self, in_features: int, out_features: int, layout: str = "kn") -> Tensor:
-        """Hold the codes of this int4 weight as their tiled copy only and
-        return it; the packed bytes are freed.  layout "kn": an [in, out]
-        weight (mx_linear, ops.prepack_weight); "nt": an [out, in] weight
-        (mx_dynamic_linear, ops.prepack_weight_nt)."""
+        """Hold the codes of this 4-bit weight (int4, or FP4 for layout "kn")
+        as their tiled copy only and return it; the packed bytes are freed.
+        layout "kn": an [in, out] weight (mx_linear, ops.prepack_weight);
+        "nt": an [out, in] int4 weight (mx_dynamic_linear,
+        ops.prepack_weight_nt)."""
         d = self.__dict__
         t = d.get("_mx_tiled")
         if t is not None:
