@@ -97,8 +97,12 @@ __device__ __forceinline__ uint32_t lm_i2pair(uint32_t d) {
   const h2v r = __builtin_bit_cast(h2v, e) - h2v{(_Float16)1026.0f, (_Float16)1026.0f};
   return __builtin_bit_cast(uint32_t, r);
 }
+// Two int1 codes at bits 0 and 16 of d (other bits ignored): code 0 is
+// +1 and code 1 is -1 (the reference's 1-bit grid), so the code is the f16
+// sign bit of 1.0.
+__device__ __forceinline__ uint32_t lm_i1pair(uint32_t d) { return ((d & 0x00010001u) << 15) | 0x3C003C00u; }
 // Weight formats: the code width in the low 4 bits, 16 for float grids
-enum : int { LM_I2 = 2, LM_I4 = 4, LM_I8 = 8, LM_F4 = 16 + 4, LM_F8 = 16 + 8 };
+enum : int { LM_I1 = 1, LM_I2 = 2, LM_I4 = 4, LM_I8 = 8, LM_F4 = 16 + 4, LM_F8 = 16 + 8 };
 __host__ __device__ constexpr int lm_bits(int fmt) { return fmt & 15; }
 // The factor the outputs take for B fragments that hold v * 2^-P instead of
 // the grid value v / vmax: RN(1/6) * 2^14, RN(1/480) * 2^8, or 1 for integer
@@ -107,7 +111,7 @@ __host__ __device__ constexpr float lm_post(int fmt) {
   return fmt == LM_F4 ? (1.0f / 6.0f) * 16384.0f : fmt == LM_F8 ? (1.0f / 480.0f) * 256.0f : 1.0f;
 }
 inline int lm_format(int kind, int bits) {
-  if (kind == MXK_KIND_INT) return bits == 2 ? LM_I2 : bits == 4 ? LM_I4 : bits == 8 ? LM_I8 : 0;
+  if (kind == MXK_KIND_INT) return bits == 1 ? LM_I1 : bits == 2 ? LM_I2 : bits == 4 ? LM_I4 : bits == 8 ? LM_I8 : 0;
   if (kind == MXK_KIND_FLOAT) return bits == 4 ? LM_F4 : bits == 8 ? LM_F8 : 0;
   return 0;
 }
@@ -117,6 +121,7 @@ __device__ __forceinline__ uint32_t lm_pair(uint32_t d) {
   if constexpr (FMT == LM_I4) return lm_i4pair(d);
   else if constexpr (FMT == LM_I8) return lm_i8pair(d);
   else if constexpr (FMT == LM_I2) return lm_i2pair(d);
+  else if constexpr (FMT == LM_I1) return lm_i1pair(d);
   else return fp_code_pair_f16<lm_bits(FMT)>(d);
 }
 
@@ -176,7 +181,9 @@ __device__ __forceinline__ void kn_load(KnCodes<BITS>& c, __amdgpu_buffer_rsrc_t
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
     const int64_t row = k0 + 8 * r8 + i;
-    if constexpr (BITS == 2) {
+    if constexpr (BITS == 1) {
+      c.w[i] = __builtin_amdgcn_raw_buffer_load_b8(rw, (int)((uint32_t)(row * (N / 8) + nb * 16 + c8) | dead), 0, 0);
+    } else if constexpr (BITS == 2) {
       c.w[i] = __builtin_amdgcn_raw_buffer_load_b16(rw, (int)((uint32_t)(row * (N / 4) + nb * 32 + 2 * c8) | dead),
                                                     0, 0);
     } else if constexpr (BITS == 4) {
@@ -197,7 +204,11 @@ __device__ __forceinline__ u4v kn_frag(const KnCodes<lm_bits(FMT)>& c, int t) {
   u4v f;
 #pragma unroll
   for (int q = 0; q < 4; ++q) {
-    if constexpr (BITS == 2) {
+    if constexpr (BITS == 1) {
+      // rows 2q and 2q+1 (8 bits each) 16 bits apart: column 8 c8 + t at bits t, 16 + t
+      const uint32_t d = c.w[2 * q] | (c.w[2 * q + 1] << 16);
+      f[q] = lm_pair<FMT>(d >> t);
+    } else if constexpr (BITS == 2) {
       // rows 2q and 2q+1 (16 bits each) side by side: column 8 c8 + t at bits 2t, 2t + 1
       const uint32_t d = c.w[2 * q] | (c.w[2 * q + 1] << 16);
       f[q] = lm_pair<FMT>(d >> (2 * t));
@@ -266,6 +277,7 @@ __device__ __forceinline__ void kn_store_tiled(const KnTiled& c, uint8_t* sB, in
 // int8: 16 lanes read one column's 256 bytes; 16 bytes are two k octets.
 // int2: 4 lanes read one column's 64 bytes, each 16 bytes two k steps; the
 // 4 columns of a 16-lane store group share a tile and differ in j.
+// int1: the same lanes and columns as int2, 8 bytes (two k steps) each.
 template <int BITS>
 struct NkCodes {
   u4v w[BITS == 4 ? 2 : BITS == 8 ? 4 : 1];
@@ -277,7 +289,13 @@ __device__ __forceinline__ int nk2_col(int p) { return ((p >> 4) & 7) + 8 * (p &
 template <int BITS>
 __device__ __forceinline__ void nk_load(NkCodes<BITS>& c, __amdgpu_buffer_rsrc_t rw, int64_t k0, int64_t K,
                                         int64_t nb, int tid, uint32_t dead) {
-  if constexpr (BITS == 2) {
+  if constexpr (BITS == 1) {
+    const int64_t n = nb * 128 + nk2_col(tid >> 2);
+    const auto v =
+        __builtin_amdgcn_raw_buffer_load_b64(rw, (int)((uint32_t)(n * (K / 8) + k0 / 8 + 8 * (tid & 3)) | dead), 0, 0);
+    c.w[0][0] = v[0];
+    c.w[0][1] = v[1];
+  } else if constexpr (BITS == 2) {
     const int64_t n = nb * 128 + nk2_col(tid >> 2);
     c.w[0] = buf_load_b128(rw, (uint32_t)(n * (K / 4) + k0 / 4 + 16 * (tid & 3)) | dead, 0u);
   } else if constexpr (BITS == 4) {
@@ -300,7 +318,25 @@ __device__ __forceinline__ void nk_load(NkCodes<BITS>& c, __amdgpu_buffer_rsrc_t
 template <int FMT>
 __device__ __forceinline__ void nk_store(const NkCodes<lm_bits(FMT)>& c, uint8_t* sB, int tid) {
   constexpr int BITS = lm_bits(FMT);
-  if constexpr (BITS == 2) {
+  if constexpr (BITS == 1) {
+    // k step 2q + s is dword s, octet v its byte v.  Byte v of wd beside
+    // byte v of wd >> 1 holds codes (0, 1) at bits 0 and 16, (2p, 2p + 1)
+    // 2p bits higher.
+    const int q = tid & 3, col = nk2_col(tid >> 2);
+    const int t = col & 7, j = col >> 3;
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      const uint32_t wd = c.w[0][s], sh = wd >> 1;
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const uint32_t d = __builtin_amdgcn_perm(sh, wd, lm_sel(v, v));
+        u4v f;
+#pragma unroll
+        for (int p = 0; p < 4; ++p) f[p] = lm_pair<FMT>(d >> (2 * p));
+        *reinterpret_cast<u4v*>(sB + lm_frag_off(2 * q + s, t, j + 16 * v)) = f;
+      }
+    }
+  } else if constexpr (BITS == 2) {
     // k step 2q + s is dwords 2s, 2s+1; octet v is bytes 2 (v & 1), +1 of
     // dword 2s + v / 2.  Byte b of wd beside byte b of wd >> 2 holds the
     // codes (0, 1) at bits 0-1 and 16-17, and (2, 3) four bits higher.
@@ -1013,7 +1049,7 @@ bool lm_common_ok(int64_t M, int64_t K, int64_t N, int kind, int bits, int block
 // Bytes of workspace the MFMA path needs for this product (0 when it does
 // not take the shape); the first LM_WS_BASE bytes are left untouched.
 size_t linear_mfma_workspace(int64_t M, int64_t K, int64_t N, int bits, int block, bool nk) {
-  if ((bits != 2 && bits != 4 && bits != 8) || block != 128 || M < 1 || K < 1 || N < 128 || N % 128 != 0) return 0;
+  if ((bits != 1 && bits != 2 && bits != 4 && bits != 8) || block != 128 || M < 1 || K < 1 || N < 128 || N % 128 != 0) return 0;
   if (nk && K % 128 != 0) return 0;
   return lm_plan(M, K, N, nk, bits).bytes;
 }
@@ -1024,7 +1060,8 @@ int linear_mfma_kn(const void* x, int x_type, int64_t M, int64_t K, const void* 
                    const float* w_scales_t, int64_t N, int kind, int bits, int block, const float* bias, float* out,
                    void* workspace, size_t workspace_nbytes, hipStream_t st) {
   if (!lm_common_ok(M, K, N, kind, bits, block, x_type, out)) return MXK_EUNSUPPORTED;
-  if ((reinterpret_cast<uintptr_t>(w_packed) & (bits == 8 ? 7u : bits == 4 ? 3u : 1u)) != 0) return MXK_EUNSUPPORTED;
+  if ((reinterpret_cast<uintptr_t>(w_packed) & (bits == 8 ? 7u : bits == 4 ? 3u : bits == 2 ? 1u : 0u)) != 0)
+    return MXK_EUNSUPPORTED;
   const LmPlan p = lm_plan(M, K, N, false, bits);
   if (!workspace || workspace_nbytes < p.bytes)
     return fail(MXK_EINVAL, "linear_wq: needs a workspace of mxk_linear_workspace() bytes");
@@ -1047,6 +1084,7 @@ int linear_mfma_kn(const void* x, int x_type, int64_t M, int64_t K, const void* 
   switch (fmt) {
 #define MXK_LMK(F) \
   case F: lm_launch_w<F, false>(p, st, xs, nullptr, nullptr, sT, 1, ex, es, w, M, K, N, bias, out, part); break;
+    MXK_LMK(LM_I1)
     MXK_LMK(LM_I2)
     MXK_LMK(LM_I4)
     MXK_LMK(LM_I8)
@@ -1111,6 +1149,7 @@ int linear_mfma_nk(const void* x, int x_type, int64_t M, int64_t K, const void* 
   switch (fmt) {
 #define MXK_LMN(F) \
   case F: lm_launch_w<F, true>(p, st, nullptr, xh, xl, sc, kbm, ex, nullptr, w, M, K, N, bias, out, part); break;
+    MXK_LMN(LM_I1)
     MXK_LMN(LM_I2)
     MXK_LMN(LM_I4)
     MXK_LMN(LM_I8)

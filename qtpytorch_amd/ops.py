@@ -345,10 +345,10 @@ def decode_prepack_eligible(dt, block: int, in_features: int, out_features: int)
 
 def scales_prepack_eligible(dt, block: int, in_features: int, out_features: int) -> bool:
     """Whether linear_wq's kernels read block-major scales for this weight:
-    the int4 decode kernels and the MFMA kernels (int2, int4 and int8 base
-    codes, FP4 and FP8 grids; block 128, whole 128-column blocks)."""
+    the int4 decode kernels and the MFMA kernels (int1, int2, int4 and int8
+    base codes, FP4 and FP8 grids; block 128, whole 128-column blocks)."""
     dt = get_mx_dtype(dt)
-    return (dt.bits in ((4, 8) if dt.is_float else (2, 4, 8)) and not dt.is_hadamard and not dt.is_vector
+    return (dt.bits in ((4, 8) if dt.is_float else (1, 2, 4, 8)) and not dt.is_hadamard and not dt.is_vector
             and block == 128 and out_features % 128 == 0)
 
 

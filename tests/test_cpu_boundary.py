@@ -155,14 +155,14 @@ def test_decode_workspace_limits():
     assert h.mxk_linear_workspace(16, 8192, 8192, 4, 128) >= 65536
     assert h.mxk_linear_workspace(1, 2048 * 255, 128, 4, 128) > 0
     # past the decode kernels' limits (more than 16 rows, 293 splits, other
-    # formats) the MFMA path takes 2-, 4- and 8-bit codes: its row exponents,
+    # formats) the MFMA path takes 1-, 2-, 4- and 8-bit codes: its row exponents,
     # scaled x (fp32), scaled scales and any split partials follow the 64 KiB
     # counter prefix, which it leaves alone
     for M, K, N, bits in ((17, 8192, 8192, 4), (1, 600000, 128, 4), (512, 8192, 8192, 8), (16, 4096, 256, 8),
-                          (64, 8192, 8192, 2)):
+                          (64, 8192, 8192, 2), (64, 8192, 8192, 1)):
         Kp = -(-K // 256) * 256
         assert h.mxk_linear_workspace(M, K, N, bits, 128) >= 65536 + M * Kp * 4 + (N // 128) * Kp * 4
-    for bits in (1, 3, 5, 16):
+    for bits in (3, 5, 16):
         assert h.mxk_linear_workspace(64, 8192, 8192, bits, 128) == 0  # other widths: generic kernel, no workspace
     assert h.mxk_linear_workspace(64, 8192, 8000, 4, 128) == 0     # N not whole 128-column blocks
     # [out, in] weights: K must be whole blocks of 128; x as f16 hi + lo

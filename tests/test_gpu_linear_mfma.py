@@ -24,7 +24,7 @@ from tests import _golden as G
 pytestmark = pytest.mark.gpu
 
 RTOL = 1e-3
-FMTS = ["int4d", "int8d", "int2d", "float4d", "float8d"]
+FMTS = ["int4d", "int8d", "int2d", "int1d", "float4d", "float8d"]
 
 
 @pytest.fixture(scope="module")
@@ -286,7 +286,7 @@ def test_mfma_repeat_bitwise(qa):
         assert torch.equal(m(x), m(x))
 
 
-@pytest.mark.parametrize("dt", ["int2d", "int4d", "int8d", "float4d", "float8d"])
+@pytest.mark.parametrize("dt", ["int1d", "int2d", "int4d", "int8d", "float4d", "float8d"])
 @pytest.mark.parametrize("layout", ["kn", "nk"])
 def test_mfma_every_code(qa, dt, layout):
     """Every code of the format in every column and k position: codes
@@ -299,7 +299,7 @@ def test_mfma_every_code(qa, dt, layout):
     s (2^-22) and, for the float grids, the factor RN(1/6) or RN(1/480):
     a code decoded to any other grid value fails by far more."""
     from qtpytorch_amd import ops
-    bits = {"int2d": 2, "int4d": 4, "int8d": 8, "float4d": 4, "float8d": 8}[dt]
+    bits = {"int1d": 1, "int2d": 2, "int4d": 4, "int8d": 8, "float4d": 4, "float8d": 8}[dt]
     K, N = 384, 256
     k = torch.arange(K)[:, None]
     n = torch.arange(N)[None, :]

@@ -63,7 +63,7 @@ def _run(qa, x, W, K, N, dt="int4d"):
 
 
 MAGS = [1e-6, 1e-3, 1.0, 1e4, 1e6]
-DTS = ["int4d", "int8d", "int2d", "float4d", "float8d"]
+DTS = ["int4d", "int8d", "int2d", "int1d", "float4d", "float8d"]
 
 
 @pytest.mark.parametrize("dt", DTS)

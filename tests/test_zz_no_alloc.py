@@ -40,7 +40,7 @@ def _noalloc(qa, x, wp, ws, st, K, N, dt=None):
     return out
 
 
-@pytest.mark.parametrize("name", ["int4d", "int8d", "float4d", "float8d"])
+@pytest.mark.parametrize("name", ["int4d", "int8d", "int2d", "int1d", "float4d", "float8d"])
 @pytest.mark.parametrize("prepacked", [True, False])
 def test_noalloc_matches_workspace_entry(qa, prepacked, name):
     dev = torch.device("cuda:0")
