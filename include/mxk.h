@@ -160,7 +160,7 @@ int mxk_qgemm(const void* a_packed, const float* a_scales, int64_t a_nscales, co
  * zero-filled before first use, and every call, of any shape, leaves the
  * counter prefix ready for the next one.  Calls sharing a workspace must
  * not overlap.  The size also covers mxk_linear_wq_tiled and the MFMA path
- * (2-, 4- and 8-bit codes, block 128, N % 128 == 0, any M): its row exponents,
+ * (1-, 2-, 4- and 8-bit codes, block 128, N % 128 == 0, any M): its row exponents,
  * x scaled by them (M * roundup(K, 256) floats), a block-major copy of the
  * scales when w_scales_t is NULL and any K-split partials, all after the
  * counter prefix, which it leaves alone. */
@@ -182,8 +182,8 @@ int mxk_linear_prepack_scales(const float* w_scales, int64_t K, int64_t N, int b
  * weight RN(code*s) (mxtorch.py:1573-1575) is formed in registers only.
  * kind/bits as for mxk_quantize (base variant).  Float32 accumulation.
  * Int2, int4, int8, FP4 and FP8 weights with x of at most 16 rows run the decode kernel;
- * int2, int4, int8, FP4 and FP8 weights (block 128, N % 128 == 0) with any
- * other x run on f16 MFMAs, x * s as an f16 hi + lo pair against the exact
+ * int1, int2, int4, int8, FP4 and FP8 weights (block 128, N % 128 == 0) with
+ * any other x, and int1 weights with any x, run on f16 MFMAs, x * s as an f16 hi + lo pair against the exact
  * codes or grid values (each term within 2^-22 of x * RN(code * s), after a
  * power-of-two scaling of every row of x and every block of scales into
  * f16's range); other widths and shapes a scalar fallback.
