@@ -277,7 +277,7 @@ def bench_config1_full(qa, reps):
 def bench_linear_mfma(qa, reps):
     """mx_linear beyond the decode shape (mxtorch.py:7454-7473): x fp32 [M,
     8192] @ dequant(W [8192, 8192] stored as quantize(W.t())), M = 512 and
-    8192, int4d, int8d, int2d, float4d and float8d weights.  The kernel issues two f16 MFMAs per
+    8192, int4d, int8d, int2d, int1d, float4d and float8d weights.  The kernel issues two f16 MFMAs per
     product (x*s as hi + lo against the exact codes), so the f16 MFMA work is
     twice 2*M*K*N; frac_f16_peak is that work over 2.5 PFLOP/s dense f16."""
     dev = torch.device("cuda:0")
@@ -288,7 +288,7 @@ def bench_linear_mfma(qa, reps):
         lin.weight.copy_(W_cpu)
     lin = lin.to(dev)
     out = {}
-    for name in ("int4d", "int8d", "int2d", "float4d", "float8d"):
+    for name in ("int4d", "int8d", "int2d", "int1d", "float4d", "float8d"):
         m = qa.mx_linear.from_linear(lin, qa.get_mx_dtype(name), 128)
         for M in (512, 8192):
             x = torch.randn(M, K, generator=gen(20 + M, "cuda"), device=dev)
@@ -300,8 +300,9 @@ def bench_linear_mfma(qa, reps):
                                           "f16_mfma_TFLOPS": round(2 * flops / t / 1e12, 1),
                                           "frac_f16_peak": round(2 * flops / t / 1e12 / F16_PEAK_TFLOPS, 4)}
             del x
-        if name in ("int8d", "int2d", "float4d", "float8d"):
-            # decode batch (16 rows): the decode kernels (float4d on its tiled copy), HBM-bound
+        if name in ("int8d", "int2d", "int1d", "float4d", "float8d"):
+            # decode batch (16 rows): the decode kernels (float4d on its tiled copy; int1d the
+            # MFMA kernel), HBM-bound
             x = torch.randn(16, K, generator=gen(36, "cuda"), device=dev)
             with torch.no_grad():
                 m(x)
