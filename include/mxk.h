@@ -154,7 +154,7 @@ int mxk_qgemm(const void* a_packed, const float* a_scales, int64_t a_nscales, co
               void* stream);
 
 /* Workspace bytes mxk_linear_wq needs (0 if none).  The decode path
- * (2-, 4- and 8-bit codes, block 128, M <= 16, K % 32 == 0, N % 128 == 0) splits K
+ * (1-, 2-, 4- and 8-bit codes, block 128, M <= 16, K % 32 == 0, N % 128 == 0) splits K
  * across workgroups; its workspace (a 64 KiB counter prefix, the partial
  * sums, then room for block-major scales when w_scales_t is NULL) must be
  * zero-filled before first use, and every call, of any shape, leaves the
@@ -181,9 +181,8 @@ int mxk_linear_prepack_scales(const float* w_scales, int64_t K, int64_t N, int b
  * blocks of `block` flat elements (mxtorch.py:7447).  The dequantized
  * weight RN(code*s) (mxtorch.py:1573-1575) is formed in registers only.
  * kind/bits as for mxk_quantize (base variant).  Float32 accumulation.
- * Int2, int4, int8, FP4 and FP8 weights with x of at most 16 rows run the decode kernel;
- * int1, int2, int4, int8, FP4 and FP8 weights (block 128, N % 128 == 0) with
- * any other x, and int1 weights with any x, run on f16 MFMAs, x * s as an f16 hi + lo pair against the exact
+ * Int1, int2, int4, int8, FP4 and FP8 weights with x of at most 16 rows run the decode kernel;
+ * the same weights (block 128, N % 128 == 0) with any other x run on f16 MFMAs, x * s as an f16 hi + lo pair against the exact
  * codes or grid values (each term within 2^-22 of x * RN(code * s), after a
  * power-of-two scaling of every row of x and every block of scales into
  * f16's range); other widths and shapes a scalar fallback.

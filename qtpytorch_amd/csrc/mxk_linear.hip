@@ -287,8 +287,10 @@ __global__ __launch_bounds__(DEC_THREADS, 1) void k_linear_w4_decode(
   // no offset), and the epilogue takes 2^E * RN(1 / vmax).
   // BITS = 2 (int2 codes): 16 bits of a row per lane, as (c + 2) at bits
   // 0-1 of an f16 half with the int4 correction scaled by 2/128.
-  static_assert(BITS == 2 || BITS == 4 || BITS == 8, "2-, 4- or 8-bit codes");
-  static_assert(!FP || BITS != 2, "no 2-bit float grid");
+  // BITS = 1 (int1 codes, 0 is +1 and 1 is -1): one byte of a row per lane,
+  // the code the sign bit of the f16 1.0 (exact, no correction).
+  static_assert(BITS == 1 || BITS == 2 || BITS == 4 || BITS == 8, "1-, 2-, 4- or 8-bit codes");
+  static_assert(!FP || BITS >= 4, "no 1- or 2-bit float grid");
   constexpr int WPR = BITS == 8 ? 2 : 1;  // 32-bit words of a lane's 8 columns in one row (int2: 16 bits)
   const __amdgpu_buffer_rsrc_t rw = make_rsrc(w, (uint32_t)(K * N * BITS / 8));
   const uint32_t row_bytes = (uint32_t)(N * BITS / 8);
@@ -299,7 +301,9 @@ __global__ __launch_bounds__(DEC_THREADS, 1) void k_linear_w4_decode(
     const uint32_t kr = k0 < K ? (uint32_t)k0 : 0u;  // wave-uniform
 #pragma unroll
     for (int r = 0; r < 8; ++r) {
-      if constexpr (BITS == 2) {
+      if constexpr (BITS == 1) {
+        wv[slot][r] = buf_load_b8_nt(rw, vw, (kr + r) * row_bytes);
+      } else if constexpr (BITS == 2) {
         wv[slot][r] = buf_load_b16_nt(rw, vw, (kr + r) * row_bytes);
       } else if constexpr (BITS == 4) {
         wv[slot][r] = buf_load_b32_nt(rw, vw, (kr + r) * row_bytes);
@@ -394,7 +398,7 @@ __global__ __launch_bounds__(DEC_THREADS, 1) void k_linear_w4_decode(
       if constexpr (BITS == 4 && !FP) {
         lo4[r] = (wv[q][r] & 0x0F0F0F0Fu) ^ 0x08080808u;
         hi4[r] = (wv[q][r] & 0xF0F0F0F0u) ^ 0x80808080u;
-      } else if constexpr (BITS == 2) {
+      } else if constexpr (BITS <= 2) {
         // rows 2h and 2h + 1 side by side (odd r: the upper half)
         lo4[r] = (r & 1) ? wv[q][r] << 16 : wv[q][r];
       } else {
@@ -420,6 +424,9 @@ __global__ __launch_bounds__(DEC_THREADS, 1) void k_linear_w4_decode(
           const int wd = t >> 2;
           const uint32_t selh = 0x0Cu | (p << 8) | 0x0C0000u | ((4u + p) << 24);
           bq[h] = fp_code_pair_f16<8>(__builtin_amdgcn_perm(lo4[2 * (2 * h + 1) + wd], lo4[2 * (2 * h) + wd], selh));
+        } else if constexpr (BITS == 1) {
+          // column 8j + t at bit t of each row's byte: the sign of +-1.0
+          bq[h] = ((((lo4[2 * h] | lo4[2 * h + 1]) >> t) & 0x00010001u) << 15) | 0x3C003C00u;
         } else if constexpr (BITS == 2) {
           // column 8j + t at bits 2t of each row's 16 bits: c ^ 2 = c + 2, the denormal (c + 2) * 2^-24
           bq[h] = (((lo4[2 * h] | lo4[2 * h + 1]) >> (2 * t)) & 0x00030003u) ^ 0x00020002u;
@@ -442,7 +449,7 @@ __global__ __launch_bounds__(DEC_THREADS, 1) void k_linear_w4_decode(
       acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi, bt, acc[t], 0, 0, 0);
       acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo, bt, acc[t], 0, 0, 0);
     }
-    if constexpr (!FP && BITS != 8) {
+    if constexpr (!FP && (BITS == 2 || BITS == 4)) {
       corr = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi, b8, corr, 0, 0, 0);
       corr = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo, b8, corr, 0, 0, 0);
     }
@@ -463,7 +470,7 @@ __global__ __launch_bounds__(DEC_THREADS, 1) void k_linear_w4_decode(
     for (int t = 0; t < 8; ++t) {
       if constexpr (FP)  // v * 2^-E for the grid value RN(v / vmax)
         v[t] = __builtin_ldexpf(acc[t][i], (BITS == 4 ? 14 : 8) + sh) * (BITS == 4 ? 1.0f / 6.0f : 1.0f / 480.0f);
-      else if constexpr (BITS == 8)  // exact codes
+      else if constexpr (BITS == 8 || BITS == 1)  // exact codes
         v[t] = __builtin_ldexpf(acc[t][i], sh);
       else if constexpr (BITS == 2)  // (c + 2) * 2^-24, corr the sum of 128 * 2^-24 terms
         v[t] = __builtin_ldexpf(acc[t][i] - corr[i] * 0.015625f, 24 + sh);
@@ -1733,6 +1740,8 @@ static void launch_decode(const DecodePlan& p, hipStream_t st, const void* x, in
       if (fp) MXK_DEC_K(STEPS, NBW, 8, true); else MXK_DEC_K(STEPS, NBW, 8, false); \
     } else if (bits == 2) {                                                         \
       MXK_DEC_K(STEPS, NBW, 2, false);                                              \
+    } else if (bits == 1) {                                                         \
+      MXK_DEC_K(STEPS, NBW, 1, false);                                              \
     } else {                                                                        \
       if (fp) MXK_DEC_K(STEPS, NBW, 4, true); else MXK_DEC_K(STEPS, NBW, 4, false); \
     }                                                                               \
@@ -1810,12 +1819,13 @@ static void launch_decode_tiled(const DecodePlan& p, hipStream_t st, const void*
 static bool decode_eligible(int64_t M, int64_t K, int64_t N, int kind, int bits, int block, const void* x,
                             int x_type, const void* w) {
   if (block != 128) return false;
-  if (!(kind == MXK_KIND_INT && (bits == 2 || bits == 4 || bits == 8)) &&
+  if (!(kind == MXK_KIND_INT && (bits == 1 || bits == 2 || bits == 4 || bits == 8)) &&
       !(kind == MXK_KIND_FLOAT && (bits == 4 || bits == 8)))
     return false;
   if (M < 1 || M > 16 || K % 32 != 0 || N % 128 != 0) return false;
   if (N / 128 > DEC_COUNTER_BYTES / 8 || K / 32 >= 65536) return false;
-  if (!aligned16(x) || (reinterpret_cast<uintptr_t>(w) & (bits == 8 ? 7u : bits == 4 ? 3u : 1u)) != 0) return false;
+  if (!aligned16(x) || (reinterpret_cast<uintptr_t>(w) & (bits == 8 ? 7u : bits == 4 ? 3u : bits == 2 ? 1u : 0u)) != 0)
+    return false;
   const int esz = x_type == MXK_IN_F32 ? 4 : 2;
   if ((K * esz) % 16 != 0) return false;
   // 32-bit buffer offsets with headroom
@@ -1928,7 +1938,7 @@ extern "C" {
 size_t mxk_linear_workspace(int64_t M, int64_t K, int64_t N, int bits, int block) {
   // the MFMA path (any M, int4/int8 codes); its buffers start past the decode counters
   const size_t c = M > 0 && K > 0 && N > 0 ? linear_mfma_workspace(M, K, N, bits, block, false) : 0;
-  if (M < 1 || M > 16 || (bits != 2 && bits != 4 && bits != 8) || block != 128 || K <= 0 || N <= 0 ||
+  if (M < 1 || M > 16 || (bits != 1 && bits != 2 && bits != 4 && bits != 8) || block != 128 || K <= 0 || N <= 0 ||
       K % 32 != 0 || N % 128 != 0)
     return c;
   // enough for mxk_linear_wq's decode path and for mxk_linear_wq_tiled

@@ -150,7 +150,7 @@ def test_decode_int8_shapes(qa, M, K, N, xdt):
     assert torch.equal(y, y2)
 
 
-@pytest.mark.parametrize("dt", ["int4d", "int8d", "int2d", "float4d", "float8d"])
+@pytest.mark.parametrize("dt", ["int4d", "int8d", "int2d", "int1d", "float4d", "float8d"])
 def test_decode_every_code(qa, dt):
     """Every code of the format in every column and k position through the
     decode kernel: x is 16 rows of the identity at a time, so each output is
@@ -160,7 +160,7 @@ def test_decode_every_code(qa, dt):
     by the hi + lo split of s (2^-22) and, for the float grids, the factor
     RN(1/6) or RN(1/480)."""
     from qtpytorch_amd import ops
-    bits = {"int4d": 4, "int8d": 8, "int2d": 2, "float4d": 4, "float8d": 8}[dt]
+    bits = {"int4d": 4, "int8d": 8, "int2d": 2, "int1d": 1, "float4d": 4, "float8d": 8}[dt]
     K, N = 384, 256
     k = torch.arange(K)[:, None]
     n = torch.arange(N)[None, :]
