@@ -301,8 +301,7 @@ def bench_linear_mfma(qa, reps):
                                           "frac_f16_peak": round(2 * flops / t / 1e12 / F16_PEAK_TFLOPS, 4)}
             del x
         if name in ("int8d", "int2d", "int1d", "float4d", "float8d"):
-            # decode batch (16 rows): the decode kernels (float4d on its tiled copy; int1d the
-            # MFMA kernel), HBM-bound
+            # decode batch (16 rows): the decode kernels (float4d on its tiled copy), HBM-bound
             x = torch.randn(16, K, generator=gen(36, "cuda"), device=dev)
             with torch.no_grad():
                 m(x)
